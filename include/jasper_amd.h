@@ -1,0 +1,149 @@
+/* jasper_amd.h -- C ABI of the MI355X Jasper hot path (libjasper_amd.so).
+ *
+ * Drop-in boundary for the reference's TVM-FFI exports
+ * (reference ffi/jasper_ffi_common.cuh:208-807, ffi/jasper_ffi_plain.cu:19-131):
+ * the same symbol names `jasper_<op>_<config>`, the same argument order and
+ * meaning. Tensor arguments of the reference become a raw pointer plus the
+ * sizes the reference read from the tensor; every call that launches device
+ * work also takes the HIP stream to run on (NULL = the default stream).
+ *
+ * Conventions
+ *   - Every function returns int64_t. A negative value is an error; the
+ *     message is available from jasper_last_error() (thread-local). The
+ *     reference raised TVM_FFI_ICHECK failures and C++ exceptions as Python
+ *     exceptions (ffi/jasper_ffi_common.cuh:226, beam_search/api.cuh:70-72);
+ *     the Python package turns a negative return into the same exceptions.
+ *   - Handles are non-negative int64 ids into a process-wide table
+ *     (ffi/jasper_ffi_plain.cu:11-13).
+ *   - Vectors and queries are contiguous [n, dim] fp16 rows (device or
+ *     host memory for construction; device memory for queries). Rows need no
+ *     padding: dim need not be a multiple of 8 (fixes the reference's
+ *     stride assumption, vector.cuh:20-22).
+ *   - Search outputs are device int32 [n_queries, k] ids and fp32
+ *     [n_queries, k] distances.
+ *
+ * Plain configs (reference _CONFIGS, python/jasper/__init__.py:29-38):
+ *   f16_r{8,16,32,64}_{l2,ip}
+ * Directional configs (reference _DIRECTIONAL_CONFIGS, __init__.py:66-84):
+ *   f16_r{32,64}_{l2,ip}_k{4,16}_d{128,32678}
+ */
+#ifndef JASPER_AMD_H
+#define JASPER_AMD_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JASPER_PLAIN_CONFIGS(X) \
+  X(f16_r8_l2) X(f16_r16_l2) X(f16_r32_l2) X(f16_r64_l2) \
+  X(f16_r8_ip) X(f16_r16_ip) X(f16_r32_ip) X(f16_r64_ip)
+
+#define JASPER_DIRECTIONAL_CONFIGS(X) \
+  X(f16_r32_l2_k4_d128) X(f16_r32_l2_k4_d32678) X(f16_r64_l2_k4_d128) X(f16_r64_l2_k4_d32678) \
+  X(f16_r32_l2_k16_d128) X(f16_r32_l2_k16_d32678) X(f16_r64_l2_k16_d128) X(f16_r64_l2_k16_d32678) \
+  X(f16_r32_ip_k4_d128) X(f16_r32_ip_k4_d32678) X(f16_r64_ip_k4_d128) X(f16_r64_ip_k4_d32678) \
+  X(f16_r32_ip_k16_d128) X(f16_r32_ip_k16_d32678) X(f16_r64_ip_k16_d128) X(f16_r64_ip_k16_d32678)
+
+/* ---- per plain config (DEFINE_OPS, ffi/jasper_ffi_common.cuh:208-431) ---- */
+#define JASPER_DECLARE_PLAIN(id)                                                              \
+  /* LoadGraph_ :210-219 -> handle */                                                         \
+  int64_t jasper_load_##id(const char* path, int64_t dim, bool on_host);                      \
+  /* ConstructGraph_ :232-261 -> handle; vectors [n_vectors, dim] fp16 */                     \
+  int64_t jasper_construct_##id(const void* vectors, int64_t n_vectors, int64_t dim,          \
+                                double alpha, int64_t workspace_budget_bytes, bool on_host,   \
+                                void* stream);                                                \
+  /* Search_ :302-369; queries [n_queries, dim] fp16 on device */                             \
+  int64_t jasper_search_##id(int64_t handle, const void* queries, int64_t n_queries,          \
+                             int64_t dim, int32_t* out_indices, float* out_distances,         \
+                             int64_t k, int64_t beam_width, int64_t limit,                    \
+                             bool print_throughput, void* stream);                            \
+  /* SaveGraph_ :221-230 */                                                                   \
+  int64_t jasper_save_##id(int64_t handle, const char* path);                                 \
+  /* GetVector_ :263-300; out: [dim] fp16 device */                                           \
+  int64_t jasper_get_vector_##id(int64_t handle, int64_t stable_id, void* out, void* stream); \
+  /* MarkDeleted_ :371-386 (next tier: returns an error) */                                   \
+  int64_t jasper_mark_deleted_##id(int64_t handle, const int32_t* ids, int64_t n_ids);        \
+  /* Consolidate_ :388-397 (next tier: returns an error) */                                   \
+  int64_t jasper_consolidate_##id(int64_t handle, double alpha);                              \
+  /* Compact_ :399-408 (next tier: returns an error) */                                       \
+  int64_t jasper_compact_##id(int64_t handle);                                                \
+  /* Append_ :412-430 (next tier: returns an error) */                                        \
+  int64_t jasper_append_##id(int64_t handle, const void* vectors, int64_t n_vectors,          \
+                             double alpha, int32_t* out_ids, void* stream);
+
+/* ---- per directional config (DEFINE_DIRECTIONAL_OPS, :442-775) ---- */
+#define JASPER_DECLARE_DIRECTIONAL(id)                                                        \
+  /* ConstructDirectionalGraph_ :444-486 -> handle */                                         \
+  int64_t jasper_construct_directional_##id(const void* vectors, int64_t n_vectors,           \
+                                            int64_t dim, double alpha,                        \
+                                            int64_t workspace_budget_bytes, bool on_host,     \
+                                            bool prerotate, int64_t prerotate_seed,           \
+                                            void* stream);                                    \
+  /* BuildLsh_ :488-505 */                                                                    \
+  int64_t jasper_build_lsh_##id(int64_t handle, int64_t n_samples, int64_t seed);             \
+  /* BuildPq_ :507-528 */                                                                     \
+  int64_t jasper_build_pq_##id(int64_t handle, int64_t n_train, int64_t kmeans_iter,          \
+                               int64_t seed);                                                 \
+  /* DirectionalSearch_ :530-608 */                                                           \
+  int64_t jasper_directional_search_##id(int64_t handle, const void* queries,                 \
+                                         int64_t n_queries, int64_t dim,                      \
+                                         int32_t* out_indices, float* out_distances,          \
+                                         int64_t k, int64_t beam_width, int64_t limit,        \
+                                         bool print_throughput, void* stream);                \
+  /* PqSearch_ :610-688 */                                                                    \
+  int64_t jasper_pq_search_##id(int64_t handle, const void* queries, int64_t n_queries,       \
+                                int64_t dim, int32_t* out_indices, float* out_distances,      \
+                                int64_t k, int64_t beam_width, int64_t limit,                 \
+                                bool print_throughput, void* stream);                         \
+  /* SaveDirectionalGraph_ :690-710 */                                                        \
+  int64_t jasper_save_directional_##id(int64_t handle, const char* path);                     \
+  /* LoadDirectionalGraph_ :712-733 -> handle */                                              \
+  int64_t jasper_load_directional_##id(const char* path, int64_t dim, bool on_host,           \
+                                       bool prerotate, int64_t prerotate_seed);               \
+  /* GetVectorDirectional_ :735-763 */                                                        \
+  int64_t jasper_get_vector_directional_##id(int64_t handle, int64_t index, void* out,        \
+                                             void* stream);                                   \
+  /* GetDirectionalFlags_ :765-775: bit 0 = LSH, bit 1 = PQ */                                \
+  int64_t jasper_get_directional_flags_##id(int64_t handle);
+
+JASPER_PLAIN_CONFIGS(JASPER_DECLARE_PLAIN)
+JASPER_DIRECTIONAL_CONFIGS(JASPER_DECLARE_DIRECTIONAL)
+
+/* ---- config-agnostic (ffi/jasper_ffi_plain.cu:19-131) ---- */
+int64_t jasper_free_graph(int64_t handle);            /* FreeGraph :19-47 */
+int64_t jasper_get_n_vectors(int64_t handle);         /* GetNumVectors :50-61 */
+int64_t jasper_get_n_tombstoned(int64_t handle);      /* GetNumTombstoned :63-74 */
+int64_t jasper_get_n_live(int64_t handle);            /* GetNumLive :96-107 */
+int64_t jasper_reserve_ids(int64_t handle, int32_t* out_ids, int64_t count); /* ReserveIds :78-94 */
+int64_t jasper_get_dim(int64_t handle);               /* GetDim :109-120 */
+
+/* Error message of the last failed call on this thread (no reference
+ * counterpart: TVM-FFI carried the message in the raised exception). */
+const char* jasper_last_error(void);
+
+/* ---- extensions without a reference counterpart ----
+ * For parity tests and measurement: copy a graph's columns to host buffers
+ * (edges [n, R] u32, edge distances [n, R] bf16 bits, counts [n] u8; any
+ * pointer may be NULL), and the per-stage timing of the last construction
+ * (ms: search, forward prune, reverse grouping, reverse prune, total;
+ * plus batches and max batch size) when JASPER_BUILD_TIMING=1 was set. */
+int64_t jasperx_export_graph(int64_t handle, uint32_t* edges, uint16_t* edge_dist, uint8_t* counts);
+int64_t jasperx_last_build_stats(double* out7);
+/* Measurement run of the plain search: same traversal with an exact
+ * per-query seen set, writing per-query work counters to host memory
+ * out_stats[n_queries * 4] = {hops, sum of degrees read, vectors scored, 0}.
+ * Used to compute algorithmic bytes per launch; not a search entry point. */
+int64_t jasperx_search_stats(int64_t handle, const void* queries, int64_t n_queries, int64_t dim,
+                             int64_t k, int64_t beam_width, int64_t limit, uint32_t* out_stats,
+                             void* stream);
+/* Library build identifier (git-independent), for load checks. */
+const char* jasperx_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JASPER_AMD_H */

@@ -1,0 +1,414 @@
+// build.hip -- batched Vamana construction (reference index/construct.cuh).
+//
+// Per batch [s, s + b) of vertex ids (reference process_batch, :743-911):
+//   1. beam search of every batch vector against the pre-batch graph
+//      (the plain search kernel in "visited" mode: k = bw = 64, limit 256,
+//      at most 256 pops recorded);
+//   2. forward merge + RobustPrune, one wave per batch vertex: candidates are
+//      the vertex's existing edges (stored bf16 distances) and its popped
+//      nodes; the new edges and the reverse pairs (target << 32 | source)
+//      are written in the same kernel (merge_candidates_kernel,
+//      robust_prune_kernel and fill_reverse_edges, :280-501);
+//   3. radix sort of the reverse pairs and a head-marking pass, which groups
+//      them by target with sources ascending (:846-879);
+//   4. reverse merge + RobustPrune, one wave per target
+//      (process_reverse_edges_kernel, :560-741).
+// Batches grow 1, 2, 4, ... up to the maximum batch size (:913-958).
+//
+// The reference keeps an arbitrary arrival-order subset when one target gets
+// more than 256 + R candidates in a batch (atomicAdd slots, :642-658). This
+// implementation fixes that order: existing edges in slot order, then new
+// sources in ascending id order. It is one of the orders the reference can
+// produce, and it makes the build deterministic.
+#include "build.hpp"
+#include "common.hpp"
+#include "prune.hpp"
+#include "search.hpp"
+
+#include <algorithm>
+#include <vector>
+
+namespace jasper_amd {
+
+constexpr uint32_t kBuildL = 64;          // graph_construct_config L (ffi/jasper_ffi_common.cuh:58-59)
+constexpr uint32_t kBuildLimit = 256;     // BEAM_SEARCH_LIMIT (construct.cuh:57)
+constexpr uint32_t kBuildMaxResult = 256; // beam_search_max_result_size (construct.cuh:62)
+constexpr uint32_t kCandBuf = 512;        // >= 256 + R, power of two
+
+int64_t reference_max_batch(int64_t n, uint32_t R, int64_t budget_bytes) {
+  const int64_t L = kBuildL, max_result = kBuildMaxResult, max_cands = max_result + R;
+  const int64_t per_item = 8 * L + 8 * max_result + 4 + 8 * max_cands + 4 + 8 * (int64_t)R + 4 * (int64_t)R +
+                           4 * (int64_t)R;
+  const int64_t fixed = 4;
+  int64_t b = budget_bytes <= fixed ? 0 : (budget_bytes - fixed) / per_item;
+  b = std::min<int64_t>(b, 0xFFFFFFFFll);
+  return std::min<int64_t>(b, n / 50);
+}
+
+struct PruneKernelArgs {
+  PruneCtx pc;
+  uint32_t* edges;
+  uint16_t* edist;
+  uint8_t* counts;
+  // forward
+  const uint64_t* visited;
+  const uint32_t* visited_counts;
+  uint32_t batch_offset;
+  uint64_t* pairs;
+  // reverse
+  const uint64_t* sorted_pairs;
+  uint32_t n_pairs;
+  const uint32_t* heads;
+  const uint32_t* n_heads;
+};
+
+// Appends the existing edges of v to C (keys with their stored bf16
+// distances); returns how many were appended.
+__device__ __forceinline__ uint32_t gather_existing(const PruneKernelArgs& a, uint32_t v, uint64_t* C) {
+  const uint32_t lane = lane_id();
+  const uint32_t R = a.pc.R;
+  const uint32_t cnt = a.counts[v];
+  bool ok = false;
+  uint64_t key = kEmptyKey;
+  if (lane < cnt && lane < R) {
+    const uint32_t id = a.edges[(size_t)v * R + lane];
+    ok = id != kInvalid32;
+    key = make_key(bf2f(a.edist[(size_t)v * R + lane]), id);
+  }
+  const uint64_t m = ballot(ok);
+  if (ok) C[mbcnt(m)] = key;
+  return (uint32_t)__builtin_popcountll(m);
+}
+
+__device__ __forceinline__ void sort_candidates(uint64_t* C, uint32_t nc) {
+  const uint32_t N = max(pow2_ceil(nc), 2u);
+  for (uint32_t i = nc + lane_id(); i < N; i += 64) C[i] = kEmptyKey;
+  wave_sync();
+  lds_bitonic_sort(C, N);
+}
+
+__device__ __forceinline__ void write_selection(const PruneKernelArgs& a, uint32_t v, uint32_t ns,
+                                                const uint32_t* S_ids, const float* S_dist) {
+  const uint32_t lane = lane_id();
+  const uint32_t R = a.pc.R;
+  if (lane < ns) {
+    a.edges[(size_t)v * R + lane] = S_ids[lane];
+    a.edist[(size_t)v * R + lane] = f2bf(S_dist[lane]);
+  }
+  if (lane == 0) a.counts[v] = (uint8_t)ns;
+}
+
+struct PruneLds {
+  uint64_t* C;
+  uint32_t* S_ids;
+  float* S_dist;
+  uint32_t* srcs;
+  uint4* Scache;
+};
+
+__device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) {
+  PruneLds l;
+  l.C = smem;
+  l.S_ids = reinterpret_cast<uint32_t*>(smem + kCandBuf);
+  l.S_dist = reinterpret_cast<float*>(l.S_ids + 64);
+  l.srcs = reinterpret_cast<uint32_t*>(l.S_dist + 64);
+  l.Scache = reinterpret_cast<uint4*>(l.srcs + kCandBuf);
+  (void)R;
+  return l;
+}
+
+static size_t prune_lds_bytes(uint32_t R, uint32_t nchunks) {
+  return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4 + (size_t)R * nchunks * 16;
+}
+
+template <int CPL, int METRIC>
+__global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
+  extern __shared__ uint64_t smem[];
+  const PruneLds l = carve_prune_lds(smem, a.pc.R);
+  const uint32_t lane = lane_id();
+  const uint32_t bid = blockIdx.x;
+  const uint32_t v = a.batch_offset + bid;
+  const uint32_t R = a.pc.R;
+
+  uint32_t nc = gather_existing(a, v, l.C);
+  const uint32_t nv = a.visited_counts[bid];
+  for (uint32_t base = 0; base < nv; base += 64) {
+    const uint32_t i = base + lane;
+    bool ok = i < nv;
+    uint64_t key = 0;
+    if (ok) {
+      key = a.visited[(size_t)bid * kBuildMaxResult + i] & ~1ull;
+      ok = key_id(key) != v;
+    }
+    const uint64_t m = ballot(ok);
+    if (ok) l.C[nc + mbcnt(m)] = key;
+    nc += (uint32_t)__builtin_popcountll(m);
+  }
+  wave_sync();
+  sort_candidates(l.C, nc);
+  const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, l.Scache);
+  write_selection(a, v, ns, l.S_ids, l.S_dist);
+  if (lane < R) {
+    a.pairs[(size_t)bid * R + lane] = lane < ns ? (((uint64_t)l.S_ids[lane] << 32) | v) : kEmptyKey;
+  }
+}
+
+__global__ void mark_heads_kernel(const uint64_t* sorted, uint32_t n, uint32_t* heads, uint32_t* n_heads) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t k = sorted[i];
+  if (k == kEmptyKey) return;
+  if (i == 0 || (sorted[i - 1] >> 32) != (k >> 32)) heads[atomicAdd(n_heads, 1u)] = i;
+}
+
+template <int CPL, int METRIC>
+__global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
+  extern __shared__ uint64_t smem[];
+  const PruneLds l = carve_prune_lds(smem, a.pc.R);
+  const uint32_t lane = lane_id();
+  const uint32_t ql = lane & 3u, qg = lane >> 2;
+  const uint32_t R = a.pc.R;
+  const uint32_t nh = *a.n_heads;
+  const uint32_t max_cands = kBuildMaxResult + R;
+  for (uint32_t h = blockIdx.x; h < nh; h += gridDim.x) {
+    const uint32_t start = a.heads[h];
+    const uint32_t w = (uint32_t)(a.sorted_pairs[start] >> 32);
+    const uint32_t nE = gather_existing(a, w, l.C);
+    // sources of w in ascending id order, self skipped, capped at 256 + R
+    const uint32_t cap = max_cands - nE;
+    uint32_t taken = 0;
+    for (uint32_t pos = start; taken < cap; pos += 64) {
+      const uint32_t i = pos + lane;
+      const uint64_t key = i < a.n_pairs ? a.sorted_pairs[i] : kEmptyKey;
+      const bool same = key != kEmptyKey && (uint32_t)(key >> 32) == w;
+      const uint32_t src = (uint32_t)key;
+      const bool ok = same && src != w;
+      const uint64_t m = ballot(ok);
+      const uint32_t rank = mbcnt(m);
+      if (ok && taken + rank < cap) l.srcs[taken + rank] = src;
+      taken = min(cap, taken + (uint32_t)__builtin_popcountll(m));
+      if (ballot(!same)) break;
+    }
+    wave_sync();
+    // d(w, v) for every source (compute_distance(src_vec = w, sink_vec = v))
+    float wf[CPL * 8];
+    {
+      uint4 xw[CPL];
+      load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
+      frag_from_rows<CPL, METRIC>(xw, ql, wf);
+    }
+    for (uint32_t base = 0; base < taken; base += 16) {
+      const uint32_t j = base + qg;
+      const bool act = j < taken;
+      const uint32_t sid = act ? l.srcs[j] : 0u;
+      uint4 xs[CPL];
+      load_row_frag<CPL>(a.pc.vecs + (size_t)sid * a.pc.nchunks, ql, a.pc.nchunks, act, xs);
+      const float d = quad_finish<METRIC>(quad_partial<CPL, METRIC>(wf, xs, ql, a.pc.nlimit));
+      if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
+    }
+    wave_sync();
+    const uint32_t nc = nE + taken;
+    sort_candidates(l.C, nc);
+    const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, l.Scache);
+    write_selection(a, w, ns, l.S_ids, l.S_dist);
+    wave_sync();
+  }
+}
+
+template <int CPL, int METRIC>
+static void launch_forward(const PruneKernelArgs& a, uint32_t bs, size_t lds, hipStream_t s) {
+  auto k = forward_prune_kernel<CPL, METRIC>;
+  if (lds > 64 * 1024)
+    hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
+  hipLaunchKernelGGL(k, dim3(bs), dim3(64), lds, s, a);
+}
+
+template <int CPL, int METRIC>
+static void launch_reverse(const PruneKernelArgs& a, uint32_t grid, size_t lds, hipStream_t s) {
+  auto k = reverse_prune_kernel<CPL, METRIC>;
+  if (lds > 64 * 1024)
+    hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
+  hipLaunchKernelGGL(k, dim3(grid), dim3(64), lds, s, a);
+}
+
+template <int METRIC>
+static void dispatch_prune(bool reverse, uint32_t cpl, const PruneKernelArgs& a, uint32_t grid, size_t lds,
+                           hipStream_t s) {
+  switch (cpl) {
+#define JA_CASE(C)                                                   \
+  case C:                                                            \
+    if (reverse) launch_reverse<C, METRIC>(a, grid, lds, s);         \
+    else launch_forward<C, METRIC>(a, grid, lds, s);                 \
+    break;
+    JA_CASE(1)
+    JA_CASE(2)
+    JA_CASE(3)
+    JA_CASE(4)
+    JA_CASE(5)
+    JA_CASE(6)
+    JA_CASE(7)
+    JA_CASE(8)
+#undef JA_CASE
+    default:
+      throw std::invalid_argument("dimension above the supported maximum of 256 for construction");
+  }
+}
+
+struct EventTimer {
+  bool on;
+  hipStream_t s;
+  hipEvent_t e0, e1;
+  EventTimer(bool on_, hipStream_t s_) : on(on_), s(s_) {
+    if (on) { (void)hipEventCreate(&e0); (void)hipEventCreate(&e1); }
+  }
+  ~EventTimer() {
+    if (on) { (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); }
+  }
+  void start() { if (on) (void)hipEventRecord(e0, s); }
+  void stop(double& acc) {
+    if (!on) return;
+    (void)hipEventRecord(e1, s);
+    (void)hipEventSynchronize(e1);
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    acc += ms;
+  }
+};
+
+void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, bool time_stages,
+                 BuildStats* stats) {
+  if (g.n <= 0) return;
+  if (max_batch < 1) max_batch = 1;  // the reference loops forever here (n < 50); clamp instead
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  const uint32_t nchunks = g.dp / 8;
+  const uint32_t cpl = (nchunks + 3) / 4;
+  if (cpl > 8) throw std::invalid_argument("dimension above the supported maximum of 256 for construction");
+  const int64_t mb = std::min<int64_t>(max_batch, g.n);
+  const uint32_t R = g.R;
+
+  // workspace
+  uint64_t* visited = nullptr;
+  uint32_t* vcounts = nullptr;
+  uint64_t* pairs = nullptr;
+  uint64_t* sorted = nullptr;
+  uint32_t* heads = nullptr;
+  uint32_t* nheads = nullptr;
+  void* temp = nullptr;
+  const size_t max_pairs = (size_t)mb * R;
+  const size_t temp_bytes = sort_u64_temp_bytes(max_pairs);
+  auto cleanup = [&]() {
+    (void)hipFree(visited);
+    (void)hipFree(vcounts);
+    (void)hipFree(pairs);
+    (void)hipFree(sorted);
+    (void)hipFree(heads);
+    (void)hipFree(nheads);
+    (void)hipFree(temp);
+  };
+  try {
+    hip_check(hipMalloc(&visited, (size_t)mb * kBuildMaxResult * 8), "alloc build visited");
+    hip_check(hipMalloc(&vcounts, (size_t)mb * 4), "alloc build visited counts");
+    hip_check(hipMalloc(&pairs, max_pairs * 8), "alloc reverse pairs");
+    hip_check(hipMalloc(&sorted, max_pairs * 8), "alloc sorted pairs");
+    hip_check(hipMalloc(&heads, max_pairs * 4), "alloc heads");
+    hip_check(hipMalloc(&nheads, 4), "alloc head count");
+    hip_check(hipMalloc(&temp, std::max<size_t>(temp_bytes, 16)), "alloc sort temp");
+  } catch (...) {
+    cleanup();
+    throw;
+  }
+
+  int end_bit = 32;
+  while (end_bit < 64 && ((uint64_t)1 << (end_bit - 32)) <= (uint64_t)g.n) ++end_bit;
+
+  PruneKernelArgs pa{};
+  pa.pc.vecs = (const uint4*)g.vecs;
+  pa.pc.nchunks = nchunks;
+  pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;  // the reference prunes with `dim`
+  pa.pc.R = R;
+  pa.pc.alpha = alpha;
+  pa.edges = g.edges;
+  pa.edist = g.edist;
+  pa.counts = g.counts;
+  pa.visited = visited;
+  pa.visited_counts = vcounts;
+  pa.pairs = pairs;
+  pa.sorted_pairs = sorted;
+  pa.heads = heads;
+  pa.n_heads = nheads;
+  const size_t plds = prune_lds_bytes(R, nchunks);
+
+  BuildStats st;
+  st.max_batch = mb;
+  EventTimer timer(time_stages, stream);
+  hipEvent_t t0, t1;
+  hip_check(hipEventCreate(&t0), "event");
+  hip_check(hipEventCreate(&t1), "event");
+  hip_check(hipEventRecord(t0, stream), "event record");
+  try {
+    int64_t count = 0, bs = 1;
+    while (count < g.n) {
+      bs = std::min<int64_t>(bs, g.n - count);
+      bs = std::min<int64_t>(bs, mb);
+      // 1. beam search of the batch against the pre-batch graph
+      SearchRequest r;
+      r.use_range = true;
+      r.q_start = (uint32_t)count;
+      r.nq = (uint32_t)bs;
+      r.medoid = g.medoid;
+      r.k = kBuildL;
+      r.beam_width = kBuildL;
+      r.limit = kBuildLimit;
+      r.max_result = kBuildMaxResult;
+      r.visited = visited;
+      r.visited_counts = vcounts;
+      r.hash_bits = 12;
+      timer.start();
+      launch_beam_search(g, r, stream);
+      timer.stop(st.search_ms);
+      // 2. forward merge + prune + reverse pairs
+      pa.batch_offset = (uint32_t)count;
+      timer.start();
+      if (g.metric == kL2) dispatch_prune<kL2>(false, cpl, pa, (uint32_t)bs, plds, stream);
+      else dispatch_prune<kIP>(false, cpl, pa, (uint32_t)bs, plds, stream);
+      hip_check(hipGetLastError(), "launch forward_prune_kernel");
+      timer.stop(st.prune_ms);
+      // 3. group reverse pairs by target
+      const uint32_t np = (uint32_t)(bs * R);
+      timer.start();
+      sort_u64(temp, temp_bytes, pairs, sorted, np, end_bit, stream);
+      hip_check(hipMemsetAsync(nheads, 0, 4, stream), "clear head count");
+      hipLaunchKernelGGL(mark_heads_kernel, dim3((np + 255) / 256), dim3(256), 0, stream, sorted, np, heads, nheads);
+      hip_check(hipGetLastError(), "launch mark_heads_kernel");
+      timer.stop(st.sort_ms);
+      // 4. reverse merge + prune
+      pa.n_pairs = np;
+      const uint32_t grid = (uint32_t)std::min<int64_t>(std::max<int64_t>(np, 1), 16384);
+      timer.start();
+      if (g.metric == kL2) dispatch_prune<kL2>(true, cpl, pa, grid, plds, stream);
+      else dispatch_prune<kIP>(true, cpl, pa, grid, plds, stream);
+      hip_check(hipGetLastError(), "launch reverse_prune_kernel");
+      timer.stop(st.reverse_ms);
+      count += bs;
+      st.batches += 1;
+      if (bs < mb) bs = std::min<int64_t>(mb, bs * 2);
+    }
+    hip_check(hipEventRecord(t1, stream), "event record");
+    hip_check(hipStreamSynchronize(stream), "build synchronize");
+    float total = 0;
+    hip_check(hipEventElapsedTime(&total, t0, t1), "event elapsed");
+    st.total_ms = total;
+  } catch (...) {
+    (void)hipStreamSynchronize(stream);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    cleanup();
+    throw;
+  }
+  (void)hipEventDestroy(t0);
+  (void)hipEventDestroy(t1);
+  cleanup();
+  if (stats) *stats = st;
+}
+
+}  // namespace jasper_amd

@@ -1,0 +1,496 @@
+// capi.hip -- the C ABI (include/jasper_amd.h): handle table, argument
+// checks, and the per-config entry points named like the reference's
+// TVM-FFI exports (ffi/jasper_ffi_common.cuh:787-807, ffi/jasper_ffi_plain.cu).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <algorithm>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/jasper_amd.h"
+#include "build.hpp"
+#include "common.hpp"
+#include "directional_api.hpp"
+#include "graph.hpp"
+#include "search.hpp"
+
+namespace jasper_amd {
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Entry {
+  std::unique_ptr<Graph> g;
+  bool directional = false;
+};
+
+std::unordered_map<int64_t, Entry> g_table;
+std::mutex g_mutex;
+int64_t g_next_handle = 0;
+BuildStats g_last_build;
+
+struct Config {
+  uint32_t R;
+  int metric;
+  bool directional;
+  uint32_t k_ranks;
+  bool small_dim;  // dim <= 128 (packed_t = u8)
+};
+
+int64_t fail(const std::string& msg) {
+  g_last_error = msg;
+  return -1;
+}
+
+template <typename F>
+int64_t guarded(F&& f) {
+  try {
+    return f();
+  } catch (const std::exception& e) {
+    return fail(e.what());
+  } catch (...) {
+    return fail("unknown error");
+  }
+}
+
+int64_t insert(std::unique_ptr<Graph> g, bool directional) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  const int64_t h = g_next_handle++;
+  g_table[h] = Entry{std::move(g), directional};
+  return h;
+}
+
+// Handle lookup under the table lock; operations run outside the lock, as
+// in the reference (ffi/jasper_ffi_common.cuh:308-314).
+Graph& lookup(int64_t handle, const Config* cfg) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  auto it = g_table.find(handle);
+  if (it == g_table.end()) throw std::invalid_argument("Invalid handle: " + std::to_string(handle));
+  Graph& g = *it->second.g;
+  if (cfg) {
+    if (cfg->directional != it->second.directional || g.R != cfg->R || g.metric != cfg->metric ||
+        (cfg->directional && g.k_ranks != cfg->k_ranks))
+      throw std::invalid_argument("handle " + std::to_string(handle) + " was created with a different config");
+  }
+  return g;
+}
+
+bool is_device_ptr(const void* p) {
+  if (!p) return false;
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+// Queries as device rows of padded length g.dp (copying when the caller's
+// rows are unpadded, misaligned or in host memory).
+struct QueryRows {
+  const void* ptr = nullptr;
+  void* owned = nullptr;
+  hipStream_t stream = nullptr;
+  ~QueryRows() {
+    if (owned) (void)hipFreeAsync(owned, stream);
+  }
+};
+
+void prepare_queries(const Graph& g, const void* q, int64_t nq, int64_t dim, hipStream_t s, QueryRows& out) {
+  if (dim != (int64_t)g.dim)
+    throw std::invalid_argument("query dim (" + std::to_string(dim) + ") != graph dim (" + std::to_string(g.dim) + ")");
+  out.stream = s;
+  const bool aligned = ((uintptr_t)q % 16) == 0;
+  if (g.dp == g.dim && aligned && is_device_ptr(q)) {
+    out.ptr = q;
+    return;
+  }
+  hip_check(hipMallocAsync(&out.owned, (size_t)nq * g.dp * 2 + 16, s), "alloc padded queries");
+  hip_check(hipMemsetAsync(out.owned, 0, (size_t)nq * g.dp * 2, s), "clear padded queries");
+  hip_check(hipMemcpy2DAsync(out.owned, (size_t)g.dp * 2, q, (size_t)dim * 2, (size_t)dim * 2, (size_t)nq,
+                             hipMemcpyDefault, s),
+            "copy queries");
+  out.ptr = out.owned;
+}
+
+int64_t do_search(const Config& cfg, int64_t handle, const void* queries, int64_t nq, int64_t dim, int32_t* out_idx,
+                  float* out_dist, int64_t k, int64_t bw, int64_t limit, bool print, void* stream) {
+  Graph& g = lookup(handle, &cfg);
+  if (nq < 0 || k < 0 || bw <= 0 || limit < 0) throw std::invalid_argument("negative size argument");
+  if (nq == 0 || k == 0) return 0;
+  if (!is_device_ptr(out_idx) || !is_device_ptr(out_dist))
+    throw std::invalid_argument("search outputs must be device memory");
+  if (nq > 0x7FFFFFFF) throw std::invalid_argument("too many queries");
+  hipStream_t s = (hipStream_t)stream;
+  QueryRows rows;
+  prepare_queries(g, queries, nq, dim, s, rows);
+  SearchRequest r;
+  r.queries = rows.ptr;
+  r.nq = (uint32_t)nq;
+  r.medoid = g.medoid;
+  r.k = (uint32_t)k;
+  r.beam_width = (uint32_t)bw;
+  r.limit = (uint32_t)limit;
+  r.max_result = 2048;  // search_params default (beam_search/api.cuh:17)
+  r.out_ids = out_idx;
+  r.out_dists = out_dist;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (print) {
+    hip_check(hipEventCreate(&e0), "event");
+    hip_check(hipEventCreate(&e1), "event");
+    hip_check(hipEventRecord(e0, s), "event record");
+  }
+  launch_beam_search(g, r, s);
+  if (print) {
+    hip_check(hipEventRecord(e1, s), "event record");
+    hip_check(hipEventSynchronize(e1), "event sync");
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    std::printf("[beam_search] duration=%gms, throughput=%g\n", ms, nq * 1000.0 / ms);
+    std::fflush(stdout);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  return 0;
+}
+
+std::unique_ptr<Graph> construct(const Config& cfg, const void* vectors, int64_t n, int64_t dim, double alpha,
+                                 int64_t budget, bool on_host, hipStream_t s) {
+  if (n <= 0) throw std::invalid_argument("vectors must contain at least one row");
+  if (n > 0x7FFFFFFF) throw std::invalid_argument("too many vectors for 31-bit ids");
+  if (dim <= 0) throw std::invalid_argument("dim must be positive");
+  auto g = std::make_unique<Graph>();
+  g->allocate(n, (uint32_t)dim, cfg.R, cfg.metric, on_host);
+  upload_vectors(*g, vectors, n, (uint32_t)dim, s);
+  const int64_t mbs = reference_max_batch(n, cfg.R, budget);
+  const char* timing = std::getenv("JASPER_BUILD_TIMING");
+  const bool time_stages = timing && timing[0] == '1';
+  BuildStats st;
+  build_graph(*g, (float)alpha, mbs, s, time_stages, &st);
+  g->next_id = (uint64_t)n;  // identity stable ids (id_map.cuh:260-281)
+  {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    g_last_build = st;
+  }
+  if (time_stages) {
+    std::printf("[construct] n=%lld batches=%lld max_batch=%lld search=%.1fms prune=%.1fms group=%.1fms "
+                "reverse=%.1fms total=%.1fms\n",
+                (long long)n, (long long)st.batches, (long long)st.max_batch, st.search_ms, st.prune_ms, st.sort_ms,
+                st.reverse_ms, st.total_ms);
+    std::fflush(stdout);
+  }
+  return g;
+}
+
+int64_t get_vector(Graph& g, int64_t index, void* out, hipStream_t s) {
+  if (index < 0 || index >= g.n) throw std::out_of_range("Stable id " + std::to_string(index) + " not found");
+  hip_check(hipMemcpyAsync(out, (const char*)g.vecs + (size_t)index * g.dp * 2, (size_t)g.dim * 2, hipMemcpyDefault, s),
+            "copy vector");
+  hip_check(hipStreamSynchronize(s), "sync");
+  return 0;
+}
+
+}  // namespace
+}  // namespace jasper_amd
+
+using namespace jasper_amd;
+
+#define JA_DEFINE_PLAIN(id)                                                                                    \
+  extern "C" int64_t jasper_load_##id(const char* path, int64_t dim, bool on_host) {                           \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      if (!path) throw std::invalid_argument("null path");                                                     \
+      auto g = load_graph_file(path, (uint32_t)dim, c.R, c.metric, on_host, nullptr);                          \
+      return insert(std::move(g), false);                                                                      \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_construct_##id(const void* vectors, int64_t n, int64_t dim, double alpha,          \
+                                           int64_t budget, bool on_host, void* stream) {                       \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      auto g = construct(c, vectors, n, dim, alpha, budget, on_host, (hipStream_t)stream);                     \
+      return insert(std::move(g), false);                                                                      \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_search_##id(int64_t h, const void* q, int64_t nq, int64_t dim, int32_t* oi,        \
+                                        float* od, int64_t k, int64_t bw, int64_t limit, bool print,           \
+                                        void* stream) {                                                        \
+    return guarded([&]() -> int64_t {                                                                          \
+      return do_search(config_of(#id), h, q, nq, dim, oi, od, k, bw, limit, print, stream);                    \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_save_##id(int64_t h, const char* path) {                                           \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      save_graph_file(lookup(h, &c), path);                                                                    \
+      return 0;                                                                                                \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_get_vector_##id(int64_t h, int64_t index, void* out, void* stream) {               \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      return get_vector(lookup(h, &c), index, out, (hipStream_t)stream);                                       \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_mark_deleted_##id(int64_t h, const int32_t* ids, int64_t n_ids) {                  \
+    (void)ids;                                                                                                 \
+    (void)n_ids;                                                                                               \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      lookup(h, &c);                                                                                           \
+      throw std::runtime_error("mark_deleted is not supported by this build (live updates are out of scope)"); \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_consolidate_##id(int64_t h, double alpha) {                                        \
+    (void)alpha;                                                                                               \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      lookup(h, &c);                                                                                           \
+      throw std::runtime_error("consolidate is not supported by this build (live updates are out of scope)");  \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_compact_##id(int64_t h) {                                                          \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      lookup(h, &c);                                                                                           \
+      throw std::runtime_error("compact is not supported by this build (live updates are out of scope)");      \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_append_##id(int64_t h, const void* v, int64_t n, double alpha, int32_t* out_ids,   \
+                                        void* stream) {                                                        \
+    (void)v;                                                                                                   \
+    (void)n;                                                                                                   \
+    (void)alpha;                                                                                               \
+    (void)out_ids;                                                                                             \
+    (void)stream;                                                                                              \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      lookup(h, &c);                                                                                           \
+      throw std::runtime_error("append is not supported by this build (live updates are out of scope)");       \
+    });                                                                                                        \
+  }
+
+namespace jasper_amd {
+namespace {
+// Parses a config id such as "f16_r64_l2" or "f16_r64_ip_k16_d128".
+Config config_of(const char* id) {
+  Config c{};
+  const std::string s(id);
+  const size_t r = s.find("_r");
+  c.R = (uint32_t)std::atoi(s.c_str() + r + 2);
+  c.metric = s.find("_ip") != std::string::npos ? kIP : kL2;
+  const size_t k = s.find("_k");
+  c.directional = k != std::string::npos;
+  c.k_ranks = c.directional ? (uint32_t)std::atoi(s.c_str() + k + 2) : 0;
+  c.small_dim = s.find("_d128") != std::string::npos;
+  return c;
+}
+}  // namespace
+}  // namespace jasper_amd
+
+JASPER_PLAIN_CONFIGS(JA_DEFINE_PLAIN)
+
+#define JA_DEFINE_DIRECTIONAL(id)                                                                              \
+  extern "C" int64_t jasper_construct_directional_##id(const void* vectors, int64_t n, int64_t dim,            \
+                                                       double alpha, int64_t budget, bool on_host,             \
+                                                       bool prerotate, int64_t seed, void* stream) {           \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      check_directional_dim(c.small_dim, dim);                                                                 \
+      auto g = construct_directional(c.R, c.metric, c.k_ranks, c.small_dim, vectors, n, dim, alpha, budget,    \
+                                     on_host, prerotate, (uint64_t)seed, (hipStream_t)stream, &g_last_build);  \
+      return insert(std::move(g), true);                                                                       \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_build_lsh_##id(int64_t h, int64_t n_samples, int64_t seed) {                       \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      build_lsh(lookup(h, &c), n_samples, (uint64_t)seed);                                                     \
+      return 0;                                                                                                \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_build_pq_##id(int64_t h, int64_t n_train, int64_t iters, int64_t seed) {           \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      build_pq(lookup(h, &c), n_train, iters, (uint64_t)seed);                                                 \
+      return 0;                                                                                                \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_directional_search_##id(int64_t h, const void* q, int64_t nq, int64_t dim,         \
+                                                    int32_t* oi, float* od, int64_t k, int64_t bw,             \
+                                                    int64_t limit, bool print, void* stream) {                 \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      directional_search(lookup(h, &c), false, q, nq, dim, oi, od, k, bw, limit, print, (hipStream_t)stream);  \
+      return 0;                                                                                                \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_pq_search_##id(int64_t h, const void* q, int64_t nq, int64_t dim, int32_t* oi,     \
+                                           float* od, int64_t k, int64_t bw, int64_t limit, bool print,        \
+                                           void* stream) {                                                     \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      directional_search(lookup(h, &c), true, q, nq, dim, oi, od, k, bw, limit, print, (hipStream_t)stream);   \
+      return 0;                                                                                                \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_save_directional_##id(int64_t h, const char* path) {                               \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      if (!path) throw std::invalid_argument("null path");                                                     \
+      save_directional_file(lookup(h, &c), path);                                                              \
+      return 0;                                                                                                \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_load_directional_##id(const char* path, int64_t dim, bool on_host, bool prerotate, \
+                                                  int64_t seed) {                                              \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      if (!path) throw std::invalid_argument("null path");                                                     \
+      check_directional_dim(c.small_dim, dim);                                                                 \
+      auto g = load_directional_file(path, (uint32_t)dim, c.R, c.metric, c.k_ranks, c.small_dim, on_host,      \
+                                     prerotate, (uint64_t)seed);                                               \
+      return insert(std::move(g), true);                                                                       \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_get_vector_directional_##id(int64_t h, int64_t index, void* out, void* stream) {   \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      return get_vector(lookup(h, &c), index, out, (hipStream_t)stream);                                       \
+    });                                                                                                        \
+  }                                                                                                            \
+  extern "C" int64_t jasper_get_directional_flags_##id(int64_t h) {                                            \
+    return guarded([&]() -> int64_t {                                                                          \
+      const Config c = config_of(#id);                                                                         \
+      Graph& g = lookup(h, &c);                                                                                \
+      return (int64_t)((g.lsh ? 1 : 0) | (g.pq ? 2 : 0));                                                      \
+    });                                                                                                        \
+  }
+
+JASPER_DIRECTIONAL_CONFIGS(JA_DEFINE_DIRECTIONAL)
+
+extern "C" int64_t jasper_free_graph(int64_t h) {
+  return guarded([&]() -> int64_t {
+    std::unique_ptr<Graph> victim;
+    {
+      std::lock_guard<std::mutex> lock(g_mutex);
+      auto it = g_table.find(h);
+      if (it == g_table.end()) throw std::invalid_argument("Invalid handle: " + std::to_string(h));
+      victim = std::move(it->second.g);
+      g_table.erase(it);
+    }
+    (void)hipDeviceSynchronize();
+    victim.reset();
+    return 0;
+  });
+}
+
+extern "C" int64_t jasper_get_n_vectors(int64_t h) {
+  return guarded([&]() -> int64_t { return lookup(h, nullptr).n; });
+}
+
+extern "C" int64_t jasper_get_n_tombstoned(int64_t h) {
+  return guarded([&]() -> int64_t { return (int64_t)lookup(h, nullptr).n_deleted; });
+}
+
+extern "C" int64_t jasper_get_n_live(int64_t h) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    return g.n - (int64_t)g.n_deleted;
+  });
+}
+
+extern "C" int64_t jasper_reserve_ids(int64_t h, int32_t* out_ids, int64_t count) {
+  return guarded([&]() -> int64_t {
+    if (count < 0) throw std::invalid_argument("negative count");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    auto it = g_table.find(h);
+    if (it == g_table.end()) throw std::invalid_argument("Invalid handle: " + std::to_string(h));
+    Graph& g = *it->second.g;
+    const uint64_t start = g.next_id;
+    g.next_id += (uint64_t)count;
+    for (int64_t i = 0; i < count; ++i) out_ids[i] = (int32_t)(start + (uint64_t)i);
+    return 0;
+  });
+}
+
+extern "C" int64_t jasper_get_dim(int64_t h) {
+  return guarded([&]() -> int64_t { return (int64_t)lookup(h, nullptr).dim; });
+}
+
+extern "C" const char* jasper_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int64_t jasperx_export_graph(int64_t h, uint32_t* edges, uint16_t* edge_dist, uint8_t* counts) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    HostGraph hg;
+    download_graph(g, hg, false);
+    if (edges) std::memcpy(edges, hg.edges.data(), hg.edges.size() * 4);
+    if (edge_dist) std::memcpy(edge_dist, hg.edist.data(), hg.edist.size() * 2);
+    if (counts) std::memcpy(counts, hg.counts.data(), hg.counts.size());
+    return g.n;
+  });
+}
+
+extern "C" int64_t jasperx_last_build_stats(double* out7) {
+  return guarded([&]() -> int64_t {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    const BuildStats& s = g_last_build;
+    const double v[7] = {s.search_ms, s.prune_ms, s.sort_ms, s.reverse_ms, s.total_ms, (double)s.batches,
+                         (double)s.max_batch};
+    std::memcpy(out7, v, sizeof(v));
+    return 0;
+  });
+}
+
+extern "C" int64_t jasperx_search_stats(int64_t h, const void* q, int64_t nq, int64_t dim, int64_t k, int64_t bw,
+                                        int64_t limit, uint32_t* out_stats, void* stream) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (nq <= 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    QueryRows rows;
+    prepare_queries(g, q, nq, dim, s, rows);
+    const size_t words = (size_t)((g.n + 31) / 32);
+    const size_t chunk = std::max<size_t>(1, std::min<size_t>((size_t)nq, ((size_t)1 << 31) / (words * 4)));
+    uint32_t* bits = nullptr;
+    uint32_t* st = nullptr;
+    hip_check(hipMalloc(&bits, chunk * words * 4), "alloc seen bitmap");
+    hip_check(hipMalloc(&st, chunk * 16), "alloc stats");
+    try {
+      for (size_t b = 0; b < (size_t)nq; b += chunk) {
+        const size_t m = std::min(chunk, (size_t)nq - b);
+        hip_check(hipMemsetAsync(bits, 0, m * words * 4, s), "clear seen bitmap");
+        SearchRequest r;
+        r.queries = (const char*)rows.ptr + b * g.dp * 2;
+        r.nq = (uint32_t)m;
+        r.medoid = g.medoid;
+        r.k = (uint32_t)k;
+        r.beam_width = (uint32_t)bw;
+        r.limit = (uint32_t)limit;
+        r.max_result = 2048;
+        r.seen_bits = bits;
+        r.stats = st;
+        launch_beam_search(g, r, s);
+        hip_check(hipMemcpyAsync(out_stats + b * 4, st, m * 16, hipMemcpyDeviceToHost, s), "copy stats");
+        hip_check(hipStreamSynchronize(s), "sync stats");
+      }
+    } catch (...) {
+      (void)hipFree(bits);
+      (void)hipFree(st);
+      throw;
+    }
+    (void)hipFree(bits);
+    (void)hipFree(st);
+    return 0;
+  });
+}
+
+extern "C" const char* jasperx_version(void) { return "jasper_amd 0.1 gfx950"; }

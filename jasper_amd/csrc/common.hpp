@@ -1,0 +1,272 @@
+// common.hpp -- device primitives shared by the search and build kernels.
+//
+// Wave64-first building blocks for gfx950:
+//   * 64-bit candidate keys that sort with one unsigned compare,
+//   * quad (4-lane) distance evaluation that reproduces the reference
+//     arithmetic bit for bit (reference include/jasper/distance/distance.cuh),
+//   * wave-wide bitonic sort of 64 keys held one per lane,
+//   * an LDS bitonic sort for up to 512 keys (one wave).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace jasper_amd {
+
+constexpr uint32_t kInvalid32 = 0xFFFFFFFFu;
+constexpr uint64_t kEmptyKey = ~0ull;
+
+enum Metric : int { kL2 = 0, kIP = 1 };
+
+// ----------------------------------------------------------------- keys --
+// A candidate is one u64: [63:32] order-preserving image of the fp32
+// distance, [31:1] the 31-bit vertex id, [0] the visited flag. Unsigned
+// comparison of (key >> 1) is the reference order "distance ascending, then
+// id ascending" (beam_search/device_kernels.cuh:132-151); -0.0 is folded onto
+// +0.0 so that the image agrees with the float comparison.
+
+__host__ __device__ __forceinline__ uint32_t dist_to_ord(float d) {
+  uint32_t b = __float_as_uint(d + 0.0f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__host__ __device__ __forceinline__ float ord_to_dist(uint32_t o) {
+  uint32_t b = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+  return __uint_as_float(b);
+}
+
+__host__ __device__ __forceinline__ uint64_t make_key(float d, uint32_t id) {
+  return ((uint64_t)dist_to_ord(d) << 32) | ((uint64_t)(id & 0x7FFFFFFFu) << 1);
+}
+
+__host__ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return (uint32_t)(k >> 1) & 0x7FFFFFFFu; }
+__host__ __device__ __forceinline__ float key_dist(uint64_t k) { return ord_to_dist((uint32_t)(k >> 32)); }
+__host__ __device__ __forceinline__ bool key_visited(uint64_t k) { return (k & 1ull) != 0; }
+__host__ __device__ __forceinline__ uint64_t key_rank(uint64_t k) { return k >> 1; }
+
+// fp32 -> bf16 bits, round to nearest even (the reference stores edge
+// distances with `(__nv_bfloat16)float`, index/graph.cuh:494).
+__host__ __device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__host__ __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ float h2f_lo(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w & 0xFFFFu))); }
+__device__ __forceinline__ float h2f_hi(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w >> 16))); }
+
+// ----------------------------------------------------------- wave helpers --
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// number of set bits of m below this lane
+__device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// LDS visibility between lanes of the one wave that owns a work-group.
+__device__ __forceinline__ void wave_sync() { __syncthreads(); }
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) { return __shfl_xor(v, m, 64); }
+
+// Quad butterfly (offset 2, then 1): every lane of the quad gets
+// (l0 + l2) + (l1 + l3), the combine order of cg::reduce over a 4-lane tile.
+__device__ __forceinline__ float quad_sum(float v) {
+  v = v + __shfl_xor(v, 2, 64);
+  v = v + __shfl_xor(v, 1, 64);
+  return v;
+}
+
+// Broadcast lane s of each quad to the whole quad (DPP quad_perm).
+template <int S>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+  constexpr int ctrl = S | (S << 2) | (S << 4) | (S << 6);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, false);
+}
+
+// Ascending bitonic sort of one key per lane over aligned blocks of W lanes
+// (W a power of two <= 64); lanes of other blocks are sorted independently.
+template <int W>
+__device__ __forceinline__ uint64_t wave_bitonic_sort(uint64_t x) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= W; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint64_t o = shfl_xor64(x, j);
+      const bool up = (lane & (uint32_t)k) == 0;
+      const bool lower = (lane & (uint32_t)j) == 0;
+      const bool take_min = (lower == up);
+      const uint64_t mn = x < o ? x : o;
+      const uint64_t mx = x < o ? o : x;
+      x = take_min ? mn : mx;
+    }
+  }
+  return x;
+}
+
+__device__ __forceinline__ uint64_t wave_sort_upto(uint64_t x, uint32_t n) {
+  if (n <= 1) return x;
+  if (n <= 2) return wave_bitonic_sort<2>(x);
+  if (n <= 4) return wave_bitonic_sort<4>(x);
+  if (n <= 8) return wave_bitonic_sort<8>(x);
+  if (n <= 16) return wave_bitonic_sort<16>(x);
+  if (n <= 32) return wave_bitonic_sort<32>(x);
+  return wave_bitonic_sort<64>(x);
+}
+
+// Ascending bitonic sort of buf[0..N) in LDS by one wave (N power of two).
+__device__ __forceinline__ void lds_bitonic_sort(uint64_t* buf, uint32_t N) {
+  const uint32_t lane = lane_id();
+  for (uint32_t k = 2; k <= N; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t t = lane; t < N / 2; t += 64) {
+        // t-th compare-exchange pair of this stage
+        const uint32_t lo = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+        const uint32_t hi = lo | j;
+        const uint64_t a = buf[lo], b = buf[hi];
+        const bool up = (lo & k) == 0;
+        const bool swap = up ? (a > b) : (a < b);
+        if (swap) { buf[lo] = b; buf[hi] = a; }
+      }
+      wave_sync();
+    }
+  }
+}
+
+// Number of entries of sorted keys[0..cnt) whose rank is below `r`
+// (branch-free lower bound; `top` is a power of two >= cnt).
+__device__ __forceinline__ uint32_t lds_lower_bound(const uint64_t* keys, uint32_t cnt, uint32_t top,
+                                                    uint64_t r) {
+  uint32_t lo = 0;
+  for (uint32_t step = top; step > 0; step >>= 1) {
+    const uint32_t probe = lo + step;
+    if (probe <= cnt && key_rank(keys[probe - 1]) < r) lo = probe;
+  }
+  return lo;
+}
+
+__host__ __device__ __forceinline__ uint32_t pow2_ceil(uint32_t x) {
+  uint32_t p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+// -------------------------------------------------------------- distances --
+// Quad layout: the 4 lanes of a quad evaluate one distance. For L2, quad
+// lane l owns the 16-byte chunks l, l+4, l+8, ... (distance.cuh:108-143) and
+// accumulates fma(d, d, acc), d = f32(a) - f32(b), over the 8 halves of each
+// chunk in order; the quad sum is (l0 + l2) + (l1 + l3). For IP, reference
+// lane l owns the elements l, l+4, l+8, ... (distance.cuh:155-167); chunks
+// are loaded as for L2 and every chunk is broadcast across the quad so that
+// lane l can accumulate its two elements of each chunk in element order.
+
+// Load the query fragment a quad lane needs into fp32 registers.
+// src is a row of fp16 with at least nchunks*8 readable elements.
+template <int CPL, int METRIC>
+__device__ __forceinline__ void load_query_frag(const uint4* src, uint32_t ql, uint32_t nchunks,
+                                                float (&qf)[CPL * 8]) {
+  if constexpr (METRIC == kL2) {
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+      const uint32_t c = ql + 4u * (uint32_t)t;
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (c < nchunks) x = src[c];
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        qf[t * 8 + 2 * k] = h2f_lo(w[k]);
+        qf[t * 8 + 2 * k + 1] = h2f_hi(w[k]);
+      }
+    }
+  } else {
+    // IP: 2 elements per chunk for every chunk c < 4*CPL.
+#pragma unroll
+    for (int c = 0; c < 4 * CPL; ++c) {
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if ((uint32_t)c < nchunks) x = src[c];
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+      const uint32_t e0 = ql, e1 = ql + 4u;
+      const uint32_t w0 = w[e0 >> 1], w1 = w[e1 >> 1];
+      qf[2 * c] = (e0 & 1u) ? h2f_hi(w0) : h2f_lo(w0);
+      qf[2 * c + 1] = (e1 & 1u) ? h2f_hi(w1) : h2f_lo(w1);
+    }
+  }
+}
+
+// Issue the chunk loads of one vector row for quad lane ql.
+template <int CPL>
+__device__ __forceinline__ void load_row_frag(const uint4* row, uint32_t ql, uint32_t nchunks, bool active,
+                                              uint4 (&x)[CPL]) {
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const uint32_t c = ql + 4u * (uint32_t)t;
+    x[t] = make_uint4(0, 0, 0, 0);
+    if (active && c < nchunks) x[t] = row[c];
+  }
+}
+
+// Partial (per quad lane) accumulation; returns the lane partial.
+// L2: nlimit = number of chunks in the sum (dim / 8 of the reference call).
+// IP: nlimit = number of elements in the sum (the reference `dim`).
+template <int CPL, int METRIC>
+__device__ __forceinline__ float quad_partial(const float (&qf)[CPL * 8], const uint4 (&x)[CPL], uint32_t ql,
+                                              uint32_t nlimit) {
+  float acc = 0.0f;
+  if constexpr (METRIC == kL2) {
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+      const uint32_t c = ql + 4u * (uint32_t)t;
+      if (c < nlimit) {
+        const uint32_t w[4] = {x[t].x, x[t].y, x[t].z, x[t].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float d0 = qf[t * 8 + 2 * k] - h2f_lo(w[k]);
+          acc = __builtin_fmaf(d0, d0, acc);
+          const float d1 = qf[t * 8 + 2 * k + 1] - h2f_hi(w[k]);
+          acc = __builtin_fmaf(d1, d1, acc);
+        }
+      }
+    }
+  } else {
+    // element order within reference lane ql: chunk 0 (ql, ql+4), chunk 1, ...
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int c = 4 * t + s;  // chunk index, held by quad lane s in slot t
+        uint32_t w[4];
+        const uint32_t src[4] = {x[t].x, x[t].y, x[t].z, x[t].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (s == 0) w[k] = quad_bcast<0>(src[k]);
+          else if (s == 1) w[k] = quad_bcast<1>(src[k]);
+          else if (s == 2) w[k] = quad_bcast<2>(src[k]);
+          else w[k] = quad_bcast<3>(src[k]);
+        }
+        const uint32_t e0 = ql, e1 = ql + 4u;
+        const uint32_t w0 = (e0 >> 1) == 0 ? w[0] : w[1];
+        const uint32_t w1 = (e1 >> 1) == 2 ? w[2] : w[3];
+        const float v0 = (e0 & 1u) ? h2f_hi(w0) : h2f_lo(w0);
+        const float v1 = (e1 & 1u) ? h2f_hi(w1) : h2f_lo(w1);
+        const uint32_t base = 8u * (uint32_t)c;
+        if (base + e0 < nlimit) acc = __builtin_fmaf(qf[2 * c], v0, acc);
+        if (base + e1 < nlimit) acc = __builtin_fmaf(qf[2 * c + 1], v1, acc);
+      }
+    }
+  }
+  return acc;
+}
+
+template <int METRIC>
+__device__ __forceinline__ float quad_finish(float partial) {
+  const float s = quad_sum(partial);
+  return METRIC == kL2 ? s : -s;
+}
+
+}  // namespace jasper_amd

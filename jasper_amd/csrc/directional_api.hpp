@@ -1,0 +1,33 @@
+// directional_api.hpp -- host entry points of the directional path
+// (reference DEFINE_DIRECTIONAL_OPS, ffi/jasper_ffi_common.cuh:442-775).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <memory>
+#include <string>
+
+#include "build.hpp"
+#include "graph.hpp"
+
+namespace jasper_amd {
+
+// The directional configs come in two dim buckets (reference
+// python/jasper/__init__.py:66-84): packed_t = u8 for dim <= 128, u16 above.
+void check_directional_dim(bool small_dim, int64_t dim);
+
+std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_ranks, bool small_dim,
+                                             const void* vectors, int64_t n, int64_t dim, double alpha,
+                                             int64_t budget, bool on_host, bool prerotate, uint64_t seed,
+                                             hipStream_t stream, BuildStats* stats);
+void build_lsh(Graph& g, int64_t n_samples, uint64_t seed);
+void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed);
+void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+                        float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream);
+void save_directional_file(const Graph& g, const std::string& path);
+std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
+                                             uint32_t k_ranks, bool small_dim, bool on_host, bool prerotate,
+                                             uint64_t seed);
+
+}  // namespace jasper_amd

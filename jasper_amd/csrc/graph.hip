@@ -1,0 +1,262 @@
+// graph.hip -- allocation, host transfer and the on-disk format.
+//
+// The base file layout is the reference's current format
+// (include/jasper/index/graph.cuh:1653-1788):
+//   u64 total_file_size | u64 N | u64 medoid | u64 bytes_per_node
+//   N records: fp16[dim] | u8 edge_count | u32 edges[R] | bf16 dist[R] | u32 slot_to_id
+//   ceil(N/8) bytes of deletion bits (bit g&7 of byte g>>3 is slot g)
+//   u64 next_id
+// and the loader accepts the three older per-node layouts the reference
+// loader accepts (graph.cuh:1460-1479).
+#include "graph.hpp"
+#include "directional.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+
+namespace jasper_amd {
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+  }
+}
+
+static void* alloc_bytes(size_t bytes, bool on_host, const char* what) {
+  if (bytes == 0) bytes = 16;
+  void* p = nullptr;
+  if (on_host) hip_check(hipHostMalloc(&p, bytes, hipHostMallocDefault), what);
+  else hip_check(hipMalloc(&p, bytes), what);
+  return p;
+}
+
+static void free_bytes(void* p, bool on_host) {
+  if (!p) return;
+  if (on_host) (void)hipHostFree(p);
+  else (void)hipFree(p);
+}
+
+Graph::Graph() = default;
+Graph::~Graph() { release(); }
+
+void Graph::allocate(int64_t n_, uint32_t dim_, uint32_t R_, int metric_, bool on_host_) {
+  release();
+  n = n_;
+  dim = dim_;
+  dp = pad_dim(dim_);
+  R = R_;
+  metric = metric_;
+  on_host = on_host_;
+  medoid = 0;
+  next_id = (uint64_t)n_;
+  n_deleted = 0;
+  const size_t nn = (size_t)std::max<int64_t>(n_, 1);
+  try {
+    vecs = alloc_bytes(nn * dp * 2, on_host, "alloc vectors");
+    edges = (uint32_t*)alloc_bytes(nn * R * 4, on_host, "alloc edges");
+    edist = (uint16_t*)alloc_bytes(nn * R * 2, on_host, "alloc edge distances");
+    counts = (uint8_t*)alloc_bytes(nn, on_host, "alloc edge counts");
+    deleted = (uint32_t*)alloc_bytes(((nn + 31) / 32) * 4, on_host, "alloc deletion bits");
+    slot_to_id = (uint32_t*)alloc_bytes(nn * 4, on_host, "alloc slot ids");
+  } catch (...) {
+    release();
+    throw;
+  }
+  if (on_host) {
+    std::memset(vecs, 0, nn * dp * 2);
+    std::memset(edges, 0xFF, nn * R * 4);
+    std::memset(edist, 0, nn * R * 2);
+    std::memset(counts, 0, nn);
+    std::memset(deleted, 0, ((nn + 31) / 32) * 4);
+    for (size_t i = 0; i < nn; ++i) slot_to_id[i] = (uint32_t)i;
+  } else {
+    hip_check(hipMemset(vecs, 0, nn * dp * 2), "memset vectors");
+    hip_check(hipMemset(edges, 0xFF, nn * R * 4), "memset edges");
+    hip_check(hipMemset(edist, 0, nn * R * 2), "memset edge distances");
+    hip_check(hipMemset(counts, 0, nn), "memset counts");
+    hip_check(hipMemset(deleted, 0, ((nn + 31) / 32) * 4), "memset deletion bits");
+    std::vector<uint32_t> ids(nn);
+    for (size_t i = 0; i < nn; ++i) ids[i] = (uint32_t)i;
+    hip_check(hipMemcpy(slot_to_id, ids.data(), nn * 4, hipMemcpyHostToDevice), "init slot ids");
+  }
+}
+
+void Graph::release() {
+  free_bytes(vecs, on_host);
+  free_bytes(edges, on_host);
+  free_bytes(edist, on_host);
+  free_bytes(counts, on_host);
+  free_bytes(deleted, on_host);
+  free_bytes(slot_to_id, on_host);
+  vecs = nullptr;
+  edges = nullptr;
+  edist = nullptr;
+  counts = nullptr;
+  deleted = nullptr;
+  slot_to_id = nullptr;
+  if (rotation) (void)hipFree(rotation);
+  rotation = nullptr;
+  if (vector_norms) (void)hipFree(vector_norms);
+  vector_norms = nullptr;
+  lsh.reset();
+  pq.reset();
+}
+
+void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream) {
+  if (n <= 0) return;
+  const hipMemcpyKind kind = hipMemcpyDefault;
+  hip_check(hipMemcpy2DAsync(g.vecs, (size_t)g.dp * 2, src, (size_t)dim * 2, (size_t)dim * 2, (size_t)n,
+                             kind, stream),
+            "upload vectors");
+}
+
+void download_graph(const Graph& g, HostGraph& h, bool with_vectors) {
+  const size_t n = (size_t)g.n;
+  h.edges.resize(n * g.R);
+  h.edist.resize(n * g.R);
+  h.counts.resize(n);
+  h.deleted.resize((n + 31) / 32);
+  h.slot_to_id.resize(n);
+  if (n == 0) return;
+  hip_check(hipDeviceSynchronize(), "sync before download");
+  hip_check(hipMemcpy(h.edges.data(), g.edges, n * g.R * 4, hipMemcpyDefault), "download edges");
+  hip_check(hipMemcpy(h.edist.data(), g.edist, n * g.R * 2, hipMemcpyDefault), "download edge distances");
+  hip_check(hipMemcpy(h.counts.data(), g.counts, n, hipMemcpyDefault), "download counts");
+  hip_check(hipMemcpy(h.deleted.data(), g.deleted, h.deleted.size() * 4, hipMemcpyDefault), "download deleted");
+  hip_check(hipMemcpy(h.slot_to_id.data(), g.slot_to_id, n * 4, hipMemcpyDefault), "download slot ids");
+  if (with_vectors) {
+    h.vecs.resize(n * g.dp);
+    hip_check(hipMemcpy(h.vecs.data(), g.vecs, n * g.dp * 2, hipMemcpyDefault), "download vectors");
+  }
+}
+
+void save_graph_file(const Graph& g, const std::string& path) {
+  std::ofstream f(path, std::ios::binary | std::ios::trunc);
+  if (!f.is_open()) throw std::runtime_error("failed to open " + path + " for graph save");
+  const uint64_t n = (uint64_t)g.n;
+  const uint64_t bpn = 2ull * g.dim + 1 + 6ull * g.R + 4;
+  const uint64_t del_bytes = (n + 7) / 8;
+  const uint64_t total = 32 + n * bpn + del_bytes + 8;
+  const uint64_t medoid = g.medoid;
+  f.write((const char*)&total, 8);
+  f.write((const char*)&n, 8);
+  f.write((const char*)&medoid, 8);
+  f.write((const char*)&bpn, 8);
+
+  HostGraph h;
+  download_graph(g, h, true);
+  std::vector<uint8_t> packed(del_bytes, 0);
+  const size_t chunk = 1u << 16;
+  std::vector<uint8_t> buf;
+  for (size_t s = 0; s < n; s += chunk) {
+    const size_t e = std::min<size_t>(n, s + chunk);
+    buf.resize((e - s) * bpn);
+    uint8_t* p = buf.data();
+    for (size_t i = s; i < e; ++i) {
+      std::memcpy(p, &h.vecs[i * g.dp], 2ull * g.dim);
+      p += 2ull * g.dim;
+      *p++ = h.counts[i];
+      std::memcpy(p, &h.edges[i * g.R], 4ull * g.R);
+      p += 4ull * g.R;
+      std::memcpy(p, &h.edist[i * g.R], 2ull * g.R);
+      p += 2ull * g.R;
+      std::memcpy(p, &h.slot_to_id[i], 4);
+      p += 4;
+      if ((h.deleted[i >> 5] >> (i & 31)) & 1u) packed[i >> 3] |= (uint8_t)(1u << (i & 7));
+    }
+    f.write((const char*)buf.data(), (std::streamsize)buf.size());
+  }
+  f.write((const char*)packed.data(), (std::streamsize)packed.size());
+  const uint64_t next_id = g.next_id;
+  f.write((const char*)&next_id, 8);
+  if (!f.good()) throw std::runtime_error("short write while saving " + path);
+}
+
+std::unique_ptr<Graph> load_graph_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
+                                       bool on_host, uint64_t* trailer_offset) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f.is_open()) throw std::runtime_error("failed to open " + path + " for graph load");
+  uint64_t hdr[4];
+  f.read((char*)hdr, 32);
+  if (f.gcount() != 32) throw std::runtime_error("truncated graph header in " + path);
+  const uint64_t total = hdr[0], n = hdr[1], medoid = hdr[2], bpn = hdr[3];
+  const uint64_t base = 2ull * dim + 1 + 6ull * R;
+  const bool bitpacked = bpn == base + 4;
+  const bool has_id = bitpacked || bpn == base + 5;
+  const bool inline_del = bpn == base + 5 || bpn == base + 1;
+  if (!bitpacked && !inline_del && bpn != base)
+    throw std::runtime_error("bytes_per_node " + std::to_string(bpn) + " matches no known layout for dim " +
+                             std::to_string(dim) + ", R " + std::to_string(R));
+  if (n > 0x7FFFFFFFull) throw std::runtime_error("graph too large for 31-bit ids");
+
+  auto g = std::make_unique<Graph>();
+  g->allocate((int64_t)n, dim, R, metric, on_host);
+  g->medoid = (uint32_t)medoid;
+  const uint32_t dp = g->dp;
+  HostGraph h;
+  h.vecs.assign((size_t)n * dp, 0);
+  h.edges.assign((size_t)n * R, 0);
+  h.edist.assign((size_t)n * R, 0);
+  h.counts.assign((size_t)n, 0);
+  h.deleted.assign(((size_t)n + 31) / 32, 0);
+  h.slot_to_id.assign((size_t)n, 0);
+  const size_t chunk = 1u << 16;
+  std::vector<uint8_t> buf;
+  uint64_t n_del = 0;
+  for (size_t s = 0; s < n; s += chunk) {
+    const size_t e = std::min<size_t>(n, s + chunk);
+    buf.resize((e - s) * bpn);
+    f.read((char*)buf.data(), (std::streamsize)buf.size());
+    if ((size_t)f.gcount() != buf.size())
+      throw std::runtime_error("short read at record " + std::to_string(s) + " of " + path);
+    const uint8_t* p = buf.data();
+    for (size_t i = s; i < e; ++i) {
+      std::memcpy(&h.vecs[i * dp], p, 2ull * dim);
+      p += 2ull * dim;
+      h.counts[i] = *p++;
+      std::memcpy(&h.edges[i * R], p, 4ull * R);
+      p += 4ull * R;
+      std::memcpy(&h.edist[i * R], p, 2ull * R);
+      p += 2ull * R;
+      if (inline_del) {
+        if (*p) { h.deleted[i >> 5] |= 1u << (i & 31); ++n_del; }
+        ++p;
+      }
+      if (has_id) { std::memcpy(&h.slot_to_id[i], p, 4); p += 4; }
+      else h.slot_to_id[i] = (uint32_t)i;
+    }
+  }
+  uint64_t pos = 32 + n * bpn;
+  if (bitpacked) {
+    std::vector<uint8_t> packed((size_t)((n + 7) / 8));
+    f.read((char*)packed.data(), (std::streamsize)packed.size());
+    if ((size_t)f.gcount() != packed.size()) throw std::runtime_error("short read of deletion bits in " + path);
+    for (size_t i = 0; i < n; ++i)
+      if ((packed[i >> 3] >> (i & 7)) & 1u) { h.deleted[i >> 5] |= 1u << (i & 31); ++n_del; }
+    pos += packed.size();
+  }
+  uint64_t next_id = n;
+  if (has_id) {
+    f.read((char*)&next_id, 8);
+    if (f.gcount() != 8) throw std::runtime_error("missing next_id in " + path);
+    pos += 8;
+  }
+  (void)total;
+  if (trailer_offset) *trailer_offset = pos;
+  g->next_id = next_id;
+  g->n_deleted = n_del;
+  if (n > 0) {
+    hip_check(hipMemcpy(g->vecs, h.vecs.data(), (size_t)n * dp * 2, hipMemcpyDefault), "upload vectors");
+    hip_check(hipMemcpy(g->edges, h.edges.data(), (size_t)n * R * 4, hipMemcpyDefault), "upload edges");
+    hip_check(hipMemcpy(g->edist, h.edist.data(), (size_t)n * R * 2, hipMemcpyDefault), "upload edge dists");
+    hip_check(hipMemcpy(g->counts, h.counts.data(), (size_t)n, hipMemcpyDefault), "upload counts");
+    hip_check(hipMemcpy(g->deleted, h.deleted.data(), h.deleted.size() * 4, hipMemcpyDefault), "upload deleted");
+    hip_check(hipMemcpy(g->slot_to_id, h.slot_to_id.data(), (size_t)n * 4, hipMemcpyDefault), "upload slot ids");
+  }
+  return g;
+}
+
+}  // namespace jasper_amd

@@ -1,0 +1,92 @@
+// graph.hpp -- device-resident Vamana graph, flat structure-of-arrays.
+//
+// The reference keeps 2^20-vector segments behind a device array of segment
+// structs (reference include/jasper/index/graph.cuh:92-496, 498-1066), which
+// costs a dependent pointer load on every access. On MI355X the whole index
+// fits one allocation per column (config 5, 100M x 128 with R = 64, is
+// ~65 GB of the 288 GB of HBM), so every column here is one flat array
+// indexed by vertex id:
+//   vecs      fp16 [n, dp]   rows padded to dp = pad(dim) (16-byte rows)
+//   edges     u32  [n, R]    adjacency rows (4R bytes: 256 B at R = 64)
+//   edist     bf16 [n, R]    stored edge distances (construction only)
+//   counts    u8   [n]       valid prefix length of each row
+//   deleted   u32  [(n+31)/32] tombstone bits
+//   slot_to_id u32 [n]       stable id of each slot (identity after build)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "directional.hpp"
+
+namespace jasper_amd {
+
+void hip_check(hipError_t e, const char* what);
+
+inline uint32_t pad_dim(uint32_t d) { return (d + 7u) / 8u * 8u; }
+
+struct Graph {
+  uint32_t dim = 0, dp = 0, R = 0;
+  int metric = 0;  // 0 = L2, 1 = IP
+  int64_t n = 0;
+  uint32_t medoid = 0;
+  uint64_t next_id = 0;
+  uint64_t n_deleted = 0;
+  bool on_host = false;
+  // directional configuration (0 for plain graphs)
+  uint32_t k_ranks = 0;
+  uint32_t packed_bytes = 0;
+
+  void* vecs = nullptr;        // fp16
+  uint32_t* edges = nullptr;
+  uint16_t* edist = nullptr;
+  uint8_t* counts = nullptr;
+  uint32_t* deleted = nullptr;
+  uint32_t* slot_to_id = nullptr;
+
+  // directional state (owned; null when absent)
+  bool prerotate = false;
+  uint64_t prerotate_seed = 42;
+  void* rotation = nullptr;    // fp16 [dim, dim] column-major, device
+  std::unique_ptr<LshArtifacts> lsh;
+  std::unique_ptr<PqArtifacts> pq;
+  float* vector_norms = nullptr;  // [n] ||x||^2
+
+  Graph();
+  Graph(const Graph&) = delete;
+  Graph& operator=(const Graph&) = delete;
+  ~Graph();
+
+  void allocate(int64_t n_, uint32_t dim_, uint32_t R_, int metric_, bool on_host_);
+  void release();
+
+  size_t vec_bytes() const { return (size_t)n * dp * 2; }
+};
+
+// File I/O, byte-compatible with the reference format
+// (save_graph_to_file / load_graph_from_file, graph.cuh:1425-1788).
+void save_graph_file(const Graph& g, const std::string& path);
+std::unique_ptr<Graph> load_graph_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
+                                       bool on_host, uint64_t* trailer_offset);
+
+// Host copies of the graph columns (for export and file writing).
+struct HostGraph {
+  std::vector<uint16_t> vecs;   // [n, dp]
+  std::vector<uint32_t> edges;  // [n, R]
+  std::vector<uint16_t> edist;  // [n, R]
+  std::vector<uint8_t> counts;
+  std::vector<uint32_t> deleted;
+  std::vector<uint32_t> slot_to_id;
+};
+void download_graph(const Graph& g, HostGraph& h, bool with_vectors = true);
+
+// Uploads a contiguous host or device fp16 matrix [n, dim] into rows padded
+// to dp on the device graph (vecs must be allocated).
+void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream);
+
+}  // namespace jasper_amd

@@ -1,0 +1,349 @@
+// search.hip -- batched plain beam search, one wave64 per query.
+//
+// Reference: beam_search_kernel (include/jasper/beam_search/beam_search.cuh:
+// 27-259) with the helpers of beam_search/device_kernels.cuh. The result is
+// the reference's, bit for bit; the mechanics are redesigned for CDNA4:
+//
+//  * One 64-lane wave owns a query; no block barriers beyond the wave.
+//  * The candidate list B (<= beam width) lives in LDS as sorted u64 keys
+//    (order-preserving distance | 31-bit id | visited bit).
+//  * A direct-mapped LDS cache of vertex ids skips re-fetching vectors that
+//    were already scored by this query. This cannot change the result: a
+//    vertex still in B would be removed by the reference's dedup (its key is
+//    identical), and a vertex that was clipped out of B can never re-enter,
+//    because the bw-th smallest key of B never increases once B is full.
+//    The cache may forget ids (it is lossy); exactness does not depend on
+//    it, because every new key is also checked for membership in B during
+//    the merge (equal keys <=> same vertex).
+//  * Adjacency rows are read as one coalesced 4R-byte load; each quad of
+//    lanes scores one new neighbour with the reference's accumulation order
+//    (lane l: chunks l, l+4, ...; quad sum (l0+l2)+(l1+l3)).
+//  * New keys are sorted with a register bitonic network, deduplicated and
+//    merged into B by rank (binary searches in LDS), then clipped to bw.
+#include "common.hpp"
+#include "search.hpp"
+
+#include <algorithm>
+
+namespace jasper_amd {
+
+struct SearchArgs {
+  const uint4* vecs;
+  int64_t n;
+  uint32_t dp, nchunks, R;
+  const uint32_t* edges;
+  const uint8_t* counts;
+  const uint32_t* deleted;
+  const uint32_t* slot_to_id;
+  const uint4* queries;
+  uint32_t use_range, q_start, medoid;
+  uint32_t k, bw, limit, max_result;
+  int32_t* out_ids;
+  float* out_dists;
+  uint64_t* visited;
+  uint32_t* visited_counts;
+  uint32_t hash_bits;
+  // measurement mode: exact per-query seen bitmap in HBM and work counters
+  uint32_t* seen_bits;      // [nq, seen_words]
+  uint32_t seen_words;
+  uint32_t* stats;          // [nq, 4]: hops, sum of degrees, vectors scored, 0
+};
+
+__device__ __forceinline__ uint32_t hash_slot(uint32_t v, uint32_t bits) {
+  return (v * 0x9E3779B1u) >> (32u - bits);
+}
+
+// Scores up to 16 (or 32 with TWO) candidate rows listed in cand[base..)
+// and stores their keys into T[j].
+template <int CPL, int METRIC, bool TWO>
+__device__ __forceinline__ void score_pass(const SearchArgs& a, const float (&qf)[CPL * 8], const uint32_t* cand,
+                                           uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql, uint32_t qg) {
+  const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
+  const uint32_t j0 = base + qg;
+  const bool act0 = j0 < nm;
+  const uint32_t v0 = act0 ? cand[j0] : 0u;
+  uint4 x0[CPL];
+  load_row_frag<CPL>(a.vecs + (size_t)v0 * a.nchunks, ql, a.nchunks, act0, x0);
+  if constexpr (TWO) {
+    const uint32_t j1 = base + 16u + qg;
+    const bool act1 = j1 < nm;
+    const uint32_t v1 = act1 ? cand[j1] : 0u;
+    uint4 x1[CPL];
+    load_row_frag<CPL>(a.vecs + (size_t)v1 * a.nchunks, ql, a.nchunks, act1, x1);
+    const float d0 = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x0, ql, nlimit));
+    const float d1 = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x1, ql, nlimit));
+    if (ql == 0 && act0) T[j0] = make_key(d0, v0);
+    if (ql == 0 && act1) T[j1] = make_key(d1, v1);
+  } else {
+    const float d0 = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x0, ql, nlimit));
+    if (ql == 0 && act0) T[j0] = make_key(d0, v0);
+  }
+}
+
+template <int CPL, int METRIC, bool STATS>
+__global__ __launch_bounds__(64) void beam_search_kernel(SearchArgs a) {
+  extern __shared__ uint64_t smem[];
+  const uint32_t lane = threadIdx.x;
+  const uint32_t qid = blockIdx.x;
+  const uint32_t bw = a.bw;
+  uint64_t* buf0 = smem;
+  uint64_t* buf1 = smem + bw;
+  uint64_t* T = smem + 2 * bw;
+  uint32_t* cand = reinterpret_cast<uint32_t*>(T + 64);
+  uint32_t* H = cand + 64;
+  const uint32_t hsize = 1u << a.hash_bits;
+  for (uint32_t i = lane; i < hsize; i += 64) H[i] = kInvalid32;
+
+  const uint32_t ql = lane & 3u, qg = lane >> 2;
+  const uint4* qrow = a.use_range ? a.vecs + (size_t)(a.q_start + qid) * a.nchunks
+                                  : a.queries + (size_t)qid * a.nchunks;
+  float qf[CPL * 8];
+  load_query_frag<CPL, METRIC>(qrow, ql, a.nchunks, qf);
+  const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
+
+  // B = [(medoid, d(q, medoid))]
+  uint32_t cnt = 1;
+  {
+    uint4 x[CPL];
+    load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
+    const float d = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x, ql, nlimit));
+    wave_sync();  // hash table initialised
+    if (lane == 0) {
+      buf0[0] = make_key(d, a.medoid);
+      H[hash_slot(a.medoid, a.hash_bits)] = a.medoid;
+      if constexpr (STATS) atomicOr(&a.seen_bits[(size_t)qid * a.seen_words + (a.medoid >> 5)], 1u << (a.medoid & 31u));
+    }
+  }
+  wave_sync();
+  uint32_t st_hops = 0, st_deg = 0, st_scored = 1;
+
+  uint64_t* B = buf0;
+  uint64_t* NB = buf1;
+  uint32_t hint = 0, vc = 0, loop = 0;
+  while (loop <= a.limit) {
+    loop += 1;
+    // ---- pop: first unvisited entry (all entries before `hint` are visited)
+    int p = -1;
+    for (uint32_t base = hint; base < cnt; base += 64) {
+      const uint32_t i = base + lane;
+      const bool unv = i < cnt && !key_visited(B[i]);
+      const uint64_t m = ballot(unv);
+      if (m) { p = (int)(base + (uint32_t)__builtin_ctzll(m)); break; }
+    }
+    if (p < 0) break;
+    const uint64_t pk = B[p] | 1ull;
+    wave_sync();
+    if (lane == 0) {
+      B[p] = pk;
+      if (a.visited) a.visited[(size_t)qid * a.max_result + vc] = pk;
+    }
+    hint = (uint32_t)p + 1;
+    vc += 1;
+    if (vc == a.max_result) break;
+
+    // ---- expand: one coalesced row read, filter through the seen cache
+    const uint32_t u = key_id(pk);
+    const uint32_t deg = min((uint32_t)a.counts[u], a.R);
+    uint32_t v = kInvalid32;
+    if (lane < deg) v = a.edges[(size_t)u * a.R + lane];
+    bool isnew = lane < deg && (int64_t)v < a.n;
+    if constexpr (STATS) {
+      // exact filter: first time this query sees v
+      if (isnew) {
+        const uint32_t bit = 1u << (v & 31u);
+        isnew = (atomicOr(&a.seen_bits[(size_t)qid * a.seen_words + (v >> 5)], bit) & bit) == 0u;
+      }
+    } else if (isnew) {
+      const uint32_t h = hash_slot(v, a.hash_bits);
+      if (H[h] == v) isnew = false;
+      else H[h] = v;
+    }
+    const uint64_t newm = ballot(isnew);
+    const uint32_t nm = (uint32_t)__builtin_popcountll(newm);
+    if constexpr (STATS) {
+      st_hops += 1;
+      st_deg += deg;
+      st_scored += nm;
+    }
+    if (isnew) cand[mbcnt(newm)] = v;
+    wave_sync();
+
+    // ---- score the new neighbours (4 lanes per vector)
+    uint32_t base = 0;
+    for (; base + 16 < nm; base += 32) score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg);
+    if (base < nm) score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg);
+    wave_sync();
+
+    // ---- sort the new keys, drop duplicates and members of B
+    uint64_t t = lane < nm ? T[lane] : kEmptyKey;
+    t = wave_sort_upto(t, nm);
+    const uint64_t prev = __shfl_up(t, 1, 64);
+    bool keep = lane < nm && !(lane > 0 && key_rank(prev) == key_rank(t));
+    uint32_t lb = 0;
+    const uint32_t top = pow2_ceil(cnt);
+    if (lane < nm) {
+      lb = lds_lower_bound(B, cnt, top, key_rank(t));
+      if (lb < cnt && key_rank(B[lb]) == key_rank(t)) keep = false;
+    }
+    const uint64_t km = ballot(keep);
+    const uint32_t nk = (uint32_t)__builtin_popcountll(km);
+    const uint32_t ti = mbcnt(km);
+    wave_sync();
+    if (keep) T[ti] = t;
+    wave_sync();
+
+    // ---- merge by rank into NB, clip to bw
+    if (keep) {
+      const uint32_t pos = ti + lb;
+      if (pos < bw) NB[pos] = t;
+    }
+    const uint32_t ttop = pow2_ceil(nk);
+    for (uint32_t j = lane; j < cnt; j += 64) {
+      const uint64_t bk = B[j];
+      const uint32_t c = nk ? lds_lower_bound(T, nk, ttop, key_rank(bk)) : 0u;
+      const uint32_t pos = j + c;
+      if (pos < bw) NB[pos] = bk;
+    }
+    if (nk) {
+      const uint32_t first = (uint32_t)__builtin_ctzll(km);
+      const uint32_t lb0 = (uint32_t)__shfl((int)lb, (int)first, 64);
+      hint = min(hint, lb0);
+    }
+    cnt = min(cnt + nk, bw);
+    uint64_t* tmp = B;
+    B = NB;
+    NB = tmp;
+    wave_sync();
+  }
+
+  // ---- output: first k valid, non-deleted entries, then padding
+  //      (beam_search.cuh:206-222, id translation id_map.cuh:49-56,
+  //       unpacking ffi/jasper_ffi_common.cuh:193-203)
+  if (a.out_ids) {
+    uint32_t out = 0;
+    for (uint32_t base = 0; base < cnt && out < a.k; base += 64) {
+      const uint32_t i = base + lane;
+      bool ok = i < cnt;
+      uint64_t key = 0;
+      uint32_t id = 0;
+      if (ok) {
+        key = B[i];
+        id = key_id(key);
+        ok = (a.deleted[id >> 5] >> (id & 31u) & 1u) == 0u;
+      }
+      const uint64_t m = ballot(ok);
+      const uint32_t pos = out + mbcnt(m);
+      if (ok && pos < a.k) {
+        a.out_ids[(size_t)qid * a.k + pos] = (int32_t)(a.slot_to_id ? a.slot_to_id[id] : id);
+        a.out_dists[(size_t)qid * a.k + pos] = key_dist(key);
+      }
+      out += (uint32_t)__builtin_popcountll(m);
+    }
+    for (uint32_t i = out + lane; i < a.k; i += 64) {
+      a.out_ids[(size_t)qid * a.k + i] = -1;
+      a.out_dists[(size_t)qid * a.k + i] = 1e30f;
+    }
+  }
+  if (a.visited_counts && lane == 0) a.visited_counts[qid] = vc;
+  if constexpr (STATS) {
+    if (lane == 0) {
+      a.stats[(size_t)qid * 4 + 0] = st_hops;
+      a.stats[(size_t)qid * 4 + 1] = st_deg;
+      a.stats[(size_t)qid * 4 + 2] = st_scored;
+      a.stats[(size_t)qid * 4 + 3] = 0;
+    }
+  }
+}
+
+static uint32_t default_hash_bits(uint32_t bw) {
+  if (bw <= 32) return 10;
+  if (bw <= 64) return 11;
+  if (bw <= 128) return 12;
+  return 13;
+}
+
+size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {
+  const uint32_t hb = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width);
+  (void)g;
+  return (size_t)2 * r.beam_width * 8 + 64 * 8 + 64 * 4 + ((size_t)1 << hb) * 4;
+}
+
+template <int CPL, int METRIC, bool STATS>
+static void launch_one(const SearchArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+  auto kern = beam_search_kernel<CPL, METRIC, STATS>;
+  if (lds > 64 * 1024)
+    hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+              "set LDS size");
+  hipLaunchKernelGGL(kern, grid, dim3(64), lds, stream, a);
+}
+
+void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stream) {
+  if (r.nq == 0) return;
+  if (r.beam_width == 0) throw std::invalid_argument("beam_width must be positive");
+  if (r.beam_width + 64 >= 2048)
+    throw std::invalid_argument("beam_width " + std::to_string(r.beam_width) +
+                                " is too large (beam_width + 64 must be < 2048)");
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  if (g.n <= 0) throw std::invalid_argument("graph is empty");
+  if ((int64_t)r.medoid >= g.n) throw std::invalid_argument("medoid out of range");
+  if (r.use_range && (int64_t)r.q_start + r.nq > g.n) throw std::invalid_argument("query range out of bounds");
+  SearchArgs a{};
+  a.vecs = (const uint4*)g.vecs;
+  a.n = g.n;
+  a.dp = g.dp;
+  a.nchunks = g.dp / 8;
+  a.R = g.R;
+  a.edges = g.edges;
+  a.counts = g.counts;
+  a.deleted = g.deleted;
+  a.slot_to_id = g.slot_to_id;
+  a.queries = (const uint4*)r.queries;
+  a.use_range = r.use_range ? 1u : 0u;
+  a.q_start = r.q_start;
+  a.medoid = r.medoid;
+  a.k = r.k;
+  a.bw = r.beam_width;
+  a.limit = r.limit;
+  a.max_result = r.max_result;
+  a.out_ids = r.out_ids;
+  a.out_dists = r.out_dists;
+  a.visited = r.visited;
+  a.visited_counts = r.visited_counts;
+  a.hash_bits = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width);
+  a.seen_bits = r.seen_bits;
+  a.seen_words = (uint32_t)((g.n + 31) / 32);
+  a.stats = r.stats;
+  const bool stats = r.stats != nullptr;
+  if (stats && !r.seen_bits) throw std::invalid_argument("stats mode needs a seen bitmap");
+  const size_t lds = beam_search_lds_bytes(g, r);
+  const uint32_t cpl = (a.nchunks + 3) / 4;
+  const dim3 grid(r.nq);
+#define JA_LAUNCH(C)                                                                                   \
+  case C: {                                                                                            \
+    if (g.metric == kL2) {                                                                             \
+      if (stats) launch_one<C, kL2, true>(a, grid, lds, stream);                                       \
+      else launch_one<C, kL2, false>(a, grid, lds, stream);                                            \
+    } else {                                                                                           \
+      if (stats) launch_one<C, kIP, true>(a, grid, lds, stream);                                       \
+      else launch_one<C, kIP, false>(a, grid, lds, stream);                                            \
+    }                                                                                                  \
+    break;                                                                                             \
+  }
+  switch (cpl) {
+    JA_LAUNCH(1)
+    JA_LAUNCH(2)
+    JA_LAUNCH(3)
+    JA_LAUNCH(4)
+    JA_LAUNCH(5)
+    JA_LAUNCH(6)
+    JA_LAUNCH(7)
+    JA_LAUNCH(8)
+    default:
+      throw std::invalid_argument("dimension " + std::to_string(g.dim) +
+                                  " is above the supported maximum of 256 for plain search");
+  }
+#undef JA_LAUNCH
+  hip_check(hipGetLastError(), "launch beam_search_kernel");
+}
+
+}  // namespace jasper_amd

@@ -1,0 +1,335 @@
+"""CPU oracle for the Jasper query/build hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package is the parity checker. Only ``tests/``, ``__graft_entry__.smoke()``
+and ``bench.py``'s ``cpu_baseline`` leg may import it, and only to check or to
+time the CPU baseline; the product (``jasper_amd``) never imports it.
+
+The arithmetic lives in ``jasper_oracle.cpp`` (built by ``oracle/Makefile`` into
+``oracle/build/liboracle.so``); this module binds it with ctypes and adds the
+on-disk format restatement (reference ``include/jasper/index/graph.cuh``
+:1425-1788, ``save_graph_to_file`` / ``load_graph_from_file``).
+
+Pinning (what checks each function, see tests/test_oracle_*.py):
+  * l2 / ip distance   -- reference KATs tests/test_distance.cu:32-136, exact
+                          integer identities, brute-force fp64 comparison.
+  * beam_search        -- brute-force equality when bw >= N on a connected
+                          graph, complete-graph one-hop, hand-computed path
+                          graph, invariants (sorted, unique, |B| <= bw).
+  * build              -- invariants (degree <= R, no self loops, alpha-prune
+                          dominance per row), recall against brute force.
+  * rotation_matrix    -- reference tests tests/test_rotation.cu:56-185.
+  * bruteforce_*       -- each other and a float64 numpy computation.
+  * file format        -- byte offsets of graph.cuh:1653-1788, bpn values.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import struct
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "build" / "liboracle.so"
+_lib = None
+
+L2 = 0
+IP = 1
+
+
+def build(force: bool = False) -> Path:
+    """Compile the oracle with its Makefile (g++ only; no GPU toolchain)."""
+    if force or not _LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+        P = ctypes.c_void_p
+        i32, i64, f32, u64 = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint64
+        _lib.jo_l2.restype = f32
+        _lib.jo_l2.argtypes = [P, P, i32]
+        _lib.jo_ip.restype = f32
+        _lib.jo_ip.argtypes = [P, P, i32]
+        _lib.jo_f2bf.restype = ctypes.c_uint16
+        _lib.jo_f2bf.argtypes = [f32]
+        _lib.jo_distance_pairs.restype = None
+        _lib.jo_distance_pairs.argtypes = [i32, P, P, i64, i32, P, i32]
+        _lib.jo_beam_search.restype = i32
+        _lib.jo_beam_search.argtypes = [P, i64, i32, P, P, i32, P, P, i32, P, i64, ctypes.c_uint32,
+                                        i32, i32, i32, i32, P, P, P, P, P, P, i32]
+        _lib.jo_max_batch_size.restype = i64
+        _lib.jo_max_batch_size.argtypes = [i64, i32, i64]
+        _lib.jo_build.restype = i32
+        _lib.jo_build.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, P, P, P, i32, P]
+        _lib.jo_bruteforce_exact.restype = None
+        _lib.jo_bruteforce_exact.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32]
+        _lib.jo_bruteforce_ref.restype = None
+        _lib.jo_bruteforce_ref.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32]
+        _lib.jo_rotation_matrix.restype = None
+        _lib.jo_rotation_matrix.argtypes = [i32, u64, P, P]
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def metric_code(distance: str) -> int:
+    return L2 if distance in ("l2", L2) else IP
+
+
+def pad_dim(dim: int) -> int:
+    """vector_view::pad, reference include/jasper/index/vector.cuh:20-22."""
+    return (dim + 7) // 8 * 8
+
+
+def as_padded_f16(x: np.ndarray) -> np.ndarray:
+    """[n, dim] float -> [n, pad(dim)] float16 bits (uint16), zero padded."""
+    x = np.asarray(x)
+    if x.dtype != np.float16:
+        x = x.astype(np.float16)
+    n, dim = x.shape
+    dp = pad_dim(dim)
+    out = np.zeros((n, dp), dtype=np.float16)
+    out[:, :dim] = x
+    return np.ascontiguousarray(out).view(np.uint16)
+
+
+def f2bf(x: float) -> int:
+    return int(lib().jo_f2bf(float(x)))
+
+
+def distance(a: np.ndarray, b: np.ndarray, distance: str = "l2", dim: int | None = None) -> float:
+    """Single distance between two fp16 vectors (reference distance.cuh:93-167)."""
+    pa = as_padded_f16(np.asarray(a).reshape(1, -1))
+    pb = as_padded_f16(np.asarray(b).reshape(1, -1))
+    d = pa.shape[1] if dim is None else dim
+    f = lib().jo_l2 if metric_code(distance) == L2 else lib().jo_ip
+    return float(f(_ptr(pa), _ptr(pb), d))
+
+
+def distance_pairs(a16: np.ndarray, b16: np.ndarray, distance: str = "l2", nthreads: int = 0) -> np.ndarray:
+    """Row-wise distances of two padded uint16 arrays of equal shape."""
+    assert a16.shape == b16.shape and a16.dtype == np.uint16
+    out = np.empty(a16.shape[0], dtype=np.float32)
+    lib().jo_distance_pairs(metric_code(distance), _ptr(a16), _ptr(b16), a16.shape[0], a16.shape[1],
+                            _ptr(out), nthreads)
+    return out
+
+
+class OracleGraph:
+    """Host graph in the oracle's flat layout: vectors [n, dp] (fp16 bits),
+    edges [n, R] u32, edge_dist [n, R] bf16 bits, counts [n] u8."""
+
+    def __init__(self, vecs16, edges, edge_dist, counts, R, dim, distance="l2", medoid=0,
+                 deleted_bits=None, slot_to_id=None, next_id=None):
+        self.vecs16 = np.ascontiguousarray(vecs16, dtype=np.uint16)
+        self.edges = np.ascontiguousarray(edges, dtype=np.uint32)
+        self.edge_dist = np.ascontiguousarray(edge_dist, dtype=np.uint16)
+        self.counts = np.ascontiguousarray(counts, dtype=np.uint8)
+        self.R = int(R)
+        self.dim = int(dim)
+        self.distance = distance
+        self.medoid = int(medoid)
+        n = self.vecs16.shape[0]
+        self.deleted_bits = (np.zeros((n + 31) // 32, dtype=np.uint32) if deleted_bits is None
+                             else np.ascontiguousarray(deleted_bits, dtype=np.uint32))
+        self.slot_to_id = (np.arange(n, dtype=np.uint32) if slot_to_id is None
+                           else np.ascontiguousarray(slot_to_id, dtype=np.uint32))
+        self.next_id = n if next_id is None else int(next_id)
+
+    @property
+    def n(self):
+        return self.vecs16.shape[0]
+
+    @property
+    def dp(self):
+        return self.vecs16.shape[1]
+
+
+def max_batch_size(n: int, R: int, budget_bytes: int = 10 ** 10) -> int:
+    return int(lib().jo_max_batch_size(n, R, budget_bytes))
+
+
+def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
+          workspace_budget: int = 10 ** 10, max_batch: int | None = None,
+          nthreads: int = 0) -> OracleGraph:
+    """Vamana construction, reference index/construct.cuh:992-1160."""
+    vecs16 = as_padded_f16(vectors)
+    n, dp = vecs16.shape
+    dim = np.asarray(vectors).shape[1]
+    if max_batch is None:
+        max_batch = max(1, max_batch_size(n, R, workspace_budget))
+    edges = np.empty((n, R), dtype=np.uint32)
+    edist = np.empty((n, R), dtype=np.uint16)
+    counts = np.empty(n, dtype=np.uint8)
+    nb = ctypes.c_int64(0)
+    rc = lib().jo_build(_ptr(vecs16), n, dp, dim, R, metric_code(distance), ctypes.c_float(alpha),
+                        int(max_batch), _ptr(edges), _ptr(edist), _ptr(counts), nthreads,
+                        ctypes.byref(nb))
+    if rc != 0:
+        raise RuntimeError(f"oracle build failed ({rc})")
+    g = OracleGraph(vecs16, edges, edist, counts, R, dim, distance)
+    g.n_batches = nb.value
+    g.max_batch = max_batch
+    return g
+
+
+def beam_search(g: OracleGraph, queries, k: int = 10, beam_width: int = 64,
+                limit: int | None = None, max_result: int = 2048, get_visited: bool = False,
+                stats: bool = False, nthreads: int = 0):
+    """Plain beam search, reference beam_search/beam_search.cuh:27-225 with
+    api.cuh defaults (limit = 2 * beam_width as python/jasper/__init__.py:501)."""
+    q16 = queries if (isinstance(queries, np.ndarray) and queries.dtype == np.uint16) else as_padded_f16(queries)
+    assert q16.shape[1] == g.dp
+    nq = q16.shape[0]
+    if limit is None:
+        limit = 2 * beam_width
+    ids = np.empty((nq, k), dtype=np.int32)
+    dists = np.empty((nq, k), dtype=np.float32)
+    vis_ids = vis_d = vis_c = None
+    if get_visited:
+        vis_ids = np.zeros((nq, max_result), dtype=np.uint32)
+        vis_d = np.zeros((nq, max_result), dtype=np.float32)
+        vis_c = np.zeros(nq, dtype=np.uint32)
+    st = np.zeros((nq, 4), dtype=np.uint64) if stats else None
+    lib().jo_beam_search(_ptr(g.vecs16), g.n, g.dp, _ptr(g.edges), _ptr(g.counts), g.R,
+                         _ptr(g.deleted_bits), _ptr(g.slot_to_id), metric_code(g.distance),
+                         _ptr(q16), nq, g.medoid, k, beam_width, limit, max_result,
+                         _ptr(ids), _ptr(dists), _ptr(vis_ids), _ptr(vis_d), _ptr(vis_c),
+                         _ptr(st), nthreads)
+    out = [ids, dists]
+    if get_visited:
+        out += [vis_ids, vis_d, vis_c]
+    if stats:
+        out.append(st)
+    return tuple(out)
+
+
+def bruteforce_exact(vectors, queries, k: int = 10, distance: str = "l2", nthreads: int = 0):
+    v16 = vectors if (isinstance(vectors, np.ndarray) and vectors.dtype == np.uint16) else as_padded_f16(vectors)
+    q16 = queries if (isinstance(queries, np.ndarray) and queries.dtype == np.uint16) else as_padded_f16(queries)
+    nq = q16.shape[0]
+    ids = np.empty((nq, k), dtype=np.int32)
+    d = np.empty((nq, k), dtype=np.float32)
+    lib().jo_bruteforce_exact(metric_code(distance), _ptr(v16), v16.shape[0], _ptr(q16), nq,
+                              v16.shape[1], k, _ptr(ids), _ptr(d), nthreads)
+    return ids, d
+
+
+def bruteforce_ref(vectors_f32, queries_f32, k: int = 10, distance: str = "l2", nthreads: int = 0):
+    """Reference ground-truth arithmetic (python/jasper/__init__.py:828-926)."""
+    v = np.ascontiguousarray(vectors_f32, dtype=np.float32)
+    q = np.ascontiguousarray(queries_f32, dtype=np.float32)
+    nq = q.shape[0]
+    ids = np.empty((nq, k), dtype=np.int32)
+    d = np.empty((nq, k), dtype=np.float32)
+    lib().jo_bruteforce_ref(metric_code(distance), _ptr(v), v.shape[0], _ptr(q), nq, v.shape[1], k,
+                            _ptr(ids), _ptr(d), nthreads)
+    return ids, d
+
+
+def rotation_matrix(d: int, seed: int = 42):
+    """set_rotation_matrix, reference rotation/rotation.cuh:75-111. Returns
+    (m, m_transpose) as column-major flat float32 arrays of length d*d."""
+    m = np.empty(d * d, dtype=np.float32)
+    mt = np.empty(d * d, dtype=np.float32)
+    lib().jo_rotation_matrix(d, seed, _ptr(m), _ptr(mt))
+    return m, mt
+
+
+# ------------------------------------------------------------- file format --
+
+def bytes_per_node(dim: int, R: int) -> int:
+    """save_graph_to_file, graph.cuh:1676-1677: 2*dim + 1 + (4R + 2R) + 4."""
+    return 2 * dim + 1 + 6 * R + 4
+
+
+def save_graph(g: OracleGraph, path: str | os.PathLike) -> int:
+    """Restates save_graph_to_file (graph.cuh:1653-1788) byte for byte."""
+    n, dim, R = g.n, g.dim, g.R
+    bpn = bytes_per_node(dim, R)
+    deleted_bytes = (n + 7) // 8
+    total = 32 + n * bpn + deleted_bytes + 8
+    rec = np.zeros((n, bpn), dtype=np.uint8)
+    off = 0
+    rec[:, off:off + 2 * dim] = g.vecs16[:, :dim].view(np.uint8).reshape(n, -1)[:, :2 * dim]
+    off += 2 * dim
+    rec[:, off] = g.counts
+    off += 1
+    rec[:, off:off + 4 * R] = g.edges.view(np.uint8).reshape(n, 4 * R)
+    off += 4 * R
+    rec[:, off:off + 2 * R] = g.edge_dist.view(np.uint8).reshape(n, 2 * R)
+    off += 2 * R
+    rec[:, off:off + 4] = g.slot_to_id.view(np.uint8).reshape(n, 4)
+    packed = np.zeros(deleted_bytes, dtype=np.uint8)
+    bits = ((g.deleted_bits[np.arange(n) >> 5] >> (np.arange(n) & 31).astype(np.uint32)) & 1).astype(np.uint8)
+    for b in range(8):
+        sel = bits[b::8]
+        packed[:len(sel)] |= (sel << b).astype(np.uint8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<QQQQ", total, n, g.medoid, bpn))
+        f.write(rec.tobytes())
+        f.write(packed.tobytes())
+        f.write(struct.pack("<Q", g.next_id))
+    return total
+
+
+def load_graph(path: str | os.PathLike, dim: int, R: int, distance: str = "l2") -> OracleGraph:
+    """Restates load_graph_from_file (graph.cuh:1425-1651) for the current
+    bit-packed layout and the three legacy layouts it accepts."""
+    data = Path(path).read_bytes()
+    total, n, medoid, bpn = struct.unpack_from("<QQQQ", data, 0)
+    base = 2 * dim + 1 + 6 * R
+    if bpn not in (base, base + 1, base + 1 + 4, base + 4):
+        raise ValueError(f"bytes_per_node {bpn} matches no known layout")
+    rec = np.frombuffer(data, dtype=np.uint8, count=n * bpn, offset=32).reshape(n, bpn)
+    dp = pad_dim(dim)
+    vecs16 = np.zeros((n, dp), dtype=np.uint16)
+    vecs16[:, :dim] = np.ascontiguousarray(rec[:, :2 * dim]).view(np.uint16)
+    off = 2 * dim
+    counts = rec[:, off].copy()
+    off += 1
+    edges = np.ascontiguousarray(rec[:, off:off + 4 * R]).view(np.uint32).reshape(n, R).copy()
+    off += 4 * R
+    edist = np.ascontiguousarray(rec[:, off:off + 2 * R]).view(np.uint16).reshape(n, R).copy()
+    off += 2 * R
+    deleted = np.zeros((n + 31) // 32, dtype=np.uint32)
+    slot_to_id = np.arange(n, dtype=np.uint32)
+    next_id = n
+    if bpn in (base + 1, base + 5):
+        dbytes = rec[:, off].astype(bool)
+        off += 1
+        for i in np.nonzero(dbytes)[0]:
+            deleted[i >> 5] |= np.uint32(1 << (i & 31))
+    if bpn in (base + 5, base + 4):
+        slot_to_id = np.ascontiguousarray(rec[:, off:off + 4]).view(np.uint32).reshape(n).copy()
+    pos = 32 + n * bpn
+    if bpn == base + 4:
+        nbytes = (n + 7) // 8
+        packed = np.frombuffer(data, dtype=np.uint8, count=nbytes, offset=pos)
+        pos += nbytes
+        for i in range(n):
+            if (packed[i >> 3] >> (i & 7)) & 1:
+                deleted[i >> 5] |= np.uint32(1 << (i & 31))
+    if bpn in (base + 5, base + 4):
+        (next_id,) = struct.unpack_from("<Q", data, pos)
+    return OracleGraph(vecs16, edges, edist, counts, R, dim, distance, medoid=medoid,
+                       deleted_bits=deleted, slot_to_id=slot_to_id, next_id=next_id)
+
+
+def recall(gt_ids: np.ndarray, ids: np.ndarray, k: int) -> float:
+    """get_recall, python/jasper/__init__.py:819-826."""
+    hit = 0
+    for a, b in zip(gt_ids[:, :k], ids[:, :k]):
+        hit += len(set(a.tolist()) & set(b.tolist()))
+    return hit / (gt_ids.shape[0] * k)

@@ -1,0 +1,595 @@
+// jasper_oracle.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// CPU restatement of the reference's query/build hot path, used as the parity
+// checker for the HIP implementation. Nothing in the product (jasper_amd/)
+// links, loads or calls this file; only tests/, __graft_entry__.smoke() and
+// bench.py's cpu_baseline leg do, and only as the checker / the reported CPU
+// baseline.
+//
+// Every function cites the reference source it restates (paths relative to
+// the reference tree, saltsystemslab/Jasper). The restatement is written from
+// the algorithm, not translated from the CUDA: the device-side parallel
+// decomposition (tiles, CUB sorts, atomics) is replaced by the sequential
+// order it is equivalent to, and every arithmetic step that decides a result
+// bit (accumulation order, fma, bf16 rounding) is spelled out.
+//
+// Build: oracle/Makefile (g++ -O3 -fopenmp -ffp-contract=off). fp contraction
+// is off so that the only fused multiply-adds are the explicit fmaf() calls.
+
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include <omp.h>
+
+namespace {
+
+constexpr uint32_t kInvalid31 = 0x7FFFFFFFu;   // beam_search/entry.cuh:24-29 (31-bit masked id)
+constexpr uint32_t kInvalid32 = 0xFFFFFFFFu;   // index/construct.cuh:303 (numeric_limits<index_t>::max)
+
+// ---------------------------------------------------------------- numerics --
+
+// IEEE binary16 -> binary32, exact.
+inline float h2f(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t man = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else {  // subnormal: normalise
+      int e = -1;
+      do { man <<= 1; ++e; } while ((man & 0x400u) == 0);
+      man &= 0x3FFu;
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7F800000u | (man << 13);
+  } else {
+    bits = sign | ((exp + 112u) << 23) | (man << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+// binary32 -> bfloat16 bits, round to nearest even (the conversion
+// `(__nv_bfloat16)float` performs; index/graph.cuh:494).
+inline uint16_t f2bf(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40u);
+  const uint32_t bias = 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)((u + bias) >> 16);
+}
+
+inline float bf2f(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// Squared L2 distance, distance/distance.cuh:93-153 (l2_distance::compute)
+// with DATA_T = __half, TILE_SIZE = 4, loads_per_round = 2.
+// Lane l of the 4-lane tile owns the 16-byte chunks w = l + 4j + 8i, i.e. the
+// chunks congruent to l mod 4 in ascending order, and accumulates
+// acc = fma(d, d, acc) with d = f32(a) - f32(b) over the 8 halves of each
+// chunk in order (nvcc contracts `local_sum += diff * diff`). The four lane
+// sums are combined by cg::reduce as a xor butterfly (offset 2, then 1):
+// (l0 + l2) + (l1 + l3).
+float l2_dist(const uint16_t* a, const uint16_t* b, int dim) {
+  const int total_loads = dim / 8;
+  float lane[4];
+  for (int l = 0; l < 4; ++l) {
+    float acc = 0.0f;
+    for (int c = l; c < total_loads; c += 4) {
+      for (int k = 0; k < 8; ++k) {
+        const float d = h2f(a[c * 8 + k]) - h2f(b[c * 8 + k]);
+        acc = std::fmaf(d, d, acc);
+      }
+    }
+    lane[l] = acc;
+  }
+  return (lane[0] + lane[2]) + (lane[1] + lane[3]);
+}
+
+// Negated inner product, distance/distance.cuh:155-167. Lane l sums elements
+// i = l, l+4, ... (products of two halves are exact in fp32, so fma and
+// mul+add agree); same butterfly; negated.
+float ip_dist(const uint16_t* a, const uint16_t* b, int dim) {
+  float lane[4];
+  for (int l = 0; l < 4; ++l) {
+    float acc = 0.0f;
+    for (int i = l; i < dim; i += 4) acc = std::fmaf(h2f(a[i]), h2f(b[i]), acc);
+    lane[l] = acc;
+  }
+  return -((lane[0] + lane[2]) + (lane[1] + lane[3]));
+}
+
+inline float dist(int metric, const uint16_t* a, const uint16_t* b, int dim) {
+  return metric == 0 ? l2_dist(a, b, dim) : ip_dist(a, b, dim);
+}
+
+// ------------------------------------------------------------ plain search --
+
+struct Entry {
+  uint32_t id;   // 31-bit masked index (entry.cuh:18)
+  float dist;
+  bool visited;  // bit 63 (entry.cuh:31-38)
+};
+
+// CustomPairLess, beam_search/device_kernels.cuh:132-151: distance ascending,
+// then 31-bit index ascending; the visited bit is ignored.
+inline bool pair_less(const Entry& a, const Entry& b) {
+  return (a.dist < b.dist) || (a.dist == b.dist && a.id < b.id);
+}
+
+struct Graph {
+  const uint16_t* vecs;  // [n, dp] fp16 bits, zero padded rows
+  int64_t n;
+  int dp;                // padded dim (row stride, multiple of 8)
+  const uint32_t* edges; // [n, R]
+  const uint8_t* counts; // [n]
+  int R;
+  const uint32_t* deleted_bits;  // [(n+31)/32] or null
+  int metric;            // 0 = L2, 1 = IP
+};
+
+struct SearchStats {
+  uint64_t hops = 0;        // expansions (frontier nodes whose edges were read)
+  uint64_t edges_read = 0;  // sum of degrees over expansions
+  uint64_t dist_calls = 0;  // distances computed, reference-equivalent (all appended)
+  uint64_t distinct = 0;    // distinct vertices whose distance was computed
+};
+
+// One query of beam_search_kernel, beam_search/beam_search.cuh:27-225, with
+// the device helpers of device_kernels.cuh restated sequentially:
+//   populate_distances :23-57, choose_new_frontier :60-92,
+//   add_frontier_out :95-129, merge_sort :154-185 (CUB BlockMergeSort, taken
+//   as stable), dedup_results :197-288, clip_k :188-193.
+// Returns the final candidate buffer; appends (id, dist) of every popped
+// node to `visited` when get_visited is set (beam_search.cuh:157-166).
+std::vector<Entry> search_one(const Graph& g, const uint16_t* q, uint32_t medoid,
+                              uint32_t bw, uint32_t limit, uint32_t max_result,
+                              bool get_visited, std::vector<Entry>* visited,
+                              SearchStats* st, std::vector<uint32_t>* seen_scratch) {
+  std::vector<Entry> B;
+  B.reserve(bw + 64 + 8);
+  B.push_back({medoid & kInvalid31, FLT_MAX, false});
+  auto compute = [&](Entry& e) {
+    e.dist = dist(g.metric, q, g.vecs + (size_t)e.id * g.dp, g.dp);
+    if (st) {
+      st->dist_calls++;
+      if (seen_scratch) seen_scratch->push_back(e.id);
+    }
+  };
+  if (B[0].id != kInvalid31) compute(B[0]);
+
+  uint32_t vc = 0, loop = 0;
+  std::vector<Entry> merged;
+  while (loop <= limit) {
+    loop += 1;
+    size_t p = B.size();
+    for (size_t i = 0; i < B.size(); ++i)
+      if (!B[i].visited) { p = i; break; }
+    if (p == B.size()) break;
+    B[p].visited = true;
+    if (get_visited && visited) visited->push_back(B[p]);
+    vc += 1;
+    if (vc == max_result) break;
+
+    const uint32_t u = B[p].id;
+    const uint32_t deg = g.counts[u];
+    const size_t offset = B.size();
+    for (uint32_t e = 0; e < deg; ++e) {
+      const uint32_t nb = g.edges[(size_t)u * g.R + e];
+      if ((int64_t)nb < g.n) B.push_back({nb & kInvalid31, FLT_MAX, false});
+      else B.push_back({kInvalid31, FLT_MAX, true});
+    }
+    if (st) { st->hops++; st->edges_read += deg; }
+    for (size_t i = offset; i < B.size(); ++i)
+      if (B[i].id != kInvalid31) compute(B[i]);
+
+    std::stable_sort(B.begin(), B.end(), pair_less);
+    merged.clear();
+    uint32_t prev = kInvalid31;  // thread 0 compares against INVALID
+    for (const Entry& e : B) {
+      if (e.id != prev) merged.push_back(e);
+      prev = e.id;
+    }
+    if (merged.size() > bw) merged.resize(bw);
+    B.swap(merged);
+  }
+  return B;
+}
+
+// beam_search.cuh:207-222 (output of the first k valid, non-deleted entries;
+// padding (0xFFFFFFFF, 1e30)) followed by translate_slots_to_ids_kernel
+// (index/id_map.cuh:49-56) and unpack_results_kernel
+// (ffi/jasper_ffi_common.cuh:193-203).
+void write_output(const Graph& g, const std::vector<Entry>& B, uint32_t k,
+                  const uint32_t* slot_to_id, int32_t* out_ids, float* out_dists) {
+  uint32_t out = 0;
+  for (size_t i = 0; i < B.size() && out < k; ++i) {
+    const uint32_t idx = B[i].id;
+    if ((int64_t)idx >= g.n) continue;
+    if (g.deleted_bits && ((g.deleted_bits[idx >> 5] >> (idx & 31u)) & 1u)) continue;
+    out_ids[out] = (int32_t)(slot_to_id ? slot_to_id[idx] : idx);
+    out_dists[out] = B[i].dist;
+    ++out;
+  }
+  for (; out < k; ++out) {
+    out_ids[out] = (int32_t)0xFFFFFFFFu;
+    out_dists[out] = 1e30f;
+  }
+}
+
+// ------------------------------------------------------------------ build --
+
+struct Cand {
+  uint32_t id;
+  float dist;
+};
+
+// EntryLess, index/construct.cuh:334-340 / :583-589.
+inline bool cand_less(const Cand& a, const Cand& b) {
+  if (a.dist != b.dist) return a.dist < b.dist;
+  return a.id < b.id;
+}
+
+// RobustPrune, index/construct.cuh:419-472 (forward) and :680-729 (reverse):
+// walk the sorted candidates; stop once R are selected; skip the node itself
+// and INVALID; drop c if some already selected s has d(c, s) * alpha < d_c.
+int robust_prune(const Graph& g, int dim_for_prune, uint32_t self,
+                 const std::vector<Cand>& C, float alpha, int R, Cand* sel) {
+  int ns = 0;
+  for (const Cand& c : C) {
+    if (ns >= R) break;
+    if (c.id == self || c.id == kInvalid32) continue;
+    const uint16_t* cv = g.vecs + (size_t)c.id * g.dp;
+    bool pruned = false;
+    for (int j = 0; j < ns; ++j) {
+      const float d = dist(g.metric, cv, g.vecs + (size_t)sel[j].id * g.dp, dim_for_prune);
+      const float lhs = d * alpha;
+      if (lhs < c.dist) { pruned = true; break; }
+    }
+    if (!pruned) sel[ns++] = c;
+  }
+  return ns;
+}
+
+}  // namespace
+
+// ================================================================ C ABI ====
+extern "C" {
+
+float jo_l2(const uint16_t* a, const uint16_t* b, int dim) { return l2_dist(a, b, dim); }
+float jo_ip(const uint16_t* a, const uint16_t* b, int dim) { return ip_dist(a, b, dim); }
+
+uint16_t jo_f2bf(float f) { return f2bf(f); }
+
+// Pairwise distances for n pairs (rows of a and b, stride dp).
+void jo_distance_pairs(int metric, const uint16_t* a, const uint16_t* b, int64_t n,
+                       int dp, float* out, int nthreads) {
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = dist(metric, a + (size_t)i * dp, b + (size_t)i * dp, dp);
+}
+
+// Batched plain beam search (Appendix A of the contract; reference
+// beam_search/beam_search.cuh + api.cuh). Queries are [nq, dp] fp16 bits.
+// visited_* may be null; when given they are [nq, max_result].
+// stats (may be null) receives per-query [hops, edges_read, dist_calls, distinct].
+int jo_beam_search(const uint16_t* vecs, int64_t n, int dp,
+                   const uint32_t* edges, const uint8_t* counts, int R,
+                   const uint32_t* deleted_bits, const uint32_t* slot_to_id,
+                   int metric, const uint16_t* queries, int64_t nq, uint32_t medoid,
+                   int k, int bw, int limit, int max_result,
+                   int32_t* out_ids, float* out_dists,
+                   uint32_t* visited_ids, float* visited_dists, uint32_t* visited_counts,
+                   uint64_t* stats, int nthreads) {
+  Graph g{vecs, n, dp, edges, counts, R, deleted_bits, metric};
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  const bool get_visited = visited_ids != nullptr;
+#pragma omp parallel
+  {
+    std::vector<Entry> vis;
+    std::vector<uint32_t> seen;
+#pragma omp for schedule(dynamic, 4)
+    for (int64_t qi = 0; qi < nq; ++qi) {
+      vis.clear();
+      seen.clear();
+      SearchStats st;
+      std::vector<Entry> B = search_one(g, queries + (size_t)qi * dp, medoid, (uint32_t)bw,
+                                        (uint32_t)limit, (uint32_t)max_result, get_visited,
+                                        &vis, stats ? &st : nullptr, stats ? &seen : nullptr);
+      if (out_ids) write_output(g, B, (uint32_t)k, slot_to_id, out_ids + qi * k, out_dists + qi * k);
+      if (get_visited) {
+        for (size_t i = 0; i < vis.size(); ++i) {
+          visited_ids[qi * max_result + i] = vis[i].id;
+          visited_dists[qi * max_result + i] = vis[i].dist;
+        }
+        visited_counts[qi] = (uint32_t)vis.size();
+      }
+      if (stats) {
+        std::sort(seen.begin(), seen.end());
+        st.distinct = (uint64_t)(std::unique(seen.begin(), seen.end()) - seen.begin());
+        stats[qi * 4 + 0] = st.hops;
+        stats[qi * 4 + 1] = st.edges_read;
+        stats[qi * 4 + 2] = st.dist_calls;
+        stats[qi * 4 + 3] = st.distinct;
+      }
+    }
+  }
+  return 0;
+}
+
+// Reference maximum batch size for a construction workspace budget:
+// graph_construct_workspace::max_batch_size_for_budget (index/construct.cuh:238-262)
+// capped at n/50 (ffi/jasper_ffi_common.cuh:245-248).
+int64_t jo_max_batch_size(int64_t n, int R, int64_t budget_bytes) {
+  const int64_t L = 64, max_result = 256, max_cands = max_result + R;
+  const int64_t per_item = 8 * L + 8 * max_result + 4 + 8 * max_cands + 4 + 8 * R + 4 * R + 4 * R;
+  const int64_t fixed = 4;
+  int64_t b = budget_bytes <= fixed ? 0 : (budget_bytes - fixed) / per_item;
+  b = std::min<int64_t>(b, 0xFFFFFFFFll);
+  return std::min<int64_t>(b, n / 50);
+}
+
+// Vamana construction (Appendix D of the contract; reference
+// index/construct.cuh construct_graph :992-1160, construction_round :913-958,
+// process_batch :743-911). Input vectors [n, dp]; outputs edges [n, R] (u32),
+// edge_dist [n, R] (bf16 bits), counts [n]. medoid = 0. max_batch must be >= 1.
+// The beam search of each batch is the plain search above with k = L = 64,
+// beam width 64, limit 256, max_result 256 (construct.cuh:57-62, :778-794).
+//
+// Candidate caps (256 + R) never bind in the forward step. In the reverse
+// step the reference keeps an arrival-order subset when a target receives
+// more than 256 + R candidates (atomicAdd, construct.cuh:642-658); this
+// restatement fixes that order as: the target's existing edges in slot order,
+// then the new sources in ascending id order.
+int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, int metric,
+             float alpha, int64_t max_batch, uint32_t* edges, uint16_t* edge_dist,
+             uint8_t* counts, int nthreads, int64_t* n_batches_out) {
+  if (n <= 0) return 0;
+  if (max_batch < 1) return -1;
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  const int L = 64, LIMIT = 256, MAX_RESULT = 256;
+  const int max_cands = MAX_RESULT + R;
+  std::fill(counts, counts + n, (uint8_t)0);
+  std::fill(edges, edges + (size_t)n * R, kInvalid32);
+  std::fill(edge_dist, edge_dist + (size_t)n * R, (uint16_t)0);
+  Graph g{vecs, n, dp, edges, counts, R, nullptr, metric};
+
+  int64_t count = 0, bs = 1, nb = 0;
+  std::vector<std::vector<Entry>> visited;
+  std::vector<uint64_t> pairs;
+  while (count < n) {
+    bs = std::min<int64_t>(bs, n - count);
+    bs = std::min<int64_t>(bs, max_batch);
+    const int64_t s = count;
+    visited.assign((size_t)bs, {});
+    // (i) beam search of every batch vector against the pre-batch graph
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t i = 0; i < bs; ++i) {
+      search_one(g, vecs + (size_t)(s + i) * dp, 0u, (uint32_t)L, (uint32_t)LIMIT,
+                 (uint32_t)MAX_RESULT, true, &visited[(size_t)i], nullptr, nullptr);
+    }
+    // (ii)+(iii) merge_candidates_kernel + robust_prune_kernel
+#pragma omp parallel
+    {
+      std::vector<Cand> C;
+      std::vector<Cand> sel((size_t)R);
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t i = 0; i < bs; ++i) {
+        const uint32_t v = (uint32_t)(s + i);
+        C.clear();
+        for (uint32_t e = 0; e < counts[v]; ++e) {
+          const uint32_t w = edges[(size_t)v * R + e];
+          if (w == kInvalid32) continue;
+          C.push_back({w, bf2f(edge_dist[(size_t)v * R + e])});
+        }
+        for (const Entry& x : visited[(size_t)i])
+          if (x.id != v && x.id != kInvalid32) C.push_back({x.id, x.dist});
+        if ((int)C.size() > max_cands) C.resize((size_t)max_cands);
+        std::sort(C.begin(), C.end(), cand_less);
+        const int ns = robust_prune(g, dim_for_prune, v, C, alpha, R, sel.data());
+        for (int j = 0; j < ns; ++j) {
+          edges[(size_t)v * R + j] = sel[(size_t)j].id;
+          edge_dist[(size_t)v * R + j] = f2bf(sel[(size_t)j].dist);
+        }
+        counts[v] = (uint8_t)ns;
+      }
+    }
+    // (iv)+(v) reverse pairs (target << 32 | source), grouped by target
+    pairs.clear();
+    for (int64_t i = 0; i < bs; ++i) {
+      const uint32_t v = (uint32_t)(s + i);
+      for (uint32_t e = 0; e < counts[v]; ++e)
+        pairs.push_back(((uint64_t)edges[(size_t)v * R + e] << 32) | v);
+    }
+    std::sort(pairs.begin(), pairs.end());
+    std::vector<size_t> heads;
+    for (size_t p = 0; p < pairs.size(); ++p)
+      if (p == 0 || (pairs[p] >> 32) != (pairs[p - 1] >> 32)) heads.push_back(p);
+    heads.push_back(pairs.size());
+    // (vi) process_reverse_edges_kernel
+#pragma omp parallel
+    {
+      std::vector<Cand> C;
+      std::vector<Cand> sel((size_t)R);
+      const int64_t n_groups = (int64_t)heads.size() - 1;
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t h = 0; h < n_groups; ++h) {
+        const uint32_t w = (uint32_t)(pairs[heads[(size_t)h]] >> 32);
+        C.clear();
+        for (uint32_t e = 0; e < counts[w]; ++e) {
+          const uint32_t x = edges[(size_t)w * R + e];
+          if (x == kInvalid32) continue;
+          C.push_back({x, bf2f(edge_dist[(size_t)w * R + e])});
+        }
+        const uint16_t* wv = vecs + (size_t)w * dp;
+        for (size_t p = heads[(size_t)h]; p < heads[(size_t)h + 1]; ++p) {
+          if ((int)C.size() >= max_cands) break;
+          const uint32_t v = (uint32_t)(pairs[p] & 0xFFFFFFFFu);
+          if (v == kInvalid32 || v == w) continue;
+          C.push_back({v, dist(metric, wv, vecs + (size_t)v * dp, dim_for_prune)});
+        }
+        std::sort(C.begin(), C.end(), cand_less);
+        const int ns = robust_prune(g, dim_for_prune, w, C, alpha, R, sel.data());
+        for (int j = 0; j < ns; ++j) {
+          edges[(size_t)w * R + j] = sel[(size_t)j].id;
+          edge_dist[(size_t)w * R + j] = f2bf(sel[(size_t)j].dist);
+        }
+        counts[w] = (uint8_t)ns;
+      }
+    }
+    count += bs;
+    ++nb;
+    if (bs < max_batch) bs = std::min<int64_t>(max_batch, bs * 2);
+  }
+  if (n_batches_out) *n_batches_out = nb;
+  return 0;
+}
+
+// Exact kNN by the contract's distance (l2_dist / ip_dist), top-k by
+// (dist, id). Used as ground truth on small configs.
+void jo_bruteforce_exact(int metric, const uint16_t* vecs, int64_t n, const uint16_t* queries,
+                         int64_t nq, int dp, int k, int32_t* out_ids, float* out_dists,
+                         int nthreads) {
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+  {
+    std::vector<Cand> all((size_t)n);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t qi = 0; qi < nq; ++qi) {
+      const uint16_t* q = queries + (size_t)qi * dp;
+      for (int64_t i = 0; i < n; ++i)
+        all[(size_t)i] = {(uint32_t)i, dist(metric, q, vecs + (size_t)i * dp, dp)};
+      const int kk = (int)std::min<int64_t>(k, n);
+      std::partial_sort(all.begin(), all.begin() + kk, all.end(), cand_less);
+      for (int j = 0; j < k; ++j) {
+        out_ids[qi * k + j] = j < kk ? (int32_t)all[(size_t)j].id : -1;
+        out_dists[qi * k + j] = j < kk ? all[(size_t)j].dist : FLT_MAX;
+      }
+    }
+  }
+}
+
+// The reference's ground-truth arithmetic, python/jasper/__init__.py:828-926:
+// L2 = ||q||^2 + ||v||^2 - 2 q.v in fp32, clamped at 0; IP = -(q.v). Dot
+// products accumulate sequentially in fp32 (torch's order is unspecified).
+// Also the CPU baseline "exact kNN scan". Vectors are pre-converted to fp32.
+void jo_bruteforce_ref(int metric, const float* vecs, int64_t n, const float* queries,
+                       int64_t nq, int dim, int k, int32_t* out_ids, float* out_dists,
+                       int nthreads) {
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  std::vector<float> vsq((size_t)n, 0.0f);
+  if (metric == 0) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+      float s = 0.0f;
+      const float* v = vecs + (size_t)i * dim;
+      for (int t = 0; t < dim; ++t) s += v[t] * v[t];
+      vsq[(size_t)i] = s;
+    }
+  }
+#pragma omp parallel
+  {
+    std::vector<Cand> heap;
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t qi = 0; qi < nq; ++qi) {
+      const float* q = queries + (size_t)qi * dim;
+      float qsq = 0.0f;
+      for (int t = 0; t < dim; ++t) qsq += q[t] * q[t];
+      heap.clear();
+      auto worse = [](const Cand& a, const Cand& b) { return cand_less(a, b); };
+      for (int64_t i = 0; i < n; ++i) {
+        const float* v = vecs + (size_t)i * dim;
+        float dot = 0.0f;
+        for (int t = 0; t < dim; ++t) dot += q[t] * v[t];
+        float d;
+        if (metric == 0) {
+          d = qsq + vsq[(size_t)i] - 2.0f * dot;
+          if (d < 0.0f) d = 0.0f;
+        } else {
+          d = -dot;
+        }
+        const Cand c{(uint32_t)i, d};
+        if ((int)heap.size() < k) {
+          heap.push_back(c);
+          std::push_heap(heap.begin(), heap.end(), worse);
+        } else if (cand_less(c, heap.front())) {
+          std::pop_heap(heap.begin(), heap.end(), worse);
+          heap.back() = c;
+          std::push_heap(heap.begin(), heap.end(), worse);
+        }
+      }
+      std::sort(heap.begin(), heap.end(), cand_less);
+      for (int j = 0; j < k; ++j) {
+        out_ids[qi * k + j] = j < (int)heap.size() ? (int32_t)heap[(size_t)j].id : -1;
+        out_dists[qi * k + j] = j < (int)heap.size() ? heap[(size_t)j].dist : FLT_MAX;
+      }
+    }
+  }
+}
+
+// Random orthogonal matrix, rotation/rotation.cuh:28-111 (householder_qr +
+// set_rotation_matrix): A ~ N(0,1) column-major from std::mt19937_64(seed)
+// and std::normal_distribution<float>; Householder QR in float; columns of Q
+// flipped where diag(R) < 0. Outputs m = Q and mt = Q^T, both column-major.
+void jo_rotation_matrix(int d, uint64_t seed, float* m, float* mt) {
+  std::mt19937_64 rng(seed);
+  std::normal_distribution<float> N(0, 1);
+  std::vector<float> A((size_t)d * d);
+  for (int j = 0; j < d; j++)
+    for (int i = 0; i < d; i++) A[(size_t)i + (size_t)j * d] = N(rng);
+
+  std::vector<float> Q((size_t)d * d, 0.0f);
+  for (int i = 0; i < d; i++) Q[(size_t)i + (size_t)i * d] = 1.0f;
+  std::vector<float> v((size_t)d);
+  for (int k = 0; k < d; k++) {
+    float norm_sq = 0;
+    for (int i = k; i < d; i++) {
+      v[i] = A[(size_t)i + (size_t)k * d];
+      norm_sq += v[i] * v[i];
+    }
+    float norm = std::sqrt(norm_sq);
+    if (norm < 1e-12f) continue;
+    float sign = (A[(size_t)k + (size_t)k * d] >= 0) ? 1.0f : -1.0f;
+    v[k] += sign * norm;
+    float v_norm_sq = 0;
+    for (int i = k; i < d; i++) v_norm_sq += v[i] * v[i];
+    float tau = 2.0f / v_norm_sq;
+    for (int j = k; j < d; j++) {
+      float dot = 0;
+      for (int i = k; i < d; i++) dot += v[i] * A[(size_t)i + (size_t)j * d];
+      for (int i = k; i < d; i++) A[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
+    }
+    for (int j = 0; j < d; j++) {
+      float dot = 0;
+      for (int i = k; i < d; i++) dot += v[i] * Q[(size_t)i + (size_t)j * d];
+      for (int i = k; i < d; i++) Q[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
+    }
+  }
+  for (int i = 0; i < d; i++) {
+    if (A[(size_t)i + (size_t)i * d] < 0.0f) {
+      for (int j = 0; j < d; j++) Q[(size_t)j + (size_t)i * d] *= -1.0f;
+    }
+  }
+  for (int j = 0; j < d; j++) {
+    for (int i = 0; i < d; i++) {
+      m[(size_t)i + (size_t)j * d] = Q[(size_t)i + (size_t)j * d];
+      mt[(size_t)i + (size_t)j * d] = Q[(size_t)j + (size_t)i * d];
+    }
+  }
+}
+
+}  // extern "C"

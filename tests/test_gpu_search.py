@@ -1,0 +1,120 @@
+"""GPU parity of plain beam search against the oracle, on fixed graphs.
+
+A graph is built by the oracle (CPU), written in the reference file format,
+loaded by the HIP library, and searched by both. Ids and distances must be
+bit-identical (reference contract: bit-exact ids on a fixed graph with the
+same entry point and beam width; distances are the same fp32 bits because
+the accumulation order is reproduced).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import compare_search, gaussian, integer_clustered, unit
+
+pytestmark = pytest.mark.gpu
+
+
+def _load(jasper, g, tmp_path, name="g.bin"):
+    path = tmp_path / name
+    oracle.save_graph(g, path)
+    return jasper.Graph.load(str(path), dim=g.dim, n_neighbors=g.R, distance=g.distance)
+
+
+def _run(jasper, gg, q, k, bw):
+    qt = torch.from_numpy(np.ascontiguousarray(q)).cuda()
+    ids, d = gg.search(qt, k=k, beam_width=bw)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), d.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def c1_small(oracle_lib):
+    base = gaussian(3000, 128, 0)
+    q = gaussian(64, 128, 1)
+    g = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    return base, q, g
+
+
+@pytest.mark.parametrize("bw", [16, 64, 128])
+def test_search_matches_oracle_gaussian_l2(jasper, c1_small, tmp_path, bw):
+    base, q, g = c1_small
+    gg = _load(jasper, g, tmp_path)
+    ids, d = _run(jasper, gg, q, 10, bw)
+    rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+    msg = compare_search(ids, d, rid, rd)
+    assert msg is None, msg
+
+
+def test_search_matches_oracle_integer_l2_r64(jasper, oracle_lib, tmp_path):
+    base = integer_clustered(4000, 128, 0)
+    q = integer_clustered(64, 128, 1)
+    g = oracle.build(base, R=64, distance="l2", alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    for bw in (32, 96, 256):
+        ids, d = _run(jasper, gg, q, 10, bw)
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
+
+
+@pytest.mark.parametrize("R,dim", [(8, 64), (16, 96), (64, 200)])
+def test_search_matches_oracle_shapes(jasper, oracle_lib, tmp_path, R, dim):
+    base = gaussian(1500, dim, 3)
+    q = gaussian(40, dim, 4)
+    g = oracle.build(base, R=R, distance="l2", alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    ids, d = _run(jasper, gg, q, 10, 48)
+    rid, rd = oracle.beam_search(g, q, k=10, beam_width=48)
+    msg = compare_search(ids, d, rid, rd)
+    assert msg is None, msg
+
+
+def test_search_matches_oracle_ip(jasper, oracle_lib, tmp_path):
+    base = unit(2500, 96, 5)
+    q = unit(48, 96, 6)
+    g = oracle.build(base, R=32, distance="ip", alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    for bw in (16, 64):
+        ids, d = _run(jasper, gg, q, 10, bw)
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
+
+
+def test_search_k_larger_than_beam_pads(jasper, c1_small, tmp_path):
+    base, q, g = c1_small
+    gg = _load(jasper, g, tmp_path)
+    ids, d = _run(jasper, gg, q[:8], 80, 16)
+    rid, rd = oracle.beam_search(g, q[:8], k=80, beam_width=16)
+    msg = compare_search(ids, d, rid, rd)
+    assert msg is None, msg
+    assert (ids[:, 16:] == -1).all() and (d[:, 16:] == np.float32(1e30)).all()
+
+
+def test_search_empty_query_batch(jasper, c1_small, tmp_path):
+    base, q, g = c1_small
+    gg = _load(jasper, g, tmp_path)
+    ids, d = gg.search(torch.empty(0, 128, dtype=torch.float16, device="cuda"), k=10, beam_width=16)
+    assert ids.shape == (0, 10)
+
+
+def test_search_single_vertex_graph(jasper, oracle_lib, tmp_path):
+    base = gaussian(1, 128, 9)
+    g = oracle.build(base, R=32, distance="l2", alpha=1.2, max_batch=1)
+    gg = _load(jasper, g, tmp_path)
+    q = gaussian(3, 128, 10)
+    ids, d = _run(jasper, gg, q, 5, 16)
+    rid, rd = oracle.beam_search(g, q, k=5, beam_width=16)
+    msg = compare_search(ids, d, rid, rd)
+    assert msg is None, msg
+    assert (ids[:, 0] == 0).all() and (ids[:, 1:] == -1).all()
+
+
+def test_search_rejects_oversized_beam(jasper, c1_small, tmp_path):
+    base, q, g = c1_small
+    gg = _load(jasper, g, tmp_path)
+    with pytest.raises(ValueError):
+        gg.search(torch.from_numpy(q).cuda(), k=10, beam_width=1990)
