@@ -58,7 +58,7 @@ def cpu_baseline(base: np.ndarray, queries: np.ndarray, target_s: float) -> dict
     """Exact kNN scan (oracle restatement of the reference ground-truth
     arithmetic) on a query sample sized to about `target_s` seconds."""
     import oracle
-    oracle.build()
+    oracle.ensure_built()
     cores = len(os.sched_getaffinity(0))
     vb = base.astype(np.float32)
     qs = queries.astype(np.float32)

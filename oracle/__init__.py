@@ -40,7 +40,7 @@ L2 = 0
 IP = 1
 
 
-def build(force: bool = False) -> Path:
+def ensure_built(force: bool = False) -> Path:
     """Compile the oracle with its Makefile (g++ only; no GPU toolchain)."""
     if force or not _LIB_PATH.exists():
         subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
@@ -51,7 +51,7 @@ def lib():
     global _lib
     if _lib is None:
         if not _LIB_PATH.exists():
-            build()
+            ensure_built()
         _lib = ctypes.CDLL(str(_LIB_PATH))
         P = ctypes.c_void_p
         i32, i64, f32, u64 = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint64
@@ -74,6 +74,8 @@ def lib():
         _lib.jo_bruteforce_exact.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32]
         _lib.jo_bruteforce_ref.restype = None
         _lib.jo_bruteforce_ref.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32]
+        _lib.jo_gaussian_matrix.restype = None
+        _lib.jo_gaussian_matrix.argtypes = [i32, u64, P]
         _lib.jo_rotation_matrix.restype = None
         _lib.jo_rotation_matrix.argtypes = [i32, u64, P, P]
     return _lib
@@ -245,6 +247,13 @@ def rotation_matrix(d: int, seed: int = 42):
     mt = np.empty(d * d, dtype=np.float32)
     lib().jo_rotation_matrix(d, seed, _ptr(m), _ptr(mt))
     return m, mt
+
+
+def gaussian_matrix(d: int, seed: int = 42) -> np.ndarray:
+    """The N(0,1) matrix set_rotation_matrix factorises (column-major flat)."""
+    a = np.empty(d * d, dtype=np.float32)
+    lib().jo_gaussian_matrix(d, seed, _ptr(a))
+    return a
 
 
 # ------------------------------------------------------------- file format --

@@ -541,6 +541,15 @@ void jo_bruteforce_ref(int metric, const float* vecs, int64_t n, const float* qu
   }
 }
 
+// The Gaussian matrix set_rotation_matrix factorises (rotation.cuh:81-88),
+// column-major; exposed so tests can check Q against an independent QR.
+void jo_gaussian_matrix(int d, uint64_t seed, float* A) {
+  std::mt19937_64 rng(seed);
+  std::normal_distribution<float> N(0, 1);
+  for (int j = 0; j < d; j++)
+    for (int i = 0; i < d; i++) A[(size_t)i + (size_t)j * d] = N(rng);
+}
+
 // Random orthogonal matrix, rotation/rotation.cuh:28-111 (householder_qr +
 // set_rotation_matrix): A ~ N(0,1) column-major from std::mt19937_64(seed)
 // and std::normal_distribution<float>; Householder QR in float; columns of Q

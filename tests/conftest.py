@@ -23,7 +23,7 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def oracle_lib():
     import oracle
-    oracle.build()
+    oracle.ensure_built()
     return oracle
 
 
