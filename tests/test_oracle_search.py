@@ -44,8 +44,12 @@ def test_complete_graph_one_hop_is_exact():
 
 
 def test_large_beam_on_connected_graph_is_exact():
-    x = datasets.gaussian(300, 32, 5)
-    g = oracle.build(x, R=16, distance="l2", alpha=1.2)
+    # a ring (connectivity) plus the 12 nearest neighbours of every vertex
+    n = 300
+    x = datasets.gaussian(n, 32, 5)
+    nn, _ = oracle.bruteforce_exact(x, x, k=13)
+    adj = [[(i + 1) % n] + [int(j) for j in nn[i] if j != i][:12] for i in range(n)]
+    g = _graph(x, adj, R=16)
     q = datasets.gaussian(20, 32, 6)
     gt, gd = oracle.bruteforce_exact(x, q, k=10)
     ids, dist = oracle.beam_search(g, q, k=10, beam_width=400, limit=1000)
@@ -62,7 +66,8 @@ def test_path_graph_pop_order():
     g = _graph(x, adj, R=2)
     q = np.zeros((1, 8), dtype=np.float32)
     q[0, 0] = 5.25
-    ids, dist, vis_ids, vis_d, vis_c = oracle.beam_search(g, q, k=2, beam_width=2, get_visited=True)
+    ids, dist, vis_ids, vis_d, vis_c = oracle.beam_search(g, q, k=2, beam_width=2, limit=20,
+                                                          get_visited=True)
     # walk 0 -> 1 -> ... -> 5, then 6 is expanded; 7 never beats {5, 6}
     assert vis_c[0] == 7
     assert vis_ids[0, :7].tolist() == [0, 1, 2, 3, 4, 5, 6]
