@@ -34,6 +34,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -41,6 +42,22 @@ import numpy as np
 
 METRIC = "QPS @ recall@10≥0.95, 1M×128 fp16 synthetic; build vectors/sec"
 PEAK_HBM_GBS = 8000.0
+
+
+def measured_traffic(beam_width: int, n: int, nq: int):
+    """HBM bytes per launch of the search kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary, when it covers this exact workload;
+    None otherwise (the counters cannot be read from inside this process)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "beam_search_c2_1M_pmc.md")
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(r"machine-readable: traffic_bytes_per_launch=(\d+) beam_width=(\d+) n=(\d+) nq=(\d+)", text)
+    if not m or (int(m.group(2)), int(m.group(3)), int(m.group(4))) != (beam_width, n, nq):
+        return None
+    return int(m.group(1))
 
 
 def _cpu_model() -> str:
@@ -98,6 +115,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--curve-out", default=None, help="also write the QPS/recall curve as JSON here")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
+                         "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -113,6 +133,15 @@ def main() -> int:
     torch.cuda.init()
     dev = torch.device("cuda:0")
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
+
+    if args.calibrate_copy:
+        src = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("calibration copy: 3 x 512 MiB device-to-device")
 
     t0 = time.perf_counter()
     base = datasets.clustered(args.n, 128, 0)
@@ -228,7 +257,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(chosen, args.n, args.nq),
             "kernel": "beam_search_kernel<4,0,false>",
             "kernel_ms": kernel_ms,
             "algorithmic_bytes_per_launch": alg_bytes,

@@ -139,6 +139,18 @@ int64_t jasperx_last_build_stats(double* out7);
 int64_t jasperx_search_stats(int64_t handle, const void* queries, int64_t n_queries, int64_t dim,
                              int64_t k, int64_t beam_width, int64_t limit, uint32_t* out_stats,
                              void* stream);
+/* Host copies of a graph's device columns for parity tests: vectors
+ * [n, padded_dim] fp16 bits (after prerotation when enabled; returns
+ * padded_dim); LSH calibration (k_ranks floats, norm_denom) and per-edge
+ * rows [n, row_bytes] (returns row_bytes); PQ centroids [M*256*dsub] f32,
+ * codes [n, M*R] and vector norms [n] (returns dsub). NULL skips a part. */
+int64_t jasperx_export_vectors(int64_t handle, uint16_t* out);
+int64_t jasperx_export_lsh(int64_t handle, float* c_per_rank, float* norm_denom, uint8_t* rows);
+int64_t jasperx_export_pq(int64_t handle, float* centroids, uint8_t* codes, float* norms);
+/* The prerotation matrix for (dim, seed), column-major f32 [dim*dim], as
+ * set_rotation_matrix returns it before the fp16 cast (reference
+ * include/jasper/rotation/rotation.cuh:71-111). Host-only. */
+int64_t jasperx_rotation_matrix(int64_t dim, int64_t seed, float* out);
 /* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 

@@ -82,6 +82,10 @@ _AGNOSTIC = {
     "jasperx_export_graph": [_i64, _ptr, _ptr, _ptr],
     "jasperx_last_build_stats": [_ptr],
     "jasperx_search_stats": [_i64, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr],
+    "jasperx_export_vectors": [_i64, _ptr],
+    "jasperx_export_lsh": [_i64, _ptr, _ptr, _ptr],
+    "jasperx_export_pq": [_i64, _ptr, _ptr, _ptr],
+    "jasperx_rotation_matrix": [_i64, _i64, _ptr],
 }
 
 
@@ -480,6 +484,40 @@ class Graph:
                                           edist.ctypes.data_as(_ptr), counts.ctypes.data_as(_ptr))
         return edges, edist, counts
 
+    def export_vectors(self) -> np.ndarray:
+        """Host copy of the stored rows [n, padded_dim] as fp16 bits (after
+        prerotation when the graph was prerotated); a test extension."""
+        self._check_alive()
+        dp = _agnostic("jasperx_export_vectors")(self._handle, None)
+        out = np.empty((self.n_vectors, dp), dtype=np.uint16)
+        _agnostic("jasperx_export_vectors")(self._handle, out.ctypes.data_as(_ptr))
+        return out
+
+    def export_lsh(self):
+        """(c_per_rank f32 [k_ranks], norm_denom, rows u8 [n, row_bytes]); a
+        test extension."""
+        self._check_alive()
+        fn = _agnostic("jasperx_export_lsh")
+        row_bytes = fn(self._handle, None, None, None)
+        c = np.empty(self._k_ranks, dtype=np.float32)
+        nd = np.empty(1, dtype=np.float32)
+        rows = np.empty((self.n_vectors, row_bytes), dtype=np.uint8)
+        fn(self._handle, c.ctypes.data_as(_ptr), nd.ctypes.data_as(_ptr), rows.ctypes.data_as(_ptr))
+        return c, float(nd[0]), rows
+
+    def export_pq(self):
+        """(centroids f32 [M*256*dsub], codes u8 [n, M*R], vector norms f32
+        [n]); a test extension."""
+        self._check_alive()
+        fn = _agnostic("jasperx_export_pq")
+        dsub = fn(self._handle, None, None, None)
+        M = self._k_ranks
+        cent = np.empty(M * 256 * dsub, dtype=np.float32)
+        codes = np.empty((self.n_vectors, M * self._n_neighbors), dtype=np.uint8)
+        norms = np.empty(self.n_vectors, dtype=np.float32)
+        fn(self._handle, cent.ctypes.data_as(_ptr), codes.ctypes.data_as(_ptr), norms.ctypes.data_as(_ptr))
+        return cent, codes, norms
+
     def search_stats(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
                      limit: int | None = None) -> np.ndarray:
         """Per-query work counters of the plain search [n_queries, 4]:
@@ -589,3 +627,11 @@ __all__ = [
     "get_recall", "generate_groundtruth", "save_groundtruth", "parse_storage_size",
     "last_build_stats", "library_path",
 ]
+
+
+def rotation_matrix(dim: int, seed: int = 42) -> np.ndarray:
+    """The prerotation matrix for (dim, seed), column-major f32 [dim*dim]
+    (reference include/jasper/rotation/rotation.cuh:71-111)."""
+    out = np.empty(dim * dim, dtype=np.float32)
+    _agnostic("jasperx_rotation_matrix")(dim, seed, out.ctypes.data_as(_ptr))
+    return out

@@ -439,6 +439,42 @@ extern "C" int64_t jasperx_export_graph(int64_t h, uint32_t* edges, uint16_t* ed
   });
 }
 
+extern "C" int64_t jasperx_export_vectors(int64_t h, uint16_t* out) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (out && g.n > 0)
+      hip_check(hipMemcpy(out, g.vecs, (size_t)g.n * g.dp * 2, hipMemcpyDefault), "download vectors");
+    return (int64_t)g.dp;
+  });
+}
+
+extern "C" int64_t jasperx_export_lsh(int64_t h, float* c_per_rank, float* norm_denom, uint8_t* rows) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (!g.lsh) throw std::runtime_error("graph has no LSH artifacts");
+    const LshArtifacts& a = *g.lsh;
+    if (c_per_rank) std::memcpy(c_per_rank, a.c_per_rank.data(), a.c_per_rank.size() * 4);
+    if (norm_denom) *norm_denom = a.norm_denom;
+    if (rows && g.n > 0) hip_check(hipMemcpy(rows, a.rows, (size_t)g.n * a.row_bytes, hipMemcpyDefault), "download lsh rows");
+    return (int64_t)a.row_bytes;
+  });
+}
+
+extern "C" int64_t jasperx_export_pq(int64_t h, float* centroids, uint8_t* codes, float* norms) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (!g.pq) throw std::runtime_error("graph has no PQ artifacts");
+    const PqArtifacts& a = *g.pq;
+    if (centroids)
+      hip_check(hipMemcpy(centroids, a.centroids, (size_t)a.m * 256 * a.dsub * 4, hipMemcpyDefault), "download centroids");
+    if (codes && g.n > 0)
+      hip_check(hipMemcpy(codes, a.codes, (size_t)g.n * a.m * g.R, hipMemcpyDefault), "download codes");
+    if (norms && g.n > 0 && g.vector_norms)
+      hip_check(hipMemcpy(norms, g.vector_norms, (size_t)g.n * 4, hipMemcpyDefault), "download norms");
+    return (int64_t)a.dsub;
+  });
+}
+
 extern "C" int64_t jasperx_last_build_stats(double* out7) {
   return guarded([&]() -> int64_t {
     std::lock_guard<std::mutex> lock(g_mutex);

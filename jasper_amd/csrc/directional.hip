@@ -1,8 +1,32 @@
-// directional.hip -- directional (LSH / PQ) path.
+// directional.hip -- directional (estimator-driven) path: prerotation, LSH
+// and PQ artifacts, the directional beam search, and the file trailer.
+//
+// References: graph_beam_search.cuh:55-347 (skeleton), beam_search_common.cuh:
+// 87-185 (exact visit, frontier list), directional_beam_search.cuh:31-192
+// (LSH estimator), pq_beam_search.cuh:32-201 (PQ estimator),
+// lsh/lsh_globals.cuh + lsh/lsh_kernels.cuh (LSH artifacts),
+// pq/pq_kernels.cuh (PQ artifacts), rotation/rotation.cuh (rotation),
+// index/graph.cuh:1790-2093 (trailer), ffi/jasper_ffi_common.cuh:442-775.
+//
+// Reductions reproduce the reference's 128-thread trees exactly: a query is
+// one wave64 whose lane l plays virtual threads l and l + 64; each 32-lane
+// half runs the warp's xor butterfly (16, 8, 4, 2, 1) and the four warp sums
+// w0..w3 combine as (w0 + w2) + (w1 + w3), which is what the second-stage
+// butterfly over {w0, w1, w2, w3, 0, ...} computes.
+#include "build.hpp"
+#include "common.hpp"
 #include "directional.hpp"
 #include "directional_api.hpp"
+#include "search.hpp"
 
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
 #include <stdexcept>
+#include <vector>
 
 namespace jasper_amd {
 
@@ -15,31 +39,1146 @@ PqArtifacts::~PqArtifacts() {
   if (codes) (void)hipFree(codes);
 }
 
+constexpr uint32_t kInv31 = 0x7FFFFFFFu;
+constexpr uint32_t kTrailerMagic = 0x484C5344u;   // graph.cuh:1815
+constexpr uint32_t kTrailerVersion = 1u;
+
 void check_directional_dim(bool small_dim, int64_t dim) {
   if (small_dim ? dim > 128 : dim <= 128)
     throw std::invalid_argument("dim " + std::to_string(dim) + " does not match the config's dim bucket");
 }
 
-static void not_yet(const char* what) {
-  throw std::runtime_error(std::string(what) + " is not available in this build yet");
+// ------------------------------------------------------------- fp16 ops --
+
+__device__ __forceinline__ uint32_t hsub2_bits(uint32_t a, uint32_t b) {
+  __half2 x = *reinterpret_cast<__half2*>(&a), y = *reinterpret_cast<__half2*>(&b);
+  __half2 r = __hsub2(x, y);
+  return *reinterpret_cast<uint32_t*>(&r);
 }
 
-std::unique_ptr<Graph> construct_directional(uint32_t, int, uint32_t, bool, const void*, int64_t, int64_t, double,
-                                             int64_t, bool, bool, uint64_t, hipStream_t, BuildStats*) {
-  not_yet("construct_directional");
-  return nullptr;
+__device__ __forceinline__ uint32_t hmul2_bits(uint32_t a, uint32_t b) {
+  __half2 x = *reinterpret_cast<__half2*>(&a), y = *reinterpret_cast<__half2*>(&b);
+  __half2 r = __hmul2(x, y);
+  return *reinterpret_cast<uint32_t*>(&r);
 }
-void build_lsh(Graph&, int64_t, uint64_t) { not_yet("build_lsh"); }
-void build_pq(Graph&, int64_t, int64_t, uint64_t) { not_yet("build_pq"); }
-void directional_search(Graph&, bool, const void*, int64_t, int64_t, int32_t*, float*, int64_t, int64_t, int64_t,
-                        bool, hipStream_t) {
-  not_yet("directional_search");
+
+__device__ __forceinline__ uint16_t hsub_bits(uint16_t a, uint16_t b) {
+  __half r = __hsub(__ushort_as_half(a), __ushort_as_half(b));
+  return __half_as_ushort(r);
 }
-void save_directional_file(const Graph&, const std::string&) { not_yet("save_directional"); }
-std::unique_ptr<Graph> load_directional_file(const std::string&, uint32_t, uint32_t, int, uint32_t, bool, bool, bool,
-                                             uint64_t) {
-  not_yet("load_directional");
-  return nullptr;
+
+__device__ __forceinline__ float h2f16(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// 32-lane xor butterfly inside each half of the wave.
+__device__ __forceinline__ float warp32_sum(float v) {
+#pragma unroll
+  for (int d = 16; d > 0; d >>= 1) v = v + __shfl_xor(v, d, 64);
+  return v;
+}
+
+// The reference 128-thread reduction, p0 = virtual thread lane, p1 =
+// virtual thread lane + 64. Every lane receives the result.
+__device__ __forceinline__ float block128_sum(float p0, float p1) {
+  p0 = warp32_sum(p0);
+  p1 = warp32_sum(p1);
+  const float w0 = __shfl(p0, 0, 64), w1 = __shfl(p0, 32, 64);
+  const float w2 = __shfl(p1, 0, 64), w3 = __shfl(p1, 32, 64);
+  return (w0 + w2) + (w1 + w3);
+}
+
+// splitmix64 counter sampler, identical to the oracle's
+// (oracle/directional_oracle.cpp, sample_edge).
+__host__ __device__ __forceinline__ uint64_t splitmix(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+// pq_hash, pq_kernels.cuh:19-24
+__host__ __device__ __forceinline__ uint64_t pq_hash(uint64_t x, uint64_t seed) {
+  x += seed + 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+// A random valid edge (u -> nb) for sample s, up to 8 attempts
+// (lsh_globals.cuh:46-67, pq_kernels.cuh:77-93).
+__device__ bool sample_edge(const uint32_t* edges, const uint8_t* counts, int64_t n, uint32_t R, uint64_t seed,
+                            uint64_t s, uint32_t* u_out, uint32_t* nb_out) {
+  uint64_t state = splitmix(seed ^ splitmix(s + 1));
+  for (int attempt = 0; attempt < 8; ++attempt) {
+    state = splitmix(state);
+    const uint32_t r1 = (uint32_t)(state >> 32);
+    state = splitmix(state);
+    const uint32_t r2 = (uint32_t)(state >> 32);
+    const uint32_t qlid = (uint32_t)((uint64_t)r1 % (uint64_t)n);
+    const uint32_t cnt = counts[qlid];
+    if (cnt == 0) continue;
+    const uint32_t e = r2 % cnt;
+    const uint32_t nb = edges[(size_t)qlid * R + e];
+    if (nb == kInvalid32) continue;
+    *u_out = qlid;
+    *nb_out = nb;
+    return true;
+  }
+  return false;
+}
+
+// ------------------------------------------------------------- rotation --
+// x'_i = sum_k P[k + i*dim] * x_k, P column-major fp16, fp32 fma in k order,
+// fp16 round-to-nearest output (construct.cuh:1077-1089 computes the same
+// product with cuBLAS GemmEx; its summation order is not specified).
+__global__ void rotate_rows_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t dim, uint32_t dp_in,
+                                   uint32_t dp_out, const uint16_t* __restrict__ P, uint16_t* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = t / dp_out;
+  const uint32_t i = (uint32_t)(t % dp_out);
+  if (row >= n) return;
+  uint16_t r = 0;
+  if (i < dim) {
+    const uint16_t* xr = x + (size_t)row * dp_in;
+    const uint16_t* pc = P + (size_t)i * dim;
+    float acc = 0.0f;
+    for (uint32_t k = 0; k < dim; ++k) acc = __builtin_fmaf(h2f16(pc[k]), h2f16(xr[k]), acc);
+    r = __half_as_ushort(__float2half_rn(acc));
+  }
+  out[(size_t)row * dp_out + i] = r;
+}
+
+static void rotate_rows(const void* x, int64_t n, uint32_t dim, uint32_t dp_in, uint32_t dp_out, const void* P,
+                        void* out, hipStream_t s) {
+  if (n <= 0) return;
+  const int64_t total = n * (int64_t)dp_out;
+  const uint32_t block = 256;
+  const int64_t grid = (total + block - 1) / block;
+  if (grid > 0x7FFFFFFFll) throw std::invalid_argument("rotation too large for one launch");
+  hipLaunchKernelGGL(rotate_rows_kernel, dim3((uint32_t)grid), dim3(block), 0, s, (const uint16_t*)x, n, dim,
+                     dp_in, dp_out, (const uint16_t*)P, (uint16_t*)out);
+  hip_check(hipGetLastError(), "launch rotate_rows_kernel");
+}
+
+// Random orthogonal matrix (rotation.cuh:28-111): mt19937_64 + float normal
+// distribution, Householder loop, column flips where R_ii < 0. Column-major.
+static std::vector<float> rotation_matrix(uint32_t d, uint64_t seed);
+
+static void* device_rotation_fp16(uint32_t d, uint64_t seed) {
+  const std::vector<float> m = rotation_matrix(d, seed);
+  std::vector<uint16_t> h(m.size());
+  for (size_t i = 0; i < m.size(); ++i) h[i] = __half_as_ushort(__float2half_rn(m[i]));
+  void* p = nullptr;
+  hip_check(hipMalloc(&p, h.size() * 2), "alloc rotation matrix");
+  hip_check(hipMemcpy(p, h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload rotation matrix");
+  return p;
+}
+
+// ------------------------------------------------------------ LSH build --
+
+// accumulate_rank_sums (lsh_globals.cuh:17-158): one wave per sample;
+// per-sample contributions are written out and summed in sample order by
+// lsh_finalize_kernel (the reference sums with float atomics).
+__global__ __launch_bounds__(64) void lsh_calib_kernel(const uint16_t* __restrict__ vecs, int64_t n, uint32_t dp,
+                                                       const uint32_t* __restrict__ edges,
+                                                       const uint8_t* __restrict__ counts, uint32_t R, uint32_t K,
+                                                       uint64_t seed, float* __restrict__ contrib,
+                                                       uint8_t* __restrict__ valid) {
+  extern __shared__ uint32_t keys[];
+  const uint32_t lane = threadIdx.x;
+  const uint64_t s = blockIdx.x;
+  uint32_t u = 0, nb = 0;
+  const bool ok = sample_edge(edges, counts, n, R, seed, s, &u, &nb);
+  if (!ok) {
+    if (lane == 0) valid[s] = 0;
+    return;
+  }
+  const uint16_t* uv = vecs + (size_t)u * dp;
+  const uint16_t* nv = vecs + (size_t)nb * dp;
+  float p0 = 0.0f, p1 = 0.0f;
+  for (uint32_t i = lane; i < dp; i += 128) {
+    const uint16_t d = hsub_bits(nv[i], uv[i]);
+    keys[i] = ((uint32_t)(d & 0x7FFFu) << 16) | ((uint32_t)(d >> 15) << 15) | (i & 0x7FFFu);
+    const float f = h2f16(d);
+    p0 = __builtin_fmaf(f, f, p0);
+  }
+  for (uint32_t i = lane + 64; i < dp; i += 128) {
+    const uint16_t d = hsub_bits(nv[i], uv[i]);
+    keys[i] = ((uint32_t)(d & 0x7FFFu) << 16) | ((uint32_t)(d >> 15) << 15) | (i & 0x7FFFu);
+    const float f = h2f16(d);
+    p1 = __builtin_fmaf(f, f, p1);
+  }
+  const float inv_norm = __fdiv_rn(1.0f, __fsqrt_rn(block128_sum(p0, p1) + 1e-20f));
+  wave_sync();
+  if (inv_norm > 1e9f) {
+    if (lane == 0) valid[s] = 0;
+    return;
+  }
+  for (uint32_t r = 0; r < K; ++r) {
+    uint32_t m = 0;
+    for (uint32_t i = lane; i < dp; i += 64) m = max(m, keys[i]);
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, d, 64));
+    if (lane == 0) {
+      contrib[s * K + r] = h2f16((uint16_t)(m >> 16)) * inv_norm;
+      keys[m & 0x7FFFu] = 0;
+    }
+    wave_sync();
+  }
+  if (lane == 0) valid[s] = 1;
+}
+
+// finalize_lsh_globals (lsh_globals.cuh:160-178), sums in sample order.
+__global__ void lsh_finalize_kernel(const float* __restrict__ contrib, const uint8_t* __restrict__ valid,
+                                    int64_t n_samples, uint32_t K, float* __restrict__ out /* K + 2 */) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float sum[16];
+  for (uint32_t r = 0; r < K; ++r) sum[r] = 0.0f;
+  int64_t nv = 0;
+  for (int64_t s = 0; s < n_samples; ++s) {
+    if (!valid[s]) continue;
+    ++nv;
+    for (uint32_t r = 0; r < K; ++r) sum[r] = sum[r] + contrib[s * K + r];
+  }
+  const float inv_n = __fdiv_rn(1.0f, (float)nv);
+  float denom = 0.0f;
+  for (uint32_t r = 0; r < K; ++r) {
+    const float c = sum[r] * inv_n;
+    out[r] = c;
+    denom = __builtin_fmaf(c, c, denom);
+  }
+  out[K] = denom;
+  out[K + 1] = (float)nv;
+}
+
+// populate_lsh (lsh/lsh_kernels.cuh:9-132): one wave per vertex, edges
+// e < count (slots past the count stay zero). The row is staged in LDS and
+// written out once.
+__global__ __launch_bounds__(64) void lsh_populate_kernel(const uint16_t* __restrict__ vecs, int64_t n, uint32_t dp,
+                                                          const uint32_t* __restrict__ edges,
+                                                          const uint8_t* __restrict__ counts, uint32_t R, uint32_t K,
+                                                          uint32_t pbytes, uint8_t* __restrict__ rows,
+                                                          uint32_t row_bytes) {
+  extern __shared__ uint32_t keys[];           // [dp] then the staged row
+  uint8_t* stage = reinterpret_cast<uint8_t*>(keys + dp);
+  const uint32_t lane = threadIdx.x;
+  const uint32_t coord_bits = pbytes * 8 - 1;
+  const uint32_t coord_mask = (1u << coord_bits) - 1u;
+  const uint32_t word_mask = (1u << (coord_bits + 1)) - 1u;
+  for (int64_t u = blockIdx.x; u < n; u += gridDim.x) {
+    for (uint32_t b = lane; b < row_bytes; b += 64) stage[b] = 0;
+    const uint16_t* uv = vecs + (size_t)u * dp;
+    const uint32_t cnt = min((uint32_t)counts[u], R);
+    for (uint32_t e = 0; e < cnt; ++e) {
+      const uint32_t nb = edges[(size_t)u * R + e];
+      const uint16_t* nv = vecs + (size_t)nb * dp;
+      wave_sync();
+      float p[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        for (uint32_t i = lane + 64u * h; i < dp; i += 128) {
+          const uint16_t d = hsub_bits(nv[i], uv[i]);
+          keys[i] = ((uint32_t)(d & 0x7FFFu) << (coord_bits + 1)) | ((uint32_t)(d >> 15) << coord_bits) |
+                    (i & coord_mask);
+          const float f = h2f16(d);
+          p[h] = __builtin_fmaf(f, f, p[h]);
+        }
+      }
+      const float mag_sq = block128_sum(p[0], p[1]);
+      wave_sync();
+      for (uint32_t r = 0; r < K; ++r) {
+        uint32_t m = 0;
+        for (uint32_t i = lane; i < dp; i += 64) m = max(m, keys[i]);
+#pragma unroll
+        for (int d = 32; d > 0; d >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, d, 64));
+        if (lane == 0) {
+          const uint32_t word = m & word_mask;
+          const size_t at = ((size_t)e * K + r) * pbytes;
+          stage[at] = (uint8_t)word;
+          if (pbytes == 2) stage[at + 1] = (uint8_t)(word >> 8);
+          keys[m & coord_mask] = 0;
+        }
+        wave_sync();
+      }
+      if (lane == 0) {
+        const uint16_t mb = f2bf(mag_sq);
+        const size_t at = (size_t)R * K * pbytes + 2 * (size_t)e;
+        stage[at] = (uint8_t)mb;
+        stage[at + 1] = (uint8_t)(mb >> 8);
+      }
+    }
+    wave_sync();
+    uint8_t* row = rows + (size_t)u * row_bytes;
+    for (uint32_t b = lane; b < row_bytes; b += 64) row[b] = stage[b];
+    wave_sync();
+  }
+}
+
+// ------------------------------------------------------------- PQ build --
+
+// pq_sample_residuals (pq_kernels.cuh:64-106): residual nb - u (fp16) of a
+// sampled edge per training row, zeros when no edge was found.
+__global__ void pq_sample_kernel(const uint16_t* __restrict__ vecs, int64_t n, uint32_t dp,
+                                 const uint32_t* __restrict__ edges, const uint8_t* __restrict__ counts, uint32_t R,
+                                 int64_t n_train, uint64_t seed, uint16_t* __restrict__ X) {
+  const int64_t p = blockIdx.x;
+  if (p >= n_train) return;
+  __shared__ uint32_t s_u, s_nb, s_ok;
+  if (threadIdx.x == 0) {
+    uint32_t u = 0, nb = 0;
+    s_ok = sample_edge(edges, counts, n, R, seed, (uint64_t)p, &u, &nb) ? 1u : 0u;
+    s_u = u;
+    s_nb = nb;
+  }
+  __syncthreads();
+  uint16_t* row = X + (size_t)p * dp;
+  for (uint32_t i = threadIdx.x; i < dp; i += blockDim.x)
+    row[i] = s_ok ? hsub_bits(vecs[(size_t)s_nb * dp + i], vecs[(size_t)s_u * dp + i]) : (uint16_t)0;
+}
+
+// pq_kmeans_init (pq_kernels.cuh:110-125)
+__global__ void pq_init_kernel(const uint16_t* __restrict__ X, int64_t n_train, uint32_t dp, uint32_t M, uint32_t dsub,
+                               uint64_t init_seed, float* __restrict__ C) {
+  const uint32_t jc = blockIdx.x;
+  const uint32_t j = jc / 256;
+  const uint64_t r = pq_hash(jc, init_seed) % (uint64_t)n_train;
+  for (uint32_t t = threadIdx.x; t < dsub; t += blockDim.x)
+    C[(size_t)jc * dsub + t] = h2f16(X[(size_t)r * dp + (size_t)j * dsub + t]);
+}
+
+// pq_kmeans_assign (pq_kernels.cuh:127-160): nearest centroid per
+// (point, subspace), sequential fma distance, ties -> smaller index.
+__global__ void pq_assign_kernel(const uint16_t* __restrict__ X, int64_t n_train, uint32_t dp, uint32_t M,
+                                 uint32_t dsub, const float* __restrict__ C, uint8_t* __restrict__ labels,
+                                 bool stage) {
+  extern __shared__ float sc_lds[];  // [256 * dsub] centroids of subspace j when staged
+  const uint32_t j = blockIdx.y;
+  const float* sc = C + (size_t)j * 256 * dsub;
+  if (stage) {
+    for (uint32_t i = threadIdx.x; i < 256 * dsub; i += blockDim.x) sc_lds[i] = sc[i];
+    __syncthreads();
+    sc = sc_lds;
+  }
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n_train) return;
+  const uint16_t* x = X + (size_t)p * dp + (size_t)j * dsub;
+  float best = FLT_MAX;
+  uint32_t bi = 0;
+  for (uint32_t c = 0; c < 256; ++c) {
+    const float* cc = sc + (size_t)c * dsub;
+    float d = 0.0f;
+    for (uint32_t t = 0; t < dsub; ++t) {
+      const float df = h2f16(x[t]) - cc[t];
+      d = __builtin_fmaf(df, df, d);
+    }
+    if (d < best) { best = d; bi = c; }
+  }
+  labels[(size_t)p * M + j] = (uint8_t)bi;
+}
+
+// pq_kmeans_accumulate + pq_kmeans_finalize (pq_kernels.cuh:162-211): one
+// thread per (subspace, centroid, coordinate); sums in sample order; empty
+// clusters reseeded from a pq_hash pick.
+__global__ void pq_update_kernel(const uint16_t* __restrict__ X, int64_t n_train, uint32_t dp, uint32_t M,
+                                 uint32_t dsub, const uint8_t* __restrict__ labels, uint64_t init_seed, uint32_t iter,
+                                 float* __restrict__ C) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= (int64_t)M * 256 * dsub) return;
+  const uint32_t jc = (uint32_t)(tid / dsub), t = (uint32_t)(tid % dsub);
+  const uint32_t j = jc / 256, c = jc % 256;
+  float s = 0.0f;
+  uint32_t cnt = 0;
+  for (int64_t p = 0; p < n_train; ++p) {
+    if (labels[(size_t)p * M + j] == c) {
+      ++cnt;
+      s = s + h2f16(X[(size_t)p * dp + (size_t)j * dsub + t]);
+    }
+  }
+  if (cnt > 0) {
+    C[(size_t)jc * dsub + t] = s * __fdiv_rn(1.0f, (float)cnt);
+  } else {
+    const uint64_t r = pq_hash((uint64_t)jc ^ ((uint64_t)iter * 0x9E3779B9u), init_seed) % (uint64_t)n_train;
+    C[(size_t)jc * dsub + t] = h2f16(X[(size_t)r * dp + (size_t)j * dsub + t]);
+  }
+}
+
+// pq_populate (pq_kernels.cuh:249-295): one wave per vertex; for each edge
+// the fp16 residual goes to LDS and each lane scores centroids c = lane + 64m
+// (argmin, ties to the smaller index). Codes are staged in LDS.
+__global__ __launch_bounds__(64) void pq_encode_kernel(const uint16_t* __restrict__ vecs, int64_t n, uint32_t dp,
+                                                       const uint32_t* __restrict__ edges,
+                                                       const uint8_t* __restrict__ counts, uint32_t R, uint32_t M,
+                                                       uint32_t dsub, const float* __restrict__ C,
+                                                       uint8_t* __restrict__ codes) {
+  extern __shared__ float res[];  // [dp] then M*R staged codes
+  uint8_t* stage = reinterpret_cast<uint8_t*>(res + dp);
+  const uint32_t lane = threadIdx.x;
+  const uint32_t row_bytes = M * R;
+  for (int64_t u = blockIdx.x; u < n; u += gridDim.x) {
+    for (uint32_t b = lane; b < row_bytes; b += 64) stage[b] = 0;
+    const uint32_t cnt = min((uint32_t)counts[u], R);
+    for (uint32_t e = 0; e < cnt; ++e) {
+      const uint32_t nb = edges[(size_t)u * R + e];
+      wave_sync();
+      for (uint32_t i = lane; i < dp; i += 64)
+        res[i] = h2f16(hsub_bits(vecs[(size_t)nb * dp + i], vecs[(size_t)u * dp + i]));
+      wave_sync();
+      for (uint32_t j = 0; j < M; ++j) {
+        float best = FLT_MAX;
+        uint32_t bi = 0;
+        const float* rj = res + (size_t)j * dsub;
+        for (uint32_t c = lane; c < 256; c += 64) {
+          const float* cc = C + ((size_t)j * 256 + c) * dsub;
+          float d = 0.0f;
+          for (uint32_t t = 0; t < dsub; ++t) {
+            const float df = rj[t] - cc[t];
+            d = __builtin_fmaf(df, df, d);
+          }
+          if (d < best) { best = d; bi = c; }
+        }
+#pragma unroll
+        for (int dd = 32; dd > 0; dd >>= 1) {
+          const float ob = __shfl_xor(best, dd, 64);
+          const uint32_t oi = (uint32_t)__shfl_xor((int)bi, dd, 64);
+          if (ob < best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+        }
+        if (lane == 0) stage[(size_t)j * R + e] = (uint8_t)bi;
+      }
+    }
+    wave_sync();
+    uint8_t* code = codes + (size_t)u * row_bytes;
+    for (uint32_t b = lane; b < row_bytes; b += 64) code[b] = stage[b];
+    wave_sync();
+  }
+}
+
+// pq_compute_vector_norms (pq_kernels.cuh:218-247)
+__global__ __launch_bounds__(64) void norms_kernel(const uint16_t* __restrict__ vecs, int64_t n, uint32_t dp,
+                                                   float* __restrict__ out) {
+  const uint32_t lane = threadIdx.x;
+  for (int64_t u = blockIdx.x; u < n; u += gridDim.x) {
+    const uint16_t* x = vecs + (size_t)u * dp;
+    float p0 = 0.0f, p1 = 0.0f;
+    for (uint32_t i = lane; i < dp; i += 128) {
+      const float v = h2f16(x[i]);
+      p0 = __builtin_fmaf(v, v, p0);
+    }
+    for (uint32_t i = lane + 64; i < dp; i += 128) {
+      const float v = h2f16(x[i]);
+      p1 = __builtin_fmaf(v, v, p1);
+    }
+    const float s = block128_sum(p0, p1);
+    if (lane == 0) out[u] = s;
+  }
+}
+
+// ---------------------------------------------------- directional search --
+
+struct DirArgs {
+  const uint16_t* vecs;
+  int64_t n;
+  uint32_t dp, R;
+  const uint32_t* edges;
+  const uint8_t* counts;
+  const uint32_t* deleted;
+  const uint16_t* queries;  // [nq, dp]
+  uint32_t medoid, k, bw, limit, max_result;
+  int32_t* out_ids;
+  float* out_dists;
+  // LSH
+  uint32_t K, pbytes;
+  const uint8_t* lsh_rows;
+  uint32_t row_bytes;
+  float c[16];
+  float inv_norm_denom;
+  // PQ
+  uint32_t M, dsub;
+  const float* centroids;
+  const uint8_t* codes;
+  const float* norms;
+};
+
+// Exact distance of the popped node (compute_qu_diff_and_exact,
+// beam_search_common.cuh:87-154). L2: fp16 q - u, stored to diff, sum of
+// f0^2 + f1^2 per half2; IP: sum of fp16 products per half2.
+template <bool L2>
+__device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4* urow, uint32_t nchunks, uint4* diff) {
+  const uint32_t lane = lane_id();
+  float p[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float local = 0.0f;
+    for (uint32_t i = lane + 64u * h; i < nchunks; i += 128) {
+      const uint4 q = qrow[i], u = urow[i];
+      const uint32_t qw[4] = {q.x, q.y, q.z, q.w}, uw[4] = {u.x, u.y, u.z, u.w};
+      uint32_t dw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (L2) {
+          dw[j] = hsub2_bits(qw[j], uw[j]);
+          const float f0 = h2f_lo(dw[j]), f1 = h2f_hi(dw[j]);
+          local = local + (f0 * f0 + f1 * f1);
+        } else {
+          const uint32_t pw = hmul2_bits(qw[j], uw[j]);
+          local = local + (h2f_lo(pw) + h2f_hi(pw));
+        }
+      }
+      if constexpr (L2) diff[i] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    }
+    p[h] = local;
+  }
+  return block128_sum(p[0], p[1]);
+}
+
+template <int METRIC, bool PQ>
+__global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
+  extern __shared__ uint64_t smem[];
+  constexpr bool L2 = METRIC == kL2;
+  const uint32_t lane = threadIdx.x;
+  const uint32_t qid = blockIdx.x;
+  const uint32_t nchunks = a.dp / 8;
+  const uint32_t cap = a.bw + a.R;
+  uint64_t* buf0 = smem;
+  uint64_t* buf1 = buf0 + cap;
+  uint64_t* T = buf1 + cap;
+  float* Fd = reinterpret_cast<float*>(T + 64);  // frontier distances (exact bits)
+  uint32_t* Fi = reinterpret_cast<uint32_t*>(Fd + a.k);
+  uint4* qv = reinterpret_cast<uint4*>(smem + ((2 * cap + 64 + a.k + 1) & ~1u));  // 16-byte aligned
+  uint4* xv = qv + nchunks;  // L2 LSH: fp16 q - u
+  float* lut = reinterpret_cast<float*>(xv + nchunks);
+
+  const uint4* qsrc = reinterpret_cast<const uint4*>(a.queries) + (size_t)qid * nchunks;
+  for (uint32_t i = lane; i < nchunks; i += 64) qv[i] = qsrc[i];
+  wave_sync();
+  const uint16_t* q16 = reinterpret_cast<const uint16_t*>(qv);
+
+  float q_sq = 0.0f;
+  if constexpr (PQ) {
+    // pq_build_lut: one 32-lane group per centroid, lanes stride dsub
+    const uint32_t half = lane >> 5, hl = lane & 31u;
+    const uint32_t total = a.M * 256;
+    for (uint32_t e0 = 0; e0 < total; e0 += 2) {
+      const uint32_t e = e0 + half;
+      float acc = 0.0f;
+      if (e < total) {
+        const uint32_t j = e / 256;
+        const float* C = a.centroids + (size_t)e * a.dsub;
+        const uint16_t* qj = q16 + (size_t)j * a.dsub;
+        for (uint32_t t = hl; t < a.dsub; t += 32) acc = __builtin_fmaf(h2f16(qj[t]), C[t], acc);
+      }
+      acc = warp32_sum(acc);
+      if (hl == 0 && e < total) lut[e] = acc;
+    }
+    if constexpr (L2) {
+      float p0 = 0.0f, p1 = 0.0f;
+      for (uint32_t i = lane; i < a.dp; i += 128) {
+        const float v = h2f16(q16[i]);
+        p0 = __builtin_fmaf(v, v, p0);
+      }
+      for (uint32_t i = lane + 64; i < a.dp; i += 128) {
+        const float v = h2f16(q16[i]);
+        p1 = __builtin_fmaf(v, v, p1);
+      }
+      q_sq = block128_sum(p0, p1);
+    }
+    wave_sync();
+  }
+
+  // B = [(medoid, est 0.0, unvisited)], F empty (graph_beam_search.cuh:141-149)
+  uint64_t* B = buf0;
+  uint64_t* NB = buf1;
+  if (lane == 0) B[0] = make_key(0.0f, a.medoid);
+  uint32_t cnt = 1, fc = 0, vc = 0, loop = 0;
+  wave_sync();
+  while (loop <= a.limit) {
+    loop += 1;
+    int p = -1;
+    for (uint32_t base = 0; base < cnt; base += 64) {
+      const uint32_t i = base + lane;
+      const bool unv = i < cnt && !key_visited(B[i]);
+      const uint64_t m = ballot(unv);
+      if (m) { p = (int)(base + (uint32_t)__builtin_ctzll(m)); break; }
+    }
+    if (p < 0) break;
+    const uint64_t pk = B[p];
+    wave_sync();
+    if (lane == 0) B[p] = pk | 1ull;
+    const uint32_t u = key_id(pk);
+    const uint4* urow = reinterpret_cast<const uint4*>(a.vecs) + (size_t)u * nchunks;
+
+    // visit: exact distance of u (the one vector fetch per hop)
+    float exact_u = 0.0f, qu_dot = 0.0f, stored;
+    if constexpr (PQ) {
+      qu_dot = visit_exact<false>(qv, urow, nchunks, nullptr);
+      stored = L2 ? (q_sq - 2.0f * qu_dot) + a.norms[u] : -qu_dot;
+    } else {
+      exact_u = visit_exact<L2>(qv, urow, nchunks, xv);
+      stored = L2 ? exact_u : -exact_u;
+    }
+    // frontier_insert_sorted (beam_search_common.cuh:156-185)
+    if (lane == 0 && a.k > 0) {
+      int j = -1;
+      if (fc < a.k) {
+        j = (int)fc;
+        fc += 1;
+      } else if (stored < Fd[a.k - 1]) {
+        j = (int)a.k - 1;
+      }
+      if (j >= 0) {
+        while (j > 0 && Fd[j - 1] > stored) {
+          Fd[j] = Fd[j - 1];
+          Fi[j] = Fi[j - 1];
+          --j;
+        }
+        Fd[j] = stored;
+        Fi[j] = u;
+      }
+    }
+    fc = (uint32_t)__shfl((int)fc, 0, 64);
+    vc += 1;
+    if (vc == a.max_result) break;
+    wave_sync();
+
+    // expand u and estimate its neighbours (no neighbour vector fetches)
+    const uint32_t deg = min((uint32_t)a.counts[u], a.R);
+    uint64_t t = kEmptyKey;
+    if (lane < deg) {
+      const uint32_t v = a.edges[(size_t)u * a.R + lane];
+      if ((int64_t)v < a.n) {
+        const uint32_t e = lane;
+        float est;
+        if constexpr (PQ) {
+          const uint8_t* code = a.codes + (size_t)u * a.M * a.R;
+          float acc = qu_dot;
+          for (uint32_t j = 0; j < a.M; ++j) acc = acc + lut[j * 256 + code[(size_t)j * a.R + e]];
+          est = L2 ? (q_sq - 2.0f * acc) + a.norms[v] : -acc;
+        } else {
+          const uint8_t* row = a.lsh_rows + (size_t)u * a.row_bytes;
+          const uint16_t* x16 = L2 ? reinterpret_cast<const uint16_t*>(xv) : q16;
+          float dot_acc = 0.0f;
+          for (uint32_t r = 0; r < a.K; ++r) {
+            uint32_t coord;
+            bool neg;
+            if (a.pbytes == 1) {
+              const uint32_t w = row[(size_t)e * a.K + r];
+              neg = (w & 0x80u) != 0;
+              coord = w & 0x7Fu;
+            } else {
+              const uint8_t* wp = row + 2 * ((size_t)e * a.K + r);
+              const uint32_t w = wp[0] | ((uint32_t)wp[1] << 8);
+              neg = (w & 0x8000u) != 0;
+              coord = w & 0x7FFFu;
+            }
+            const float cs = neg ? -a.c[r] : a.c[r];
+            const float xc = coord < a.dp ? h2f16(x16[coord]) : 0.0f;  // guards a corrupt row
+            dot_acc = __builtin_fmaf(cs, xc, dot_acc);
+          }
+          const uint8_t* mb = row + (size_t)a.R * a.K * a.pbytes + 2 * (size_t)e;
+          const float mag_sq = bf2f((uint16_t)(mb[0] | ((uint32_t)mb[1] << 8)));
+          const float dot_est = dot_acc * a.inv_norm_denom;
+          const float mag = __fsqrt_rn(mag_sq);
+          est = L2 ? __builtin_fmaf(-(2.0f * mag), dot_est, exact_u + mag_sq)
+                   : -__builtin_fmaf(mag, dot_est, exact_u);
+        }
+        t = make_key(est, v);
+      } else {
+        t = make_key(FLT_MAX, kInv31) | 1ull;  // INVALID, visited (device_kernels.cuh:115-122)
+      }
+    }
+    // merge_sort_tail: sort the tail, merge with the head (head first on ties)
+    t = wave_sort_upto(t, deg);
+    if (lane < deg) T[lane] = t;
+    wave_sync();
+    const uint32_t top = pow2_ceil(cnt);
+    if (lane < deg) {
+      // upper bound: head entries with rank <= rank(t) precede t
+      uint32_t lo = 0;
+      for (uint32_t step = top; step > 0; step >>= 1) {
+        const uint32_t probe = lo + step;
+        if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
+      }
+      NB[lane + lo] = t;
+    }
+    const uint32_t ttop = pow2_ceil(deg);
+    for (uint32_t j = lane; j < cnt; j += 64) {
+      const uint64_t bk = B[j];
+      const uint32_t c = deg ? lds_lower_bound(T, deg, ttop, key_rank(bk)) : 0u;
+      NB[j + c] = bk;
+    }
+    wave_sync();
+    // dedup_results + clip_k: drop entries whose id equals the previous one
+    const uint32_t total = cnt + deg;
+    uint32_t kept = 0;
+    for (uint32_t base = 0; base < total; base += 64) {
+      const uint32_t m = base + lane;
+      bool keep = false;
+      uint64_t cur = 0;
+      if (m < total) {
+        cur = NB[m];
+        const uint32_t prev_id = m == 0 ? kInv31 : key_id(NB[m - 1]);
+        keep = key_id(cur) != prev_id;
+      }
+      const uint64_t km = ballot(keep);
+      const uint32_t pos = kept + mbcnt(km);
+      if (keep && pos < a.bw) B[pos] = cur;
+      kept += (uint32_t)__builtin_popcountll(km);
+    }
+    cnt = min(kept, a.bw);
+    wave_sync();
+  }
+
+  // output: F in order, skipping invalid / deleted, pad (0x7FFFFFFF, FLT_MAX)
+  // (graph_beam_search.cuh:246-266)
+  wave_sync();
+  uint32_t out = 0;
+  for (uint32_t base = 0; base < fc && out < a.k; base += 64) {
+    const uint32_t i = base + lane;
+    bool ok = i < fc;
+    float dist = 0.0f;
+    uint32_t id = 0;
+    if (ok) {
+      dist = Fd[i];
+      id = Fi[i];
+      ok = (int64_t)id < a.n && ((a.deleted[id >> 5] >> (id & 31u)) & 1u) == 0u;
+    }
+    const uint64_t m = ballot(ok);
+    const uint32_t pos = out + mbcnt(m);
+    if (ok && pos < a.k) {
+      a.out_ids[(size_t)qid * a.k + pos] = (int32_t)id;
+      a.out_dists[(size_t)qid * a.k + pos] = dist;
+    }
+    out += (uint32_t)__builtin_popcountll(m);
+  }
+  for (uint32_t i = out + lane; i < a.k; i += 64) {
+    a.out_ids[(size_t)qid * a.k + i] = (int32_t)kInv31;
+    a.out_dists[(size_t)qid * a.k + i] = FLT_MAX;
+  }
+}
+
+// ------------------------------------------------------------ host side --
+
+std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_ranks, bool small_dim,
+                                             const void* vectors, int64_t n, int64_t dim, double alpha,
+                                             int64_t budget, bool on_host, bool prerotate, uint64_t seed,
+                                             hipStream_t stream, BuildStats* stats) {
+  if (n <= 0) throw std::invalid_argument("vectors must contain at least one row");
+  if (n > 0x7FFFFFFF) throw std::invalid_argument("too many vectors for 31-bit ids");
+  auto g = std::make_unique<Graph>();
+  g->allocate(n, (uint32_t)dim, R, metric, on_host);
+  g->k_ranks = k_ranks;
+  g->packed_bytes = small_dim ? 1 : 2;
+  upload_vectors(*g, vectors, n, (uint32_t)dim, stream);
+  g->prerotate = prerotate;
+  g->prerotate_seed = seed;
+  if (prerotate) {
+    // The reference rotates the caller's buffer in place (E.4,
+    // construct.cuh:1104-1107); here the graph's own copy is rotated.
+    g->rotation = device_rotation_fp16((uint32_t)dim, seed);
+    void* tmp = nullptr;
+    hip_check(hipMalloc(&tmp, (size_t)n * g->dp * 2), "alloc rotation output");
+    rotate_rows(g->vecs, n, (uint32_t)dim, g->dp, g->dp, g->rotation, tmp, stream);
+    hip_check(hipMemcpyAsync(g->vecs, tmp, (size_t)n * g->dp * 2, hipMemcpyDeviceToDevice, stream), "copy rotated");
+    hip_check(hipStreamSynchronize(stream), "sync rotation");
+    (void)hipFree(tmp);
+  }
+  const int64_t mbs = reference_max_batch(n, R, budget);
+  build_graph(*g, (float)alpha, mbs, stream, false, stats);
+  g->next_id = (uint64_t)n;
+  return g;
+}
+
+void build_lsh(Graph& g, int64_t n_samples, uint64_t seed) {
+  if (g.n <= 0) throw std::runtime_error("generate_lsh_globals: graph is empty");
+  const uint32_t K = g.k_ranks, P = g.packed_bytes;
+  if (K == 0 || K > 16) throw std::invalid_argument("k_ranks must be in 1..16");
+  if (n_samples <= 0 || n_samples > 0xFFFFFFFFll) throw std::invalid_argument("n_samples must be in 1..2^32-1");
+  if (P == 1 && g.dp > 128) throw std::invalid_argument("dim too large for 7-bit LSH coordinates");
+  hipStream_t s = nullptr;
+  float* contrib = nullptr;
+  uint8_t* valid = nullptr;
+  float* out = nullptr;
+  hip_check(hipMalloc(&contrib, (size_t)std::max<int64_t>(n_samples, 1) * K * 4), "alloc lsh contrib");
+  hip_check(hipMalloc(&valid, (size_t)std::max<int64_t>(n_samples, 1)), "alloc lsh valid");
+  hip_check(hipMalloc(&out, (K + 2) * 4), "alloc lsh globals");
+  auto art = std::make_unique<LshArtifacts>();
+  art->k_ranks = K;
+  art->packed_bytes = P;
+  art->row_bytes = (size_t)g.R * K * P + 2 * (size_t)g.R;
+  try {
+    const size_t plds = (size_t)g.dp * 4 + ((art->row_bytes + 3) & ~(size_t)3);
+    if (plds > 160 * 1024) throw std::invalid_argument("dim too large for the LSH kernels");
+    if (plds > 64 * 1024) {
+      hip_check(hipFuncSetAttribute((const void*)lsh_calib_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)plds), "LDS size");
+      hip_check(hipFuncSetAttribute((const void*)lsh_populate_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)plds), "LDS size");
+    }
+    if (n_samples > 0)
+      hipLaunchKernelGGL(lsh_calib_kernel, dim3((uint32_t)n_samples), dim3(64), g.dp * 4, s, (const uint16_t*)g.vecs,
+                         g.n, g.dp, g.edges, g.counts, g.R, K, seed, contrib, valid);
+    hip_check(hipGetLastError(), "launch lsh_calib_kernel");
+    hipLaunchKernelGGL(lsh_finalize_kernel, dim3(1), dim3(1), 0, s, contrib, valid, n_samples, K, out);
+    hip_check(hipGetLastError(), "launch lsh_finalize_kernel");
+    std::vector<float> h(K + 2);
+    hip_check(hipMemcpy(h.data(), out, (K + 2) * 4, hipMemcpyDeviceToHost), "download lsh globals");
+    art->c_per_rank.assign(h.begin(), h.begin() + K);
+    art->norm_denom = h[K];
+    hip_check(hipMalloc(&art->rows, (size_t)g.n * art->row_bytes), "alloc edge lsh rows");
+    const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
+    hipLaunchKernelGGL(lsh_populate_kernel, dim3(grid), dim3(64), plds, s, (const uint16_t*)g.vecs, g.n, g.dp,
+                       g.edges, g.counts, g.R, K, P, (uint8_t*)art->rows, (uint32_t)art->row_bytes);
+    hip_check(hipGetLastError(), "launch lsh_populate_kernel");
+    hip_check(hipDeviceSynchronize(), "lsh build");
+  } catch (...) {
+    (void)hipFree(contrib);
+    (void)hipFree(valid);
+    (void)hipFree(out);
+    throw;
+  }
+  (void)hipFree(contrib);
+  (void)hipFree(valid);
+  (void)hipFree(out);
+  g.lsh = std::move(art);
+}
+
+static void compute_norms(Graph& g) {
+  if (!g.vector_norms) hip_check(hipMalloc(&g.vector_norms, (size_t)g.n * 4), "alloc vector norms");
+  const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
+  hipLaunchKernelGGL(norms_kernel, dim3(grid), dim3(64), 0, nullptr, (const uint16_t*)g.vecs, g.n, g.dp,
+                     g.vector_norms);
+  hip_check(hipGetLastError(), "launch norms_kernel");
+}
+
+void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed) {
+  if (g.n <= 0) throw std::runtime_error("generate_pq_codebooks: graph is empty");
+  const uint32_t M = g.k_ranks;
+  if (M == 0 || g.dp % M != 0)
+    throw std::runtime_error("generate_pq_codebooks: padded_dim (" + std::to_string(g.dp) +
+                             ") must be divisible by M=" + std::to_string(M));
+  const uint32_t dsub = g.dp / M;
+  if (n_train < 256) n_train = 256;
+  uint16_t* X = nullptr;
+  uint8_t* labels = nullptr;
+  auto art = std::make_unique<PqArtifacts>();
+  art->m = M;
+  art->dsub = dsub;
+  try {
+    hip_check(hipMalloc(&X, (size_t)n_train * g.dp * 2), "alloc pq training rows");
+    hip_check(hipMalloc(&labels, (size_t)n_train * M), "alloc pq labels");
+    hip_check(hipMalloc(&art->centroids, (size_t)M * 256 * dsub * 4), "alloc pq centroids");
+    hipLaunchKernelGGL(pq_sample_kernel, dim3((uint32_t)n_train), dim3(128), 0, nullptr, (const uint16_t*)g.vecs, g.n,
+                       g.dp, g.edges, g.counts, g.R, n_train, seed, X);
+    const uint64_t init_seed = seed ^ 0xA5A5A5A5ull;
+    hipLaunchKernelGGL(pq_init_kernel, dim3(M * 256), dim3(64), 0, nullptr, X, n_train, g.dp, M, dsub, init_seed,
+                       art->centroids);
+    const size_t lds_want = (size_t)256 * dsub * 4;
+    const bool stage = lds_want <= 64 * 1024;
+    const size_t lds = stage ? lds_want : 0;
+    const int64_t upd = (int64_t)M * 256 * dsub;
+    for (int64_t it = 0; it < iters; ++it) {
+      hipLaunchKernelGGL(pq_assign_kernel, dim3((uint32_t)((n_train + 255) / 256), M), dim3(256), lds, nullptr, X,
+                         n_train, g.dp, M, dsub, art->centroids, labels, stage);
+      hipLaunchKernelGGL(pq_update_kernel, dim3((uint32_t)((upd + 255) / 256)), dim3(256), 0, nullptr, X, n_train,
+                         g.dp, M, dsub, labels, init_seed, (uint32_t)it, art->centroids);
+    }
+    hip_check(hipGetLastError(), "launch pq training");
+    hip_check(hipMalloc(&art->codes, (size_t)g.n * M * g.R), "alloc pq codes");
+    const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
+    const size_t elds = (size_t)g.dp * 4 + (size_t)M * g.R;
+    if (elds > 160 * 1024) throw std::invalid_argument("dim too large for the PQ encoder");
+    if (elds > 64 * 1024)
+      hip_check(hipFuncSetAttribute((const void*)pq_encode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)elds), "LDS size");
+    hipLaunchKernelGGL(pq_encode_kernel, dim3(grid), dim3(64), elds, nullptr, (const uint16_t*)g.vecs, g.n, g.dp,
+                       g.edges, g.counts, g.R, M, dsub, art->centroids, art->codes);
+    hip_check(hipGetLastError(), "launch pq_encode_kernel");
+    compute_norms(g);
+    hip_check(hipDeviceSynchronize(), "pq build");
+  } catch (...) {
+    (void)hipFree(X);
+    (void)hipFree(labels);
+    throw;
+  }
+  (void)hipFree(X);
+  (void)hipFree(labels);
+  g.pq = std::move(art);
+}
+
+void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+                        float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream) {
+  if (use_pq && !g.pq) throw std::runtime_error("graph has no PQ artifacts built — call build_pq() first");
+  if (!use_pq && !g.lsh) throw std::runtime_error("graph has no LSH artifacts built — call build_lsh() first");
+  if (dim != (int64_t)g.dim)
+    throw std::invalid_argument("query dim (" + std::to_string(dim) + ") != graph dim (" + std::to_string(g.dim) + ")");
+  if (nq < 0 || k < 0 || bw <= 0 || limit < 0) throw std::invalid_argument("negative size argument");
+  if (nq == 0 || k == 0) return;
+  if (bw + 64 >= 2048)
+    throw std::invalid_argument("beam_width " + std::to_string(bw) + " is too large (beam_width + 64 must be < 2048)");
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  // padded (and, if the graph was prerotated, rotated) query rows
+  void* qrows = nullptr;
+  hip_check(hipMallocAsync(&qrows, (size_t)nq * g.dp * 2, stream), "alloc query rows");
+  hip_check(hipMemsetAsync(qrows, 0, (size_t)nq * g.dp * 2, stream), "clear query rows");
+  hip_check(hipMemcpy2DAsync(qrows, (size_t)g.dp * 2, queries, (size_t)dim * 2, (size_t)dim * 2, (size_t)nq,
+                             hipMemcpyDefault, stream),
+            "copy queries");
+  void* rot = nullptr;
+  if (g.prerotate) {
+    hip_check(hipMallocAsync(&rot, (size_t)nq * g.dp * 2, stream), "alloc rotated queries");
+    rotate_rows(qrows, nq, g.dim, g.dp, g.dp, g.rotation, rot, stream);
+  }
+  DirArgs a{};
+  a.vecs = (const uint16_t*)g.vecs;
+  a.n = g.n;
+  a.dp = g.dp;
+  a.R = g.R;
+  a.edges = g.edges;
+  a.counts = g.counts;
+  a.deleted = g.deleted;
+  a.queries = (const uint16_t*)(rot ? rot : qrows);
+  a.medoid = g.medoid;
+  a.k = (uint32_t)k;
+  a.bw = (uint32_t)bw;
+  a.limit = (uint32_t)limit;
+  a.max_result = 2048;
+  a.out_ids = out_ids;
+  a.out_dists = out_dists;
+  if ((int64_t)g.medoid >= g.n) throw std::runtime_error("graph medoid is out of range");
+  size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
+  if (use_pq) {
+    a.M = g.pq->m;
+    a.dsub = g.pq->dsub;
+    a.centroids = g.pq->centroids;
+    a.codes = g.pq->codes;
+    a.norms = g.vector_norms;
+    lds += (size_t)a.M * 256 * 4;
+    if (g.metric == kL2 && !g.vector_norms) throw std::runtime_error("graph has no vector norms");
+  } else {
+    a.K = g.lsh->k_ranks;
+    a.pbytes = g.lsh->packed_bytes;
+    a.lsh_rows = (const uint8_t*)g.lsh->rows;
+    a.row_bytes = (uint32_t)g.lsh->row_bytes;
+    for (uint32_t r = 0; r < a.K; ++r) a.c[r] = g.lsh->c_per_rank[r];
+    a.inv_norm_denom = 1.0f / g.lsh->norm_denom;
+  }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (print) {
+    hip_check(hipEventCreate(&e0), "event");
+    hip_check(hipEventCreate(&e1), "event");
+    hip_check(hipEventRecord(e0, stream), "event record");
+  }
+  const void* kern = nullptr;
+  if (use_pq) kern = g.metric == kL2 ? (const void*)directional_kernel<kL2, true> : (const void*)directional_kernel<kIP, true>;
+  else kern = g.metric == kL2 ? (const void*)directional_kernel<kL2, false> : (const void*)directional_kernel<kIP, false>;
+  if (lds > 160 * 1024) throw std::invalid_argument("beam_width, k and dim need more than 160 KB of LDS");
+  if (lds > 64 * 1024)
+    hip_check(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS size");
+  const dim3 grid((uint32_t)nq);
+  if (use_pq) {
+    if (g.metric == kL2) hipLaunchKernelGGL((directional_kernel<kL2, true>), grid, dim3(64), lds, stream, a);
+    else hipLaunchKernelGGL((directional_kernel<kIP, true>), grid, dim3(64), lds, stream, a);
+  } else {
+    if (g.metric == kL2) hipLaunchKernelGGL((directional_kernel<kL2, false>), grid, dim3(64), lds, stream, a);
+    else hipLaunchKernelGGL((directional_kernel<kIP, false>), grid, dim3(64), lds, stream, a);
+  }
+  hip_check(hipGetLastError(), "launch directional_kernel");
+  if (print) {
+    hip_check(hipEventRecord(e1, stream), "event record");
+    hip_check(hipEventSynchronize(e1), "event sync");
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    std::printf("[%s] duration=%gms, throughput=%g\n", use_pq ? "pq_search" : "directional_search", ms,
+                nq * 1000.0 / ms);
+    std::fflush(stdout);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  if (rot) (void)hipFreeAsync(rot, stream);
+  (void)hipFreeAsync(qrows, stream);
+}
+
+// ---------------------------------------------------------------- files --
+// Trailer after the base section (graph.cuh:1790-1937): u32 magic, u32
+// version, u8 flags (1 LSH, 2 PQ, 4 norms); LSH: u8 K, u8 sizeof(packed_t),
+// K floats c_per_rank + float norm_denom, N rows; PQ: u32 M, u32 256,
+// u32 dsub, centroids, N code rows; norms: N floats. Read back at the end of
+// the base section (total_file_size), where the saver puts it; the
+// reference loader looks elsewhere (graph.cuh:1959-1964) and never finds it.
+
+void save_directional_file(const Graph& g, const std::string& path) {
+  save_graph_file(g, path);
+  if (g.n == 0) return;
+  const bool has_lsh = (bool)g.lsh, has_pq = (bool)g.pq, has_norms = g.vector_norms != nullptr;
+  if (!has_lsh && !has_pq && !has_norms) return;
+  std::ofstream f(path, std::ios::binary | std::ios::app);
+  if (!f.is_open()) throw std::runtime_error("save_directional_graph_to_file: cannot reopen " + path);
+  const uint8_t flags = (has_lsh ? 1u : 0u) | (has_pq ? 2u : 0u) | (has_norms ? 4u : 0u);
+  f.write((const char*)&kTrailerMagic, 4);
+  f.write((const char*)&kTrailerVersion, 4);
+  f.write((const char*)&flags, 1);
+  hip_check(hipDeviceSynchronize(), "sync before save");
+  if (has_lsh) {
+    const uint8_t K = (uint8_t)g.lsh->k_ranks, P = (uint8_t)g.lsh->packed_bytes;
+    f.write((const char*)&K, 1);
+    f.write((const char*)&P, 1);
+    f.write((const char*)g.lsh->c_per_rank.data(), (std::streamsize)K * 4);
+    f.write((const char*)&g.lsh->norm_denom, 4);
+    std::vector<uint8_t> h((size_t)g.n * g.lsh->row_bytes);
+    hip_check(hipMemcpy(h.data(), g.lsh->rows, h.size(), hipMemcpyDeviceToHost), "download lsh rows");
+    f.write((const char*)h.data(), (std::streamsize)h.size());
+  }
+  if (has_pq) {
+    const uint32_t M = g.pq->m, K = 256, dsub = g.pq->dsub;
+    f.write((const char*)&M, 4);
+    f.write((const char*)&K, 4);
+    f.write((const char*)&dsub, 4);
+    std::vector<float> c((size_t)M * K * dsub);
+    hip_check(hipMemcpy(c.data(), g.pq->centroids, c.size() * 4, hipMemcpyDeviceToHost), "download centroids");
+    f.write((const char*)c.data(), (std::streamsize)c.size() * 4);
+    std::vector<uint8_t> codes((size_t)g.n * M * g.R);
+    hip_check(hipMemcpy(codes.data(), g.pq->codes, codes.size(), hipMemcpyDeviceToHost), "download codes");
+    f.write((const char*)codes.data(), (std::streamsize)codes.size());
+  }
+  if (has_norms) {
+    std::vector<float> nrm((size_t)g.n);
+    hip_check(hipMemcpy(nrm.data(), g.vector_norms, nrm.size() * 4, hipMemcpyDeviceToHost), "download norms");
+    f.write((const char*)nrm.data(), (std::streamsize)nrm.size() * 4);
+  }
+  if (!f.good()) throw std::runtime_error("short write while saving " + path);
+}
+
+std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
+                                             uint32_t k_ranks, bool small_dim, bool on_host, bool prerotate,
+                                             uint64_t seed) {
+  uint64_t off = 0;
+  auto g = load_graph_file(path, dim, R, metric, on_host, &off);
+  g->k_ranks = k_ranks;
+  g->packed_bytes = small_dim ? 1 : 2;
+  g->prerotate = prerotate;
+  g->prerotate_seed = seed;
+  if (prerotate) g->rotation = device_rotation_fp16(dim, seed);
+  if (g->n == 0) return g;
+  std::ifstream f(path, std::ios::binary | std::ios::ate);
+  if (!f.is_open()) throw std::runtime_error("load_directional_graph_from_file: cannot reopen " + path);
+  const uint64_t size = (uint64_t)f.tellg();
+  if (size < off + 9) return g;
+  f.seekg((std::streamoff)off);
+  uint32_t magic = 0, version = 0;
+  uint8_t flags = 0;
+  f.read((char*)&magic, 4);
+  f.read((char*)&version, 4);
+  f.read((char*)&flags, 1);
+  if (magic != kTrailerMagic || version != kTrailerVersion) return g;
+  if (flags & 1u) {
+    uint8_t K = 0, P = 0;
+    f.read((char*)&K, 1);
+    f.read((char*)&P, 1);
+    if (K != k_ranks || P != g->packed_bytes)
+      throw std::runtime_error("load_directional_graph_from_file: LSH trailer k_ranks/packed_t mismatch — file was "
+                               "written with a different graph_cfg");
+    auto art = std::make_unique<LshArtifacts>();
+    art->k_ranks = K;
+    art->packed_bytes = P;
+    art->row_bytes = (size_t)R * K * P + 2 * (size_t)R;
+    art->c_per_rank.resize(K);
+    f.read((char*)art->c_per_rank.data(), (std::streamsize)K * 4);
+    f.read((char*)&art->norm_denom, 4);
+    std::vector<uint8_t> h((size_t)g->n * art->row_bytes);
+    f.read((char*)h.data(), (std::streamsize)h.size());
+    if ((size_t)f.gcount() != h.size()) throw std::runtime_error("truncated LSH trailer in " + path);
+    hip_check(hipMalloc(&art->rows, h.size()), "alloc lsh rows");
+    hip_check(hipMemcpy(art->rows, h.data(), h.size(), hipMemcpyHostToDevice), "upload lsh rows");
+    g->lsh = std::move(art);
+  }
+  if (flags & 2u) {
+    uint32_t M = 0, K = 0, dsub = 0;
+    f.read((char*)&M, 4);
+    f.read((char*)&K, 4);
+    f.read((char*)&dsub, 4);
+    if (M != k_ranks || K != 256)
+      throw std::runtime_error("load_directional_graph_from_file: PQ trailer M/K mismatch — file was written with a "
+                               "different graph_cfg");
+    auto art = std::make_unique<PqArtifacts>();
+    art->m = M;
+    art->dsub = dsub;
+    std::vector<float> c((size_t)M * K * dsub);
+    f.read((char*)c.data(), (std::streamsize)c.size() * 4);
+    std::vector<uint8_t> codes((size_t)g->n * M * R);
+    f.read((char*)codes.data(), (std::streamsize)codes.size());
+    if ((size_t)f.gcount() != codes.size()) throw std::runtime_error("truncated PQ trailer in " + path);
+    hip_check(hipMalloc(&art->centroids, c.size() * 4), "alloc centroids");
+    hip_check(hipMemcpy(art->centroids, c.data(), c.size() * 4, hipMemcpyHostToDevice), "upload centroids");
+    hip_check(hipMalloc(&art->codes, codes.size()), "alloc codes");
+    hip_check(hipMemcpy(art->codes, codes.data(), codes.size(), hipMemcpyHostToDevice), "upload codes");
+    g->pq = std::move(art);
+  }
+  if (flags & 4u) {
+    std::vector<float> nrm((size_t)g->n);
+    f.read((char*)nrm.data(), (std::streamsize)nrm.size() * 4);
+    if ((size_t)f.gcount() != nrm.size() * 4) throw std::runtime_error("truncated norms in " + path);
+    hip_check(hipMalloc(&g->vector_norms, nrm.size() * 4), "alloc norms");
+    hip_check(hipMemcpy(g->vector_norms, nrm.data(), nrm.size() * 4, hipMemcpyHostToDevice), "upload norms");
+  }
+  return g;
+}
+
+// ------------------------------------------------------ rotation matrix --
+// Host restatement of set_rotation_matrix (rotation.cuh:28-111).
+
+}  // namespace jasper_amd
+
+#include <random>
+
+extern "C" int64_t jasperx_rotation_matrix(int64_t dim, int64_t seed, float* out);
+
+namespace jasper_amd {
+
+static std::vector<float> rotation_matrix(uint32_t dd, uint64_t seed) {
+  const int d = (int)dd;
+  std::mt19937_64 rng(seed);
+  std::normal_distribution<float> N(0, 1);
+  std::vector<float> A((size_t)d * d);
+  for (int j = 0; j < d; j++)
+    for (int i = 0; i < d; i++) A[(size_t)i + (size_t)j * d] = N(rng);
+  std::vector<float> Q((size_t)d * d, 0.0f);
+  for (int i = 0; i < d; i++) Q[(size_t)i + (size_t)i * d] = 1.0f;
+  std::vector<float> v((size_t)d);
+  for (int k = 0; k < d; k++) {
+    float norm_sq = 0;
+    for (int i = k; i < d; i++) {
+      v[i] = A[(size_t)i + (size_t)k * d];
+      norm_sq += v[i] * v[i];
+    }
+    const float norm = std::sqrt(norm_sq);
+    if (norm < 1e-12f) continue;
+    const float sign = (A[(size_t)k + (size_t)k * d] >= 0) ? 1.0f : -1.0f;
+    v[k] += sign * norm;
+    float v_norm_sq = 0;
+    for (int i = k; i < d; i++) v_norm_sq += v[i] * v[i];
+    const float tau = 2.0f / v_norm_sq;
+    for (int j = k; j < d; j++) {
+      float dot = 0;
+      for (int i = k; i < d; i++) dot += v[i] * A[(size_t)i + (size_t)j * d];
+      for (int i = k; i < d; i++) A[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
+    }
+    for (int j = 0; j < d; j++) {
+      float dot = 0;
+      for (int i = k; i < d; i++) dot += v[i] * Q[(size_t)i + (size_t)j * d];
+      for (int i = k; i < d; i++) Q[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
+    }
+  }
+  for (int i = 0; i < d; i++)
+    if (A[(size_t)i + (size_t)i * d] < 0.0f)
+      for (int j = 0; j < d; j++) Q[(size_t)j + (size_t)i * d] *= -1.0f;
+  return Q;
 }
 
 }  // namespace jasper_amd
+
+// The prerotation matrix (column-major fp32, before the fp16 cast), for
+// callers that rotate on their own and for tests.
+extern "C" int64_t jasperx_rotation_matrix(int64_t dim, int64_t seed, float* out) {
+  if (dim <= 0 || dim > 65536 || out == nullptr) return -1;
+  const std::vector<float> m = jasper_amd::rotation_matrix((uint32_t)dim, (uint64_t)seed);
+  std::memcpy(out, m.data(), m.size() * sizeof(float));
+  return 0;
+}

@@ -78,6 +78,40 @@ def lib():
         _lib.jo_gaussian_matrix.argtypes = [i32, u64, P]
         _lib.jo_rotation_matrix.restype = None
         _lib.jo_rotation_matrix.argtypes = [i32, u64, P, P]
+        u16, f64 = ctypes.c_uint16, ctypes.c_double
+        _lib.jo_d2h.restype = u16
+        _lib.jo_d2h.argtypes = [f64]
+        _lib.jo_hsub.restype = u16
+        _lib.jo_hsub.argtypes = [u16, u16]
+        _lib.jo_hmul.restype = u16
+        _lib.jo_hmul.argtypes = [u16, u16]
+        _lib.jo_visit_exact.restype = f32
+        _lib.jo_visit_exact.argtypes = [P, P, i32, i32, P]
+        _lib.jo_vector_norms.restype = None
+        _lib.jo_vector_norms.argtypes = [P, i64, i32, P, i32]
+        _lib.jo_directional_search.restype = i32
+        _lib.jo_directional_search.argtypes = [i32, P, i64, i32, P, P, i32, P, i32,
+                                               i32, i32, P, f32, P,
+                                               i32, i32, P, P, P,
+                                               P, i64, ctypes.c_uint32, i32, i32, i32, i32, P, P, P, P, P, P, i32]
+        _lib.jo_populate_lsh.restype = None
+        _lib.jo_populate_lsh.argtypes = [P, i64, i32, P, P, i32, i32, i32, P, i32]
+        _lib.jo_lsh_globals.restype = i64
+        _lib.jo_lsh_globals.argtypes = [P, i64, i32, P, P, i32, i32, i64, u64, P, P]
+        _lib.jo_pq_train.restype = None
+        _lib.jo_pq_train.argtypes = [P, i64, i32, P, P, i32, i32, i64, i32, u64, P, P, i32]
+        _lib.jo_pq_hash.restype = u64
+        _lib.jo_pq_hash.argtypes = [u64, u64]
+        _lib.jo_splitmix.restype = u64
+        _lib.jo_splitmix.argtypes = [u64]
+        _lib.jo_sample_edge.restype = i32
+        _lib.jo_sample_edge.argtypes = [P, P, i64, i32, u64, u64, P, P]
+        _lib.jo_frontier_insert_seq.restype = None
+        _lib.jo_frontier_insert_seq.argtypes = [P, P, i32, i32, P, P, P]
+        _lib.jo_pq_encode.restype = None
+        _lib.jo_pq_encode.argtypes = [P, i64, i32, P, P, i32, i32, P, P, i32]
+        _lib.jo_rotate_rows.restype = None
+        _lib.jo_rotate_rows.argtypes = [P, i64, i32, i32, P, P, i32]
     return _lib
 
 
@@ -254,6 +288,176 @@ def gaussian_matrix(d: int, seed: int = 42) -> np.ndarray:
     a = np.empty(d * d, dtype=np.float32)
     lib().jo_gaussian_matrix(d, seed, _ptr(a))
     return a
+
+
+# ------------------------------------------------------------- directional --
+# Restatements of graph_beam_search_kernel (Appendix B) and its estimator
+# artifacts; see directional_oracle.cpp.
+
+def d2h(x: float) -> int:
+    return int(lib().jo_d2h(float(x)))
+
+
+def hsub(a: int, b: int) -> int:
+    return int(lib().jo_hsub(a, b))
+
+
+def hmul(a: int, b: int) -> int:
+    return int(lib().jo_hmul(a, b))
+
+
+def visit_exact(q16: np.ndarray, u16: np.ndarray, l2: bool = True):
+    """compute_qu_diff_and_exact (beam_search_common.cuh:87-154): returns
+    (exact, fp16 bits of q - u) for L2, (sum of fp16 products, None) for IP."""
+    q16 = np.ascontiguousarray(q16, dtype=np.uint16)
+    u16 = np.ascontiguousarray(u16, dtype=np.uint16)
+    diff = np.zeros_like(q16) if l2 else None
+    v = lib().jo_visit_exact(_ptr(q16), _ptr(u16), q16.shape[0], 1 if l2 else 0, _ptr(diff))
+    return float(v), diff
+
+
+def vector_norms(vecs16: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    out = np.empty(vecs16.shape[0], dtype=np.float32)
+    lib().jo_vector_norms(_ptr(vecs16), vecs16.shape[0], vecs16.shape[1], _ptr(out), nthreads)
+    return out
+
+
+class LshArtifacts:
+    def __init__(self, K, pbytes, c_per_rank, norm_denom, rows):
+        self.K, self.pbytes = int(K), int(pbytes)
+        self.c_per_rank = np.ascontiguousarray(c_per_rank, dtype=np.float32)
+        self.norm_denom = float(np.float32(norm_denom))
+        self.rows = np.ascontiguousarray(rows, dtype=np.uint8)
+
+
+class PqArtifacts:
+    def __init__(self, M, dsub, centroids, codes, norms):
+        self.M, self.dsub = int(M), int(dsub)
+        self.centroids = np.ascontiguousarray(centroids, dtype=np.float32)
+        self.codes = np.ascontiguousarray(codes, dtype=np.uint8)
+        self.norms = np.ascontiguousarray(norms, dtype=np.float32)
+
+
+def lsh_row_bytes(R: int, K: int, pbytes: int) -> int:
+    """sizeof(edge_lsh_list) (lsh/edge_lsh.cuh:9-27): packed[R*K] + bf16 mag[R]."""
+    return R * K * pbytes + 2 * R
+
+
+def populate_lsh(g: OracleGraph, K: int, pbytes: int, nthreads: int = 0) -> np.ndarray:
+    rows = np.zeros((g.n, lsh_row_bytes(g.R, K, pbytes)), dtype=np.uint8)
+    lib().jo_populate_lsh(_ptr(g.vecs16), g.n, g.dp, _ptr(g.edges), _ptr(g.counts), g.R, K, pbytes,
+                          _ptr(rows), nthreads)
+    return rows
+
+
+def lsh_globals(g: OracleGraph, K: int, n_samples: int = 32768, seed: int = 42):
+    c = np.zeros(K, dtype=np.float32)
+    nd = ctypes.c_float(0.0)
+    nv = lib().jo_lsh_globals(_ptr(g.vecs16), g.n, g.dp, _ptr(g.edges), _ptr(g.counts), g.R, K, n_samples,
+                              seed, _ptr(c), ctypes.byref(nd))
+    return c, float(nd.value), int(nv)
+
+
+def build_lsh(g: OracleGraph, K: int, pbytes: int, n_samples: int = 32768, seed: int = 42,
+              nthreads: int = 0) -> LshArtifacts:
+    c, nd, _ = lsh_globals(g, K, n_samples, seed)
+    return LshArtifacts(K, pbytes, c, nd, populate_lsh(g, K, pbytes, nthreads))
+
+
+def pq_train(g: OracleGraph, M: int, n_train: int = 40000, iters: int = 12, seed: int = 123,
+             nthreads: int = 0):
+    """Codebook training (graph.cuh:1206-1273); returns (centroids
+    [M*256*dsub], training residual rows [max(n_train, 256), dp] fp16 bits)."""
+    dsub = g.dp // M
+    nt = max(n_train, 256)
+    cent = np.zeros(M * 256 * dsub, dtype=np.float32)
+    X = np.zeros((nt, g.dp), dtype=np.uint16)
+    lib().jo_pq_train(_ptr(g.vecs16), g.n, g.dp, _ptr(g.edges), _ptr(g.counts), g.R, M, n_train, iters, seed,
+                      _ptr(cent), _ptr(X), nthreads)
+    return cent, X
+
+
+def pq_encode(g: OracleGraph, M: int, cent: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    codes = np.zeros((g.n, M * g.R), dtype=np.uint8)
+    lib().jo_pq_encode(_ptr(g.vecs16), g.n, g.dp, _ptr(g.edges), _ptr(g.counts), g.R, M,
+                       _ptr(np.ascontiguousarray(cent, dtype=np.float32)), _ptr(codes), nthreads)
+    return codes
+
+
+def pq_hash(x: int, seed: int) -> int:
+    return int(lib().jo_pq_hash(x, seed))
+
+
+def splitmix(x: int) -> int:
+    return int(lib().jo_splitmix(x))
+
+
+def sample_edge(g: OracleGraph, seed: int, s: int):
+    u = ctypes.c_uint32(0)
+    nb = ctypes.c_uint32(0)
+    ok = lib().jo_sample_edge(_ptr(g.edges), _ptr(g.counts), g.n, g.R, seed, s, ctypes.byref(u), ctypes.byref(nb))
+    return (int(u.value), int(nb.value)) if ok else None
+
+
+def frontier_insert_seq(dists, ids, k: int):
+    """frontier_insert_sorted (beam_search_common.cuh:156-185) applied to a
+    sequence of (id, distance) visits; returns the frontier."""
+    d = np.ascontiguousarray(dists, dtype=np.float32)
+    i = np.ascontiguousarray(ids, dtype=np.uint32)
+    od = np.zeros(max(k, 1), dtype=np.float32)
+    oi = np.zeros(max(k, 1), dtype=np.uint32)
+    cnt = ctypes.c_int(0)
+    lib().jo_frontier_insert_seq(_ptr(d), _ptr(i), len(d), k, _ptr(od), _ptr(oi), ctypes.byref(cnt))
+    return oi[:cnt.value].copy(), od[:cnt.value].copy()
+
+
+def build_pq(g: OracleGraph, M: int, n_train: int = 40000, iters: int = 12, seed: int = 123,
+             nthreads: int = 0) -> PqArtifacts:
+    dsub = g.dp // M
+    cent, _ = pq_train(g, M, n_train, iters, seed, nthreads)
+    codes = np.zeros((g.n, M * g.R), dtype=np.uint8)
+    lib().jo_pq_encode(_ptr(g.vecs16), g.n, g.dp, _ptr(g.edges), _ptr(g.counts), g.R, M, _ptr(cent),
+                       _ptr(codes), nthreads)
+    return PqArtifacts(M, dsub, cent, codes, vector_norms(g.vecs16, nthreads))
+
+
+def directional_search(g: OracleGraph, queries, lsh: LshArtifacts | None = None, pq: PqArtifacts | None = None,
+                       k: int = 10, beam_width: int = 64, limit: int | None = None, max_result: int = 2048,
+                       get_visited: bool = False, nthreads: int = 0):
+    """graph_beam_search_kernel (graph_beam_search.cuh:55-270) with the LSH or
+    PQ estimator; returns (ids, dists[, visited ids, visited dists, counts])."""
+    assert (lsh is None) != (pq is None)
+    q16 = queries if (isinstance(queries, np.ndarray) and queries.dtype == np.uint16) else as_padded_f16(queries)
+    nq = q16.shape[0]
+    if limit is None:
+        limit = 2 * beam_width
+    ids = np.empty((nq, k), dtype=np.int32)
+    d = np.empty((nq, k), dtype=np.float32)
+    vi = vd = vc = None
+    if get_visited:
+        vi = np.zeros((nq, max_result), dtype=np.uint32)
+        vd = np.zeros((nq, max_result), dtype=np.float32)
+        vc = np.zeros(nq, dtype=np.uint32)
+    L = lsh or LshArtifacts(0, 1, np.zeros(1, np.float32), 1.0, np.zeros(1, np.uint8))
+    Q = pq or PqArtifacts(0, 0, np.zeros(1, np.float32), np.zeros(1, np.uint8), np.zeros(1, np.float32))
+    lib().jo_directional_search(0 if lsh is not None else 1, _ptr(g.vecs16), g.n, g.dp, _ptr(g.edges),
+                                _ptr(g.counts), g.R, _ptr(g.deleted_bits), metric_code(g.distance),
+                                L.K, L.pbytes, _ptr(L.c_per_rank), ctypes.c_float(L.norm_denom), _ptr(L.rows),
+                                Q.M, Q.dsub, _ptr(Q.centroids), _ptr(Q.codes), _ptr(Q.norms),
+                                _ptr(q16), nq, g.medoid, k, beam_width, limit, max_result, _ptr(ids), _ptr(d),
+                                _ptr(vi), _ptr(vd), _ptr(vc), None, nthreads)
+    out = (ids, d)
+    if get_visited:
+        out += (vi, vd, vc)
+    return out
+
+
+def rotate_rows(vecs16: np.ndarray, dim: int, P16: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """x' = P^T x per row, P column-major fp16 [dim*dim], fp32 accumulation."""
+    out = np.zeros_like(vecs16)
+    lib().jo_rotate_rows(_ptr(vecs16), vecs16.shape[0], dim, vecs16.shape[1],
+                         _ptr(np.ascontiguousarray(P16, dtype=np.uint16)), _ptr(out), nthreads)
+    return out
 
 
 # ------------------------------------------------------------- file format --

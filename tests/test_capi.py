@@ -81,3 +81,19 @@ def test_load_missing_file_raises():
     import jasper_amd
     with pytest.raises(jasper_amd.JasperError, match="failed to open"):
         jasper_amd.Graph.load("/nonexistent/graph.bin", dim=128, n_neighbors=32)
+
+
+@pytest.mark.parametrize("dim", [1, 8, 96, 128, 200])
+def test_rotation_matrix_matches_oracle(lib, oracle_lib, dim):
+    """The library's prerotation matrix (host code, no GPU) is bit-identical
+    to the oracle's restatement of set_rotation_matrix."""
+    import numpy as np
+    import oracle
+    fn = lib.jasperx_rotation_matrix
+    fn.restype = ctypes.c_int64
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    for seed in (42, 7):
+        out = np.zeros(dim * dim, dtype=np.float32)
+        assert fn(dim, seed, out.ctypes.data_as(ctypes.c_void_p)) == 0
+        m, _ = oracle.rotation_matrix(dim, seed)
+        assert np.array_equal(out.view(np.uint32), np.asarray(m, dtype=np.float32).view(np.uint32))

@@ -1,0 +1,146 @@
+"""GPU parity of the directional path against the oracle.
+
+Each case builds a directional graph on the GPU (Vamana build, optional
+prerotation, LSH and/or PQ artifacts), saves it in the reference format,
+reads the base section back with the oracle's loader, and checks:
+  * prerotated rows equal the oracle's rotation of the input (bit-exact);
+  * the graph equals the oracle's build of the same rows;
+  * LSH calibration constants and per-edge rows are bit-identical to the
+    oracle's, and so are PQ centroids, codes and vector norms;
+  * directional_search / pq_search ids and distances are bit-identical to
+    the oracle's traversal with the same artifacts;
+  * a save -> load round trip (trailer included) searches identically.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import compare_search, gaussian, integer_clustered, unit
+
+pytestmark = pytest.mark.gpu
+
+
+def _rotated_rows(x, dim, seed):
+    m, _ = oracle.rotation_matrix(dim, seed)
+    P16 = m.astype(np.float16).view(np.uint16)
+    return oracle.rotate_rows(oracle.as_padded_f16(x), dim, P16)
+
+
+def _search(gg, fn, q, k, bw, limit=None):
+    qt = torch.from_numpy(np.ascontiguousarray(q.astype(np.float16))).cuda()
+    ids, d = getattr(gg, fn)(qt, k=k, beam_width=bw, limit=limit)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), d.cpu().numpy()
+
+
+def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, bws=(16, 64),
+          lsh_samples=4000, pq_train=3000, pq_iters=4):
+    n, dim = x.shape
+    xt = torch.from_numpy(x.astype(np.float16)).cuda()
+    gg = jasper.Graph.build(xt, n_neighbors=R, distance=distance, build_lsh=lsh, build_pq=pq, k_ranks=k_ranks,
+                            prerotate=prerotate, lsh_samples=lsh_samples, lsh_seed=7, pq_train=pq_train,
+                            pq_kmeans_iter=pq_iters, pq_seed=11)
+    path = tmp_path / "dir.bin"
+    gg.save(str(path))
+    g = oracle.load_graph(path, dim, R, distance)
+
+    rows = _rotated_rows(x, dim, 42) if prerotate else oracle.as_padded_f16(x)
+    assert np.array_equal(gg.export_vectors(), rows), "stored rows differ"
+    assert np.array_equal(g.vecs16, rows)
+    ref = oracle.build(rows.view(np.float16)[:, :dim].astype(np.float32), R=R, distance=distance, alpha=1.2)
+    assert g.medoid == ref.medoid
+    assert np.array_equal(g.counts, ref.counts)
+    for i in range(n):
+        c = int(ref.counts[i])
+        assert np.array_equal(g.edges[i, :c], ref.edges[i, :c]), f"vertex {i}"
+
+    q_rows = _rotated_rows(q, dim, 42) if prerotate else oracle.as_padded_f16(q)
+    pbytes = 1 if dim <= 128 else 2
+    out = {}
+    if lsh:
+        c, nd, lrows = gg.export_lsh()
+        rc, rnd, nv = oracle.lsh_globals(g, k_ranks, n_samples=lsh_samples, seed=7)
+        assert nv > 0
+        assert np.array_equal(c.view(np.uint32), rc.view(np.uint32)), (c, rc)
+        assert np.float32(nd).view(np.uint32) == np.float32(rnd).view(np.uint32)
+        want_rows = oracle.populate_lsh(g, k_ranks, pbytes)
+        assert np.array_equal(lrows, want_rows), "LSH rows differ"
+        art = oracle.LshArtifacts(k_ranks, pbytes, c, nd, lrows)
+        for bw in bws:
+            ids, d = _search(gg, "directional_search", q, 10, bw)
+            rid, rd = oracle.directional_search(g, q_rows, lsh=art, k=10, beam_width=bw)
+            msg = compare_search(ids, d, rid, rd)
+            assert msg is None, f"lsh bw={bw}: {msg}"
+            out[("lsh", bw)] = (ids, d)
+    if pq:
+        cent, codes, norms = gg.export_pq()
+        rcent, _ = oracle.pq_train(g, k_ranks, n_train=pq_train, iters=pq_iters, seed=11)
+        assert np.array_equal(cent.view(np.uint32), rcent.view(np.uint32)), "PQ centroids differ"
+        rcodes = oracle.pq_encode(g, k_ranks, rcent)
+        assert np.array_equal(codes, rcodes), "PQ codes differ"
+        rnorms = oracle.vector_norms(g.vecs16)
+        assert np.array_equal(norms.view(np.uint32), rnorms.view(np.uint32)), "vector norms differ"
+        art = oracle.PqArtifacts(k_ranks, g.dp // k_ranks, cent, codes, norms)
+        for bw in bws:
+            ids, d = _search(gg, "pq_search", q, 10, bw)
+            rid, rd = oracle.directional_search(g, q_rows, pq=art, k=10, beam_width=bw)
+            msg = compare_search(ids, d, rid, rd)
+            assert msg is None, f"pq bw={bw}: {msg}"
+            out[("pq", bw)] = (ids, d)
+
+    # save -> load round trip keeps the artifacts and the results
+    g2 = jasper.Graph.load(str(path), dim=dim, n_neighbors=R, distance=distance, k_ranks=k_ranks,
+                           prerotate=prerotate)
+    for (kind, bw), (ids, d) in out.items():
+        ids2, d2 = _search(g2, "directional_search" if kind == "lsh" else "pq_search", q, 10, bw)
+        msg = compare_search(ids2, d2, ids, d)
+        assert msg is None, f"after load, {kind} bw={bw}: {msg}"
+    g2.free()
+    gg.free()
+
+
+def test_lsh_pq_l2_small_dim(jasper, oracle_lib, tmp_path):
+    x = gaussian(2000, 96, 20)
+    q = gaussian(48, 96, 21)
+    _case(jasper, tmp_path, x, q, R=32, distance="l2", k_ranks=4, prerotate=False, lsh=True, pq=True)
+
+
+def test_lsh_pq_l2_prerotated(jasper, oracle_lib, tmp_path):
+    x = integer_clustered(2500, 128, 22)
+    q = integer_clustered(40, 128, 23)
+    _case(jasper, tmp_path, x, q, R=64, distance="l2", k_ranks=16, prerotate=True, lsh=True, pq=True,
+          bws=(32, 96))
+
+
+def test_lsh_ip(jasper, oracle_lib, tmp_path):
+    x = unit(2000, 64, 24)
+    q = unit(40, 64, 25)
+    _case(jasper, tmp_path, x, q, R=32, distance="ip", k_ranks=4, prerotate=True, lsh=True, pq=True)
+
+
+def test_large_dim_u16_words(jasper, oracle_lib, tmp_path):
+    x = gaussian(1200, 200, 26)
+    q = gaussian(24, 200, 27)
+    _case(jasper, tmp_path, x, q, R=32, distance="l2", k_ranks=4, prerotate=False, lsh=True, pq=True,
+          bws=(32,))
+
+
+def test_lsh_only_then_pq_search_rejected(jasper, oracle_lib):
+    x = gaussian(600, 64, 28)
+    gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=32, build_lsh=True,
+                            k_ranks=4, lsh_samples=1000)
+    with pytest.raises(RuntimeError):
+        gg.pq_search(torch.from_numpy(x[:4].astype(np.float16)).cuda(), k=5)
+    gg.free()
+
+
+def test_directional_k_larger_than_visits(jasper, oracle_lib):
+    x = gaussian(600, 64, 29)
+    gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=32, build_lsh=True,
+                            k_ranks=4, lsh_samples=1000, prerotate=False)
+    ids, d = _search(gg, "directional_search", x[:3], k=30, bw=4, limit=2)
+    assert (ids[:, 3:] == 0x7FFFFFFF).all()
+    assert (d[:, 3:] == np.finfo(np.float32).max).all()
+    gg.free()
