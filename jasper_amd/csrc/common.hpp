@@ -58,6 +58,13 @@ __host__ __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_fl
 __device__ __forceinline__ float h2f_lo(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w & 0xFFFFu))); }
 __device__ __forceinline__ float h2f_hi(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w >> 16))); }
 
+// Correctly rounded fp32 square root and quotient. The hardware v_sqrt_f32
+// is not correctly rounded (and HIP's __fsqrt_rn maps to it), so both go
+// through f64, whose LLVM lowering is correctly rounded; rounding the f64
+// result to f32 is then exact-then-round (53 >= 2 * 24 + 2).
+__device__ __forceinline__ float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
+__device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
+
 // ----------------------------------------------------------- wave helpers --
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(64) void lsh_calib_kernel(const uint16_t* __restric
     const float f = h2f16(d);
     p1 = __builtin_fmaf(f, f, p1);
   }
-  const float inv_norm = __fdiv_rn(1.0f, __fsqrt_rn(block128_sum(p0, p1) + 1e-20f));
+  const float inv_norm = div_rn(1.0f, sqrt_rn(block128_sum(p0, p1) + 1e-20f));
   wave_sync();
   if (inv_norm > 1e9f) {
     if (lane == 0) valid[s] = 0;
@@ -239,7 +239,7 @@ __global__ void lsh_finalize_kernel(const float* __restrict__ contrib, const uin
     ++nv;
     for (uint32_t r = 0; r < K; ++r) sum[r] = sum[r] + contrib[s * K + r];
   }
-  const float inv_n = __fdiv_rn(1.0f, (float)nv);
+  const float inv_n = div_rn(1.0f, (float)nv);
   float denom = 0.0f;
   for (uint32_t r = 0; r < K; ++r) {
     const float c = sum[r] * inv_n;
@@ -394,7 +394,7 @@ __global__ void pq_update_kernel(const uint16_t* __restrict__ X, int64_t n_train
     }
   }
   if (cnt > 0) {
-    C[(size_t)jc * dsub + t] = s * __fdiv_rn(1.0f, (float)cnt);
+    C[(size_t)jc * dsub + t] = s * div_rn(1.0f, (float)cnt);
   } else {
     const uint64_t r = pq_hash((uint64_t)jc ^ ((uint64_t)iter * 0x9E3779B9u), init_seed) % (uint64_t)n_train;
     C[(size_t)jc * dsub + t] = h2f16(X[(size_t)r * dp + (size_t)j * dsub + t]);
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
           const uint8_t* mb = row + (size_t)a.R * a.K * a.pbytes + 2 * (size_t)e;
           const float mag_sq = bf2f((uint16_t)(mb[0] | ((uint32_t)mb[1] << 8)));
           const float dot_est = dot_acc * a.inv_norm_denom;
-          const float mag = __fsqrt_rn(mag_sq);
+          const float mag = sqrt_rn(mag_sq);
           est = L2 ? __builtin_fmaf(-(2.0f * mag), dot_est, exact_u + mag_sq)
                    : -__builtin_fmaf(mag, dot_est, exact_u);
         }
