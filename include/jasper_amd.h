@@ -147,10 +147,22 @@ int64_t jasperx_search_stats(int64_t handle, const void* queries, int64_t n_quer
 int64_t jasperx_export_vectors(int64_t handle, uint16_t* out);
 int64_t jasperx_export_lsh(int64_t handle, float* c_per_rank, float* norm_denom, uint8_t* rows);
 int64_t jasperx_export_pq(int64_t handle, float* centroids, uint8_t* codes, float* norms);
+/* The query rows a directional search reads (padded to padded_dim, and
+ * rotated when the graph was prerotated), written to host memory
+ * out[n_queries * padded_dim] as fp16 bits; returns padded_dim. */
+int64_t jasperx_directional_query_rows(int64_t handle, const void* queries, int64_t n_queries, int64_t dim,
+                                       uint16_t* out, void* stream);
 /* The prerotation matrix for (dim, seed), column-major f32 [dim*dim], as
  * set_rotation_matrix returns it before the fp16 cast (reference
  * include/jasper/rotation/rotation.cuh:71-111). Host-only. */
 int64_t jasperx_rotation_matrix(int64_t dim, int64_t seed, float* out);
+/* Rotate fp16 rows by that matrix on the GPU: out[r][i] = fp16(sum_k
+ * P[k + i*dim] * x[r][k]) with fp32 accumulation (the prerotation of
+ * include/jasper/index/construct.cuh:1068-1090 as an operator). x: n rows of
+ * stride x_stride elements (device or host memory); out: device, stride
+ * out_stride. Synchronises the stream before returning. */
+int64_t jasperx_rotate_rows(int64_t dim, int64_t seed, const void* x, int64_t n, int64_t x_stride, void* out,
+                            int64_t out_stride, void* stream);
 /* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 

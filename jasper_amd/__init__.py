@@ -86,6 +86,8 @@ _AGNOSTIC = {
     "jasperx_export_lsh": [_i64, _ptr, _ptr, _ptr],
     "jasperx_export_pq": [_i64, _ptr, _ptr, _ptr],
     "jasperx_rotation_matrix": [_i64, _i64, _ptr],
+    "jasperx_directional_query_rows": [_i64, _ptr, _i64, _i64, _ptr, _ptr],
+    "jasperx_rotate_rows": [_i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr],
 }
 
 
@@ -493,6 +495,18 @@ class Graph:
         _agnostic("jasperx_export_vectors")(self._handle, out.ctypes.data_as(_ptr))
         return out
 
+    def directional_query_rows(self, queries: torch.Tensor) -> np.ndarray:
+        """The rows a directional search reads for these queries [nq,
+        padded_dim] fp16 bits (rotated when prerotated); a test extension."""
+        self._check_alive()
+        queries = self._query_check(queries)
+        nq = queries.size(0)
+        dp = (self._dim + 7) // 8 * 8
+        out = np.zeros((nq, dp), dtype=np.uint16)
+        _agnostic("jasperx_directional_query_rows")(self._handle, _tensor_ptr(queries), nq, self._dim,
+                                                    out.ctypes.data_as(_ptr), _stream_ptr(queries.device))
+        return out
+
     def export_lsh(self):
         """(c_per_rank f32 [k_ranks], norm_denom, rows u8 [n, row_bytes]); a
         test extension."""
@@ -634,4 +648,19 @@ def rotation_matrix(dim: int, seed: int = 42) -> np.ndarray:
     (reference include/jasper/rotation/rotation.cuh:71-111)."""
     out = np.empty(dim * dim, dtype=np.float32)
     _agnostic("jasperx_rotation_matrix")(dim, seed, out.ctypes.data_as(_ptr))
+    return out
+
+
+def rotate(vectors: torch.Tensor, seed: int = 42) -> torch.Tensor:
+    """Rows x -> P^T x with the prerotation matrix of (dim, seed) on the
+    matrix cores (fp16 in and out, fp32 accumulation)."""
+    if vectors.ndim != 2 or vectors.dtype != torch.float16:
+        raise ValueError("vectors must be a 2D float16 tensor")
+    vectors = vectors.contiguous()
+    n, dim = vectors.shape
+    dev = vectors.device if vectors.is_cuda else torch.device("cuda")
+    out = torch.empty((n, dim), dtype=torch.float16, device=dev)
+    if n:
+        _agnostic("jasperx_rotate_rows")(dim, seed, _tensor_ptr(vectors), n, dim, _tensor_ptr(out), dim,
+                                         _stream_ptr(dev))
     return out

@@ -475,6 +475,28 @@ extern "C" int64_t jasperx_export_pq(int64_t h, float* centroids, uint8_t* codes
   });
 }
 
+extern "C" int64_t jasperx_directional_query_rows(int64_t h, const void* queries, int64_t nq, int64_t dim,
+                                                  uint16_t* out, void* stream) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    directional_query_rows_to_host(g, queries, nq, dim, out, (hipStream_t)stream);
+    return (int64_t)g.dp;
+  });
+}
+
+extern "C" int64_t jasperx_rotate_rows(int64_t dim, int64_t seed, const void* x, int64_t n, int64_t x_stride,
+                                       void* out, int64_t out_stride, void* stream) {
+  return guarded([&]() -> int64_t {
+    if (dim <= 0 || dim > 65536) throw std::invalid_argument("dim must be in 1..65536");
+    if (n < 0 || x_stride < dim || out_stride < dim) throw std::invalid_argument("bad row counts or strides");
+    auto r = make_rotation(rotation_matrix((uint32_t)dim, (uint64_t)seed), (uint32_t)dim);
+    hipStream_t s = (hipStream_t)stream;
+    rotate_rows_any(*r, x, n, x_stride, out, out_stride, s);
+    hip_check(hipStreamSynchronize(s), "rotation");
+    return 0;
+  });
+}
+
 extern "C" int64_t jasperx_last_build_stats(double* out7) {
   return guarded([&]() -> int64_t {
     std::lock_guard<std::mutex> lock(g_mutex);

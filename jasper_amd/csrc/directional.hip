@@ -17,6 +17,7 @@
 #include "common.hpp"
 #include "directional.hpp"
 #include "directional_api.hpp"
+#include "rotation.hpp"
 #include "search.hpp"
 
 #include <algorithm>
@@ -124,53 +125,6 @@ __device__ bool sample_edge(const uint32_t* edges, const uint8_t* counts, int64_
     return true;
   }
   return false;
-}
-
-// ------------------------------------------------------------- rotation --
-// x'_i = sum_k P[k + i*dim] * x_k, P column-major fp16, fp32 fma in k order,
-// fp16 round-to-nearest output (construct.cuh:1077-1089 computes the same
-// product with cuBLAS GemmEx; its summation order is not specified).
-__global__ void rotate_rows_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t dim, uint32_t dp_in,
-                                   uint32_t dp_out, const uint16_t* __restrict__ P, uint16_t* __restrict__ out) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = t / dp_out;
-  const uint32_t i = (uint32_t)(t % dp_out);
-  if (row >= n) return;
-  uint16_t r = 0;
-  if (i < dim) {
-    const uint16_t* xr = x + (size_t)row * dp_in;
-    const uint16_t* pc = P + (size_t)i * dim;
-    float acc = 0.0f;
-    for (uint32_t k = 0; k < dim; ++k) acc = __builtin_fmaf(h2f16(pc[k]), h2f16(xr[k]), acc);
-    r = __half_as_ushort(__float2half_rn(acc));
-  }
-  out[(size_t)row * dp_out + i] = r;
-}
-
-static void rotate_rows(const void* x, int64_t n, uint32_t dim, uint32_t dp_in, uint32_t dp_out, const void* P,
-                        void* out, hipStream_t s) {
-  if (n <= 0) return;
-  const int64_t total = n * (int64_t)dp_out;
-  const uint32_t block = 256;
-  const int64_t grid = (total + block - 1) / block;
-  if (grid > 0x7FFFFFFFll) throw std::invalid_argument("rotation too large for one launch");
-  hipLaunchKernelGGL(rotate_rows_kernel, dim3((uint32_t)grid), dim3(block), 0, s, (const uint16_t*)x, n, dim,
-                     dp_in, dp_out, (const uint16_t*)P, (uint16_t*)out);
-  hip_check(hipGetLastError(), "launch rotate_rows_kernel");
-}
-
-// Random orthogonal matrix (rotation.cuh:28-111): mt19937_64 + float normal
-// distribution, Householder loop, column flips where R_ii < 0. Column-major.
-static std::vector<float> rotation_matrix(uint32_t d, uint64_t seed);
-
-static void* device_rotation_fp16(uint32_t d, uint64_t seed) {
-  const std::vector<float> m = rotation_matrix(d, seed);
-  std::vector<uint16_t> h(m.size());
-  for (size_t i = 0; i < m.size(); ++i) h[i] = __half_as_ushort(__float2half_rn(m[i]));
-  void* p = nullptr;
-  hip_check(hipMalloc(&p, h.size() * 2), "alloc rotation matrix");
-  hip_check(hipMemcpy(p, h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload rotation matrix");
-  return p;
 }
 
 // ------------------------------------------------------------ LSH build --
@@ -772,10 +726,10 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
   if (prerotate) {
     // The reference rotates the caller's buffer in place (E.4,
     // construct.cuh:1104-1107); here the graph's own copy is rotated.
-    g->rotation = device_rotation_fp16((uint32_t)dim, seed);
+    g->rotation = make_rotation(rotation_matrix((uint32_t)dim, seed), (uint32_t)dim);
     void* tmp = nullptr;
     hip_check(hipMalloc(&tmp, (size_t)n * g->dp * 2), "alloc rotation output");
-    rotate_rows(g->vecs, n, (uint32_t)dim, g->dp, g->dp, g->rotation, tmp, stream);
+    rotate_rows(*g->rotation, g->vecs, n, g->dp, tmp, g->dp, stream);
     hip_check(hipMemcpyAsync(g->vecs, tmp, (size_t)n * g->dp * 2, hipMemcpyDeviceToDevice, stream), "copy rotated");
     hip_check(hipStreamSynchronize(stream), "sync rotation");
     (void)hipFree(tmp);
@@ -903,6 +857,36 @@ void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed) {
   g.pq = std::move(art);
 }
 
+// Padded and, when the graph was prerotated, rotated query rows [nq, dp] in
+// device memory from the stream's pool; *scratch is a second buffer to free.
+static const uint16_t* directional_query_rows(const Graph& g, const void* queries, int64_t nq, int64_t dim,
+                                              hipStream_t stream, void** qrows, void** rot) {
+  *qrows = nullptr;
+  *rot = nullptr;
+  hip_check(hipMallocAsync(qrows, (size_t)nq * g.dp * 2, stream), "alloc query rows");
+  hip_check(hipMemsetAsync(*qrows, 0, (size_t)nq * g.dp * 2, stream), "clear query rows");
+  hip_check(hipMemcpy2DAsync(*qrows, (size_t)g.dp * 2, queries, (size_t)dim * 2, (size_t)dim * 2, (size_t)nq,
+                             hipMemcpyDefault, stream),
+            "copy queries");
+  if (!g.prerotate) return (const uint16_t*)*qrows;
+  if (!g.rotation) throw std::runtime_error("prerotated graph has no rotation matrix");
+  hip_check(hipMallocAsync(rot, (size_t)nq * g.dp * 2, stream), "alloc rotated queries");
+  rotate_rows(*g.rotation, *qrows, nq, g.dp, *rot, g.dp, stream);
+  return (const uint16_t*)*rot;
+}
+
+void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t nq, int64_t dim, uint16_t* out,
+                                    hipStream_t stream) {
+  if (dim != (int64_t)g.dim) throw std::invalid_argument("query dim does not match the graph");
+  if (nq <= 0) return;
+  void *qrows, *rot;
+  const uint16_t* rows = directional_query_rows(g, queries, nq, dim, stream, &qrows, &rot);
+  hip_check(hipMemcpyAsync(out, rows, (size_t)nq * g.dp * 2, hipMemcpyDefault, stream), "download query rows");
+  hip_check(hipStreamSynchronize(stream), "sync query rows");
+  if (rot) (void)hipFreeAsync(rot, stream);
+  (void)hipFreeAsync(qrows, stream);
+}
+
 void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                         float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream) {
   if (use_pq && !g.pq) throw std::runtime_error("graph has no PQ artifacts built — call build_pq() first");
@@ -914,18 +898,9 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
   if (bw + 64 >= 2048)
     throw std::invalid_argument("beam_width " + std::to_string(bw) + " is too large (beam_width + 64 must be < 2048)");
   if (g.R > 64) throw std::invalid_argument("R must be <= 64");
-  // padded (and, if the graph was prerotated, rotated) query rows
-  void* qrows = nullptr;
-  hip_check(hipMallocAsync(&qrows, (size_t)nq * g.dp * 2, stream), "alloc query rows");
-  hip_check(hipMemsetAsync(qrows, 0, (size_t)nq * g.dp * 2, stream), "clear query rows");
-  hip_check(hipMemcpy2DAsync(qrows, (size_t)g.dp * 2, queries, (size_t)dim * 2, (size_t)dim * 2, (size_t)nq,
-                             hipMemcpyDefault, stream),
-            "copy queries");
-  void* rot = nullptr;
-  if (g.prerotate) {
-    hip_check(hipMallocAsync(&rot, (size_t)nq * g.dp * 2, stream), "alloc rotated queries");
-    rotate_rows(qrows, nq, g.dim, g.dp, g.dp, g.rotation, rot, stream);
-  }
+  if ((int64_t)g.medoid >= g.n) throw std::runtime_error("graph medoid is out of range");
+  void *qrows, *rot;
+  const uint16_t* qsrc = directional_query_rows(g, queries, nq, dim, stream, &qrows, &rot);
   DirArgs a{};
   a.vecs = (const uint16_t*)g.vecs;
   a.n = g.n;
@@ -934,7 +909,7 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
   a.edges = g.edges;
   a.counts = g.counts;
   a.deleted = g.deleted;
-  a.queries = (const uint16_t*)(rot ? rot : qrows);
+  a.queries = qsrc;
   a.medoid = g.medoid;
   a.k = (uint32_t)k;
   a.bw = (uint32_t)bw;
@@ -942,7 +917,6 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
   a.max_result = 2048;
   a.out_ids = out_ids;
   a.out_dists = out_dists;
-  if ((int64_t)g.medoid >= g.n) throw std::runtime_error("graph medoid is out of range");
   size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
   if (use_pq) {
     a.M = g.pq->m;
@@ -1055,7 +1029,7 @@ std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t d
   g->packed_bytes = small_dim ? 1 : 2;
   g->prerotate = prerotate;
   g->prerotate_seed = seed;
-  if (prerotate) g->rotation = device_rotation_fp16(dim, seed);
+  if (prerotate) g->rotation = make_rotation(rotation_matrix(dim, seed), dim);
   if (g->n == 0) return g;
   std::ifstream f(path, std::ios::binary | std::ios::ate);
   if (!f.is_open()) throw std::runtime_error("load_directional_graph_from_file: cannot reopen " + path);
@@ -1119,57 +1093,6 @@ std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t d
     hip_check(hipMemcpy(g->vector_norms, nrm.data(), nrm.size() * 4, hipMemcpyHostToDevice), "upload norms");
   }
   return g;
-}
-
-// ------------------------------------------------------ rotation matrix --
-// Host restatement of set_rotation_matrix (rotation.cuh:28-111).
-
-}  // namespace jasper_amd
-
-#include <random>
-
-extern "C" int64_t jasperx_rotation_matrix(int64_t dim, int64_t seed, float* out);
-
-namespace jasper_amd {
-
-static std::vector<float> rotation_matrix(uint32_t dd, uint64_t seed) {
-  const int d = (int)dd;
-  std::mt19937_64 rng(seed);
-  std::normal_distribution<float> N(0, 1);
-  std::vector<float> A((size_t)d * d);
-  for (int j = 0; j < d; j++)
-    for (int i = 0; i < d; i++) A[(size_t)i + (size_t)j * d] = N(rng);
-  std::vector<float> Q((size_t)d * d, 0.0f);
-  for (int i = 0; i < d; i++) Q[(size_t)i + (size_t)i * d] = 1.0f;
-  std::vector<float> v((size_t)d);
-  for (int k = 0; k < d; k++) {
-    float norm_sq = 0;
-    for (int i = k; i < d; i++) {
-      v[i] = A[(size_t)i + (size_t)k * d];
-      norm_sq += v[i] * v[i];
-    }
-    const float norm = std::sqrt(norm_sq);
-    if (norm < 1e-12f) continue;
-    const float sign = (A[(size_t)k + (size_t)k * d] >= 0) ? 1.0f : -1.0f;
-    v[k] += sign * norm;
-    float v_norm_sq = 0;
-    for (int i = k; i < d; i++) v_norm_sq += v[i] * v[i];
-    const float tau = 2.0f / v_norm_sq;
-    for (int j = k; j < d; j++) {
-      float dot = 0;
-      for (int i = k; i < d; i++) dot += v[i] * A[(size_t)i + (size_t)j * d];
-      for (int i = k; i < d; i++) A[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
-    }
-    for (int j = 0; j < d; j++) {
-      float dot = 0;
-      for (int i = k; i < d; i++) dot += v[i] * Q[(size_t)i + (size_t)j * d];
-      for (int i = k; i < d; i++) Q[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
-    }
-  }
-  for (int i = 0; i < d; i++)
-    if (A[(size_t)i + (size_t)i * d] < 0.0f)
-      for (int j = 0; j < d; j++) Q[(size_t)j + (size_t)i * d] *= -1.0f;
-  return Q;
 }
 
 }  // namespace jasper_amd

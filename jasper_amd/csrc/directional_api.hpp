@@ -25,6 +25,10 @@ void build_lsh(Graph& g, int64_t n_samples, uint64_t seed);
 void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed);
 void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                         float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream);
+// The query rows the directional kernels read (padded, rotated when the
+// graph was prerotated), copied to host memory [nq, padded_dim].
+void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t nq, int64_t dim, uint16_t* out,
+                                    hipStream_t stream);
 void save_directional_file(const Graph& g, const std::string& path);
 std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
                                              uint32_t k_ranks, bool small_dim, bool on_host, bool prerotate,

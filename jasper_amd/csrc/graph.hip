@@ -97,8 +97,7 @@ void Graph::release() {
   counts = nullptr;
   deleted = nullptr;
   slot_to_id = nullptr;
-  if (rotation) (void)hipFree(rotation);
-  rotation = nullptr;
+  rotation.reset();
   if (vector_norms) (void)hipFree(vector_norms);
   vector_norms = nullptr;
   lsh.reset();

@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "directional.hpp"
+#include "rotation.hpp"
 
 namespace jasper_amd {
 
@@ -52,7 +53,7 @@ struct Graph {
   // directional state (owned; null when absent)
   bool prerotate = false;
   uint64_t prerotate_seed = 42;
-  void* rotation = nullptr;    // fp16 [dim, dim] column-major, device
+  std::unique_ptr<RotationMatrix> rotation;  // prerotation (MFMA layout)
   std::unique_ptr<LshArtifacts> lsh;
   std::unique_ptr<PqArtifacts> pq;
   float* vector_norms = nullptr;  // [n] ||x||^2

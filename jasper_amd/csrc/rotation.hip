@@ -1,0 +1,257 @@
+// rotation.hip -- row rotation x' = P^T x on the matrix cores.
+//
+// Reference: construct.cuh:1021-1112 (cublasGemmEx, fp16 in/out, fp32
+// compute, stride padded_dim) and rotation.cuh:122-151 (rotate_data_vec,
+// queries). Here one wave computes a 16-row tile with
+// v_mfma_f32_16x16x32_f16: the MFMA's M side is 16 outputs i, its N side the
+// 16 rows, K runs over the input coordinates. P is held transposed and
+// K-padded (Pt[i][k] = P[k + i*dim], zero for i or k >= dim) so that both
+// operands are 16-byte loads along K. Each lane ends with four consecutive
+// outputs of one row per M tile, rounded to fp16 (round to nearest even).
+#include "common.hpp"
+#include "graph.hpp"
+#include "rotation.hpp"
+
+#include <cmath>
+#include <random>
+#include <stdexcept>
+#include <vector>
+
+namespace jasper_amd {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ half8 as_half8(uint4 v) {
+  half8 h;
+  __builtin_memcpy(&h, &v, 16);
+  return h;
+}
+
+// KS = number of 32-wide K steps held in registers (Kp = 32 * KS). With
+// KS == 0 the K loop runs over kp32 steps and reloads operands per M tile.
+template <int KS, bool PT_LDS>
+__global__ __launch_bounds__(256) void rotate_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t dp_in,
+                                                          const uint16_t* __restrict__ pt, uint32_t kp,
+                                                          uint32_t dim, uint16_t* __restrict__ out,
+                                                          uint32_t dp_out) {
+  extern __shared__ uint4 pt_lds[];  // [mp][kp/8] when PT_LDS
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t mp = (dim + 15u) & ~15u;  // outputs padded to the M tile
+  const uint32_t kc = kp / 8;               // uint4 chunks per Pt row
+  const uint4* ptg = reinterpret_cast<const uint4*>(pt);
+  if constexpr (PT_LDS) {
+    for (uint32_t i = threadIdx.x; i < mp * kc; i += blockDim.x) pt_lds[i] = ptg[i];
+    __syncthreads();
+  }
+  const uint4* ptv = PT_LDS ? pt_lds : ptg;
+  const uint32_t col = lane & 15u;   // row of the tile (MFMA N index)
+  const uint32_t kq = lane >> 4;     // which 8-wide K slice of the 32-wide step
+  const uint32_t in_chunks = dp_in / 8;
+  const int64_t tiles = (n + 15) / 16;
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < tiles; tile += (int64_t)gridDim.x * 4) {
+    const int64_t row = tile * 16 + col;
+    const bool row_ok = row < n;
+    const uint4* xr = reinterpret_cast<const uint4*>(x) + (size_t)(row_ok ? row : 0) * in_chunks;
+    uint16_t* orow = out + (size_t)(row_ok ? row : 0) * dp_out;
+    if constexpr (KS > 0) {
+      uint4 xf[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t c = (uint32_t)s * 4 + kq;
+        xf[s] = (row_ok && c < in_chunks) ? xr[c] : make_uint4(0, 0, 0, 0);
+      }
+      for (uint32_t m0 = 0; m0 < mp; m0 += 16) {
+        float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const uint4 pf = ptv[(size_t)(m0 + col) * kc + (uint32_t)s * 4 + kq];
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(pf), as_half8(xf[s]), acc, 0, 0, 0);
+        }
+        if (row_ok) {
+          const uint32_t i0 = m0 + 4 * kq;
+          if (i0 + 3 < dp_out) {
+            uint2 w;
+            w.x = (uint32_t)__half_as_ushort(__float2half_rn(acc[0])) |
+                  ((uint32_t)__half_as_ushort(__float2half_rn(acc[1])) << 16);
+            w.y = (uint32_t)__half_as_ushort(__float2half_rn(acc[2])) |
+                  ((uint32_t)__half_as_ushort(__float2half_rn(acc[3])) << 16);
+            *reinterpret_cast<uint2*>(orow + i0) = w;
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (i0 + j < dp_out) orow[i0 + j] = __half_as_ushort(__float2half_rn(acc[j]));
+          }
+        }
+      }
+    } else {
+      const uint32_t ksteps = kp / 32;
+      for (uint32_t m0 = 0; m0 < mp; m0 += 16) {
+        float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t s = 0; s < ksteps; ++s) {
+          const uint32_t c = s * 4 + kq;
+          const uint4 xv = (row_ok && c < in_chunks) ? xr[c] : make_uint4(0, 0, 0, 0);
+          const uint4 pf = ptv[(size_t)(m0 + col) * kc + c];
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(pf), as_half8(xv), acc, 0, 0, 0);
+        }
+        if (row_ok) {
+          const uint32_t i0 = m0 + 4 * kq;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (i0 + j < dp_out) orow[i0 + j] = __half_as_ushort(__float2half_rn(acc[j]));
+        }
+      }
+    }
+  }
+}
+
+// Zero the output pad columns [dim, dp_out) that the tiles do not cover.
+__global__ void clear_pad_kernel(uint16_t* out, int64_t n, uint32_t mp, uint32_t dp_out) {
+  const uint32_t w = dp_out - mp;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * (int64_t)w) return;
+  out[(size_t)(t / w) * dp_out + mp + (uint32_t)(t % w)] = 0;
+}
+
+// Host restatement of householder_qr + set_rotation_matrix
+// (rotation.cuh:28-111): the matrix must be the reference's, bit for bit, for
+// graphs built with prerotation to be searched with the same rotation.
+std::vector<float> rotation_matrix(uint32_t dd, uint64_t seed) {
+  const int d = (int)dd;
+  std::mt19937_64 rng(seed);
+  std::normal_distribution<float> N(0, 1);
+  std::vector<float> A((size_t)d * d);
+  for (int j = 0; j < d; j++)
+    for (int i = 0; i < d; i++) A[(size_t)i + (size_t)j * d] = N(rng);
+  std::vector<float> Q((size_t)d * d, 0.0f);
+  for (int i = 0; i < d; i++) Q[(size_t)i + (size_t)i * d] = 1.0f;
+  std::vector<float> v((size_t)d);
+  for (int k = 0; k < d; k++) {
+    float norm_sq = 0;
+    for (int i = k; i < d; i++) {
+      v[i] = A[(size_t)i + (size_t)k * d];
+      norm_sq += v[i] * v[i];
+    }
+    const float norm = std::sqrt(norm_sq);
+    if (norm < 1e-12f) continue;
+    const float sign = (A[(size_t)k + (size_t)k * d] >= 0) ? 1.0f : -1.0f;
+    v[k] += sign * norm;
+    float v_norm_sq = 0;
+    for (int i = k; i < d; i++) v_norm_sq += v[i] * v[i];
+    const float tau = 2.0f / v_norm_sq;
+    for (int j = k; j < d; j++) {
+      float dot = 0;
+      for (int i = k; i < d; i++) dot += v[i] * A[(size_t)i + (size_t)j * d];
+      for (int i = k; i < d; i++) A[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
+    }
+    for (int j = 0; j < d; j++) {
+      float dot = 0;
+      for (int i = k; i < d; i++) dot += v[i] * Q[(size_t)i + (size_t)j * d];
+      for (int i = k; i < d; i++) Q[(size_t)i + (size_t)j * d] -= tau * v[i] * dot;
+    }
+  }
+  for (int i = 0; i < d; i++)
+    if (A[(size_t)i + (size_t)i * d] < 0.0f)
+      for (int j = 0; j < d; j++) Q[(size_t)j + (size_t)i * d] *= -1.0f;
+  return Q;
+}
+
+RotationMatrix::~RotationMatrix() {
+  if (pt) (void)hipFree(pt);
+}
+
+std::unique_ptr<RotationMatrix> make_rotation(const std::vector<float>& P, uint32_t dim) {
+  auto r = std::make_unique<RotationMatrix>();
+  r->dim = dim;
+  r->kp = (dim + 31u) & ~31u;
+  r->mp = (dim + 15u) & ~15u;
+  std::vector<uint16_t> h((size_t)r->mp * r->kp, 0);
+  for (uint32_t i = 0; i < dim; ++i)
+    for (uint32_t k = 0; k < dim; ++k) h[(size_t)i * r->kp + k] = f2h_rn(P[(size_t)k + (size_t)i * dim]);
+  hip_check(hipMalloc(&r->pt, h.size() * 2), "alloc rotation matrix");
+  hip_check(hipMemcpy(r->pt, h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload rotation matrix");
+  return r;
+}
+
+void rotate_rows(const RotationMatrix& r, const void* x, int64_t n, uint32_t dp_in, void* out, uint32_t dp_out,
+                 hipStream_t s) {
+  if (n <= 0) return;
+  if (dp_in % 8 != 0 || dp_out < r.dim) throw std::invalid_argument("rotate_rows: bad row strides");
+  const uint32_t ks = r.kp / 32;
+  const size_t lds = (size_t)r.mp * r.kp * 2;
+  const bool use_lds = lds <= 64 * 1024;
+  const int64_t tiles = (n + 15) / 16;
+  const uint32_t grid = (uint32_t)std::min<int64_t>((tiles + 3) / 4, 8192);
+  const uint16_t* xi = (const uint16_t*)x;
+  uint16_t* o = (uint16_t*)out;
+  auto launch = [&](auto kern, size_t shm) {
+    if (shm > 64 * 1024)
+      hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm),
+                "rotation LDS");
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), shm, s, xi, n, dp_in, (const uint16_t*)r.pt, r.kp, r.dim, o,
+                       dp_out);
+  };
+  if (use_lds) {
+    switch (ks) {
+      case 1: launch(rotate_mfma_kernel<1, true>, lds); break;
+      case 2: launch(rotate_mfma_kernel<2, true>, lds); break;
+      case 3: launch(rotate_mfma_kernel<3, true>, lds); break;
+      case 4: launch(rotate_mfma_kernel<4, true>, lds); break;
+      case 5: launch(rotate_mfma_kernel<5, true>, lds); break;
+      case 6: launch(rotate_mfma_kernel<6, true>, lds); break;
+      default: launch(rotate_mfma_kernel<0, true>, lds); break;
+    }
+  } else {
+    launch(rotate_mfma_kernel<0, false>, 0);
+  }
+  hip_check(hipGetLastError(), "launch rotate_mfma_kernel");
+  if (dp_out > r.mp) {
+    const int64_t total = n * (int64_t)(dp_out - r.mp);
+    hipLaunchKernelGGL(clear_pad_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, o, n, r.mp, dp_out);
+    hip_check(hipGetLastError(), "launch clear_pad_kernel");
+  }
+}
+
+// Rotation as a stand-alone operator: x [n, dim] fp16 rows with stride
+// x_stride elements (device or host memory) -> out [n, dim] with stride
+// out_stride (device). Rows that are not 16-byte aligned multiples of 8
+// elements go through padded staging buffers.
+void rotate_rows_any(const RotationMatrix& r, const void* x, int64_t n, int64_t x_stride, void* out,
+                     int64_t out_stride, hipStream_t s) {
+  if (n <= 0) return;
+  const uint32_t dp = (r.dim + 7u) & ~7u;
+  const bool in_ok = x_stride % 8 == 0 && ((uintptr_t)x & 15u) == 0 && x_stride >= (int64_t)dp;
+  const bool out_ok = out_stride % 8 == 0 && ((uintptr_t)out & 15u) == 0 && out_stride >= (int64_t)dp;
+  hipPointerAttribute_t attr{};
+  const bool in_dev = hipPointerGetAttributes(&attr, x) == hipSuccess && attr.type == hipMemoryTypeDevice;
+  (void)hipGetLastError();
+  void* xin = const_cast<void*>(x);
+  void* xs = nullptr;
+  void* os = nullptr;
+  if (!in_ok || !in_dev) {
+    hip_check(hipMallocAsync(&xs, (size_t)n * dp * 2, s), "alloc rotation input");
+    hip_check(hipMemsetAsync(xs, 0, (size_t)n * dp * 2, s), "clear rotation input");
+    hip_check(hipMemcpy2DAsync(xs, (size_t)dp * 2, x, (size_t)x_stride * 2, (size_t)r.dim * 2, (size_t)n,
+                               hipMemcpyDefault, s),
+              "stage rotation input");
+    xin = xs;
+  }
+  const int64_t in_stride = xs ? dp : x_stride;
+  if (out_ok) {
+    rotate_rows(r, xin, n, (uint32_t)in_stride, out, (uint32_t)out_stride, s);
+  } else {
+    hip_check(hipMallocAsync(&os, (size_t)n * dp * 2, s), "alloc rotation output");
+    rotate_rows(r, xin, n, (uint32_t)in_stride, os, dp, s);
+    hip_check(hipMemcpy2DAsync(out, (size_t)out_stride * 2, os, (size_t)dp * 2, (size_t)r.dim * 2, (size_t)n,
+                               hipMemcpyDefault, s),
+              "copy rotation output");
+  }
+  if (xs) (void)hipFreeAsync(xs, s);
+  if (os) (void)hipFreeAsync(os, s);
+}
+
+}  // namespace jasper_amd
+
+extern "C" int64_t jasperx_rotate_rows(int64_t dim, int64_t seed, const void* x, int64_t n, int64_t x_stride,
+                                       void* out, int64_t out_stride, void* stream);

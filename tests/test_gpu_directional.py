@@ -3,8 +3,10 @@
 Each case builds a directional graph on the GPU (Vamana build, optional
 prerotation, LSH and/or PQ artifacts), saves it in the reference format,
 reads the base section back with the oracle's loader, and checks:
-  * prerotated rows equal the oracle's rotation of the input (bit-exact);
-  * the graph equals the oracle's build of the same rows;
+  * prerotated rows (matrix-core GEMM, fp32 accumulation) are within one
+    fp16 rounding plus the fp32 accumulation bound of the oracle's rotation;
+    the same holds for rotated queries;
+  * the graph equals the oracle's build of the stored rows;
   * LSH calibration constants and per-edge rows are bit-identical to the
     oracle's, and so are PQ centroids, codes and vector norms;
   * directional_search / pq_search ids and distances are bit-identical to
@@ -22,10 +24,19 @@ from tests.helpers import compare_search, gaussian, integer_clustered, unit
 pytestmark = pytest.mark.gpu
 
 
-def _rotated_rows(x, dim, seed):
+def assert_rotation_close(got16, x, dim, seed=42):
+    """GEMM rows vs the exact product P^T x (fp16 P): at most half an fp16
+    ulp from rounding plus the fp32 accumulation bound."""
     m, _ = oracle.rotation_matrix(dim, seed)
-    P16 = m.astype(np.float16).view(np.uint16)
-    return oracle.rotate_rows(oracle.as_padded_f16(x), dim, P16)
+    P = m.astype(np.float16).astype(np.float64).reshape(dim, dim).T   # P[k, i]
+    xf = x.astype(np.float16).astype(np.float64)
+    want = xf @ P
+    got = got16[:, :dim].view(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    acc = dim * 2.0 ** -23 * (np.abs(xf) @ np.abs(P))
+    bad = np.abs(got - want) > 0.5 * ulp + acc
+    assert not bad.any(), f"{bad.sum()} rotated entries off, worst {np.abs(got - want).max()}"
+    assert not got16[:, dim:].any()
 
 
 def _search(gg, fn, q, k, bw, limit=None):
@@ -46,8 +57,11 @@ def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, b
     gg.save(str(path))
     g = oracle.load_graph(path, dim, R, distance)
 
-    rows = _rotated_rows(x, dim, 42) if prerotate else oracle.as_padded_f16(x)
-    assert np.array_equal(gg.export_vectors(), rows), "stored rows differ"
+    rows = gg.export_vectors()
+    if prerotate:
+        assert_rotation_close(rows, x, dim)
+    else:
+        assert np.array_equal(rows, oracle.as_padded_f16(x)), "stored rows differ"
     assert np.array_equal(g.vecs16, rows)
     ref = oracle.build(rows.view(np.float16)[:, :dim].astype(np.float32), R=R, distance=distance, alpha=1.2)
     assert g.medoid == ref.medoid
@@ -56,7 +70,11 @@ def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, b
         c = int(ref.counts[i])
         assert np.array_equal(g.edges[i, :c], ref.edges[i, :c]), f"vertex {i}"
 
-    q_rows = _rotated_rows(q, dim, 42) if prerotate else oracle.as_padded_f16(q)
+    q_rows = gg.directional_query_rows(torch.from_numpy(q.astype(np.float16)).cuda())
+    if prerotate:
+        assert_rotation_close(q_rows, q, dim)
+    else:
+        assert np.array_equal(q_rows, oracle.as_padded_f16(q))
     pbytes = 1 if dim <= 128 else 2
     out = {}
     if lsh:
@@ -144,3 +162,30 @@ def test_directional_k_larger_than_visits(jasper, oracle_lib):
     assert (ids[:, 3:] == 0x7FFFFFFF).all()
     assert (d[:, 3:] == np.finfo(np.float32).max).all()
     gg.free()
+
+
+@pytest.mark.parametrize("dim", [40, 100, 200])
+def test_prerotated_build_rows(jasper, oracle_lib, dim):
+    """Prerotated build: stored rows and query rows at dims that exercise the
+    K/M padding cases of the matrix-core rotation."""
+    x = gaussian(300, dim, 30) * 3
+    q = gaussian(37, dim, 31) * 3
+    gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=32, build_lsh=True,
+                            k_ranks=4, lsh_samples=500, prerotate=True)
+    assert_rotation_close(gg.export_vectors(), x, dim)
+    assert_rotation_close(gg.directional_query_rows(torch.from_numpy(q.astype(np.float16)).cuda()), q, dim)
+    gg.free()
+
+
+@pytest.mark.parametrize("dim,n", [(8, 5), (33, 70), (96, 1000), (128, 4099), (250, 64), (960, 300)])
+def test_rotate_operator(jasper, oracle_lib, dim, n):
+    """The stand-alone rotation (device and host inputs, unaligned strides,
+    the global-memory path for dim 960)."""
+    x = (gaussian(n, dim, 32) * 4).astype(np.float16)
+    got = jasper.rotate(torch.from_numpy(x).cuda(), seed=42)
+    torch.cuda.synchronize()
+    g16 = np.zeros((n, (dim + 7) // 8 * 8), dtype=np.uint16)
+    g16[:, :dim] = got.cpu().numpy().view(np.uint16)
+    assert_rotation_close(g16, x.astype(np.float32), dim)
+    got_h = jasper.rotate(torch.from_numpy(x), seed=42)     # host input
+    assert torch.equal(got_h.cpu(), got.cpu())
