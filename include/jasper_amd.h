@@ -163,6 +163,18 @@ int64_t jasperx_rotation_matrix(int64_t dim, int64_t seed, float* out);
  * out_stride. Synchronises the stream before returning. */
 int64_t jasperx_rotate_rows(int64_t dim, int64_t seed, const void* x, int64_t n, int64_t x_stride, void* out,
                             int64_t out_stride, void* stream);
+/* One-bit RaBitQ quantizer (include/jasper/rabitq/quantize.cuh:322-354,
+ * rabitq_quantize<1>; the reference has no FFI binding for it). vectors:
+ * device rows, dtype 0 = fp16 (stride a multiple of 8, 16-byte aligned) or
+ * 1 = fp32, row stride `stride` elements; rotation: device fp32 [dim*dim]
+ * column-major; centroid: device fp32 [dim] or NULL (zero); metric 0 = L2,
+ * 1 = IP; out: device [n * node_bytes], node = code bytes (ceil(dim/8)
+ * rounded up to 4, bits LSB-first) + f_add + f_rescale (fp32). Returns
+ * node_bytes; supports dim <= 256. Asynchronous on `stream`. */
+int64_t jasperx_rabitq_node_bytes(int64_t dim);
+int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, int64_t n, int64_t dim, int64_t stride,
+                                const float* rotation, const float* centroid, int32_t metric, void* out,
+                                void* stream);
 /* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 

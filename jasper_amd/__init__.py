@@ -88,6 +88,8 @@ _AGNOSTIC = {
     "jasperx_rotation_matrix": [_i64, _i64, _ptr],
     "jasperx_directional_query_rows": [_i64, _ptr, _i64, _i64, _ptr, _ptr],
     "jasperx_rotate_rows": [_i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr],
+    "jasperx_rabitq_node_bytes": [_i64],
+    "jasperx_rabitq_quantize": [_ptr, ctypes.c_int32, _i64, _i64, _i64, _ptr, _ptr, ctypes.c_int32, _ptr, _ptr],
 }
 
 
@@ -664,3 +666,76 @@ def rotate(vectors: torch.Tensor, seed: int = 42) -> torch.Tensor:
         _agnostic("jasperx_rotate_rows")(dim, seed, _tensor_ptr(vectors), n, dim, _tensor_ptr(out), dim,
                                          _stream_ptr(dev))
     return out
+
+
+class RabitqCodes:
+    """One-bit RaBitQ store (reference rabitq/layout.cuh:43-117): `nodes` is
+    a device uint8 tensor [n, node_bytes] of code bytes (LSB-first) followed
+    by f_add and f_rescale (fp32)."""
+
+    def __init__(self, nodes: torch.Tensor, dim: int):
+        self.nodes = nodes
+        self.dim = dim
+        self.node_bytes = nodes.size(1)
+        self.code_bytes = self.node_bytes - 8
+
+    @property
+    def codes(self) -> torch.Tensor:
+        return self.nodes[:, :self.code_bytes]
+
+    @property
+    def f_add(self) -> torch.Tensor:
+        return self.nodes[:, self.code_bytes:self.code_bytes + 4].contiguous().view(torch.float32).view(-1)
+
+    @property
+    def f_rescale(self) -> torch.Tensor:
+        return self.nodes[:, self.code_bytes + 4:].contiguous().view(torch.float32).view(-1)
+
+    def bits(self) -> torch.Tensor:
+        """Unpacked codes [n, dim] as uint8 0/1."""
+        b = self.codes.to(torch.int32)
+        shifts = torch.arange(8, device=b.device, dtype=torch.int32)
+        out = (b.unsqueeze(-1) >> shifts) & 1
+        return out.reshape(b.size(0), -1)[:, :self.dim].to(torch.uint8)
+
+
+def rabitq_quantize(vectors: torch.Tensor, rotation: torch.Tensor | None = None,
+                    centroid: torch.Tensor | None = None, distance: DistanceFunc | str = DistanceFunc.L2,
+                    seed: int = 42) -> RabitqCodes:
+    """One-bit RaBitQ codes of `vectors` [n, dim] (fp16 or fp32, CUDA)
+    (reference rabitq_quantize<1>, rabitq/quantize.cuh:322-383). `rotation`
+    is a column-major fp32 [dim, dim] matrix (default: the prerotation matrix
+    of `seed`); `centroid` defaults to zero."""
+    if isinstance(distance, str):
+        distance = DistanceFunc(distance)
+    if vectors.ndim != 2 or not vectors.is_cuda:
+        raise ValueError("vectors must be a 2D CUDA tensor")
+    if vectors.dtype not in (torch.float16, torch.float32):
+        raise ValueError("vectors must be float16 or float32")
+    n, dim = vectors.shape
+    dev = vectors.device
+    if rotation is None:
+        rotation = torch.from_numpy(rotation_matrix(dim, seed)).to(dev)
+    rotation = rotation.to(device=dev, dtype=torch.float32).contiguous()
+    if rotation.numel() != dim * dim:
+        raise ValueError(f"rotation must hold {dim}x{dim} values")
+    if centroid is not None:
+        centroid = centroid.to(device=dev, dtype=torch.float32).contiguous()
+        if centroid.numel() != dim:
+            raise ValueError(f"centroid must hold {dim} values")
+    if vectors.dtype == torch.float16 and (dim % 8 != 0 or vectors.data_ptr() % 16 != 0):
+        stride = (dim + 7) // 8 * 8
+        padded = torch.zeros((n, stride), dtype=torch.float16, device=dev)
+        padded[:, :dim] = vectors
+        vectors = padded
+    else:
+        vectors = vectors.contiguous()
+        stride = dim
+    node_bytes = _agnostic("jasperx_rabitq_node_bytes")(dim)
+    nodes = torch.empty((n, node_bytes), dtype=torch.uint8, device=dev)
+    if n:
+        _agnostic("jasperx_rabitq_quantize")(
+            _tensor_ptr(vectors), 0 if vectors.dtype == torch.float16 else 1, n, dim, stride,
+            _tensor_ptr(rotation), None if centroid is None else _tensor_ptr(centroid),
+            0 if distance == DistanceFunc.L2 else 1, _tensor_ptr(nodes), _stream_ptr(dev))
+    return RabitqCodes(nodes, dim)

@@ -18,6 +18,7 @@
 #include "common.hpp"
 #include "directional_api.hpp"
 #include "graph.hpp"
+#include "rabitq.hpp"
 #include "search.hpp"
 
 namespace jasper_amd {
@@ -494,6 +495,27 @@ extern "C" int64_t jasperx_rotate_rows(int64_t dim, int64_t seed, const void* x,
     rotate_rows_any(*r, x, n, x_stride, out, out_stride, s);
     hip_check(hipStreamSynchronize(s), "rotation");
     return 0;
+  });
+}
+
+extern "C" int64_t jasperx_rabitq_node_bytes(int64_t dim) {
+  return guarded([&]() -> int64_t {
+    if (dim <= 0 || dim > 65536) throw std::invalid_argument("dim must be in 1..65536");
+    return (int64_t)rabitq_code_bytes((uint32_t)dim) + 8;
+  });
+}
+
+extern "C" int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, int64_t n, int64_t dim, int64_t stride,
+                                           const float* rotation, const float* centroid, int32_t metric, void* out,
+                                           void* stream) {
+  return guarded([&]() -> int64_t {
+    if (dtype != 0 && dtype != 1) throw std::invalid_argument("dtype must be 0 (fp16) or 1 (fp32)");
+    if (metric != kL2 && metric != kIP) throw std::invalid_argument("metric must be 0 (L2) or 1 (IP)");
+    if (n < 0 || dim <= 0 || stride < dim) throw std::invalid_argument("bad sizes");
+    if (!rotation) throw std::invalid_argument("rotation matrix is required");
+    rabitq_quantize(vectors, dtype == 0, n, (uint32_t)dim, (uint32_t)stride, rotation, centroid, metric, out,
+                    (hipStream_t)stream);
+    return (int64_t)rabitq_code_bytes((uint32_t)dim) + 8;
   });
 }
 

@@ -106,6 +106,10 @@ def lib():
         _lib.jo_splitmix.argtypes = [u64]
         _lib.jo_sample_edge.restype = i32
         _lib.jo_sample_edge.argtypes = [P, P, i64, i32, u64, u64, P, P]
+        _lib.jo_rabitq_code_bytes.restype = ctypes.c_uint32
+        _lib.jo_rabitq_code_bytes.argtypes = [i32]
+        _lib.jo_rabitq_quantize.restype = None
+        _lib.jo_rabitq_quantize.argtypes = [P, i64, i32, P, P, i32, P, P, i32]
         _lib.jo_frontier_insert_seq.restype = None
         _lib.jo_frontier_insert_seq.argtypes = [P, P, i32, i32, P, P, P]
         _lib.jo_pq_encode.restype = None
@@ -458,6 +462,34 @@ def rotate_rows(vecs16: np.ndarray, dim: int, P16: np.ndarray, nthreads: int = 0
     lib().jo_rotate_rows(_ptr(vecs16), vecs16.shape[0], dim, vecs16.shape[1],
                          _ptr(np.ascontiguousarray(P16, dtype=np.uint16)), _ptr(out), nthreads)
     return out
+
+
+# ------------------------------------------------------------------ RaBitQ --
+# rabitq_quantize<1> (rabitq/quantize.cuh:144-383); see rabitq_oracle.cpp.
+
+def rabitq_code_bytes(dim: int) -> int:
+    """rabitq_data_store::code_bytes (layout.cuh:57-63) at one bit per dim."""
+    return int(lib().jo_rabitq_code_bytes(dim))
+
+
+def rabitq_quantize(x, P, centroid=None, metric: str = "l2", nthreads: int = 0, return_residuals: bool = False):
+    """One-bit RaBitQ codes of rows x [n, dim] (fp32) with rotation P
+    (column-major [dim*dim]) and centroid c [dim] (None: zero). Returns
+    (nodes u8 [n, code_bytes + 8], codes u8 [n, code_bytes], f_add f32 [n],
+    f_rescale f32 [n][, residuals f32 [n, dim]])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, dim = x.shape
+    P = np.ascontiguousarray(P, dtype=np.float32).ravel()
+    c = None if centroid is None else np.ascontiguousarray(centroid, dtype=np.float32)
+    cb = rabitq_code_bytes(dim)
+    out = np.zeros((n, cb + 8), dtype=np.uint8)
+    res = np.zeros((n, dim), dtype=np.float32) if return_residuals else None
+    lib().jo_rabitq_quantize(_ptr(x), n, dim, _ptr(P), _ptr(c), 0 if metric == "l2" else 1, _ptr(out), _ptr(res),
+                             nthreads)
+    f_add = np.ascontiguousarray(out[:, cb:cb + 4]).view(np.float32).ravel()
+    f_rescale = np.ascontiguousarray(out[:, cb + 4:cb + 8]).view(np.float32).ravel()
+    r = (out, out[:, :cb].copy(), f_add, f_rescale)
+    return r + (res,) if return_residuals else r
 
 
 # ------------------------------------------------------------- file format --
