@@ -175,6 +175,16 @@ int64_t jasperx_rabitq_node_bytes(int64_t dim);
 int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, int64_t n, int64_t dim, int64_t stride,
                                 const float* rotation, const float* centroid, int32_t metric, void* out,
                                 void* stream);
+/* Exact k-NN by brute force on the matrix cores (the ground-truth utility
+ * generate_groundtruth, python/jasper/__init__.py:828-926, which the
+ * reference runs in torch): L2 = (||q||^2 + ||v||^2) - 2 q.v in fp32 clamped
+ * at 0; IP = -(fp16(q.v)). base [n][stride] and queries [nq][stride] are
+ * device fp16 rows padded with zeros to stride = the next multiple of 8 of
+ * dim, 16-byte aligned. Results (device) ordered by (distance, id); k <= 64,
+ * dim <= 512. Asynchronous on `stream`. */
+int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t base_stride, const void* queries,
+                               int64_t n_queries, int64_t query_stride, int64_t k, int32_t metric,
+                               int32_t* out_ids, float* out_dists, void* stream);
 /* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 

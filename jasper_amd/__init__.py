@@ -89,6 +89,7 @@ _AGNOSTIC = {
     "jasperx_directional_query_rows": [_i64, _ptr, _i64, _i64, _ptr, _ptr],
     "jasperx_rotate_rows": [_i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr],
     "jasperx_rabitq_node_bytes": [_i64],
+    "jasperx_bruteforce_knn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, ctypes.c_int32, _ptr, _ptr, _ptr],
     "jasperx_rabitq_quantize": [_ptr, ctypes.c_int32, _i64, _i64, _i64, _ptr, _ptr, ctypes.c_int32, _ptr, _ptr],
 }
 
@@ -636,11 +637,11 @@ def save_groundtruth(path: str, indices: torch.Tensor, distances: torch.Tensor):
         f.write(dists_np.tobytes())
 
 
-from .groundtruth import generate_groundtruth  # noqa: E402
+from .groundtruth import bruteforce_knn, generate_groundtruth  # noqa: E402
 
 __all__ = [
     "Graph", "DistanceFunc", "DataType", "JasperError", "read_bin", "read_groundtruth",
-    "get_recall", "generate_groundtruth", "save_groundtruth", "parse_storage_size",
+    "get_recall", "generate_groundtruth", "bruteforce_knn", "save_groundtruth", "parse_storage_size",
     "last_build_stats", "library_path",
 ]
 

@@ -14,6 +14,7 @@
 #include <unordered_map>
 
 #include "../../include/jasper_amd.h"
+#include "bruteforce.hpp"
 #include "build.hpp"
 #include "common.hpp"
 #include "directional_api.hpp"
@@ -516,6 +517,21 @@ extern "C" int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, i
     rabitq_quantize(vectors, dtype == 0, n, (uint32_t)dim, (uint32_t)stride, rotation, centroid, metric, out,
                     (hipStream_t)stream);
     return (int64_t)rabitq_code_bytes((uint32_t)dim) + 8;
+  });
+}
+
+extern "C" int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t base_stride,
+                                          const void* queries, int64_t nq, int64_t query_stride, int64_t k,
+                                          int32_t metric, int32_t* out_ids, float* out_dists, void* stream) {
+  return guarded([&]() -> int64_t {
+    if (metric != kL2 && metric != kIP) throw std::invalid_argument("metric must be 0 (L2) or 1 (IP)");
+    if (dim <= 0 || n <= 0 || nq < 0 || k <= 0) throw std::invalid_argument("bad sizes");
+    if (base_stride != query_stride || base_stride % 8 != 0 || base_stride < dim || base_stride - dim >= 8)
+      throw std::invalid_argument("rows must be padded to the next multiple of 8 (same stride for both)");
+    if (((uintptr_t)base & 15u) || ((uintptr_t)queries & 15u)) throw std::invalid_argument("rows must be 16-byte aligned");
+    bruteforce_knn(base, n, (uint32_t)dim, (uint32_t)base_stride, queries, nq, (uint32_t)k, metric, out_ids,
+                   out_dists, (hipStream_t)stream);
+    return 0;
   });
 }
 

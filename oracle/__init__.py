@@ -73,7 +73,7 @@ def lib():
         _lib.jo_bruteforce_exact.restype = None
         _lib.jo_bruteforce_exact.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32]
         _lib.jo_bruteforce_ref.restype = None
-        _lib.jo_bruteforce_ref.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32]
+        _lib.jo_bruteforce_ref.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32, i32]
         _lib.jo_gaussian_matrix.restype = None
         _lib.jo_gaussian_matrix.argtypes = [i32, u64, P]
         _lib.jo_rotation_matrix.restype = None
@@ -266,15 +266,17 @@ def bruteforce_exact(vectors, queries, k: int = 10, distance: str = "l2", nthrea
     return ids, d
 
 
-def bruteforce_ref(vectors_f32, queries_f32, k: int = 10, distance: str = "l2", nthreads: int = 0):
-    """Reference ground-truth arithmetic (python/jasper/__init__.py:828-926)."""
+def bruteforce_ref(vectors_f32, queries_f32, k: int = 10, distance: str = "l2", nthreads: int = 0,
+                   ip_round_fp16: bool = False):
+    """Reference ground-truth arithmetic (python/jasper/__init__.py:828-926);
+    ip_round_fp16 models the fp16 matmul output of fp16 inputs under IP."""
     v = np.ascontiguousarray(vectors_f32, dtype=np.float32)
     q = np.ascontiguousarray(queries_f32, dtype=np.float32)
     nq = q.shape[0]
     ids = np.empty((nq, k), dtype=np.int32)
     d = np.empty((nq, k), dtype=np.float32)
     lib().jo_bruteforce_ref(metric_code(distance), _ptr(v), v.shape[0], _ptr(q), nq, v.shape[1], k,
-                            _ptr(ids), _ptr(d), nthreads)
+                            _ptr(ids), _ptr(d), nthreads, 1 if ip_round_fp16 else 0)
     return ids, d
 
 

@@ -484,12 +484,27 @@ void jo_bruteforce_exact(int metric, const uint16_t* vecs, int64_t n, const uint
 }
 
 // The reference's ground-truth arithmetic, python/jasper/__init__.py:828-926:
-// L2 = ||q||^2 + ||v||^2 - 2 q.v in fp32, clamped at 0; IP = -(q.v). Dot
-// products accumulate sequentially in fp32 (torch's order is unspecified).
-// Also the CPU baseline "exact kNN scan". Vectors are pre-converted to fp32.
+// L2 = ||q||^2 + ||v||^2 - 2 q.v in fp32, clamped at 0; IP = -(q.v), where
+// with fp16 inputs the matmul result is fp16 (ip_round_fp16 != 0 rounds q.v
+// to fp16 before the negation). Dot products accumulate sequentially in fp32
+// (torch's order is unspecified). Also the CPU baseline "exact kNN scan".
+// Vectors are pre-converted to fp32.
+extern "C" uint16_t jo_d2h(double x);  // directional_oracle.cpp: double -> fp16, RNE
+
+static float round_to_fp16(float x) {
+  const uint16_t h = jo_d2h((double)x);
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  float v;
+  if (e == 0) v = std::ldexp((float)m, -24);
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = std::ldexp((float)(m | 0x400u), (int)e - 25);
+  return sign ? -v : v;
+}
+
 void jo_bruteforce_ref(int metric, const float* vecs, int64_t n, const float* queries,
                        int64_t nq, int dim, int k, int32_t* out_ids, float* out_dists,
-                       int nthreads) {
+                       int nthreads, int ip_round_fp16) {
   if (nthreads > 0) omp_set_num_threads(nthreads);
   std::vector<float> vsq((size_t)n, 0.0f);
   if (metric == 0) {
@@ -520,7 +535,7 @@ void jo_bruteforce_ref(int metric, const float* vecs, int64_t n, const float* qu
           d = qsq + vsq[(size_t)i] - 2.0f * dot;
           if (d < 0.0f) d = 0.0f;
         } else {
-          d = -dot;
+          d = ip_round_fp16 ? -round_to_fp16(dot) : -dot;
         }
         const Cand c{(uint32_t)i, d};
         if ((int)heap.size() < k) {
