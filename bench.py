@@ -118,6 +118,12 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--path", default="search",
+                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq"],
+                    help="search (default, the headline metric) or one of the other hot-path rows, each "
+                         "printing its own JSON line: directional (config 3, LSH), pq (PQ-ADC on "
+                         "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
+                         "rabitq (one-bit codes)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -142,6 +148,8 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
         log("calibration copy: 3 x 512 MiB device-to-device")
+    if args.path != "search":
+        return OTHER_PATHS[args.path](args, torch, jasper_amd, datasets, dev, log)
 
     t0 = time.perf_counter()
     base = datasets.clustered(args.n, 128, 0)
@@ -275,6 +283,158 @@ def main() -> int:
     print(json.dumps(result), flush=True)
     g.free()
     return 0
+
+
+# ------------------------------------------------------------------ other rows
+
+def _timed(torch, fn, steps, warmup):
+    """Wall ms per call and HIP-event ms per call on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    out = None
+    for e0, e1 in evs:
+        e0.record(stream)
+        out = fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
+    ev_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    return wall_ms, ev_ms, out
+
+
+def _line(args, metric, value, unit, ms, dtype, config, roofline, higher=True):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": higher, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config, "roofline": roofline}
+
+
+def _recall(gt, ids):
+    hits = 0
+    for a, b in zip(gt, ids):
+        hits += len(set(a.tolist()) & set(b.tolist()))
+    return hits / (gt.shape[0] * gt.shape[1])
+
+
+def run_directional(args, torch, jasper_amd, datasets, dev, log, use_pq=False):
+    """Config 3: 1M x 96 unit vectors, IP, R=64, k_ranks=4 (u8 words),
+    prerotated; LSH (or PQ with M=4) directional search over 10k queries."""
+    n, nq, dim = args.n, args.nq, 96
+    t0 = time.perf_counter()
+    base = datasets.unit_sphere(n, dim, 0)
+    queries = datasets.unit_sphere(nq, dim, 1)
+    log(f"data in {time.perf_counter() - t0:.1f}s")
+    base_t = torch.from_numpy(base).to(dev)
+    q_t = torch.from_numpy(queries).to(dev)
+    t0 = time.perf_counter()
+    g = jasper_amd.Graph.build(base_t, n_neighbors=64, distance="ip", alpha=1.2, build_lsh=not use_pq,
+                               build_pq=use_pq, k_ranks=4, prerotate=True, lsh_samples=32768)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    log(f"directional build ({'pq' if use_pq else 'lsh'}) in {build_s:.2f}s")
+    gt_ids, _ = jasper_amd.generate_groundtruth(base_t, q_t, k=10, distance="ip")
+    gt = gt_ids.numpy()
+    fn = g.pq_search if use_pq else g.directional_search
+    sweep = [32, 48, 64, 96, 128] if args.sweep == "16,24,32,48,64,96,128,192,256" else \
+        [int(x) for x in args.sweep.split(",")]
+    curve, chosen = [], None
+    for bw in sweep:
+        ids, _ = fn(q_t, k=10, beam_width=bw)
+        r = _recall(gt, ids.cpu().numpy())
+        wall, ev, _ = _timed(torch, lambda: fn(q_t, k=10, beam_width=bw), 3, 1)
+        curve.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
+        log(f"bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+        if chosen is None and r >= args.target_recall:
+            chosen = bw
+    if chosen is None:
+        chosen = max(curve, key=lambda c: c["recall_at_10"])["beam_width"]
+    wall, ev, _ = _timed(torch, lambda: fn(q_t, k=10, beam_width=chosen), args.steps, args.warmup)
+    ids, _ = fn(q_t, k=10, beam_width=chosen)
+    rec = _recall(gt, ids.cpu().numpy())
+    st = g.directional_stats(q_t, k=10, beam_width=chosen, pq=use_pq).astype(np.int64)
+    dp, R = 96, 64
+    visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
+    # per edge: PQ reads M = 4 code bytes (IP: no norm gather); LSH K*P + 2 = 6 (u8 words + bf16 m^2)
+    per_edge = 4 if use_pq else 4 * 1 + 2
+    alg = int(visits * 2 * dp + hops + adj * (4 + per_edge) + nq * (2 * dp + 8 * 10))
+    ach = alg / (ev / 1000.0) / 1e9
+    kind = "pq_search" if use_pq else "directional_search"
+    res = _line(args, f"QPS @ recall@10, config 3 {kind} (1M x 96 unit vectors, IP, R=64, k_ranks=4, "
+                      "prerotated)", nq / (wall / 1000.0), "queries/s", wall, "f16",
+                {"workload": f"config 3: {n} x {dim} unit-norm N(0,1) fp16, IP, R=64 alpha=1.2, "
+                             f"{'PQ M=4' if use_pq else 'LSH k_ranks=4 u8 words'}, prerotate, {nq} queries, k=10",
+                 "beam_width": chosen, "recall_at_10": rec, "build_s": build_s,
+                 "build_vectors_per_s": n / build_s, "curve": curve},
+                {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
+                 "traffic": None, "kernel": f"directional_kernel<IP,{'PQ' if use_pq else 'LSH'}>",
+                 "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
+                 "per_query": {"visits": float(st[:, 0].mean()), "hops": float(st[:, 1].mean()),
+                               "adjacency_entries": float(st[:, 2].mean())}})
+    print(json.dumps(res), flush=True)
+    g.free()
+    return 0
+
+
+def run_pq(args, torch, jasper_amd, datasets, dev, log):
+    return run_directional(args, torch, jasper_amd, datasets, dev, log, use_pq=True)
+
+
+def run_bruteforce(args, torch, jasper_amd, datasets, dev, log):
+    """Exact k-NN of config 2's 10k queries over its 1M x 128 base."""
+    base = torch.from_numpy(datasets.clustered(args.n, 128, 0)).to(dev)
+    q = torch.from_numpy(datasets.clustered(args.nq, 128, 1)).to(dev)
+    wall, ev, _ = _timed(torch, lambda: jasper_amd.bruteforce_knn(base, q, 10, "l2"), args.steps, args.warmup)
+    flop = 2.0 * args.nq * args.n * 128
+    tf = flop / (ev / 1000.0) / 1e12
+    res = _line(args, "exact k-NN TFLOP/s (matrix cores), config 2", tf, "TFLOP/s", wall, "f16",
+                {"workload": f"config 2 ground truth: {args.nq} queries x {args.n} x 128 fp16, L2, k=10",
+                 "queries_per_s": args.nq / (wall / 1000.0)},
+                {"bound": "mfma", "achieved": tf, "peak": 2500.0, "unit": "TFLOP/s", "frac": tf / 2500.0,
+                 "traffic": None, "kernel": "bf_scan_kernel<8,L2> + bf_merge_kernel", "kernel_ms": ev,
+                 "algorithmic_flop_per_launch": flop})
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def run_rotate(args, torch, jasper_amd, datasets, dev, log):
+    """Prerotation of 1M x 128 fp16 rows (the construct-time GEMM)."""
+    x = torch.from_numpy(datasets.clustered(args.n, 128, 0)).to(dev)
+    wall, ev, _ = _timed(torch, lambda: jasper_amd.rotate(x, 42), args.steps, args.warmup)
+    nbytes = 4.0 * args.n * 128 + 2 * 128 * 128
+    gbs = nbytes / (ev / 1000.0) / 1e9
+    res = _line(args, "prerotation GB/s, 1M x 128 fp16", gbs, "GB/s", wall, "f16",
+                {"workload": f"{args.n} x 128 fp16 rows times a 128 x 128 fp16 rotation, fp32 accumulation",
+                 "tflops": 2.0 * args.n * 128 * 128 / (ev / 1000.0) / 1e12},
+                {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                 "traffic": None, "kernel": "rotate_mfma_kernel<4,true>", "kernel_ms": ev,
+                 "algorithmic_bytes_per_launch": nbytes})
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def run_rabitq(args, torch, jasper_amd, datasets, dev, log):
+    """One-bit RaBitQ codes of 1M x 128 fp16 rows (fp32 matrix cores)."""
+    x = torch.from_numpy(datasets.clustered(args.n, 128, 0)).to(dev)
+    rot = torch.from_numpy(jasper_amd.rotation_matrix(128, 42)).to(dev)
+    wall, ev, _ = _timed(torch, lambda: jasper_amd.rabitq_quantize(x, rotation=rot), args.steps, args.warmup)
+    flop = 2.0 * args.n * 128 * 128
+    tf = flop / (ev / 1000.0) / 1e12
+    res = _line(args, "RaBitQ one-bit quantize vectors/s, 1M x 128 fp16", args.n / (ev / 1000.0), "vectors/s",
+                wall, "f32",
+                {"workload": f"{args.n} x 128 fp16 rows, rotation 128 x 128 fp32, zero centroid, L2",
+                 "hbm_gbs": args.n * (256 + 24) / (ev / 1000.0) / 1e9},
+                {"bound": "mfma", "achieved": tf, "peak": 157.3, "unit": "TFLOP/s", "frac": tf / 157.3,
+                 "traffic": None, "kernel": "rabitq_kernel<8,true>", "kernel_ms": ev,
+                 "algorithmic_flop_per_launch": flop})
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+OTHER_PATHS = {"directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
+               "rotate": run_rotate, "rabitq": run_rabitq}
 
 
 if __name__ == "__main__":

@@ -160,7 +160,8 @@ int64_t jasperx_rotation_matrix(int64_t dim, int64_t seed, float* out);
  * P[k + i*dim] * x[r][k]) with fp32 accumulation (the prerotation of
  * include/jasper/index/construct.cuh:1068-1090 as an operator). x: n rows of
  * stride x_stride elements (device or host memory); out: device, stride
- * out_stride. Synchronises the stream before returning. */
+ * out_stride. Asynchronous on `stream` (matrices are cached per device, dim
+ * and seed). */
 int64_t jasperx_rotate_rows(int64_t dim, int64_t seed, const void* x, int64_t n, int64_t x_stride, void* out,
                             int64_t out_stride, void* stream);
 /* One-bit RaBitQ quantizer (include/jasper/rabitq/quantize.cuh:322-354,
@@ -185,6 +186,13 @@ int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, int64_t n, i
 int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t base_stride, const void* queries,
                                int64_t n_queries, int64_t query_stride, int64_t k, int32_t metric,
                                int32_t* out_ids, float* out_dists, void* stream);
+/* Measurement run of directional_search (use_pq = 0) or pq_search
+ * (use_pq = 1): the same traversal, writing per-query work counters to host
+ * memory out_stats[n_queries * 3] = {visits, hops expanded, adjacency
+ * entries read}. Not a search entry point. */
+int64_t jasperx_directional_stats(int64_t handle, int32_t use_pq, const void* queries, int64_t n_queries,
+                                  int64_t dim, int64_t k, int64_t beam_width, int64_t limit, uint32_t* out_stats,
+                                  void* stream);
 /* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 

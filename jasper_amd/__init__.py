@@ -89,6 +89,7 @@ _AGNOSTIC = {
     "jasperx_directional_query_rows": [_i64, _ptr, _i64, _i64, _ptr, _ptr],
     "jasperx_rotate_rows": [_i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr],
     "jasperx_rabitq_node_bytes": [_i64],
+    "jasperx_directional_stats": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr],
     "jasperx_bruteforce_knn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, ctypes.c_int32, _ptr, _ptr, _ptr],
     "jasperx_rabitq_quantize": [_ptr, ctypes.c_int32, _i64, _i64, _i64, _ptr, _ptr, ctypes.c_int32, _ptr, _ptr],
 }
@@ -508,6 +509,21 @@ class Graph:
         out = np.zeros((nq, dp), dtype=np.uint16)
         _agnostic("jasperx_directional_query_rows")(self._handle, _tensor_ptr(queries), nq, self._dim,
                                                     out.ctypes.data_as(_ptr), _stream_ptr(queries.device))
+        return out
+
+    def directional_stats(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
+                          limit: int | None = None, pq: bool = False) -> np.ndarray:
+        """Per-query work counters of directional_search (pq=False) or
+        pq_search (pq=True) [n_queries, 3]: visits, hops expanded, adjacency
+        entries read. A measurement extension."""
+        self._check_alive()
+        queries = self._query_check(queries)
+        nq = queries.size(0)
+        out = np.zeros((nq, 3), dtype=np.uint32)
+        lim = limit if limit is not None else 2 * beam_width
+        _agnostic("jasperx_directional_stats")(self._handle, 1 if pq else 0, _tensor_ptr(queries), nq, self._dim,
+                                               k, beam_width, lim, out.ctypes.data_as(_ptr),
+                                               _stream_ptr(queries.device))
         return out
 
     def export_lsh(self):

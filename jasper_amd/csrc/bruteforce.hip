@@ -9,8 +9,8 @@
 //
 // Phase 1 (bf_scan_kernel): one wave owns 32 queries and one chunk of the
 // base. It holds the A fragments of its queries in registers and walks the
-// chunk 64 vectors at a time (two 32x32 output tiles, K over the padded dim),
-// loading the next 64 vectors while the current ones are on the matrix cores.
+// chunk 32 vectors at a time (one 32x32 output tile, K over the padded dim),
+// loading the next 32 vectors while the current ones are on the matrix cores.
 // Work-groups of one chunk run side by side (query tile is the fast grid
 // index), so the chunk is read from HBM about once and served from L2 to the
 // other query tiles. A score enters a per-query candidate buffer in LDS only
@@ -32,7 +32,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kBfMaxK = 64;          // k the fused scan supports
-constexpr int kBfStep = 64;          // vectors per step = most keys a query can gain per step
+constexpr int kBfStep = 32;          // vectors per step = most keys a query can gain per step
 
 __device__ __forceinline__ half8 u4_as_h8(uint4 v) {
   half8 h;
@@ -108,63 +108,57 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
     af[s] = (aq < nq && c < nck) ? reinterpret_cast<const uint4*>(queries + (size_t)aq * dp)[c]
                                  : make_uint4(0, 0, 0, 0);
   }
-  // the query rows of this lane's accumulators: m = 8g + 4*(lane/32) + j
-  float qs[16];
-  uint64_t th[16];
+  // the query rows of this lane's accumulators: m = 8g + 4*(lane/32) + j.
+  // thd[r] is the distance of row r's current k-th key (+inf until known);
+  // a score passes the cheap test d <= thd[r] and then the exact key test.
+  float qs[16], thd[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t q = q0 + 8 * (r >> 2) + 4 * ah + (r & 3);
     qs[r] = (METRIC == kL2 && q < nq) ? qsq[q] : 0.0f;
-    th[r] = ~0ull;
+    thd[r] = __builtin_inff();
   }
 
-  uint4 na[KS], nb[KS];
+  // one 32-vector tile per step; the next tile's rows load while this one
+  // is on the matrix cores
+  uint4 nb[KS];
   auto load_step = [&](int64_t v0) {
-    const int64_t va = v0 + am, vb = v0 + 32 + am;
-    const uint4* ra = reinterpret_cast<const uint4*>(base + (size_t)(va < v_end ? va : v_begin) * dp);
-    const uint4* rb = reinterpret_cast<const uint4*>(base + (size_t)(vb < v_end ? vb : v_begin) * dp);
+    const int64_t v = v0 + am;
+    const uint4* rv = reinterpret_cast<const uint4*>(base + (size_t)(v < v_end ? v : v_begin) * dp);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const uint32_t c = (uint32_t)s * 2 + ah;
-      na[s] = (va < v_end && c < nck) ? ra[c] : make_uint4(0, 0, 0, 0);
-      nb[s] = (vb < v_end && c < nck) ? rb[c] : make_uint4(0, 0, 0, 0);
+      nb[s] = (v < v_end && c < nck) ? rv[c] : make_uint4(0, 0, 0, 0);
     }
   };
   if (v_begin < v_end) load_step(v_begin);
 
-  for (int64_t v0 = v_begin; v0 < v_end; v0 += 64) {
-    uint4 ca[KS], cb[KS];
+  for (int64_t v0 = v_begin; v0 < v_end; v0 += 32) {
+    uint4 cb[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      ca[s] = na[s];
-      cb[s] = nb[s];
-    }
-    if (v0 + 64 < v_end) load_step(v0 + 64);
-    float16v acc0 = {}, acc1 = {};
+    for (int s = 0; s < KS; ++s) cb[s] = nb[s];
+    if (v0 + 32 < v_end) load_step(v0 + 32);
+    float16v acc = {};
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[s]), u4_as_h8(ca[s]), acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[s]), u4_as_h8(cb[s]), acc1, 0, 0, 0);
-    }
+    for (int s = 0; s < KS; ++s)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[s]), u4_as_h8(cb[s]), acc, 0, 0, 0);
     // lane holds column n = lane % 32 (vector) and rows 8g + 4*(lane/32) + j
+    const int64_t v = v0 + am;
+    if (v < v_end) {
+      const float vs = METRIC == kL2 ? vsq[v] : 0.0f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int64_t v = v0 + 32 * h + am;
-      if (v < v_end) {
-        const float vs = METRIC == kL2 ? vsq[v] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float dot = h ? acc1[r] : acc0[r];
-          float d;
-          if constexpr (METRIC == kL2) {
-            d = (qs[r] + vs) - 2.0f * dot;
-            d = d < 0.0f ? 0.0f : d;
-          } else {
-            d = -__half2float(__float2half_rn(dot));
-          }
+      for (int r = 0; r < 16; ++r) {
+        float d;
+        if constexpr (METRIC == kL2) {
+          d = __builtin_fmaf(-2.0f, acc[r], qs[r] + vs);  // == (qs + vs) - 2 dot: 2 dot is exact
+        } else {
+          d = -__half2float(__float2half_rn(acc[r]));
+        }
+        if (d <= thd[r]) {
+          if constexpr (METRIC == kL2) d = d < 0.0f ? 0.0f : d;
+          const uint32_t m = 8u * (r >> 2) + 4u * ah + (r & 3);
           const uint64_t key = bf_key(d, (uint32_t)v);
-          if (key < th[r]) {
-            const uint32_t m = 8u * (r >> 2) + 4u * ah + (r & 3);
+          if (key < thr[m]) {
             const uint32_t slot = atomicAdd(&cnt[m], 1u);
             cand[m * cap + slot] = key;
           }
@@ -172,21 +166,26 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
       }
     }
     wave_sync();
-    // compact the buffers that could overflow in the next step (64 new keys at most)
+    // compact the buffers that could overflow in the next step (32 new keys at most)
     uint64_t full = ballot(lane < 32 && cnt[lane] > cap - kBfStep);
-    while (full) {
-      const uint32_t m = (uint32_t)__builtin_ctzll(full);
-      full &= full - 1;
-      uint64_t kth;
-      const uint32_t keep = bf_compact(cand + m * cap, cnt[m], k, scratch, &kth);
-      if (lane == 0) {
-        cnt[m] = keep;
-        thr[m] = kth;
+    if (full) {
+      while (full) {
+        const uint32_t m = (uint32_t)__builtin_ctzll(full);
+        full &= full - 1;
+        uint64_t kth;
+        const uint32_t keep = bf_compact(cand + m * cap, cnt[m], k, scratch, &kth);
+        if (lane == 0) {
+          cnt[m] = keep;
+          thr[m] = kth;
+        }
+        wave_sync();
       }
-      wave_sync();
-    }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) th[r] = thr[8u * (r >> 2) + 4u * ah + (r & 3)];
+      for (int r = 0; r < 16; ++r) {
+        const uint64_t t = thr[8u * (r >> 2) + 4u * ah + (r & 3)];
+        thd[r] = t == ~0ull ? __builtin_inff() : ord_to_dist((uint32_t)(t >> 32));
+      }
+    }
   }
   // final: best k of each query, sorted, padded with ~0
   for (uint32_t m = 0; m < 32; ++m) {
@@ -245,7 +244,7 @@ void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, cons
                        (const uint16_t*)queries, nq, dp, dim, qsq);
   }
   // chunks: about 8192 work-groups (single waves) in all, each chunk a
-  // multiple of 64 vectors
+  // multiple of 64 vectors (a whole number of 32-vector steps)
   const int64_t qtiles = (nq + 31) / 32;
   int64_t want = std::max<int64_t>(1, 8192 / qtiles);
   want = std::min<int64_t>(want, (n + 63) / 64);

@@ -7,6 +7,8 @@
 #include <cstdlib>
 #include <algorithm>
 #include <cstring>
+#include <map>
+#include <tuple>
 #include <exception>
 #include <memory>
 #include <mutex>
@@ -491,10 +493,20 @@ extern "C" int64_t jasperx_rotate_rows(int64_t dim, int64_t seed, const void* x,
   return guarded([&]() -> int64_t {
     if (dim <= 0 || dim > 65536) throw std::invalid_argument("dim must be in 1..65536");
     if (n < 0 || x_stride < dim || out_stride < dim) throw std::invalid_argument("bad row counts or strides");
-    auto r = make_rotation(rotation_matrix((uint32_t)dim, (uint64_t)seed), (uint32_t)dim);
+    // matrices are cached per (device, dim, seed): the Householder QR runs on the host
+    static std::mutex cache_mutex;
+    static std::map<std::tuple<int, int64_t, int64_t>, std::unique_ptr<RotationMatrix>> cache;
+    int device = 0;
+    hip_check(hipGetDevice(&device), "get device");
+    const RotationMatrix* r = nullptr;
+    {
+      std::lock_guard<std::mutex> lock(cache_mutex);
+      auto& slot = cache[std::make_tuple(device, dim, seed)];
+      if (!slot) slot = make_rotation(rotation_matrix((uint32_t)dim, (uint64_t)seed), (uint32_t)dim);
+      r = slot.get();
+    }
     hipStream_t s = (hipStream_t)stream;
     rotate_rows_any(*r, x, n, x_stride, out, out_stride, s);
-    hip_check(hipStreamSynchronize(s), "rotation");
     return 0;
   });
 }
@@ -531,6 +543,36 @@ extern "C" int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t d
     if (((uintptr_t)base & 15u) || ((uintptr_t)queries & 15u)) throw std::invalid_argument("rows must be 16-byte aligned");
     bruteforce_knn(base, n, (uint32_t)dim, (uint32_t)base_stride, queries, nq, (uint32_t)k, metric, out_ids,
                    out_dists, (hipStream_t)stream);
+    return 0;
+  });
+}
+
+extern "C" int64_t jasperx_directional_stats(int64_t h, int32_t use_pq, const void* q, int64_t nq, int64_t dim,
+                                             int64_t k, int64_t bw, int64_t limit, uint32_t* out_stats,
+                                             void* stream) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (nq <= 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    int32_t* ids = nullptr;
+    float* d = nullptr;
+    uint32_t* st = nullptr;
+    hip_check(hipMalloc(&ids, (size_t)nq * k * 4), "alloc ids");
+    hip_check(hipMalloc(&d, (size_t)nq * k * 4), "alloc dists");
+    hip_check(hipMalloc(&st, (size_t)nq * 12), "alloc stats");
+    try {
+      directional_search(g, use_pq != 0, q, nq, dim, ids, d, k, bw, limit, false, s, st);
+      hip_check(hipMemcpyAsync(out_stats, st, (size_t)nq * 12, hipMemcpyDeviceToHost, s), "download stats");
+      hip_check(hipStreamSynchronize(s), "sync stats");
+    } catch (...) {
+      (void)hipFree(ids);
+      (void)hipFree(d);
+      (void)hipFree(st);
+      throw;
+    }
+    (void)hipFree(ids);
+    (void)hipFree(d);
+    (void)hipFree(st);
     return 0;
   });
 }

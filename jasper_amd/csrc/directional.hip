@@ -449,6 +449,8 @@ struct DirArgs {
   const float* centroids;
   const uint8_t* codes;
   const float* norms;
+  // optional work counters per query: {visits, hops expanded, adjacency entries}
+  uint32_t* stats;
 };
 
 // Exact distance of the popped node (compute_qu_diff_and_exact,
@@ -541,7 +543,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   uint64_t* B = buf0;
   uint64_t* NB = buf1;
   if (lane == 0) B[0] = make_key(0.0f, a.medoid);
-  uint32_t cnt = 1, fc = 0, vc = 0, loop = 0;
+  uint32_t cnt = 1, fc = 0, vc = 0, loop = 0, n_hops = 0, n_adj = 0;
   wave_sync();
   while (loop <= a.limit) {
     loop += 1;
@@ -594,6 +596,8 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
 
     // expand u and estimate its neighbours (no neighbour vector fetches)
     const uint32_t deg = min((uint32_t)a.counts[u], a.R);
+    n_hops += 1;
+    n_adj += deg;
     uint64_t t = kEmptyKey;
     if (lane < deg) {
       const uint32_t v = a.edges[(size_t)u * a.R + lane];
@@ -680,6 +684,11 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     wave_sync();
   }
 
+  if (a.stats && lane == 0) {
+    a.stats[(size_t)qid * 3] = vc;
+    a.stats[(size_t)qid * 3 + 1] = n_hops;
+    a.stats[(size_t)qid * 3 + 2] = n_adj;
+  }
   // output: F in order, skipping invalid / deleted, pad (0x7FFFFFFF, FLT_MAX)
   // (graph_beam_search.cuh:246-266)
   wave_sync();
@@ -888,7 +897,8 @@ void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t
 }
 
 void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
-                        float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream) {
+                        float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
+                        uint32_t* stats) {
   if (use_pq && !g.pq) throw std::runtime_error("graph has no PQ artifacts built — call build_pq() first");
   if (!use_pq && !g.lsh) throw std::runtime_error("graph has no LSH artifacts built — call build_lsh() first");
   if (dim != (int64_t)g.dim)
@@ -917,6 +927,7 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
   a.max_result = 2048;
   a.out_ids = out_ids;
   a.out_dists = out_dists;
+  a.stats = stats;
   size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
   if (use_pq) {
     a.M = g.pq->m;

@@ -106,6 +106,68 @@ __global__ __launch_bounds__(256) void rotate_mfma_kernel(const uint16_t* __rest
   }
 }
 
+// The common case (P and four 16-row output tiles fit in LDS): every wave of
+// the block iterates the same number of times, so block barriers are safe.
+// Each wave rounds its 16 x dim results to fp16 into an LDS tile (row stride
+// dp_out + 8 halves, 16-byte aligned, 2-way bank conflicts at most), then
+// writes whole rows with 16-byte stores.
+template <int KS>
+__global__ __launch_bounds__(256) void rotate_tile_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t dp_in,
+                                                          const uint16_t* __restrict__ pt, uint32_t kp,
+                                                          uint32_t dim, uint16_t* __restrict__ out,
+                                                          uint32_t dp_out) {
+  extern __shared__ uint4 lds4[];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t mp = (dim + 15u) & ~15u;
+  const uint32_t kc = kp / 8;
+  const uint32_t ostride = dp_out + 8;  // halves
+  uint4* pt_lds = lds4;
+  uint16_t* otile = reinterpret_cast<uint16_t*>(lds4 + (size_t)mp * kc) + (size_t)wave * 16 * ostride;
+  const uint4* ptg = reinterpret_cast<const uint4*>(pt);
+  for (uint32_t i = threadIdx.x; i < mp * kc; i += blockDim.x) pt_lds[i] = ptg[i];
+  __syncthreads();
+  const uint32_t col = lane & 15u, kq = lane >> 4;
+  const uint32_t in_chunks = dp_in / 8, out_chunks = dp_out / 8;
+  const int64_t tiles = (n + 15) / 16;
+  for (int64_t tb = (int64_t)blockIdx.x * 4; tb < tiles; tb += (int64_t)gridDim.x * 4) {
+    const int64_t tile = tb + wave;
+    const int64_t row = tile * 16 + col;
+    const bool row_ok = row < n;
+    const uint4* xr = reinterpret_cast<const uint4*>(x) + (size_t)(row_ok ? row : 0) * in_chunks;
+    uint4 xf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t c = (uint32_t)s * 4 + kq;
+      xf[s] = (row_ok && c < in_chunks) ? xr[c] : make_uint4(0, 0, 0, 0);
+    }
+    for (uint32_t m0 = 0; m0 < mp; m0 += 16) {
+      float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint4 pf = pt_lds[(size_t)(m0 + col) * kc + (uint32_t)s * 4 + kq];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(pf), as_half8(xf[s]), acc, 0, 0, 0);
+      }
+      const uint32_t i0 = m0 + 4 * kq;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i0 + j < dp_out) otile[col * ostride + i0 + j] = __half_as_ushort(__float2half_rn(acc[j]));
+    }
+    __syncthreads();
+    const int64_t row0 = tile * 16;
+    for (uint32_t idx = lane; idx < 16 * out_chunks; idx += 64) {
+      const uint32_t r = idx / out_chunks, c = idx % out_chunks;
+      if (row0 + r < n) {
+        // output columns in [mp, dp_out) never reach here (dp_out <= mp); zero-fill above dim came from
+        // the zero rows of Pt
+        reinterpret_cast<uint4*>(out + (size_t)(row0 + r) * dp_out)[c] =
+            *reinterpret_cast<const uint4*>(otile + r * ostride + c * 8);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // Zero the output pad columns [dim, dp_out) that the tiles do not cover.
 __global__ void clear_pad_kernel(uint16_t* out, int64_t n, uint32_t mp, uint32_t dp_out) {
   const uint32_t w = dp_out - mp;
@@ -192,7 +254,22 @@ void rotate_rows(const RotationMatrix& r, const void* x, int64_t n, uint32_t dp_
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), shm, s, xi, n, dp_in, (const uint16_t*)r.pt, r.kp, r.dim, o,
                        dp_out);
   };
-  if (use_lds) {
+  const size_t tile_lds = lds + (size_t)4 * 16 * (dp_out + 8) * 2;
+  if (tile_lds <= 64 * 1024 && dp_out <= r.mp && ks <= 6) {
+    const uint32_t g2 = (uint32_t)std::min<int64_t>((tiles + 3) / 4, 1024);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(g2), dim3(256), tile_lds, s, xi, n, dp_in, (const uint16_t*)r.pt, r.kp, r.dim,
+                         o, dp_out);
+    };
+    switch (ks) {
+      case 1: go(rotate_tile_kernel<1>); break;
+      case 2: go(rotate_tile_kernel<2>); break;
+      case 3: go(rotate_tile_kernel<3>); break;
+      case 4: go(rotate_tile_kernel<4>); break;
+      case 5: go(rotate_tile_kernel<5>); break;
+      default: go(rotate_tile_kernel<6>); break;
+    }
+  } else if (use_lds) {
     switch (ks) {
       case 1: launch(rotate_mfma_kernel<1, true>, lds); break;
       case 2: launch(rotate_mfma_kernel<2, true>, lds); break;
