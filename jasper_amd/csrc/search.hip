@@ -24,6 +24,7 @@
 #include "search.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace jasper_amd {
 
@@ -256,10 +257,19 @@ __global__ __launch_bounds__(64) void beam_search_kernel(SearchArgs a) {
 }
 
 static uint32_t default_hash_bits(uint32_t bw) {
-  if (bw <= 32) return 10;
-  if (bw <= 64) return 11;
-  if (bw <= 128) return 12;
-  return 13;
+  // JASPER_SEARCH_HASH_BITS (8..15) overrides the size of the per-query seen
+  // cache for tuning; the results do not depend on it.
+  static const int override_bits = [] {
+    const char* e = std::getenv("JASPER_SEARCH_HASH_BITS");
+    const int v = e ? std::atoi(e) : 0;
+    return (v >= 8 && v <= 15) ? v : 0;
+  }();
+  if (override_bits) return (uint32_t)override_bits;
+  // measured on config 2 at bw 32..64: 2^10 entries beat 2^9 (more re-scoring)
+  // and 2^11..2^12 (fewer resident waves)
+  if (bw <= 64) return 10;
+  if (bw <= 128) return 11;
+  return 12;
 }
 
 size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {
