@@ -108,10 +108,9 @@ __device__ __forceinline__ uint64_t wave_bitonic_sort(uint64_t x) {
       const uint64_t o = shfl_xor64(x, j);
       const bool up = (lane & (uint32_t)k) == 0;
       const bool lower = (lane & (uint32_t)j) == 0;
-      const bool take_min = (lower == up);
-      const uint64_t mn = x < o ? x : o;
-      const uint64_t mx = x < o ? o : x;
-      x = take_min ? mn : mx;
+      // keep min when (lower == up), else max: take the partner exactly
+      // when (o < x) agrees with "keep min" (equal keys are interchangeable)
+      x = ((o < x) == (lower == up)) ? o : x;
     }
   }
   return x;
@@ -264,6 +263,46 @@ __device__ __forceinline__ float quad_partial(const float (&qf)[CPL * 8], const 
         const uint32_t base = 8u * (uint32_t)c;
         if (base + e0 < nlimit) acc = __builtin_fmaf(qf[2 * c], v0, acc);
         if (base + e1 < nlimit) acc = __builtin_fmaf(qf[2 * c + 1], v1, acc);
+      }
+    }
+  }
+  return acc;
+}
+
+// f32(a) - f32(b) for the low (or high) fp16 halves of two words, rounded
+// once: v_fma_mix_f32 converts the fp16 operands inside the instruction and
+// computes a * 1.0 + (-b) exactly before rounding, which is the fp32
+// subtraction of the converted values bit for bit, subnormals included.
+__device__ __forceinline__ float mix_diff_lo(uint32_t a, uint32_t b) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[1,0,1]" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ __forceinline__ float mix_diff_hi(uint32_t a, uint32_t b) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
+// L2 lane partial with the query fragment kept as fp16 chunks (the lane's
+// chunks ql, ql+4, ... as load_row_frag reads them): the same accumulation
+// order as quad_partial<CPL, kL2>, two VALU operations per element.
+template <int CPL>
+__device__ __forceinline__ float quad_partial_l2h(const uint4 (&qh)[CPL], const uint4 (&x)[CPL], uint32_t ql,
+                                                  uint32_t nlimit) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const uint32_t c = ql + 4u * (uint32_t)t;
+    if (c < nlimit) {
+      const uint32_t qw[4] = {qh[t].x, qh[t].y, qh[t].z, qh[t].w};
+      const uint32_t w[4] = {x[t].x, x[t].y, x[t].z, x[t].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float d0 = mix_diff_lo(qw[k], w[k]);
+        acc = __builtin_fmaf(d0, d0, acc);
+        const float d1 = mix_diff_hi(qw[k], w[k]);
+        acc = __builtin_fmaf(d1, d1, acc);
       }
     }
   }

@@ -54,10 +54,34 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t v, uint32_t bits) {
   return (v * 0x9E3779B1u) >> (32u - bits);
 }
 
+// The query fragment of a quad lane: fp16 chunks for L2 (converted inside
+// v_fma_mix_f32), fp32 elements for IP (quad_partial's broadcast layout).
+template <int CPL, int METRIC>
+struct QueryFrag {
+  float f[CPL * 8];
+};
+template <int CPL>
+struct QueryFrag<CPL, kL2> {
+  uint4 h[CPL];
+};
+
+template <int CPL, int METRIC>
+__device__ __forceinline__ void load_query(const uint4* qrow, uint32_t ql, uint32_t nchunks, QueryFrag<CPL, METRIC>& q) {
+  if constexpr (METRIC == kL2) load_row_frag<CPL>(qrow, ql, nchunks, true, q.h);
+  else load_query_frag<CPL, METRIC>(qrow, ql, nchunks, q.f);
+}
+
+template <int CPL, int METRIC>
+__device__ __forceinline__ float score(const QueryFrag<CPL, METRIC>& q, const uint4 (&x)[CPL], uint32_t ql,
+                                       uint32_t nlimit) {
+  if constexpr (METRIC == kL2) return quad_finish<METRIC>(quad_partial_l2h<CPL>(q.h, x, ql, nlimit));
+  else return quad_finish<METRIC>(quad_partial<CPL, METRIC>(q.f, x, ql, nlimit));
+}
+
 // Scores up to 16 (or 32 with TWO) candidate rows listed in cand[base..)
 // and stores their keys into T[j].
 template <int CPL, int METRIC, bool TWO>
-__device__ __forceinline__ void score_pass(const SearchArgs& a, const float (&qf)[CPL * 8], const uint32_t* cand,
+__device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<CPL, METRIC>& qf, const uint32_t* cand,
                                            uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql, uint32_t qg) {
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
   const uint32_t j0 = base + qg;
@@ -71,12 +95,12 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const float (&qf
     const uint32_t v1 = act1 ? cand[j1] : 0u;
     uint4 x1[CPL];
     load_row_frag<CPL>(a.vecs + (size_t)v1 * a.nchunks, ql, a.nchunks, act1, x1);
-    const float d0 = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x0, ql, nlimit));
-    const float d1 = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x1, ql, nlimit));
+    const float d0 = score<CPL, METRIC>(qf, x0, ql, nlimit);
+    const float d1 = score<CPL, METRIC>(qf, x1, ql, nlimit);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
     if (ql == 0 && act1) T[j1] = make_key(d1, v1);
   } else {
-    const float d0 = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x0, ql, nlimit));
+    const float d0 = score<CPL, METRIC>(qf, x0, ql, nlimit);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
   }
 }
@@ -98,8 +122,8 @@ __global__ __launch_bounds__(64) void beam_search_kernel(SearchArgs a) {
   const uint32_t ql = lane & 3u, qg = lane >> 2;
   const uint4* qrow = a.use_range ? a.vecs + (size_t)(a.q_start + qid) * a.nchunks
                                   : a.queries + (size_t)qid * a.nchunks;
-  float qf[CPL * 8];
-  load_query_frag<CPL, METRIC>(qrow, ql, a.nchunks, qf);
+  QueryFrag<CPL, METRIC> qf;
+  load_query<CPL, METRIC>(qrow, ql, a.nchunks, qf);
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
 
   // B = [(medoid, d(q, medoid))]
@@ -107,7 +131,7 @@ __global__ __launch_bounds__(64) void beam_search_kernel(SearchArgs a) {
   {
     uint4 x[CPL];
     load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
-    const float d = quad_finish<METRIC>(quad_partial<CPL, METRIC>(qf, x, ql, nlimit));
+    const float d = score<CPL, METRIC>(qf, x, ql, nlimit);
     wave_sync();  // hash table initialised
     if (lane == 0) {
       buf0[0] = make_key(d, a.medoid);

@@ -118,3 +118,18 @@ def test_search_rejects_oversized_beam(jasper, c1_small, tmp_path):
     gg = _load(jasper, g, tmp_path)
     with pytest.raises(ValueError):
         gg.search(torch.from_numpy(q).cuda(), k=10, beam_width=1990)
+
+
+def test_search_matches_oracle_subnormal_range(jasper, oracle_lib, tmp_path):
+    """Values in the fp16 subnormal range exercise the in-instruction fp16
+    conversion of the L2 scoring (and the oracle's exact conversions)."""
+    base = gaussian(1500, 64, 50) * 3e-5
+    q = gaussian(40, 64, 51) * 3e-5
+    assert (np.abs(base.astype(np.float16)) < 6.1e-5).mean() > 0.5
+    g = oracle.build(base, R=16, distance="l2", alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    for bw in (16, 64):
+        ids, d = _run(jasper, gg, q, 10, bw)
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
