@@ -192,18 +192,16 @@ __global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
     wave_sync();
     // d(w, v) for every source (compute_distance(src_vec = w, sink_vec = v))
     float wf[CPL * 8];
-    {
-      uint4 xw[CPL];
-      load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
-      frag_from_rows<CPL, METRIC>(xw, ql, wf);
-    }
+    uint4 xw[CPL];
+    load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
+    if constexpr (METRIC != kL2) frag_from_rows<CPL, METRIC>(xw, ql, wf);
     for (uint32_t base = 0; base < taken; base += 16) {
       const uint32_t j = base + qg;
       const bool act = j < taken;
       const uint32_t sid = act ? l.srcs[j] : 0u;
       uint4 xs[CPL];
       load_row_frag<CPL>(a.pc.vecs + (size_t)sid * a.pc.nchunks, ql, a.pc.nchunks, act, xs);
-      const float d = quad_finish<METRIC>(quad_partial<CPL, METRIC>(wf, xs, ql, a.pc.nlimit));
+      const float d = pair_distance<CPL, METRIC>(xw, wf, xs, ql, a.pc.nlimit);
       if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
     }
     wave_sync();

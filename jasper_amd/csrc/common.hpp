@@ -79,13 +79,36 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
 // LDS visibility between lanes of the one wave that owns a work-group.
 __device__ __forceinline__ void wave_sync() { __syncthreads(); }
 
-__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) { return __shfl_xor(v, m, 64); }
+// Value of lane (lane ^ J). Masks 1 and 2 are DPP quad permutations, 4..16
+// ds_swizzle swaps (no address operand), 32 a v_permlane32_swap; none goes
+// through LDS memory.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  static_assert(J == 1 || J == 2 || J == 4 || J == 8 || J == 16 || J == 32, "xor mask");
+  if constexpr (J == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+  else if constexpr (J == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+  else if constexpr (J < 32) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (J << 10));
+  else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __lane_id() < 32 ? r[1] : r[0];
+  }
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  return (uint64_t)xor_lane<J>((uint32_t)v) | ((uint64_t)xor_lane<J>((uint32_t)(v >> 32)) << 32);
+}
+
+template <int J>
+__device__ __forceinline__ float xor_lane_f(float v) {
+  return __uint_as_float(xor_lane<J>(__float_as_uint(v)));
+}
 
 // Quad butterfly (offset 2, then 1): every lane of the quad gets
 // (l0 + l2) + (l1 + l3), the combine order of cg::reduce over a 4-lane tile.
 __device__ __forceinline__ float quad_sum(float v) {
-  v = v + __shfl_xor(v, 2, 64);
-  v = v + __shfl_xor(v, 1, 64);
+  v = v + xor_lane_f<2>(v);
+  v = v + xor_lane_f<1>(v);
   return v;
 }
 
@@ -96,23 +119,31 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, false);
 }
 
+// One compare-exchange stage of a bitonic sort: partner lane ^ J, blocks of
+// K lanes alternate direction. Keep the min when (lower == up), else the
+// max: take the partner exactly when (o < x) agrees with "keep min" (equal
+// keys are interchangeable).
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_stage(uint64_t x, uint32_t lane) {
+  const uint64_t o = xor_lane64<J>(x);
+  const bool up = (lane & (uint32_t)K) == 0;
+  const bool lower = (lane & (uint32_t)J) == 0;
+  return ((o < x) == (lower == up)) ? o : x;
+}
+
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_merge_steps(uint64_t x, uint32_t lane) {
+  x = bitonic_stage<K, J>(x, lane);
+  if constexpr (J > 1) x = bitonic_merge_steps<K, J / 2>(x, lane);
+  return x;
+}
+
 // Ascending bitonic sort of one key per lane over aligned blocks of W lanes
 // (W a power of two <= 64); lanes of other blocks are sorted independently.
-template <int W>
+template <int W, int K = 2>
 __device__ __forceinline__ uint64_t wave_bitonic_sort(uint64_t x) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int k = 2; k <= W; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const uint64_t o = shfl_xor64(x, j);
-      const bool up = (lane & (uint32_t)k) == 0;
-      const bool lower = (lane & (uint32_t)j) == 0;
-      // keep min when (lower == up), else max: take the partner exactly
-      // when (o < x) agrees with "keep min" (equal keys are interchangeable)
-      x = ((o < x) == (lower == up)) ? o : x;
-    }
-  }
+  x = bitonic_merge_steps<K, K / 2>(x, lane_id());
+  if constexpr (K < W) x = wave_bitonic_sort<W, K * 2>(x);
   return x;
 }
 
@@ -205,15 +236,17 @@ __device__ __forceinline__ void load_query_frag(const uint4* src, uint32_t ql, u
   }
 }
 
-// Issue the chunk loads of one vector row for quad lane ql.
+// Issue the chunk loads of one vector row for quad lane ql. Every lane loads
+// (inactive lanes pass a valid row and ignore the result), and a chunk past
+// the row's end re-reads chunk 0: the partial sums skip chunks >= their
+// limit, so no masking or zero-fill is needed.
 template <int CPL>
-__device__ __forceinline__ void load_row_frag(const uint4* row, uint32_t ql, uint32_t nchunks, bool active,
+__device__ __forceinline__ void load_row_frag(const uint4* row, uint32_t ql, uint32_t nchunks, bool /*active*/,
                                               uint4 (&x)[CPL]) {
 #pragma unroll
   for (int t = 0; t < CPL; ++t) {
     const uint32_t c = ql + 4u * (uint32_t)t;
-    x[t] = make_uint4(0, 0, 0, 0);
-    if (active && c < nchunks) x[t] = row[c];
+    x[t] = row[c < nchunks ? c : 0u];
   }
 }
 

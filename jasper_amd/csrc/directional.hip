@@ -72,8 +72,11 @@ __device__ __forceinline__ float h2f16(uint16_t h) { return __half2float(__ushor
 
 // 32-lane xor butterfly inside each half of the wave.
 __device__ __forceinline__ float warp32_sum(float v) {
-#pragma unroll
-  for (int d = 16; d > 0; d >>= 1) v = v + __shfl_xor(v, d, 64);
+  v = v + xor_lane_f<16>(v);
+  v = v + xor_lane_f<8>(v);
+  v = v + xor_lane_f<4>(v);
+  v = v + xor_lane_f<2>(v);
+  v = v + xor_lane_f<1>(v);
   return v;
 }
 

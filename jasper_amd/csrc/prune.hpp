@@ -64,6 +64,15 @@ __device__ __forceinline__ void frag_from_rows(const uint4 (&x)[CPL], uint32_t q
   }
 }
 
+// Distance between a left row (fp16 chunks xl; for IP also its fp32 layout
+// fl) and a right row xr, in the reference's per-lane order.
+template <int CPL, int METRIC>
+__device__ __forceinline__ float pair_distance(const uint4 (&xl)[CPL], const float (&fl)[CPL * 8],
+                                               const uint4 (&xr)[CPL], uint32_t ql, uint32_t nlimit) {
+  if constexpr (METRIC == kL2) return quad_finish<METRIC>(quad_partial_l2h<CPL>(xl, xr, ql, nlimit));
+  else return quad_finish<METRIC>(quad_partial<CPL, METRIC>(fl, xr, ql, nlimit));
+}
+
 template <int CPL>
 __device__ __forceinline__ void load_cache_frag(const uint4* cache_row, uint32_t ql, uint32_t nchunks,
                                                 uint4 (&x)[CPL]) {
@@ -92,14 +101,14 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     uint4 xc[CPL];
     load_row_frag<CPL>(p.vecs + (size_t)(valid ? cid : 0u) * p.nchunks, ql, p.nchunks, valid, xc);
     float cf[CPL * 8];
-    frag_from_rows<CPL, METRIC>(xc, ql, cf);
+    if constexpr (METRIC != kL2) frag_from_rows<CPL, METRIC>(xc, ql, cf);
     bool pruned = false;
     // members selected before this block
     const uint32_t ns0 = ns;
     for (uint32_t s = 0; s < ns0; ++s) {
       uint4 xs[CPL];
       load_cache_frag<CPL>(Scache + (size_t)s * p.nchunks, ql, p.nchunks, xs);
-      const float d = quad_finish<METRIC>(quad_partial<CPL, METRIC>(cf, xs, ql, p.nlimit));
+      const float d = pair_distance<CPL, METRIC>(xc, cf, xs, ql, p.nlimit);
       if (d * p.alpha < cd) pruned = true;
       if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
     }
@@ -121,7 +130,7 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
       wave_sync();
       uint4 xs[CPL];
       load_cache_frag<CPL>(Scache + (size_t)ns * p.nchunks, ql, p.nchunks, xs);
-      const float d = quad_finish<METRIC>(quad_partial<CPL, METRIC>(cf, xs, ql, p.nlimit));
+      const float d = pair_distance<CPL, METRIC>(xc, cf, xs, ql, p.nlimit);
       if (qg > g && d * p.alpha < cd) pruned = true;
       ns += 1;
       live = ballot(valid && !pruned && ql == 0 && qg > g);

@@ -105,8 +105,15 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<
   }
 }
 
+// At dim <= 128 with L2 the registers fit six waves per SIMD (the LDS of a
+// query at bw <= 64 is about 5.6 KB, so registers decide the occupancy).
+template <int CPL, int METRIC>
+constexpr int search_waves_per_simd() {
+  return (CPL <= 4 && METRIC == kL2) ? 6 : 1;
+}
+
 template <int CPL, int METRIC, bool STATS>
-__global__ __launch_bounds__(64) void beam_search_kernel(SearchArgs a) {
+__global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void beam_search_kernel(SearchArgs a) {
   extern __shared__ uint64_t smem[];
   const uint32_t lane = threadIdx.x;
   const uint32_t qid = blockIdx.x;
