@@ -123,12 +123,29 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
 // K lanes alternate direction. Keep the min when (lower == up), else the
 // max: take the partner exactly when (o < x) agrees with "keep min" (equal
 // keys are interchangeable).
+// Lanes that keep the minimum in stage (K, J): ((l & K) == 0) == ((l & J) == 0).
+constexpr uint64_t bitonic_min_lanes(int K, int J) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if (((l & K) == 0) == ((l & J) == 0)) m |= 1ull << l;
+  return m;
+}
+
+// Per-lane select by a wave-uniform lane mask held in SGPRs: bit set -> b.
+__device__ __forceinline__ uint32_t select_by_mask(uint32_t a, uint32_t b, uint64_t mask) {
+  uint32_t r;
+  asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+  return r;
+}
+
 template <int K, int J>
-__device__ __forceinline__ uint64_t bitonic_stage(uint64_t x, uint32_t lane) {
+__device__ __forceinline__ uint64_t bitonic_stage(uint64_t x, uint32_t /*lane*/) {
   const uint64_t o = xor_lane64<J>(x);
-  const bool up = (lane & (uint32_t)K) == 0;
-  const bool lower = (lane & (uint32_t)J) == 0;
-  return ((o < x) == (lower == up)) ? o : x;
+  // take the partner where (o < x) agrees with "keep the minimum"
+  const uint64_t take = ~(ballot(o < x) ^ bitonic_min_lanes(K, J));
+  const uint32_t lo = select_by_mask((uint32_t)x, (uint32_t)o, take);
+  const uint32_t hi = select_by_mask((uint32_t)(x >> 32), (uint32_t)(o >> 32), take);
+  return (uint64_t)lo | ((uint64_t)hi << 32);
 }
 
 template <int K, int J>
