@@ -79,18 +79,32 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
 // LDS visibility between lanes of the one wave that owns a work-group.
 __device__ __forceinline__ void wave_sync() { __syncthreads(); }
 
-// Value of lane (lane ^ J). Masks 1 and 2 are DPP quad permutations, 4..16
-// ds_swizzle swaps (no address operand), 32 a v_permlane32_swap; none goes
-// through LDS memory.
+// Per-lane select by a wave-uniform lane mask held in SGPRs: bit set -> b.
+__device__ __forceinline__ uint32_t select_by_mask(uint32_t a, uint32_t b, uint64_t mask) {
+  uint32_t r;
+  asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+  return r;
+}
+
+// Value of lane (lane ^ J), without the LDS crossbar: xor 1 and 2 are DPP
+// quad permutations, xor 4 a row half-mirror followed by a quad mirror,
+// xor 8 a row rotation by 8, xor 16 and 32 v_permlane16/32_swap.
 template <int J>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
   static_assert(J == 1 || J == 2 || J == 4 || J == 8 || J == 16 || J == 32, "xor mask");
   if constexpr (J == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
   else if constexpr (J == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
-  else if constexpr (J < 32) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (J << 10));
-  else {
+  else if constexpr (J == 4) {
+    const int m8 = __builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);  // row_half_mirror: i <-> 7 - i
+    return (uint32_t)__builtin_amdgcn_mov_dpp(m8, 0x1B, 0xF, 0xF, false);    // quad_perm [3,2,1,0]
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return select_by_mask(r[1], r[0], 0xFFFF0000FFFF0000ull);
+  } else {
     const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return __lane_id() < 32 ? r[1] : r[0];
+    return select_by_mask(r[1], r[0], 0xFFFFFFFF00000000ull);
   }
 }
 
@@ -129,13 +143,6 @@ constexpr uint64_t bitonic_min_lanes(int K, int J) {
   for (int l = 0; l < 64; ++l)
     if (((l & K) == 0) == ((l & J) == 0)) m |= 1ull << l;
   return m;
-}
-
-// Per-lane select by a wave-uniform lane mask held in SGPRs: bit set -> b.
-__device__ __forceinline__ uint32_t select_by_mask(uint32_t a, uint32_t b, uint64_t mask) {
-  uint32_t r;
-  asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
-  return r;
 }
 
 template <int K, int J>
