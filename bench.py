@@ -119,11 +119,13 @@ def main() -> int:
                     help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--path", default="search",
-                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq"],
+                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c5"],
                     help="search (default, the headline metric) or one of the other hot-path rows, each "
                          "printing its own JSON line: directional (config 3, LSH), pq (PQ-ADC on "
                          "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
-                         "rabitq (one-bit codes)")
+                         "rabitq (one-bit codes), c5 (config 5: 100M x 128 in-HBM build + LSH k=16 "
+                         "directional search)")
+    ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -433,7 +435,88 @@ def run_rabitq(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
-OTHER_PATHS = {"directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
+def run_c5(args, torch, jasper_amd, datasets, dev, log):
+    """Config 5: 100M x 128 clustered integer vectors (10,000 clusters)
+    generated in HBM, R=64, alpha=1.2, prerotated, LSH k_ranks=16 (u8 words),
+    32768 samples; RaBitQ one-bit codes of the base; 10k queries, k=10,
+    directional search, QPS at recall@10 >= 0.9."""
+    n, nq, dim = args.c5_n, args.nq, 128
+    t0 = time.perf_counter()
+    base = datasets.clustered_device(n, dim, 0, dev)
+    queries = datasets.clustered_device(nq, dim, 1, dev)
+    torch.cuda.synchronize()
+    log(f"c5 data {n} x {dim} generated in HBM in {time.perf_counter() - t0:.1f}s")
+    cfg = jasper_amd._resolve_directional_config(jasper_amd.DataType.FLOAT16, 64, jasper_amd.DistanceFunc.L2,
+                                                  16, dim)
+    stream = jasper_amd._stream_ptr(dev)
+    t0 = time.perf_counter()
+    handle = jasper_amd._op("construct_directional", cfg)(
+        jasper_amd._tensor_ptr(base), n, dim, 1.2, jasper_amd.parse_storage_size("10GB"), False, True, 42, stream)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    bst = jasper_amd.last_build_stats()
+    log(f"c5 construct (prerotation + Vamana) {build_s:.1f}s = {n / build_s:,.0f} vec/s, "
+        f"batches={int(bst['batches'])} max_batch={int(bst['max_batch'])}")
+    t0 = time.perf_counter()
+    jasper_amd._op("build_lsh", cfg)(handle, 32768, 42)
+    torch.cuda.synchronize()
+    lsh_s = time.perf_counter() - t0
+    log(f"c5 LSH artifacts {lsh_s:.1f}s")
+    g = jasper_amd.Graph(handle, cfg, jasper_amd.DataType.FLOAT16, jasper_amd.DistanceFunc.L2, 64, dim,
+                         is_directional=True, k_ranks=16, has_lsh=True, has_pq=False, prerotate=True,
+                         prerotate_seed=42)
+    rot = torch.from_numpy(jasper_amd.rotation_matrix(dim, 42)).to(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    codes = jasper_amd.rabitq_quantize(base, rotation=rot)
+    torch.cuda.synchronize()
+    rabitq_s = time.perf_counter() - t0
+    del codes
+    log(f"c5 RaBitQ one-bit codes {rabitq_s:.2f}s")
+    t0 = time.perf_counter()
+    gt_ids, _ = jasper_amd.bruteforce_knn(base, queries, 10, "l2")
+    gt = gt_ids.cpu().numpy()
+    log(f"c5 ground truth {time.perf_counter() - t0:.1f}s")
+    free, total = torch.cuda.mem_get_info()
+    curve, chosen = [], None
+    for bw in [16, 24, 32, 48, 64, 96, 128]:
+        ids, _ = g.directional_search(queries, k=10, beam_width=bw)
+        r = _recall(gt, ids.cpu().numpy())
+        wall, ev, _ = _timed(torch, lambda: g.directional_search(queries, k=10, beam_width=bw), 3, 1)
+        curve.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
+        log(f"c5 bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+        if chosen is None and r >= 0.9:
+            chosen = bw
+    if chosen is None:
+        chosen = max(curve, key=lambda c: c["recall_at_10"])["beam_width"]
+    wall, ev, _ = _timed(torch, lambda: g.directional_search(queries, k=10, beam_width=chosen), args.steps,
+                         args.warmup)
+    ids, _ = g.directional_search(queries, k=10, beam_width=chosen)
+    rec = _recall(gt, ids.cpu().numpy())
+    st = g.directional_stats(queries, k=10, beam_width=chosen).astype(np.int64)
+    visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
+    alg = int(visits * 2 * dim + hops + adj * (4 + 16 + 2) + nq * (2 * dim + 80))
+    ach = alg / (ev / 1000.0) / 1e9
+    res = _line(args, "config 5: build vectors/s (100M x 128 in HBM) and QPS @ recall@10>=0.9, directional LSH",
+                nq / (wall / 1000.0), "queries/s", wall, "f16",
+                {"workload": f"config 5: {n} x {dim} clustered integer fp16 (10,000 clusters, generated in HBM), "
+                             "R=64 alpha=1.2, prerotate, LSH k_ranks=16 u8 words, 32768 samples, "
+                             f"{nq} queries, k=10",
+                 "build_vectors_per_s": n / build_s, "build_s": build_s, "lsh_s": lsh_s,
+                 "rabitq_vectors_per_s": n / rabitq_s, "build_max_batch": int(bst["max_batch"]),
+                 "beam_width": chosen, "recall_at_10": rec, "target_recall": 0.9, "curve": curve,
+                 "hbm_used_gb": (total - free) / 1e9},
+                {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
+                 "traffic": None, "kernel": "directional_kernel<L2,LSH>", "kernel_ms": ev,
+                 "algorithmic_bytes_per_launch": alg,
+                 "per_query": {"visits": float(st[:, 0].mean()), "hops": float(st[:, 1].mean()),
+                               "adjacency_entries": float(st[:, 2].mean())}})
+    print(json.dumps(res), flush=True)
+    g.free()
+    return 0
+
+
+OTHER_PATHS = {"c5": run_c5, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
                "rotate": run_rotate, "rabitq": run_rabitq}
 
 

@@ -106,3 +106,26 @@ def config(name: str, n: int | None = None, nq: int | None = None):
         return (clustered(n, 128, 0, n_clusters=10_000), clustered(nq, 128, 1, n_clusters=10_000),
                 dict(R=64, distance="l2", alpha=1.2))
     raise ValueError(f"unknown config {name!r}")
+
+
+def clustered_device(n: int, dim: int, seed: int, device, n_clusters: int = 10_000, sigma: float = 20.0,
+                     lo: float = 0.0, hi: float = 218.0, chunk: int = 1 << 22):
+    """The clustered integer mixture generated on the GPU, for sizes whose
+    host generation would dominate a benchmark (config 5: 100M rows). Same
+    centres as `clustered` (cluster_centers), labels and noise from torch's
+    device generator seeded with `seed`, so the values differ from the host
+    generator's. Returns a device fp16 tensor [n, dim]."""
+    import torch
+    dev = torch.device(device)
+    centers = torch.from_numpy(cluster_centers(n_clusters, dim)).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    out = torch.empty((n, dim), dtype=torch.float16, device=dev)
+    for a in range(0, n, chunk):
+        b = min(n, a + chunk)
+        lab = torch.randint(0, n_clusters, (b - a,), generator=gen, device=dev)
+        x = torch.randn((b - a, dim), generator=gen, device=dev, dtype=torch.float32)
+        x.mul_(sigma).add_(centers[lab]).clamp_(lo, hi).round_()
+        out[a:b] = x.to(torch.float16)
+        del x, lab
+    return out
