@@ -478,22 +478,27 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
     gt = gt_ids.cpu().numpy()
     log(f"c5 ground truth {time.perf_counter() - t0:.1f}s")
     free, total = torch.cuda.mem_get_info()
+    # reference traversal (repeats ids, cannot reach the target here) and the
+    # distinct-results traversal (unique=True, an extension)
     curve, chosen = [], None
-    for bw in [16, 24, 32, 48, 64, 96, 128]:
-        ids, _ = g.directional_search(queries, k=10, beam_width=bw)
-        r = _recall(gt, ids.cpu().numpy())
-        wall, ev, _ = _timed(torch, lambda: g.directional_search(queries, k=10, beam_width=bw), 3, 1)
-        curve.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
-        log(f"c5 bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
-        if chosen is None and r >= 0.9:
-            chosen = bw
+    for unique, bws in ((False, [32, 64, 128, 256]), (True, [32, 64, 96, 128, 192, 256, 384, 512])):
+        for bw in bws:
+            run = lambda bw=bw, unique=unique: g.directional_search(queries, k=10, beam_width=bw, unique=unique)
+            ids, _ = run()
+            r = _recall(gt, ids.cpu().numpy())
+            wall, ev, _ = _timed(torch, run, 3, 1)
+            curve.append({"unique": unique, "beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
+            log(f"c5 unique={unique} bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+            if r >= 0.9 and (chosen is None or curve[-1]["qps"] > chosen["qps"]):
+                chosen = curve[-1]
     if chosen is None:
-        chosen = max(curve, key=lambda c: c["recall_at_10"])["beam_width"]
-    wall, ev, _ = _timed(torch, lambda: g.directional_search(queries, k=10, beam_width=chosen), args.steps,
-                         args.warmup)
-    ids, _ = g.directional_search(queries, k=10, beam_width=chosen)
+        chosen = max(curve, key=lambda c: c["recall_at_10"])
+    bw, unique = chosen["beam_width"], chosen["unique"]
+    wall, ev, _ = _timed(torch, lambda: g.directional_search(queries, k=10, beam_width=bw, unique=unique),
+                         args.steps, args.warmup)
+    ids, _ = g.directional_search(queries, k=10, beam_width=bw, unique=unique)
     rec = _recall(gt, ids.cpu().numpy())
-    st = g.directional_stats(queries, k=10, beam_width=chosen).astype(np.int64)
+    st = g.directional_stats(queries, k=10, beam_width=bw, unique=unique).astype(np.int64)
     visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
     alg = int(visits * 2 * dim + hops + adj * (4 + 16 + 2) + nq * (2 * dim + 80))
     ach = alg / (ev / 1000.0) / 1e9
@@ -504,8 +509,8 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
                              f"{nq} queries, k=10",
                  "build_vectors_per_s": n / build_s, "build_s": build_s, "lsh_s": lsh_s,
                  "rabitq_vectors_per_s": n / rabitq_s, "build_max_batch": int(bst["max_batch"]),
-                 "beam_width": chosen, "recall_at_10": rec, "target_recall": 0.9, "curve": curve,
-                 "hbm_used_gb": (total - free) / 1e9},
+                 "beam_width": bw, "unique": unique, "recall_at_10": rec, "target_recall": 0.9,
+                 "curve": curve, "hbm_used_gb": (total - free) / 1e9},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
                  "traffic": None, "kernel": "directional_kernel<L2,LSH>", "kernel_ms": ev,
                  "algorithmic_bytes_per_launch": alg,

@@ -186,13 +186,25 @@ int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, int64_t n, i
 int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t base_stride, const void* queries,
                                int64_t n_queries, int64_t query_stride, int64_t k, int32_t metric,
                                int32_t* out_ids, float* out_dists, void* stream);
+/* directional_search (use_pq = 0) or pq_search (use_pq = 1) with option
+ * flags; no reference counterpart. JASPERX_DIR_UNIQUE skips every pop of a
+ * node already in the exact top-k list: the reference's traversal
+ * (graph_beam_search.cuh:160-206) re-visits such nodes and inserts them
+ * into that list again, so one node can fill several of the k slots. With
+ * the flag the k results are distinct ids. flags = 0 is the reference's
+ * traversal, identical to jasper_directional_search_<cfg>. Queries, outputs
+ * and stream as for jasper_directional_search_<cfg>. */
+#define JASPERX_DIR_UNIQUE 1u
+int64_t jasperx_directional_search_ex(int64_t handle, int32_t use_pq, const void* queries, int64_t n_queries,
+                                      int64_t dim, int32_t* out_ids, float* out_dists, int64_t k,
+                                      int64_t beam_width, int64_t limit, uint32_t flags, void* stream);
 /* Measurement run of directional_search (use_pq = 0) or pq_search
- * (use_pq = 1): the same traversal, writing per-query work counters to host
- * memory out_stats[n_queries * 3] = {visits, hops expanded, adjacency
- * entries read}. Not a search entry point. */
+ * (use_pq = 1), flags as above: the same traversal, writing per-query work
+ * counters to host memory out_stats[n_queries * 3] = {visits, hops
+ * expanded, adjacency entries read}. Not a search entry point. */
 int64_t jasperx_directional_stats(int64_t handle, int32_t use_pq, const void* queries, int64_t n_queries,
-                                  int64_t dim, int64_t k, int64_t beam_width, int64_t limit, uint32_t* out_stats,
-                                  void* stream);
+                                  int64_t dim, int64_t k, int64_t beam_width, int64_t limit, uint32_t flags,
+                                  uint32_t* out_stats, void* stream);
 /* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 

@@ -51,6 +51,9 @@ _bool = ctypes.c_bool
 _f64 = ctypes.c_double
 _str = ctypes.c_char_p
 
+# option flag of jasperx_directional_search_ex: distinct results
+DIR_UNIQUE = 1
+
 _SIGS = {
     "load": ([_str, _i64, _bool]),
     "construct": ([_ptr, _i64, _i64, _f64, _i64, _bool, _ptr]),
@@ -89,7 +92,10 @@ _AGNOSTIC = {
     "jasperx_directional_query_rows": [_i64, _ptr, _i64, _i64, _ptr, _ptr],
     "jasperx_rotate_rows": [_i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr],
     "jasperx_rabitq_node_bytes": [_i64],
-    "jasperx_directional_stats": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr],
+    "jasperx_directional_stats": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_uint32,
+                                  _ptr, _ptr],
+    "jasperx_directional_search_ex": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
+                                      ctypes.c_uint32, _ptr],
     "jasperx_bruteforce_knn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, ctypes.c_int32, _ptr, _ptr, _ptr],
     "jasperx_rabitq_quantize": [_ptr, ctypes.c_int32, _i64, _i64, _i64, _ptr, _ptr, ctypes.c_int32, _ptr, _ptr],
 }
@@ -385,9 +391,25 @@ class Graph:
         return self._run_search(self._search_fn, queries, k, beam_width, beam_width * 2,
                                 print_throughput)
 
+    def _run_unique(self, use_pq, queries, k, beam_width, limit):
+        n_queries = queries.size(0)
+        out_indices = torch.empty(n_queries, k, dtype=torch.int32, device=queries.device)
+        out_distances = torch.empty(n_queries, k, dtype=torch.float32, device=queries.device)
+        _agnostic("jasperx_directional_search_ex")(
+            self._handle, 1 if use_pq else 0, _tensor_ptr(queries), n_queries, self._dim,
+            _tensor_ptr(out_indices), _tensor_ptr(out_distances), k, beam_width, limit, DIR_UNIQUE,
+            _stream_ptr(queries.device))
+        return out_indices, out_distances
+
     def directional_search(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
-                           limit: int | None = None, print_throughput: bool = False):
-        """LSH-estimated beam search (reference __init__.py:525-572)."""
+                           limit: int | None = None, print_throughput: bool = False,
+                           unique: bool = False):
+        """LSH-estimated beam search (reference __init__.py:525-572).
+
+        unique=True (an extension, no reference counterpart) skips every pop
+        of a node already among the k exact results, so the results are
+        distinct ids; the default keeps the reference's traversal, which can
+        return one id in several slots."""
         self._check_alive()
         if not self._is_directional or not self._has_lsh:
             raise RuntimeError(
@@ -395,12 +417,16 @@ class Graph:
                 "build_lsh=True (or loaded with LSH artifacts present)")
         queries = self._query_check(queries)
         resolved_limit = limit if limit is not None else beam_width * 2
+        if unique:
+            return self._run_unique(False, queries, k, beam_width, resolved_limit)
         return self._run_search(self._directional_search_fn, queries, k, beam_width,
                                 resolved_limit, print_throughput)
 
     def pq_search(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
-                  limit: int | None = None, print_throughput: bool = False):
-        """PQ-ADC-estimated beam search (reference __init__.py:574-621)."""
+                  limit: int | None = None, print_throughput: bool = False,
+                  unique: bool = False):
+        """PQ-ADC-estimated beam search (reference __init__.py:574-621);
+        unique as for directional_search."""
         self._check_alive()
         if not self._is_directional or not self._has_pq:
             raise RuntimeError(
@@ -408,6 +434,8 @@ class Graph:
                 "(or loaded with PQ artifacts present)")
         queries = self._query_check(queries)
         resolved_limit = limit if limit is not None else beam_width * 2
+        if unique:
+            return self._run_unique(True, queries, k, beam_width, resolved_limit)
         return self._run_search(self._pq_search_fn, queries, k, beam_width, resolved_limit,
                                 print_throughput)
 
@@ -512,7 +540,7 @@ class Graph:
         return out
 
     def directional_stats(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
-                          limit: int | None = None, pq: bool = False) -> np.ndarray:
+                          limit: int | None = None, pq: bool = False, unique: bool = False) -> np.ndarray:
         """Per-query work counters of directional_search (pq=False) or
         pq_search (pq=True) [n_queries, 3]: visits, hops expanded, adjacency
         entries read. A measurement extension."""
@@ -522,7 +550,8 @@ class Graph:
         out = np.zeros((nq, 3), dtype=np.uint32)
         lim = limit if limit is not None else 2 * beam_width
         _agnostic("jasperx_directional_stats")(self._handle, 1 if pq else 0, _tensor_ptr(queries), nq, self._dim,
-                                               k, beam_width, lim, out.ctypes.data_as(_ptr),
+                                               k, beam_width, lim, DIR_UNIQUE if unique else 0,
+                                               out.ctypes.data_as(_ptr),
                                                _stream_ptr(queries.device))
         return out
 

@@ -547,9 +547,20 @@ extern "C" int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t d
   });
 }
 
+extern "C" int64_t jasperx_directional_search_ex(int64_t h, int32_t use_pq, const void* q, int64_t nq, int64_t dim,
+                                                 int32_t* out_ids, float* out_dists, int64_t k, int64_t bw,
+                                                 int64_t limit, uint32_t flags, void* stream) {
+  return guarded([&]() -> int64_t {
+    if (flags & ~kDirFlagsKnown) throw std::invalid_argument("unknown directional search flags");
+    directional_search(lookup(h, nullptr), use_pq != 0, q, nq, dim, out_ids, out_dists, k, bw, limit, false,
+                       (hipStream_t)stream, nullptr, (flags & kDirUnique) != 0);
+    return 0;
+  });
+}
+
 extern "C" int64_t jasperx_directional_stats(int64_t h, int32_t use_pq, const void* q, int64_t nq, int64_t dim,
-                                             int64_t k, int64_t bw, int64_t limit, uint32_t* out_stats,
-                                             void* stream) {
+                                             int64_t k, int64_t bw, int64_t limit, uint32_t flags,
+                                             uint32_t* out_stats, void* stream) {
   return guarded([&]() -> int64_t {
     Graph& g = lookup(h, nullptr);
     if (nq <= 0) return 0;
@@ -561,7 +572,8 @@ extern "C" int64_t jasperx_directional_stats(int64_t h, int32_t use_pq, const vo
     hip_check(hipMalloc(&d, (size_t)nq * k * 4), "alloc dists");
     hip_check(hipMalloc(&st, (size_t)nq * 12), "alloc stats");
     try {
-      directional_search(g, use_pq != 0, q, nq, dim, ids, d, k, bw, limit, false, s, st);
+      if (flags & ~kDirFlagsKnown) throw std::invalid_argument("unknown directional search flags");
+      directional_search(g, use_pq != 0, q, nq, dim, ids, d, k, bw, limit, false, s, st, (flags & kDirUnique) != 0);
       hip_check(hipMemcpyAsync(out_stats, st, (size_t)nq * 12, hipMemcpyDeviceToHost, s), "download stats");
       hip_check(hipStreamSynchronize(s), "sync stats");
     } catch (...) {

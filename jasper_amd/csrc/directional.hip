@@ -454,6 +454,8 @@ struct DirArgs {
   const float* norms;
   // optional work counters per query: {visits, hops expanded, adjacency entries}
   uint32_t* stats;
+  // skip pops of ids already in the frontier (distinct results; an extension)
+  uint32_t unique;
 };
 
 // Exact distance of the popped node (compute_qu_diff_and_exact,
@@ -562,6 +564,19 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     wave_sync();
     if (lane == 0) B[p] = pk | 1ull;
     const uint32_t u = key_id(pk);
+    if (a.unique) {
+      // u already in F: its exact distance and its neighbours' estimates are
+      // those of its first visit, so the hop would only duplicate F entries
+      bool in_f = false;
+      for (uint32_t base = 0; base < fc && !in_f; base += 64) {
+        const uint32_t i = base + lane;
+        in_f = ballot(i < fc && Fi[i] == u) != 0;
+      }
+      if (in_f) {
+        wave_sync();
+        continue;
+      }
+    }
     const uint4* urow = reinterpret_cast<const uint4*>(a.vecs) + (size_t)u * nchunks;
 
     // visit: exact distance of u (the one vector fetch per hop)
@@ -901,7 +916,7 @@ void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t
 
 void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                         float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
-                        uint32_t* stats) {
+                        uint32_t* stats, bool unique) {
   if (use_pq && !g.pq) throw std::runtime_error("graph has no PQ artifacts built — call build_pq() first");
   if (!use_pq && !g.lsh) throw std::runtime_error("graph has no LSH artifacts built — call build_lsh() first");
   if (dim != (int64_t)g.dim)
@@ -931,6 +946,7 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
   a.out_ids = out_ids;
   a.out_dists = out_dists;
   a.stats = stats;
+  a.unique = unique ? 1u : 0u;
   size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
   if (use_pq) {
     a.M = g.pq->m;

@@ -23,11 +23,16 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
                                              hipStream_t stream, BuildStats* stats);
 void build_lsh(Graph& g, int64_t n_samples, uint64_t seed);
 void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed);
+// option flags of jasperx_directional_search_ex
+constexpr uint32_t kDirUnique = 1u;
+constexpr uint32_t kDirFlagsKnown = kDirUnique;
+
 // stats (optional, device [nq * 3]): per query visits, hops expanded and
-// adjacency entries read.
+// adjacency entries read. unique: skip pops of ids already in the frontier,
+// so the k results are distinct (an extension; the reference re-visits them).
 void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                         float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
-                        uint32_t* stats = nullptr);
+                        uint32_t* stats = nullptr, bool unique = false);
 // The query rows the directional kernels read (padded, rotated when the
 // graph was prerotated), copied to host memory [nq, padded_dim].
 void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t nq, int64_t dim, uint16_t* out,

@@ -93,7 +93,7 @@ def lib():
         _lib.jo_directional_search.argtypes = [i32, P, i64, i32, P, P, i32, P, i32,
                                                i32, i32, P, f32, P,
                                                i32, i32, P, P, P,
-                                               P, i64, ctypes.c_uint32, i32, i32, i32, i32, P, P, P, P, P, P, i32]
+                                               P, i64, ctypes.c_uint32, i32, i32, i32, i32, P, P, P, P, P, P, i32, i32]
         _lib.jo_populate_lsh.restype = None
         _lib.jo_populate_lsh.argtypes = [P, i64, i32, P, P, i32, i32, i32, P, i32]
         _lib.jo_lsh_globals.restype = i64
@@ -429,9 +429,11 @@ def build_pq(g: OracleGraph, M: int, n_train: int = 40000, iters: int = 12, seed
 
 def directional_search(g: OracleGraph, queries, lsh: LshArtifacts | None = None, pq: PqArtifacts | None = None,
                        k: int = 10, beam_width: int = 64, limit: int | None = None, max_result: int = 2048,
-                       get_visited: bool = False, nthreads: int = 0):
+                       get_visited: bool = False, unique: bool = False, nthreads: int = 0):
     """graph_beam_search_kernel (graph_beam_search.cuh:55-270) with the LSH or
-    PQ estimator; returns (ids, dists[, visited ids, visited dists, counts])."""
+    PQ estimator; returns (ids, dists[, visited ids, visited dists, counts]).
+    unique=True is this build's extension: pops of a node already in the
+    frontier are skipped, so the results hold distinct ids."""
     assert (lsh is None) != (pq is None)
     q16 = queries if (isinstance(queries, np.ndarray) and queries.dtype == np.uint16) else as_padded_f16(queries)
     nq = q16.shape[0]
@@ -451,7 +453,7 @@ def directional_search(g: OracleGraph, queries, lsh: LshArtifacts | None = None,
                                 L.K, L.pbytes, _ptr(L.c_per_rank), ctypes.c_float(L.norm_denom), _ptr(L.rows),
                                 Q.M, Q.dsub, _ptr(Q.centroids), _ptr(Q.codes), _ptr(Q.norms),
                                 _ptr(q16), nq, g.medoid, k, beam_width, limit, max_result, _ptr(ids), _ptr(d),
-                                _ptr(vi), _ptr(vd), _ptr(vc), None, nthreads)
+                                _ptr(vi), _ptr(vd), _ptr(vc), None, 1 if unique else 0, nthreads)
     out = (ids, d)
     if get_visited:
         out += (vi, vd, vc)

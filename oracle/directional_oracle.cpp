@@ -226,9 +226,16 @@ void frontier_insert(std::vector<DEntry>& F, DEntry e, uint32_t k) {
 // graph_beam_search_kernel, graph_beam_search.cuh:55-270, with the LSH
 // (directional_beam_search.cuh:31-192) or PQ (pq_beam_search.cuh:32-201)
 // estimator.
+//
+// unique != 0 is this build's extension (no reference counterpart): a popped
+// node whose id is already in the frontier F is skipped (no visit, no
+// expansion; the hop still counts against `limit`), so the results hold
+// distinct ids. The reference re-visits such nodes and re-inserts them into
+// F, which lets one node fill several of the k result slots.
 void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const uint16_t* q, uint32_t medoid,
                      uint32_t k, uint32_t bw, uint32_t limit, uint32_t max_result, int32_t* out_ids,
-                     float* out_d, uint32_t* vis_ids, float* vis_d, uint32_t* vis_count, uint64_t* stats) {
+                     float* out_d, uint32_t* vis_ids, float* vis_d, uint32_t* vis_count, uint64_t* stats,
+                     bool unique) {
   const bool l2 = g.metric == 0;
   std::vector<DEntry> B, tail, merged;
   std::vector<DEntry> F;
@@ -266,6 +273,11 @@ void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const uint16
     if (p == B.size()) break;
     B[p].visited = true;
     const uint32_t u = B[p].id;
+    if (unique) {
+      bool in_f = false;
+      for (const DEntry& f : F) in_f = in_f || f.id == u;
+      if (in_f) continue;
+    }
     const uint16_t* uv = g.vecs + (size_t)u * g.dp;
     float stored, exact_u = 0.0f, qu_dot = 0.0f;
     if (lsh) {
@@ -448,7 +460,7 @@ int jo_directional_search(int mode, const uint16_t* vecs, int64_t n, int dp, con
                           int M, int dsub, const float* centroids, const uint8_t* codes, const float* norms,
                           const uint16_t* queries, int64_t nq, uint32_t medoid, int k, int bw, int limit,
                           int max_result, int32_t* out_ids, float* out_d, uint32_t* vis_ids, float* vis_d,
-                          uint32_t* vis_counts, uint64_t* stats, int nthreads) {
+                          uint32_t* vis_counts, uint64_t* stats, int unique, int nthreads) {
   DGraph g{vecs, n, dp, edges, counts, R, deleted, metric};
   Lsh lsh{K, pbytes, c_per_rank, norm_denom, lsh_rows, (size_t)R * K * pbytes + 2 * (size_t)R};
   Pq pq{M, dsub, centroids, codes, norms};
@@ -459,7 +471,7 @@ int jo_directional_search(int mode, const uint16_t* vecs, int64_t n, int dp, con
                     (uint32_t)k, (uint32_t)bw, (uint32_t)limit, (uint32_t)max_result, out_ids + i * k,
                     out_d + i * k, vis_ids ? vis_ids + i * max_result : nullptr,
                     vis_d ? vis_d + i * max_result : nullptr, vis_counts ? vis_counts + i : nullptr,
-                    stats ? stats + i * 2 : nullptr);
+                    stats ? stats + i * 2 : nullptr, unique != 0);
   }
   return 0;
 }

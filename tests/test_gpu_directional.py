@@ -39,11 +39,22 @@ def assert_rotation_close(got16, x, dim, seed=42):
     assert not got16[:, dim:].any()
 
 
-def _search(gg, fn, q, k, bw, limit=None):
+def _search(gg, fn, q, k, bw, limit=None, unique=False):
     qt = torch.from_numpy(np.ascontiguousarray(q.astype(np.float16))).cuda()
-    ids, d = getattr(gg, fn)(qt, k=k, beam_width=bw, limit=limit)
+    ids, d = getattr(gg, fn)(qt, k=k, beam_width=bw, limit=limit, unique=unique)
     torch.cuda.synchronize()
     return ids.cpu().numpy(), d.cpu().numpy()
+
+
+def _check_unique(gg, g, fn, q, q_rows, bw, **art):
+    """unique=True (distinct results) against the oracle's same mode."""
+    ids, d = _search(gg, fn, q, 10, bw, unique=True)
+    rid, rd = oracle.directional_search(g, q_rows, k=10, beam_width=bw, unique=True, **art)
+    msg = compare_search(ids, d, rid, rd)
+    assert msg is None, f"{fn} unique bw={bw}: {msg}"
+    for row in ids:
+        live = row[row != 0x7FFFFFFF]
+        assert len(set(live.tolist())) == len(live), f"{fn} unique bw={bw}: repeated id in {row}"
 
 
 def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, bws=(16, 64),
@@ -92,6 +103,7 @@ def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, b
             msg = compare_search(ids, d, rid, rd)
             assert msg is None, f"lsh bw={bw}: {msg}"
             out[("lsh", bw)] = (ids, d)
+            _check_unique(gg, g, "directional_search", q, q_rows, bw, lsh=art)
     if pq:
         cent, codes, norms = gg.export_pq()
         rcent, _ = oracle.pq_train(g, k_ranks, n_train=pq_train, iters=pq_iters, seed=11)
@@ -107,6 +119,7 @@ def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, b
             msg = compare_search(ids, d, rid, rd)
             assert msg is None, f"pq bw={bw}: {msg}"
             out[("pq", bw)] = (ids, d)
+            _check_unique(gg, g, "pq_search", q, q_rows, bw, pq=art)
 
     # save -> load round trip keeps the artifacts and the results
     g2 = jasper.Graph.load(str(path), dim=dim, n_neighbors=R, distance=distance, k_ranks=k_ranks,

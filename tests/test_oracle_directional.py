@@ -328,6 +328,53 @@ def test_output_is_stable_topk_of_visits():
         assert np.array_equal(d[i, :len(order)], vd[i, :m][order])
 
 
+def _replay_frontier(vi, vd, k):
+    """The exact top-k list after each visit (frontier_insert_sorted,
+    beam_search_common.cuh:156-185: ascending distance, a new entry after
+    equal ones, full list only takes strictly smaller)."""
+    F, states = [], []
+    for u, dist in zip(vi.tolist(), vd.tolist()):
+        states.append([f[0] for f in F])
+        if len(F) < k or dist < F[-1][1]:
+            j = len(F) if len(F) < k else k - 1
+            if len(F) < k:
+                F.append(None)
+            while j > 0 and F[j - 1][1] > dist:
+                F[j] = F[j - 1]
+                j -= 1
+            F[j] = (u, dist)
+    return F, states
+
+
+def test_reference_mode_repeats_nodes_unique_mode_does_not():
+    _, g = _small_graph(n=800, dim=32, R=16)
+    lsh = oracle.build_lsh(g, K=4, pbytes=1, n_samples=2000, seed=1)
+    q = datasets.gaussian(20, 32, 99) * 4
+    ids, *_ = oracle.directional_search(g, q, lsh=lsh, k=10, beam_width=32)
+    assert any(len(set(r.tolist())) < len(r) for r in ids), "expected repeated ids in the reference mode"
+    uids, ud, vi, vd, vc = oracle.directional_search(g, q, lsh=lsh, k=10, beam_width=32, get_visited=True,
+                                                     unique=True)
+    for i in range(len(q)):
+        m = int(vc[i])
+        F, states = _replay_frontier(vi[i, :m], vd[i, :m], 10)
+        # a pop is skipped exactly when the node is in the top-k list: no
+        # visit is of a node that list held at that moment
+        for t in range(m):
+            assert int(vi[i, t]) not in states[t], f"query {i}: visit {t} re-visits a listed node"
+        assert [f[0] for f in F] == uids[i, :len(F)].astype(np.int64).tolist()
+        assert np.array_equal(np.array([f[1] for f in F], dtype=np.float32), ud[i, :len(F)])
+        assert len(set(uids[i, :len(F)].tolist())) == len(F)
+
+
+def test_unique_mode_pq_distinct():
+    _, g = _small_graph(n=600, dim=32, R=16)
+    pq = oracle.build_pq(g, M=4, n_train=600, iters=3, seed=2)
+    q = datasets.gaussian(10, 32, 97) * 4
+    ids, d = oracle.directional_search(g, q, pq=pq, k=10, beam_width=24, unique=True)
+    for r in ids:
+        assert len(set(r.tolist())) == len(r)
+
+
 def test_limit_and_max_result():
     _, g = _small_graph(n=500, dim=32, R=16)
     lsh = oracle.build_lsh(g, K=4, pbytes=1, n_samples=1000, seed=1)
