@@ -117,8 +117,8 @@ __device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) 
   return l;
 }
 
-static size_t prune_lds_bytes(uint32_t R, uint32_t nchunks) {
-  return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4 + (size_t)R * nchunks * 16;
+static size_t prune_lds_bytes(uint32_t cpl, uint32_t R, uint32_t nchunks) {
+  return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4 + prune_cache_bytes(cpl, R, nchunks);
 }
 
 template <int CPL, int METRIC>
@@ -191,17 +191,17 @@ __global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
     }
     wave_sync();
     // d(w, v) for every source (compute_distance(src_vec = w, sink_vec = v))
-    float wf[CPL * 8];
-    uint4 xw[CPL];
+    RowFrag<CPL> xw;
     load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
-    if constexpr (METRIC != kL2) frag_from_rows<CPL, METRIC>(xw, ql, wf);
+    LeftFrag<CPL, METRIC> wf;
+    left_from_row<CPL, METRIC>(xw, ql, wf);
     for (uint32_t base = 0; base < taken; base += 16) {
       const uint32_t j = base + qg;
       const bool act = j < taken;
       const uint32_t sid = act ? l.srcs[j] : 0u;
-      uint4 xs[CPL];
+      RowFrag<CPL> xs;
       load_row_frag<CPL>(a.pc.vecs + (size_t)sid * a.pc.nchunks, ql, a.pc.nchunks, act, xs);
-      const float d = pair_distance<CPL, METRIC>(xw, wf, xs, ql, a.pc.nlimit);
+      const float d = left_distance<CPL, METRIC>(wf, xs, ql, a.pc.nchunks, a.pc.nlimit);
       if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
     }
     wave_sync();
@@ -238,6 +238,7 @@ static void dispatch_prune(bool reverse, uint32_t cpl, const PruneKernelArgs& a,
     if (reverse) launch_reverse<C, METRIC>(a, grid, lds, s);         \
     else launch_forward<C, METRIC>(a, grid, lds, s);                 \
     break;
+    JA_CASE(0)
     JA_CASE(1)
     JA_CASE(2)
     JA_CASE(3)
@@ -248,7 +249,7 @@ static void dispatch_prune(bool reverse, uint32_t cpl, const PruneKernelArgs& a,
     JA_CASE(8)
 #undef JA_CASE
     default:
-      throw std::invalid_argument("dimension above the supported maximum of 256 for construction");
+      throw std::logic_error("unreachable chunks-per-lane case");
   }
 }
 
@@ -279,8 +280,8 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   if (max_batch < 1) max_batch = 1;  // the reference loops forever here (n < 50); clamp instead
   if (g.R > 64) throw std::invalid_argument("R must be <= 64");
   const uint32_t nchunks = g.dp / 8;
-  const uint32_t cpl = (nchunks + 3) / 4;
-  if (cpl > 8) throw std::invalid_argument("dimension above the supported maximum of 256 for construction");
+  // chunks per quad lane held in registers; 0 streams rows longer than 32 chunks
+  const uint32_t cpl = (nchunks + 3) / 4 > 8 ? 0u : (nchunks + 3) / 4;
   const int64_t mb = std::min<int64_t>(max_batch, g.n);
   const uint32_t R = g.R;
 
@@ -334,7 +335,7 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   pa.sorted_pairs = sorted;
   pa.heads = heads;
   pa.n_heads = nheads;
-  const size_t plds = prune_lds_bytes(R, nchunks);
+  const size_t plds = prune_lds_bytes(cpl, R, nchunks);
 
   BuildStats st;
   st.max_batch = mb;

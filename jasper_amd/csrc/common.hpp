@@ -260,17 +260,33 @@ __device__ __forceinline__ void load_query_frag(const uint4* src, uint32_t ql, u
   }
 }
 
+// A quad lane's view of one vector row: its chunks ql, ql+4, ... held in
+// registers (CPL = chunks per lane, rows of up to 32 chunks), or for longer
+// rows (CPL = 0) the row's address, read chunk by chunk while scoring.
+template <int CPL>
+struct RowFrag {
+  uint4 x[CPL];
+};
+template <>
+struct RowFrag<0> {
+  const uint4* row;
+};
+
 // Issue the chunk loads of one vector row for quad lane ql. Every lane loads
 // (inactive lanes pass a valid row and ignore the result), and a chunk past
 // the row's end re-reads chunk 0: the partial sums skip chunks >= their
 // limit, so no masking or zero-fill is needed.
 template <int CPL>
 __device__ __forceinline__ void load_row_frag(const uint4* row, uint32_t ql, uint32_t nchunks, bool /*active*/,
-                                              uint4 (&x)[CPL]) {
+                                              RowFrag<CPL>& f) {
+  if constexpr (CPL == 0) {
+    f.row = row;
+  } else {
 #pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const uint32_t c = ql + 4u * (uint32_t)t;
-    x[t] = row[c < nchunks ? c : 0u];
+    for (int t = 0; t < CPL; ++t) {
+      const uint32_t c = ql + 4u * (uint32_t)t;
+      f.x[t] = row[c < nchunks ? c : 0u];
+    }
   }
 }
 
@@ -278,8 +294,9 @@ __device__ __forceinline__ void load_row_frag(const uint4* row, uint32_t ql, uin
 // L2: nlimit = number of chunks in the sum (dim / 8 of the reference call).
 // IP: nlimit = number of elements in the sum (the reference `dim`).
 template <int CPL, int METRIC>
-__device__ __forceinline__ float quad_partial(const float (&qf)[CPL * 8], const uint4 (&x)[CPL], uint32_t ql,
+__device__ __forceinline__ float quad_partial(const float (&qf)[CPL * 8], const RowFrag<CPL>& xf, uint32_t ql,
                                               uint32_t nlimit) {
+  const uint4 (&x)[CPL] = xf.x;
   float acc = 0.0f;
   if constexpr (METRIC == kL2) {
 #pragma unroll
@@ -345,8 +362,10 @@ __device__ __forceinline__ float mix_diff_hi(uint32_t a, uint32_t b) {
 // chunks ql, ql+4, ... as load_row_frag reads them): the same accumulation
 // order as quad_partial<CPL, kL2>, two VALU operations per element.
 template <int CPL>
-__device__ __forceinline__ float quad_partial_l2h(const uint4 (&qh)[CPL], const uint4 (&x)[CPL], uint32_t ql,
+__device__ __forceinline__ float quad_partial_l2h(const RowFrag<CPL>& qf, const RowFrag<CPL>& xf, uint32_t ql,
                                                   uint32_t nlimit) {
+  const uint4 (&qh)[CPL] = qf.x;
+  const uint4 (&x)[CPL] = xf.x;
   float acc = 0.0f;
 #pragma unroll
   for (int t = 0; t < CPL; ++t) {
@@ -370,6 +389,124 @@ template <int METRIC>
 __device__ __forceinline__ float quad_finish(float partial) {
   const float s = quad_sum(partial);
   return METRIC == kL2 ? s : -s;
+}
+
+// ------------------------------------------------- rows longer than 32 chunks
+// Streamed forms of the lane partials: both rows are read from memory
+// (global or LDS) chunk by chunk, in the same per-lane order as the register
+// forms above, so the sums are identical bit for bit.
+
+__device__ __forceinline__ void l2_chunk(const uint4& q, const uint4& x, float& acc) {
+  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float d0 = mix_diff_lo(qw[k], w[k]);
+    acc = __builtin_fmaf(d0, d0, acc);
+    const float d1 = mix_diff_hi(qw[k], w[k]);
+    acc = __builtin_fmaf(d1, d1, acc);
+  }
+}
+
+// L2 lane partial over chunks ql, ql+4, ... < nlimit.
+__device__ __forceinline__ float stream_partial_l2(const uint4* a, const uint4* b, uint32_t ql, uint32_t nlimit) {
+  float acc = 0.0f;
+  uint32_t c = ql;
+  for (; c + 28 < nlimit; c += 32) {  // 8 chunks per lane in flight
+    uint4 qa[8], xb[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      qa[u] = a[c + 4u * (uint32_t)u];
+      xb[u] = b[c + 4u * (uint32_t)u];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) l2_chunk(qa[u], xb[u], acc);
+  }
+  for (; c < nlimit; c += 4) l2_chunk(a[c], b[c], acc);
+  return acc;
+}
+
+// IP lane partial in the reference's element order (lane l: elements l,
+// l+4, l+8, ... below nlimit): lane s of the quad loads chunk 4t+s of both
+// rows and each chunk is broadcast across the quad. Every lane of a quad
+// must call this with the same arguments.
+__device__ __forceinline__ float stream_partial_ip(const uint4* a, const uint4* b, uint32_t ql, uint32_t nchunks,
+                                                   uint32_t nlimit) {
+  float acc = 0.0f;
+  const uint32_t groups = (nchunks + 3u) / 4u;
+  const uint32_t e0 = ql, e1 = ql + 4u;
+  for (uint32_t t = 0; t < groups; ++t) {
+    const uint32_t c = 4u * t + ql;
+    uint4 xa = make_uint4(0, 0, 0, 0), xb = make_uint4(0, 0, 0, 0);
+    if (c < nchunks) {
+      xa = a[c];
+      xb = b[c];
+    }
+    const uint32_t sa[4] = {xa.x, xa.y, xa.z, xa.w}, sb[4] = {xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      uint32_t wa[4], wb[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (s == 0) { wa[k] = quad_bcast<0>(sa[k]); wb[k] = quad_bcast<0>(sb[k]); }
+        else if (s == 1) { wa[k] = quad_bcast<1>(sa[k]); wb[k] = quad_bcast<1>(sb[k]); }
+        else if (s == 2) { wa[k] = quad_bcast<2>(sa[k]); wb[k] = quad_bcast<2>(sb[k]); }
+        else { wa[k] = quad_bcast<3>(sa[k]); wb[k] = quad_bcast<3>(sb[k]); }
+      }
+      const uint32_t a0 = (e0 >> 1) == 0 ? wa[0] : wa[1], b0 = (e0 >> 1) == 0 ? wb[0] : wb[1];
+      const uint32_t a1 = (e1 >> 1) == 2 ? wa[2] : wa[3], b1 = (e1 >> 1) == 2 ? wb[2] : wb[3];
+      const float qa0 = (e0 & 1u) ? h2f_hi(a0) : h2f_lo(a0), xb0 = (e0 & 1u) ? h2f_hi(b0) : h2f_lo(b0);
+      const float qa1 = (e1 & 1u) ? h2f_hi(a1) : h2f_lo(a1), xb1 = (e1 & 1u) ? h2f_hi(b1) : h2f_lo(b1);
+      const uint32_t base = 8u * (4u * t + (uint32_t)s);
+      if (base + e0 < nlimit) acc = __builtin_fmaf(qa0, xb0, acc);
+      if (base + e1 < nlimit) acc = __builtin_fmaf(qa1, xb1, acc);
+    }
+  }
+  return acc;
+}
+
+// ----------------------------------------------------------- left operands
+// The operand a row is compared against (a query, or a pruning candidate):
+// L2 keeps its fp16 chunks (v_fma_mix converts them), IP its fp32 elements
+// in quad_partial's broadcast layout, and long rows (CPL = 0) their address.
+template <int CPL, int METRIC>
+struct LeftFrag {
+  float f[CPL * 8];
+};
+template <int CPL>
+struct LeftFrag<CPL, kL2> {
+  RowFrag<CPL> h;
+};
+template <>
+struct LeftFrag<0, kL2> {
+  const uint4* row;
+};
+template <>
+struct LeftFrag<0, kIP> {
+  const uint4* row;
+};
+
+// The left operand of a row held in memory (queries).
+template <int CPL, int METRIC>
+__device__ __forceinline__ void load_left(const uint4* row, uint32_t ql, uint32_t nchunks, LeftFrag<CPL, METRIC>& l) {
+  if constexpr (CPL == 0) l.row = row;
+  else if constexpr (METRIC == kL2) load_row_frag<CPL>(row, ql, nchunks, true, l.h);
+  else load_query_frag<CPL, METRIC>(row, ql, nchunks, l.f);
+}
+
+// Distance between a left operand and a row fragment (nlimit: L2 chunks,
+// IP elements), in the reference's per-lane order and quad combine.
+template <int CPL, int METRIC>
+__device__ __forceinline__ float left_distance(const LeftFrag<CPL, METRIC>& l, const RowFrag<CPL>& x, uint32_t ql,
+                                               uint32_t nchunks, uint32_t nlimit) {
+  if constexpr (CPL == 0) {
+    if constexpr (METRIC == kL2) return quad_finish<METRIC>(stream_partial_l2(l.row, x.row, ql, nlimit));
+    else return quad_finish<METRIC>(stream_partial_ip(l.row, x.row, ql, nchunks, nlimit));
+  } else if constexpr (METRIC == kL2) {
+    return quad_finish<METRIC>(quad_partial_l2h<CPL>(l.h, x, ql, nlimit));
+  } else {
+    return quad_finish<METRIC>(quad_partial<CPL, METRIC>(l.f, x, ql, nlimit));
+  }
 }
 
 }  // namespace jasper_amd

@@ -25,21 +25,18 @@ struct PruneCtx {
   float alpha;
 };
 
-// Convert a row fragment in load layout (lane l: chunks l, l+4, ...) to the
-// fp32 "left operand" layout quad_partial expects.
+// The left operand of a loaded row: L2 keeps the fp16 chunks; IP converts
+// the load layout (lane l: chunks l, l+4, ...) to quad_partial's fp32
+// broadcast layout; long rows (CPL = 0) keep the address.
 template <int CPL, int METRIC>
-__device__ __forceinline__ void frag_from_rows(const uint4 (&x)[CPL], uint32_t ql, float (&f)[CPL * 8]) {
-  if constexpr (METRIC == kL2) {
-#pragma unroll
-    for (int t = 0; t < CPL; ++t) {
-      const uint32_t w[4] = {x[t].x, x[t].y, x[t].z, x[t].w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        f[t * 8 + 2 * k] = h2f_lo(w[k]);
-        f[t * 8 + 2 * k + 1] = h2f_hi(w[k]);
-      }
-    }
+__device__ __forceinline__ void left_from_row(const RowFrag<CPL>& xf, uint32_t ql, LeftFrag<CPL, METRIC>& l) {
+  if constexpr (CPL == 0) {
+    l.row = xf.row;
+  } else if constexpr (METRIC == kL2) {
+    l.h = xf;
   } else {
+    float (&f)[CPL * 8] = l.f;
+    const uint4 (&x)[CPL] = xf.x;
 #pragma unroll
     for (int t = 0; t < CPL; ++t) {
 #pragma unroll
@@ -64,23 +61,26 @@ __device__ __forceinline__ void frag_from_rows(const uint4 (&x)[CPL], uint32_t q
   }
 }
 
-// Distance between a left row (fp16 chunks xl; for IP also its fp32 layout
-// fl) and a right row xr, in the reference's per-lane order.
-template <int CPL, int METRIC>
-__device__ __forceinline__ float pair_distance(const uint4 (&xl)[CPL], const float (&fl)[CPL * 8],
-                                               const uint4 (&xr)[CPL], uint32_t ql, uint32_t nlimit) {
-  if constexpr (METRIC == kL2) return quad_finish<METRIC>(quad_partial_l2h<CPL>(xl, xr, ql, nlimit));
-  else return quad_finish<METRIC>(quad_partial<CPL, METRIC>(fl, xr, ql, nlimit));
+// A selected member's row: from the LDS cache (register fragments), or for
+// long rows straight from the vector array (the cache is not kept).
+template <int CPL>
+__device__ __forceinline__ void load_member(const PruneCtx& p, const uint4* Scache, const uint32_t* S_ids, uint32_t s,
+                                            uint32_t ql, RowFrag<CPL>& x) {
+  if constexpr (CPL == 0) {
+    x.row = p.vecs + (size_t)S_ids[s] * p.nchunks;
+  } else {
+    const uint4* cache_row = Scache + (size_t)s * p.nchunks;
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+      const uint32_t c = ql + 4u * (uint32_t)t;
+      x.x[t] = c < p.nchunks ? cache_row[c] : make_uint4(0, 0, 0, 0);
+    }
+  }
 }
 
-template <int CPL>
-__device__ __forceinline__ void load_cache_frag(const uint4* cache_row, uint32_t ql, uint32_t nchunks,
-                                                uint4 (&x)[CPL]) {
-#pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const uint32_t c = ql + 4u * (uint32_t)t;
-    x[t] = c < nchunks ? cache_row[c] : make_uint4(0, 0, 0, 0);
-  }
+// LDS bytes of the selected-member cache (none for long rows).
+__host__ __device__ inline size_t prune_cache_bytes(uint32_t cpl, uint32_t R, uint32_t nchunks) {
+  return cpl == 0 ? 0 : (size_t)R * nchunks * 16;
 }
 
 // C: sorted keys [0, nc) in LDS. Writes the selection to S_ids / S_dist and
@@ -98,17 +98,17 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     const uint32_t cid = key_id(ck);
     const float cd = key_dist(ck);
     valid = valid && cid != self;
-    uint4 xc[CPL];
+    RowFrag<CPL> xc;
     load_row_frag<CPL>(p.vecs + (size_t)(valid ? cid : 0u) * p.nchunks, ql, p.nchunks, valid, xc);
-    float cf[CPL * 8];
-    if constexpr (METRIC != kL2) frag_from_rows<CPL, METRIC>(xc, ql, cf);
+    LeftFrag<CPL, METRIC> cf;
+    left_from_row<CPL, METRIC>(xc, ql, cf);
     bool pruned = false;
     // members selected before this block
     const uint32_t ns0 = ns;
     for (uint32_t s = 0; s < ns0; ++s) {
-      uint4 xs[CPL];
-      load_cache_frag<CPL>(Scache + (size_t)s * p.nchunks, ql, p.nchunks, xs);
-      const float d = pair_distance<CPL, METRIC>(xc, cf, xs, ql, p.nlimit);
+      RowFrag<CPL> xs;
+      load_member<CPL>(p, Scache, S_ids, s, ql, xs);
+      const float d = left_distance<CPL, METRIC>(cf, xs, ql, p.nchunks, p.nlimit);
       if (d * p.alpha < cd) pruned = true;
       if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
     }
@@ -117,10 +117,12 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     while (live && ns < p.R) {
       const uint32_t g = (uint32_t)__builtin_ctzll(live) >> 2;
       if (qg == g) {
+        if constexpr (CPL > 0) {
 #pragma unroll
-        for (int t = 0; t < CPL; ++t) {
-          const uint32_t c = ql + 4u * (uint32_t)t;
-          if (c < p.nchunks) Scache[(size_t)ns * p.nchunks + c] = xc[t];
+          for (int t = 0; t < CPL; ++t) {
+            const uint32_t c = ql + 4u * (uint32_t)t;
+            if (c < p.nchunks) Scache[(size_t)ns * p.nchunks + c] = xc.x[t];
+          }
         }
         if (ql == 0) {
           S_ids[ns] = cid;
@@ -128,9 +130,9 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
         }
       }
       wave_sync();
-      uint4 xs[CPL];
-      load_cache_frag<CPL>(Scache + (size_t)ns * p.nchunks, ql, p.nchunks, xs);
-      const float d = pair_distance<CPL, METRIC>(xc, cf, xs, ql, p.nlimit);
+      RowFrag<CPL> xs;
+      load_member<CPL>(p, Scache, S_ids, ns, ql, xs);
+      const float d = left_distance<CPL, METRIC>(cf, xs, ql, p.nchunks, p.nlimit);
       if (qg > g && d * p.alpha < cd) pruned = true;
       ns += 1;
       live = ballot(valid && !pruned && ql == 0 && qg > g);

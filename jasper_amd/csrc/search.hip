@@ -54,28 +54,16 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t v, uint32_t bits) {
   return (v * 0x9E3779B1u) >> (32u - bits);
 }
 
-// The query fragment of a quad lane: fp16 chunks for L2 (converted inside
-// v_fma_mix_f32), fp32 elements for IP (quad_partial's broadcast layout).
+// The query as a left operand: fp16 chunks for L2 (converted inside
+// v_fma_mix_f32), fp32 elements for IP (quad_partial's broadcast layout),
+// or for rows longer than 32 chunks (CPL = 0) its address.
 template <int CPL, int METRIC>
-struct QueryFrag {
-  float f[CPL * 8];
-};
-template <int CPL>
-struct QueryFrag<CPL, kL2> {
-  uint4 h[CPL];
-};
+using QueryFrag = LeftFrag<CPL, METRIC>;
 
 template <int CPL, int METRIC>
-__device__ __forceinline__ void load_query(const uint4* qrow, uint32_t ql, uint32_t nchunks, QueryFrag<CPL, METRIC>& q) {
-  if constexpr (METRIC == kL2) load_row_frag<CPL>(qrow, ql, nchunks, true, q.h);
-  else load_query_frag<CPL, METRIC>(qrow, ql, nchunks, q.f);
-}
-
-template <int CPL, int METRIC>
-__device__ __forceinline__ float score(const QueryFrag<CPL, METRIC>& q, const uint4 (&x)[CPL], uint32_t ql,
-                                       uint32_t nlimit) {
-  if constexpr (METRIC == kL2) return quad_finish<METRIC>(quad_partial_l2h<CPL>(q.h, x, ql, nlimit));
-  else return quad_finish<METRIC>(quad_partial<CPL, METRIC>(q.f, x, ql, nlimit));
+__device__ __forceinline__ float score(const SearchArgs& a, const QueryFrag<CPL, METRIC>& q, const RowFrag<CPL>& x,
+                                       uint32_t ql, uint32_t nlimit) {
+  return left_distance<CPL, METRIC>(q, x, ql, a.nchunks, nlimit);
 }
 
 // Scores up to 16 (or 32 with TWO) candidate rows listed in cand[base..)
@@ -87,29 +75,30 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<
   const uint32_t j0 = base + qg;
   const bool act0 = j0 < nm;
   const uint32_t v0 = act0 ? cand[j0] : 0u;
-  uint4 x0[CPL];
+  RowFrag<CPL> x0;
   load_row_frag<CPL>(a.vecs + (size_t)v0 * a.nchunks, ql, a.nchunks, act0, x0);
   if constexpr (TWO) {
     const uint32_t j1 = base + 16u + qg;
     const bool act1 = j1 < nm;
     const uint32_t v1 = act1 ? cand[j1] : 0u;
-    uint4 x1[CPL];
+    RowFrag<CPL> x1;
     load_row_frag<CPL>(a.vecs + (size_t)v1 * a.nchunks, ql, a.nchunks, act1, x1);
-    const float d0 = score<CPL, METRIC>(qf, x0, ql, nlimit);
-    const float d1 = score<CPL, METRIC>(qf, x1, ql, nlimit);
+    const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit);
+    const float d1 = score<CPL, METRIC>(a, qf, x1, ql, nlimit);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
     if (ql == 0 && act1) T[j1] = make_key(d1, v1);
   } else {
-    const float d0 = score<CPL, METRIC>(qf, x0, ql, nlimit);
+    const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
   }
 }
 
 // At dim <= 128 with L2 the registers fit six waves per SIMD (the LDS of a
 // query at bw <= 64 is about 5.6 KB, so registers decide the occupancy).
+// Streamed long rows hold no row in registers.
 template <int CPL, int METRIC>
 constexpr int search_waves_per_simd() {
-  return (CPL <= 4 && METRIC == kL2) ? 6 : 1;
+  return CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? 6 : 1;
 }
 
 template <int CPL, int METRIC, bool STATS>
@@ -130,15 +119,15 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   const uint4* qrow = a.use_range ? a.vecs + (size_t)(a.q_start + qid) * a.nchunks
                                   : a.queries + (size_t)qid * a.nchunks;
   QueryFrag<CPL, METRIC> qf;
-  load_query<CPL, METRIC>(qrow, ql, a.nchunks, qf);
+  load_left<CPL, METRIC>(qrow, ql, a.nchunks, qf);
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
 
   // B = [(medoid, d(q, medoid))]
   uint32_t cnt = 1;
   {
-    uint4 x[CPL];
+    RowFrag<CPL> x;
     load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
-    const float d = score<CPL, METRIC>(qf, x, ql, nlimit);
+    const float d = score<CPL, METRIC>(a, qf, x, ql, nlimit);
     wave_sync();  // hash table initialised
     if (lane == 0) {
       buf0[0] = make_key(d, a.medoid);
@@ -370,7 +359,8 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
     }                                                                                                  \
     break;                                                                                             \
   }
-  switch (cpl) {
+  switch (cpl > 8 ? 0u : cpl) {
+    JA_LAUNCH(0)
     JA_LAUNCH(1)
     JA_LAUNCH(2)
     JA_LAUNCH(3)
@@ -380,8 +370,7 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
     JA_LAUNCH(7)
     JA_LAUNCH(8)
     default:
-      throw std::invalid_argument("dimension " + std::to_string(g.dim) +
-                                  " is above the supported maximum of 256 for plain search");
+      throw std::logic_error("unreachable chunks-per-lane case");
   }
 #undef JA_LAUNCH
   hip_check(hipGetLastError(), "launch beam_search_kernel");

@@ -59,6 +59,16 @@ def test_build_matches_oracle_ip(jasper, oracle_lib):
     _compare(gg, og)
 
 
+@pytest.mark.parametrize("distance,dim,R", [("l2", 960, 32), ("ip", 264, 16)])
+def test_build_matches_oracle_long_rows(jasper, oracle_lib, distance, dim, R):
+    """dim > 256: search and prune distances stream the rows from memory."""
+    from jasper_amd import datasets
+    base = unit(1200, dim, 15) if distance == "ip" else datasets.sparse_abs(1500, dim, 15)
+    og = oracle.build(base, R=R, distance=distance, alpha=1.2)
+    gg = _gpu_build(jasper, base, R, distance)
+    _compare(gg, og)
+
+
 def test_build_tiny_inputs(jasper, oracle_lib):
     # n < 50 makes the reference's batch size 0 (an endless loop); both the
     # oracle and the GPU build clamp it to 1.

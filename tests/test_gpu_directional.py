@@ -145,6 +145,16 @@ def test_lsh_pq_l2_prerotated(jasper, oracle_lib, tmp_path):
           bws=(32, 96))
 
 
+def test_lsh_pq_long_rows(jasper, oracle_lib, tmp_path):
+    """Config 4's shape at small n: dim 960 (u16 LSH words, PQ M=16 with
+    dsub=60), prerotated as the Python default for build_pq does."""
+    from jasper_amd import datasets
+    x = datasets.sparse_abs(1200, 960, 26)
+    q = datasets.sparse_abs(24, 960, 27)
+    _case(jasper, tmp_path, x, q, R=32, distance="l2", k_ranks=16, prerotate=True, lsh=True, pq=True,
+          bws=(16, 64), pq_train=1500, pq_iters=3)
+
+
 def test_lsh_ip(jasper, oracle_lib, tmp_path):
     x = unit(2000, 64, 24)
     q = unit(40, 64, 25)

@@ -133,3 +133,21 @@ def test_search_matches_oracle_subnormal_range(jasper, oracle_lib, tmp_path):
         rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
         msg = compare_search(ids, d, rid, rd)
         assert msg is None, f"bw={bw}: {msg}"
+
+
+@pytest.mark.parametrize("distance,dim,R", [("l2", 264, 32), ("l2", 960, 64), ("ip", 300, 32)])
+def test_search_matches_oracle_long_rows(jasper, oracle_lib, tmp_path, distance, dim, R):
+    """Rows longer than 32 chunks (dim > 256) are scored streamed from
+    memory instead of from register fragments; same order, same bits."""
+    from jasper_amd import datasets
+    if distance == "ip":
+        base, q = unit(1200, dim, 60), unit(32, dim, 61)
+    else:
+        base, q = datasets.sparse_abs(1200, dim, 60), datasets.sparse_abs(32, dim, 61)
+    g = oracle.build(base, R=R, distance=distance, alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    for bw in (16, 64):
+        ids, d = _run(jasper, gg, q, 10, bw)
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
