@@ -119,12 +119,12 @@ def main() -> int:
                     help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--path", default="search",
-                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c5"],
+                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5"],
                     help="search (default, the headline metric) or one of the other hot-path rows, each "
                          "printing its own JSON line: directional (config 3, LSH), pq (PQ-ADC on "
                          "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
-                         "rabitq (one-bit codes), c5 (config 5: 100M x 128 in-HBM build + LSH k=16 "
-                         "directional search)")
+                         "rabitq (one-bit codes), c4 (config 4: 1M x 960 build + PQ search), c5 "
+                         "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     args = ap.parse_args()
 
@@ -521,7 +521,64 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
-OTHER_PATHS = {"c5": run_c5, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
+def run_c4(args, torch, jasper_amd, datasets, dev, log):
+    """Config 4: 1M x 960 non-negative sparse vectors (|N(0,1)| * 0.05, 192
+    dims zeroed per row) generated in HBM, L2, R=64, alpha=1.2, PQ with
+    M=16 subspaces of 60 dims (8-bit codebooks), prerotated (the Python
+    default with build_pq); 1,000 queries, k=10, pq_search at bw=64."""
+    n, nq, dim = args.n, min(args.nq, 1000), 960
+    base = datasets.sparse_abs_device(n, dim, 0, dev)
+    queries = datasets.sparse_abs_device(nq, dim, 1, dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2, build_pq=True, k_ranks=16,
+                               prerotate=True)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    bst = jasper_amd.last_build_stats()
+    log(f"c4 build (prerotation + Vamana + PQ) {build_s:.1f}s = {n / build_s:,.0f} vec/s")
+    t0 = time.perf_counter()
+    gt_ids, _ = jasper_amd.generate_groundtruth(base, queries, k=10, distance="l2")
+    gt = gt_ids.numpy()
+    log(f"c4 ground truth {time.perf_counter() - t0:.1f}s")
+    curve, chosen = [], None
+    for unique in (False, True):
+        for bw in (32, 64, 128, 256):
+            run = lambda bw=bw, unique=unique: g.pq_search(queries, k=10, beam_width=bw, unique=unique)
+            ids, _ = run()
+            r = _recall(gt, ids.cpu().numpy())
+            wall, ev, _ = _timed(torch, run, 3, 1)
+            curve.append({"unique": unique, "beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
+            log(f"c4 unique={unique} bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+    # the configured point: beam width 64, reference traversal
+    bw, unique = 64, False
+    wall, ev, _ = _timed(torch, lambda: g.pq_search(queries, k=10, beam_width=bw), args.steps, args.warmup)
+    ids, _ = g.pq_search(queries, k=10, beam_width=bw)
+    rec = _recall(gt, ids.cpu().numpy())
+    st = g.directional_stats(queries, k=10, beam_width=bw, pq=True).astype(np.int64)
+    visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
+    M = 16
+    # per hop: count byte, vector 2*dp; per edge: id 4, M code bytes, L2 norm 4
+    alg = int(visits * 2 * dim + hops + adj * (4 + M + 4) + nq * (2 * dim + 80))
+    ach = alg / (ev / 1000.0) / 1e9
+    res = _line(args, "config 4: QPS @ bw=64 and build vectors/s, PQ-ADC directional search (1M x 960, L2)",
+                nq / (wall / 1000.0), "queries/s", wall, "f16",
+                {"workload": f"config 4: {n} x {dim} |N(0,1)|*0.05 with 192 zero dims (generated in HBM), L2, "
+                             f"R=64 alpha=1.2, PQ M=16 dsub=60, prerotate, {nq} queries, k=10, bw=64",
+                 "build_vectors_per_s": n / build_s, "build_s": build_s, "build_max_batch": int(bst["max_batch"]),
+                 "beam_width": bw, "recall_at_10": rec, "curve": curve},
+                {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
+                 "traffic": None, "kernel": "directional_kernel<L2,PQ>", "kernel_ms": ev,
+                 "algorithmic_bytes_per_launch": alg,
+                 "lut_centroid_bytes_per_query": M * 256 * (dim // M) * 4,
+                 "per_query": {"visits": float(st[:, 0].mean()), "hops": float(st[:, 1].mean()),
+                               "adjacency_entries": float(st[:, 2].mean())}})
+    print(json.dumps(res), flush=True)
+    g.free()
+    return 0
+
+
+OTHER_PATHS = {"c4": run_c4, "c5": run_c5, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
                "rotate": run_rotate, "rabitq": run_rabitq}
 
 

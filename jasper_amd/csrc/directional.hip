@@ -408,6 +408,63 @@ __global__ __launch_bounds__(64) void pq_encode_kernel(const uint16_t* __restric
   }
 }
 
+// The same codes with the work turned around for subspaces of at most 64
+// dims: a 256-thread block holds the 256 centroids of one subspace j in LDS
+// (rows padded with zeros to DS floats), each wave takes one vertex at a
+// time and each lane one edge, with its residual slice in registers; the
+// centroids are read as wave-wide LDS broadcasts. Per centroid the distance
+// is the same ordered fma sum (padding adds exact zeros) and the argmin
+// keeps the first minimum, as a scan over c = 0..255 does.
+template <int DS>
+__global__ __launch_bounds__(256) void pq_encode_lds_kernel(const uint16_t* __restrict__ vecs, int64_t n,
+                                                            uint32_t dp, const uint32_t* __restrict__ edges,
+                                                            const uint8_t* __restrict__ counts, uint32_t R,
+                                                            uint32_t M, uint32_t dsub, const float* __restrict__ C,
+                                                            uint8_t* __restrict__ codes) {
+  __shared__ float4 sc4[256 * DS / 4];
+  float* sc = reinterpret_cast<float*>(sc4);
+  const uint32_t j = blockIdx.y;
+  const float* cj = C + (size_t)j * 256 * dsub;
+  for (uint32_t i = threadIdx.x; i < 256u * DS; i += 256) {
+    const uint32_t c = i / DS, t = i % DS;
+    sc[i] = t < dsub ? cj[(size_t)c * dsub + t] : 0.0f;
+  }
+  __syncthreads();
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const size_t row_bytes = (size_t)M * R;
+  for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < n; u += (int64_t)gridDim.x * 4) {
+    const uint32_t cnt = min((uint32_t)counts[u], R);
+    const bool act = lane < cnt;
+    const uint32_t nb = act ? edges[(size_t)u * R + lane] : (uint32_t)u;
+    const uint16_t* vrow = vecs + (size_t)nb * dp + (size_t)j * dsub;
+    const uint16_t* urow = vecs + (size_t)u * dp + (size_t)j * dsub;
+    float r[DS];
+#pragma unroll
+    for (int t = 0; t < DS; ++t) r[t] = (uint32_t)t < dsub ? h2f16(hsub_bits(vrow[t], urow[t])) : 0.0f;
+    float best = FLT_MAX;
+    uint32_t bi = 0;
+    for (uint32_t c = 0; c < 256; ++c) {
+      const float4* cc = sc4 + c * (DS / 4);
+      float d = 0.0f;
+#pragma unroll
+      for (int q = 0; q < DS / 4; ++q) {
+        const float4 w = cc[q];
+        const float wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float df = r[4 * q + k] - wv[k];
+          d = __builtin_fmaf(df, df, d);
+        }
+      }
+      if (d < best) {
+        best = d;
+        bi = c;
+      }
+    }
+    if (lane < R) codes[(size_t)u * row_bytes + (size_t)j * R + lane] = act ? (uint8_t)bi : (uint8_t)0;
+  }
+}
+
 // pq_compute_vector_norms (pq_kernels.cuh:218-247)
 __global__ __launch_bounds__(64) void norms_kernel(const uint16_t* __restrict__ vecs, int64_t n, uint32_t dp,
                                                    float* __restrict__ out) {
@@ -863,15 +920,32 @@ void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed) {
     }
     hip_check(hipGetLastError(), "launch pq training");
     hip_check(hipMalloc(&art->codes, (size_t)g.n * M * g.R), "alloc pq codes");
-    const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
-    const size_t elds = (size_t)g.dp * 4 + (size_t)M * g.R;
-    if (elds > 160 * 1024) throw std::invalid_argument("dim too large for the PQ encoder");
-    if (elds > 64 * 1024)
-      hip_check(hipFuncSetAttribute((const void*)pq_encode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)elds), "LDS size");
-    hipLaunchKernelGGL(pq_encode_kernel, dim3(grid), dim3(64), elds, nullptr, (const uint16_t*)g.vecs, g.n, g.dp,
-                       g.edges, g.counts, g.R, M, dsub, art->centroids, art->codes);
-    hip_check(hipGetLastError(), "launch pq_encode_kernel");
+    if (dsub <= 64) {
+      // subspace centroids in LDS, one edge per lane
+      const uint32_t gx = (uint32_t)std::max<int64_t>(1, std::min<int64_t>((g.n + 3) / 4, 2048 / M + 1));
+      const dim3 egrid(gx, M);
+      const auto launch = [&](auto kern) {
+        hipLaunchKernelGGL(kern, egrid, dim3(256), 0, nullptr, (const uint16_t*)g.vecs, g.n, g.dp, g.edges,
+                           g.counts, g.R, M, dsub, art->centroids, art->codes);
+      };
+      if (dsub <= 8) launch(pq_encode_lds_kernel<8>);
+      else if (dsub <= 16) launch(pq_encode_lds_kernel<16>);
+      else if (dsub <= 24) launch(pq_encode_lds_kernel<24>);
+      else if (dsub <= 32) launch(pq_encode_lds_kernel<32>);
+      else if (dsub <= 48) launch(pq_encode_lds_kernel<48>);
+      else launch(pq_encode_lds_kernel<64>);
+      hip_check(hipGetLastError(), "launch pq_encode_lds_kernel");
+    } else {
+      const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
+      const size_t elds = (size_t)g.dp * 4 + (size_t)M * g.R;
+      if (elds > 160 * 1024) throw std::invalid_argument("dim too large for the PQ encoder");
+      if (elds > 64 * 1024)
+        hip_check(hipFuncSetAttribute((const void*)pq_encode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)elds), "LDS size");
+      hipLaunchKernelGGL(pq_encode_kernel, dim3(grid), dim3(64), elds, nullptr, (const uint16_t*)g.vecs, g.n, g.dp,
+                         g.edges, g.counts, g.R, M, dsub, art->centroids, art->codes);
+      hip_check(hipGetLastError(), "launch pq_encode_kernel");
+    }
     compute_norms(g);
     hip_check(hipDeviceSynchronize(), "pq build");
   } catch (...) {

@@ -129,3 +129,27 @@ def clustered_device(n: int, dim: int, seed: int, device, n_clusters: int = 10_0
         out[a:b] = x.to(torch.float16)
         del x, lab
     return out
+
+
+def sparse_abs_device(n: int, dim: int, seed: int, device, zero_frac: float = 0.2, scale: float = 0.05,
+                      chunk: int = 1 << 18):
+    """`sparse_abs` generated on the GPU (config 4: 1M x 960): |N(0,1)| *
+    scale with round(zero_frac * dim) coordinates per row set to zero,
+    chosen uniformly. Uses torch's device generator seeded with `seed`, so
+    the values differ from the host generator's. Returns a device fp16
+    tensor [n, dim]."""
+    import torch
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    n_zero = int(round(zero_frac * dim))
+    out = torch.empty((n, dim), dtype=torch.float16, device=dev)
+    for a in range(0, n, chunk):
+        b = min(n, a + chunk)
+        x = torch.randn((b - a, dim), generator=gen, device=dev, dtype=torch.float32).abs_().mul_(scale)
+        if n_zero:
+            idx = torch.rand((b - a, dim), generator=gen, device=dev).argsort(dim=1)[:, :n_zero]
+            x.scatter_(1, idx, 0.0)
+        out[a:b] = x.to(torch.float16)
+        del x
+    return out
