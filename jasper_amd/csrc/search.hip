@@ -44,14 +44,38 @@ struct SearchArgs {
   uint64_t* visited;
   uint32_t* visited_counts;
   uint32_t hash_bits;
+  // seen-cache entry format: tag_bits = 0 stores full 32-bit ids; otherwise
+  // 16-bit tags (see seen_test_insert) with dom_mask = 2^b - 1, b = hash_bits
+  // + tag_bits >= log2(n)
+  uint32_t tag_bits, dom_mask;
   // measurement mode: exact per-query seen bitmap in HBM and work counters
   uint32_t* seen_bits;      // [nq, seen_words]
   uint32_t seen_words;
   uint32_t* stats;          // [nq, 4]: hops, sum of degrees, vectors scored, 0
 };
 
-__device__ __forceinline__ uint32_t hash_slot(uint32_t v, uint32_t bits) {
-  return (v * 0x9E3779B1u) >> (32u - bits);
+// Seen cache: returns true when v is recorded, else records it (replacing
+// the slot's previous id). A hit is exact (never a false positive), a miss
+// may be an id that was replaced, which only costs a re-score. With 16-bit
+// entries the id is first mapped through h = v * K mod 2^b (K odd: a
+// bijection of [0, 2^b), which holds every id below n); the top hash_bits
+// bits of h pick the slot and the low tag_bits bits (+1, 0 = empty) are
+// stored, so (slot, tag) still identifies v uniquely.
+__device__ __forceinline__ bool seen_test_insert(const SearchArgs& a, uint32_t* H, uint32_t v) {
+  const uint32_t hm = v * 0x9E3779B1u;
+  if (a.tag_bits) {
+    uint16_t* H16 = reinterpret_cast<uint16_t*>(H);
+    const uint32_t hd = hm & a.dom_mask;
+    const uint32_t slot = hd >> a.tag_bits;
+    const uint16_t tag = (uint16_t)((hd & ((1u << a.tag_bits) - 1u)) + 1u);
+    if (H16[slot] == tag) return true;
+    H16[slot] = tag;
+    return false;
+  }
+  const uint32_t slot = hm >> (32u - a.hash_bits);
+  if (H[slot] == v) return true;
+  H[slot] = v;
+  return false;
 }
 
 // The query as a left operand: fp16 chunks for L2 (converted inside
@@ -112,8 +136,12 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   uint64_t* T = smem + 2 * bw;
   uint32_t* cand = reinterpret_cast<uint32_t*>(T + 64);
   uint32_t* H = cand + 64;
-  const uint32_t hsize = 1u << a.hash_bits;
-  for (uint32_t i = lane; i < hsize; i += 64) H[i] = kInvalid32;
+  {
+    // 32-bit words of the cache: empty = all ones (ids) or zero (tags)
+    const uint32_t words = a.tag_bits ? (1u << a.hash_bits) / 2u : 1u << a.hash_bits;
+    const uint32_t fill = a.tag_bits ? 0u : kInvalid32;
+    for (uint32_t i = lane; i < words; i += 64) H[i] = fill;
+  }
 
   const uint32_t ql = lane & 3u, qg = lane >> 2;
   const uint4* qrow = a.use_range ? a.vecs + (size_t)(a.q_start + qid) * a.nchunks
@@ -131,7 +159,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     wave_sync();  // hash table initialised
     if (lane == 0) {
       buf0[0] = make_key(d, a.medoid);
-      H[hash_slot(a.medoid, a.hash_bits)] = a.medoid;
+      seen_test_insert(a, H, a.medoid);
       if constexpr (STATS) atomicOr(&a.seen_bits[(size_t)qid * a.seen_words + (a.medoid >> 5)], 1u << (a.medoid & 31u));
     }
   }
@@ -175,9 +203,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
         isnew = (atomicOr(&a.seen_bits[(size_t)qid * a.seen_words + (v >> 5)], bit) & bit) == 0u;
       }
     } else if (isnew) {
-      const uint32_t h = hash_slot(v, a.hash_bits);
-      if (H[h] == v) isnew = false;
-      else H[h] = v;
+      isnew = !seen_test_insert(a, H, v);
     }
     const uint64_t newm = ballot(isnew);
     const uint32_t nm = (uint32_t)__builtin_popcountll(newm);
@@ -276,7 +302,16 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   }
 }
 
-static uint32_t default_hash_bits(uint32_t bw) {
+// Tag width of 16-bit seen-cache entries for a graph of n vertices, or 0
+// when the ids need full 32-bit entries (more than 15 tag bits).
+static uint32_t seen_tag_bits(int64_t n, uint32_t hash_bits) {
+  uint32_t b = 1;
+  while (b < 32 && ((int64_t)1 << b) < n) ++b;
+  b = std::max(b, hash_bits + 1);
+  return b - hash_bits <= 15 ? b - hash_bits : 0u;
+}
+
+static uint32_t default_hash_bits(uint32_t bw, int64_t n) {
   // JASPER_SEARCH_HASH_BITS (8..15) overrides the size of the per-query seen
   // cache for tuning; the results do not depend on it.
   static const int override_bits = [] {
@@ -285,17 +320,18 @@ static uint32_t default_hash_bits(uint32_t bw) {
     return (v >= 8 && v <= 15) ? v : 0;
   }();
   if (override_bits) return (uint32_t)override_bits;
-  // measured on config 2 at bw 32..64: 2^10 entries beat 2^9 (more re-scoring)
-  // and 2^11..2^12 (fewer resident waves)
-  if (bw <= 64) return 10;
-  if (bw <= 128) return 11;
-  return 12;
+  // LDS budget of the cache: 4 KB at bw <= 64, 8 KB at bw <= 128, else 16 KB
+  // (measured on config 2: 2^11 16-bit entries beat 2^10 (more re-scoring)
+  // and 2^12 (fewer resident waves) at bw 32..64); 16-bit entries when the
+  // ids fit them, else half as many 32-bit ones
+  const uint32_t budget_log2 = bw <= 64 ? 12 : bw <= 128 ? 13 : 14;
+  return seen_tag_bits(n, budget_log2 - 1) ? budget_log2 - 1 : budget_log2 - 2;
 }
 
 size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {
-  const uint32_t hb = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width);
-  (void)g;
-  return (size_t)2 * r.beam_width * 8 + 64 * 8 + 64 * 4 + ((size_t)1 << hb) * 4;
+  const uint32_t hb = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width, g.n);
+  const size_t entry = seen_tag_bits(g.n, hb) ? 2 : 4;
+  return (size_t)2 * r.beam_width * 8 + 64 * 8 + 64 * 4 + std::max<size_t>(((size_t)1 << hb) * entry, 4);
 }
 
 template <int CPL, int METRIC, bool STATS>
@@ -339,7 +375,9 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
   a.out_dists = r.out_dists;
   a.visited = r.visited;
   a.visited_counts = r.visited_counts;
-  a.hash_bits = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width);
+  a.hash_bits = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width, g.n);
+  a.tag_bits = seen_tag_bits(g.n, a.hash_bits);
+  a.dom_mask = a.tag_bits ? (uint32_t)(((uint64_t)1 << (a.hash_bits + a.tag_bits)) - 1u) : 0u;
   a.seen_bits = r.seen_bits;
   a.seen_words = (uint32_t)((g.n + 31) / 32);
   a.stats = r.stats;
