@@ -48,6 +48,7 @@ struct SearchArgs {
   // 16-bit tags (see seen_test_insert) with dom_mask = 2^b - 1, b = hash_bits
   // + tag_bits >= log2(n)
   uint32_t tag_bits, dom_mask;
+  uint32_t two_way;  // 16-bit entries as 2-way sets (one 32-bit word per set)
   // measurement mode: exact per-query seen bitmap in HBM and work counters
   uint32_t* seen_bits;      // [nq, seen_words]
   uint32_t seen_words;
@@ -64,12 +65,19 @@ struct SearchArgs {
 __device__ __forceinline__ bool seen_test_insert(const SearchArgs& a, uint32_t* H, uint32_t v) {
   const uint32_t hm = v * 0x9E3779B1u;
   if (a.tag_bits) {
-    uint16_t* H16 = reinterpret_cast<uint16_t*>(H);
     const uint32_t hd = hm & a.dom_mask;
     const uint32_t slot = hd >> a.tag_bits;
-    const uint16_t tag = (uint16_t)((hd & ((1u << a.tag_bits) - 1u)) + 1u);
+    const uint32_t tag = (hd & ((1u << a.tag_bits) - 1u)) + 1u;
+    if (a.two_way) {
+      // set of two tags, newest in the low half; a miss evicts the older
+      const uint32_t w = H[slot];
+      if ((w & 0xFFFFu) == tag || (w >> 16) == tag) return true;
+      H[slot] = (w << 16) | tag;
+      return false;
+    }
+    uint16_t* H16 = reinterpret_cast<uint16_t*>(H);
     if (H16[slot] == tag) return true;
-    H16[slot] = tag;
+    H16[slot] = (uint16_t)tag;
     return false;
   }
   const uint32_t slot = hm >> (32u - a.hash_bits);
@@ -376,8 +384,23 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
   a.visited = r.visited;
   a.visited_counts = r.visited_counts;
   a.hash_bits = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width, g.n);
-  a.tag_bits = seen_tag_bits(g.n, a.hash_bits);
-  a.dom_mask = a.tag_bits ? (uint32_t)(((uint64_t)1 << (a.hash_bits + a.tag_bits)) - 1u) : 0u;
+  {
+    // JASPER_SEARCH_SEEN_WAYS=1 keeps direct-mapped 16-bit entries (tuning)
+    static const bool direct = [] {
+      const char* e = std::getenv("JASPER_SEARCH_SEEN_WAYS");
+      return e && std::atoi(e) == 1;
+    }();
+    const uint32_t set_bits = a.hash_bits - 1;  // 2^hash_bits entries in 2-way sets
+    const uint32_t tb2 = a.hash_bits >= 2 ? seen_tag_bits(g.n, set_bits) : 0u;
+    if (!direct && tb2) {
+      a.two_way = 1;
+      a.tag_bits = tb2;
+      a.dom_mask = (uint32_t)(((uint64_t)1 << (set_bits + tb2)) - 1u);
+    } else {
+      a.tag_bits = seen_tag_bits(g.n, a.hash_bits);
+      a.dom_mask = a.tag_bits ? (uint32_t)(((uint64_t)1 << (a.hash_bits + a.tag_bits)) - 1u) : 0u;
+    }
+  }
   a.seen_bits = r.seen_bits;
   a.seen_words = (uint32_t)((g.n + 31) / 32);
   a.stats = r.stats;
