@@ -128,9 +128,12 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<
 // At dim <= 128 with L2 the registers fit six waves per SIMD (the LDS of a
 // query at bw <= 64 is about 5.6 KB, so registers decide the occupancy).
 // Streamed long rows hold no row in registers.
+#ifndef JASPER_SEARCH_WAVES_L2
+#define JASPER_SEARCH_WAVES_L2 6
+#endif
 template <int CPL, int METRIC>
 constexpr int search_waves_per_simd() {
-  return CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? 6 : 1;
+  return CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? JASPER_SEARCH_WAVES_L2 : 1;
 }
 
 template <int CPL, int METRIC, bool STATS>
