@@ -103,7 +103,6 @@ struct PruneLds {
   uint32_t* S_ids;
   float* S_dist;
   uint32_t* srcs;
-  uint4* Scache;
 };
 
 __device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) {
@@ -112,14 +111,11 @@ __device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) 
   l.S_ids = reinterpret_cast<uint32_t*>(smem + kCandBuf);
   l.S_dist = reinterpret_cast<float*>(l.S_ids + 64);
   l.srcs = reinterpret_cast<uint32_t*>(l.S_dist + 64);
-  l.Scache = reinterpret_cast<uint4*>(l.srcs + kCandBuf);
   (void)R;
   return l;
 }
 
-static size_t prune_lds_bytes(uint32_t cpl, uint32_t R, uint32_t nchunks) {
-  return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4 + prune_cache_bytes(cpl, R, nchunks);
-}
+static size_t prune_lds_bytes() { return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4; }
 
 template <int CPL, int METRIC>
 __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
@@ -146,7 +142,7 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   }
   wave_sync();
   sort_candidates(l.C, nc);
-  const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, l.Scache);
+  const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   write_selection(a, v, ns, l.S_ids, l.S_dist);
   if (lane < R) {
     a.pairs[(size_t)bid * R + lane] = lane < ns ? (((uint64_t)l.S_ids[lane] << 32) | v) : kEmptyKey;
@@ -207,7 +203,7 @@ __global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
     wave_sync();
     const uint32_t nc = nE + taken;
     sort_candidates(l.C, nc);
-    const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, l.Scache);
+    const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
     write_selection(a, w, ns, l.S_ids, l.S_dist);
     wave_sync();
   }
@@ -335,7 +331,7 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   pa.sorted_pairs = sorted;
   pa.heads = heads;
   pa.n_heads = nheads;
-  const size_t plds = prune_lds_bytes(cpl, R, nchunks);
+  const size_t plds = prune_lds_bytes();
 
   BuildStats st;
   st.max_batch = mb;

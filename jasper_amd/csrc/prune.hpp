@@ -61,33 +61,22 @@ __device__ __forceinline__ void left_from_row(const RowFrag<CPL>& xf, uint32_t q
   }
 }
 
-// A selected member's row: from the LDS cache (register fragments), or for
-// long rows straight from the vector array (the cache is not kept).
+// A selected member's row, read from the vector array by id. The 16 quads
+// of a wave read the same member, so each chunk load is one wave-wide
+// request served from L1/L2; keeping members in LDS instead (R x dim x 2
+// bytes per wave) cut residency to 1.5 waves per SIMD and measured 1.6x
+// slower on the build.
 template <int CPL>
-__device__ __forceinline__ void load_member(const PruneCtx& p, const uint4* Scache, const uint32_t* S_ids, uint32_t s,
-                                            uint32_t ql, RowFrag<CPL>& x) {
-  if constexpr (CPL == 0) {
-    x.row = p.vecs + (size_t)S_ids[s] * p.nchunks;
-  } else {
-    const uint4* cache_row = Scache + (size_t)s * p.nchunks;
-#pragma unroll
-    for (int t = 0; t < CPL; ++t) {
-      const uint32_t c = ql + 4u * (uint32_t)t;
-      x.x[t] = c < p.nchunks ? cache_row[c] : make_uint4(0, 0, 0, 0);
-    }
-  }
+__device__ __forceinline__ void load_member(const PruneCtx& p, const uint32_t* S_ids, uint32_t s, uint32_t ql,
+                                            RowFrag<CPL>& x) {
+  load_row_frag<CPL>(p.vecs + (size_t)S_ids[s] * p.nchunks, ql, p.nchunks, true, x);
 }
 
-// LDS bytes of the selected-member cache (none for long rows).
-__host__ __device__ inline size_t prune_cache_bytes(uint32_t cpl, uint32_t R, uint32_t nchunks) {
-  return cpl == 0 ? 0 : (size_t)R * nchunks * 16;
-}
-
-// C: sorted keys [0, nc) in LDS. Writes the selection to S_ids / S_dist and
-// the selected vectors to Scache ([R][nchunks] uint4, LDS). Returns |S|.
+// C: sorted keys [0, nc) in LDS. Writes the selection to S_ids / S_dist.
+// Returns |S|.
 template <int CPL, int METRIC>
 __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
-                                      uint32_t* S_ids, float* S_dist, uint4* Scache) {
+                                      uint32_t* S_ids, float* S_dist) {
   const uint32_t lane = lane_id();
   const uint32_t ql = lane & 3u, qg = lane >> 2;
   uint32_t ns = 0;
@@ -103,27 +92,30 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     LeftFrag<CPL, METRIC> cf;
     left_from_row<CPL, METRIC>(xc, ql, cf);
     bool pruned = false;
-    // members selected before this block
+    // members selected before this block: ids held one per lane and read
+    // with v_readlane, the next member's row loading while this one scores
     const uint32_t ns0 = ns;
-    for (uint32_t s = 0; s < ns0; ++s) {
-      RowFrag<CPL> xs;
-      load_member<CPL>(p, Scache, S_ids, s, ql, xs);
-      const float d = left_distance<CPL, METRIC>(cf, xs, ql, p.nchunks, p.nlimit);
-      if (d * p.alpha < cd) pruned = true;
-      if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
+    if (ns0) {
+      const uint32_t sid_lane = lane < ns0 ? S_ids[lane] : 0u;
+      RowFrag<CPL> xn;
+      load_row_frag<CPL>(p.vecs + (size_t)(uint32_t)__builtin_amdgcn_readlane((int)sid_lane, 0) * p.nchunks, ql,
+                         p.nchunks, true, xn);
+      for (uint32_t s = 0; s < ns0; ++s) {
+        const RowFrag<CPL> xs = xn;
+        if (s + 1 < ns0)
+          load_row_frag<CPL>(p.vecs + (size_t)(uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)(s + 1)) *
+                                          p.nchunks,
+                             ql, p.nchunks, true, xn);
+        const float d = left_distance<CPL, METRIC>(cf, xs, ql, p.nchunks, p.nlimit);
+        if (d * p.alpha < cd) pruned = true;
+        if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
+      }
     }
     // resolve the block in candidate order
     uint64_t live = ballot(valid && !pruned && ql == 0);
     while (live && ns < p.R) {
       const uint32_t g = (uint32_t)__builtin_ctzll(live) >> 2;
       if (qg == g) {
-        if constexpr (CPL > 0) {
-#pragma unroll
-          for (int t = 0; t < CPL; ++t) {
-            const uint32_t c = ql + 4u * (uint32_t)t;
-            if (c < p.nchunks) Scache[(size_t)ns * p.nchunks + c] = xc.x[t];
-          }
-        }
         if (ql == 0) {
           S_ids[ns] = cid;
           S_dist[ns] = cd;
@@ -131,7 +123,19 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
       }
       wave_sync();
       RowFrag<CPL> xs;
-      load_member<CPL>(p, Scache, S_ids, ns, ql, xs);
+      if constexpr (CPL == 0) {
+        load_member<CPL>(p, S_ids, ns, ql, xs);
+      } else {
+        // the selected row is quad g's: lane 4g + ql holds the chunks this lane needs
+        const int src = (int)(g * 4u + ql);
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+          xs.x[t].x = (uint32_t)__shfl((int)xc.x[t].x, src, 64);
+          xs.x[t].y = (uint32_t)__shfl((int)xc.x[t].y, src, 64);
+          xs.x[t].z = (uint32_t)__shfl((int)xc.x[t].z, src, 64);
+          xs.x[t].w = (uint32_t)__shfl((int)xc.x[t].w, src, 64);
+        }
+      }
       const float d = left_distance<CPL, METRIC>(cf, xs, ql, p.nchunks, p.nlimit);
       if (qg > g && d * p.alpha < cd) pruned = true;
       ns += 1;
