@@ -7,17 +7,18 @@
 // products are exact in fp32, accumulation in fp32); the squared norms are
 // fp32 sums in element order. Ties are ordered by (distance, id).
 //
-// Phase 1 (bf_scan_kernel): one wave owns 32 queries and one chunk of the
-// base. It holds the A fragments of its queries in registers and walks the
-// chunk 32 vectors at a time (one 32x32 output tile, K over the padded dim),
-// loading the next 32 vectors while the current ones are on the matrix cores.
-// Work-groups of one chunk run side by side (query tile is the fast grid
-// index), so the chunk is read from HBM about once and served from L2 to the
-// other query tiles. A score enters a per-query candidate buffer in LDS only
-// if it beats the query's current k-th best; a buffer that could overflow in
-// the next step is compacted (sorted, cut to k), which also lowers the
-// threshold. At the end each (query, chunk) writes its best k, sorted.
-// Phase 2 (bf_merge_kernel): one wave per query merges the chunk lists.
+// One-pass path, used for bases under 262,144 rows, for the threshold
+// sample of the two-pass path and for queries that overflow it:
+// bf_scan_kernel: one wave owns 32 queries and one chunk of the base. It
+// holds the A fragments of its queries in registers and walks the chunk 32
+// vectors at a time (one 32x32 output tile, K over the padded dim), loading
+// the next 32 vectors while the current ones are on the matrix cores. A
+// score enters a per-query candidate buffer in LDS only if it beats the
+// query's current k-th best; a buffer that could overflow in the next step
+// is compacted (sorted, cut to k), which also lowers the threshold. At the
+// end each (query, chunk) writes its best k, sorted. bf_merge_kernel: one
+// wave per query merges the chunk lists.
+// The two-pass path for large bases is described before bf_filter_kernel.
 #include "bruteforce.hpp"
 #include "common.hpp"
 #include "graph.hpp"
@@ -29,10 +30,13 @@
 namespace jasper_amd {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kBfMaxK = 64;          // k the fused scan supports
 constexpr int kBfStep = 32;          // vectors per step = most keys a query can gain per step
+
+__device__ uint4 kBfZeroChunk = {0u, 0u, 0u, 0u};  // never written
 
 __device__ __forceinline__ half8 u4_as_h8(uint4 v) {
   half8 h;
@@ -40,16 +44,23 @@ __device__ __forceinline__ half8 u4_as_h8(uint4 v) {
   return h;
 }
 
-// ||x||^2 per row, fp32 fma in element order.
+// ||x||^2 per row, fp32 fma in element order (16-byte loads).
 __global__ void row_sqnorm_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t dp, uint32_t dim,
                                   float* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const uint16_t* r = x + (size_t)i * dp;
+  const uint4* r = reinterpret_cast<const uint4*>(x + (size_t)i * dp);
   float s = 0.0f;
-  for (uint32_t t = 0; t < dim; ++t) {
-    const float v = __half2float(__ushort_as_half(r[t]));
-    s = __builtin_fmaf(v, v, s);
+  for (uint32_t c = 0; c * 8 < dim; ++c) {
+    const uint4 v = r[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (c * 8 + (uint32_t)j < dim) {
+        const float f = j & 1 ? h2f_hi(w[j >> 1]) : h2f_lo(w[j >> 1]);
+        s = __builtin_fmaf(f, f, s);
+      }
+    }
   }
   out[i] = s;
 }
@@ -62,6 +73,17 @@ __device__ __forceinline__ uint64_t bf_key(float d, uint32_t id) { return ((uint
 // key (~0 when fewer than k remain). Wave-wide.
 __device__ uint32_t bf_compact(uint64_t* buf, uint32_t cnt, uint32_t k, uint64_t* scratch, uint64_t* kth) {
   const uint32_t lane = lane_id();
+  if (cnt <= 64) {
+    // one key per lane, sorted in registers
+    uint64_t x = lane < cnt ? buf[lane] : ~0ull;
+    x = wave_bitonic_sort<64>(x);
+    const uint32_t keep = min(cnt, k);
+    const uint64_t kk = (uint64_t)__shfl((long long)x, (int)(k - 1), 64);
+    if (lane < keep) buf[lane] = x;
+    *kth = keep == k ? kk : ~0ull;
+    lds_wave_sync();
+    return keep;
+  }
   scratch[lane] = lane < cnt ? buf[lane] : ~0ull;
   scratch[lane + 64] = lane + 64 < cnt ? buf[lane + 64] : ~0ull;
   wave_sync();
@@ -78,7 +100,8 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ queries, int64_t nq,
                                                      const float* __restrict__ vsq, const float* __restrict__ qsq,
                                                      uint32_t k, uint32_t cap, int64_t chunk, uint32_t n_chunks,
-                                                     uint64_t* __restrict__ out /* [nq][n_chunks][k] */) {
+                                                     uint64_t* __restrict__ out /* [nq][n_chunks][k] */,
+                                                     const uint8_t* __restrict__ tile_flags) {
   // cap = k + kBfStep rounded up to 8: candidate slots per query
   extern __shared__ uint64_t bf_lds[];
   uint64_t* cand = bf_lds;                 // [32][cap]
@@ -91,6 +114,7 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
   const int64_t v_begin = (int64_t)ci * chunk;
   const int64_t v_end = min(n, v_begin + chunk);
   const uint32_t nck = dp / 8;  // 16-byte chunks per row
+  if (tile_flags && !tile_flags[blockIdx.x]) return;  // only the flagged query tiles
 
   if (lane < 32) {
     cnt[lane] = 0;
@@ -119,25 +143,24 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
     thd[r] = __builtin_inff();
   }
 
-  // one 32-vector tile per step; the next tile's rows load while this one
-  // is on the matrix cores
-  uint4 nb[KS];
-  auto load_step = [&](int64_t v0) {
+  // one 32-vector tile per step, double-buffered by hand so that a step's
+  // MFMAs wait only for its own rows: the next tile's rows (and squared
+  // norms) load while this one is on the matrix cores
+  // a K slot past the row (dp % 16 == 8) reads the zero chunk: no per-lane
+  // branch in the loop, and the product stays an exact 0 (the query side is
+  // zero there too)
+  auto load_step = [&](int64_t v0, uint4 (&nb)[KS], float& nvs) {
     const int64_t v = v0 + am;
-    const uint4* rv = reinterpret_cast<const uint4*>(base + (size_t)(v < v_end ? v : v_begin) * dp);
+    const int64_t vr = v < v_end ? v : v_begin;
+    if constexpr (METRIC == kL2) nvs = vsq[vr];
+    const uint4* rv = reinterpret_cast<const uint4*>(base + (size_t)vr * dp);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const uint32_t c = (uint32_t)s * 2 + ah;
-      nb[s] = (v < v_end && c < nck) ? rv[c] : make_uint4(0, 0, 0, 0);
+      nb[s] = *(c < nck ? rv + c : &kBfZeroChunk);
     }
   };
-  if (v_begin < v_end) load_step(v_begin);
-
-  for (int64_t v0 = v_begin; v0 < v_end; v0 += 32) {
-    uint4 cb[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) cb[s] = nb[s];
-    if (v0 + 32 < v_end) load_step(v0 + 32);
+  auto step = [&](int64_t v0, const uint4 (&cb)[KS], float vs) {
     float16v acc = {};
 #pragma unroll
     for (int s = 0; s < KS; ++s)
@@ -145,7 +168,6 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
     // lane holds column n = lane % 32 (vector) and rows 8g + 4*(lane/32) + j
     const int64_t v = v0 + am;
     if (v < v_end) {
-      const float vs = METRIC == kL2 ? vsq[v] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float d;
@@ -165,7 +187,7 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
         }
       }
     }
-    wave_sync();
+    lds_wave_sync();
     // compact the buffers that could overflow in the next step (32 new keys at most)
     uint64_t full = ballot(lane < 32 && cnt[lane] > cap - kBfStep);
     if (full) {
@@ -178,7 +200,7 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
           cnt[m] = keep;
           thr[m] = kth;
         }
-        wave_sync();
+        lds_wave_sync();
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -186,6 +208,17 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
         thd[r] = t == ~0ull ? __builtin_inff() : ord_to_dist((uint32_t)(t >> 32));
       }
     }
+  };
+  // two tiles per iteration; tiles past v_end load a clamped row and add no
+  // candidates (v < v_end fails), so the loop needs no mid-iteration exit
+  uint4 ba[KS], bb[KS];
+  float vsa = 0.0f, vsb = 0.0f;
+  if (v_begin < v_end) load_step(v_begin, ba, vsa);
+  for (int64_t v0 = v_begin; v0 < v_end; v0 += 64) {
+    load_step(v0 + 32, bb, vsb);
+    step(v0, ba, vsa);
+    load_step(v0 + 64, ba, vsa);
+    step(v0 + 32, bb, vsb);
   }
   // final: best k of each query, sorted, padded with ~0
   for (uint32_t m = 0; m < 32; ++m) {
@@ -202,10 +235,11 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
 // Merge the n_chunks sorted lists of one query (one wave per query).
 __global__ __launch_bounds__(64) void bf_merge_kernel(const uint64_t* __restrict__ lists, int64_t nq,
                                                       uint32_t n_chunks, uint32_t k, int32_t* __restrict__ out_ids,
-                                                      float* __restrict__ out_d) {
+                                                      float* __restrict__ out_d, const uint8_t* __restrict__ q_flags) {
   __shared__ uint64_t buf[256];
   const int64_t q = blockIdx.x;
   if (q >= nq) return;
+  if (q_flags && !q_flags[q]) return;
   const uint32_t lane = threadIdx.x;
   const uint64_t* src = lists + (size_t)q * n_chunks * k;
   const size_t total = (size_t)n_chunks * k;
@@ -225,24 +259,223 @@ __global__ __launch_bounds__(64) void bf_merge_kernel(const uint64_t* __restrict
   }
 }
 
-void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, const void* queries, int64_t nq,
-                    uint32_t k, int metric, int32_t* out_ids, float* out_d, hipStream_t s) {
-  if (k == 0 || nq <= 0) return;
-  if (k > (uint32_t)kBfMaxK) throw std::invalid_argument("bruteforce_knn supports k <= 64");
-  if (dp % 8 != 0 || dp > 512) throw std::invalid_argument("bruteforce_knn supports padded dim <= 512");
-  if (n <= 0) throw std::invalid_argument("empty base");
-  if (n > 0x7FFFFFFFll) throw std::invalid_argument("too many base vectors");
-  const uint32_t ks = (dp + 15) / 16;  // 16-wide K steps (the last may be half empty)
-  float* vsq = nullptr;
-  float* qsq = nullptr;
-  if (metric == kL2) {
-    hip_check(hipMallocAsync((void**)&vsq, (size_t)n * 4, s), "alloc base norms");
-    hip_check(hipMallocAsync((void**)&qsq, (size_t)nq * 4, s), "alloc query norms");
-    hipLaunchKernelGGL(row_sqnorm_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, (const uint16_t*)base,
-                       n, dp, dim, vsq);
-    hipLaunchKernelGGL(row_sqnorm_kernel, dim3((uint32_t)((nq + 255) / 256)), dim3(256), 0, s,
-                       (const uint16_t*)queries, nq, dp, dim, qsq);
+// ----------------------------------------------------------- two-pass path
+// For large bases the exact top-k is found in two passes over a GEMM:
+//  1. the one-pass kernels above on a sample (the first kBfSample rows) give
+//     each query the k-th smallest distance T_q of that sample. The true
+//     k-th smallest over the whole base is <= T_q (the sample's k nearest are
+//     k base rows), so every true neighbour has d <= T_q;
+//  2. bf_filter_kernel computes every distance (same arithmetic) and appends
+//     the keys with d <= T_q to a per-query list in HBM (about k * n / sample
+//     entries per query), with no per-query state in the loop, so its
+//     work-groups share one base tile in LDS across 256 (or 128) queries;
+//  3. bf_select_kernel sorts each list by (distance, id) and writes the top k.
+// A query whose list would exceed kBfCandCap is flagged and redone with the
+// one-pass kernels (only its 32-query tile runs). Results are identical to
+// the one-pass path: the same distances, the same (distance, id) order.
+constexpr int64_t kBfSample = 65536;
+constexpr int64_t kBfTwoPassMin = 4 * kBfSample;
+constexpr uint32_t kBfCandCap = 1024;
+
+// Appends a candidate key to query q's list (a rare path, kept out of line
+// so that its address arithmetic does not occupy registers in the loop).
+__device__ __noinline__ void bf_append(uint32_t* qcount, uint64_t* qcand, uint32_t q, uint64_t key) {
+  const uint32_t slot = atomicAdd(&qcount[q], 1u);
+  if (slot < kBfCandCap) qcand[(size_t)q * kBfCandCap + slot] = key;
+}
+
+// Cooperative base-tile staging of bf_filter_kernel: thread element i is
+// (row srow[i], chunk scol[i]) of the 32-row tile starting at v0.
+// (native vector registers: a uint4 struct copied under a condition stays in
+// private memory)
+template <int PER, int METRIC>
+__device__ __forceinline__ void bf_gload(const uint4* base4, const float* vsq, int64_t v0, int64_t v_begin,
+                                         int64_t v_end, uint32_t nck, uint32_t nel, uint32_t tid,
+                                         const uint32_t (&srow)[PER], const uint32_t (&scol)[PER],
+                                         u32x4 (&stage)[PER], float& svs) {
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    // elements past the tile re-read chunk 0 of the first row and are not stored
+    const bool in = tid + 256u * (uint32_t)i < nel;
+    const int64_t vv = v0 + (in ? srow[i] : 0u);
+    stage[i] = *reinterpret_cast<const u32x4*>(base4 + (size_t)(vv < v_end ? vv : v_begin) * nck + (in ? scol[i] : 0u));
   }
+  if constexpr (METRIC == kL2) {
+    const int64_t vv = v0 + (tid & 31u);
+    svs = vsq[vv < v_end ? vv : v_begin];
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ void bf_sstore(uint4* tile, float* tvs, uint32_t buf, uint32_t rs, uint32_t nel,
+                                          uint32_t tid, const uint32_t (&srow)[PER], const uint32_t (&scol)[PER],
+                                          const u32x4 (&stage)[PER], float svs) {
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (tid + 256u * (uint32_t)i < nel)
+      *reinterpret_cast<u32x4*>(tile + buf * 32 * rs + srow[i] * rs + scol[i]) = stage[i];
+  if (tid < 32) tvs[buf * 32 + tid] = svs;
+}
+
+template <int KS, int TILES, int METRIC>
+__global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restrict__ base, int64_t n, uint32_t dp,
+                                                        const uint16_t* __restrict__ queries, int64_t nq,
+                                                        const float* __restrict__ vsq, const float* __restrict__ qsq,
+                                                        const float* __restrict__ qthr, uint32_t thr_stride,
+                                                        int64_t chunk, uint32_t* __restrict__ qcount,
+                                                        uint64_t* __restrict__ qcand) {
+  // LDS: two base tiles of 32 rows, row stride nck + 1 chunks (the extra
+  // chunk is zero: it is the K slot past the row when dp % 16 == 8, and it
+  // staggers the rows across banks); two sets of 32 squared norms; per wave
+  // and query tile the 32 query norms and thresholds
+  extern __shared__ uint4 bf_tile[];
+  const uint32_t nck = dp / 8, rs = nck + 1;
+  float* tvs = reinterpret_cast<float*>(bf_tile + 2 * 32 * rs);  // [2][32]
+  float* sqs = tvs + 64;              // [4 waves][TILES][32]
+  float* sth = sqs + 4 * TILES * 32;   // [4 waves][TILES][32]
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u, am = lane & 31u, ah = lane >> 5;
+  const int64_t qbase = (int64_t)blockIdx.x * (128 * TILES) + (int64_t)w * (32 * TILES);
+  const int64_t v_begin = (int64_t)blockIdx.y * chunk;
+  const int64_t v_end = min(n, v_begin + chunk);
+  const uint4* base4 = reinterpret_cast<const uint4*>(base);
+
+  if (tid < 64) bf_tile[(tid >> 5) * 32 * rs + (tid & 31u) * rs + nck] = make_uint4(0, 0, 0, 0);
+  uint4 af[TILES][KS];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    const int64_t aq = qbase + 32 * t + am;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t c = (uint32_t)s * 2 + ah;
+      af[t][s] = (aq < nq && c < nck) ? reinterpret_cast<const uint4*>(queries + (size_t)aq * dp)[c]
+                                      : make_uint4(0, 0, 0, 0);
+    }
+    if (ah == 0) {
+      // a NaN threshold passes nothing (rows past the last query)
+      sqs[(w * TILES + t) * 32 + am] = (METRIC == kL2 && aq < nq) ? qsq[aq] : 0.0f;
+      sth[(w * TILES + t) * 32 + am] = aq < nq ? qthr[(size_t)aq * thr_stride] : __builtin_nanf("");
+    }
+  }
+
+  // cooperative tile loads: thread element i is (row srow[i], chunk scol[i])
+  constexpr int kPer = (32 * 2 * KS + 255) / 256;
+  const uint32_t nel = 32 * nck;
+  uint32_t srow[kPer], scol[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t e = tid + 256u * (uint32_t)i;
+    srow[i] = e / nck;
+    scol[i] = e % nck;
+  }
+  // base tiles: tile i is in LDS buffer i % 2 while tile i + 1 waits in
+  // registers and tile i + 2 is loading, so a load has two steps of work to
+  // hide behind
+  u32x4 sta[kPer], stb[kPer];
+  float sva = 0.0f, svb = 0.0f;
+  if (v_begin < v_end) {
+    bf_gload<kPer, METRIC>(base4, vsq, v_begin, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
+    bf_sstore<kPer>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
+    bf_gload<kPer, METRIC>(base4, vsq, v_begin + 32, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
+  }
+  __syncthreads();
+  // every load issued so far (query fragments, first tiles) completes here:
+  // otherwise the loop's first MFMA waits for all outstanding loads on every
+  // iteration, the prefetched tile included
+  __builtin_amdgcn_s_waitcnt(0);
+  auto step = [&](int64_t v0, uint32_t buf) {
+    const uint4* brow = bf_tile + buf * 32 * rs + am * rs;
+    uint4 b[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) b[s] = brow[(uint32_t)s * 2 + ah];
+    const float vs = tvs[buf * 32 + am];
+    const int64_t v = v0 + am;
+    const bool vok = v < v_end;
+    // the tiles' MFMA chains interleaved (each tile accumulates over s in
+    // order, as bf_scan_kernel does: the distances must match it bit for bit)
+    float16v accs[TILES];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) accs[t] = float16v{};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int t = 0; t < TILES; ++t)
+        accs[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[t][s]), u4_as_h8(b[s]), accs[t], 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const float16v acc = accs[t];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        // rows 8g + 4ah + j, j = 0..3
+        const uint32_t row0 = 8u * (uint32_t)g + 4u * ah;
+        const float4 q4 = *reinterpret_cast<const float4*>(sqs + (w * TILES + t) * 32 + row0);
+        const float4 t4 = *reinterpret_cast<const float4*>(sth + (w * TILES + t) * 32 + row0);
+        const float qsv[4] = {q4.x, q4.y, q4.z, q4.w}, thv[4] = {t4.x, t4.y, t4.z, t4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float d;
+          if constexpr (METRIC == kL2) d = __builtin_fmaf(-2.0f, acc[4 * g + j], qsv[j] + vs);
+          else d = -__half2float(__float2half_rn(acc[4 * g + j]));
+          if (vok && d <= thv[j]) {
+            if constexpr (METRIC == kL2) d = d < 0.0f ? 0.0f : d;
+            bf_append(qcount, qcand, (uint32_t)qbase + (uint32_t)(32 * t + j) + row0, bf_key(d, (uint32_t)v));
+          }
+        }
+      }
+    }
+  };
+  for (int64_t v0 = v_begin; v0 < v_end; v0 += 64) {
+    // tile v0 in buffer 0, tile v0 + 32 in stb, tile v0 + 64 loads into sta
+    // loads are unconditional (rows past the chunk are clamped and never
+    // stored), so the wait counts before each store are static
+    bf_gload<kPer, METRIC>(base4, vsq, v0 + 64, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
+    step(v0, 0u);
+    if (v0 + 32 < v_end) bf_sstore<kPer>(bf_tile, tvs, 1u, rs, nel, tid, srow, scol, stb, svb);
+    __syncthreads();
+    if (v0 + 32 >= v_end) break;
+    // tile v0 + 32 in buffer 1, tile v0 + 64 in sta, tile v0 + 96 loads into stb
+    bf_gload<kPer, METRIC>(base4, vsq, v0 + 96, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
+    step(v0 + 32, 1u);
+    if (v0 + 64 < v_end) bf_sstore<kPer>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
+    __syncthreads();
+  }
+}
+
+// Per query: sort the candidate list by (distance, id) and write the best k;
+// a list that overflowed flags the query (and its 32-query tile) for the
+// one-pass kernels.
+__global__ __launch_bounds__(64) void bf_select_kernel(const uint32_t* __restrict__ qcount,
+                                                       const uint64_t* __restrict__ qcand, int64_t nq, uint32_t k,
+                                                       int32_t* __restrict__ out_ids, float* __restrict__ out_d,
+                                                       uint8_t* __restrict__ q_flags, uint8_t* __restrict__ tile_flags) {
+  __shared__ uint64_t buf[kBfCandCap];
+  const int64_t q = blockIdx.x;
+  const uint32_t lane = threadIdx.x;
+  const uint32_t cnt = qcount[q];
+  if (cnt > kBfCandCap) {
+    if (lane == 0) {
+      q_flags[q] = 1;
+      tile_flags[q >> 5] = 1;
+    }
+    return;
+  }
+  const uint32_t N = max(pow2_ceil(cnt), 2u);
+  const uint64_t* src = qcand + (size_t)q * kBfCandCap;
+  for (uint32_t i = lane; i < N; i += 64) buf[i] = i < cnt ? src[i] : ~0ull;
+  wave_sync();
+  lds_bitonic_sort(buf, N);
+  for (uint32_t i = lane; i < k; i += 64) {
+    const uint64_t key = i < N ? buf[i] : ~0ull;
+    out_ids[(size_t)q * k + i] = key == ~0ull ? -1 : (int32_t)(uint32_t)key;
+    out_d[(size_t)q * k + i] = key == ~0ull ? FLT_MAX : ord_to_dist((uint32_t)(key >> 32));
+  }
+}
+
+// The one-pass path (scan + merge) over base rows [0, n), for all queries or
+// only the flagged ones.
+static void bf_one_pass(const void* base, int64_t n, uint32_t dp, const void* queries, int64_t nq, uint32_t k,
+                        int metric, const float* vsq, const float* qsq, int32_t* out_ids, float* out_d,
+                        const uint8_t* tile_flags, const uint8_t* q_flags, hipStream_t s) {
+  const uint32_t ks = (dp + 15) / 16;  // 16-wide K steps (the last may be half empty)
   // chunks: about 8192 work-groups (single waves) in all, each chunk a
   // multiple of 64 vectors (a whole number of 32-vector steps)
   const int64_t qtiles = (nq + 31) / 32;
@@ -257,7 +490,7 @@ void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, cons
   const size_t lds = ((size_t)32 * cap + 128) * 8;
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(64), lds, s, (const uint16_t*)base, n, dp, (const uint16_t*)queries, nq,
-                       (const float*)vsq, (const float*)qsq, k, cap, chunk, n_chunks, lists);
+                       vsq, qsq, k, cap, chunk, n_chunks, lists, tile_flags);
   };
 #define JA_BF_CASE(K)                                              \
   case K:                                                          \
@@ -275,9 +508,99 @@ void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, cons
 #undef JA_BF_CASE
   hip_check(hipGetLastError(), "launch bf_scan_kernel");
   hipLaunchKernelGGL(bf_merge_kernel, dim3((uint32_t)nq), dim3(64), 0, s, (const uint64_t*)lists, nq, n_chunks, k,
-                     out_ids, out_d);
+                     out_ids, out_d, q_flags);
   hip_check(hipGetLastError(), "launch bf_merge_kernel");
   (void)hipFreeAsync(lists, s);
+}
+
+template <int KS, int METRIC>
+static void launch_filter(const void* base, int64_t n, uint32_t dp, const void* queries, int64_t nq,
+                          const float* vsq, const float* qsq, const float* qthr, uint32_t thr_stride,
+                          uint32_t* qcount, uint64_t* qcand, hipStream_t s) {
+  constexpr int TILES = 1;
+  const int64_t qblocks = (nq + 128 * TILES - 1) / (128 * TILES);
+  // about 2,500 work-groups; the query block is the fast grid index so the
+  // work-groups running at once share base tiles in L2
+  int64_t want = std::max<int64_t>(1, 2560 / qblocks);
+  want = std::min<int64_t>(want, (n + 31) / 32);
+  const int64_t chunk = ((n + want - 1) / want + 31) / 32 * 32;
+  const uint32_t n_chunks = (uint32_t)((n + chunk - 1) / chunk);
+  const uint32_t rs = dp / 8 + 1;
+  const size_t lds = (size_t)2 * 32 * rs * 16 + 2 * 32 * 4 + (size_t)2 * 4 * TILES * 32 * 4;
+  auto kern = bf_filter_kernel<KS, TILES, METRIC>;
+  if (lds > 64 * 1024)
+    hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
+  hipLaunchKernelGGL(kern, dim3((uint32_t)qblocks, n_chunks), dim3(256), lds, s, (const uint16_t*)base, n, dp,
+                     (const uint16_t*)queries, nq, vsq, qsq, qthr, thr_stride, chunk, qcount, qcand);
+  hip_check(hipGetLastError(), "launch bf_filter_kernel");
+}
+
+template <int METRIC>
+static void dispatch_filter(uint32_t ks, const void* base, int64_t n, uint32_t dp, const void* queries, int64_t nq,
+                            const float* vsq, const float* qsq, const float* qthr, uint32_t thr_stride,
+                            uint32_t* qcount, uint64_t* qcand, hipStream_t s) {
+  switch (ks) {
+#define JA_F(K) \
+  case K: launch_filter<K, METRIC>(base, n, dp, queries, nq, vsq, qsq, qthr, thr_stride, qcount, qcand, s); break;
+    JA_F(1) JA_F(2) JA_F(3) JA_F(4) JA_F(5) JA_F(6) JA_F(7) JA_F(8) JA_F(9) JA_F(10) JA_F(11) JA_F(12) JA_F(13)
+    JA_F(14) JA_F(15) JA_F(16) JA_F(17) JA_F(18) JA_F(19) JA_F(20) JA_F(21) JA_F(22) JA_F(23) JA_F(24) JA_F(25)
+    JA_F(26) JA_F(27) JA_F(28) JA_F(29) JA_F(30) JA_F(31) JA_F(32)
+#undef JA_F
+    default: throw std::invalid_argument("bruteforce_knn: unsupported dim");
+  }
+}
+
+void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, const void* queries, int64_t nq,
+                    uint32_t k, int metric, int32_t* out_ids, float* out_d, hipStream_t s) {
+  if (k == 0 || nq <= 0) return;
+  if (k > (uint32_t)kBfMaxK) throw std::invalid_argument("bruteforce_knn supports k <= 64");
+  if (dp % 8 != 0 || dp > 512) throw std::invalid_argument("bruteforce_knn supports padded dim <= 512");
+  if (n <= 0) throw std::invalid_argument("empty base");
+  if (n > 0x7FFFFFFFll) throw std::invalid_argument("too many base vectors");
+  if (nq > 0x7FFFFFFFll) throw std::invalid_argument("too many queries");
+  float* vsq = nullptr;
+  float* qsq = nullptr;
+  if (metric == kL2) {
+    hip_check(hipMallocAsync((void**)&vsq, (size_t)n * 4, s), "alloc base norms");
+    hip_check(hipMallocAsync((void**)&qsq, (size_t)nq * 4, s), "alloc query norms");
+    hipLaunchKernelGGL(row_sqnorm_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, (const uint16_t*)base,
+                       n, dp, dim, vsq);
+    hipLaunchKernelGGL(row_sqnorm_kernel, dim3((uint32_t)((nq + 255) / 256)), dim3(256), 0, s,
+                       (const uint16_t*)queries, nq, dp, dim, qsq);
+  }
+  if (n < kBfTwoPassMin) {
+    bf_one_pass(base, n, dp, queries, nq, k, metric, vsq, qsq, out_ids, out_d, nullptr, nullptr, s);
+  } else {
+    // 1. thresholds from the sample rows [0, kBfSample)
+    int32_t* sid = nullptr;
+    float* sd = nullptr;
+    uint32_t* qcount = nullptr;
+    uint64_t* qcand = nullptr;
+    uint8_t* flags = nullptr;  // [nq] query flags, then [ceil(nq / 32)] tile flags
+    const int64_t ntiles = (nq + 31) / 32;
+    hip_check(hipMallocAsync((void**)&sid, (size_t)nq * k * 4, s), "alloc sample ids");
+    hip_check(hipMallocAsync((void**)&sd, (size_t)nq * k * 4, s), "alloc sample dists");
+    hip_check(hipMallocAsync((void**)&qcount, (size_t)nq * 4, s), "alloc candidate counts");
+    hip_check(hipMallocAsync((void**)&qcand, (size_t)nq * kBfCandCap * 8, s), "alloc candidate lists");
+    hip_check(hipMallocAsync((void**)&flags, (size_t)(nq + ntiles), s), "alloc overflow flags");
+    hip_check(hipMemsetAsync(qcount, 0, (size_t)nq * 4, s), "clear candidate counts");
+    hip_check(hipMemsetAsync(flags, 0, (size_t)(nq + ntiles), s), "clear overflow flags");
+    bf_one_pass(base, kBfSample, dp, queries, nq, k, metric, vsq, qsq, sid, sd, nullptr, nullptr, s);
+    // 2. every distance against the thresholds (the k-th sample distance)
+    const uint32_t ks = (dp + 15) / 16;
+    if (metric == kL2) dispatch_filter<kL2>(ks, base, n, dp, queries, nq, vsq, qsq, sd + (k - 1), k, qcount, qcand, s);
+    else dispatch_filter<kIP>(ks, base, n, dp, queries, nq, vsq, qsq, sd + (k - 1), k, qcount, qcand, s);
+    // 3. select, and redo overflowed queries in one pass
+    hipLaunchKernelGGL(bf_select_kernel, dim3((uint32_t)nq), dim3(64), 0, s, (const uint32_t*)qcount,
+                       (const uint64_t*)qcand, nq, k, out_ids, out_d, flags, flags + nq);
+    hip_check(hipGetLastError(), "launch bf_select_kernel");
+    bf_one_pass(base, n, dp, queries, nq, k, metric, vsq, qsq, out_ids, out_d, flags + nq, flags, s);
+    (void)hipFreeAsync(sid, s);
+    (void)hipFreeAsync(sd, s);
+    (void)hipFreeAsync(qcount, s);
+    (void)hipFreeAsync(qcand, s);
+    (void)hipFreeAsync(flags, s);
+  }
   if (vsq) (void)hipFreeAsync(vsq, s);
   if (qsq) (void)hipFreeAsync(qsq, s);
 }

@@ -79,6 +79,12 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
 // LDS visibility between lanes of the one wave that owns a work-group.
 __device__ __forceinline__ void wave_sync() { __syncthreads(); }
 
+// LDS ordering for a work-group of one wave, without the workgroup fence of
+// __syncthreads (which also waits for every outstanding global load): waits
+// for this wave's LDS operations, which execute in order, and keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // Per-lane select by a wave-uniform lane mask held in SGPRs: bit set -> b.
 __device__ __forceinline__ uint32_t select_by_mask(uint32_t a, uint32_t b, uint64_t mask) {
   uint32_t r;

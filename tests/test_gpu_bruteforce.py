@@ -86,3 +86,32 @@ def test_generate_groundtruth_uses_kernel(jasper, oracle_lib):
                                            torch.from_numpy(q.astype(np.float16)), k=80)
     rid2, rd2 = _ref(base, q, 80, "l2")
     assert np.array_equal(d2.numpy(), rd2)
+
+
+@pytest.mark.parametrize("distance", ["l2", "ip"])
+def test_two_pass_integer_exact(jasper, oracle_lib, distance):
+    """n >= 262,144 takes the two-pass path (sample thresholds, filtered GEMM,
+    per-query select); on integer data it must equal the reference arithmetic
+    bit for bit, ties ordered by id."""
+    base = integer_clustered(300_000, 64, 44)
+    q = integer_clustered(100, 64, 45)
+    for k in (10, 64):
+        ids, d = _run(jasper, base, q, k, distance)
+        rid, rd = _ref(base, q, k, distance)
+        assert np.array_equal(d, rd), f"k={k}"
+        assert np.array_equal(ids, rid), f"k={k}"
+
+
+def test_two_pass_overflow_falls_back(jasper, oracle_lib):
+    """Most rows equal: every copy ties at the sample's k-th distance, the
+    candidate lists overflow, and the flagged queries are redone in one pass."""
+    rng = np.random.default_rng(46)
+    base = np.repeat(rng.integers(0, 50, size=(1, 32)), 290_000, axis=0).astype(np.float32)
+    idx = rng.choice(290_000, size=5_000, replace=False)
+    base[idx] = rng.integers(0, 50, size=(5_000, 32))
+    q = rng.integers(0, 50, size=(40, 32)).astype(np.float32)
+    q[:20] = base[0]  # these queries see ~285k ties at distance 0
+    ids, d = _run(jasper, base, q, 10, "l2")
+    rid, rd = _ref(base, q, 10, "l2")
+    assert np.array_equal(d, rd)
+    assert np.array_equal(ids, rid)
