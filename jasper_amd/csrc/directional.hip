@@ -547,10 +547,21 @@ __device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4* uro
   return block128_sum(p[0], p[1]);
 }
 
-template <int METRIC, bool PQ>
+// One LSH word (sign in the MSB, coordinate below) of rank r from the
+// edge's K * P bytes held in registers.
+template <int P>
+__device__ __forceinline__ uint32_t lsh_word(const uint32_t* w, int r) {
+  if constexpr (P == 1) return (w[r >> 2] >> (8 * (r & 3))) & 0xFFu;
+  else return (w[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
+}
+
+// K = 0: the PQ estimator; K in {4, 16} with P-byte words: the LSH estimator.
+template <int METRIC, int K, int P>
 __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
   constexpr bool L2 = METRIC == kL2;
+  constexpr bool PQ = K == 0;
+  constexpr int KW = PQ ? 1 : K * P / 4;  // dwords of LSH words per edge
   const uint32_t lane = threadIdx.x;
   const uint32_t qid = blockIdx.x;
   const uint32_t nchunks = a.dp / 8;
@@ -634,6 +645,45 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         continue;
       }
     }
+    // every read that depends only on u, issued before the visit: the edge
+    // count, the adjacency row, and u's estimator data for edge slot `lane`
+    // (slots past the count are read and ignored; they lie inside u's rows)
+    const bool slot = lane < a.R;
+    const uint32_t deg_raw = a.counts[u];
+    const uint32_t v_raw = slot ? a.edges[(size_t)u * a.R + lane] : 0u;
+    uint32_t wl[KW];
+    uint32_t mag_bits = 0;
+    uint8_t codes[PQ ? 16 : 1];
+    if constexpr (!PQ) {
+      const uint8_t* row = a.lsh_rows + (size_t)u * a.row_bytes;
+      if (slot) {
+        const uint8_t* wp = row + (size_t)lane * (K * P);
+        if constexpr (KW == 1) wl[0] = *reinterpret_cast<const uint32_t*>(wp);
+        else if constexpr (KW == 2) {
+          const uint2 t2 = *reinterpret_cast<const uint2*>(wp);
+          wl[0] = t2.x; wl[1] = t2.y;
+        } else {
+#pragma unroll
+          for (int c = 0; c < KW / 4; ++c) {
+            const uint4 t4 = reinterpret_cast<const uint4*>(wp)[c];
+            wl[4 * c] = t4.x; wl[4 * c + 1] = t4.y; wl[4 * c + 2] = t4.z; wl[4 * c + 3] = t4.w;
+          }
+        }
+        mag_bits = *reinterpret_cast<const uint16_t*>(row + (size_t)a.R * (K * P) + 2 * (size_t)lane);
+      } else {
+#pragma unroll
+        for (int c = 0; c < KW; ++c) wl[c] = 0;
+      }
+    } else {
+      const uint8_t* code = a.codes + (size_t)u * a.M * a.R;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) codes[j] = (slot && (uint32_t)j < a.M) ? code[(size_t)j * a.R + lane] : (uint8_t)0;
+    }
+    const uint32_t deg = min(deg_raw, a.R);
+    const bool has = lane < deg;
+    const bool valid_v = has && (int64_t)v_raw < a.n;
+    float vnorm = 0.0f;
+    if constexpr (PQ && L2) vnorm = valid_v ? a.norms[v_raw] : 0.0f;
     const uint4* urow = reinterpret_cast<const uint4*>(a.vecs) + (size_t)u * nchunks;
 
     // visit: exact distance of u (the one vector fetch per hop)
@@ -645,74 +695,89 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       exact_u = visit_exact<L2>(qv, urow, nchunks, xv);
       stored = L2 ? exact_u : -exact_u;
     }
-    // frontier_insert_sorted (beam_search_common.cuh:156-185)
-    if (lane == 0 && a.k > 0) {
-      int j = -1;
-      if (fc < a.k) {
-        j = (int)fc;
-        fc += 1;
-      } else if (stored < Fd[a.k - 1]) {
-        j = (int)a.k - 1;
-      }
-      if (j >= 0) {
-        while (j > 0 && Fd[j - 1] > stored) {
-          Fd[j] = Fd[j - 1];
-          Fi[j] = Fi[j - 1];
-          --j;
+    // frontier_insert_sorted (beam_search_common.cuh:156-185): the new entry
+    // goes after the last entry that is not greater (its insertion loop runs
+    // from the end while F[j - 1] > stored); when F is full it enters only
+    // below the last entry, which drops out
+    if (a.k > 0) {
+      if (a.k <= 64) {
+        const bool full = fc == a.k;
+        const uint32_t lim = full ? a.k - 1 : fc;
+        float fdl = 0.0f;
+        uint32_t fil = 0;
+        if (lane < fc) {
+          fdl = Fd[lane];
+          fil = Fi[lane];
         }
-        Fd[j] = stored;
-        Fi[j] = u;
+        const bool enter = !full || stored < __shfl(fdl, (int)(a.k - 1), 64);
+        const uint64_t le = ballot(lane < lim && !(fdl > stored));
+        const uint32_t pos = le ? 64u - (uint32_t)__builtin_clzll(le) : 0u;
+        wave_sync();
+        if (enter) {
+          if (lane >= pos && lane < lim) {
+            Fd[lane + 1] = fdl;
+            Fi[lane + 1] = fil;
+          }
+          if (lane == pos) {
+            Fd[pos] = stored;
+            Fi[pos] = u;
+          }
+          if (!full) fc += 1;
+        }
+      } else if (lane == 0) {
+        int j = -1;
+        if (fc < a.k) {
+          j = (int)fc;
+          fc += 1;
+        } else if (stored < Fd[a.k - 1]) {
+          j = (int)a.k - 1;
+        }
+        if (j >= 0) {
+          while (j > 0 && Fd[j - 1] > stored) {
+            Fd[j] = Fd[j - 1];
+            Fi[j] = Fi[j - 1];
+            --j;
+          }
+          Fd[j] = stored;
+          Fi[j] = u;
+        }
       }
+      if (a.k > 64) fc = (uint32_t)__shfl((int)fc, 0, 64);
     }
-    fc = (uint32_t)__shfl((int)fc, 0, 64);
     vc += 1;
     if (vc == a.max_result) break;
     wave_sync();
 
-    // expand u and estimate its neighbours (no neighbour vector fetches)
-    const uint32_t deg = min((uint32_t)a.counts[u], a.R);
+    // estimate u's neighbours from the data read above (no neighbour vector fetches)
     n_hops += 1;
     n_adj += deg;
     uint64_t t = kEmptyKey;
-    if (lane < deg) {
-      const uint32_t v = a.edges[(size_t)u * a.R + lane];
-      if ((int64_t)v < a.n) {
-        const uint32_t e = lane;
+    if (has) {
+      if (valid_v) {
         float est;
         if constexpr (PQ) {
-          const uint8_t* code = a.codes + (size_t)u * a.M * a.R;
           float acc = qu_dot;
-          for (uint32_t j = 0; j < a.M; ++j) acc = acc + lut[j * 256 + code[(size_t)j * a.R + e]];
-          est = L2 ? (q_sq - 2.0f * acc) + a.norms[v] : -acc;
+          for (uint32_t j = 0; j < a.M; ++j) acc = acc + lut[j * 256 + codes[j]];
+          est = L2 ? (q_sq - 2.0f * acc) + vnorm : -acc;
         } else {
-          const uint8_t* row = a.lsh_rows + (size_t)u * a.row_bytes;
           const uint16_t* x16 = L2 ? reinterpret_cast<const uint16_t*>(xv) : q16;
+          constexpr uint32_t kSign = P == 1 ? 0x80u : 0x8000u;
           float dot_acc = 0.0f;
-          for (uint32_t r = 0; r < a.K; ++r) {
-            uint32_t coord;
-            bool neg;
-            if (a.pbytes == 1) {
-              const uint32_t w = row[(size_t)e * a.K + r];
-              neg = (w & 0x80u) != 0;
-              coord = w & 0x7Fu;
-            } else {
-              const uint8_t* wp = row + 2 * ((size_t)e * a.K + r);
-              const uint32_t w = wp[0] | ((uint32_t)wp[1] << 8);
-              neg = (w & 0x8000u) != 0;
-              coord = w & 0x7FFFu;
-            }
-            const float cs = neg ? -a.c[r] : a.c[r];
+#pragma unroll
+          for (int r = 0; r < K; ++r) {
+            const uint32_t w = lsh_word<P>(wl, r);
+            const uint32_t coord = w & (kSign - 1u);
+            const float cs = (w & kSign) ? -a.c[r] : a.c[r];
             const float xc = coord < a.dp ? h2f16(x16[coord]) : 0.0f;  // guards a corrupt row
             dot_acc = __builtin_fmaf(cs, xc, dot_acc);
           }
-          const uint8_t* mb = row + (size_t)a.R * a.K * a.pbytes + 2 * (size_t)e;
-          const float mag_sq = bf2f((uint16_t)(mb[0] | ((uint32_t)mb[1] << 8)));
+          const float mag_sq = bf2f((uint16_t)mag_bits);
           const float dot_est = dot_acc * a.inv_norm_denom;
           const float mag = sqrt_rn(mag_sq);
           est = L2 ? __builtin_fmaf(-(2.0f * mag), dot_est, exact_u + mag_sq)
                    : -__builtin_fmaf(mag, dot_est, exact_u);
         }
-        t = make_key(est, v);
+        t = make_key(est, v_raw);
       } else {
         t = make_key(FLT_MAX, kInv31) | 1ull;  // INVALID, visited (device_kernels.cuh:115-122)
       }
@@ -1044,20 +1109,23 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
     hip_check(hipEventCreate(&e1), "event");
     hip_check(hipEventRecord(e0, stream), "event record");
   }
-  const void* kern = nullptr;
-  if (use_pq) kern = g.metric == kL2 ? (const void*)directional_kernel<kL2, true> : (const void*)directional_kernel<kIP, true>;
-  else kern = g.metric == kL2 ? (const void*)directional_kernel<kL2, false> : (const void*)directional_kernel<kIP, false>;
   if (lds > 160 * 1024) throw std::invalid_argument("beam_width, k and dim need more than 160 KB of LDS");
-  if (lds > 64 * 1024)
-    hip_check(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS size");
+  if (use_pq && a.M > 16) throw std::invalid_argument("pq_search supports at most 16 subspaces");
+  if (!use_pq && !((a.K == 4 || a.K == 16) && (a.pbytes == 1 || a.pbytes == 2)))
+    throw std::invalid_argument("k_ranks must be 4 or 16 with 1- or 2-byte words");
   const dim3 grid((uint32_t)nq);
-  if (use_pq) {
-    if (g.metric == kL2) hipLaunchKernelGGL((directional_kernel<kL2, true>), grid, dim3(64), lds, stream, a);
-    else hipLaunchKernelGGL((directional_kernel<kIP, true>), grid, dim3(64), lds, stream, a);
-  } else {
-    if (g.metric == kL2) hipLaunchKernelGGL((directional_kernel<kL2, false>), grid, dim3(64), lds, stream, a);
-    else hipLaunchKernelGGL((directional_kernel<kIP, false>), grid, dim3(64), lds, stream, a);
-  }
+  auto launch = [&](auto kern) {
+    if (lds > 64 * 1024)
+      hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                "LDS size");
+    hipLaunchKernelGGL(kern, grid, dim3(64), lds, stream, a);
+  };
+  const bool l2 = g.metric == kL2;
+  if (use_pq) launch(l2 ? directional_kernel<kL2, 0, 1> : directional_kernel<kIP, 0, 1>);
+  else if (a.K == 4 && a.pbytes == 1) launch(l2 ? directional_kernel<kL2, 4, 1> : directional_kernel<kIP, 4, 1>);
+  else if (a.K == 16 && a.pbytes == 1) launch(l2 ? directional_kernel<kL2, 16, 1> : directional_kernel<kIP, 16, 1>);
+  else if (a.K == 4) launch(l2 ? directional_kernel<kL2, 4, 2> : directional_kernel<kIP, 4, 2>);
+  else launch(l2 ? directional_kernel<kL2, 16, 2> : directional_kernel<kIP, 16, 2>);
   hip_check(hipGetLastError(), "launch directional_kernel");
   if (print) {
     hip_check(hipEventRecord(e1, stream), "event record");
