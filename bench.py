@@ -290,7 +290,9 @@ def main() -> int:
 # ------------------------------------------------------------------ other rows
 
 def _timed(torch, fn, steps, warmup):
-    """Wall ms per call and HIP-event ms per call on the current stream."""
+    """Wall ms per call and HIP-event ms per call on the current stream (the
+    median over the steps: the first calls after a synchronisation can wait
+    on the host's launch, which is not the kernel's time)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -304,7 +306,7 @@ def _timed(torch, fn, steps, warmup):
         e1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
-    ev_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    ev_ms = float(np.median([a.elapsed_time(b) for a, b in evs]))
     return wall_ms, ev_ms, out
 
 
@@ -395,7 +397,7 @@ def run_bruteforce(args, torch, jasper_amd, datasets, dev, log):
                 {"workload": f"config 2 ground truth: {args.nq} queries x {args.n} x 128 fp16, L2, k=10",
                  "queries_per_s": args.nq / (wall / 1000.0)},
                 {"bound": "mfma", "achieved": tf, "peak": 2500.0, "unit": "TFLOP/s", "frac": tf / 2500.0,
-                 "traffic": None, "kernel": "bf_scan_kernel<8,L2> + bf_merge_kernel", "kernel_ms": ev,
+                 "traffic": None, "kernel": "bruteforce_knn (sample scan + bf_filter_kernel + bf_select_kernel)", "kernel_ms": ev,
                  "algorithmic_flop_per_launch": flop})
     print(json.dumps(res), flush=True)
     return 0
@@ -411,7 +413,7 @@ def run_rotate(args, torch, jasper_amd, datasets, dev, log):
                 {"workload": f"{args.n} x 128 fp16 rows times a 128 x 128 fp16 rotation, fp32 accumulation",
                  "tflops": 2.0 * args.n * 128 * 128 / (ev / 1000.0) / 1e12},
                 {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
-                 "traffic": None, "kernel": "rotate_mfma_kernel<4,true>", "kernel_ms": ev,
+                 "traffic": None, "kernel": "rotate_tile_kernel<4>", "kernel_ms": ev,
                  "algorithmic_bytes_per_launch": nbytes})
     print(json.dumps(res), flush=True)
     return 0
