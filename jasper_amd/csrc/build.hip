@@ -80,9 +80,27 @@ __device__ __forceinline__ uint32_t gather_existing(const PruneKernelArgs& a, ui
   return (uint32_t)__builtin_popcountll(m);
 }
 
+// Sort candidates C[0, nc) ascending (empty keys sort last). Up to 128
+// keys are sorted in registers, one or two per lane; longer lists in LDS.
 __device__ __forceinline__ void sort_candidates(uint64_t* C, uint32_t nc) {
-  const uint32_t N = max(pow2_ceil(nc), 2u);
-  for (uint32_t i = nc + lane_id(); i < N; i += 64) C[i] = kEmptyKey;
+  const uint32_t lane = lane_id();
+  if (nc <= 64) {
+    uint64_t x = lane < nc ? C[lane] : kEmptyKey;
+    x = wave_bitonic_sort<64>(x);
+    C[lane] = x;
+    wave_sync();
+    return;
+  }
+  if (nc <= 128) {
+    uint64_t x0 = C[lane], x1 = lane + 64 < nc ? C[lane + 64] : kEmptyKey;
+    wave_bitonic_sort128(x0, x1);
+    C[lane] = x0;
+    C[lane + 64] = x1;
+    wave_sync();
+    return;
+  }
+  const uint32_t N = pow2_ceil(nc);
+  for (uint32_t i = nc + lane; i < N; i += 64) C[i] = kEmptyKey;
   wave_sync();
   lds_bitonic_sort(C, N);
 }

@@ -177,6 +177,42 @@ __device__ __forceinline__ uint64_t wave_bitonic_sort(uint64_t x) {
   return x;
 }
 
+// Ascending bitonic sort of 128 keys held two per lane (element r * 64 +
+// lane in register r). Stages with partner distance 64 compare a lane's two
+// registers; the others exchange within each register as above.
+constexpr uint64_t bitonic_min_lanes2(int K, int J, int r) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l) {
+    const int i = r * 64 + l;
+    if (((i & K) == 0) == ((i & J) == 0)) m |= 1ull << l;
+  }
+  return m;
+}
+
+template <int K, int J>
+__device__ __forceinline__ void bitonic_stage128(uint64_t& x0, uint64_t& x1) {
+  if constexpr (J == 64) {
+    const uint64_t lo = x0 < x1 ? x0 : x1, hi = x0 < x1 ? x1 : x0;
+    x0 = lo;
+    x1 = hi;
+  } else {
+    const uint64_t o0 = xor_lane64<J>(x0), o1 = xor_lane64<J>(x1);
+    const uint64_t t0 = ~(ballot(o0 < x0) ^ bitonic_min_lanes2(K, J, 0));
+    const uint64_t t1 = ~(ballot(o1 < x1) ^ bitonic_min_lanes2(K, J, 1));
+    x0 = (uint64_t)select_by_mask((uint32_t)x0, (uint32_t)o0, t0) |
+         ((uint64_t)select_by_mask((uint32_t)(x0 >> 32), (uint32_t)(o0 >> 32), t0) << 32);
+    x1 = (uint64_t)select_by_mask((uint32_t)x1, (uint32_t)o1, t1) |
+         ((uint64_t)select_by_mask((uint32_t)(x1 >> 32), (uint32_t)(o1 >> 32), t1) << 32);
+  }
+  if constexpr (J > 1) bitonic_stage128<K, J / 2>(x0, x1);
+}
+
+template <int K = 2>
+__device__ __forceinline__ void wave_bitonic_sort128(uint64_t& x0, uint64_t& x1) {
+  bitonic_stage128<K, K / 2>(x0, x1);
+  if constexpr (K < 128) wave_bitonic_sort128<K * 2>(x0, x1);
+}
+
 __device__ __forceinline__ uint64_t wave_sort_upto(uint64_t x, uint32_t n) {
   if (n <= 1) return x;
   if (n <= 2) return wave_bitonic_sort<2>(x);
