@@ -135,7 +135,7 @@ __device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) 
 
 static size_t prune_lds_bytes() { return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4; }
 
-template <int CPL, int METRIC>
+template <int CPL, int METRIC, bool INTX>
 __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   }
   wave_sync();
   sort_candidates(l.C, nc);
-  const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  const uint32_t ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   write_selection(a, v, ns, l.S_ids, l.S_dist);
   if (lane < R) {
     a.pairs[(size_t)bid * R + lane] = lane < ns ? (((uint64_t)l.S_ids[lane] << 32) | v) : kEmptyKey;
@@ -175,7 +175,7 @@ __global__ void mark_heads_kernel(const uint64_t* sorted, uint32_t n, uint32_t* 
   if (i == 0 || (sorted[i - 1] >> 32) != (k >> 32)) heads[atomicAdd(n_heads, 1u)] = i;
 }
 
-template <int CPL, int METRIC>
+template <int CPL, int METRIC, bool INTX>
 __global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
@@ -215,42 +215,42 @@ __global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
       const uint32_t sid = act ? l.srcs[j] : 0u;
       RowFrag<CPL> xs;
       load_row_frag<CPL>(a.pc.vecs + (size_t)sid * a.pc.nchunks, ql, a.pc.nchunks, act, xs);
-      const float d = left_distance<CPL, METRIC>(wf, xs, ql, a.pc.nchunks, a.pc.nlimit);
+      const float d = left_distance<CPL, METRIC, INTX>(wf, xs, ql, a.pc.nchunks, a.pc.nlimit);
       if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
     }
     wave_sync();
     const uint32_t nc = nE + taken;
     sort_candidates(l.C, nc);
-    const uint32_t ns = robust_prune_wave<CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+    const uint32_t ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
     write_selection(a, w, ns, l.S_ids, l.S_dist);
     wave_sync();
   }
 }
 
-template <int CPL, int METRIC>
+template <int CPL, int METRIC, bool INTX>
 static void launch_forward(const PruneKernelArgs& a, uint32_t bs, size_t lds, hipStream_t s) {
-  auto k = forward_prune_kernel<CPL, METRIC>;
+  auto k = forward_prune_kernel<CPL, METRIC, INTX>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
   hipLaunchKernelGGL(k, dim3(bs), dim3(64), lds, s, a);
 }
 
-template <int CPL, int METRIC>
+template <int CPL, int METRIC, bool INTX>
 static void launch_reverse(const PruneKernelArgs& a, uint32_t grid, size_t lds, hipStream_t s) {
-  auto k = reverse_prune_kernel<CPL, METRIC>;
+  auto k = reverse_prune_kernel<CPL, METRIC, INTX>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
   hipLaunchKernelGGL(k, dim3(grid), dim3(64), lds, s, a);
 }
 
-template <int METRIC>
+template <int METRIC, bool INTX>
 static void dispatch_prune(bool reverse, uint32_t cpl, const PruneKernelArgs& a, uint32_t grid, size_t lds,
                            hipStream_t s) {
   switch (cpl) {
 #define JA_CASE(C)                                                   \
   case C:                                                            \
-    if (reverse) launch_reverse<C, METRIC>(a, grid, lds, s);         \
-    else launch_forward<C, METRIC>(a, grid, lds, s);                 \
+    if (reverse) launch_reverse<C, METRIC, INTX && C != 0>(a, grid, lds, s); \
+    else launch_forward<C, METRIC, INTX && C != 0>(a, grid, lds, s);         \
     break;
     JA_CASE(0)
     JA_CASE(1)
@@ -350,6 +350,9 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   pa.heads = heads;
   pa.n_heads = nheads;
   const size_t plds = prune_lds_bytes();
+  // integer-valued rows in the exact range: packed-difference distances,
+  // the same bits as the fp32 chain (int_exact_l2)
+  const bool intx = int_exact_l2(g, stream);
 
   BuildStats st;
   st.max_batch = mb;
@@ -376,14 +379,16 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
       r.visited = visited;
       r.visited_counts = vcounts;
       r.hash_bits = 12;
+      r.int_exact = intx;
       timer.start();
       launch_beam_search(g, r, stream);
       timer.stop(st.search_ms);
       // 2. forward merge + prune + reverse pairs
       pa.batch_offset = (uint32_t)count;
       timer.start();
-      if (g.metric == kL2) dispatch_prune<kL2>(false, cpl, pa, (uint32_t)bs, plds, stream);
-      else dispatch_prune<kIP>(false, cpl, pa, (uint32_t)bs, plds, stream);
+      if (intx) dispatch_prune<kL2, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+      else if (g.metric == kL2) dispatch_prune<kL2, false>(false, cpl, pa, (uint32_t)bs, plds, stream);
+      else dispatch_prune<kIP, false>(false, cpl, pa, (uint32_t)bs, plds, stream);
       hip_check(hipGetLastError(), "launch forward_prune_kernel");
       timer.stop(st.prune_ms);
       // 3. group reverse pairs by target
@@ -398,8 +403,9 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
       pa.n_pairs = np;
       const uint32_t grid = (uint32_t)std::min<int64_t>(std::max<int64_t>(np, 1), 16384);
       timer.start();
-      if (g.metric == kL2) dispatch_prune<kL2>(true, cpl, pa, grid, plds, stream);
-      else dispatch_prune<kIP>(true, cpl, pa, grid, plds, stream);
+      if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
+      else if (g.metric == kL2) dispatch_prune<kL2, false>(true, cpl, pa, grid, plds, stream);
+      else dispatch_prune<kIP, false>(true, cpl, pa, grid, plds, stream);
       hip_check(hipGetLastError(), "launch reverse_prune_kernel");
       timer.stop(st.reverse_ms);
       count += bs;

@@ -507,6 +507,41 @@ __device__ __forceinline__ float stream_partial_ip(const uint4* a, const uint4* 
   return acc;
 }
 
+// ------------------------------------------------------ integer-valued data
+// When every value is an integer and the values span at most 2,048 (see
+// int_exact_l2), each fp16 difference a - b is exact, each square is an
+// exact fp32 integer and every partial sum stays below 2^24: the reference's
+// ordered fp32 sum then equals the exact integer whatever the order. The
+// fast form takes the differences of two halves at once (v_pk_add_f16) and
+// adds both squares with one v_dot2_f32_f16: one VALU per element instead of
+// two, and the same bits as quad_partial_l2h on such data.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_sqdiff(uint32_t a, uint32_t b, float acc) {
+  half2_t x, y;
+  __builtin_memcpy(&x, &a, 4);
+  __builtin_memcpy(&y, &b, 4);
+  const half2_t d = x - y;
+  return __builtin_amdgcn_fdot2(d, d, acc, false);
+}
+
+template <int CPL>
+__device__ __forceinline__ float quad_partial_l2_int(const RowFrag<CPL>& qf, const RowFrag<CPL>& xf, uint32_t ql,
+                                                     uint32_t nlimit) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const uint32_t c = ql + 4u * (uint32_t)t;
+    if (c < nlimit) {
+      acc = dot2_sqdiff(qf.x[t].x, xf.x[t].x, acc);
+      acc = dot2_sqdiff(qf.x[t].y, xf.x[t].y, acc);
+      acc = dot2_sqdiff(qf.x[t].z, xf.x[t].z, acc);
+      acc = dot2_sqdiff(qf.x[t].w, xf.x[t].w, acc);
+    }
+  }
+  return acc;
+}
+
 // ----------------------------------------------------------- left operands
 // The operand a row is compared against (a query, or a pruning candidate):
 // L2 keeps its fp16 chunks (v_fma_mix converts them), IP its fp32 elements
@@ -538,10 +573,13 @@ __device__ __forceinline__ void load_left(const uint4* row, uint32_t ql, uint32_
 
 // Distance between a left operand and a row fragment (nlimit: L2 chunks,
 // IP elements), in the reference's per-lane order and quad combine.
-template <int CPL, int METRIC>
+// INTX: the rows are integer-valued within the exact range (int_exact_l2).
+template <int CPL, int METRIC, bool INTX = false>
 __device__ __forceinline__ float left_distance(const LeftFrag<CPL, METRIC>& l, const RowFrag<CPL>& x, uint32_t ql,
                                                uint32_t nchunks, uint32_t nlimit) {
-  if constexpr (CPL == 0) {
+  if constexpr (INTX && CPL > 0 && METRIC == kL2) {
+    return quad_finish<METRIC>(quad_partial_l2_int<CPL>(l.h, x, ql, nlimit));
+  } else if constexpr (CPL == 0) {
     if constexpr (METRIC == kL2) return quad_finish<METRIC>(stream_partial_l2(l.row, x.row, ql, nlimit));
     else return quad_finish<METRIC>(stream_partial_ip(l.row, x.row, ql, nchunks, nlimit));
   } else if constexpr (METRIC == kL2) {

@@ -12,7 +12,9 @@
 #include "directional.hpp"
 
 #include <algorithm>
+#include <climits>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 
@@ -102,6 +104,57 @@ void Graph::release() {
   vector_norms = nullptr;
   lsh.reset();
   pq.reset();
+}
+
+// out = {non-integer flag, min, max} over fp16 values (infinities and NaN
+// count as non-integer)
+__global__ void int_range_kernel(const uint16_t* __restrict__ v, size_t count, int32_t* __restrict__ out) {
+  int32_t lo = INT32_MAX, hi = INT32_MIN, bad = 0;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
+    _Float16 hv;
+    const uint16_t bits = v[i];
+    __builtin_memcpy(&hv, &bits, 2);
+    const float h = (float)hv;
+    if (!(fabsf(h) <= 65504.0f) || h != rintf(h)) {
+      bad = 1;
+    } else {
+      lo = min(lo, (int32_t)h);
+      hi = max(hi, (int32_t)h);
+    }
+  }
+  for (int d = 32; d > 0; d >>= 1) {
+    lo = min(lo, __shfl_xor(lo, d, 64));
+    hi = max(hi, __shfl_xor(hi, d, 64));
+    bad = max(bad, __shfl_xor(bad, d, 64));
+  }
+  if ((threadIdx.x & 63u) == 0) {
+    if (bad) atomicMax(&out[0], 1);
+    atomicMin(&out[1], lo);
+    atomicMax(&out[2], hi);
+  }
+}
+
+bool int_exact_l2(const Graph& g, hipStream_t stream) {
+  static const bool enabled = [] {
+    const char* e = std::getenv("JASPER_INT_EXACT");
+    return !(e && std::atoi(e) == 0);
+  }();
+  if (!enabled || g.metric != 0 || g.n <= 0 || !g.vecs || g.on_host) return false;
+  int32_t* d = nullptr;
+  hip_check(hipMallocAsync((void**)&d, 12, stream), "alloc range");
+  const int32_t init[3] = {0, INT32_MAX, INT32_MIN};
+  hip_check(hipMemcpyAsync(d, init, 12, hipMemcpyHostToDevice, stream), "init range");
+  const size_t count = (size_t)g.n * g.dp;
+  const uint32_t grid = (uint32_t)std::min<size_t>((count + 255) / 256, 4096);
+  hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, (const uint16_t*)g.vecs, count, d);
+  hip_check(hipGetLastError(), "launch int_range_kernel");
+  int32_t h[3];
+  hip_check(hipMemcpyAsync(h, d, 12, hipMemcpyDeviceToHost, stream), "read range");
+  hip_check(hipStreamSynchronize(stream), "sync range");
+  hip_check(hipFreeAsync(d, stream), "free range");
+  if (h[0] != 0 || h[1] > h[2]) return false;
+  const double span = (double)h[2] - (double)h[1];
+  return span <= 2048.0 && (double)g.dim * span * span < 16777216.0;
 }
 
 void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream) {

@@ -86,6 +86,13 @@ struct HostGraph {
 };
 void download_graph(const Graph& g, HostGraph& h, bool with_vectors = true);
 
+// True when L2 distances between stored rows are exact integers in any
+// summation order: every stored value (padding included) is an integer, the
+// values span at most 2,048 (exact fp16 differences) and dim * span^2 < 2^24
+// (exact fp32 partial sums). Scans the device rows; synchronises `stream`.
+// JASPER_INT_EXACT=0 turns the packed form off (measurement).
+bool int_exact_l2(const Graph& g, hipStream_t stream);
+
 // Uploads a contiguous host or device fp16 matrix [n, dim] into rows padded
 // to dp on the device graph (vecs must be allocated).
 void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream);

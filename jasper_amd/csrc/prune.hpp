@@ -73,8 +73,9 @@ __device__ __forceinline__ void load_member(const PruneCtx& p, const uint32_t* S
 }
 
 // C: sorted keys [0, nc) in LDS. Writes the selection to S_ids / S_dist.
-// Returns |S|.
-template <int CPL, int METRIC>
+// Returns |S|. INTX: rows are integer-valued within the exact range
+// (int_exact_l2), so pair distances take the packed-difference form.
+template <int CPL, int METRIC, bool INTX>
 __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
                                       uint32_t* S_ids, float* S_dist) {
   const uint32_t lane = lane_id();
@@ -106,7 +107,7 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
           load_row_frag<CPL>(p.vecs + (size_t)(uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)(s + 1)) *
                                           p.nchunks,
                              ql, p.nchunks, true, xn);
-        const float d = left_distance<CPL, METRIC>(cf, xs, ql, p.nchunks, p.nlimit);
+        const float d = left_distance<CPL, METRIC, INTX>(cf, xs, ql, p.nchunks, p.nlimit);
         if (d * p.alpha < cd) pruned = true;
         if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
       }
@@ -136,7 +137,7 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
           xs.x[t].w = (uint32_t)__shfl((int)xc.x[t].w, src, 64);
         }
       }
-      const float d = left_distance<CPL, METRIC>(cf, xs, ql, p.nchunks, p.nlimit);
+      const float d = left_distance<CPL, METRIC, INTX>(cf, xs, ql, p.nchunks, p.nlimit);
       if (qg > g && d * p.alpha < cd) pruned = true;
       ns += 1;
       live = ballot(valid && !pruned && ql == 0 && qg > g);

@@ -92,15 +92,17 @@ __device__ __forceinline__ bool seen_test_insert(const SearchArgs& a, uint32_t* 
 template <int CPL, int METRIC>
 using QueryFrag = LeftFrag<CPL, METRIC>;
 
-template <int CPL, int METRIC>
+// INTX: query and rows are integer-valued within the exact range
+// (int_exact_l2); set only by the build, whose queries are graph rows.
+template <int CPL, int METRIC, bool INTX>
 __device__ __forceinline__ float score(const SearchArgs& a, const QueryFrag<CPL, METRIC>& q, const RowFrag<CPL>& x,
                                        uint32_t ql, uint32_t nlimit) {
-  return left_distance<CPL, METRIC>(q, x, ql, a.nchunks, nlimit);
+  return left_distance<CPL, METRIC, INTX>(q, x, ql, a.nchunks, nlimit);
 }
 
 // Scores up to 16 (or 32 with TWO) candidate rows listed in cand[base..)
 // and stores their keys into T[j].
-template <int CPL, int METRIC, bool TWO>
+template <int CPL, int METRIC, bool INTX, bool TWO>
 __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<CPL, METRIC>& qf, const uint32_t* cand,
                                            uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql, uint32_t qg) {
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
@@ -115,12 +117,12 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<
     const uint32_t v1 = act1 ? cand[j1] : 0u;
     RowFrag<CPL> x1;
     load_row_frag<CPL>(a.vecs + (size_t)v1 * a.nchunks, ql, a.nchunks, act1, x1);
-    const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit);
-    const float d1 = score<CPL, METRIC>(a, qf, x1, ql, nlimit);
+    const float d0 = score<CPL, METRIC, INTX>(a, qf, x0, ql, nlimit);
+    const float d1 = score<CPL, METRIC, INTX>(a, qf, x1, ql, nlimit);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
     if (ql == 0 && act1) T[j1] = make_key(d1, v1);
   } else {
-    const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit);
+    const float d0 = score<CPL, METRIC, INTX>(a, qf, x0, ql, nlimit);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
   }
 }
@@ -136,7 +138,7 @@ constexpr int search_waves_per_simd() {
   return CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? JASPER_SEARCH_WAVES_L2 : 1;
 }
 
-template <int CPL, int METRIC, bool STATS>
+template <int CPL, int METRIC, bool STATS, bool INTX>
 __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void beam_search_kernel(SearchArgs a) {
   extern __shared__ uint64_t smem[];
   const uint32_t lane = threadIdx.x;
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   {
     RowFrag<CPL> x;
     load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
-    const float d = score<CPL, METRIC>(a, qf, x, ql, nlimit);
+    const float d = score<CPL, METRIC, INTX>(a, qf, x, ql, nlimit);
     wave_sync();  // hash table initialised
     if (lane == 0) {
       buf0[0] = make_key(d, a.medoid);
@@ -180,18 +182,30 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   uint64_t* B = buf0;
   uint64_t* NB = buf1;
   uint32_t hint = 0, vc = 0, loop = 0;
+  // adjacency (degree, row) of the predicted next pop, loaded one hop ahead
+  // so that a correct prediction takes the adjacency read off the hop's
+  // chain of dependent memory reads; the prediction is the next unvisited
+  // entry of B, which is the next pop unless a new neighbour displaces it
+  const uint32_t elane = min(lane, a.R - 1u);
+  uint32_t spec_u = kInvalid32, spec_c = 0, spec_v = kInvalid32;
   while (loop <= a.limit) {
     loop += 1;
     // ---- pop: first unvisited entry (all entries before `hint` are visited)
-    int p = -1;
+    int p = -1, p2 = -1;
     for (uint32_t base = hint; base < cnt; base += 64) {
       const uint32_t i = base + lane;
       const bool unv = i < cnt && !key_visited(B[i]);
       const uint64_t m = ballot(unv);
-      if (m) { p = (int)(base + (uint32_t)__builtin_ctzll(m)); break; }
+      if (m) {
+        p = (int)(base + (uint32_t)__builtin_ctzll(m));
+        const uint64_t m2 = m & (m - 1u);
+        if (m2) p2 = (int)(base + (uint32_t)__builtin_ctzll(m2));
+        break;
+      }
     }
     if (p < 0) break;
     const uint64_t pk = B[p] | 1ull;
+    const uint32_t next_u = p2 >= 0 ? key_id(B[p2]) : kInvalid32;
     wave_sync();
     if (lane == 0) {
       B[p] = pk;
@@ -201,11 +215,25 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     vc += 1;
     if (vc == a.max_result) break;
 
-    // ---- expand: one coalesced row read, filter through the seen cache
+    // ---- expand: one coalesced row read (degree and row issued together,
+    //      or taken from the prediction), filter through the seen cache
     const uint32_t u = key_id(pk);
-    const uint32_t deg = min((uint32_t)a.counts[u], a.R);
-    uint32_t v = kInvalid32;
-    if (lane < deg) v = a.edges[(size_t)u * a.R + lane];
+    uint32_t cu, v;
+    if (u == spec_u) {
+      cu = spec_c;
+      v = spec_v;
+    } else {
+      cu = a.counts[u];
+      v = a.edges[(size_t)u * a.R + elane];
+    }
+    // the next prediction's reads, unconditional (a valid id either way)
+    {
+      const uint32_t su = next_u != kInvalid32 ? next_u : u;
+      spec_u = next_u;
+      spec_c = a.counts[su];
+      spec_v = a.edges[(size_t)su * a.R + elane];
+    }
+    const uint32_t deg = min(cu, a.R);
     bool isnew = lane < deg && (int64_t)v < a.n;
     if constexpr (STATS) {
       // exact filter: first time this query sees v
@@ -228,8 +256,8 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
 
     // ---- score the new neighbours (4 lanes per vector)
     uint32_t base = 0;
-    for (; base + 16 < nm; base += 32) score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg);
-    if (base < nm) score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg);
+    for (; base + 16 < nm; base += 32) score_pass<CPL, METRIC, INTX, true>(a, qf, cand, T, base, nm, ql, qg);
+    if (base < nm) score_pass<CPL, METRIC, INTX, false>(a, qf, cand, T, base, nm, ql, qg);
     wave_sync();
 
     // ---- sort the new keys, drop duplicates and members of B
@@ -345,9 +373,9 @@ size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {
   return (size_t)2 * r.beam_width * 8 + 64 * 8 + 64 * 4 + std::max<size_t>(((size_t)1 << hb) * entry, 4);
 }
 
-template <int CPL, int METRIC, bool STATS>
+template <int CPL, int METRIC, bool STATS, bool INTX = false>
 static void launch_one(const SearchArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  auto kern = beam_search_kernel<CPL, METRIC, STATS>;
+  auto kern = beam_search_kernel<CPL, METRIC, STATS, INTX>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
               "set LDS size");
@@ -412,10 +440,12 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
   const size_t lds = beam_search_lds_bytes(g, r);
   const uint32_t cpl = (a.nchunks + 3) / 4;
   const dim3 grid(r.nq);
+  const bool intx = r.int_exact && g.metric == kL2 && !stats;
 #define JA_LAUNCH(C)                                                                                   \
   case C: {                                                                                            \
     if (g.metric == kL2) {                                                                             \
-      if (stats) launch_one<C, kL2, true>(a, grid, lds, stream);                                       \
+      if (intx) launch_one<C, kL2, false, C != 0>(a, grid, lds, stream);                               \
+      else if (stats) launch_one<C, kL2, true>(a, grid, lds, stream);                                  \
       else launch_one<C, kL2, false>(a, grid, lds, stream);                                            \
     } else {                                                                                           \
       if (stats) launch_one<C, kIP, true>(a, grid, lds, stream);                                       \

@@ -52,6 +52,19 @@ def test_build_matches_oracle_integer_r64(jasper, oracle_lib):
     _compare(gg, og)
 
 
+@pytest.mark.parametrize("hi", [362, 363])
+def test_build_matches_oracle_integer_range_limit(jasper, oracle_lib, hi):
+    # values {0, hi} at dim 128: hi = 362 keeps dim * hi^2 just under 2^24
+    # (packed fp16 differences with v_dot2), 363 just over (fp32 chain);
+    # distances reach the limit, and the many ties test the (dist, id) order
+    rng = np.random.default_rng(14)
+    base = (rng.integers(0, 2, size=(1500, 128)) * hi).astype(np.float16)
+    base[:, :16] = rng.integers(0, hi + 1, size=(1500, 16)).astype(np.float16)
+    og = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    gg = _gpu_build(jasper, base, 32, "l2")
+    _compare(gg, og)
+
+
 def test_build_matches_oracle_ip(jasper, oracle_lib):
     base = unit(2500, 96, 13)
     og = oracle.build(base, R=32, distance="ip", alpha=1.2)
