@@ -26,6 +26,7 @@
 #include "search.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 namespace jasper_amd {
@@ -133,7 +134,12 @@ __device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) 
   return l;
 }
 
+#ifndef JASPER_GRAM_WAVES
+#define JASPER_GRAM_WAVES 3
+#endif
+
 static size_t prune_lds_bytes() { return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4; }
+static_assert(kGramLdsWords <= kCandBuf, "the Gram prune's scratch reuses the source list");
 
 template <int CPL, int METRIC, bool INTX>
 __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
@@ -175,8 +181,15 @@ __global__ void mark_heads_kernel(const uint64_t* sorted, uint32_t n, uint32_t* 
   if (i == 0 || (sorted[i - 1] >> 32) != (k >> 32)) heads[atomicAdd(n_heads, 1u)] = i;
 }
 
+// The Gram prune holds 96 candidate rows of up to 128 values in registers
+// (96 VGPRs) beside its accumulators; three waves per SIMD keep it unspilled.
+template <int CPL, bool INTX>
+constexpr int reverse_waves_per_simd() {
+  return INTX && CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
+}
+
 template <int CPL, int METRIC, bool INTX>
-__global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
+__global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void reverse_prune_kernel(PruneKernelArgs a) {
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
   const uint32_t lane = lane_id();
@@ -221,7 +234,20 @@ __global__ __launch_bounds__(64) void reverse_prune_kernel(PruneKernelArgs a) {
     wave_sync();
     const uint32_t nc = nE + taken;
     sort_candidates(l.C, nc);
-    const uint32_t ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+    uint32_t ns;
+    if constexpr (INTX && CPL >= 1 && CPL <= 4) {
+      // integer rows, up to 96 candidates: pair distances on the matrix cores
+      if (nc <= kGramMaxCands && a.pc.nlimit <= kGramMaxChunks) {
+        float* gn = reinterpret_cast<float*>(l.srcs);
+        if (nc <= 32) ns = robust_prune_gram<1>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+        else if (nc <= 64) ns = robust_prune_gram<2>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+        else ns = robust_prune_gram<3>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+      } else {
+        ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+      }
+    } else {
+      ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+    }
     write_selection(a, w, ns, l.S_ids, l.S_dist);
     wave_sync();
   }
@@ -352,7 +378,14 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   const size_t plds = prune_lds_bytes();
   // integer-valued rows in the exact range: packed-difference distances,
   // the same bits as the fp32 chain (int_exact_l2)
-  const bool intx = int_exact_l2(g, stream);
+  int32_t int_lo = 0;
+  const bool intx = int_exact_l2(g, stream, &int_lo);
+  {
+    const _Float16 lo = (_Float16)int_lo;  // exact: an fp16 value of the rows
+    uint16_t bits;
+    std::memcpy(&bits, &lo, 2);
+    pa.pc.lo2 = (uint32_t)bits * 0x10001u;
+  }
 
   BuildStats st;
   st.max_batch = mb;

@@ -134,7 +134,7 @@ __global__ void int_range_kernel(const uint16_t* __restrict__ v, size_t count, i
   }
 }
 
-bool int_exact_l2(const Graph& g, hipStream_t stream) {
+bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out) {
   static const bool enabled = [] {
     const char* e = std::getenv("JASPER_INT_EXACT");
     return !(e && std::atoi(e) == 0);
@@ -154,7 +154,9 @@ bool int_exact_l2(const Graph& g, hipStream_t stream) {
   hip_check(hipFreeAsync(d, stream), "free range");
   if (h[0] != 0 || h[1] > h[2]) return false;
   const double span = (double)h[2] - (double)h[1];
-  return span <= 2048.0 && (double)g.dim * span * span < 16777216.0;
+  if (!(span <= 2048.0 && (double)g.dim * span * span < 16777216.0)) return false;
+  if (lo_out) *lo_out = h[1];
+  return true;
 }
 
 void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream) {

@@ -90,8 +90,9 @@ void download_graph(const Graph& g, HostGraph& h, bool with_vectors = true);
 // summation order: every stored value (padding included) is an integer, the
 // values span at most 2,048 (exact fp16 differences) and dim * span^2 < 2^24
 // (exact fp32 partial sums). Scans the device rows; synchronises `stream`.
+// lo_out receives the smallest value when the test passes.
 // JASPER_INT_EXACT=0 turns the packed form off (measurement).
-bool int_exact_l2(const Graph& g, hipStream_t stream);
+bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out = nullptr);
 
 // Uploads a contiguous host or device fp16 matrix [n, dim] into rows padded
 // to dp on the device graph (vecs must be allocated).

@@ -23,6 +23,7 @@ struct PruneCtx {
   uint32_t nlimit;   // L2: chunks summed (dim / 8); IP: elements summed (dim)
   uint32_t R;
   float alpha;
+  uint32_t lo2;      // integer-valued rows: the smallest value, as two fp16
 };
 
 // The left operand of a loaded row: L2 keeps the fp16 chunks; IP converts
@@ -142,6 +143,179 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
       ns += 1;
       live = ballot(valid && !pruned && ql == 0 && qg > g);
     }
+  }
+  wave_sync();
+  return ns;
+}
+
+// ------------------------------------------------ integer rows: Gram form
+// On integer-valued rows within the exact range (int_exact_l2), shifted by
+// their smallest value lo to a' = a - lo in [0, span] (exact in fp16), every
+// product and partial sum of a'_i . a'_j and |a'_i|^2 is an integer below
+// 2^24, so the matrix cores' fp32 accumulation is exact in any order, and
+//   d(i, j) = (|a'_i|^2 - a'_i.a'_j) + (|a'_j|^2 - a'_i.a'_j)
+// is the exact integer the reference's fp32 chain produces: each bracket is
+// an exact integer of magnitude below 2^24 and so is the sum. One
+// v_mfma_f32_32x32x16_f16 chain per pair of 32-candidate tiles gives all
+// pair distances of up to 96 candidates; the prune then works on bits:
+// dom(i, j) = [j < i and d(i, j) * alpha < d_i], and candidate i is
+// selected when no selected j has dom(i, j) -- the reference rule, as each
+// selection settles every candidate before it.
+constexpr uint32_t kGramMaxCands = 96;    // three tiles of 32
+constexpr uint32_t kGramMaxChunks = 16;   // rows of up to 128 fp16 values
+
+typedef _Float16 gram_h8 __attribute__((ext_vector_type(8)));
+typedef float gram_f16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t sub_half2(uint32_t a, uint32_t b) {
+  half2_t x, y;
+  __builtin_memcpy(&x, &a, 4);
+  __builtin_memcpy(&y, &b, 4);
+  const half2_t d = x - y;
+  uint32_t r;
+  __builtin_memcpy(&r, &d, 4);
+  return r;
+}
+
+__device__ __forceinline__ gram_h8 as_gram_h8(const uint4& x) {
+  gram_h8 r;
+  __builtin_memcpy(&r, &x, 16);
+  return r;
+}
+
+// C: sorted keys [0, nc) in LDS, nc <= 32 * T; p.nlimit <= kGramMaxChunks.
+// gn: LDS scratch of kGramLdsWords words. Writes the selection to S_ids /
+// S_dist and returns |S| (the selection robust_prune_wave makes).
+constexpr uint32_t kGramLdsWords = 2 * kGramMaxCands + 3 * kGramMaxCands;
+
+template <int T>
+__device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
+                                      uint32_t* S_ids, float* S_dist, float* gn) {
+  static_assert(T >= 1 && T <= 3, "one to three tiles");
+  constexpr int KS = kGramMaxChunks / 2;  // 16 fp16 values per step
+  const uint32_t lane = lane_id();
+  const uint32_t r = lane & 31u, h = lane >> 5;
+  float* gcd = gn + kGramMaxCands;
+  // dom[i * 3 + t2]: bit b set when candidate 32 t2 + b < i prunes i
+  uint32_t* dom = reinterpret_cast<uint32_t*>(gcd + kGramMaxCands);
+
+  // MFMA operand of tile t, step s: lane (r, h) holds values 16s + 8h .. +8
+  // of candidate 32t + r, shifted; steps past the summed length are zero
+  uint4 fr[T][KS];
+  float nrm[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const uint32_t i = 32u * (uint32_t)t + r;
+    const uint64_t key = i < nc ? C[i] : kEmptyKey;
+    const uint32_t id = i < nc ? key_id(key) : self;
+    const uint4* row = p.vecs + (size_t)id * p.nchunks;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t c = 2u * (uint32_t)s + h;
+      fr[t][s] = row[min(c, p.nchunks - 1u)];
+    }
+    if (h == 0) gcd[i] = key_dist(key);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t c = 2u * (uint32_t)s + h;
+      const uint32_t keep = c < p.nlimit ? ~0u : 0u;  // per word: no struct select
+      uint4 x = fr[t][s];
+      x.x = sub_half2(x.x, p.lo2) & keep;
+      x.y = sub_half2(x.y, p.lo2) & keep;
+      x.z = sub_half2(x.z, p.lo2) & keep;
+      x.w = sub_half2(x.w, p.lo2) & keep;
+      fr[t][s] = x;
+      acc = dot2_sqdiff(x.x, 0u, acc);
+      acc = dot2_sqdiff(x.y, 0u, acc);
+      acc = dot2_sqdiff(x.z, 0u, acc);
+      acc = dot2_sqdiff(x.w, 0u, acc);
+    }
+    nrm[t] = acc + xor_lane_f<32>(acc);  // exact: integers below 2^24
+    if (h == 0) gn[32u * (uint32_t)t + r] = nrm[t];
+  }
+  wave_sync();
+
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int t2 = 0; t2 <= t; ++t2) {
+      gram_f16 acc = {};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_gram_h8(fr[t][s]), as_gram_h8(fr[t2][s]), acc, 0, 0, 0);
+      // lane holds column j = 32 t2 + r (whose norm it holds) and rows
+      // 32 t + 8g + 4h + q
+      const float nj = nrm[t2];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 ni = *reinterpret_cast<const float4*>(gn + 32 * t + 8 * g + 4 * h);
+        const float4 cd = *reinterpret_cast<const float4*>(gcd + 32 * t + 8 * g + 4 * h);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float gij = acc[4 * g + q];
+          const float niq = q == 0 ? ni.x : q == 1 ? ni.y : q == 2 ? ni.z : ni.w;
+          const float cdq = q == 0 ? cd.x : q == 1 ? cd.y : q == 2 ? cd.z : cd.w;
+          const float d = (niq - gij) + (nj - gij);
+          bool bit = d * p.alpha < cdq;
+          if (t == t2) bit = bit && r < (uint32_t)(8 * g + 4 * (int)h + q);
+          const uint64_t m = ballot(bit);
+          // low half: row 8g + q (lanes h = 0), high half: row 8g + 4 + q
+          if (lane == 0) {
+            dom[(32 * t + 8 * g + q) * 3 + t2] = (uint32_t)m;
+            dom[(32 * t + 8 * g + 4 + q) * 3 + t2] = (uint32_t)(m >> 32);
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  wave_sync();
+
+  // selection: the first live candidate after the last selection is taken;
+  // its column bit prunes the later candidates it dominates (rows before
+  // it, whose words were not written, are settled and no longer live)
+  uint32_t dwA[T], dwB[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    dwA[t] = dom[lane * 3u + (uint32_t)t];
+    dwB[t] = T == 3 && lane < 32u ? dom[(64u + lane) * 3u + (uint32_t)t] : 0u;
+  }
+  const bool validA = lane < nc && key_id(C[lane]) != self;
+  const bool validB = T == 3 && lane < 32u && 64u + lane < nc && key_id(C[64u + lane]) != self;
+  bool prA = false, prB = false;
+  uint64_t liveA = ballot(validA), liveB = ballot(validB);
+  uint32_t ns = 0;
+  while (ns < p.R) {
+    liveA &= ~ballot(prA);
+    liveB &= ~ballot(prB);
+    uint32_t i;
+    if (liveA) {
+      i = (uint32_t)__builtin_ctzll(liveA);
+      liveA &= liveA - 1u;
+    } else if (liveB) {
+      i = 64u + (uint32_t)__builtin_ctzll(liveB);
+      liveB &= liveB - 1u;
+    } else {
+      break;
+    }
+    if (lane == 0) {
+      const uint64_t k = C[i];
+      S_ids[ns] = key_id(k);
+      S_dist[ns] = key_dist(k);
+    }
+    ns += 1;
+    const uint32_t tc = i >> 5, b = i & 31u;
+    uint32_t wA = dwA[0], wB = dwB[0];
+#pragma unroll
+    for (int t = 1; t < T; ++t) {
+      if (tc == (uint32_t)t) { wA = dwA[t]; wB = dwB[t]; }
+    }
+    prA = prA || ((wA >> b) & 1u);
+    prB = prB || ((wB >> b) & 1u);
   }
   wave_sync();
   return ns;
