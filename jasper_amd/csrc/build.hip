@@ -63,21 +63,30 @@ struct PruneKernelArgs {
   const uint32_t* n_heads;
 };
 
-// Appends the existing edges of v to C (keys with their stored bf16
-// distances); returns how many were appended.
-__device__ __forceinline__ uint32_t gather_existing(const PruneKernelArgs& a, uint32_t v, uint64_t* C) {
-  const uint32_t lane = lane_id();
+// The adjacency row of v as loaded: degree, and per lane one slot (lanes
+// past R read slot R - 1), issued together with no dependence on the degree.
+struct ExistingRow {
+  uint32_t cnt, id;
+  uint16_t ed;
+};
+
+__device__ __forceinline__ ExistingRow load_existing(const PruneKernelArgs& a, uint32_t v) {
   const uint32_t R = a.pc.R;
-  const uint32_t cnt = a.counts[v];
-  bool ok = false;
-  uint64_t key = kEmptyKey;
-  if (lane < cnt && lane < R) {
-    const uint32_t id = a.edges[(size_t)v * R + lane];
-    ok = id != kInvalid32;
-    key = make_key(bf2f(a.edist[(size_t)v * R + lane]), id);
-  }
+  const size_t o = (size_t)v * R + min(lane_id(), R - 1u);
+  ExistingRow e;
+  e.cnt = a.counts[v];
+  e.id = a.edges[o];
+  e.ed = a.edist[o];
+  return e;
+}
+
+// Appends the loaded existing edges to C (keys with their stored bf16
+// distances); returns how many were appended.
+__device__ __forceinline__ uint32_t append_existing(const ExistingRow& e, uint32_t R, uint64_t* C) {
+  const uint32_t lane = lane_id();
+  const bool ok = lane < e.cnt && lane < R && e.id != kInvalid32;
   const uint64_t m = ballot(ok);
-  if (ok) C[mbcnt(m)] = key;
+  if (ok) C[mbcnt(m)] = make_key(bf2f(e.ed), e.id);
   return (uint32_t)__builtin_popcountll(m);
 }
 
@@ -135,7 +144,7 @@ __device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) 
 }
 
 #ifndef JASPER_GRAM_WAVES
-#define JASPER_GRAM_WAVES 3
+#define JASPER_GRAM_WAVES 2
 #endif
 
 static size_t prune_lds_bytes() { return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4; }
@@ -150,8 +159,9 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   const uint32_t v = a.batch_offset + bid;
   const uint32_t R = a.pc.R;
 
-  uint32_t nc = gather_existing(a, v, l.C);
+  const ExistingRow er = load_existing(a, v);
   const uint32_t nv = a.visited_counts[bid];
+  uint32_t nc = append_existing(er, R, l.C);
   for (uint32_t base = 0; base < nv; base += 64) {
     const uint32_t i = base + lane;
     bool ok = i < nv;
@@ -182,7 +192,8 @@ __global__ void mark_heads_kernel(const uint64_t* sorted, uint32_t n, uint32_t* 
 }
 
 // The Gram prune holds 96 candidate rows of up to 128 values in registers
-// (96 VGPRs) beside its accumulators; three waves per SIMD keep it unspilled.
+// (96 VGPRs) beside its accumulators; two waves per SIMD keep it unspilled (three
+// spill, and measured slower).
 template <int CPL, bool INTX>
 constexpr int reverse_waves_per_simd() {
   return INTX && CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
@@ -197,16 +208,25 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
   const uint32_t R = a.pc.R;
   const uint32_t nh = *a.n_heads;
   const uint32_t max_cands = kBuildMaxResult + R;
-  for (uint32_t h = blockIdx.x; h < nh; h += gridDim.x) {
-    const uint32_t start = a.heads[h];
-    const uint32_t w = (uint32_t)(a.sorted_pairs[start] >> 32);
-    const uint32_t nE = gather_existing(a, w, l.C);
+  uint32_t h = blockIdx.x;
+  if (h >= nh) return;
+  // the first pair of the next head is read one target ahead
+  uint32_t start = a.heads[h];
+  uint32_t w = (uint32_t)(a.sorted_pairs[start] >> 32);
+  for (; h < nh; h += gridDim.x) {
+    // this target's reads, issued together: its adjacency row, its row of
+    // values, the first 64 pairs of its group, and the next head
+    const ExistingRow er = load_existing(a, w);
+    RowFrag<CPL> xw;
+    load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
+    uint64_t key = a.sorted_pairs[min(start + lane, a.n_pairs - 1u)];
+    if (start + lane >= a.n_pairs) key = kEmptyKey;
+    const uint32_t start_next = a.heads[min(h + gridDim.x, nh - 1u)];
+    const uint32_t nE = append_existing(er, R, l.C);
     // sources of w in ascending id order, self skipped, capped at 256 + R
     const uint32_t cap = max_cands - nE;
     uint32_t taken = 0;
-    for (uint32_t pos = start; taken < cap; pos += 64) {
-      const uint32_t i = pos + lane;
-      const uint64_t key = i < a.n_pairs ? a.sorted_pairs[i] : kEmptyKey;
+    for (uint32_t pos = start;;) {
       const bool same = key != kEmptyKey && (uint32_t)(key >> 32) == w;
       const uint32_t src = (uint32_t)key;
       const bool ok = same && src != w;
@@ -214,12 +234,14 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
       const uint32_t rank = mbcnt(m);
       if (ok && taken + rank < cap) l.srcs[taken + rank] = src;
       taken = min(cap, taken + (uint32_t)__builtin_popcountll(m));
-      if (ballot(!same)) break;
+      if (taken >= cap || ballot(!same)) break;
+      pos += 64;
+      const uint32_t i = pos + lane;
+      key = i < a.n_pairs ? a.sorted_pairs[i] : kEmptyKey;
     }
+    const uint32_t w_next = (uint32_t)(a.sorted_pairs[start_next] >> 32);
     wave_sync();
     // d(w, v) for every source (compute_distance(src_vec = w, sink_vec = v))
-    RowFrag<CPL> xw;
-    load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
     LeftFrag<CPL, METRIC> wf;
     left_from_row<CPL, METRIC>(xw, ql, wf);
     for (uint32_t base = 0; base < taken; base += 16) {
@@ -250,6 +272,8 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
     }
     write_selection(a, w, ns, l.S_ids, l.S_dist);
     wave_sync();
+    start = start_next;
+    w = w_next;
   }
 }
 

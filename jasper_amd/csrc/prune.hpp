@@ -186,7 +186,12 @@ __device__ __forceinline__ gram_h8 as_gram_h8(const uint4& x) {
 // C: sorted keys [0, nc) in LDS, nc <= 32 * T; p.nlimit <= kGramMaxChunks.
 // gn: LDS scratch of kGramLdsWords words. Writes the selection to S_ids /
 // S_dist and returns |S| (the selection robust_prune_wave makes).
-constexpr uint32_t kGramLdsWords = 2 * kGramMaxCands + 3 * kGramMaxCands;
+constexpr uint32_t kGramLdsWords = 2 * kGramMaxCands;
+
+// Spreads 16 bits (bit 4g + q) to bit 8g + q of a word.
+__device__ __forceinline__ uint32_t spread_nibbles(uint32_t w) {
+  return (w & 0xFu) | ((w & 0xF0u) << 4) | ((w & 0xF00u) << 8) | ((w & 0xF000u) << 12);
+}
 
 template <int T>
 __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
@@ -196,8 +201,6 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   const uint32_t lane = lane_id();
   const uint32_t r = lane & 31u, h = lane >> 5;
   float* gcd = gn + kGramMaxCands;
-  // dom[i * 3 + t2]: bit b set when candidate 32 t2 + b < i prunes i
-  uint32_t* dom = reinterpret_cast<uint32_t*>(gcd + kGramMaxCands);
 
   // MFMA operand of tile t, step s: lane (r, h) holds values 16s + 8h .. +8
   // of candidate 32t + r, shifted; steps past the summed length are zero
@@ -239,6 +242,14 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   }
   wave_sync();
 
+  // W[t][t2], lane (r, h): bit b set when candidate 32 t + b is pruned by
+  // candidate 32 t2 + r (which precedes it): the column of the pair block
+  uint32_t W[T][T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int t2 = 0; t2 < T; ++t2) W[t][t2] = 0u;
+  }
 #pragma unroll
   for (int t = 0; t < T; ++t) {
 #pragma unroll
@@ -250,6 +261,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
       // lane holds column j = 32 t2 + r (whose norm it holds) and rows
       // 32 t + 8g + 4h + q
       const float nj = nrm[t2];
+      uint32_t w16 = 0u;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float4 ni = *reinterpret_cast<const float4*>(gn + 32 * t + 8 * g + 4 * h);
@@ -262,60 +274,64 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
           const float d = (niq - gij) + (nj - gij);
           bool bit = d * p.alpha < cdq;
           if (t == t2) bit = bit && r < (uint32_t)(8 * g + 4 * (int)h + q);
-          const uint64_t m = ballot(bit);
-          // low half: row 8g + q (lanes h = 0), high half: row 8g + 4 + q
-          if (lane == 0) {
-            dom[(32 * t + 8 * g + q) * 3 + t2] = (uint32_t)m;
-            dom[(32 * t + 8 * g + 4 + q) * 3 + t2] = (uint32_t)(m >> 32);
-          }
+          w16 |= bit ? (1u << (4 * g + q)) : 0u;
         }
       }
+      const uint32_t w = spread_nibbles(w16) << (4u * h);  // rows 8g + 4h + q
+      W[t][t2] = w | xor_lane<32>(w);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  wave_sync();
-
-  // selection: the first live candidate after the last selection is taken;
-  // its column bit prunes the later candidates it dominates (rows before
-  // it, whose words were not written, are settled and no longer live)
-  uint32_t dwA[T], dwB[T];
+  // column words by candidate: lane i % 64 of set A (candidates 0..63) or
+  // set B (64..95) holds, per row tile t, the rows that candidate prunes
+  uint32_t colA[T], colB[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    dwA[t] = dom[lane * 3u + (uint32_t)t];
-    dwB[t] = T == 3 && lane < 32u ? dom[(64u + lane) * 3u + (uint32_t)t] : 0u;
+    colA[t] = T >= 2 && h ? W[t][T >= 2 ? 1 : 0] : W[t][0];
+    colB[t] = T == 3 ? W[t][T - 1] : 0u;
   }
+
+  // selection: the first live candidate is taken and the candidates it
+  // prunes leave the live set (every one before it is already settled)
   const bool validA = lane < nc && key_id(C[lane]) != self;
   const bool validB = T == 3 && lane < 32u && 64u + lane < nc && key_id(C[64u + lane]) != self;
-  bool prA = false, prB = false;
   uint64_t liveA = ballot(validA), liveB = ballot(validB);
+  uint64_t selA = 0, selB = 0;
   uint32_t ns = 0;
-  while (ns < p.R) {
-    liveA &= ~ballot(prA);
-    liveB &= ~ballot(prB);
-    uint32_t i;
+  while (ns < p.R && (liveA | liveB)) {
+    uint32_t p0, p1, p2;
     if (liveA) {
-      i = (uint32_t)__builtin_ctzll(liveA);
+      const uint32_t i = (uint32_t)__builtin_ctzll(liveA);
       liveA &= liveA - 1u;
-    } else if (liveB) {
-      i = 64u + (uint32_t)__builtin_ctzll(liveB);
-      liveB &= liveB - 1u;
+      selA |= 1ull << i;
+      p0 = (uint32_t)__builtin_amdgcn_readlane((int)colA[0], (int)i);
+      p1 = T >= 2 ? (uint32_t)__builtin_amdgcn_readlane((int)colA[T >= 2 ? 1 : 0], (int)i) : 0u;
+      p2 = T == 3 ? (uint32_t)__builtin_amdgcn_readlane((int)colA[T - 1], (int)i) : 0u;
     } else {
-      break;
+      const uint32_t i = (uint32_t)__builtin_ctzll(liveB);
+      liveB &= liveB - 1u;
+      selB |= 1ull << i;
+      p0 = 0u;  // rows before the candidate are settled
+      p1 = 0u;
+      p2 = (uint32_t)__builtin_amdgcn_readlane((int)colB[T - 1], (int)i);
     }
-    if (lane == 0) {
-      const uint64_t k = C[i];
-      S_ids[ns] = key_id(k);
-      S_dist[ns] = key_dist(k);
-    }
+    liveA &= ~((uint64_t)p0 | ((uint64_t)p1 << 32));
+    liveB &= ~(uint64_t)p2;
     ns += 1;
-    const uint32_t tc = i >> 5, b = i & 31u;
-    uint32_t wA = dwA[0], wB = dwB[0];
-#pragma unroll
-    for (int t = 1; t < T; ++t) {
-      if (tc == (uint32_t)t) { wA = dwA[t]; wB = dwB[t]; }
-    }
-    prA = prA || ((wA >> b) & 1u);
-    prB = prB || ((wB >> b) & 1u);
+  }
+  // the selection in candidate order
+  const uint32_t nA = (uint32_t)__builtin_popcountll(selA);
+  if ((selA >> lane) & 1ull) {
+    const uint32_t k = mbcnt(selA);
+    const uint64_t key = C[lane];
+    S_ids[k] = key_id(key);
+    S_dist[k] = key_dist(key);
+  }
+  if (lane < 32u && ((selB >> lane) & 1ull)) {
+    const uint32_t k = nA + mbcnt(selB);
+    const uint64_t key = C[64u + lane];
+    S_ids[k] = key_id(key);
+    S_dist[k] = key_dist(key);
   }
   wave_sync();
   return ns;
