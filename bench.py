@@ -233,6 +233,7 @@ def main() -> int:
     achieved = alg_bytes / (kernel_ms / 1000.0) / 1e9
     log(f"bw={chosen}: {ms_per_step:.3f} ms/step, kernel {kernel_ms:.3f} ms, qps={qps:,.0f}, "
         f"recall={final_recall:.4f}, hops/q={hops / args.nq:.1f}, scored/q={scored / args.nq:.1f}, "
+        f"predicted adjacency {st[:, 3].sum() / max(hops, 1):.2f} of hops, "
         f"{alg_bytes / args.nq / 1e3:.1f} KB/q, {achieved:.0f} GB/s")
 
     result = {

@@ -134,7 +134,8 @@ int64_t jasperx_export_graph(int64_t handle, uint32_t* edges, uint16_t* edge_dis
 int64_t jasperx_last_build_stats(double* out7);
 /* Measurement run of the plain search: same traversal with an exact
  * per-query seen set, writing per-query work counters to host memory
- * out_stats[n_queries * 4] = {hops, sum of degrees read, vectors scored, 0}.
+ * out_stats[n_queries * 4] = {hops, sum of degrees read, vectors scored,
+ * hops whose adjacency row was read one hop ahead}.
  * Used to compute algorithmic bytes per launch; not a search entry point. */
 int64_t jasperx_search_stats(int64_t handle, const void* queries, int64_t n_queries, int64_t dim,
                              int64_t k, int64_t beam_width, int64_t limit, uint32_t* out_stats,

@@ -584,7 +584,8 @@ class Graph:
                      limit: int | None = None) -> np.ndarray:
         """Per-query work counters of the plain search [n_queries, 4]:
         hops, adjacency entries read, vectors scored (exact distinct count),
-        0. A measurement extension used for algorithmic-bytes accounting."""
+        hops whose adjacency row was read one hop ahead (predicted pop). A
+        measurement extension used for algorithmic-bytes accounting."""
         self._check_alive()
         queries = self._query_check(queries)
         nq = queries.size(0)

@@ -52,7 +52,7 @@ struct SearchArgs {
   // measurement mode: exact per-query seen bitmap in HBM and work counters
   uint32_t* seen_bits;      // [nq, seen_words]
   uint32_t seen_words;
-  uint32_t* stats;          // [nq, 4]: hops, sum of degrees, vectors scored, 0
+  uint32_t* stats;          // [nq, 4]: hops, sum of degrees, vectors scored, predicted hops
 };
 
 // Seen cache: returns true when v is recorded, else records it (replacing
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     }
   }
   wave_sync();
-  uint32_t st_hops = 0, st_deg = 0, st_scored = 1;
+  uint32_t st_hops = 0, st_deg = 0, st_scored = 1, st_pred = 0;
 
   uint64_t* B = buf0;
   uint64_t* NB = buf1;
@@ -222,6 +222,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     if (u == spec_u) {
       cu = spec_c;
       v = spec_v;
+      if constexpr (STATS) st_pred += 1;
     } else {
       cu = a.counts[u];
       v = a.edges[(size_t)u * a.R + elane];
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       a.stats[(size_t)qid * 4 + 0] = st_hops;
       a.stats[(size_t)qid * 4 + 1] = st_deg;
       a.stats[(size_t)qid * 4 + 2] = st_scored;
-      a.stats[(size_t)qid * 4 + 3] = 0;
+      a.stats[(size_t)qid * 4 + 3] = st_pred;
     }
   }
 }

@@ -25,7 +25,8 @@ struct SearchRequest {
   bool int_exact = false;
   // measurement mode (exact seen set, work counters); both or neither
   uint32_t* seen_bits = nullptr;   // [nq, ceil(n/32)], zeroed by the caller
-  uint32_t* stats = nullptr;       // [nq, 4]: hops, sum of degrees, vectors scored, 0
+  uint32_t* stats = nullptr;       // [nq, 4]: hops, sum of degrees, vectors scored,
+                                   // hops whose adjacency was read one hop ahead
 };
 
 // Launches the search kernel on `stream`; asynchronous.

@@ -151,3 +151,19 @@ def test_search_matches_oracle_long_rows(jasper, oracle_lib, tmp_path, distance,
         rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
         msg = compare_search(ids, d, rid, rd)
         assert msg is None, f"bw={bw}: {msg}"
+
+
+@pytest.mark.parametrize("bw", [16, 64])
+def test_search_stats_match_oracle_counters(jasper, c1_small, tmp_path, bw):
+    # the measurement run (exact seen set) walks the same traversal as the
+    # reference: hops and degrees read equal the oracle's, vectors scored
+    # equal the oracle's distinct scored ids; predicted hops are a subset
+    base, q, g = c1_small
+    gg = _load(jasper, g, tmp_path)
+    st = gg.search_stats(torch.from_numpy(q).cuda(), k=10, beam_width=bw).astype(np.int64)
+    _, _, ost = oracle.beam_search(g, q, k=10, beam_width=bw, stats=True)
+    ost = ost.astype(np.int64)
+    assert np.array_equal(st[:, 0], ost[:, 0])
+    assert np.array_equal(st[:, 1], ost[:, 1])
+    assert np.array_equal(st[:, 2], ost[:, 3])
+    assert (st[:, 3] >= 0).all() and (st[:, 3] <= st[:, 0]).all()
