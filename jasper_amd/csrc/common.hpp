@@ -114,6 +114,22 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
   }
 }
 
+// Value of lane 63 - lane: a mirror within each row of 16 lanes (DPP)
+// composed with xor 16 and xor 32.
+__device__ __forceinline__ uint32_t reverse_lanes(uint32_t v) {
+  const uint32_t m = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);  // row_mirror
+  return xor_lane<32>(xor_lane<16>(m));
+}
+
+__device__ __forceinline__ uint64_t reverse_lanes64(uint64_t v) {
+  return (uint64_t)reverse_lanes((uint32_t)v) | ((uint64_t)reverse_lanes((uint32_t)(v >> 32)) << 32);
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  return (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l) |
+         ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l) << 32);
+}
+
 template <int J>
 __device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
   return (uint64_t)xor_lane<J>((uint32_t)v) | ((uint64_t)xor_lane<J>((uint32_t)(v >> 32)) << 32);

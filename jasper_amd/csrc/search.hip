@@ -261,9 +261,40 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     if (base < nm) score_pass<CPL, METRIC, INTX, false>(a, qf, cand, T, base, nm, ql, qg);
     wave_sync();
 
-    // ---- sort the new keys, drop duplicates and members of B
+    // ---- sort the new keys
     uint64_t t = lane < nm ? T[lane] : kEmptyKey;
     t = wave_sort_upto(t, nm);
+    if (bw <= 64u) {
+      // B fits one key per lane: bitonic merge in registers. B ascending
+      // against the new keys reversed: the lane-wise minima are a bitonic
+      // sequence holding the 64 smallest keys, sorted by six more stages.
+      // Equal ranks (a re-scored member of B, an id scored twice) are left
+      // to the general path below: they sit side by side in the merged
+      // order, or across its 64th key.
+      const uint64_t b = lane < cnt ? B[lane] : kEmptyKey;
+      const uint64_t tr = reverse_lanes64(t);
+      const bool lt = b < tr;
+      uint64_t x0 = lt ? b : tr;
+      const uint64_t x1 = lt ? tr : b;
+      x0 = bitonic_merge_steps<64, 32>(x0, lane);
+      const uint64_t nx = __shfl_down(x0, 1, 64);
+      const uint64_t last = readlane64(x0, 63);
+      const bool dup = (lane < 63u && x0 != kEmptyKey && key_rank(x0) == key_rank(nx)) ||
+                       (last != kEmptyKey && key_rank(x1) == key_rank(last));
+      if (ballot(dup) == 0) {
+        const uint32_t ncnt = min(cnt + nm, bw);
+        if (lane < ncnt) NB[lane] = x0;
+        const uint64_t unv = ballot(lane < ncnt && !key_visited(x0));
+        hint = unv ? (uint32_t)__builtin_ctzll(unv) : ncnt;
+        cnt = ncnt;
+        uint64_t* tmp = B;
+        B = NB;
+        NB = tmp;
+        wave_sync();
+        continue;
+      }
+    }
+    // ---- general path: drop duplicates and members of B, merge by rank
     const uint64_t prev = __shfl_up(t, 1, 64);
     bool keep = lane < nm && !(lane > 0 && key_rank(prev) == key_rank(t));
     uint32_t lb = 0;

@@ -167,3 +167,48 @@ def test_search_stats_match_oracle_counters(jasper, c1_small, tmp_path, bw):
     assert np.array_equal(st[:, 1], ost[:, 1])
     assert np.array_equal(st[:, 2], ost[:, 3])
     assert (st[:, 3] >= 0).all() and (st[:, 3] <= st[:, 0]).all()
+
+
+_SMALL_CACHE_CHILD = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import jasper_amd
+g = jasper_amd.Graph.load(sys.argv[2], dim=int(sys.argv[3]), n_neighbors=int(sys.argv[4]), distance="l2")
+q = torch.from_numpy(np.load(sys.argv[5])).cuda()
+out = {}
+for bw in (16, 48, 64):
+    ids, d = g.search(q, k=10, beam_width=bw)
+    torch.cuda.synchronize()
+    out[f"ids{bw}"] = ids.cpu().numpy()
+    out[f"d{bw}"] = d.cpu().numpy()
+np.savez(sys.argv[6], **out)
+print("child done", flush=True)
+"""
+
+
+def test_search_small_seen_cache_matches_oracle(jasper, oracle_lib, tmp_path):
+    # a 256-entry seen cache forgets most of the ~1,000 vectors a query
+    # scores, so members of the beam are re-scored and come back as
+    # duplicates: the merge's general path (duplicates, members of B) runs
+    # on many hops beside the register merge; results must not change
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    base = integer_clustered(4000, 128, 3)
+    q = integer_clustered(64, 128, 4)
+    g = oracle.build(base, R=64, distance="l2", alpha=1.2)
+    path = tmp_path / "g.bin"
+    oracle.save_graph(g, path)
+    np.save(tmp_path / "q.npy", q)
+    env = dict(os.environ, JASPER_SEARCH_HASH_BITS="8")
+    root = str(Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _SMALL_CACHE_CHILD, root, str(path), "128", "64",
+                        str(tmp_path / "q.npy"), str(tmp_path / "out.npz")],
+                       env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = np.load(tmp_path / "out.npz")
+    for bw in (16, 48, 64):
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(out[f"ids{bw}"], out[f"d{bw}"], rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
