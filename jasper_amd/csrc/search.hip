@@ -163,12 +163,17 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   load_left<CPL, METRIC>(qrow, ql, a.nchunks, qf);
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
 
-  // B = [(medoid, d(q, medoid))]
+  // B = [(medoid, d(q, medoid))]; at bw <= 64 B lives in registers, one key
+  // per lane (`b`), and is written to LDS only for the merge's general path
+  // and the epilogue
+  const bool regb = bw <= 64u;
   uint32_t cnt = 1;
+  uint64_t b = kEmptyKey;
   {
     RowFrag<CPL> x;
     load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
     const float d = score<CPL, METRIC, INTX>(a, qf, x, ql, nlimit);
+    if (lane == 0) b = make_key(d, a.medoid);
     wave_sync();  // hash table initialised
     if (lane == 0) {
       buf0[0] = make_key(d, a.medoid);
@@ -191,27 +196,40 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   while (loop <= a.limit) {
     loop += 1;
     // ---- pop: first unvisited entry (all entries before `hint` are visited)
-    int p = -1, p2 = -1;
-    for (uint32_t base = hint; base < cnt; base += 64) {
-      const uint32_t i = base + lane;
-      const bool unv = i < cnt && !key_visited(B[i]);
-      const uint64_t m = ballot(unv);
-      if (m) {
-        p = (int)(base + (uint32_t)__builtin_ctzll(m));
-        const uint64_t m2 = m & (m - 1u);
-        if (m2) p2 = (int)(base + (uint32_t)__builtin_ctzll(m2));
-        break;
+    uint64_t pk;
+    uint32_t next_u;
+    if (regb) {
+      const uint64_t m = ballot(lane < cnt && !key_visited(b));
+      if (m == 0) break;
+      const uint32_t p = (uint32_t)__builtin_ctzll(m);
+      const uint64_t m2 = m & (m - 1u);
+      pk = readlane64(b, (int)p) | 1ull;
+      next_u = m2 ? key_id(readlane64(b, (int)__builtin_ctzll(m2))) : kInvalid32;
+      if (lane == p) b = pk;
+      if (a.visited && lane == 0) a.visited[(size_t)qid * a.max_result + vc] = pk;
+    } else {
+      int p = -1, p2 = -1;
+      for (uint32_t base = hint; base < cnt; base += 64) {
+        const uint32_t i = base + lane;
+        const bool unv = i < cnt && !key_visited(B[i]);
+        const uint64_t m = ballot(unv);
+        if (m) {
+          p = (int)(base + (uint32_t)__builtin_ctzll(m));
+          const uint64_t m2 = m & (m - 1u);
+          if (m2) p2 = (int)(base + (uint32_t)__builtin_ctzll(m2));
+          break;
+        }
       }
+      if (p < 0) break;
+      pk = B[p] | 1ull;
+      next_u = p2 >= 0 ? key_id(B[p2]) : kInvalid32;
+      wave_sync();
+      if (lane == 0) {
+        B[p] = pk;
+        if (a.visited) a.visited[(size_t)qid * a.max_result + vc] = pk;
+      }
+      hint = (uint32_t)p + 1;
     }
-    if (p < 0) break;
-    const uint64_t pk = B[p] | 1ull;
-    const uint32_t next_u = p2 >= 0 ? key_id(B[p2]) : kInvalid32;
-    wave_sync();
-    if (lane == 0) {
-      B[p] = pk;
-      if (a.visited) a.visited[(size_t)qid * a.max_result + vc] = pk;
-    }
-    hint = (uint32_t)p + 1;
     vc += 1;
     if (vc == a.max_result) break;
 
@@ -264,14 +282,13 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     // ---- sort the new keys
     uint64_t t = lane < nm ? T[lane] : kEmptyKey;
     t = wave_sort_upto(t, nm);
-    if (bw <= 64u) {
-      // B fits one key per lane: bitonic merge in registers. B ascending
-      // against the new keys reversed: the lane-wise minima are a bitonic
-      // sequence holding the 64 smallest keys, sorted by six more stages.
-      // Equal ranks (a re-scored member of B, an id scored twice) are left
-      // to the general path below: they sit side by side in the merged
-      // order, or across its 64th key.
-      const uint64_t b = lane < cnt ? B[lane] : kEmptyKey;
+    if (regb) {
+      // B one key per lane: bitonic merge in registers. B ascending against
+      // the new keys reversed: the lane-wise minima are a bitonic sequence
+      // holding the 64 smallest keys, sorted by six more stages. Equal ranks
+      // (a re-scored member of B, an id scored twice) are left to the
+      // general path below: they sit side by side in the merged order, or
+      // across its 64th key.
       const uint64_t tr = reverse_lanes64(t);
       const bool lt = b < tr;
       uint64_t x0 = lt ? b : tr;
@@ -282,17 +299,15 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       const bool dup = (lane < 63u && x0 != kEmptyKey && key_rank(x0) == key_rank(nx)) ||
                        (last != kEmptyKey && key_rank(x1) == key_rank(last));
       if (ballot(dup) == 0) {
-        const uint32_t ncnt = min(cnt + nm, bw);
-        if (lane < ncnt) NB[lane] = x0;
-        const uint64_t unv = ballot(lane < ncnt && !key_visited(x0));
-        hint = unv ? (uint32_t)__builtin_ctzll(unv) : ncnt;
-        cnt = ncnt;
-        uint64_t* tmp = B;
-        B = NB;
-        NB = tmp;
-        wave_sync();
+        cnt = min(cnt + nm, bw);
+        b = lane < cnt ? x0 : kEmptyKey;
+        lds_wave_sync();
         continue;
       }
+      // B to LDS for the general path
+      if (lane < cnt) B[lane] = b;
+      hint = 0;
+      wave_sync();
     }
     // ---- general path: drop duplicates and members of B, merge by rank
     const uint64_t prev = __shfl_up(t, 1, 64);
@@ -331,6 +346,11 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     uint64_t* tmp = B;
     B = NB;
     NB = tmp;
+    wave_sync();
+    if (regb) b = lane < cnt ? B[lane] : kEmptyKey;
+  }
+  if (regb) {
+    if (lane < cnt) B[lane] = b;
     wave_sync();
   }
 
