@@ -436,7 +436,6 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
       r.visited = visited;
       r.visited_counts = vcounts;
       r.hash_bits = 12;
-      r.int_exact = intx;
       timer.start();
       launch_beam_search(g, r, stream);
       timer.stop(st.search_ms);

@@ -880,6 +880,7 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
     hip_check(hipMalloc(&tmp, (size_t)n * g->dp * 2), "alloc rotation output");
     rotate_rows(*g->rotation, g->vecs, n, g->dp, tmp, g->dp, stream);
     hip_check(hipMemcpyAsync(g->vecs, tmp, (size_t)n * g->dp * 2, hipMemcpyDeviceToDevice, stream), "copy rotated");
+    g->int_state = 0;
     hip_check(hipStreamSynchronize(stream), "sync rotation");
     (void)hipFree(tmp);
   }

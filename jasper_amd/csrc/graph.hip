@@ -46,6 +46,7 @@ Graph::~Graph() { release(); }
 
 void Graph::allocate(int64_t n_, uint32_t dim_, uint32_t R_, int metric_, bool on_host_) {
   release();
+  int_state = 0;
   n = n_;
   dim = dim_;
   dp = pad_dim(dim_);
@@ -134,32 +135,48 @@ __global__ void int_range_kernel(const uint16_t* __restrict__ v, size_t count, i
   }
 }
 
-bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out) {
+int32_t int_exact_span(uint32_t dim) {
+  int32_t S = 2048;
+  while (S > 0 && (double)dim * (double)S * (double)S >= 16777216.0) --S;
+  return S;
+}
+
+bool int_range(const Graph& g, hipStream_t stream) {
   static const bool enabled = [] {
     const char* e = std::getenv("JASPER_INT_EXACT");
     return !(e && std::atoi(e) == 0);
   }();
-  if (!enabled || g.metric != 0 || g.n <= 0 || !g.vecs || g.on_host) return false;
-  int32_t* d = nullptr;
-  hip_check(hipMallocAsync((void**)&d, 12, stream), "alloc range");
-  const int32_t init[3] = {0, INT32_MAX, INT32_MIN};
-  hip_check(hipMemcpyAsync(d, init, 12, hipMemcpyHostToDevice, stream), "init range");
-  const size_t count = (size_t)g.n * g.dp;
-  const uint32_t grid = (uint32_t)std::min<size_t>((count + 255) / 256, 4096);
-  hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, (const uint16_t*)g.vecs, count, d);
-  hip_check(hipGetLastError(), "launch int_range_kernel");
-  int32_t h[3];
-  hip_check(hipMemcpyAsync(h, d, 12, hipMemcpyDeviceToHost, stream), "read range");
-  hip_check(hipStreamSynchronize(stream), "sync range");
-  hip_check(hipFreeAsync(d, stream), "free range");
-  if (h[0] != 0 || h[1] > h[2]) return false;
-  const double span = (double)h[2] - (double)h[1];
-  if (!(span <= 2048.0 && (double)g.dim * span * span < 16777216.0)) return false;
-  if (lo_out) *lo_out = h[1];
+  if (!enabled || g.n <= 0 || !g.vecs || g.on_host) return false;
+  if (g.int_state == 0) {
+    int32_t* d = nullptr;
+    hip_check(hipMallocAsync((void**)&d, 12, stream), "alloc range");
+    const int32_t init[3] = {0, INT32_MAX, INT32_MIN};
+    hip_check(hipMemcpyAsync(d, init, 12, hipMemcpyHostToDevice, stream), "init range");
+    const size_t count = (size_t)g.n * g.dp;
+    const uint32_t grid = (uint32_t)std::min<size_t>((count + 255) / 256, 4096);
+    hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, (const uint16_t*)g.vecs, count, d);
+    hip_check(hipGetLastError(), "launch int_range_kernel");
+    int32_t h[3];
+    hip_check(hipMemcpyAsync(h, d, 12, hipMemcpyDeviceToHost, stream), "read range");
+    hip_check(hipStreamSynchronize(stream), "sync range");
+    hip_check(hipFreeAsync(d, stream), "free range");
+    const bool ok = h[0] == 0 && h[1] <= h[2];
+    g.int_lo = ok ? h[1] : 0;
+    g.int_hi = ok ? h[2] : -1;
+    g.int_state = ok ? 1 : 2;
+  }
+  return g.int_state == 1;
+}
+
+bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out) {
+  if (g.metric != 0 || !int_range(g, stream)) return false;
+  if ((int64_t)g.int_hi - (int64_t)g.int_lo > (int64_t)int_exact_span(g.dim)) return false;
+  if (lo_out) *lo_out = g.int_lo;
   return true;
 }
 
 void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream) {
+  g.int_state = 0;
   if (n <= 0) return;
   const hipMemcpyKind kind = hipMemcpyDefault;
   hip_check(hipMemcpy2DAsync(g.vecs, (size_t)g.dp * 2, src, (size_t)dim * 2, (size_t)dim * 2, (size_t)n,

@@ -44,6 +44,11 @@ struct Graph {
   uint32_t packed_bytes = 0;
 
   void* vecs = nullptr;        // fp16
+  // cached value range of vecs (int_range): 0 = not scanned, 1 = all values
+  // integers in [int_lo, int_hi], 2 = some value is not an integer; reset
+  // by whatever rewrites vecs
+  mutable int int_state = 0;
+  mutable int32_t int_lo = 0, int_hi = -1;
   uint32_t* edges = nullptr;
   uint16_t* edist = nullptr;
   uint8_t* counts = nullptr;
@@ -86,12 +91,20 @@ struct HostGraph {
 };
 void download_graph(const Graph& g, HostGraph& h, bool with_vectors = true);
 
+// Largest span S of integer values for which L2 sums over `dim` values are
+// exact in any order: S <= 2,048 (exact fp16 differences) and dim * S^2 <
+// 2^24 (exact fp32 partial sums).
+int32_t int_exact_span(uint32_t dim);
+
+// Scans the device rows once (synchronising `stream`) and caches whether all
+// stored values (padding included) are integers, and their range. Returns
+// false when they are not, or when the packed form is off
+// (JASPER_INT_EXACT=0, for measurement).
+bool int_range(const Graph& g, hipStream_t stream);
+
 // True when L2 distances between stored rows are exact integers in any
-// summation order: every stored value (padding included) is an integer, the
-// values span at most 2,048 (exact fp16 differences) and dim * span^2 < 2^24
-// (exact fp32 partial sums). Scans the device rows; synchronises `stream`.
+// summation order (int_range holds and the span is within int_exact_span).
 // lo_out receives the smallest value when the test passes.
-// JASPER_INT_EXACT=0 turns the packed form off (measurement).
 bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out = nullptr);
 
 // Uploads a contiguous host or device fp16 matrix [n, dim] into rows padded

@@ -53,6 +53,10 @@ struct SearchArgs {
   uint32_t* seen_bits;      // [nq, seen_words]
   uint32_t seen_words;
   uint32_t* stats;          // [nq, 4]: hops, sum of degrees, vectors scored, predicted hops
+  // the graph's rows are integers in [glo, ghi] (gint); queries that are
+  // integers too, with the union spanning at most smax, take the packed form
+  uint32_t gint;
+  int32_t glo, ghi, smax;
 };
 
 // Seen cache: returns true when v is recorded, else records it (replacing
@@ -92,19 +96,59 @@ __device__ __forceinline__ bool seen_test_insert(const SearchArgs& a, uint32_t* 
 template <int CPL, int METRIC>
 using QueryFrag = LeftFrag<CPL, METRIC>;
 
-// INTX: query and rows are integer-valued within the exact range
-// (int_exact_l2); set only by the build, whose queries are graph rows.
-template <int CPL, int METRIC, bool INTX>
+// True (wave-uniform) when every value of the query is an integer and the
+// query's values together with the graph's span at most smax: then every
+// difference to a row is exact in fp16 and every partial sum of squares an
+// exact fp32 integer, whatever the order.
+template <int CPL>
+__device__ __forceinline__ bool query_int_exact(const SearchArgs& a, const RowFrag<CPL>& qh) {
+  bool ok = true;
+  float lo = 65504.0f, hi = -65504.0f;
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const uint32_t w[4] = {qh.x[t].x, qh.x[t].y, qh.x[t].z, qh.x[t].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        _Float16 hv;
+        const uint16_t bits = (uint16_t)(w[k] >> (16 * e));
+        __builtin_memcpy(&hv, &bits, 2);
+        const float v = (float)hv;
+        ok = ok && fabsf(v) <= 65504.0f && v == rintf(v);
+        lo = fminf(lo, v);
+        hi = fmaxf(hi, v);
+      }
+    }
+  }
+  if (ballot(!ok)) return false;
+#pragma unroll
+  for (int j = 1; j < 64; j <<= 1) {
+    lo = fminf(lo, __shfl_xor(lo, j, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, j, 64));
+  }
+  const float ulo = fminf(lo, (float)a.glo), uhi = fmaxf(hi, (float)a.ghi);
+  return uhi - ulo <= (float)a.smax;
+}
+
+// intx (wave-uniform): the query and the rows are integer-valued within
+// the exact span (query_int_exact), so the packed-difference form gives the
+// same bits.
+template <int CPL, int METRIC>
 __device__ __forceinline__ float score(const SearchArgs& a, const QueryFrag<CPL, METRIC>& q, const RowFrag<CPL>& x,
-                                       uint32_t ql, uint32_t nlimit) {
-  return left_distance<CPL, METRIC, INTX>(q, x, ql, a.nchunks, nlimit);
+                                       uint32_t ql, uint32_t nlimit, bool intx) {
+  if constexpr (METRIC == kL2 && CPL > 0) {
+    if (intx) return left_distance<CPL, METRIC, true>(q, x, ql, a.nchunks, nlimit);
+  }
+  return left_distance<CPL, METRIC, false>(q, x, ql, a.nchunks, nlimit);
 }
 
 // Scores up to 16 (or 32 with TWO) candidate rows listed in cand[base..)
 // and stores their keys into T[j].
-template <int CPL, int METRIC, bool INTX, bool TWO>
+template <int CPL, int METRIC, bool TWO>
 __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<CPL, METRIC>& qf, const uint32_t* cand,
-                                           uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql, uint32_t qg) {
+                                           uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql, uint32_t qg,
+                                           bool intx) {
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
   const uint32_t j0 = base + qg;
   const bool act0 = j0 < nm;
@@ -117,12 +161,12 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<
     const uint32_t v1 = act1 ? cand[j1] : 0u;
     RowFrag<CPL> x1;
     load_row_frag<CPL>(a.vecs + (size_t)v1 * a.nchunks, ql, a.nchunks, act1, x1);
-    const float d0 = score<CPL, METRIC, INTX>(a, qf, x0, ql, nlimit);
-    const float d1 = score<CPL, METRIC, INTX>(a, qf, x1, ql, nlimit);
+    const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit, intx);
+    const float d1 = score<CPL, METRIC>(a, qf, x1, ql, nlimit, intx);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
     if (ql == 0 && act1) T[j1] = make_key(d1, v1);
   } else {
-    const float d0 = score<CPL, METRIC, INTX>(a, qf, x0, ql, nlimit);
+    const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit, intx);
     if (ql == 0 && act0) T[j0] = make_key(d0, v0);
   }
 }
@@ -138,7 +182,7 @@ constexpr int search_waves_per_simd() {
   return CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? JASPER_SEARCH_WAVES_L2 : 1;
 }
 
-template <int CPL, int METRIC, bool STATS, bool INTX>
+template <int CPL, int METRIC, bool STATS>
 __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void beam_search_kernel(SearchArgs a) {
   extern __shared__ uint64_t smem[];
   const uint32_t lane = threadIdx.x;
@@ -162,6 +206,10 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   QueryFrag<CPL, METRIC> qf;
   load_left<CPL, METRIC>(qrow, ql, a.nchunks, qf);
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
+  bool intx = false;
+  if constexpr (METRIC == kL2 && CPL > 0 && !STATS) {
+    if (a.gint) intx = query_int_exact<CPL>(a, qf.h);
+  }
 
   // B = [(medoid, d(q, medoid))]; at bw <= 64 B lives in registers, one key
   // per lane (`b`), and is written to LDS only for the merge's general path
@@ -172,7 +220,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   {
     RowFrag<CPL> x;
     load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
-    const float d = score<CPL, METRIC, INTX>(a, qf, x, ql, nlimit);
+    const float d = score<CPL, METRIC>(a, qf, x, ql, nlimit, intx);
     if (lane == 0) b = make_key(d, a.medoid);
     wave_sync();  // hash table initialised
     if (lane == 0) {
@@ -275,8 +323,8 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
 
     // ---- score the new neighbours (4 lanes per vector)
     uint32_t base = 0;
-    for (; base + 16 < nm; base += 32) score_pass<CPL, METRIC, INTX, true>(a, qf, cand, T, base, nm, ql, qg);
-    if (base < nm) score_pass<CPL, METRIC, INTX, false>(a, qf, cand, T, base, nm, ql, qg);
+    for (; base + 16 < nm; base += 32) score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx);
+    if (base < nm) score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx);
     wave_sync();
 
     // ---- sort the new keys
@@ -425,9 +473,9 @@ size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {
   return (size_t)2 * r.beam_width * 8 + 64 * 8 + 64 * 4 + std::max<size_t>(((size_t)1 << hb) * entry, 4);
 }
 
-template <int CPL, int METRIC, bool STATS, bool INTX = false>
+template <int CPL, int METRIC, bool STATS>
 static void launch_one(const SearchArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  auto kern = beam_search_kernel<CPL, METRIC, STATS, INTX>;
+  auto kern = beam_search_kernel<CPL, METRIC, STATS>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
               "set LDS size");
@@ -484,6 +532,19 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
       a.dom_mask = a.tag_bits ? (uint32_t)(((uint64_t)1 << (a.hash_bits + a.tag_bits)) - 1u) : 0u;
     }
   }
+  {
+    // the graph's value range, scanned once and cached (not while the
+    // stream is being captured: then the exact chain is used throughout)
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    (void)hipStreamIsCapturing(stream, &cap);
+    a.gint = 0;
+    if (g.metric == kL2 && cap == hipStreamCaptureStatusNone && int_range(g, stream)) {
+      a.gint = 1;
+      a.glo = g.int_lo;
+      a.ghi = g.int_hi;
+      a.smax = int_exact_span(g.dim);
+    }
+  }
   a.seen_bits = r.seen_bits;
   a.seen_words = (uint32_t)((g.n + 31) / 32);
   a.stats = r.stats;
@@ -492,12 +553,10 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
   const size_t lds = beam_search_lds_bytes(g, r);
   const uint32_t cpl = (a.nchunks + 3) / 4;
   const dim3 grid(r.nq);
-  const bool intx = r.int_exact && g.metric == kL2 && !stats;
 #define JA_LAUNCH(C)                                                                                   \
   case C: {                                                                                            \
     if (g.metric == kL2) {                                                                             \
-      if (intx) launch_one<C, kL2, false, C != 0>(a, grid, lds, stream);                               \
-      else if (stats) launch_one<C, kL2, true>(a, grid, lds, stream);                                  \
+      if (stats) launch_one<C, kL2, true>(a, grid, lds, stream);                                       \
       else launch_one<C, kL2, false>(a, grid, lds, stream);                                            \
     } else {                                                                                           \
       if (stats) launch_one<C, kIP, true>(a, grid, lds, stream);                                       \

@@ -20,9 +20,6 @@ struct SearchRequest {
   uint64_t* visited = nullptr;     // [nq, max_result] popped keys in pop order (may be null)
   uint32_t* visited_counts = nullptr;
   uint32_t hash_bits = 0;          // 0 = choose from beam width
-  // queries and rows are integer-valued within the exact range
-  // (int_exact_l2): distances take the packed-difference form, same bits
-  bool int_exact = false;
   // measurement mode (exact seen set, work counters); both or neither
   uint32_t* seen_bits = nullptr;   // [nq, ceil(n/32)], zeroed by the caller
   uint32_t* stats = nullptr;       // [nq, 4]: hops, sum of degrees, vectors scored,

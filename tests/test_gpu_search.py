@@ -212,3 +212,27 @@ def test_search_small_seen_cache_matches_oracle(jasper, oracle_lib, tmp_path):
         rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
         msg = compare_search(out[f"ids{bw}"], out[f"d{bw}"], rid, rd)
         assert msg is None, f"bw={bw}: {msg}"
+
+
+def test_search_integer_queries_exact_span(jasper, oracle_lib, tmp_path):
+    # rows are integers in [260, 299]; the packed form is taken per query
+    # only when the query is integer-valued and the union of its values with
+    # the rows' spans at most 362 (dim 128: 128 * 362^2 < 2^24). A query at
+    # -100 spans 399: its partial sums pass 2^24 with odd terms, where the
+    # fp32 chain rounds in order, so only the chain matches the oracle.
+    rng = np.random.default_rng(21)
+    base = rng.integers(260, 300, size=(2000, 128)).astype(np.float16)
+    q = np.concatenate([
+        rng.integers(260, 300, size=(16, 128)),
+        np.full((4, 128), -63),                      # union span 362: packed form
+        np.full((4, 128), -100),                     # span 399: fp32 chain
+        rng.integers(-100, 300, size=(8, 128)),      # mixed spans
+    ]).astype(np.float32)
+    q = np.concatenate([q, q[:8] + 0.5]).astype(np.float16)  # non-integer queries
+    g = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    for bw in (16, 64, 128):
+        ids, d = _run(jasper, gg, q, 10, bw)
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
