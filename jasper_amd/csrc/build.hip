@@ -6,7 +6,8 @@
 //      at most 256 pops recorded);
 //   2. forward merge + RobustPrune, one wave per batch vertex: candidates are
 //      the vertex's existing edges (stored bf16 distances) and its popped
-//      nodes; the new edges and the reverse pairs (target << 32 | source)
+//      nodes; the new edges and the reverse pairs (target << sb | source -
+//      batch start, sb = bits of the largest batch)
 //      are written in the same kernel (merge_candidates_kernel,
 //      robust_prune_kernel and fill_reverse_edges, :280-501);
 //   3. radix sort of the reverse pairs and a head-marking pass, which groups
@@ -55,6 +56,7 @@ struct PruneKernelArgs {
   const uint64_t* visited;
   const uint32_t* visited_counts;
   uint32_t batch_offset;
+  uint32_t pair_shift;  // reverse pair keys: target << pair_shift | (source - batch_offset)
   uint64_t* pairs;
   // reverse
   const uint64_t* sorted_pairs;
@@ -179,16 +181,27 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   const uint32_t ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   write_selection(a, v, ns, l.S_ids, l.S_dist);
   if (lane < R) {
-    a.pairs[(size_t)bid * R + lane] = lane < ns ? (((uint64_t)l.S_ids[lane] << 32) | v) : kEmptyKey;
+    a.pairs[(size_t)bid * R + lane] = lane < ns ? (((uint64_t)l.S_ids[lane] << a.pair_shift) | bid) : kEmptyKey;
   }
 }
 
-__global__ void mark_heads_kernel(const uint64_t* sorted, uint32_t n, uint32_t* heads, uint32_t* n_heads) {
+// Records the first position of every target group; one counter atomic
+// per wave (the order of heads does not matter: each is pruned on its own).
+__global__ void mark_heads_kernel(const uint64_t* sorted, uint32_t n, uint32_t shift, uint32_t* heads,
+                                  uint32_t* n_heads) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint64_t k = sorted[i];
-  if (k == kEmptyKey) return;
-  if (i == 0 || (sorted[i - 1] >> 32) != (k >> 32)) heads[atomicAdd(n_heads, 1u)] = i;
+  bool head = false;
+  if (i < n) {
+    const uint64_t k = sorted[i];
+    head = k != kEmptyKey && (i == 0 || (sorted[i - 1] >> shift) != (k >> shift));
+  }
+  const uint64_t m = ballot(head);
+  if (m == 0) return;
+  const uint32_t leader = (uint32_t)__builtin_ctzll(m);
+  uint32_t base = 0;
+  if (lane_id() == leader) base = atomicAdd(n_heads, (uint32_t)__builtin_popcountll(m));
+  base = (uint32_t)__shfl((int)base, (int)leader, 64);
+  if (head) heads[base + mbcnt(m)] = i;
 }
 
 // The Gram prune holds 96 candidate rows of up to 128 values in registers
@@ -212,7 +225,7 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
   if (h >= nh) return;
   // the first pair of the next head is read one target ahead
   uint32_t start = a.heads[h];
-  uint32_t w = (uint32_t)(a.sorted_pairs[start] >> 32);
+  uint32_t w = (uint32_t)(a.sorted_pairs[start] >> a.pair_shift);
   for (; h < nh; h += gridDim.x) {
     // this target's reads, issued together: its adjacency row, its row of
     // values, the first 64 pairs of its group, and the next head
@@ -227,8 +240,8 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
     const uint32_t cap = max_cands - nE;
     uint32_t taken = 0;
     for (uint32_t pos = start;;) {
-      const bool same = key != kEmptyKey && (uint32_t)(key >> 32) == w;
-      const uint32_t src = (uint32_t)key;
+      const bool same = key != kEmptyKey && (uint32_t)(key >> a.pair_shift) == w;
+      const uint32_t src = a.batch_offset + ((uint32_t)key & ((1u << a.pair_shift) - 1u));
       const bool ok = same && src != w;
       const uint64_t m = ballot(ok);
       const uint32_t rank = mbcnt(m);
@@ -239,7 +252,7 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
       const uint32_t i = pos + lane;
       key = i < a.n_pairs ? a.sorted_pairs[i] : kEmptyKey;
     }
-    const uint32_t w_next = (uint32_t)(a.sorted_pairs[start_next] >> 32);
+    const uint32_t w_next = (uint32_t)(a.sorted_pairs[start_next] >> a.pair_shift);
     wave_sync();
     // d(w, v) for every source (compute_distance(src_vec = w, sink_vec = v))
     LeftFrag<CPL, METRIC> wf;
@@ -381,10 +394,15 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
     throw;
   }
 
-  int end_bit = 32;
-  while (end_bit < 64 && ((uint64_t)1 << (end_bit - 32)) <= (uint64_t)g.n) ++end_bit;
+  // pair keys: target << sb | (source - batch start); the radix sort covers
+  // the bits of both
+  uint32_t sb = 1;
+  while (((uint64_t)1 << sb) < (uint64_t)mb) ++sb;
+  int end_bit = (int)sb;
+  while (end_bit < 64 && ((uint64_t)1 << (end_bit - sb)) <= (uint64_t)g.n) ++end_bit;
 
   PruneKernelArgs pa{};
+  pa.pair_shift = sb;
   pa.pc.vecs = (const uint4*)g.vecs;
   pa.pc.nchunks = nchunks;
   pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;  // the reference prunes with `dim`
@@ -452,7 +470,8 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
       timer.start();
       sort_u64(temp, temp_bytes, pairs, sorted, np, end_bit, stream);
       hip_check(hipMemsetAsync(nheads, 0, 4, stream), "clear head count");
-      hipLaunchKernelGGL(mark_heads_kernel, dim3((np + 255) / 256), dim3(256), 0, stream, sorted, np, heads, nheads);
+      hipLaunchKernelGGL(mark_heads_kernel, dim3((np + 255) / 256), dim3(256), 0, stream, sorted, np, sb, heads,
+                         nheads);
       hip_check(hipGetLastError(), "launch mark_heads_kernel");
       timer.stop(st.sort_ms);
       // 4. reverse merge + prune

@@ -108,30 +108,34 @@ void Graph::release() {
 }
 
 // out = {non-integer flag, min, max} over fp16 values (infinities and NaN
-// count as non-integer)
-__global__ void int_range_kernel(const uint16_t* __restrict__ v, size_t count, int32_t* __restrict__ out) {
-  int32_t lo = INT32_MAX, hi = INT32_MIN, bad = 0;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
-    _Float16 hv;
-    const uint16_t bits = v[i];
-    __builtin_memcpy(&hv, &bits, 2);
-    const float h = (float)hv;
-    if (!(fabsf(h) <= 65504.0f) || h != rintf(h)) {
-      bad = 1;
-    } else {
-      lo = min(lo, (int32_t)h);
-      hi = max(hi, (int32_t)h);
+// count as non-integer); count8 = values / 8, read as 16-byte chunks
+__global__ void int_range_kernel(const uint4* __restrict__ v, size_t count8, int32_t* __restrict__ out) {
+  float lo = 65504.0f, hi = -65504.0f;
+  bool bad = false;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count8; i += (size_t)gridDim.x * blockDim.x) {
+    const uint4 c = v[i];
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      _Float16 hv;
+      const uint16_t bits = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+      __builtin_memcpy(&hv, &bits, 2);
+      const float h = (float)hv;
+      bad = bad || !(fabsf(h) <= 65504.0f) || h != rintf(h);
+      const float hc = fminf(fmaxf(h, -65504.0f), 65504.0f);  // NaN -> -65504
+      lo = fminf(lo, hc);
+      hi = fmaxf(hi, hc);
     }
   }
   for (int d = 32; d > 0; d >>= 1) {
-    lo = min(lo, __shfl_xor(lo, d, 64));
-    hi = max(hi, __shfl_xor(hi, d, 64));
-    bad = max(bad, __shfl_xor(bad, d, 64));
+    lo = fminf(lo, __shfl_xor(lo, d, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, d, 64));
   }
+  const bool any_bad = __ballot(bad) != 0;
   if ((threadIdx.x & 63u) == 0) {
-    if (bad) atomicMax(&out[0], 1);
-    atomicMin(&out[1], lo);
-    atomicMax(&out[2], hi);
+    if (any_bad) atomicMax(&out[0], 1);
+    atomicMin(&out[1], (int32_t)lo);
+    atomicMax(&out[2], (int32_t)hi);
   }
 }
 
@@ -152,9 +156,9 @@ bool int_range(const Graph& g, hipStream_t stream) {
     hip_check(hipMallocAsync((void**)&d, 12, stream), "alloc range");
     const int32_t init[3] = {0, INT32_MAX, INT32_MIN};
     hip_check(hipMemcpyAsync(d, init, 12, hipMemcpyHostToDevice, stream), "init range");
-    const size_t count = (size_t)g.n * g.dp;
-    const uint32_t grid = (uint32_t)std::min<size_t>((count + 255) / 256, 4096);
-    hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, (const uint16_t*)g.vecs, count, d);
+    const size_t count8 = (size_t)g.n * g.dp / 8;  // dp is a multiple of 8
+    const uint32_t grid = (uint32_t)std::min<size_t>((count8 + 255) / 256, 8192);
+    hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)g.vecs, count8, d);
     hip_check(hipGetLastError(), "launch int_range_kernel");
     int32_t h[3];
     hip_check(hipMemcpyAsync(h, d, 12, hipMemcpyDeviceToHost, stream), "read range");
