@@ -26,6 +26,8 @@
 #include "prune.hpp"
 #include "search.hpp"
 
+#include <rocprim/device/device_scan.hpp>
+
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -57,6 +59,7 @@ struct PruneKernelArgs {
   const uint32_t* visited_counts;
   uint32_t batch_offset;
   uint32_t pair_shift;  // reverse pair keys: target << pair_shift | (source - batch_offset)
+  uint32_t pair_mask;   // (1 << pair_shift) - 1, all ones at a shift of 32
   uint64_t* pairs;
   // reverse
   const uint64_t* sorted_pairs;
@@ -241,7 +244,7 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
     uint32_t taken = 0;
     for (uint32_t pos = start;;) {
       const bool same = key != kEmptyKey && (uint32_t)(key >> a.pair_shift) == w;
-      const uint32_t src = a.batch_offset + ((uint32_t)key & ((1u << a.pair_shift) - 1u));
+      const uint32_t src = a.batch_offset + ((uint32_t)key & a.pair_mask);
       const bool ok = same && src != w;
       const uint64_t m = ballot(ok);
       const uint32_t rank = mbcnt(m);
@@ -353,13 +356,19 @@ struct EventTimer {
 
 void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, bool time_stages,
                  BuildStats* stats) {
-  if (g.n <= 0) return;
+  build_range(g, alpha, 0, g.n, max_batch, true, stream, time_stages, stats);
+}
+
+void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max_batch, bool doubling,
+                 hipStream_t stream, bool time_stages, BuildStats* stats) {
+  if (last <= first) return;
+  if (first < 0 || last > g.n) throw std::invalid_argument("vertex range outside the graph");
   if (max_batch < 1) max_batch = 1;  // the reference loops forever here (n < 50); clamp instead
   if (g.R > 64) throw std::invalid_argument("R must be <= 64");
   const uint32_t nchunks = g.dp / 8;
   // chunks per quad lane held in registers; 0 streams rows longer than 32 chunks
   const uint32_t cpl = (nchunks + 3) / 4 > 8 ? 0u : (nchunks + 3) / 4;
-  const int64_t mb = std::min<int64_t>(max_batch, g.n);
+  const int64_t mb = std::min<int64_t>(max_batch, last - first);
   const uint32_t R = g.R;
 
   // workspace
@@ -403,6 +412,7 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
 
   PruneKernelArgs pa{};
   pa.pair_shift = sb;
+  pa.pair_mask = (1u << sb) - 1u;
   pa.pc.vecs = (const uint4*)g.vecs;
   pa.pc.nchunks = nchunks;
   pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;  // the reference prunes with `dim`
@@ -437,9 +447,9 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   hip_check(hipEventCreate(&t1), "event");
   hip_check(hipEventRecord(t0, stream), "event record");
   try {
-    int64_t count = 0, bs = 1;
-    while (count < g.n) {
-      bs = std::min<int64_t>(bs, g.n - count);
+    int64_t count = first, bs = doubling ? 1 : mb;
+    while (count < last) {
+      bs = std::min<int64_t>(bs, last - count);
       bs = std::min<int64_t>(bs, mb);
       // 1. beam search of the batch against the pre-batch graph
       SearchRequest r;
@@ -485,7 +495,7 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
       timer.stop(st.reverse_ms);
       count += bs;
       st.batches += 1;
-      if (bs < mb) bs = std::min<int64_t>(mb, bs * 2);
+      if (doubling && bs < mb) bs = std::min<int64_t>(mb, bs * 2);
     }
     hip_check(hipEventRecord(t1, stream), "event record");
     hip_check(hipStreamSynchronize(stream), "build synchronize");
@@ -503,6 +513,325 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   (void)hipEventDestroy(t1);
   cleanup();
   if (stats) *stats = st;
+}
+
+// ------------------------------------------------------------ live updates
+
+void append_rows(Graph& g, const void* rows, int64_t count, float alpha, int32_t* out_ids, hipStream_t stream) {
+  if (count <= 0) return;
+  if (g.on_host) throw std::runtime_error("append_batch requires graph on device");
+  const int64_t old_n = g.n, new_n = old_n + count;
+  if (new_n > 0x7FFFFFFF) throw std::invalid_argument("too many vectors for 31-bit ids");
+  // storage grows geometrically, so repeated appends are amortized
+  if (new_n > g.capacity) g.reserve(std::max<int64_t>(new_n, g.capacity + g.capacity / 2), stream);
+  upload_rows(g, rows, old_n, count, g.dim, stream);
+  g.n = new_n;
+  build_range(g, alpha, old_n, new_n, std::min<int64_t>(count, 100000), false, stream, false, nullptr);
+  // fresh monotonic ids (id_map.cuh assign_ids, set_id_range_kernel)
+  std::vector<uint32_t> ids((size_t)count);
+  for (int64_t i = 0; i < count; ++i) ids[(size_t)i] = (uint32_t)(g.next_id + (uint64_t)i);
+  g.next_id += (uint64_t)count;
+  hip_check(hipMemcpyAsync(g.slot_to_id + old_n, ids.data(), (size_t)count * 4, hipMemcpyHostToDevice, stream),
+            "write slot ids");
+  hip_check(hipMemcpyAsync(out_ids, ids.data(), (size_t)count * 4, hipMemcpyDefault, stream), "write ids");
+  hip_check(hipStreamSynchronize(stream), "append");
+}
+
+// mark_deleted_batch_kernel (deletion.cuh:21-42): one thread per id; the old
+// word tells whether the id was newly deleted.
+__global__ void mark_deleted_kernel(const int32_t* ids, int64_t n_ids, int64_t n, uint32_t* bits, uint32_t* newly) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_ids) return;
+  const uint32_t v = (uint32_t)ids[i];
+  if ((int64_t)v >= n) return;
+  const uint32_t m = 1u << (v & 31u);
+  if ((atomicOr(&bits[v >> 5], m) & m) == 0u) atomicAdd(newly, 1u);
+}
+
+// Lowest vertex whose tombstone bit is clear (out = n when none).
+__global__ void first_live_kernel(const uint32_t* bits, int64_t n, uint32_t* out) {
+  const int64_t words = (n + 31) / 32;
+  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words; w += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t free_bits = ~bits[w];
+    const int64_t base = w * 32;
+    if (base + 32 > n) free_bits &= (1u << (uint32_t)(n - base)) - 1u;
+    if (free_bits) atomicMin(out, (uint32_t)(base + __builtin_ctz(free_bits)));
+  }
+}
+
+int64_t mark_deleted(Graph& g, const int32_t* ids, int64_t n_ids, hipStream_t stream) {
+  if (n_ids <= 0 || g.n <= 0) return 0;
+  if (g.on_host) throw std::runtime_error("mark_deleted requires graph on device");
+  int32_t* d_ids = nullptr;
+  uint32_t* d_cnt = nullptr;
+  int64_t newly = 0;
+  try {
+    hip_check(hipMalloc(&d_ids, (size_t)n_ids * 4), "alloc ids");
+    hip_check(hipMalloc(&d_cnt, 8), "alloc count");
+    hip_check(hipMemcpyAsync(d_ids, ids, (size_t)n_ids * 4, hipMemcpyDefault, stream), "upload ids");
+    hip_check(hipMemsetAsync(d_cnt, 0, 8, stream), "clear count");
+    hipLaunchKernelGGL(mark_deleted_kernel, dim3((uint32_t)((n_ids + 255) / 256)), dim3(256), 0, stream, d_ids, n_ids,
+                       g.n, g.deleted, d_cnt);
+    hip_check(hipGetLastError(), "launch mark_deleted_kernel");
+    uint32_t h = 0;
+    hip_check(hipMemcpyAsync(&h, d_cnt, 4, hipMemcpyDeviceToHost, stream), "read count");
+    hip_check(hipStreamSynchronize(stream), "mark deleted");
+    newly = h;
+    g.n_deleted += h;
+    // update_medoid_if_deleted (graph_ops.cuh:50-88) with find_new_medoid_kernel
+    // (deletion.cuh:245-266): the first live neighbour in edge order, else the
+    // lowest live vertex
+    uint32_t mw = 0;
+    hip_check(hipMemcpy(&mw, g.deleted + (g.medoid >> 5), 4, hipMemcpyDeviceToHost), "read medoid bit");
+    if ((mw >> (g.medoid & 31u)) & 1u) {
+      uint8_t deg = 0;
+      std::vector<uint32_t> row(g.R);
+      hip_check(hipMemcpy(&deg, g.counts + g.medoid, 1, hipMemcpyDeviceToHost), "read medoid degree");
+      hip_check(hipMemcpy(row.data(), g.edges + (size_t)g.medoid * g.R, (size_t)g.R * 4, hipMemcpyDeviceToHost),
+                "read medoid edges");
+      int64_t pick = -1;
+      for (uint32_t j = 0; j < deg && j < g.R && pick < 0; ++j) {
+        const uint32_t nb = row[j];
+        if (nb == kInvalid32 || (int64_t)nb >= g.n) continue;
+        uint32_t w = 0;
+        hip_check(hipMemcpy(&w, g.deleted + (nb >> 5), 4, hipMemcpyDeviceToHost), "read bit");
+        if (!((w >> (nb & 31u)) & 1u)) pick = nb;
+      }
+      if (pick < 0) {
+        const uint32_t init = 0xFFFFFFFFu;
+        hip_check(hipMemcpy(d_cnt, &init, 4, hipMemcpyHostToDevice), "init first live");
+        const int64_t words = (g.n + 31) / 32;
+        hipLaunchKernelGGL(first_live_kernel, dim3((uint32_t)std::min<int64_t>((words + 255) / 256, 4096)), dim3(256), 0,
+                           stream, g.deleted, g.n, d_cnt);
+        hip_check(hipGetLastError(), "launch first_live_kernel");
+        uint32_t f = 0;
+        hip_check(hipMemcpyAsync(&f, d_cnt, 4, hipMemcpyDeviceToHost, stream), "read first live");
+        hip_check(hipStreamSynchronize(stream), "first live");
+        if ((int64_t)f < g.n) pick = f;
+      }
+      if (pick >= 0) g.medoid = (uint32_t)pick;
+      else std::fprintf(stderr, "Warning: update_medoid_if_deleted found no live vertex\n");
+    }
+  } catch (...) {
+    (void)hipFree(d_ids);
+    (void)hipFree(d_cnt);
+    throw;
+  }
+  (void)hipFree(d_ids);
+  (void)hipFree(d_cnt);
+  return newly;
+}
+
+__device__ __forceinline__ bool is_deleted_bit(const uint32_t* bits, uint32_t v) {
+  return ((bits[v >> 5] >> (v & 31u)) & 1u) != 0u;
+}
+
+// count / fill_repair_candidates_kernel (deletion.cuh:45-109), one wave per
+// live vertex N of [n_min, n_max): the live neighbours M != N of each deleted
+// neighbour D of N, in N's edge order and then D's. FILL writes the pairs
+// (N << 32 | M) from offsets[N - n_min]; otherwise counts go to offsets.
+template <bool FILL>
+__global__ __launch_bounds__(256) void repair_candidates_kernel(const uint32_t* edges, const uint8_t* counts,
+                                                                const uint32_t* bits, int64_t n, uint32_t R,
+                                                                int64_t n_min, int64_t n_max, uint64_t* offsets,
+                                                                uint64_t* pairs) {
+  const uint32_t lane = lane_id();
+  const int64_t N = n_min + (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (N >= n_max) return;
+  if (is_deleted_bit(bits, (uint32_t)N)) {
+    if constexpr (!FILL) {
+      if (lane == 0) offsets[N - n_min] = 0;
+    }
+    return;
+  }
+  const uint32_t degN = min((uint32_t)counts[N], R);
+  const uint32_t D = lane < degN ? edges[(size_t)N * R + lane] : kInvalid32;
+  uint64_t dm = ballot(D != kInvalid32 && (int64_t)D < n && is_deleted_bit(bits, D));
+  uint64_t pos = FILL ? offsets[N - n_min] : 0;
+  while (dm) {
+    const uint32_t j = (uint32_t)__builtin_ctzll(dm);
+    dm &= dm - 1u;
+    const uint32_t d = (uint32_t)__shfl((int)D, (int)j, 64);
+    const uint32_t degD = min((uint32_t)counts[d], R);
+    const uint32_t M = lane < degD ? edges[(size_t)d * R + lane] : kInvalid32;
+    const bool ok = M != kInvalid32 && (int64_t)M < n && !is_deleted_bit(bits, M) && M != (uint32_t)N;
+    const uint64_t m = ballot(ok);
+    if constexpr (FILL) {
+      if (ok) pairs[pos + mbcnt(m)] = ((uint64_t)N << 32) | M;
+    }
+    pos += (uint64_t)__builtin_popcountll(m);
+  }
+  if constexpr (!FILL) {
+    if (lane == 0) offsets[N - n_min] = pos;
+  }
+}
+
+// compact_deleted_neighbors_kernel (deletion.cuh:111-143): drops deleted
+// neighbours from the lists of the live vertices of [n_min, n_max), keeping
+// order and moving each distance with its edge.
+__global__ __launch_bounds__(256) void drop_deleted_neighbors_kernel(uint32_t* edges, uint16_t* edist,
+                                                                     uint8_t* counts, const uint32_t* bits,
+                                                                     int64_t n, uint32_t R, int64_t n_min,
+                                                                     int64_t n_max) {
+  const uint32_t lane = lane_id();
+  const int64_t N = n_min + (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (N >= n_max || is_deleted_bit(bits, (uint32_t)N)) return;
+  const uint32_t deg = min((uint32_t)counts[N], R);
+  const uint32_t e = lane < deg ? edges[(size_t)N * R + lane] : kInvalid32;
+  const uint16_t w = lane < deg ? edist[(size_t)N * R + lane] : (uint16_t)0;
+  const bool keep = e != kInvalid32 && (int64_t)e < n && !is_deleted_bit(bits, e);
+  const uint64_t m = ballot(keep);
+  if (keep) {
+    const uint32_t k = mbcnt(m);
+    edges[(size_t)N * R + k] = e;
+    edist[(size_t)N * R + k] = w;
+  }
+  if (lane == 0) counts[N] = (uint8_t)__builtin_popcountll(m);
+}
+
+// clear_deleted_nodes_kernel (deletion.cuh:145-160)
+__global__ void clear_deleted_nodes_kernel(uint32_t* edges, uint8_t* counts, const uint32_t* bits, int64_t n,
+                                           uint32_t R) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t v = i / R;
+  if (v >= n || !is_deleted_bit(bits, (uint32_t)v)) return;
+  edges[i] = kInvalid32;
+  if (i % R == 0) counts[v] = 0;
+}
+
+int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
+  if (g.n_deleted == 0) return 0;
+  if (g.on_host) throw std::runtime_error("consolidate requires graph on device");
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  const int64_t n = g.n;
+  const uint32_t R = g.R;
+  const uint32_t nchunks = g.dp / 8;
+  const uint32_t cpl = (nchunks + 3) / 4 > 8 ? 0u : (nchunks + 3) / 4;
+  int32_t int_lo = 0;
+  const bool intx = int_exact_l2(g, stream, &int_lo);
+  // vertices per chunk, so that one chunk's candidates stay within bounds
+  // (the reference splits the source range the same way, graph_ops.cuh:175-185)
+  const int64_t chunk = std::min<int64_t>(n, (int64_t)1 << 20);
+  uint64_t* per_vertex = nullptr;
+  uint64_t* offsets = nullptr;
+  uint64_t* pairs = nullptr;
+  uint64_t* sorted = nullptr;
+  uint32_t* heads = nullptr;
+  uint32_t* nheads = nullptr;
+  void* temp = nullptr;
+  void* scan_temp = nullptr;
+  size_t cap_pairs = 0, temp_bytes = 0, scan_bytes = 0;
+  int64_t total_pairs = 0;
+  auto cleanup = [&]() {
+    (void)hipFree(per_vertex);
+    (void)hipFree(offsets);
+    (void)hipFree(pairs);
+    (void)hipFree(sorted);
+    (void)hipFree(heads);
+    (void)hipFree(nheads);
+    (void)hipFree(temp);
+    (void)hipFree(scan_temp);
+  };
+  try {
+    hip_check(hipMalloc(&per_vertex, (size_t)(chunk + 1) * 8), "alloc repair counts");
+    hip_check(hipMalloc(&offsets, (size_t)(chunk + 1) * 8), "alloc repair offsets");
+    hip_check(hipMalloc(&nheads, 4), "alloc head count");
+    hip_check(rocprim::exclusive_scan(nullptr, scan_bytes, per_vertex, offsets, (uint64_t)0, (size_t)chunk + 1,
+                                      rocprim::plus<uint64_t>(), stream),
+              "scan temp size");
+    hip_check(hipMalloc(&scan_temp, std::max<size_t>(scan_bytes, 16)), "alloc scan temp");
+    int end_bit = 32;
+    while (end_bit < 64 && ((uint64_t)1 << (end_bit - 32)) <= (uint64_t)n) ++end_bit;
+
+    PruneKernelArgs pa{};
+    pa.pc.vecs = (const uint4*)g.vecs;
+    pa.pc.nchunks = nchunks;
+    pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;
+    pa.pc.R = R;
+    pa.pc.alpha = alpha;
+    {
+      const _Float16 lo = (_Float16)int_lo;
+      uint16_t bits;
+      std::memcpy(&bits, &lo, 2);
+      pa.pc.lo2 = (uint32_t)bits * 0x10001u;
+    }
+    pa.edges = g.edges;
+    pa.edist = g.edist;
+    pa.counts = g.counts;
+    pa.batch_offset = 0;
+    pa.pair_shift = 32;
+    pa.pair_mask = 0xFFFFFFFFu;
+    const size_t plds = prune_lds_bytes();
+
+    for (int64_t n_min = 0; n_min < n; n_min += chunk) {
+      const int64_t n_max = std::min<int64_t>(n, n_min + chunk), cn = n_max - n_min;
+      const dim3 wgrid((uint32_t)((cn + 3) / 4));
+      hipLaunchKernelGGL(repair_candidates_kernel<false>, wgrid, dim3(256), 0, stream, g.edges, g.counts, g.deleted,
+                         n, R, n_min, n_max, per_vertex, (uint64_t*)nullptr);
+      hip_check(hipGetLastError(), "launch repair_candidates_kernel");
+      hip_check(hipMemsetAsync(per_vertex + cn, 0, 8, stream), "clear scan tail");
+      hip_check(rocprim::exclusive_scan(scan_temp, scan_bytes, per_vertex, offsets, (uint64_t)0, (size_t)cn + 1,
+                                        rocprim::plus<uint64_t>(), stream),
+                "scan repair counts");
+      uint64_t np = 0;
+      hip_check(hipMemcpyAsync(&np, offsets + cn, 8, hipMemcpyDeviceToHost, stream), "read repair count");
+      hip_check(hipStreamSynchronize(stream), "repair count");
+      if (np > 0xFFFFFFFFull) throw std::runtime_error("too many repair candidates in one chunk");
+      if (np > cap_pairs) {
+        (void)hipFree(pairs);
+        (void)hipFree(sorted);
+        (void)hipFree(heads);
+        (void)hipFree(temp);
+        pairs = sorted = nullptr;
+        heads = nullptr;
+        temp = nullptr;
+        cap_pairs = np;
+        temp_bytes = sort_u64_temp_bytes(cap_pairs);
+        hip_check(hipMalloc(&pairs, cap_pairs * 8), "alloc repair pairs");
+        hip_check(hipMalloc(&sorted, cap_pairs * 8), "alloc sorted repair pairs");
+        hip_check(hipMalloc(&heads, cap_pairs * 4), "alloc repair heads");
+        hip_check(hipMalloc(&temp, std::max<size_t>(temp_bytes, 16)), "alloc sort temp");
+      }
+      if (np > 0) {
+        hipLaunchKernelGGL(repair_candidates_kernel<true>, wgrid, dim3(256), 0, stream, g.edges, g.counts, g.deleted, n,
+                           R, n_min, n_max, offsets, pairs);
+        hip_check(hipGetLastError(), "launch repair_candidates_kernel");
+      }
+      hipLaunchKernelGGL(drop_deleted_neighbors_kernel, wgrid, dim3(256), 0, stream, g.edges, g.edist, g.counts,
+                         g.deleted, n, R, n_min, n_max);
+      hip_check(hipGetLastError(), "launch drop_deleted_neighbors_kernel");
+      if (np == 0) continue;
+      total_pairs += (int64_t)np;
+      const uint32_t np32 = (uint32_t)np;
+      sort_u64(temp, temp_bytes, pairs, sorted, np32, end_bit, stream);
+      hip_check(hipMemsetAsync(nheads, 0, 4, stream), "clear head count");
+      hipLaunchKernelGGL(mark_heads_kernel, dim3((np32 + 255) / 256), dim3(256), 0, stream, sorted, np32, 32u, heads,
+                         nheads);
+      hip_check(hipGetLastError(), "launch mark_heads_kernel");
+      pa.sorted_pairs = sorted;
+      pa.n_pairs = np32;
+      pa.heads = heads;
+      pa.n_heads = nheads;
+      const uint32_t grid = (uint32_t)std::min<uint64_t>(np, 16384);
+      if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
+      else if (g.metric == kL2) dispatch_prune<kL2, false>(true, cpl, pa, grid, plds, stream);
+      else dispatch_prune<kIP, false>(true, cpl, pa, grid, plds, stream);
+      hip_check(hipGetLastError(), "launch reverse_prune_kernel");
+    }
+    const int64_t slots = n * (int64_t)R;
+    hipLaunchKernelGGL(clear_deleted_nodes_kernel, dim3((uint32_t)((slots + 255) / 256)), dim3(256), 0, stream,
+                       g.edges, g.counts, g.deleted, n, R);
+    hip_check(hipGetLastError(), "launch clear_deleted_nodes_kernel");
+    hip_check(hipMemsetAsync(g.deleted, 0, (size_t)((n + 31) / 32) * 4, stream), "clear tombstones");
+    hip_check(hipStreamSynchronize(stream), "consolidate");
+  } catch (...) {
+    (void)hipStreamSynchronize(stream);
+    cleanup();
+    throw;
+  }
+  cleanup();
+  g.n_deleted = 0;
+  return total_pairs;
 }
 
 }  // namespace jasper_amd

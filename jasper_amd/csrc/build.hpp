@@ -25,6 +25,25 @@ int64_t reference_max_batch(int64_t n, uint32_t R, int64_t budget_bytes);
 void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, bool time_stages,
                  BuildStats* stats);
 
+// The same per-batch steps over the vertices [first, last) only, in batches
+// of 1, 2, 4, ... up to max_batch (doubling) or of max_batch; the rows of
+// [first, last) must hold no edges yet.
+void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max_batch, bool doubling,
+                 hipStream_t stream, bool time_stages, BuildStats* stats);
+
+// Live updates (reference construct.cuh:1169-1265, graph_ops.cuh:94-258).
+// append_rows: copies `count` rows (host or device fp16 [count, dim]) into
+// new slots, wires them in with build_range in batches of min(count, 100000),
+// assigns fresh stable ids from next_id and writes them to out_ids (host or
+// device int32 [count]).
+void append_rows(Graph& g, const void* rows, int64_t count, float alpha, int32_t* out_ids, hipStream_t stream);
+// mark_deleted: tombstones the given ids (slot == id; out-of-range ignored),
+// replacing a deleted medoid. Returns the number newly deleted.
+int64_t mark_deleted(Graph& g, const int32_t* ids, int64_t n_ids, hipStream_t stream);
+// consolidate: repairs the edges of live vertices through deleted ones and
+// clears the tombstones. Returns the number of repair candidates.
+int64_t consolidate(Graph& g, float alpha, hipStream_t stream);
+
 // Radix sort of u64 keys (defined in sort.hip).
 size_t sort_u64_temp_bytes(size_t max_items);
 void sort_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, size_t n, int end_bit,

@@ -244,40 +244,38 @@ using namespace jasper_amd;
     });                                                                                                        \
   }                                                                                                            \
   extern "C" int64_t jasper_mark_deleted_##id(int64_t h, const int32_t* ids, int64_t n_ids) {                  \
-    (void)ids;                                                                                                 \
-    (void)n_ids;                                                                                               \
     return guarded([&]() -> int64_t {                                                                          \
       const Config c = config_of(#id);                                                                         \
-      lookup(h, &c);                                                                                           \
-      throw std::runtime_error("mark_deleted is not supported by this build (live updates are out of scope)"); \
+      if (n_ids < 0) throw std::invalid_argument("negative id count");                                       \
+      Graph& g = lookup(h, &c);                                                                                \
+      mark_deleted(g, ids, n_ids, nullptr);                                                                    \
+      return 0;                                                                                                \
     });                                                                                                        \
   }                                                                                                            \
   extern "C" int64_t jasper_consolidate_##id(int64_t h, double alpha) {                                        \
-    (void)alpha;                                                                                               \
     return guarded([&]() -> int64_t {                                                                          \
       const Config c = config_of(#id);                                                                         \
-      lookup(h, &c);                                                                                           \
-      throw std::runtime_error("consolidate is not supported by this build (live updates are out of scope)");  \
+      Graph& g = lookup(h, &c);                                                                                \
+      consolidate(g, (float)alpha, nullptr);                                                                   \
+      return 0;                                                                                                \
     });                                                                                                        \
   }                                                                                                            \
   extern "C" int64_t jasper_compact_##id(int64_t h) {                                                          \
     return guarded([&]() -> int64_t {                                                                          \
       const Config c = config_of(#id);                                                                         \
       lookup(h, &c);                                                                                           \
-      throw std::runtime_error("compact is not supported by this build (live updates are out of scope)");      \
+      throw std::runtime_error(                                                                                \
+          "compact() is disabled in this build (deletion path is mark_deleted + consolidate only)");          \
     });                                                                                                        \
   }                                                                                                            \
   extern "C" int64_t jasper_append_##id(int64_t h, const void* v, int64_t n, double alpha, int32_t* out_ids,   \
                                         void* stream) {                                                        \
-    (void)v;                                                                                                   \
-    (void)n;                                                                                                   \
-    (void)alpha;                                                                                               \
-    (void)out_ids;                                                                                             \
-    (void)stream;                                                                                              \
     return guarded([&]() -> int64_t {                                                                          \
       const Config c = config_of(#id);                                                                         \
-      lookup(h, &c);                                                                                           \
-      throw std::runtime_error("append is not supported by this build (live updates are out of scope)");       \
+      if (n < 0) throw std::invalid_argument("negative vector count");                                       \
+      Graph& g = lookup(h, &c);                                                                                \
+      append_rows(g, v, n, (float)alpha, out_ids, (hipStream_t)stream);                                        \
+      return 0;                                                                                                \
     });                                                                                                        \
   }
 

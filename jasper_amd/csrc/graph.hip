@@ -57,6 +57,7 @@ void Graph::allocate(int64_t n_, uint32_t dim_, uint32_t R_, int metric_, bool o
   next_id = (uint64_t)n_;
   n_deleted = 0;
   const size_t nn = (size_t)std::max<int64_t>(n_, 1);
+  capacity = (int64_t)nn;
   try {
     vecs = alloc_bytes(nn * dp * 2, on_host, "alloc vectors");
     edges = (uint32_t*)alloc_bytes(nn * R * 4, on_host, "alloc edges");
@@ -85,6 +86,59 @@ void Graph::allocate(int64_t n_, uint32_t dim_, uint32_t R_, int metric_, bool o
     for (size_t i = 0; i < nn; ++i) ids[i] = (uint32_t)i;
     hip_check(hipMemcpy(slot_to_id, ids.data(), nn * 4, hipMemcpyHostToDevice), "init slot ids");
   }
+}
+
+void Graph::reserve(int64_t rows, hipStream_t stream) {
+  if (rows <= capacity) return;
+  if (on_host) throw std::runtime_error("growing a graph requires it on the device");
+  const size_t oc = (size_t)capacity, nc = (size_t)rows;
+  const size_t ow = (oc + 31) / 32, nw = (nc + 31) / 32;
+  void* v2 = nullptr;
+  uint32_t *e2 = nullptr, *d2 = nullptr, *s2 = nullptr;
+  uint16_t* w2 = nullptr;
+  uint8_t* c2 = nullptr;
+  try {
+    v2 = alloc_bytes(nc * dp * 2, false, "grow vectors");
+    e2 = (uint32_t*)alloc_bytes(nc * R * 4, false, "grow edges");
+    w2 = (uint16_t*)alloc_bytes(nc * R * 2, false, "grow edge distances");
+    c2 = (uint8_t*)alloc_bytes(nc, false, "grow edge counts");
+    d2 = (uint32_t*)alloc_bytes(nw * 4, false, "grow deletion bits");
+    s2 = (uint32_t*)alloc_bytes(nc * 4, false, "grow slot ids");
+    hip_check(hipMemcpyAsync(v2, vecs, oc * dp * 2, hipMemcpyDeviceToDevice, stream), "copy vectors");
+    hip_check(hipMemsetAsync((char*)v2 + oc * dp * 2, 0, (nc - oc) * dp * 2, stream), "clear vectors");
+    hip_check(hipMemcpyAsync(e2, edges, oc * R * 4, hipMemcpyDeviceToDevice, stream), "copy edges");
+    hip_check(hipMemsetAsync(e2 + oc * R, 0xFF, (nc - oc) * R * 4, stream), "clear edges");
+    hip_check(hipMemcpyAsync(w2, edist, oc * R * 2, hipMemcpyDeviceToDevice, stream), "copy edge distances");
+    hip_check(hipMemsetAsync(w2 + oc * R, 0, (nc - oc) * R * 2, stream), "clear edge distances");
+    hip_check(hipMemcpyAsync(c2, counts, oc, hipMemcpyDeviceToDevice, stream), "copy edge counts");
+    hip_check(hipMemsetAsync(c2 + oc, 0, nc - oc, stream), "clear edge counts");
+    hip_check(hipMemcpyAsync(d2, deleted, ow * 4, hipMemcpyDeviceToDevice, stream), "copy deletion bits");
+    hip_check(hipMemsetAsync(d2 + ow, 0, (nw - ow) * 4, stream), "clear deletion bits");
+    hip_check(hipMemcpyAsync(s2, slot_to_id, oc * 4, hipMemcpyDeviceToDevice, stream), "copy slot ids");
+    hip_check(hipMemsetAsync(s2 + oc, 0xFF, (nc - oc) * 4, stream), "clear slot ids");
+    hip_check(hipStreamSynchronize(stream), "grow graph");
+  } catch (...) {
+    free_bytes(v2, false);
+    free_bytes(e2, false);
+    free_bytes(w2, false);
+    free_bytes(c2, false);
+    free_bytes(d2, false);
+    free_bytes(s2, false);
+    throw;
+  }
+  free_bytes(vecs, false);
+  free_bytes(edges, false);
+  free_bytes(edist, false);
+  free_bytes(counts, false);
+  free_bytes(deleted, false);
+  free_bytes(slot_to_id, false);
+  vecs = v2;
+  edges = e2;
+  edist = w2;
+  counts = c2;
+  deleted = d2;
+  slot_to_id = s2;
+  capacity = rows;
 }
 
 void Graph::release() {
@@ -180,11 +234,16 @@ bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out) {
 }
 
 void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream) {
+  upload_rows(g, src, 0, n, dim, stream);
+}
+
+void upload_rows(Graph& g, const void* src, int64_t row0, int64_t n, uint32_t dim, hipStream_t stream) {
   g.int_state = 0;
   if (n <= 0) return;
+  if (row0 < 0 || row0 + n > g.capacity) throw std::out_of_range("rows outside the graph's storage");
   const hipMemcpyKind kind = hipMemcpyDefault;
-  hip_check(hipMemcpy2DAsync(g.vecs, (size_t)g.dp * 2, src, (size_t)dim * 2, (size_t)dim * 2, (size_t)n,
-                             kind, stream),
+  hip_check(hipMemcpy2DAsync((char*)g.vecs + (size_t)row0 * g.dp * 2, (size_t)g.dp * 2, src, (size_t)dim * 2,
+                             (size_t)dim * 2, (size_t)n, kind, stream),
             "upload vectors");
 }
 

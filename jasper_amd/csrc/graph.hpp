@@ -70,6 +70,10 @@ struct Graph {
 
   void allocate(int64_t n_, uint32_t dim_, uint32_t R_, int metric_, bool on_host_);
   void release();
+  // Grows the device arrays to hold at least `rows` vertices, keeping their
+  // contents; new slots start empty (no edges, not deleted, no stable id).
+  void reserve(int64_t rows, hipStream_t stream);
+  int64_t capacity = 0;  // rows allocated (>= n)
 
   size_t vec_bytes() const { return (size_t)n * dp * 2; }
 };
@@ -110,5 +114,8 @@ bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out = nullptr)
 // Uploads a contiguous host or device fp16 matrix [n, dim] into rows padded
 // to dp on the device graph (vecs must be allocated).
 void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStream_t stream);
+
+// Same into rows [row0, row0 + n) (within capacity).
+void upload_rows(Graph& g, const void* src, int64_t row0, int64_t n, uint32_t dim, hipStream_t stream);
 
 }  // namespace jasper_amd

@@ -174,6 +174,10 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<
 // At dim <= 128 with L2 the registers fit six waves per SIMD (the LDS of a
 // query at bw <= 64 is about 5.6 KB, so registers decide the occupancy).
 // Streamed long rows hold no row in registers.
+// two rows per quad in flight in the score passes (tuning)
+#ifndef JASPER_SEARCH_TWO_ROWS
+#define JASPER_SEARCH_TWO_ROWS 1
+#endif
 #ifndef JASPER_SEARCH_WAVES_L2
 #define JASPER_SEARCH_WAVES_L2 6
 #endif
@@ -323,7 +327,10 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
 
     // ---- score the new neighbours (4 lanes per vector)
     uint32_t base = 0;
+#if JASPER_SEARCH_TWO_ROWS
     for (; base + 16 < nm; base += 32) score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx);
+#endif
+    for (; base + 16 < nm; base += 16) score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx);
     if (base < nm) score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx);
     wave_sync();
 

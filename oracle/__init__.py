@@ -70,6 +70,10 @@ def lib():
         _lib.jo_max_batch_size.argtypes = [i64, i32, i64]
         _lib.jo_build.restype = i32
         _lib.jo_build.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, P, P, P, i32, P]
+        _lib.jo_append.restype = i32
+        _lib.jo_append.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, i64, ctypes.c_uint32, P, P, P, P, i32, P]
+        _lib.jo_consolidate.restype = i64
+        _lib.jo_consolidate.argtypes = [P, i64, i32, i32, i32, i32, f32, P, P, P, P, i32]
         _lib.jo_bruteforce_exact.restype = None
         _lib.jo_bruteforce_exact.argtypes = [i32, P, i64, P, i64, i32, i32, P, P, i32]
         _lib.jo_bruteforce_ref.restype = None
@@ -222,6 +226,92 @@ def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
     g.n_batches = nb.value
     g.max_batch = max_batch
     return g
+
+
+def append(g: OracleGraph, vectors, alpha: float = 1.2, max_batch: int | None = None,
+           nthreads: int = 0):
+    """Live batch append, reference index/construct.cuh:1169-1265: the rows go
+    to slots [n, n + count), are wired in by process_batch in batches of
+    min(count, 100000), and get fresh stable ids from the monotonic counter.
+    Returns (new graph, ids)."""
+    new16 = as_padded_f16(vectors)
+    assert new16.shape[1] == g.dp
+    count = new16.shape[0]
+    old_n = g.n
+    n = old_n + count
+    if max_batch is None:
+        max_batch = min(count, 100000)
+    vecs16 = np.concatenate([g.vecs16, new16])
+    edges = np.concatenate([g.edges, np.full((count, g.R), 0xFFFFFFFF, dtype=np.uint32)])
+    edist = np.concatenate([g.edge_dist, np.zeros((count, g.R), dtype=np.uint16)])
+    counts = np.concatenate([g.counts, np.zeros(count, dtype=np.uint8)])
+    bits = np.zeros((n + 31) // 32, dtype=np.uint32)
+    bits[:g.deleted_bits.size] = g.deleted_bits
+    nb = ctypes.c_int64(0)
+    if count:
+        rc = lib().jo_append(_ptr(vecs16), n, g.dp, g.dim, g.R, metric_code(g.distance), ctypes.c_float(alpha),
+                             old_n, int(max_batch), g.medoid, _ptr(bits), _ptr(edges), _ptr(edist), _ptr(counts),
+                             nthreads, ctypes.byref(nb))
+        if rc != 0:
+            raise RuntimeError(f"oracle append failed ({rc})")
+    ids = np.arange(g.next_id, g.next_id + count, dtype=np.int64)
+    slot_to_id = np.concatenate([g.slot_to_id, ids.astype(np.uint32)])
+    out = OracleGraph(vecs16, edges, edist, counts, g.R, g.dim, g.distance, medoid=g.medoid,
+                      deleted_bits=bits, slot_to_id=slot_to_id, next_id=g.next_id + count)
+    out.n_deleted = getattr(g, "n_deleted", 0)
+    out.n_batches = nb.value
+    return out, ids.astype(np.int32)
+
+
+def mark_deleted(g: OracleGraph, ids) -> int:
+    """Soft delete by id (reference graph_ops.cuh:94-135 with stable-id labels
+    off, the default: id == slot). Out-of-range ids are ignored; ids already
+    deleted are counted once. A deleted medoid is replaced by its first live
+    neighbour in edge order, else the lowest live vertex
+    (find_new_medoid_kernel, deletion.cuh:245-266). Returns the number of
+    newly deleted vertices."""
+    newly = 0
+    for x in np.asarray(ids, dtype=np.int64).ravel():
+        v = int(x) & 0xFFFFFFFF
+        if v >= g.n:
+            continue
+        w, b = v >> 5, np.uint32(1 << (v & 31))
+        if not (g.deleted_bits[w] & b):
+            g.deleted_bits[w] |= b
+            newly += 1
+    g.n_deleted = getattr(g, "n_deleted", 0) + newly
+
+    def dead(v):
+        return bool((g.deleted_bits[v >> 5] >> np.uint32(v & 31)) & np.uint32(1))
+
+    if g.n and dead(g.medoid):
+        new = None
+        for e in range(int(g.counts[g.medoid])):
+            nb = int(g.edges[g.medoid, e])
+            if nb != 0xFFFFFFFF and nb < g.n and not dead(nb):
+                new = nb
+                break
+        if new is None:
+            for v in range(g.n):
+                if not dead(v):
+                    new = v
+                    break
+        if new is not None:
+            g.medoid = new
+    return newly
+
+
+def consolidate(g: OracleGraph, alpha: float = 1.2, nthreads: int = 0) -> int:
+    """Repair edges through deleted vertices and clear the tombstones
+    (reference graph_ops.cuh:151-258); in place. Returns the number of repair
+    candidates."""
+    if getattr(g, "n_deleted", 0) == 0 and not g.deleted_bits.any():
+        return 0
+    n_rep = lib().jo_consolidate(_ptr(g.vecs16), g.n, g.dp, g.dim, g.R, metric_code(g.distance),
+                                 ctypes.c_float(alpha), _ptr(g.deleted_bits), _ptr(g.edges), _ptr(g.edge_dist),
+                                 _ptr(g.counts), nthreads)
+    g.n_deleted = 0
+    return int(n_rep)
 
 
 def beam_search(g: OracleGraph, queries, k: int = 10, beam_width: int = 64,

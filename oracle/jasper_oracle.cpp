@@ -355,31 +355,75 @@ int64_t jo_max_batch_size(int64_t n, int R, int64_t budget_bytes) {
 // more than 256 + R candidates (atomicAdd, construct.cuh:642-658); this
 // restatement fixes that order as: the target's existing edges in slot order,
 // then the new sources in ascending id order.
-int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, int metric,
-             float alpha, int64_t max_batch, uint32_t* edges, uint16_t* edge_dist,
-             uint8_t* counts, int nthreads, int64_t* n_batches_out) {
-  if (n <= 0) return 0;
-  if (max_batch < 1) return -1;
-  if (nthreads > 0) omp_set_num_threads(nthreads);
+namespace {
+
+// process_reverse_edges_kernel (construct.cuh:560-741) over pairs
+// (target << 32 | source) sorted ascending: per target, its existing edges in
+// slot order, then the sources in ascending id order (capped at 256 + R),
+// sorted by (distance, id), then RobustPrune. Also the repair step of
+// consolidate (graph_ops.cuh:151-258), whose pairs are (live vertex, repair
+// candidate).
+void reverse_step(const Graph& g, int dim_for_prune, float alpha, const std::vector<uint64_t>& pairs,
+                  uint32_t* edges, uint16_t* edge_dist, uint8_t* counts) {
+  const int R = g.R, max_cands = 256 + R;
+  std::vector<size_t> heads;
+  for (size_t p = 0; p < pairs.size(); ++p)
+    if (p == 0 || (pairs[p] >> 32) != (pairs[p - 1] >> 32)) heads.push_back(p);
+  heads.push_back(pairs.size());
+#pragma omp parallel
+  {
+    std::vector<Cand> C;
+    std::vector<Cand> sel((size_t)R);
+    const int64_t n_groups = (int64_t)heads.size() - 1;
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t h = 0; h < n_groups; ++h) {
+      const uint32_t w = (uint32_t)(pairs[heads[(size_t)h]] >> 32);
+      C.clear();
+      for (uint32_t e = 0; e < counts[w]; ++e) {
+        const uint32_t x = edges[(size_t)w * R + e];
+        if (x == kInvalid32) continue;
+        C.push_back({x, bf2f(edge_dist[(size_t)w * R + e])});
+      }
+      const uint16_t* wv = g.vecs + (size_t)w * g.dp;
+      for (size_t p = heads[(size_t)h]; p < heads[(size_t)h + 1]; ++p) {
+        if ((int)C.size() >= max_cands) break;
+        const uint32_t v = (uint32_t)(pairs[p] & 0xFFFFFFFFu);
+        if (v == kInvalid32 || v == w) continue;
+        C.push_back({v, dist(g.metric, wv, g.vecs + (size_t)v * g.dp, dim_for_prune)});
+      }
+      std::sort(C.begin(), C.end(), cand_less);
+      const int ns = robust_prune(g, dim_for_prune, w, C, alpha, R, sel.data());
+      for (int j = 0; j < ns; ++j) {
+        edges[(size_t)w * R + j] = sel[(size_t)j].id;
+        edge_dist[(size_t)w * R + j] = f2bf(sel[(size_t)j].dist);
+      }
+      counts[w] = (uint8_t)ns;
+    }
+  }
+}
+
+// process_batch (construct.cuh:743-911) over the vertices [first, last), in
+// batches of 1, 2, 4, ... up to max_batch (construction) or of max_batch
+// (append_batch, construct.cuh:1226-1241), searching from `medoid`.
+int64_t process_batches(const Graph& g, int dim_for_prune, float alpha, int64_t first, int64_t last,
+                        int64_t max_batch, bool doubling, uint32_t medoid, uint32_t* edges,
+                        uint16_t* edge_dist, uint8_t* counts) {
+  const uint16_t* vecs = g.vecs;
+  const int dp = g.dp, R = g.R;
   const int L = 64, LIMIT = 256, MAX_RESULT = 256;
   const int max_cands = MAX_RESULT + R;
-  std::fill(counts, counts + n, (uint8_t)0);
-  std::fill(edges, edges + (size_t)n * R, kInvalid32);
-  std::fill(edge_dist, edge_dist + (size_t)n * R, (uint16_t)0);
-  Graph g{vecs, n, dp, edges, counts, R, nullptr, metric};
-
-  int64_t count = 0, bs = 1, nb = 0;
+  int64_t count = first, bs = doubling ? 1 : max_batch, nb = 0;
   std::vector<std::vector<Entry>> visited;
   std::vector<uint64_t> pairs;
-  while (count < n) {
-    bs = std::min<int64_t>(bs, n - count);
+  while (count < last) {
+    bs = std::min<int64_t>(bs, last - count);
     bs = std::min<int64_t>(bs, max_batch);
     const int64_t s = count;
     visited.assign((size_t)bs, {});
     // (i) beam search of every batch vector against the pre-batch graph
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t i = 0; i < bs; ++i) {
-      search_one(g, vecs + (size_t)(s + i) * dp, 0u, (uint32_t)L, (uint32_t)LIMIT,
+      search_one(g, vecs + (size_t)(s + i) * dp, medoid, (uint32_t)L, (uint32_t)LIMIT,
                  (uint32_t)MAX_RESULT, true, &visited[(size_t)i], nullptr, nullptr);
     }
     // (ii)+(iii) merge_candidates_kernel + robust_prune_kernel
@@ -416,47 +460,98 @@ int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, 
         pairs.push_back(((uint64_t)edges[(size_t)v * R + e] << 32) | v);
     }
     std::sort(pairs.begin(), pairs.end());
-    std::vector<size_t> heads;
-    for (size_t p = 0; p < pairs.size(); ++p)
-      if (p == 0 || (pairs[p] >> 32) != (pairs[p - 1] >> 32)) heads.push_back(p);
-    heads.push_back(pairs.size());
     // (vi) process_reverse_edges_kernel
-#pragma omp parallel
-    {
-      std::vector<Cand> C;
-      std::vector<Cand> sel((size_t)R);
-      const int64_t n_groups = (int64_t)heads.size() - 1;
-#pragma omp for schedule(dynamic, 1)
-      for (int64_t h = 0; h < n_groups; ++h) {
-        const uint32_t w = (uint32_t)(pairs[heads[(size_t)h]] >> 32);
-        C.clear();
-        for (uint32_t e = 0; e < counts[w]; ++e) {
-          const uint32_t x = edges[(size_t)w * R + e];
-          if (x == kInvalid32) continue;
-          C.push_back({x, bf2f(edge_dist[(size_t)w * R + e])});
-        }
-        const uint16_t* wv = vecs + (size_t)w * dp;
-        for (size_t p = heads[(size_t)h]; p < heads[(size_t)h + 1]; ++p) {
-          if ((int)C.size() >= max_cands) break;
-          const uint32_t v = (uint32_t)(pairs[p] & 0xFFFFFFFFu);
-          if (v == kInvalid32 || v == w) continue;
-          C.push_back({v, dist(metric, wv, vecs + (size_t)v * dp, dim_for_prune)});
-        }
-        std::sort(C.begin(), C.end(), cand_less);
-        const int ns = robust_prune(g, dim_for_prune, w, C, alpha, R, sel.data());
-        for (int j = 0; j < ns; ++j) {
-          edges[(size_t)w * R + j] = sel[(size_t)j].id;
-          edge_dist[(size_t)w * R + j] = f2bf(sel[(size_t)j].dist);
-        }
-        counts[w] = (uint8_t)ns;
-      }
-    }
+    reverse_step(g, dim_for_prune, alpha, pairs, edges, edge_dist, counts);
     count += bs;
     ++nb;
-    if (bs < max_batch) bs = std::min<int64_t>(max_batch, bs * 2);
+    if (doubling && bs < max_batch) bs = std::min<int64_t>(max_batch, bs * 2);
   }
+  return nb;
+}
+
+}  // namespace
+
+int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, int metric,
+             float alpha, int64_t max_batch, uint32_t* edges, uint16_t* edge_dist,
+             uint8_t* counts, int nthreads, int64_t* n_batches_out) {
+  if (n <= 0) return 0;
+  if (max_batch < 1) return -1;
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  std::fill(counts, counts + n, (uint8_t)0);
+  std::fill(edges, edges + (size_t)n * R, kInvalid32);
+  std::fill(edge_dist, edge_dist + (size_t)n * R, (uint16_t)0);
+  Graph g{vecs, n, dp, edges, counts, R, nullptr, metric};
+  const int64_t nb = process_batches(g, dim_for_prune, alpha, 0, n, max_batch, true, 0u, edges, edge_dist, counts);
   if (n_batches_out) *n_batches_out = nb;
   return 0;
+}
+
+// append_batch (construct.cuh:1169-1265): the rows [first, n) were appended
+// to a graph of `first` vertices (their counts must be 0); wires them in with
+// process_batch in batches of max_batch (the reference's default is
+// min(count, 100000)), searching from `medoid`. Deleted vertices stay in the
+// graph and are traversed like the reference's construction search does.
+int jo_append(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, int metric, float alpha,
+              int64_t first, int64_t max_batch, uint32_t medoid, const uint32_t* deleted_bits, uint32_t* edges,
+              uint16_t* edge_dist, uint8_t* counts, int nthreads, int64_t* n_batches_out) {
+  if (first < 0 || first > n || max_batch < 1) return -1;
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  Graph g{vecs, n, dp, edges, counts, R, deleted_bits, metric};
+  const int64_t nb =
+      process_batches(g, dim_for_prune, alpha, first, n, max_batch, false, medoid, edges, edge_dist, counts);
+  if (n_batches_out) *n_batches_out = nb;
+  return 0;
+}
+
+// consolidate (graph_ops.cuh:151-258, deletion.cuh:45-174): for every live
+// vertex N, each live neighbour M != N of each deleted neighbour D of N is a
+// repair candidate (N, M) (count/fill_repair_candidates_kernel, in N's edge
+// order, then D's); deleted neighbours are dropped from the live lists
+// (compact_deleted_neighbors_kernel, order kept, distances moved along); the
+// candidates are grouped by N with M ascending and merged and pruned as the
+// reverse step of construction; then the deleted vertices' lists are cleared
+// and every tombstone is reset. Returns the number of repair candidates.
+int64_t jo_consolidate(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, int metric, float alpha,
+                       uint32_t* deleted_bits, uint32_t* edges, uint16_t* edge_dist, uint8_t* counts,
+                       int nthreads) {
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  auto is_del = [&](uint32_t v) { return ((deleted_bits[v >> 5] >> (v & 31u)) & 1u) != 0u; };
+  std::vector<uint64_t> pairs;
+  for (int64_t N = 0; N < n; ++N) {
+    if (is_del((uint32_t)N)) continue;
+    for (uint32_t j = 0; j < counts[N]; ++j) {
+      const uint32_t D = edges[(size_t)N * R + j];
+      if (D == kInvalid32 || (int64_t)D >= n || !is_del(D)) continue;
+      for (uint32_t k = 0; k < counts[D]; ++k) {
+        const uint32_t M = edges[(size_t)D * R + k];
+        if (M == kInvalid32 || (int64_t)M >= n) continue;
+        if (is_del(M) || M == (uint32_t)N) continue;
+        pairs.push_back(((uint64_t)N << 32) | M);
+      }
+    }
+  }
+  for (int64_t N = 0; N < n; ++N) {
+    if (is_del((uint32_t)N)) continue;
+    uint32_t nc = 0;
+    for (uint32_t j = 0; j < counts[N]; ++j) {
+      const uint32_t nb = edges[(size_t)N * R + j];
+      if (nb == kInvalid32 || (int64_t)nb >= n || is_del(nb)) continue;
+      edges[(size_t)N * R + nc] = nb;
+      edge_dist[(size_t)N * R + nc] = edge_dist[(size_t)N * R + j];
+      ++nc;
+    }
+    counts[N] = (uint8_t)nc;
+  }
+  std::sort(pairs.begin(), pairs.end());
+  Graph g{vecs, n, dp, edges, counts, R, nullptr, metric};
+  reverse_step(g, dim_for_prune, alpha, pairs, edges, edge_dist, counts);
+  for (int64_t D = 0; D < n; ++D) {
+    if (!is_del((uint32_t)D)) continue;
+    std::fill(edges + (size_t)D * R, edges + (size_t)(D + 1) * R, kInvalid32);
+    counts[D] = 0;
+  }
+  std::fill(deleted_bits, deleted_bits + (n + 31) / 32, 0u);
+  return (int64_t)pairs.size();
 }
 
 // Exact kNN by the contract's distance (l2_dist / ip_dist), top-k by
