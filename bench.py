@@ -119,12 +119,13 @@ def main() -> int:
                     help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--path", default="search",
-                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5"],
+                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5", "updates"],
                     help="search (default, the headline metric) or one of the other hot-path rows, each "
                          "printing its own JSON line: directional (config 3, LSH), pq (PQ-ADC on "
                          "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
                          "rabitq (one-bit codes), c4 (config 4: 1M x 960 build + PQ search), c5 "
-                         "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search)")
+                         "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search), updates "
+                         "(config 2: mark_deleted 10%, consolidate, append 100k)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     args = ap.parse_args()
 
@@ -581,8 +582,84 @@ def run_c4(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
+def run_updates(args, torch, jasper_amd, datasets, dev, log):
+    """Live updates on config 2: build 1M x 128, soft-delete 10% of the ids,
+    consolidate, append 100k new vectors of the same mixture. Each operation
+    is timed once on the GPU graph (they mutate it); recall@10 of the 10k
+    queries at bw = 48 is measured against exact ground truth over the live
+    vectors after each step, and viol counts deleted ids in the results (the
+    reference's CI gate, scripts/ci/bench.py:132-134)."""
+    n, nq, dim, bw = args.n, args.nq, 128, 48
+    n_del, n_add = n // 10, n // 10
+    base = torch.from_numpy(datasets.clustered(n, dim, 0)).to(dev)
+    extra = torch.from_numpy(datasets.clustered(n_add, dim, 2)).to(dev)
+    q = torch.from_numpy(datasets.clustered(nq, dim, 1)).to(dev)
+    t0 = time.perf_counter()
+    g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    rng = np.random.default_rng(7)
+    dels = torch.from_numpy(np.sort(rng.choice(n, size=n_del, replace=False)).astype(np.int32))
+
+    def live_recall(live_rows, live_ids):
+        gt, _ = jasper_amd.bruteforce_knn(live_rows, q, 10, "l2")
+        gt = live_ids[gt.long()].cpu().numpy()
+        ids, _ = g.search(q, k=10, beam_width=bw)
+        torch.cuda.synchronize()
+        ids = ids.cpu().numpy()
+        return _recall(gt, ids), ids
+
+    def once(fn):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        out = fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) * 1000.0, out
+
+    all_ids = torch.arange(n, device=dev)
+    r0, _ = live_recall(base, all_ids)
+    # self-recall of built vectors, for comparison with the appended ones
+    out, _ = g.search(base[:nq].contiguous(), k=10, beam_width=64)
+    out = out.cpu().numpy()
+    base_self = float(np.mean([i in out[i] for i in range(nq)]))
+    del_ms, _ = once(lambda: g.mark_deleted(dels))
+    keep = torch.ones(n, dtype=torch.bool, device=dev)
+    keep[dels.long().to(dev)] = False
+    r1, ids1 = live_recall(base[keep].contiguous(), all_ids[keep])
+    dead = set(dels.tolist())
+    viol = int(sum(1 for x in ids1.ravel().tolist() if x in dead))
+    cons_ms, _ = once(lambda: g.consolidate(1.2))
+    r2, ids2 = live_recall(base[keep].contiguous(), all_ids[keep])
+    viol += int(sum(1 for x in ids2.ravel().tolist() if x in dead))
+    add_ms, new_ids = once(lambda: g.append(extra, 1.2))
+    rows = torch.cat([base[keep], extra]).contiguous()
+    labels = torch.cat([all_ids[keep], new_ids.to(dev).long()])
+    r3, _ = live_recall(rows, labels)
+    out, _ = g.search(extra[:nq], k=10, beam_width=64)
+    out = out.cpu().numpy()
+    nid = new_ids.numpy()
+    self_recall = float(np.mean([nid[i] in out[i] for i in range(min(nq, n_add))]))
+    log(f"build {build_s:.2f}s; recall@10 bw={bw}: {r0:.4f} -> after deleting {n_del}: {r1:.4f} "
+        f"(mark_deleted {del_ms:.1f} ms, viol={viol}) -> consolidate {cons_ms:.1f} ms: {r2:.4f} -> "
+        f"append {n_add} in {add_ms:.1f} ms ({n_add / (add_ms / 1000.0):,.0f} vec/s): {r3:.4f}; "
+        f"appended self-recall@10 {self_recall:.4f} (built vectors: {base_self:.4f})")
+    res = _line(args, "live updates, config 2: append vectors/s (100k into 1M x 128)", n_add / (add_ms / 1000.0),
+                "vectors/s", add_ms, "f32",
+                {"workload": f"config 2 graph ({n} x 128, R=64); mark_deleted {n_del} random ids, consolidate "
+                             f"(alpha 1.2), append {n_add} vectors of the same mixture (seed 2); recall@10 of "
+                             f"{nq} queries at bw {bw} against exact ground truth over the live vectors",
+                 "build_s": build_s, "mark_deleted_ms": del_ms, "consolidate_ms": cons_ms, "append_ms": add_ms,
+                 "recall_built": r0, "recall_after_delete": r1, "recall_after_consolidate": r2,
+                 "recall_after_append": r3, "viol": viol, "appended_self_recall_at_10": self_recall,
+                 "built_self_recall_at_10": base_self},
+                None)
+    res["steps"], res["warmup"] = 1, 0
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 OTHER_PATHS = {"c4": run_c4, "c5": run_c5, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
-               "rotate": run_rotate, "rabitq": run_rabitq}
+               "rotate": run_rotate, "rabitq": run_rabitq, "updates": run_updates}
 
 
 if __name__ == "__main__":
