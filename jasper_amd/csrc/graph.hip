@@ -30,8 +30,19 @@ void hip_check(hipError_t e, const char* what) {
 static void* alloc_bytes(size_t bytes, bool on_host, const char* what) {
   if (bytes == 0) bytes = 16;
   void* p = nullptr;
-  if (on_host) hip_check(hipHostMalloc(&p, bytes, hipHostMallocDefault), what);
-  else hip_check(hipMalloc(&p, bytes), what);
+  if (on_host) {
+    // pinned host memory that kernels read in place: its device address must
+    // be the host address, since the graph keeps one pointer for both
+    hip_check(hipHostMalloc(&p, bytes, hipHostMallocMapped | hipHostMallocPortable), what);
+    void* dp = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&dp, p, 0);
+    if (e != hipSuccess || dp != p) {
+      (void)hipHostFree(p);
+      throw std::runtime_error(std::string(what) + ": host memory is not addressable by the device at its host address");
+    }
+  } else {
+    hip_check(hipMalloc(&p, bytes), what);
+  }
   return p;
 }
 

@@ -104,3 +104,12 @@ def test_build_then_search_recall_c1(jasper, oracle_lib):
     rid, _ = oracle.beam_search(og, q, k=10, beam_width=64)
     r_ref = oracle.recall(gt, rid, 10)
     assert abs(r_gpu - r_ref) <= 0.005, (r_gpu, r_ref)
+
+
+def test_build_host_resident_matches_oracle(jasper, oracle_lib):
+    base = integer_clustered(2000, 128, 53)
+    og = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    t = torch.from_numpy(np.ascontiguousarray(base)).cuda()
+    gg = jasper.Graph.build(t, n_neighbors=32, distance="l2", alpha=1.2, on_host=True)
+    torch.cuda.synchronize()
+    _compare(gg, og)

@@ -236,3 +236,19 @@ def test_search_integer_queries_exact_span(jasper, oracle_lib, tmp_path):
         rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
         msg = compare_search(ids, d, rid, rd)
         assert msg is None, f"bw={bw}: {msg}"
+
+
+def test_search_host_resident_graph_matches_oracle(jasper, oracle_lib, tmp_path):
+    # on_host graphs live in pinned host memory and the kernels read them in
+    # place over the host link (reference graph.cuh:140-147): same results
+    base = integer_clustered(3000, 128, 51)
+    q = integer_clustered(64, 128, 52)
+    g = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    path = tmp_path / "g.bin"
+    oracle.save_graph(g, path)
+    gg = jasper.Graph.load(str(path), dim=128, n_neighbors=32, distance="l2", on_host=True)
+    for bw in (16, 64):
+        ids, d = _run(jasper, gg, q, 10, bw)
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
