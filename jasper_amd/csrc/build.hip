@@ -29,6 +29,7 @@
 #include <rocprim/device/device_scan.hpp>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -148,6 +149,18 @@ __device__ __forceinline__ PruneLds carve_prune_lds(uint64_t* smem, uint32_t R) 
   return l;
 }
 
+// JASPER_GRAM_MARGIN (>= 1, default 1) widens the proof margin of the Gram
+// prune on non-integer rows, sending more pairs to the exact chain; the
+// results do not change (used by the tests to exercise that path).
+static float gram_margin_scale() {
+  static const float v = [] {
+    const char* e = std::getenv("JASPER_GRAM_MARGIN");
+    const float f = e ? (float)std::atof(e) : 1.0f;
+    return f >= 1.0f ? f : 1.0f;
+  }();
+  return v;
+}
+
 #ifndef JASPER_GRAM_WAVES
 #define JASPER_GRAM_WAVES 2
 #endif
@@ -212,7 +225,7 @@ __global__ void mark_heads_kernel(const uint64_t* sorted, uint32_t n, uint32_t s
 // spill, and measured slower).
 template <int CPL, bool INTX>
 constexpr int reverse_waves_per_simd() {
-  return INTX && CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
+  return CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
 }
 
 template <int CPL, int METRIC, bool INTX>
@@ -273,13 +286,21 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
     const uint32_t nc = nE + taken;
     sort_candidates(l.C, nc);
     uint32_t ns;
-    if constexpr (INTX && CPL >= 1 && CPL <= 4) {
-      // integer rows, up to 96 candidates: pair distances on the matrix cores
-      if (nc <= kGramMaxCands && a.pc.nlimit <= kGramMaxChunks) {
+    if constexpr (CPL >= 1 && CPL <= 4) {
+      // up to 96 candidates of rows of up to 128 values: pair distances on
+      // the matrix cores, exact for integer rows, proved otherwise
+      const uint32_t climit = METRIC == kL2 ? a.pc.nlimit : (a.pc.nlimit + 7u) / 8u;
+      if (nc <= kGramMaxCands && climit <= kGramMaxChunks) {
         float* gn = reinterpret_cast<float*>(l.srcs);
-        if (nc <= 32) ns = robust_prune_gram<1>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
-        else if (nc <= 64) ns = robust_prune_gram<2>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
-        else ns = robust_prune_gram<3>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+        if constexpr (INTX) {
+          if (nc <= 32) ns = robust_prune_gram<1>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+          else if (nc <= 64) ns = robust_prune_gram<2>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+          else ns = robust_prune_gram<3>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+        } else {
+          if (nc <= 32) ns = robust_prune_gram_f<1, CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+          else if (nc <= 64) ns = robust_prune_gram_f<2, CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+          else ns = robust_prune_gram_f<3, CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+        }
       } else {
         ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
       }
@@ -418,6 +439,7 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
   pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;  // the reference prunes with `dim`
   pa.pc.R = R;
   pa.pc.alpha = alpha;
+  pa.pc.margin_scale = gram_margin_scale();
   pa.edges = g.edges;
   pa.edist = g.edist;
   pa.counts = g.counts;
@@ -749,6 +771,8 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
     pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;
     pa.pc.R = R;
     pa.pc.alpha = alpha;
+    pa.pc.margin_scale = gram_margin_scale();
+  pa.pc.margin_scale = gram_margin_scale();
     {
       const _Float16 lo = (_Float16)int_lo;
       uint16_t bits;

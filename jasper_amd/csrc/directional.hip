@@ -885,7 +885,18 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
     (void)hipFree(tmp);
   }
   const int64_t mbs = reference_max_batch(n, R, budget);
-  build_graph(*g, (float)alpha, mbs, stream, false, stats);
+  const char* timing = std::getenv("JASPER_BUILD_TIMING");
+  const bool time_stages = timing && timing[0] == '1';
+  BuildStats local;
+  BuildStats* st = stats ? stats : &local;
+  build_graph(*g, (float)alpha, mbs, stream, time_stages, st);
+  if (time_stages) {
+    std::printf("[construct] n=%lld batches=%lld max_batch=%lld search=%.1fms prune=%.1fms group=%.1fms "
+                "reverse=%.1fms total=%.1fms\n",
+                (long long)n, (long long)st->batches, (long long)st->max_batch, st->search_ms, st->prune_ms,
+                st->sort_ms, st->reverse_ms, st->total_ms);
+    std::fflush(stdout);
+  }
   g->next_id = (uint64_t)n;
   return g;
 }

@@ -24,6 +24,7 @@ struct PruneCtx {
   uint32_t R;
   float alpha;
   uint32_t lo2;      // integer-valued rows: the smallest value, as two fp16
+  float margin_scale;  // >= 1: widens the Gram prune's proof margin (testing)
 };
 
 // The left operand of a loaded row: L2 keeps the fp16 chunks; IP converts
@@ -320,6 +321,249 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
     ns += 1;
   }
   // the selection in candidate order
+  const uint32_t nA = (uint32_t)__builtin_popcountll(selA);
+  if ((selA >> lane) & 1ull) {
+    const uint32_t k = mbcnt(selA);
+    const uint64_t key = C[lane];
+    S_ids[k] = key_id(key);
+    S_dist[k] = key_dist(key);
+  }
+  if (lane < 32u && ((selB >> lane) & 1ull)) {
+    const uint32_t k = nA + mbcnt(selB);
+    const uint64_t key = C[64u + lane];
+    S_ids[k] = key_id(key);
+    S_dist[k] = key_dist(key);
+  }
+  wave_sync();
+  return ns;
+}
+
+// ------------------------------------------- any fp16 rows: Gram + proof
+// For rows that are not integer-valued the matrix cores' sums are not the
+// reference's fp32 chain bit for bit, so the Gram matrix only decides the
+// pairs it can prove. With S = sum |a_i,k a_j,k| <= (|a_i|^2 + |a_j|^2) / 2,
+// the Gram form d~ = (|a_i|^2 - a_i.a_j) + (|a_j|^2 - a_i.a_j) (L2; -a_i.a_j
+// for IP) and the chain's own result are both within a few n*u (u = 2^-24,
+// n summed values) of the exact real value: the matrix-core sum of products
+// within n*u*S, the norms within (n/2+2)*u*|a|^2, the chain within
+// (n/4+8)*u*d (L2: nonnegative terms) or (n/4+8)*u*S (IP). The margin M
+// takes four times those bounds (plus 2^-13 per unit of sqrt(n)*|a| in case
+// fp16 subnormals are flushed, and the roundings of d*alpha and of the
+// comparison). A pair with |d~*alpha - d_i| > M has the chain's decision;
+// the others are settled by the chain itself when they matter: when their
+// row becomes the first live candidate, the exact d(i, j) to each selected
+// member j of an unproved pair is computed in the reference's order.
+template <int T, int CPL, int METRIC>
+__device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
+                                        uint32_t* S_ids, float* S_dist, float* gn) {
+  static_assert(T >= 1 && T <= 3, "one to three tiles");
+  static_assert(CPL >= 1, "rows held in registers");
+  constexpr int KS = kGramMaxChunks / 2;
+  const uint32_t lane = lane_id();
+  const uint32_t r = lane & 31u, h = lane >> 5;
+  float* gcd = gn + kGramMaxCands;
+  // chunks summed: L2 counts chunks, IP elements (padding past dim is zero)
+  const uint32_t climit = METRIC == kL2 ? p.nlimit : (p.nlimit + 7u) / 8u;
+  const float nsum = 8.0f * (float)climit;
+  constexpr float U = 5.9604645e-8f;  // 2^-24
+  const float sub = 1.2207031e-4f * sqrtf(nsum);  // 2^-13 * sqrt(n)
+
+  uint4 fr[T][KS];
+  float nrm[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const uint32_t i = 32u * (uint32_t)t + r;
+    const uint64_t key = i < nc ? C[i] : kEmptyKey;
+    const uint32_t id = i < nc ? key_id(key) : self;
+    const uint4* row = p.vecs + (size_t)id * p.nchunks;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t c = 2u * (uint32_t)s + h;
+      fr[t][s] = row[min(c, p.nchunks - 1u)];
+    }
+    if (h == 0) gcd[i] = key_dist(key);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t c = 2u * (uint32_t)s + h;
+      const uint32_t keep = c < climit ? ~0u : 0u;
+      uint4 x = fr[t][s];
+      x.x &= keep;
+      x.y &= keep;
+      x.z &= keep;
+      x.w &= keep;
+      fr[t][s] = x;
+      acc = dot2_sqdiff(x.x, 0u, acc);
+      acc = dot2_sqdiff(x.y, 0u, acc);
+      acc = dot2_sqdiff(x.z, 0u, acc);
+      acc = dot2_sqdiff(x.w, 0u, acc);
+    }
+    nrm[t] = acc + xor_lane_f<32>(acc);
+    if (h == 0) gn[32u * (uint32_t)t + r] = nrm[t];
+  }
+  wave_sync();
+
+  // P: proved pruned, A: not proved either way (column words as in
+  // robust_prune_gram)
+  uint32_t WP[T][T], WA[T][T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int t2 = 0; t2 < T; ++t2) {
+      WP[t][t2] = 0u;
+      WA[t][t2] = 0u;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int t2 = 0; t2 <= t; ++t2) {
+      gram_f16 acc = {};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_gram_h8(fr[t][s]), as_gram_h8(fr[t2][s]), acc, 0, 0, 0);
+      const float nj = nrm[t2];
+      const float sj = sqrtf(nj);
+      uint32_t wp = 0u, wa = 0u;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 ni = *reinterpret_cast<const float4*>(gn + 32 * t + 8 * g + 4 * h);
+        const float4 cd = *reinterpret_cast<const float4*>(gcd + 32 * t + 8 * g + 4 * h);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float gij = acc[4 * g + q];
+          const float niq = q == 0 ? ni.x : q == 1 ? ni.y : q == 2 ? ni.z : ni.w;
+          const float cdq = q == 0 ? cd.x : q == 1 ? cd.y : q == 2 ? cd.z : cd.w;
+          float d, e;
+          if constexpr (METRIC == kL2) {
+            d = (niq - gij) + (nj - gij);
+            e = U * (1.5f * nsum + 16.0f) * (niq + nj) + U * (0.25f * nsum + 8.0f) * fabsf(d);
+          } else {
+            d = -gij;
+            e = U * (1.25f * nsum + 16.0f) * (niq + nj);
+          }
+          e += sub * (sqrtf(niq) + sj);
+          const float x = d * p.alpha - cdq;
+          const float m = p.margin_scale * 4.0f * (p.alpha * e + 2.0f * U * (fabsf(d * p.alpha) + fabsf(cdq)));
+          bool pr = x < -m;
+          bool am = !pr && !(x > m);  // NaN or infinite values: not proved
+          if (t == t2) {
+            const bool before = r < (uint32_t)(8 * g + 4 * (int)h + q);
+            pr = pr && before;
+            am = am && before;
+          }
+          wp |= pr ? (1u << (4 * g + q)) : 0u;
+          wa |= am ? (1u << (4 * g + q)) : 0u;
+        }
+      }
+      const uint32_t sp = spread_nibbles(wp) << (4u * h);
+      const uint32_t sa = spread_nibbles(wa) << (4u * h);
+      WP[t][t2] = sp | xor_lane<32>(sp);
+      WA[t][t2] = sa | xor_lane<32>(sa);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  uint32_t pA[T], pB[T], aA[T], aB[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    pA[t] = T >= 2 && h ? WP[t][T >= 2 ? 1 : 0] : WP[t][0];
+    aA[t] = T >= 2 && h ? WA[t][T >= 2 ? 1 : 0] : WA[t][0];
+    pB[t] = T == 3 ? WP[t][T - 1] : 0u;
+    aB[t] = T == 3 ? WA[t][T - 1] : 0u;
+  }
+
+  const bool validA = lane < nc && key_id(C[lane]) != self;
+  const bool validB = T == 3 && lane < 32u && 64u + lane < nc && key_id(C[64u + lane]) != self;
+  uint64_t liveA = ballot(validA), liveB = ballot(validB);
+  uint64_t selA = 0, selB = 0, pendA = 0, pendB = 0;
+  uint32_t ns = 0;
+  const uint32_t ql = lane & 3u, qg = lane >> 2;
+  while (ns < p.R && (liveA | liveB)) {
+    const bool inA = liveA != 0;
+    const uint32_t i = inA ? (uint32_t)__builtin_ctzll(liveA) : 64u + (uint32_t)__builtin_ctzll(liveB);
+    const bool pend = inA ? ((pendA >> i) & 1u) : ((pendB >> (i - 64u)) & 1u);
+    if (pend) {
+      // members j < i selected so far whose pair with i was not proved
+      const uint32_t ti = i >> 5, bi = i & 31u;
+      uint32_t wa = aA[0], wb = aB[0];
+#pragma unroll
+      for (int t = 1; t < T; ++t) {
+        if (ti == (uint32_t)t) { wa = aA[t]; wb = aB[t]; }
+      }
+      uint64_t jm_a = ballot(((selA >> lane) & 1u) && ((wa >> bi) & 1u));
+      uint64_t jm_b = ballot(lane < 32u && ((selB >> lane) & 1u) && ((wb >> bi) & 1u));
+      const uint64_t ki = C[i];
+      const float cdi = key_dist(ki);
+      RowFrag<CPL> xi;
+      load_row_frag<CPL>(p.vecs + (size_t)key_id(ki) * p.nchunks, ql, p.nchunks, true, xi);
+      LeftFrag<CPL, METRIC> li;
+      left_from_row<CPL, METRIC>(xi, ql, li);
+      bool pruned = false;
+      while ((jm_a | jm_b) && !pruned) {
+        // up to 16 members per pass, one per quad
+        uint32_t jq = 0xFFFFFFFFu;
+        for (uint32_t g = 0; g < 16u && (jm_a | jm_b); ++g) {
+          uint32_t j;
+          if (jm_a) {
+            j = (uint32_t)__builtin_ctzll(jm_a);
+            jm_a &= jm_a - 1u;
+          } else {
+            j = 64u + (uint32_t)__builtin_ctzll(jm_b);
+            jm_b &= jm_b - 1u;
+          }
+          if (qg == g) jq = j;
+        }
+        const bool act = jq != 0xFFFFFFFFu;
+        const uint32_t jid = act ? key_id(C[jq]) : key_id(ki);
+        RowFrag<CPL> xj;
+        load_row_frag<CPL>(p.vecs + (size_t)jid * p.nchunks, ql, p.nchunks, true, xj);
+        const float d = left_distance<CPL, METRIC, false>(li, xj, ql, p.nchunks, p.nlimit);
+        pruned = ballot(act && d * p.alpha < cdi) != 0;
+      }
+      if (inA) {
+        pendA &= ~(1ull << i);
+      } else {
+        pendB &= ~(1ull << (i - 64u));
+      }
+      if (pruned) {
+        if (inA) liveA &= ~(1ull << i);
+        else liveB &= ~(1ull << (i - 64u));
+        continue;
+      }
+    }
+    if (inA) {
+      liveA &= ~(1ull << i);
+      selA |= 1ull << i;
+    } else {
+      liveB &= ~(1ull << (i - 64u));
+      selB |= 1ull << (i - 64u);
+    }
+    ns += 1;
+    const uint32_t src = inA ? i : i - 64u;
+    uint32_t p0 = 0, p1 = 0, p2 = 0, a0 = 0, a1 = 0, a2 = 0;
+    if (inA) {
+      p0 = (uint32_t)__builtin_amdgcn_readlane((int)pA[0], (int)src);
+      a0 = (uint32_t)__builtin_amdgcn_readlane((int)aA[0], (int)src);
+      if constexpr (T >= 2) {
+        p1 = (uint32_t)__builtin_amdgcn_readlane((int)pA[T >= 2 ? 1 : 0], (int)src);
+        a1 = (uint32_t)__builtin_amdgcn_readlane((int)aA[T >= 2 ? 1 : 0], (int)src);
+      }
+      if constexpr (T == 3) {
+        p2 = (uint32_t)__builtin_amdgcn_readlane((int)pA[T - 1], (int)src);
+        a2 = (uint32_t)__builtin_amdgcn_readlane((int)aA[T - 1], (int)src);
+      }
+    } else {
+      p2 = (uint32_t)__builtin_amdgcn_readlane((int)pB[T - 1], (int)src);
+      a2 = (uint32_t)__builtin_amdgcn_readlane((int)aB[T - 1], (int)src);
+    }
+    liveA &= ~((uint64_t)p0 | ((uint64_t)p1 << 32));
+    liveB &= ~(uint64_t)p2;
+    pendA |= ((uint64_t)a0 | ((uint64_t)a1 << 32)) & liveA;
+    pendB |= (uint64_t)a2 & liveB;
+  }
   const uint32_t nA = (uint32_t)__builtin_popcountll(selA);
   if ((selA >> lane) & 1ull) {
     const uint32_t k = mbcnt(selA);

@@ -113,3 +113,46 @@ def test_build_host_resident_matches_oracle(jasper, oracle_lib):
     gg = jasper.Graph.build(t, n_neighbors=32, distance="l2", alpha=1.2, on_host=True)
     torch.cuda.synchronize()
     _compare(gg, og)
+
+
+_WIDE_MARGIN_CHILD = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import jasper_amd
+out = {}
+for name in ("l2", "ip"):
+    x = np.load(sys.argv[2] + f"/{name}.npy")
+    g = jasper_amd.Graph.build(torch.from_numpy(x).cuda(), n_neighbors=32, distance=name, alpha=1.2)
+    torch.cuda.synchronize()
+    e, d, c = g.export_edges()
+    out[name + "_e"], out[name + "_d"], out[name + "_c"] = e, d, c
+np.savez(sys.argv[2] + "/out.npz", **out)
+print("child done", flush=True)
+"""
+
+
+def test_build_gram_proof_path_matches_oracle(jasper, oracle_lib, tmp_path):
+    # with the proof margin widened past every distance, no pair of the
+    # non-integer Gram prune is decided by the matrix cores: each is settled
+    # by the exact chain when its row comes up; the graphs must not change
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    l2 = gaussian(2000, 128, 61)
+    ip = unit(2000, 96, 62)
+    np.save(tmp_path / "l2.npy", l2)
+    np.save(tmp_path / "ip.npy", ip)
+    env = dict(os.environ, JASPER_GRAM_MARGIN="1e30")
+    root = str(Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _WIDE_MARGIN_CHILD, root, str(tmp_path)], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = np.load(tmp_path / "out.npz")
+    for name, x in (("l2", l2), ("ip", ip)):
+        og = oracle.build(x, R=32, distance=name, alpha=1.2)
+        counts, edges, edist = out[name + "_c"], out[name + "_e"], out[name + "_d"]
+        assert np.array_equal(counts, og.counts), name
+        mask = np.arange(32)[None, :] < counts[:, None]
+        assert np.array_equal(edges[mask], og.edges[mask]), name
+        assert np.array_equal(edist[mask], og.edge_dist[mask]), name
