@@ -131,7 +131,7 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); every "
-              "index here fits one MI355X and the sharded design is described in DESIGN.md.",
+              "index here fits one MI355X, and sharding across GPUs is a design, not code.",
               file=sys.stderr)
         return 2
 

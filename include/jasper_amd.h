@@ -106,7 +106,7 @@ extern "C" {
   /* GetVectorDirectional_ :735-763 */                                                        \
   int64_t jasper_get_vector_directional_##id(int64_t handle, int64_t index, void* out,        \
                                              void* stream);                                   \
-  /* GetDirectionalFlags_ :765-775: bit 0 = LSH, bit 1 = PQ */                                \
+  /* GetDirectionalFlags_ :765-775: bit 0 = LSH, bit 1 = PQ; bit 3 = prerotated rows */       \
   int64_t jasper_get_directional_flags_##id(int64_t handle);
 
 JASPER_PLAIN_CONFIGS(JASPER_DECLARE_PLAIN)
@@ -207,6 +207,12 @@ int64_t jasperx_directional_stats(int64_t handle, int32_t use_pq, const void* qu
                                   int64_t dim, int64_t k, int64_t beam_width, int64_t limit, uint32_t flags,
                                   uint32_t* out_stats, void* stream);
 /* Library build identifier (git-independent), for load checks. */
+/* The prerotation seed of a directional graph (-1 when its rows are not
+ * prerotated). Directional files written by this build record the
+ * prerotation in the trailer (flag 8, a u64 seed after the other sections;
+ * readers of flags 1, 2 and 4 stop before it), and loading them restores it
+ * whatever prerotate/seed the caller passed. No reference counterpart. */
+int64_t jasperx_prerotate_seed(int64_t handle);
 const char* jasperx_version(void);
 
 #ifdef __cplusplus

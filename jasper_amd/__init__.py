@@ -84,6 +84,7 @@ _AGNOSTIC = {
     "jasper_get_dim": [_i64],
     "jasperx_export_graph": [_i64, _ptr, _ptr, _ptr],
     "jasperx_last_build_stats": [_ptr],
+    "jasperx_prerotate_seed": [_i64],
     "jasperx_search_stats": [_i64, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr],
     "jasperx_export_vectors": [_i64, _ptr],
     "jasperx_export_lsh": [_i64, _ptr, _ptr, _ptr],
@@ -283,6 +284,8 @@ class Graph:
         handle = _op("load_directional", config_id)(str(path).encode(), dim, on_host, prerotate,
                                                     prerotate_seed)
         flags = _op("get_directional_flags", config_id)(handle)
+        if flags & 8:  # the file records its prerotation; it wins over the arguments
+            prerotate, prerotate_seed = True, int(_agnostic("jasperx_prerotate_seed")(handle))
         return cls(handle, config_id, data_type, distance, n_neighbors, dim,
                    is_directional=True, k_ranks=k_ranks, has_lsh=bool(flags & 1),
                    has_pq=bool(flags & 2), prerotate=prerotate, prerotate_seed=prerotate_seed)

@@ -372,11 +372,18 @@ JASPER_PLAIN_CONFIGS(JA_DEFINE_PLAIN)
     return guarded([&]() -> int64_t {                                                                          \
       const Config c = config_of(#id);                                                                         \
       Graph& g = lookup(h, &c);                                                                                \
-      return (int64_t)((g.lsh ? 1 : 0) | (g.pq ? 2 : 0));                                                      \
+      return (int64_t)((g.lsh ? 1 : 0) | (g.pq ? 2 : 0) | (g.prerotate ? 8 : 0));                             \
     });                                                                                                        \
   }
 
 JASPER_DIRECTIONAL_CONFIGS(JA_DEFINE_DIRECTIONAL)
+
+extern "C" int64_t jasperx_prerotate_seed(int64_t h) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    return g.prerotate ? (int64_t)(g.prerotate_seed & 0x7FFFFFFFFFFFFFFFull) : -1;
+  });
+}
 
 extern "C" int64_t jasper_free_graph(int64_t h) {
   return guarded([&]() -> int64_t {

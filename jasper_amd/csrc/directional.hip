@@ -1158,7 +1158,9 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
 // Trailer after the base section (graph.cuh:1790-1937): u32 magic, u32
 // version, u8 flags (1 LSH, 2 PQ, 4 norms); LSH: u8 K, u8 sizeof(packed_t),
 // K floats c_per_rank + float norm_denom, N rows; PQ: u32 M, u32 256,
-// u32 dsub, centroids, N code rows; norms: N floats. Read back at the end of
+// u32 dsub, centroids, N code rows; norms: N floats. This build adds flag 8
+// (prerotated rows) with a u64 seed after the other sections: readers that
+// know flags 1, 2 and 4 only stop before it. Read back at the end of
 // the base section (total_file_size), where the saver puts it; the
 // reference loader looks elsewhere (graph.cuh:1959-1964) and never finds it.
 
@@ -1166,10 +1168,11 @@ void save_directional_file(const Graph& g, const std::string& path) {
   save_graph_file(g, path);
   if (g.n == 0) return;
   const bool has_lsh = (bool)g.lsh, has_pq = (bool)g.pq, has_norms = g.vector_norms != nullptr;
-  if (!has_lsh && !has_pq && !has_norms) return;
+  if (!has_lsh && !has_pq && !has_norms && !g.prerotate) return;
   std::ofstream f(path, std::ios::binary | std::ios::app);
   if (!f.is_open()) throw std::runtime_error("save_directional_graph_to_file: cannot reopen " + path);
-  const uint8_t flags = (has_lsh ? 1u : 0u) | (has_pq ? 2u : 0u) | (has_norms ? 4u : 0u);
+  const uint8_t flags =
+      (has_lsh ? 1u : 0u) | (has_pq ? 2u : 0u) | (has_norms ? 4u : 0u) | (g.prerotate ? 8u : 0u);
   f.write((const char*)&kTrailerMagic, 4);
   f.write((const char*)&kTrailerVersion, 4);
   f.write((const char*)&flags, 1);
@@ -1201,31 +1204,30 @@ void save_directional_file(const Graph& g, const std::string& path) {
     hip_check(hipMemcpy(nrm.data(), g.vector_norms, nrm.size() * 4, hipMemcpyDeviceToHost), "download norms");
     f.write((const char*)nrm.data(), (std::streamsize)nrm.size() * 4);
   }
+  if (g.prerotate) {
+    const uint64_t seed = g.prerotate_seed;
+    f.write((const char*)&seed, 8);
+  }
   if (!f.good()) throw std::runtime_error("short write while saving " + path);
 }
 
-std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
-                                             uint32_t k_ranks, bool small_dim, bool on_host, bool prerotate,
-                                             uint64_t seed) {
-  uint64_t off = 0;
-  auto g = load_graph_file(path, dim, R, metric, on_host, &off);
-  g->k_ranks = k_ranks;
-  g->packed_bytes = small_dim ? 1 : 2;
-  g->prerotate = prerotate;
-  g->prerotate_seed = seed;
-  if (prerotate) g->rotation = make_rotation(rotation_matrix(dim, seed), dim);
-  if (g->n == 0) return g;
+// The trailer of a directional file from byte `off` (absent or foreign
+// trailers leave the graph as loaded).
+static void read_directional_trailer(Graph& gr, const std::string& path, uint64_t off) {
+  Graph* g = &gr;
+  const uint32_t k_ranks = g->k_ranks, R = g->R;
+  if (g->n == 0) return;
   std::ifstream f(path, std::ios::binary | std::ios::ate);
   if (!f.is_open()) throw std::runtime_error("load_directional_graph_from_file: cannot reopen " + path);
   const uint64_t size = (uint64_t)f.tellg();
-  if (size < off + 9) return g;
+  if (size < off + 9) return;
   f.seekg((std::streamoff)off);
   uint32_t magic = 0, version = 0;
   uint8_t flags = 0;
   f.read((char*)&magic, 4);
   f.read((char*)&version, 4);
   f.read((char*)&flags, 1);
-  if (magic != kTrailerMagic || version != kTrailerVersion) return g;
+  if (magic != kTrailerMagic || version != kTrailerVersion) return;
   if (flags & 1u) {
     uint8_t K = 0, P = 0;
     f.read((char*)&K, 1);
@@ -1276,6 +1278,28 @@ std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t d
     hip_check(hipMalloc(&g->vector_norms, nrm.size() * 4), "alloc norms");
     hip_check(hipMemcpy(g->vector_norms, nrm.data(), nrm.size() * 4, hipMemcpyHostToDevice), "upload norms");
   }
+  if (flags & 8u) {
+    uint64_t s = 0;
+    f.read((char*)&s, 8);
+    if (f.gcount() != 8) throw std::runtime_error("truncated prerotation record in " + path);
+    g->prerotate = true;
+    g->prerotate_seed = s;
+  }
+  return;
+}
+
+std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
+                                             uint32_t k_ranks, bool small_dim, bool on_host, bool prerotate,
+                                             uint64_t seed) {
+  uint64_t off = 0;
+  auto g = load_graph_file(path, dim, R, metric, on_host, &off);
+  g->k_ranks = k_ranks;
+  g->packed_bytes = small_dim ? 1 : 2;
+  g->prerotate = prerotate;
+  g->prerotate_seed = seed;
+  read_directional_trailer(*g, path, off);
+  // a prerotation recorded in the file (flag 8) wins over the arguments
+  if (g->prerotate) g->rotation = make_rotation(rotation_matrix(dim, g->prerotate_seed), dim);
   return g;
 }
 

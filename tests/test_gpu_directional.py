@@ -212,3 +212,26 @@ def test_rotate_operator(jasper, oracle_lib, dim, n):
     assert_rotation_close(g16, x.astype(np.float32), dim)
     got_h = jasper.rotate(torch.from_numpy(x), seed=42)     # host input
     assert torch.equal(got_h.cpu(), got.cpu())
+
+
+def test_prerotation_recorded_in_file(jasper, oracle_lib, tmp_path):
+    # the trailer records the prerotation (flag 8 and the seed); a load that
+    # does not ask for it still rotates queries the same way
+    x = integer_clustered(1500, 64, 71)
+    q = integer_clustered(32, 64, 72)
+    xt = torch.from_numpy(x.astype(np.float16)).cuda()
+    gg = jasper.Graph.build(xt, n_neighbors=32, distance="l2", build_lsh=True, k_ranks=4, prerotate=True,
+                            prerotate_seed=7, lsh_samples=4000, lsh_seed=7)
+    path = tmp_path / "rot.bin"
+    gg.save(str(path))
+    ids, d = _search(gg, "directional_search", q, 10, 32)
+    g2 = jasper.Graph.load(str(path), dim=64, n_neighbors=32, distance="l2", k_ranks=4, prerotate=False)
+    assert g2._prerotate and g2._prerotate_seed == 7
+    assert "prerotate=True" in repr(g2)
+    ids2, d2 = _search(g2, "directional_search", q, 10, 32)
+    assert compare_search(ids2, d2, ids, d) is None
+    # the base section is the reference's format: its loader reads it as before
+    g = oracle.load_graph(path, 64, 32, "l2")
+    assert np.array_equal(g.vecs16, gg.export_vectors())
+    g2.free()
+    gg.free()
