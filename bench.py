@@ -111,7 +111,7 @@ def main() -> int:
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--target-recall", type=float, default=0.95)
-    ap.add_argument("--sweep", default="16,24,32,48,64,96,128,192,256")
+    ap.add_argument("--sweep", default="16,24,32,40,44,48,64,96,128,192,256")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--curve-out", default=None, help="also write the QPS/recall curve as JSON here")
