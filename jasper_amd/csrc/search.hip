@@ -143,12 +143,23 @@ __device__ __forceinline__ float score(const SearchArgs& a, const QueryFrag<CPL,
   return left_distance<CPL, METRIC, false>(q, x, ql, a.nchunks, nlimit);
 }
 
+// Appends the key of a scored row to T[nt..) when its rank is below thr
+// (the quad's first lane writes); returns the new count (wave-uniform).
+__device__ __forceinline__ uint32_t append_key(uint64_t* T, uint32_t nt, bool act, uint32_t ql, float d, uint32_t v,
+                                               uint64_t thr) {
+  const uint64_t key = make_key(d, v);
+  const bool w = ql == 0 && act && key_rank(key) < thr;
+  const uint64_t m = ballot(w);
+  if (w) T[nt + mbcnt(m)] = key;
+  return nt + (uint32_t)__builtin_popcountll(m);
+}
+
 // Scores up to 16 (or 32 with TWO) candidate rows listed in cand[base..)
-// and stores their keys into T[j].
+// and appends the keys that rank below thr to T[nt..); returns the count.
 template <int CPL, int METRIC, bool TWO>
-__device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<CPL, METRIC>& qf, const uint32_t* cand,
-                                           uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql, uint32_t qg,
-                                           bool intx) {
+__device__ __forceinline__ uint32_t score_pass(const SearchArgs& a, const QueryFrag<CPL, METRIC>& qf,
+                                               const uint32_t* cand, uint64_t* T, uint32_t base, uint32_t nm,
+                                               uint32_t ql, uint32_t qg, bool intx, uint64_t thr, uint32_t nt) {
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
   const uint32_t j0 = base + qg;
   const bool act0 = j0 < nm;
@@ -163,11 +174,11 @@ __device__ __forceinline__ void score_pass(const SearchArgs& a, const QueryFrag<
     load_row_frag<CPL>(a.vecs + (size_t)v1 * a.nchunks, ql, a.nchunks, act1, x1);
     const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit, intx);
     const float d1 = score<CPL, METRIC>(a, qf, x1, ql, nlimit, intx);
-    if (ql == 0 && act0) T[j0] = make_key(d0, v0);
-    if (ql == 0 && act1) T[j1] = make_key(d1, v1);
+    nt = append_key(T, nt, act0, ql, d0, v0, thr);
+    return append_key(T, nt, act1, ql, d1, v1, thr);
   } else {
     const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit, intx);
-    if (ql == 0 && act0) T[j0] = make_key(d0, v0);
+    return append_key(T, nt, act0, ql, d0, v0, thr);
   }
 }
 
@@ -325,18 +336,31 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     if (isnew) cand[mbcnt(newm)] = v;
     wave_sync();
 
-    // ---- score the new neighbours (4 lanes per vector)
-    uint32_t base = 0;
+    // ---- score the new neighbours (4 lanes per vector). Once B is full,
+    //      a key ranked above B's last cannot enter: B's bw distinct ranks
+    //      all survive the dedup and precede it, so after the clip it is
+    //      gone; a key equal to B's last is that member again. Only keys
+    //      ranked below B's last are kept (nt of them), and a hop that
+    //      keeps none leaves B as it is.
+    uint64_t thr = ~0ull;
+    if (cnt == bw) thr = key_rank(regb ? readlane64(b, (int)(bw - 1u)) : B[bw - 1u]);
+    uint32_t nt = 0, base = 0;
 #if JASPER_SEARCH_TWO_ROWS
-    for (; base + 16 < nm; base += 32) score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx);
+    for (; base + 16 < nm; base += 32)
+      nt = score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
 #endif
-    for (; base + 16 < nm; base += 16) score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx);
-    if (base < nm) score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx);
+    for (; base + 16 < nm; base += 16)
+      nt = score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+    if (base < nm) nt = score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+    if (nt == 0) {
+      lds_wave_sync();
+      continue;
+    }
     wave_sync();
 
     // ---- sort the new keys
-    uint64_t t = lane < nm ? T[lane] : kEmptyKey;
-    t = wave_sort_upto(t, nm);
+    uint64_t t = lane < nt ? T[lane] : kEmptyKey;
+    t = wave_sort_upto(t, nt);
     if (regb) {
       // B one key per lane: bitonic merge in registers. B ascending against
       // the new keys reversed: the lane-wise minima are a bitonic sequence
@@ -354,7 +378,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       const bool dup = (lane < 63u && x0 != kEmptyKey && key_rank(x0) == key_rank(nx)) ||
                        (last != kEmptyKey && key_rank(x1) == key_rank(last));
       if (ballot(dup) == 0) {
-        cnt = min(cnt + nm, bw);
+        cnt = min(cnt + nt, bw);
         b = lane < cnt ? x0 : kEmptyKey;
         lds_wave_sync();
         continue;
@@ -366,10 +390,10 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     }
     // ---- general path: drop duplicates and members of B, merge by rank
     const uint64_t prev = __shfl_up(t, 1, 64);
-    bool keep = lane < nm && !(lane > 0 && key_rank(prev) == key_rank(t));
+    bool keep = lane < nt && !(lane > 0 && key_rank(prev) == key_rank(t));
     uint32_t lb = 0;
     const uint32_t top = pow2_ceil(cnt);
-    if (lane < nm) {
+    if (lane < nt) {
       lb = lds_lower_bound(B, cnt, top, key_rank(t));
       if (lb < cnt && key_rank(B[lb]) == key_rank(t)) keep = false;
     }
