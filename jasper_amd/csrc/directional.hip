@@ -617,11 +617,12 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   uint64_t* NB = buf1;
   if (lane == 0) B[0] = make_key(0.0f, a.medoid);
   uint32_t cnt = 1, fc = 0, vc = 0, loop = 0, n_hops = 0, n_adj = 0;
+  uint32_t hint = 0;  // every entry of B before `hint` is visited
   wave_sync();
   while (loop <= a.limit) {
     loop += 1;
     int p = -1;
-    for (uint32_t base = 0; base < cnt; base += 64) {
+    for (uint32_t base = hint; base < cnt; base += 64) {
       const uint32_t i = base + lane;
       const bool unv = i < cnt && !key_visited(B[i]);
       const uint64_t m = ballot(unv);
@@ -631,6 +632,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     const uint64_t pk = B[p];
     wave_sync();
     if (lane == 0) B[p] = pk | 1ull;
+    hint = (uint32_t)p + 1u;
     const uint32_t u = key_id(pk);
     if (a.unique) {
       // u already in F: its exact distance and its neighbours' estimates are
@@ -782,45 +784,67 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         t = make_key(FLT_MAX, kInv31) | 1ull;  // INVALID, visited (device_kernels.cuh:115-122)
       }
     }
-    // merge_sort_tail: sort the tail, merge with the head (head first on ties)
-    t = wave_sort_upto(t, deg);
-    if (lane < deg) T[lane] = t;
+    // merge_sort_tail: sort the tail, merge with the head (head first on
+    // ties), drop entries whose id equals the previous one, clip to bw.
+    // Once B is full, a key ranked at or above B's last entry cannot enter:
+    // the merged order puts B's bw entries before it, and each of those the
+    // dedup drops heads no run of equal ids (B holds no two adjacent equal
+    // ids, so a run holds at most one member of B) -- the run is headed by a
+    // kept new key that also precedes it. Only keys ranked below B's last
+    // are merged (nt of them); a hop that keeps none leaves B as it is.
+    const uint64_t thr = cnt == a.bw ? key_rank(B[a.bw - 1u]) : ~0ull;
+    const bool kt = lane < deg && key_rank(t) < thr;
+    const uint64_t km = ballot(kt);
+    const uint32_t nt = (uint32_t)__builtin_popcountll(km);
+    if (nt == 0) {
+      wave_sync();
+      continue;
+    }
+    if (kt) T[mbcnt(km)] = t;
     wave_sync();
+    t = lane < nt ? T[lane] : kEmptyKey;
+    t = wave_sort_upto(t, nt);
+    if (lane < nt) T[lane] = t;
+    wave_sync();
+    // positions below the smallest key's insertion point lo0 keep their
+    // entries; the merge and the dedup start there
     const uint32_t top = pow2_ceil(cnt);
-    if (lane < deg) {
+    uint32_t lo = 0;
+    if (lane < nt) {
       // upper bound: head entries with rank <= rank(t) precede t
-      uint32_t lo = 0;
       for (uint32_t step = top; step > 0; step >>= 1) {
         const uint32_t probe = lo + step;
         if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
       }
       NB[lane + lo] = t;
     }
-    const uint32_t ttop = pow2_ceil(deg);
-    for (uint32_t j = lane; j < cnt; j += 64) {
+    const uint32_t lo0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
+    const uint32_t ttop = pow2_ceil(nt);
+    for (uint32_t j = lo0 + lane; j < cnt; j += 64) {
       const uint64_t bk = B[j];
-      const uint32_t c = deg ? lds_lower_bound(T, deg, ttop, key_rank(bk)) : 0u;
+      const uint32_t c = lds_lower_bound(T, nt, ttop, key_rank(bk));
       NB[j + c] = bk;
     }
     wave_sync();
-    // dedup_results + clip_k: drop entries whose id equals the previous one
-    const uint32_t total = cnt + deg;
-    uint32_t kept = 0;
-    for (uint32_t base = 0; base < total; base += 64) {
+    const uint32_t total = cnt + nt;
+    const uint32_t id0 = lo0 == 0 ? kInv31 : key_id(B[lo0 - 1u]);
+    uint32_t kept = lo0;
+    for (uint32_t base = lo0; base < total; base += 64) {
       const uint32_t m = base + lane;
       bool keep = false;
       uint64_t cur = 0;
       if (m < total) {
         cur = NB[m];
-        const uint32_t prev_id = m == 0 ? kInv31 : key_id(NB[m - 1]);
+        const uint32_t prev_id = m == lo0 ? id0 : key_id(NB[m - 1]);
         keep = key_id(cur) != prev_id;
       }
-      const uint64_t km = ballot(keep);
-      const uint32_t pos = kept + mbcnt(km);
+      const uint64_t kmask = ballot(keep);
+      const uint32_t pos = kept + mbcnt(kmask);
       if (keep && pos < a.bw) B[pos] = cur;
-      kept += (uint32_t)__builtin_popcountll(km);
+      kept += (uint32_t)__builtin_popcountll(kmask);
     }
     cnt = min(kept, a.bw);
+    hint = min(hint, lo0);
     wave_sync();
   }
 

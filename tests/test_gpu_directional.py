@@ -142,7 +142,7 @@ def test_lsh_pq_l2_prerotated(jasper, oracle_lib, tmp_path):
     x = integer_clustered(2500, 128, 22)
     q = integer_clustered(40, 128, 23)
     _case(jasper, tmp_path, x, q, R=64, distance="l2", k_ranks=16, prerotate=True, lsh=True, pq=True,
-          bws=(32, 96))
+          bws=(32, 96, 256))
 
 
 def test_lsh_pq_long_rows(jasper, oracle_lib, tmp_path):
