@@ -228,9 +228,8 @@ def main() -> int:
 
     # ---- algorithmic bytes per launch (exact work counters of the same traversal)
     st = g.search_stats(q_t, k=10, beam_width=chosen).astype(np.int64)
-    dp = 128
     hops, deg, scored = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
-    alg_bytes = int(hops * 1 + deg * 4 + scored * 2 * dp + args.nq * (2 * dp + 8 * 10))
+    alg_bytes = algorithmic_bytes(st, 128, args.nq)
     achieved = alg_bytes / (kernel_ms / 1000.0) / 1e9
     log(f"bw={chosen}: {ms_per_step:.3f} ms/step, kernel {kernel_ms:.3f} ms, qps={qps:,.0f}, "
         f"recall={final_recall:.4f}, hops/q={hops / args.nq:.1f}, scored/q={scored / args.nq:.1f}, "
@@ -290,6 +289,15 @@ def main() -> int:
 
 
 # ------------------------------------------------------------------ other rows
+
+def algorithmic_bytes(st, dp, nq):
+    """Bytes one plain-search launch must move, from its exact work counters
+    [nq, 4] (hops, adjacency entries, vectors scored): a 1-byte degree per
+    hop, 4 bytes per adjacency entry, 2*dp bytes per distinct vector scored,
+    plus the query rows and the k=10 (id, distance) outputs."""
+    hops, deg, scored = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
+    return int(hops * 1 + deg * 4 + scored * 2 * dp + nq * (2 * dp + 8 * 10))
+
 
 def _timed(torch, fn, steps, warmup):
     """Wall ms per call and HIP-event ms per call on the current stream (the
@@ -506,6 +514,8 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
     visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
     alg = int(visits * 2 * dim + hops + adj * (4 + 16 + 2) + nq * (2 * dim + 80))
     ach = alg / (ev / 1000.0) / 1e9
+    g.free()
+    plain = _c5_plain(args, torch, jasper_amd, base, queries, gt, log)
     res = _line(args, "config 5: build vectors/s (100M x 128 in HBM) and QPS @ recall@10>=0.9, directional LSH",
                 nq / (wall / 1000.0), "queries/s", wall, "f16",
                 {"workload": f"config 5: {n} x {dim} clustered integer fp16 (10,000 clusters, generated in HBM), "
@@ -514,15 +524,51 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
                  "build_vectors_per_s": n / build_s, "build_s": build_s, "lsh_s": lsh_s,
                  "rabitq_vectors_per_s": n / rabitq_s, "build_max_batch": int(bst["max_batch"]),
                  "beam_width": bw, "unique": unique, "recall_at_10": rec, "target_recall": 0.9,
-                 "curve": curve, "hbm_used_gb": (total - free) / 1e9},
+                 "curve": curve, "hbm_used_gb": (total - free) / 1e9, "plain_search": plain},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
                  "traffic": None, "kernel": "directional_kernel<L2,LSH>", "kernel_ms": ev,
                  "algorithmic_bytes_per_launch": alg,
                  "per_query": {"visits": float(st[:, 0].mean()), "hops": float(st[:, 1].mean()),
                                "adjacency_entries": float(st[:, 2].mean())}})
     print(json.dumps(res), flush=True)
-    g.free()
     return 0
+
+
+def _c5_plain(args, torch, jasper_amd, base, queries, gt, log):
+    """The same 100M base as a plain graph (Graph.build + search, no
+    prerotation): build vectors/s and the smallest swept beam width whose
+    recall@10 reaches 0.9, with its QPS and HBM roofline."""
+    n, nq = base.size(0), queries.size(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    log(f"c5 plain build {build_s:.1f}s = {n / build_s:,.0f} vec/s")
+    curve, chosen = [], None
+    for bw in (32, 64, 128, 192, 256, 384, 512, 768, 1024):
+        ids, _ = g.search(queries, k=10, beam_width=bw)
+        r = _recall(gt, ids.cpu().numpy())
+        wall, ev, _ = _timed(torch, lambda bw=bw: g.search(queries, k=10, beam_width=bw), 3, 1)
+        curve.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
+        log(f"c5 plain bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+        if r >= 0.9:
+            chosen = bw
+            break
+    if chosen is None:
+        chosen = max(curve, key=lambda c: c["recall_at_10"])["beam_width"]
+    wall, ev, _ = _timed(torch, lambda: g.search(queries, k=10, beam_width=chosen), args.steps, args.warmup)
+    ids, _ = g.search(queries, k=10, beam_width=chosen)
+    rec = _recall(gt, ids.cpu().numpy())
+    st = g.search_stats(queries, k=10, beam_width=chosen).astype(np.int64)
+    alg = algorithmic_bytes(st, 128, nq)
+    ach = alg / (ev / 1000.0) / 1e9
+    log(f"c5 plain bw={chosen}: recall={rec:.4f} qps={nq / (wall / 1000.0):,.0f} kernel {ev:.3f} ms "
+        f"{ach:.0f} GB/s")
+    g.free()
+    return {"build_s": build_s, "build_vectors_per_s": n / build_s, "beam_width": chosen, "recall_at_10": rec,
+            "qps": nq / (wall / 1000.0), "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
+            "achieved_gbs": ach, "frac": ach / PEAK_HBM_GBS, "curve": curve}
 
 
 def run_c4(args, torch, jasper_amd, datasets, dev, log):
