@@ -399,32 +399,43 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     }
     const uint64_t km = ballot(keep);
     const uint32_t nk = (uint32_t)__builtin_popcountll(km);
+    if (nk == 0) {  // every new key was a repeat or a member of B
+      lds_wave_sync();
+      continue;
+    }
     const uint32_t ti = mbcnt(km);
     wave_sync();
     if (keep) T[ti] = t;
     wave_sync();
 
-    // ---- merge by rank into NB, clip to bw
+    // ---- merge by rank into NB, clip to bw. Entries of B below the
+    //      smallest kept key's position lb0 keep their places; only
+    //      positions from lb0 on are merged, and the shorter of the
+    //      unchanged prefix and the merged tail is copied across
+    const uint32_t lb0 = (uint32_t)__shfl((int)lb, (int)__builtin_ctzll(km), 64);
     if (keep) {
       const uint32_t pos = ti + lb;
       if (pos < bw) NB[pos] = t;
     }
     const uint32_t ttop = pow2_ceil(nk);
-    for (uint32_t j = lane; j < cnt; j += 64) {
+    for (uint32_t j = lb0 + lane; j < cnt; j += 64) {
       const uint64_t bk = B[j];
-      const uint32_t c = nk ? lds_lower_bound(T, nk, ttop, key_rank(bk)) : 0u;
+      const uint32_t c = lds_lower_bound(T, nk, ttop, key_rank(bk));
       const uint32_t pos = j + c;
       if (pos < bw) NB[pos] = bk;
     }
-    if (nk) {
-      const uint32_t first = (uint32_t)__builtin_ctzll(km);
-      const uint32_t lb0 = (uint32_t)__shfl((int)lb, (int)first, 64);
-      hint = min(hint, lb0);
+    const uint32_t ncnt = min(cnt + nk, bw);
+    if (lb0 <= ncnt - lb0) {
+      for (uint32_t j = lane; j < lb0; j += 64) NB[j] = B[j];
+      uint64_t* tmp = B;
+      B = NB;
+      NB = tmp;
+    } else {
+      wave_sync();
+      for (uint32_t j = lb0 + lane; j < ncnt; j += 64) B[j] = NB[j];
     }
-    cnt = min(cnt + nk, bw);
-    uint64_t* tmp = B;
-    B = NB;
-    NB = tmp;
+    hint = min(hint, lb0);
+    cnt = ncnt;
     wave_sync();
     if (regb) b = lane < cnt ? B[lane] : kEmptyKey;
   }
@@ -490,11 +501,12 @@ static uint32_t default_hash_bits(uint32_t bw, int64_t n) {
     return (v >= 8 && v <= 15) ? v : 0;
   }();
   if (override_bits) return (uint32_t)override_bits;
-  // LDS budget of the cache: 4 KB at bw <= 64, 8 KB at bw <= 128, else 16 KB
-  // (measured on config 2: 2^11 16-bit entries beat 2^10 (more re-scoring)
-  // and 2^12 (fewer resident waves) at bw 32..64); 16-bit entries when the
-  // ids fit them, else half as many 32-bit ones
-  const uint32_t budget_log2 = bw <= 64 ? 12 : bw <= 128 ? 13 : 14;
+  // LDS budget of the cache: 4 KB at every beam width (measured on config 2:
+  // 2^11 16-bit entries beat 2^10 (more re-scoring) and 2^12 or 2^13 (fewer
+  // resident waves) at bw 32..384); 16-bit entries when the ids fit them,
+  // else half as many 32-bit ones
+  (void)bw;
+  const uint32_t budget_log2 = 12;
   return seen_tag_bits(n, budget_log2 - 1) ? budget_log2 - 1 : budget_log2 - 2;
 }
 

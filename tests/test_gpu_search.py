@@ -53,7 +53,7 @@ def test_search_matches_oracle_integer_l2_r64(jasper, oracle_lib, tmp_path):
     q = integer_clustered(64, 128, 1)
     g = oracle.build(base, R=64, distance="l2", alpha=1.2)
     gg = _load(jasper, g, tmp_path)
-    for bw in (32, 96, 256):
+    for bw in (32, 96, 256, 600):
         ids, d = _run(jasper, gg, q, 10, bw)
         rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
         msg = compare_search(ids, d, rid, rd)
