@@ -485,7 +485,7 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       r.max_result = kBuildMaxResult;
       r.visited = visited;
       r.visited_counts = vcounts;
-      r.hash_bits = 12;
+      r.hash_bits = 11;  // 4 KB seen cache: measured faster than 8 KB (more resident queries)
       timer.start();
       launch_beam_search(g, r, stream);
       timer.stop(st.search_ms);
