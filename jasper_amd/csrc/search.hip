@@ -492,6 +492,19 @@ static uint32_t seen_tag_bits(int64_t n, uint32_t hash_bits) {
   return b - hash_bits <= 15 ? b - hash_bits : 0u;
 }
 
+// Size of the per-query seen cache (2^hash_bits entries) for a graph of n
+// vertices, shared by queries and the build's searches. Up to 2^25 ids the
+// entries are 15-bit tags in two-way sets, 2^11 of them (4 KB): on config 2
+// (1M) this beat 2^10 (more re-scoring) and 2^12 or 2^13 (fewer resident
+// waves) at bw 32..384. Up to 2^27 ids, 2^12 direct-mapped 16-bit tags (8 KB):
+// at 100M vectors they beat 2^10 and 2^11 full 32-bit ids by 9-18 % at bw
+// 32..128. Beyond, 2^11 32-bit ids (8 KB).
+uint32_t seen_cache_hash_bits(int64_t n) {
+  if (n <= ((int64_t)1 << 25)) return 11;
+  if (n <= ((int64_t)1 << 27)) return 12;
+  return 11;
+}
+
 static uint32_t default_hash_bits(uint32_t bw, int64_t n) {
   // JASPER_SEARCH_HASH_BITS (8..15) overrides the size of the per-query seen
   // cache for tuning; the results do not depend on it.
@@ -501,13 +514,8 @@ static uint32_t default_hash_bits(uint32_t bw, int64_t n) {
     return (v >= 8 && v <= 15) ? v : 0;
   }();
   if (override_bits) return (uint32_t)override_bits;
-  // LDS budget of the cache: 4 KB at every beam width (measured on config 2:
-  // 2^11 16-bit entries beat 2^10 (more re-scoring) and 2^12 or 2^13 (fewer
-  // resident waves) at bw 32..384); 16-bit entries when the ids fit them,
-  // else half as many 32-bit ones
   (void)bw;
-  const uint32_t budget_log2 = 12;
-  return seen_tag_bits(n, budget_log2 - 1) ? budget_log2 - 1 : budget_log2 - 2;
+  return seen_cache_hash_bits(n);
 }
 
 size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {

@@ -32,4 +32,7 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
 // LDS bytes one query (one wave) uses for the given request.
 size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r);
 
+// log2 of the seen-cache entries for a graph of n vertices (queries and build).
+uint32_t seen_cache_hash_bits(int64_t n);
+
 }  // namespace jasper_amd
