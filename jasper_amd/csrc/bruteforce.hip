@@ -517,6 +517,8 @@ template <int KS, int METRIC>
 static void launch_filter(const void* base, int64_t n, uint32_t dp, const void* queries, int64_t nq,
                           const float* vsq, const float* qsq, const float* qthr, uint32_t thr_stride,
                           uint32_t* qcount, uint64_t* qcand, hipStream_t s) {
+  // one 32-query tile per wave: two (208 VGPRs) and three (272) measured
+  // 7.48 and 11.7 ms against 7.15 ms on config 2's 10k x 1M ground truth
   constexpr int TILES = 1;
   const int64_t qblocks = (nq + 128 * TILES - 1) / (128 * TILES);
   // about 2,500 work-groups; the query block is the fast grid index so the
