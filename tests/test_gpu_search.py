@@ -38,7 +38,7 @@ def c1_small(oracle_lib):
     return base, q, g
 
 
-@pytest.mark.parametrize("bw", [16, 64, 128])
+@pytest.mark.parametrize("bw", [16, 64, 128, 300])
 def test_search_matches_oracle_gaussian_l2(jasper, c1_small, tmp_path, bw):
     base, q, g = c1_small
     gg = _load(jasper, g, tmp_path)
@@ -77,7 +77,7 @@ def test_search_matches_oracle_ip(jasper, oracle_lib, tmp_path):
     q = unit(48, 96, 6)
     g = oracle.build(base, R=32, distance="ip", alpha=1.2)
     gg = _load(jasper, g, tmp_path)
-    for bw in (16, 64):
+    for bw in (16, 64, 160):
         ids, d = _run(jasper, gg, q, 10, bw)
         rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
         msg = compare_search(ids, d, rid, rd)
@@ -153,7 +153,7 @@ def test_search_matches_oracle_long_rows(jasper, oracle_lib, tmp_path, distance,
         assert msg is None, f"bw={bw}: {msg}"
 
 
-@pytest.mark.parametrize("bw", [16, 64])
+@pytest.mark.parametrize("bw", [16, 64, 128])
 def test_search_stats_match_oracle_counters(jasper, c1_small, tmp_path, bw):
     # the measurement run (exact seen set) walks the same traversal as the
     # reference: hops and degrees read equal the oracle's, vectors scored
