@@ -585,17 +585,46 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     // pq_build_lut: one 32-lane group per centroid, lanes stride dsub
     const uint32_t half = lane >> 5, hl = lane & 31u;
     const uint32_t total = a.M * 256;
-    for (uint32_t e0 = 0; e0 < total; e0 += 2) {
-      const uint32_t e = e0 + half;
-      float acc = 0.0f;
-      if (e < total) {
-        const uint32_t j = e / 256;
-        const float* C = a.centroids + (size_t)e * a.dsub;
-        const uint16_t* qj = q16 + (size_t)j * a.dsub;
-        for (uint32_t t = hl; t < a.dsub; t += 32) acc = __builtin_fmaf(h2f16(qj[t]), C[t], acc);
+    if (a.dsub <= 64) {
+      // at most two strided elements per lane (hl, hl + 32): the centroid
+      // values of kLutBatch entry pairs are loaded together before their
+      // products, so the loads' latency is paid once per batch; each entry
+      // keeps the same fma chain and 32-lane sum
+      constexpr uint32_t kLutBatch = 8;
+      const bool v0 = hl < a.dsub, v1 = hl + 32u < a.dsub;
+      for (uint32_t e0 = 0; e0 < total; e0 += 2 * kLutBatch) {
+        float c0[kLutBatch], c1[kLutBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kLutBatch; ++u) {
+          const uint32_t e = e0 + 2u * u + half;
+          const float* C = a.centroids + (size_t)(e < total ? e : 0u) * a.dsub;
+          c0[u] = (e < total && v0) ? C[hl] : 0.0f;
+          c1[u] = (e < total && v1) ? C[hl + 32u] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kLutBatch; ++u) {
+          const uint32_t e = e0 + 2u * u + half;
+          const uint16_t* qj = q16 + (size_t)(min(e, total - 1u) / 256u) * a.dsub;
+          float acc = 0.0f;
+          if (e < total && v0) acc = __builtin_fmaf(h2f16(qj[hl]), c0[u], acc);
+          if (e < total && v1) acc = __builtin_fmaf(h2f16(qj[hl + 32u]), c1[u], acc);
+          acc = warp32_sum(acc);
+          if (hl == 0 && e < total) lut[e] = acc;
+        }
       }
-      acc = warp32_sum(acc);
-      if (hl == 0 && e < total) lut[e] = acc;
+    } else {
+      for (uint32_t e0 = 0; e0 < total; e0 += 2) {
+        const uint32_t e = e0 + half;
+        float acc = 0.0f;
+        if (e < total) {
+          const uint32_t j = e / 256;
+          const float* C = a.centroids + (size_t)e * a.dsub;
+          const uint16_t* qj = q16 + (size_t)j * a.dsub;
+          for (uint32_t t = hl; t < a.dsub; t += 32) acc = __builtin_fmaf(h2f16(qj[t]), C[t], acc);
+        }
+        acc = warp32_sum(acc);
+        if (hl == 0 && e < total) lut[e] = acc;
+      }
     }
     if constexpr (L2) {
       float p0 = 0.0f, p1 = 0.0f;
