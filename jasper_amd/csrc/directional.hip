@@ -487,6 +487,68 @@ __global__ __launch_bounds__(64) void norms_kernel(const uint16_t* __restrict__ 
 
 // ---------------------------------------------------- directional search --
 
+// LUT entries [e_begin, e_end) of one query (pq_build_lut: entry e =
+// <q_j, C_e> with j = e / 256, pq_beam_search.cuh:32-60): one 32-lane half
+// per entry, lanes stride dsub with an fma chain, then the 32-lane
+// butterfly sum. At dsub <= 64 a lane holds at most two elements (hl,
+// hl + 32) and the centroid values of kLutBatch entry pairs are loaded
+// together before their products; each entry keeps the same chain.
+__device__ __forceinline__ void pq_lut_range(const uint16_t* q16, const float* centroids, uint32_t dsub,
+                                             uint32_t e_begin, uint32_t e_end, float* lut) {
+  const uint32_t lane = lane_id();
+  const uint32_t half = lane >> 5, hl = lane & 31u;
+  if (dsub <= 64) {
+    constexpr uint32_t kLutBatch = 8;
+    const bool v0 = hl < dsub, v1 = hl + 32u < dsub;
+    for (uint32_t e0 = e_begin; e0 < e_end; e0 += 2 * kLutBatch) {
+      float c0[kLutBatch], c1[kLutBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kLutBatch; ++u) {
+        const uint32_t e = e0 + 2u * u + half;
+        const float* C = centroids + (size_t)(e < e_end ? e : e_begin) * dsub;
+        c0[u] = (e < e_end && v0) ? C[hl] : 0.0f;
+        c1[u] = (e < e_end && v1) ? C[hl + 32u] : 0.0f;
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kLutBatch; ++u) {
+        const uint32_t e = e0 + 2u * u + half;
+        const uint16_t* qj = q16 + (size_t)(min(e, e_end - 1u) / 256u) * dsub;
+        float acc = 0.0f;
+        if (e < e_end && v0) acc = __builtin_fmaf(h2f16(qj[hl]), c0[u], acc);
+        if (e < e_end && v1) acc = __builtin_fmaf(h2f16(qj[hl + 32u]), c1[u], acc);
+        acc = warp32_sum(acc);
+        if (hl == 0 && e < e_end) lut[e] = acc;
+      }
+    }
+  } else {
+    for (uint32_t e0 = e_begin; e0 < e_end; e0 += 2) {
+      const uint32_t e = e0 + half;
+      float acc = 0.0f;
+      if (e < e_end) {
+        const float* C = centroids + (size_t)e * dsub;
+        const uint16_t* qj = q16 + (size_t)(e / 256u) * dsub;
+        for (uint32_t t = hl; t < dsub; t += 32) acc = __builtin_fmaf(h2f16(qj[t]), C[t], acc);
+      }
+      acc = warp32_sum(acc);
+      if (hl == 0 && e < e_end) lut[e] = acc;
+    }
+  }
+}
+
+// Every query's LUT [nq, M * 256] in one launch, kLutWaveEntries entries per
+// wave, so the whole GPU builds them instead of one wave per query.
+constexpr uint32_t kLutWaveEntries = 64;
+__global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* __restrict__ queries, uint32_t dp, uint32_t M,
+                                                    uint32_t dsub, const float* __restrict__ centroids,
+                                                    float* __restrict__ lut) {
+  const uint32_t total = M * 256;
+  const uint32_t e_begin = blockIdx.y * kLutWaveEntries;
+  const uint32_t e_end = min(total, e_begin + kLutWaveEntries);
+  pq_lut_range(queries + (size_t)blockIdx.x * dp, centroids, dsub, e_begin, e_end,
+               lut + (size_t)blockIdx.x * total);
+}
+
+
 struct DirArgs {
   const uint16_t* vecs;
   int64_t n;
@@ -509,6 +571,7 @@ struct DirArgs {
   const float* centroids;
   const uint8_t* codes;
   const float* norms;
+  const float* luts;  // [nq, M * 256] from pq_lut_kernel
   // optional work counters per query: {visits, hops expanded, adjacency entries}
   uint32_t* stats;
   // skip pops of ids already in the frontier (distinct results; an extension)
@@ -582,50 +645,11 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
 
   float q_sq = 0.0f;
   if constexpr (PQ) {
-    // pq_build_lut: one 32-lane group per centroid, lanes stride dsub
-    const uint32_t half = lane >> 5, hl = lane & 31u;
-    const uint32_t total = a.M * 256;
-    if (a.dsub <= 64) {
-      // at most two strided elements per lane (hl, hl + 32): the centroid
-      // values of kLutBatch entry pairs are loaded together before their
-      // products, so the loads' latency is paid once per batch; each entry
-      // keeps the same fma chain and 32-lane sum
-      constexpr uint32_t kLutBatch = 8;
-      const bool v0 = hl < a.dsub, v1 = hl + 32u < a.dsub;
-      for (uint32_t e0 = 0; e0 < total; e0 += 2 * kLutBatch) {
-        float c0[kLutBatch], c1[kLutBatch];
-#pragma unroll
-        for (uint32_t u = 0; u < kLutBatch; ++u) {
-          const uint32_t e = e0 + 2u * u + half;
-          const float* C = a.centroids + (size_t)(e < total ? e : 0u) * a.dsub;
-          c0[u] = (e < total && v0) ? C[hl] : 0.0f;
-          c1[u] = (e < total && v1) ? C[hl + 32u] : 0.0f;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kLutBatch; ++u) {
-          const uint32_t e = e0 + 2u * u + half;
-          const uint16_t* qj = q16 + (size_t)(min(e, total - 1u) / 256u) * a.dsub;
-          float acc = 0.0f;
-          if (e < total && v0) acc = __builtin_fmaf(h2f16(qj[hl]), c0[u], acc);
-          if (e < total && v1) acc = __builtin_fmaf(h2f16(qj[hl + 32u]), c1[u], acc);
-          acc = warp32_sum(acc);
-          if (hl == 0 && e < total) lut[e] = acc;
-        }
-      }
-    } else {
-      for (uint32_t e0 = 0; e0 < total; e0 += 2) {
-        const uint32_t e = e0 + half;
-        float acc = 0.0f;
-        if (e < total) {
-          const uint32_t j = e / 256;
-          const float* C = a.centroids + (size_t)e * a.dsub;
-          const uint16_t* qj = q16 + (size_t)j * a.dsub;
-          for (uint32_t t = hl; t < a.dsub; t += 32) acc = __builtin_fmaf(h2f16(qj[t]), C[t], acc);
-        }
-        acc = warp32_sum(acc);
-        if (hl == 0 && e < total) lut[e] = acc;
-      }
-    }
+    // the query's LUT, built by pq_lut_kernel, into LDS
+    const uint32_t total4 = a.M * 64;
+    const float4* src = reinterpret_cast<const float4*>(a.luts + (size_t)qid * a.M * 256);
+    float4* dst = reinterpret_cast<float4*>(lut);
+    for (uint32_t i = lane; i < total4; i += 64) dst[i] = src[i];
     if constexpr (L2) {
       float p0 = 0.0f, p1 = 0.0f;
       for (uint32_t i = lane; i < a.dp; i += 128) {
@@ -1176,6 +1200,15 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
   }
   if (lds > 160 * 1024) throw std::invalid_argument("beam_width, k and dim need more than 160 KB of LDS");
   if (use_pq && a.M > 16) throw std::invalid_argument("pq_search supports at most 16 subspaces");
+  void* luts = nullptr;
+  if (use_pq) {
+    hip_check(hipMallocAsync(&luts, (size_t)nq * a.M * 256 * 4, stream), "alloc PQ tables");
+    const dim3 lgrid((uint32_t)nq, (a.M * 256 + kLutWaveEntries - 1) / kLutWaveEntries);
+    hipLaunchKernelGGL(pq_lut_kernel, lgrid, dim3(64), 0, stream, qsrc, a.dp, a.M, a.dsub, a.centroids,
+                       (float*)luts);
+    hip_check(hipGetLastError(), "launch pq_lut_kernel");
+    a.luts = (const float*)luts;
+  }
   if (!use_pq && !((a.K == 4 || a.K == 16) && (a.pbytes == 1 || a.pbytes == 2)))
     throw std::invalid_argument("k_ranks must be 4 or 16 with 1- or 2-byte words");
   const dim3 grid((uint32_t)nq);
@@ -1203,6 +1236,7 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
   }
+  if (luts) (void)hipFreeAsync(luts, stream);
   if (rot) (void)hipFreeAsync(rot, stream);
   (void)hipFreeAsync(qrows, stream);
 }
