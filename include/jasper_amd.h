@@ -64,13 +64,14 @@ extern "C" {
   int64_t jasper_save_##id(int64_t handle, const char* path);                                 \
   /* GetVector_ :263-300; out: [dim] fp16 device */                                           \
   int64_t jasper_get_vector_##id(int64_t handle, int64_t stable_id, void* out, void* stream); \
-  /* MarkDeleted_ :371-386 (next tier: returns an error) */                                   \
+  /* MarkDeleted_ :371-386; ids: host int32 [n_ids] */                                        \
   int64_t jasper_mark_deleted_##id(int64_t handle, const int32_t* ids, int64_t n_ids);        \
-  /* Consolidate_ :388-397 (next tier: returns an error) */                                   \
+  /* Consolidate_ :388-397 */                                                                 \
   int64_t jasper_consolidate_##id(int64_t handle, double alpha);                              \
-  /* Compact_ :399-408 (next tier: returns an error) */                                       \
+  /* Compact_ :399-408: returns an error, as the reference's default build                  \
+   * (graph_ops.cuh:265-270, JASPER_ENABLE_COMPACT off) */                                    \
   int64_t jasper_compact_##id(int64_t handle);                                                \
-  /* Append_ :412-430 (next tier: returns an error) */                                        \
+  /* Append_ :412-430; out_ids: host int32 [n_vectors] */                                     \
   int64_t jasper_append_##id(int64_t handle, const void* vectors, int64_t n_vectors,          \
                              double alpha, int32_t* out_ids, void* stream);
 
@@ -187,6 +188,13 @@ int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, int64_t n, i
 int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t base_stride, const void* queries,
                                int64_t n_queries, int64_t query_stride, int64_t k, int32_t metric,
                                int32_t* out_ids, float* out_dists, void* stream);
+/* build_pq with m subspaces instead of the config's k_ranks (the
+ * reference's pq_m is k_ranks, graph.cuh:89, so it offers 4 or 16): any m
+ * that divides the padded dim, up to 128 (one subspace per 8 dims at
+ * d = 960 is m = 120). The file trailer records m; this library's loader
+ * reads it back. Otherwise as jasper_build_pq_<cfg> (BuildPq_,
+ * ffi/jasper_ffi_common.cuh:507-528). No reference counterpart. */
+int64_t jasperx_build_pq_m(int64_t handle, int64_t m, int64_t n_train, int64_t kmeans_iter, int64_t seed);
 /* directional_search (use_pq = 0) or pq_search (use_pq = 1) with option
  * flags; no reference counterpart. JASPERX_DIR_UNIQUE skips every pop of a
  * node already in the exact top-k list: the reference's traversal
@@ -206,13 +214,13 @@ int64_t jasperx_directional_search_ex(int64_t handle, int32_t use_pq, const void
 int64_t jasperx_directional_stats(int64_t handle, int32_t use_pq, const void* queries, int64_t n_queries,
                                   int64_t dim, int64_t k, int64_t beam_width, int64_t limit, uint32_t flags,
                                   uint32_t* out_stats, void* stream);
-/* Library build identifier (git-independent), for load checks. */
 /* The prerotation seed of a directional graph (-1 when its rows are not
  * prerotated). Directional files written by this build record the
  * prerotation in the trailer (flag 8, a u64 seed after the other sections;
  * readers of flags 1, 2 and 4 stop before it), and loading them restores it
  * whatever prerotate/seed the caller passed. No reference counterpart. */
 int64_t jasperx_prerotate_seed(int64_t handle);
+/* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 
 #ifdef __cplusplus

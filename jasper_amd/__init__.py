@@ -95,6 +95,7 @@ _AGNOSTIC = {
     "jasperx_rabitq_node_bytes": [_i64],
     "jasperx_directional_stats": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_uint32,
                                   _ptr, _ptr],
+    "jasperx_build_pq_m": [_i64, _i64, _i64, _i64, _i64],
     "jasperx_directional_search_ex": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
                                       ctypes.c_uint32, _ptr],
     "jasperx_bruteforce_knn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, ctypes.c_int32, _ptr, _ptr, _ptr],
@@ -301,8 +302,14 @@ class Graph:
               workspace_budget: str = "10GB", on_host: bool = False, build_lsh: bool = False,
               build_pq: bool = False, k_ranks: int = 4, prerotate: bool | None = None,
               prerotate_seed: int = 42, lsh_samples: int = 32768, lsh_seed: int = 42,
-              pq_train: int = 40000, pq_kmeans_iter: int = 12, pq_seed: int = 123) -> "Graph":
-        """Construct a Vamana graph on the GPU (reference __init__.py:322-428)."""
+              pq_train: int = 40000, pq_kmeans_iter: int = 12, pq_seed: int = 123,
+              pq_m: int | None = None) -> "Graph":
+        """Construct a Vamana graph on the GPU (reference __init__.py:322-428).
+
+        pq_m (an extension, no reference counterpart) sets the number of PQ
+        subspaces; None keeps the reference's pq_m = k_ranks. Any value that
+        divides the padded dim, up to 128, e.g. 120 for one subspace per 8
+        dims at d = 960."""
         if isinstance(distance, str):
             distance = DistanceFunc(distance)
         workspace_budget_bytes = parse_storage_size(workspace_budget)
@@ -329,7 +336,10 @@ class Graph:
         if build_lsh:
             _op("build_lsh", config_id)(handle, lsh_samples, lsh_seed)
         if build_pq:
-            _op("build_pq", config_id)(handle, pq_train, pq_kmeans_iter, pq_seed)
+            if pq_m is None or pq_m == k_ranks:
+                _op("build_pq", config_id)(handle, pq_train, pq_kmeans_iter, pq_seed)
+            else:
+                _agnostic("jasperx_build_pq_m")(handle, pq_m, pq_train, pq_kmeans_iter, pq_seed)
         return cls(handle, config_id, data_type, distance, n_neighbors, dim,
                    is_directional=True, k_ranks=k_ranks, has_lsh=build_lsh, has_pq=build_pq,
                    prerotate=resolved_prerotate, prerotate_seed=prerotate_seed)
@@ -576,7 +586,7 @@ class Graph:
         self._check_alive()
         fn = _agnostic("jasperx_export_pq")
         dsub = fn(self._handle, None, None, None)
-        M = self._k_ranks
+        M = ((self._dim + 7) // 8 * 8) // dsub
         cent = np.empty(M * 256 * dsub, dtype=np.float32)
         codes = np.empty((self.n_vectors, M * self._n_neighbors), dtype=np.uint8)
         norms = np.empty(self.n_vectors, dtype=np.float32)

@@ -789,7 +789,6 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
     pa.pc.R = R;
     pa.pc.alpha = alpha;
     pa.pc.margin_scale = gram_margin_scale();
-  pa.pc.margin_scale = gram_margin_scale();
     {
       const _Float16 lo = (_Float16)int_lo;
       uint16_t bits;

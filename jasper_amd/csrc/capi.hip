@@ -19,6 +19,7 @@
 #include "bruteforce.hpp"
 #include "build.hpp"
 #include "common.hpp"
+#include "directional.hpp"
 #include "directional_api.hpp"
 #include "graph.hpp"
 #include "rabitq.hpp"
@@ -476,8 +477,7 @@ extern "C" int64_t jasperx_export_pq(int64_t h, float* centroids, uint8_t* codes
     const PqArtifacts& a = *g.pq;
     if (centroids)
       hip_check(hipMemcpy(centroids, a.centroids, (size_t)a.m * 256 * a.dsub * 4, hipMemcpyDefault), "download centroids");
-    if (codes && g.n > 0)
-      hip_check(hipMemcpy(codes, a.codes, (size_t)g.n * a.m * g.R, hipMemcpyDefault), "download codes");
+    if (codes && g.n > 0) pq_codes_to_file_layout(g, codes);
     if (norms && g.n > 0 && g.vector_norms)
       hip_check(hipMemcpy(norms, g.vector_norms, (size_t)g.n * 4, hipMemcpyDefault), "download norms");
     return (int64_t)a.dsub;
@@ -548,6 +548,17 @@ extern "C" int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t d
     if (((uintptr_t)base & 15u) || ((uintptr_t)queries & 15u)) throw std::invalid_argument("rows must be 16-byte aligned");
     bruteforce_knn(base, n, (uint32_t)dim, (uint32_t)base_stride, queries, nq, (uint32_t)k, metric, out_ids,
                    out_dists, (hipStream_t)stream);
+    return 0;
+  });
+}
+
+extern "C" int64_t jasperx_build_pq_m(int64_t h, int64_t m, int64_t n_train, int64_t iters, int64_t seed) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (g.k_ranks == 0) throw std::invalid_argument("build_pq needs a directional graph");
+    if (m <= 0 || m > (int64_t)kPqMaxM)
+      throw std::invalid_argument("m must be in 1.." + std::to_string(kPqMaxM));
+    build_pq(g, n_train, iters, (uint64_t)seed, (uint32_t)m);
     return 0;
   });
 }

@@ -107,6 +107,12 @@ __host__ __device__ __forceinline__ uint64_t pq_hash(uint64_t x, uint64_t seed) 
   return x ^ (x >> 31);
 }
 
+// Offset of subspace j's code for edge e inside a vertex's device code row
+// (the edge-interleaved layout [G][R][W] of PqArtifacts).
+__host__ __device__ __forceinline__ size_t pq_code_at(uint32_t j, uint32_t e, uint32_t R, uint32_t W) {
+  return ((size_t)(j / W) * R + e) * W + (j % W);
+}
+
 // A random valid edge (u -> nb) for sample s, up to 8 attempts
 // (lsh_globals.cuh:46-67, pq_kernels.cuh:77-93).
 __device__ bool sample_edge(const uint32_t* edges, const uint8_t* counts, int64_t n, uint32_t R, uint64_t seed,
@@ -366,10 +372,11 @@ __global__ __launch_bounds__(64) void pq_encode_kernel(const uint16_t* __restric
                                                        const uint8_t* __restrict__ counts, uint32_t R, uint32_t M,
                                                        uint32_t dsub, const float* __restrict__ C,
                                                        uint8_t* __restrict__ codes) {
-  extern __shared__ float res[];  // [dp] then M*R staged codes
+  extern __shared__ float res[];  // [dp] then the vertex's staged code row
   uint8_t* stage = reinterpret_cast<uint8_t*>(res + dp);
   const uint32_t lane = threadIdx.x;
-  const uint32_t row_bytes = M * R;
+  const uint32_t W = pq_group_width(M);
+  const uint32_t row_bytes = (uint32_t)pq_row_bytes(M, R);
   for (int64_t u = blockIdx.x; u < n; u += gridDim.x) {
     for (uint32_t b = lane; b < row_bytes; b += 64) stage[b] = 0;
     const uint32_t cnt = min((uint32_t)counts[u], R);
@@ -398,7 +405,7 @@ __global__ __launch_bounds__(64) void pq_encode_kernel(const uint16_t* __restric
           const uint32_t oi = (uint32_t)__shfl_xor((int)bi, dd, 64);
           if (ob < best || (ob == best && oi < bi)) { best = ob; bi = oi; }
         }
-        if (lane == 0) stage[(size_t)j * R + e] = (uint8_t)bi;
+        if (lane == 0) stage[pq_code_at(j, e, R, W)] = (uint8_t)bi;
       }
     }
     wave_sync();
@@ -431,7 +438,8 @@ __global__ __launch_bounds__(256) void pq_encode_lds_kernel(const uint16_t* __re
   }
   __syncthreads();
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const size_t row_bytes = (size_t)M * R;
+  const uint32_t W = pq_group_width(M);
+  const size_t row_bytes = pq_row_bytes(M, R);
   for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < n; u += (int64_t)gridDim.x * 4) {
     const uint32_t cnt = min((uint32_t)counts[u], R);
     const bool act = lane < cnt;
@@ -461,7 +469,7 @@ __global__ __launch_bounds__(256) void pq_encode_lds_kernel(const uint16_t* __re
         bi = c;
       }
     }
-    if (lane < R) codes[(size_t)u * row_bytes + (size_t)j * R + lane] = act ? (uint8_t)bi : (uint8_t)0;
+    if (lane < R) codes[(size_t)u * row_bytes + pq_code_at(j, lane, R, W)] = act ? (uint8_t)bi : (uint8_t)0;
   }
 }
 
@@ -482,6 +490,24 @@ __global__ __launch_bounds__(64) void norms_kernel(const uint16_t* __restrict__ 
     }
     const float s = block128_sum(p0, p1);
     if (lane == 0) out[u] = s;
+  }
+}
+
+// Codes between the device layout and the file's subspace-major rows
+// [M][R] for vertices [u0, u0 + count): one thread per (vertex, edge).
+// to_file: dev -> file; otherwise file -> dev (the padding bytes of dev's
+// last group must already be zero).
+__global__ void pq_layout_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t count,
+                                 uint32_t R, uint32_t M, bool to_file) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= count * R) return;
+  const int64_t u = t / R;
+  const uint32_t e = (uint32_t)(t % R), W = pq_group_width(M);
+  const size_t dev_row = pq_row_bytes(M, R), file_row = (size_t)M * R;
+  for (uint32_t j = 0; j < M; ++j) {
+    const size_t di = (size_t)u * dev_row + pq_code_at(j, e, R, W), fi = (size_t)u * file_row + (size_t)j * R + e;
+    if (to_file) dst[fi] = src[di];
+    else dst[di] = src[fi];
   }
 }
 
@@ -548,6 +574,33 @@ __global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* __restrict__
                lut + (size_t)blockIdx.x * total);
 }
 
+// dsub <= 32: one table entry per thread; a 256-thread block builds the 256
+// entries of subspace j = blockIdx.y for query blockIdx.x. In the 32-lane
+// form above, lane t holds the leaf v_t = fma(q_t, C_t, +0.0) for t < dsub
+// and +0.0 beyond, and the butterfly leaves the writing lane with the tree
+// v_l + v_(l+16), then + the partner 8 lanes away, 4, 2, 1. The thread sums
+// its own leaves in that tree. Leaves past DS are left out, which is exact:
+// no leaf is -0.0 (fma(a, b, +0.0) of a zero product is +0.0) and
+// x + 0.0 == x for every other x.
+template <int DS>
+__global__ __launch_bounds__(256) void pq_lut_small_kernel(const uint16_t* __restrict__ queries, uint32_t dp,
+                                                           uint32_t M, uint32_t dsub,
+                                                           const float* __restrict__ centroids,
+                                                           float* __restrict__ lut) {
+  const uint32_t e = blockIdx.y * 256 + threadIdx.x;
+  const uint16_t* qj = queries + (size_t)blockIdx.x * dp + (size_t)blockIdx.y * dsub;
+  const float* C = centroids + (size_t)e * dsub;
+  float v[DS];
+#pragma unroll
+  for (int t = 0; t < DS; ++t) v[t] = (uint32_t)t < dsub ? __builtin_fmaf(h2f16(qj[t]), C[t], 0.0f) : 0.0f;
+#pragma unroll
+  for (int h = 16; h >= 1; h >>= 1) {
+#pragma unroll
+    for (int t = 0; t < h; ++t)
+      if (t + h < DS) v[t] = v[t] + v[t + h];
+  }
+  lut[(size_t)blockIdx.x * M * 256 + e] = v[0];
+}
 
 struct DirArgs {
   const uint16_t* vecs;
@@ -569,7 +622,8 @@ struct DirArgs {
   // PQ
   uint32_t M, dsub;
   const float* centroids;
-  const uint8_t* codes;
+  const uint8_t* codes;  // edge-interleaved rows of code_row_bytes
+  uint32_t code_row_bytes, pq_w, pq_groups;
   const float* norms;
   const float* luts;  // [nq, M * 256] from pq_lut_kernel
   // optional work counters per query: {visits, hops expanded, adjacency entries}
@@ -618,7 +672,9 @@ __device__ __forceinline__ uint32_t lsh_word(const uint32_t* w, int r) {
   else return (w[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
 }
 
-// K = 0: the PQ estimator; K in {4, 16} with P-byte words: the LSH estimator.
+// K = 0: the PQ estimator, with up to 16 * P subspaces (the edge's codes are
+// P groups of 16 bytes in registers); K in {4, 16} with P-byte words: the
+// LSH estimator.
 template <int METRIC, int K, int P>
 __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
@@ -708,7 +764,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     const uint32_t v_raw = slot ? a.edges[(size_t)u * a.R + lane] : 0u;
     uint32_t wl[KW];
     uint32_t mag_bits = 0;
-    uint8_t codes[PQ ? 16 : 1];
+    uint4 cw[PQ ? P : 1];  // PQ: codes of subspaces 16g .. 16g + 15 in cw[g]
     if constexpr (!PQ) {
       const uint8_t* row = a.lsh_rows + (size_t)u * a.row_bytes;
       if (slot) {
@@ -730,9 +786,23 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         for (int c = 0; c < KW; ++c) wl[c] = 0;
       }
     } else {
-      const uint8_t* code = a.codes + (size_t)u * a.M * a.R;
+      const uint8_t* crow = a.codes + (size_t)u * a.code_row_bytes + (size_t)lane * a.pq_w;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) codes[j] = (slot && (uint32_t)j < a.M) ? code[(size_t)j * a.R + lane] : (uint8_t)0;
+      for (int g = 0; g < (PQ ? P : 1); ++g) {
+        cw[g] = make_uint4(0u, 0u, 0u, 0u);
+        if (slot && (uint32_t)g < a.pq_groups) {
+          const uint8_t* cp = crow + (size_t)g * a.R * a.pq_w;
+          if (a.pq_w == 16) {
+            cw[g] = *reinterpret_cast<const uint4*>(cp);
+          } else if (a.pq_w == 8) {
+            const uint2 t2 = *reinterpret_cast<const uint2*>(cp);
+            cw[g].x = t2.x;
+            cw[g].y = t2.y;
+          } else {
+            cw[g].x = *reinterpret_cast<const uint32_t*>(cp);
+          }
+        }
+      }
     }
     const uint32_t deg = min(deg_raw, a.R);
     const bool has = lane < deg;
@@ -811,8 +881,23 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       if (valid_v) {
         float est;
         if constexpr (PQ) {
+          // acc = <q,u> + sum over j = 0, 1, ..., M - 1 of LUT[j][code_j], in
+          // that order (pq_beam_search.cuh:97-100)
           float acc = qu_dot;
-          for (uint32_t j = 0; j < a.M; ++j) acc = acc + lut[j * 256 + codes[j]];
+          const uint32_t full = a.M >> 4, rem = a.M & 15u;
+#pragma unroll
+          for (int g = 0; g < (PQ ? P : 1); ++g) {
+            const uint32_t w4[4] = {cw[g].x, cw[g].y, cw[g].z, cw[g].w};
+            const float* lg = lut + g * 16 * 256;
+            if ((uint32_t)g < full) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) acc = acc + lg[i * 256 + ((w4[i >> 2] >> (8 * (i & 3))) & 0xFFu)];
+            } else if ((uint32_t)g == full) {
+#pragma unroll
+              for (int i = 0; i < 15; ++i)
+                if ((uint32_t)i < rem) acc = acc + lg[i * 256 + ((w4[i >> 2] >> (8 * (i & 3))) & 0xFFu)];
+            }
+          }
           est = L2 ? (q_sq - 2.0f * acc) + vnorm : -acc;
         } else {
           const uint16_t* x16 = L2 ? reinterpret_cast<const uint16_t*>(xv) : q16;
@@ -957,8 +1042,7 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
     hip_check(hipMalloc(&tmp, (size_t)n * g->dp * 2), "alloc rotation output");
     rotate_rows(*g->rotation, g->vecs, n, g->dp, tmp, g->dp, stream);
     hip_check(hipMemcpyAsync(g->vecs, tmp, (size_t)n * g->dp * 2, hipMemcpyDeviceToDevice, stream), "copy rotated");
-    g->int_state = 0;
-    hip_check(hipStreamSynchronize(stream), "sync rotation");
+    scan_int_range(*g, 0, n, stream);  // synchronises the stream
     (void)hipFree(tmp);
   }
   const int64_t mbs = reference_max_batch(n, R, budget);
@@ -1040,12 +1124,13 @@ static void compute_norms(Graph& g) {
   hip_check(hipGetLastError(), "launch norms_kernel");
 }
 
-void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed) {
+void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed, uint32_t m) {
   if (g.n <= 0) throw std::runtime_error("generate_pq_codebooks: graph is empty");
-  const uint32_t M = g.k_ranks;
+  const uint32_t M = m ? m : g.k_ranks;
   if (M == 0 || g.dp % M != 0)
     throw std::runtime_error("generate_pq_codebooks: padded_dim (" + std::to_string(g.dp) +
                              ") must be divisible by M=" + std::to_string(M));
+  if (M > kPqMaxM) throw std::invalid_argument("PQ supports at most " + std::to_string(kPqMaxM) + " subspaces");
   const uint32_t dsub = g.dp / M;
   if (n_train < 256) n_train = 256;
   uint16_t* X = nullptr;
@@ -1073,7 +1158,9 @@ void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed) {
                          g.dp, M, dsub, labels, init_seed, (uint32_t)it, art->centroids);
     }
     hip_check(hipGetLastError(), "launch pq training");
-    hip_check(hipMalloc(&art->codes, (size_t)g.n * M * g.R), "alloc pq codes");
+    const size_t code_bytes = (size_t)g.n * pq_row_bytes(M, g.R);
+    hip_check(hipMalloc(&art->codes, code_bytes), "alloc pq codes");
+    hip_check(hipMemset(art->codes, 0, code_bytes), "clear pq codes");
     if (dsub <= 64) {
       // subspace centroids in LDS, one edge per lane
       const uint32_t gx = (uint32_t)std::max<int64_t>(1, std::min<int64_t>((g.n + 3) / 4, 2048 / M + 1));
@@ -1091,7 +1178,7 @@ void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed) {
       hip_check(hipGetLastError(), "launch pq_encode_lds_kernel");
     } else {
       const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
-      const size_t elds = (size_t)g.dp * 4 + (size_t)M * g.R;
+      const size_t elds = (size_t)g.dp * 4 + pq_row_bytes(M, g.R);
       if (elds > 160 * 1024) throw std::invalid_argument("dim too large for the PQ encoder");
       if (elds > 64 * 1024)
         hip_check(hipFuncSetAttribute((const void*)pq_encode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1112,51 +1199,151 @@ void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed) {
   g.pq = std::move(art);
 }
 
-// Padded and, when the graph was prerotated, rotated query rows [nq, dp] in
-// device memory from the stream's pool; *scratch is a second buffer to free.
-static const uint16_t* directional_query_rows(const Graph& g, const void* queries, int64_t nq, int64_t dim,
-                                              hipStream_t stream, void** qrows, void** rot) {
-  *qrows = nullptr;
-  *rot = nullptr;
-  hip_check(hipMallocAsync(qrows, (size_t)nq * g.dp * 2, stream), "alloc query rows");
-  hip_check(hipMemsetAsync(*qrows, 0, (size_t)nq * g.dp * 2, stream), "clear query rows");
-  hip_check(hipMemcpy2DAsync(*qrows, (size_t)g.dp * 2, queries, (size_t)dim * 2, (size_t)dim * 2, (size_t)nq,
-                             hipMemcpyDefault, stream),
-            "copy queries");
-  if (!g.prerotate) return (const uint16_t*)*qrows;
-  if (!g.rotation) throw std::runtime_error("prerotated graph has no rotation matrix");
-  hip_check(hipMallocAsync(rot, (size_t)nq * g.dp * 2, stream), "alloc rotated queries");
-  rotate_rows(*g.rotation, *qrows, nq, g.dp, *rot, g.dp, stream);
-  return (const uint16_t*)*rot;
+// Query rows [nq, dim] (device memory) into rows of stride dp, zero padded.
+__global__ void pad_rows_kernel(const uint16_t* __restrict__ src, int64_t nq, uint32_t dim, uint32_t dp,
+                                uint16_t* __restrict__ dst) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= nq * dp) return;
+  const int64_t r = t / dp;
+  const uint32_t i = (uint32_t)(t % dp);
+  dst[t] = i < dim ? src[(size_t)r * dim + i] : (uint16_t)0;
 }
 
-void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t nq, int64_t dim, uint16_t* out,
-                                    hipStream_t stream) {
-  if (dim != (int64_t)g.dim) throw std::invalid_argument("query dim does not match the graph");
-  if (nq <= 0) return;
-  void *qrows, *rot;
-  const uint16_t* rows = directional_query_rows(g, queries, nq, dim, stream, &qrows, &rot);
-  hip_check(hipMemcpyAsync(out, rows, (size_t)nq * g.dp * 2, hipMemcpyDefault, stream), "download query rows");
-  hip_check(hipStreamSynchronize(stream), "sync query rows");
-  if (rot) (void)hipFreeAsync(rot, stream);
-  (void)hipFreeAsync(qrows, stream);
+namespace {
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Device scratch of one directional search: either stream-ordered
+// allocations that are freed (stream-ordered) when the search returns or
+// throws, or slices of a caller-provided buffer, which allocate nothing.
+class SearchScratch {
+ public:
+  explicit SearchScratch(hipStream_t s) : s_(s) {}
+  SearchScratch(hipStream_t s, void* base, size_t cap) : s_(s), base_((char*)base), cap_(cap) {}
+  SearchScratch(const SearchScratch&) = delete;
+  SearchScratch& operator=(const SearchScratch&) = delete;
+  ~SearchScratch() {
+    for (void* p : owned_) (void)hipFreeAsync(p, s_);
+  }
+  bool fixed() const { return base_ != nullptr; }
+  void* take(size_t bytes) {
+    bytes = round256(bytes);
+    if (base_) {
+      if (used_ + bytes > cap_) throw std::logic_error("directional search scratch overrun");
+      void* p = base_ + used_;
+      used_ += bytes;
+      return p;
+    }
+    void* p = nullptr;
+    hip_check(hipMallocAsync(&p, bytes, s_), "alloc directional search scratch");
+    owned_.push_back(p);
+    return p;
+  }
+
+ private:
+  hipStream_t s_;
+  char* base_ = nullptr;
+  size_t cap_ = 0, used_ = 0;
+  std::vector<void*> owned_;
+};
+
+// Timing events of print_throughput, destroyed on every exit.
+struct EventPair {
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  ~EventPair() {
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+  }
+};
+
+bool device_rows(const void* p) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
-void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
-                        float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
-                        uint32_t* stats, bool unique) {
+// Padded and, when the graph was prerotated, rotated query rows [nq, dp]
+// in scratch. Device queries are padded by a kernel; host queries (only
+// with allocating scratch) by a copy.
+const uint16_t* directional_query_rows(const Graph& g, const void* queries, int64_t nq, int64_t dim,
+                                       hipStream_t stream, SearchScratch& scratch) {
+  if (g.prerotate && !g.rotation) throw std::runtime_error("prerotated graph has no rotation matrix");
+  uint16_t* rows = (uint16_t*)scratch.take((size_t)nq * g.dp * 2);
+  if (device_rows(queries)) {
+    const int64_t total = nq * (int64_t)g.dp;
+    hipLaunchKernelGGL(pad_rows_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, stream,
+                       (const uint16_t*)queries, nq, (uint32_t)dim, g.dp, rows);
+    hip_check(hipGetLastError(), "launch pad_rows_kernel");
+  } else {
+    if (scratch.fixed()) throw std::invalid_argument("queries must be device memory");
+    hip_check(hipMemsetAsync(rows, 0, (size_t)nq * g.dp * 2, stream), "clear query rows");
+    hip_check(hipMemcpy2DAsync(rows, (size_t)g.dp * 2, queries, (size_t)dim * 2, (size_t)dim * 2, (size_t)nq,
+                               hipMemcpyDefault, stream),
+              "copy queries");
+  }
+  if (!g.prerotate) return rows;
+  uint16_t* rot = (uint16_t*)scratch.take((size_t)nq * g.dp * 2);
+  rotate_rows(*g.rotation, rows, nq, g.dp, rot, g.dp, stream);
+  return rot;
+}
+
+size_t directional_lds_bytes(const Graph& g, bool use_pq, int64_t k, int64_t bw) {
+  size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
+  if (use_pq) lds += (size_t)g.pq->m * 256 * 4;
+  return lds;
+}
+
+// Every argument check of directional_search, before anything is allocated
+// or launched.
+void check_directional_search(const Graph& g, bool use_pq, int64_t nq, int64_t dim, int64_t k, int64_t bw,
+                              int64_t limit) {
   if (use_pq && !g.pq) throw std::runtime_error("graph has no PQ artifacts built — call build_pq() first");
   if (!use_pq && !g.lsh) throw std::runtime_error("graph has no LSH artifacts built — call build_lsh() first");
   if (dim != (int64_t)g.dim)
     throw std::invalid_argument("query dim (" + std::to_string(dim) + ") != graph dim (" + std::to_string(g.dim) + ")");
   if (nq < 0 || k < 0 || bw <= 0 || limit < 0) throw std::invalid_argument("negative size argument");
-  if (nq == 0 || k == 0) return;
+  if (nq > 0x7FFFFFFF) throw std::invalid_argument("too many queries");
   if (bw + 64 >= 2048)
     throw std::invalid_argument("beam_width " + std::to_string(bw) + " is too large (beam_width + 64 must be < 2048)");
   if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  if (g.n <= 0) throw std::runtime_error("graph is empty");
   if ((int64_t)g.medoid >= g.n) throw std::runtime_error("graph medoid is out of range");
-  void *qrows, *rot;
-  const uint16_t* qsrc = directional_query_rows(g, queries, nq, dim, stream, &qrows, &rot);
+  if (use_pq) {
+    if (g.metric == kL2 && !g.vector_norms) throw std::runtime_error("graph has no vector norms");
+    if (g.pq->m == 0 || g.pq->m > kPqMaxM)
+      throw std::invalid_argument("pq_search supports at most " + std::to_string(kPqMaxM) + " subspaces");
+  } else if (!((g.lsh->k_ranks == 4 || g.lsh->k_ranks == 16) &&
+               (g.lsh->packed_bytes == 1 || g.lsh->packed_bytes == 2))) {
+    throw std::invalid_argument("k_ranks must be 4 or 16 with 1- or 2-byte words");
+  }
+  if (directional_lds_bytes(g, use_pq, k, bw) > 160 * 1024)
+    throw std::invalid_argument("beam_width, k and dim need more than 160 KB of LDS");
+}
+
+template <int METRIC, int K, int P>
+void launch_directional(const DirArgs& a, uint32_t nq, size_t lds, hipStream_t stream) {
+  auto kern = directional_kernel<METRIC, K, P>;
+  if (lds > 64 * 1024)
+    hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+              "LDS size");
+  hipLaunchKernelGGL(kern, dim3(nq), dim3(64), lds, stream, a);
+}
+
+// The search after check_directional_search, with its device buffers taken
+// from `scratch`.
+void directional_search_run(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+                            float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
+                            uint32_t* stats, bool unique, SearchScratch& scratch) {
+  EventPair ev;
+  if (print) {
+    hip_check(hipEventCreate(&ev.e0), "event");
+    hip_check(hipEventCreate(&ev.e1), "event");
+    hip_check(hipEventRecord(ev.e0, stream), "event record");
+  }
+  const uint16_t* qsrc = directional_query_rows(g, queries, nq, dim, stream, scratch);
   DirArgs a{};
   a.vecs = (const uint16_t*)g.vecs;
   a.n = g.n;
@@ -1175,15 +1362,38 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
   a.out_dists = out_dists;
   a.stats = stats;
   a.unique = unique ? 1u : 0u;
-  size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
+  const size_t lds = directional_lds_bytes(g, use_pq, k, bw);
+  const bool l2 = g.metric == kL2;
   if (use_pq) {
     a.M = g.pq->m;
     a.dsub = g.pq->dsub;
     a.centroids = g.pq->centroids;
     a.codes = g.pq->codes;
+    a.code_row_bytes = (uint32_t)pq_row_bytes(a.M, g.R);
+    a.pq_w = pq_group_width(a.M);
+    a.pq_groups = pq_groups(a.M);
     a.norms = g.vector_norms;
-    lds += (size_t)a.M * 256 * 4;
-    if (g.metric == kL2 && !g.vector_norms) throw std::runtime_error("graph has no vector norms");
+    float* luts = (float*)scratch.take((size_t)nq * a.M * 256 * 4);
+    const auto small_lut = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3((uint32_t)nq, a.M), dim3(256), 0, stream, qsrc, a.dp, a.M, a.dsub, a.centroids,
+                         luts);
+    };
+    if (a.dsub <= 8) small_lut(pq_lut_small_kernel<8>);
+    else if (a.dsub <= 16) small_lut(pq_lut_small_kernel<16>);
+    else if (a.dsub <= 32) small_lut(pq_lut_small_kernel<32>);
+    else {
+      const dim3 lgrid((uint32_t)nq, (a.M * 256 + kLutWaveEntries - 1) / kLutWaveEntries);
+      hipLaunchKernelGGL(pq_lut_kernel, lgrid, dim3(64), 0, stream, qsrc, a.dp, a.M, a.dsub, a.centroids, luts);
+    }
+    hip_check(hipGetLastError(), "launch PQ table kernel");
+    a.luts = luts;
+    if (a.M <= 16) {
+      if (l2) launch_directional<kL2, 0, 1>(a, (uint32_t)nq, lds, stream);
+      else launch_directional<kIP, 0, 1>(a, (uint32_t)nq, lds, stream);
+    } else {
+      if (l2) launch_directional<kL2, 0, 8>(a, (uint32_t)nq, lds, stream);
+      else launch_directional<kIP, 0, 8>(a, (uint32_t)nq, lds, stream);
+    }
   } else {
     a.K = g.lsh->k_ranks;
     a.pbytes = g.lsh->packed_bytes;
@@ -1191,54 +1401,77 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
     a.row_bytes = (uint32_t)g.lsh->row_bytes;
     for (uint32_t r = 0; r < a.K; ++r) a.c[r] = g.lsh->c_per_rank[r];
     a.inv_norm_denom = 1.0f / g.lsh->norm_denom;
+    const uint32_t n32 = (uint32_t)nq;
+    if (a.K == 4 && a.pbytes == 1) {
+      if (l2) launch_directional<kL2, 4, 1>(a, n32, lds, stream);
+      else launch_directional<kIP, 4, 1>(a, n32, lds, stream);
+    } else if (a.K == 16 && a.pbytes == 1) {
+      if (l2) launch_directional<kL2, 16, 1>(a, n32, lds, stream);
+      else launch_directional<kIP, 16, 1>(a, n32, lds, stream);
+    } else if (a.K == 4) {
+      if (l2) launch_directional<kL2, 4, 2>(a, n32, lds, stream);
+      else launch_directional<kIP, 4, 2>(a, n32, lds, stream);
+    } else {
+      if (l2) launch_directional<kL2, 16, 2>(a, n32, lds, stream);
+      else launch_directional<kIP, 16, 2>(a, n32, lds, stream);
+    }
   }
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (print) {
-    hip_check(hipEventCreate(&e0), "event");
-    hip_check(hipEventCreate(&e1), "event");
-    hip_check(hipEventRecord(e0, stream), "event record");
-  }
-  if (lds > 160 * 1024) throw std::invalid_argument("beam_width, k and dim need more than 160 KB of LDS");
-  if (use_pq && a.M > 16) throw std::invalid_argument("pq_search supports at most 16 subspaces");
-  void* luts = nullptr;
-  if (use_pq) {
-    hip_check(hipMallocAsync(&luts, (size_t)nq * a.M * 256 * 4, stream), "alloc PQ tables");
-    const dim3 lgrid((uint32_t)nq, (a.M * 256 + kLutWaveEntries - 1) / kLutWaveEntries);
-    hipLaunchKernelGGL(pq_lut_kernel, lgrid, dim3(64), 0, stream, qsrc, a.dp, a.M, a.dsub, a.centroids,
-                       (float*)luts);
-    hip_check(hipGetLastError(), "launch pq_lut_kernel");
-    a.luts = (const float*)luts;
-  }
-  if (!use_pq && !((a.K == 4 || a.K == 16) && (a.pbytes == 1 || a.pbytes == 2)))
-    throw std::invalid_argument("k_ranks must be 4 or 16 with 1- or 2-byte words");
-  const dim3 grid((uint32_t)nq);
-  auto launch = [&](auto kern) {
-    if (lds > 64 * 1024)
-      hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                "LDS size");
-    hipLaunchKernelGGL(kern, grid, dim3(64), lds, stream, a);
-  };
-  const bool l2 = g.metric == kL2;
-  if (use_pq) launch(l2 ? directional_kernel<kL2, 0, 1> : directional_kernel<kIP, 0, 1>);
-  else if (a.K == 4 && a.pbytes == 1) launch(l2 ? directional_kernel<kL2, 4, 1> : directional_kernel<kIP, 4, 1>);
-  else if (a.K == 16 && a.pbytes == 1) launch(l2 ? directional_kernel<kL2, 16, 1> : directional_kernel<kIP, 16, 1>);
-  else if (a.K == 4) launch(l2 ? directional_kernel<kL2, 4, 2> : directional_kernel<kIP, 4, 2>);
-  else launch(l2 ? directional_kernel<kL2, 16, 2> : directional_kernel<kIP, 16, 2>);
   hip_check(hipGetLastError(), "launch directional_kernel");
   if (print) {
-    hip_check(hipEventRecord(e1, stream), "event record");
-    hip_check(hipEventSynchronize(e1), "event sync");
+    hip_check(hipEventRecord(ev.e1, stream), "event record");
+    hip_check(hipEventSynchronize(ev.e1), "event sync");
     float ms = 0;
-    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventElapsedTime(&ms, ev.e0, ev.e1);
     std::printf("[%s] duration=%gms, throughput=%g\n", use_pq ? "pq_search" : "directional_search", ms,
                 nq * 1000.0 / ms);
     std::fflush(stdout);
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
   }
-  if (luts) (void)hipFreeAsync(luts, stream);
-  if (rot) (void)hipFreeAsync(rot, stream);
-  (void)hipFreeAsync(qrows, stream);
+}
+
+}  // namespace
+
+size_t directional_scratch_bytes(const Graph& g, bool use_pq, int64_t nq) {
+  if (nq <= 0) return 0;
+  const size_t rows = round256((size_t)nq * g.dp * 2);
+  size_t b = rows + (g.prerotate ? rows : 0);
+  if (use_pq && g.pq) b += round256((size_t)nq * g.pq->m * 256 * 4);
+  return b;
+}
+
+void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t nq, int64_t dim, uint16_t* out,
+                                    hipStream_t stream) {
+  if (dim != (int64_t)g.dim) throw std::invalid_argument("query dim does not match the graph");
+  if (nq <= 0) return;
+  SearchScratch scratch(stream);
+  const uint16_t* rows = directional_query_rows(g, queries, nq, dim, stream, scratch);
+  hip_check(hipMemcpyAsync(out, rows, (size_t)nq * g.dp * 2, hipMemcpyDefault, stream), "download query rows");
+  hip_check(hipStreamSynchronize(stream), "sync query rows");
+}
+
+void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+                        float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
+                        uint32_t* stats, bool unique) {
+  check_directional_search(g, use_pq, nq, dim, k, bw, limit);
+  if (nq == 0 || k == 0) return;
+  SearchScratch scratch(stream);
+  directional_search_run(g, use_pq, queries, nq, dim, out_ids, out_dists, k, bw, limit, print, stream, stats,
+                         unique, scratch);
+}
+
+void directional_search_fixed(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+                              float* out_dists, int64_t k, int64_t bw, int64_t limit, bool unique, hipStream_t stream,
+                              void* scratch_base, size_t scratch_bytes) {
+  check_directional_search(g, use_pq, nq, dim, k, bw, limit);
+  if (nq == 0 || k == 0) return;
+  const size_t need = directional_scratch_bytes(g, use_pq, nq);
+  if (need > scratch_bytes)
+    throw std::invalid_argument("directional search of " + std::to_string(nq) + " queries needs " +
+                                std::to_string(need) + " bytes of scratch; at most " + std::to_string(scratch_bytes) +
+                                " are available (search fewer queries per call)");
+  if (!device_rows(queries)) throw std::invalid_argument("queries must be device memory");
+  SearchScratch scratch(stream, scratch_base, scratch_bytes);
+  directional_search_run(g, use_pq, queries, nq, dim, out_ids, out_dists, k, bw, limit, false, stream, nullptr,
+                         unique, scratch);
 }
 
 // ---------------------------------------------------------------- files --
@@ -1250,6 +1483,59 @@ void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, 
 // know flags 1, 2 and 4 only stop before it. Read back at the end of
 // the base section (total_file_size), where the saver puts it; the
 // reference loader looks elsewhere (graph.cuh:1959-1964) and never finds it.
+
+// Vertices per pass of the code layout conversion (bounds its device buffer).
+constexpr int64_t kPqLayoutChunk = 1 << 18;
+
+void pq_codes_to_file_layout(const Graph& g, uint8_t* out) {
+  const uint32_t M = g.pq->m, R = g.R;
+  const size_t dev_row = pq_row_bytes(M, R), file_row = (size_t)M * R;
+  const int64_t chunk = std::min<int64_t>(g.n, kPqLayoutChunk);
+  void* tmp = nullptr;
+  hip_check(hipMalloc(&tmp, (size_t)chunk * file_row), "alloc code layout buffer");
+  try {
+    for (int64_t u0 = 0; u0 < g.n; u0 += chunk) {
+      const int64_t cnt = std::min<int64_t>(chunk, g.n - u0);
+      const int64_t threads = cnt * R;
+      hipLaunchKernelGGL(pq_layout_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, nullptr,
+                         g.pq->codes + (size_t)u0 * dev_row, (uint8_t*)tmp, cnt, R, M, true);
+      hip_check(hipGetLastError(), "launch pq_layout_kernel");
+      hip_check(hipMemcpy(out + (size_t)u0 * file_row, tmp, (size_t)cnt * file_row, hipMemcpyDeviceToHost),
+                "download codes");
+    }
+  } catch (...) {
+    (void)hipFree(tmp);
+    throw;
+  }
+  (void)hipFree(tmp);
+}
+
+// Device codes (allocated here) of n vertices from subspace-major rows.
+static void pq_codes_from_file_layout(PqArtifacts& art, int64_t n, uint32_t R, const uint8_t* in) {
+  const uint32_t M = art.m;
+  const size_t dev_row = pq_row_bytes(M, R), file_row = (size_t)M * R;
+  hip_check(hipMalloc(&art.codes, (size_t)n * dev_row), "alloc codes");
+  hip_check(hipMemset(art.codes, 0, (size_t)n * dev_row), "clear codes");
+  const int64_t chunk = std::min<int64_t>(n, kPqLayoutChunk);
+  void* tmp = nullptr;
+  hip_check(hipMalloc(&tmp, (size_t)chunk * file_row), "alloc code layout buffer");
+  try {
+    for (int64_t u0 = 0; u0 < n; u0 += chunk) {
+      const int64_t cnt = std::min<int64_t>(chunk, n - u0);
+      hip_check(hipMemcpy(tmp, in + (size_t)u0 * file_row, (size_t)cnt * file_row, hipMemcpyHostToDevice),
+                "upload codes");
+      const int64_t threads = cnt * R;
+      hipLaunchKernelGGL(pq_layout_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, nullptr,
+                         (const uint8_t*)tmp, art.codes + (size_t)u0 * dev_row, cnt, R, M, false);
+      hip_check(hipGetLastError(), "launch pq_layout_kernel");
+    }
+    hip_check(hipDeviceSynchronize(), "code layout");
+  } catch (...) {
+    (void)hipFree(tmp);
+    throw;
+  }
+  (void)hipFree(tmp);
+}
 
 void save_directional_file(const Graph& g, const std::string& path) {
   save_graph_file(g, path);
@@ -1283,7 +1569,7 @@ void save_directional_file(const Graph& g, const std::string& path) {
     hip_check(hipMemcpy(c.data(), g.pq->centroids, c.size() * 4, hipMemcpyDeviceToHost), "download centroids");
     f.write((const char*)c.data(), (std::streamsize)c.size() * 4);
     std::vector<uint8_t> codes((size_t)g.n * M * g.R);
-    hip_check(hipMemcpy(codes.data(), g.pq->codes, codes.size(), hipMemcpyDeviceToHost), "download codes");
+    pq_codes_to_file_layout(g, codes.data());
     f.write((const char*)codes.data(), (std::streamsize)codes.size());
   }
   if (has_norms) {
@@ -1341,7 +1627,9 @@ static void read_directional_trailer(Graph& gr, const std::string& path, uint64_
     f.read((char*)&M, 4);
     f.read((char*)&K, 4);
     f.read((char*)&dsub, 4);
-    if (M != k_ranks || K != 256)
+    // the reference requires M == k_ranks; this build also reads the other
+    // subspace counts it writes (build_pq with m)
+    if (M == 0 || M > kPqMaxM || K != 256 || g->dp % M != 0 || dsub != g->dp / M)
       throw std::runtime_error("load_directional_graph_from_file: PQ trailer M/K mismatch — file was written with a "
                                "different graph_cfg");
     auto art = std::make_unique<PqArtifacts>();
@@ -1354,8 +1642,7 @@ static void read_directional_trailer(Graph& gr, const std::string& path, uint64_
     if ((size_t)f.gcount() != codes.size()) throw std::runtime_error("truncated PQ trailer in " + path);
     hip_check(hipMalloc(&art->centroids, c.size() * 4), "alloc centroids");
     hip_check(hipMemcpy(art->centroids, c.data(), c.size() * 4, hipMemcpyHostToDevice), "upload centroids");
-    hip_check(hipMalloc(&art->codes, codes.size()), "alloc codes");
-    hip_check(hipMemcpy(art->codes, codes.data(), codes.size(), hipMemcpyHostToDevice), "upload codes");
+    pq_codes_from_file_layout(*art, g->n, R, codes.data());
     g->pq = std::move(art);
   }
   if (flags & 4u) {

@@ -22,7 +22,9 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
                                              int64_t budget, bool on_host, bool prerotate, uint64_t seed,
                                              hipStream_t stream, BuildStats* stats);
 void build_lsh(Graph& g, int64_t n_samples, uint64_t seed);
-void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed);
+// m = number of subspaces (0: the config's k_ranks, as the reference, whose
+// pq_m equals k_ranks); any m dividing the padded dim, up to kPqMaxM.
+void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed, uint32_t m = 0);
 // option flags of jasperx_directional_search_ex
 constexpr uint32_t kDirUnique = 1u;
 constexpr uint32_t kDirFlagsKnown = kDirUnique;
@@ -33,10 +35,23 @@ constexpr uint32_t kDirFlagsKnown = kDirUnique;
 void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                         float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
                         uint32_t* stats = nullptr, bool unique = false);
+// Device scratch bytes a directional search of nq queries takes (query
+// rows, their rotation, PQ tables).
+size_t directional_scratch_bytes(const Graph& g, bool use_pq, int64_t nq);
+// The same search with its scratch carved from [scratch_base,
+// scratch_base + scratch_bytes): it allocates nothing and throws before
+// launching anything when the call needs more. Queries must be device
+// memory; there is no print_throughput and no work counters.
+void directional_search_fixed(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+                              float* out_dists, int64_t k, int64_t bw, int64_t limit, bool unique, hipStream_t stream,
+                              void* scratch_base, size_t scratch_bytes);
 // The query rows the directional kernels read (padded, rotated when the
 // graph was prerotated), copied to host memory [nq, padded_dim].
 void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t nq, int64_t dim, uint16_t* out,
                                     hipStream_t stream);
+// A graph's PQ codes as the reference's subspace-major rows, host
+// out[n][m][R] (the file and export layout).
+void pq_codes_to_file_layout(const Graph& g, uint8_t* out);
 void save_directional_file(const Graph& g, const std::string& path);
 std::unique_ptr<Graph> load_directional_file(const std::string& path, uint32_t dim, uint32_t R, int metric,
                                              uint32_t k_ranks, bool small_dim, bool on_host, bool prerotate,

@@ -210,35 +210,59 @@ int32_t int_exact_span(uint32_t dim) {
   return S;
 }
 
-bool int_range(const Graph& g, hipStream_t stream) {
+static bool int_exact_enabled() {
   static const bool enabled = [] {
     const char* e = std::getenv("JASPER_INT_EXACT");
     return !(e && std::atoi(e) == 0);
   }();
-  if (!enabled || g.n <= 0 || !g.vecs || g.on_host) return false;
-  if (g.int_state == 0) {
-    int32_t* d = nullptr;
-    hip_check(hipMallocAsync((void**)&d, 12, stream), "alloc range");
-    const int32_t init[3] = {0, INT32_MAX, INT32_MIN};
-    hip_check(hipMemcpyAsync(d, init, 12, hipMemcpyHostToDevice, stream), "init range");
-    const size_t count8 = (size_t)g.n * g.dp / 8;  // dp is a multiple of 8
-    const uint32_t grid = (uint32_t)std::min<size_t>((count8 + 255) / 256, 8192);
-    hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)g.vecs, count8, d);
-    hip_check(hipGetLastError(), "launch int_range_kernel");
-    int32_t h[3];
-    hip_check(hipMemcpyAsync(h, d, 12, hipMemcpyDeviceToHost, stream), "read range");
-    hip_check(hipStreamSynchronize(stream), "sync range");
-    hip_check(hipFreeAsync(d, stream), "free range");
-    const bool ok = h[0] == 0 && h[1] <= h[2];
-    g.int_lo = ok ? h[1] : 0;
-    g.int_hi = ok ? h[2] : -1;
-    g.int_state = ok ? 1 : 2;
-  }
-  return g.int_state == 1;
+  return enabled;
 }
 
+void scan_int_range(Graph& g, int64_t row0, int64_t n, hipStream_t stream) {
+  if (!int_exact_enabled() || !g.vecs || g.on_host) {
+    g.int_state = 2;
+    return;
+  }
+  if (row0 > 0 && g.int_state == 0) {  // rows before row0 were never scanned
+    n += row0;
+    row0 = 0;
+  }
+  if (row0 > 0 && g.int_state == 2) return;  // already known not to be integers
+  if (n <= 0) {
+    if (row0 == 0) g.int_state = 0;
+    return;
+  }
+  int32_t* d = nullptr;
+  hip_check(hipMallocAsync((void**)&d, 12, stream), "alloc range");
+  const int32_t init[3] = {0, INT32_MAX, INT32_MIN};
+  hip_check(hipMemcpyAsync(d, init, 12, hipMemcpyHostToDevice, stream), "init range");
+  const size_t count8 = (size_t)n * g.dp / 8;  // dp is a multiple of 8
+  const uint4* first = (const uint4*)g.vecs + (size_t)row0 * g.dp / 8;
+  const uint32_t grid = (uint32_t)std::min<size_t>((count8 + 255) / 256, 8192);
+  hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, first, count8, d);
+  hip_check(hipGetLastError(), "launch int_range_kernel");
+  int32_t h[3];
+  hip_check(hipMemcpyAsync(h, d, 12, hipMemcpyDeviceToHost, stream), "read range");
+  hip_check(hipStreamSynchronize(stream), "sync range");
+  hip_check(hipFreeAsync(d, stream), "free range");
+  const bool ok = h[0] == 0 && h[1] <= h[2];
+  if (!ok) {
+    g.int_state = 2;
+  } else if (row0 > 0) {  // state 1: merge with the range of rows [0, row0)
+    g.int_lo = std::min(g.int_lo, h[1]);
+    g.int_hi = std::max(g.int_hi, h[2]);
+  } else {
+    g.int_lo = h[1];
+    g.int_hi = h[2];
+    g.int_state = 1;
+  }
+}
+
+bool int_range(const Graph& g) { return g.int_state == 1; }
+
 bool int_exact_l2(const Graph& g, hipStream_t stream, int32_t* lo_out) {
-  if (g.metric != 0 || !int_range(g, stream)) return false;
+  (void)stream;
+  if (g.metric != 0 || !int_range(g)) return false;
   if ((int64_t)g.int_hi - (int64_t)g.int_lo > (int64_t)int_exact_span(g.dim)) return false;
   if (lo_out) *lo_out = g.int_lo;
   return true;
@@ -249,13 +273,13 @@ void upload_vectors(Graph& g, const void* src, int64_t n, uint32_t dim, hipStrea
 }
 
 void upload_rows(Graph& g, const void* src, int64_t row0, int64_t n, uint32_t dim, hipStream_t stream) {
-  g.int_state = 0;
   if (n <= 0) return;
   if (row0 < 0 || row0 + n > g.capacity) throw std::out_of_range("rows outside the graph's storage");
   const hipMemcpyKind kind = hipMemcpyDefault;
   hip_check(hipMemcpy2DAsync((char*)g.vecs + (size_t)row0 * g.dp * 2, (size_t)g.dp * 2, src, (size_t)dim * 2,
                              (size_t)dim * 2, (size_t)n, kind, stream),
             "upload vectors");
+  scan_int_range(g, row0, n, stream);
 }
 
 void download_graph(const Graph& g, HostGraph& h, bool with_vectors) {
@@ -400,6 +424,7 @@ std::unique_ptr<Graph> load_graph_file(const std::string& path, uint32_t dim, ui
     hip_check(hipMemcpy(g->counts, h.counts.data(), (size_t)n, hipMemcpyDefault), "upload counts");
     hip_check(hipMemcpy(g->deleted, h.deleted.data(), h.deleted.size() * 4, hipMemcpyDefault), "upload deleted");
     hip_check(hipMemcpy(g->slot_to_id, h.slot_to_id.data(), (size_t)n * 4, hipMemcpyDefault), "upload slot ids");
+    scan_int_range(*g, 0, n, nullptr);
   }
   return g;
 }

@@ -44,11 +44,11 @@ struct Graph {
   uint32_t packed_bytes = 0;
 
   void* vecs = nullptr;        // fp16
-  // cached value range of vecs (int_range): 0 = not scanned, 1 = all values
-  // integers in [int_lo, int_hi], 2 = some value is not an integer; reset
-  // by whatever rewrites vecs
-  mutable int int_state = 0;
-  mutable int32_t int_lo = 0, int_hi = -1;
+  // value range of vecs, written by scan_int_range wherever rows are
+  // written: 0 = no rows, 1 = all values integers in [int_lo, int_hi],
+  // 2 = some value is not an integer (or the scan is off)
+  int int_state = 0;
+  int32_t int_lo = 0, int_hi = -1;
   uint32_t* edges = nullptr;
   uint16_t* edist = nullptr;
   uint8_t* counts = nullptr;
@@ -100,11 +100,17 @@ void download_graph(const Graph& g, HostGraph& h, bool with_vectors = true);
 // 2^24 (exact fp32 partial sums).
 int32_t int_exact_span(uint32_t dim);
 
-// Scans the device rows once (synchronising `stream`) and caches whether all
-// stored values (padding included) are integers, and their range. Returns
-// false when they are not, or when the packed form is off
-// (JASPER_INT_EXACT=0, for measurement).
-bool int_range(const Graph& g, hipStream_t stream);
+// Scans device rows [row0, row0 + n) (synchronising `stream`) and records on
+// the graph whether all stored values (padding included) are integers, and
+// their range; with row0 > 0 the result is merged with what rows [0, row0)
+// gave. Every path that writes rows (upload, load, prerotation) calls it
+// there, so searches only read the result. JASPER_INT_EXACT=0 (measurement)
+// records "not integers".
+void scan_int_range(Graph& g, int64_t row0, int64_t n, hipStream_t stream);
+
+// The recorded result: true when every stored value is an integer in
+// [int_lo, int_hi].
+bool int_range(const Graph& g);
 
 // True when L2 distances between stored rows are exact integers in any
 // summation order (int_range holds and the span is within int_exact_span).

@@ -584,12 +584,9 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
     }
   }
   {
-    // the graph's value range, scanned once and cached (not while the
-    // stream is being captured: then the exact chain is used throughout)
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    (void)hipStreamIsCapturing(stream, &cap);
+    // the graph's value range, recorded when its rows were written
     a.gint = 0;
-    if (g.metric == kL2 && cap == hipStreamCaptureStatusNone && int_range(g, stream)) {
+    if (g.metric == kL2 && int_range(g)) {
       a.gint = 1;
       a.glo = g.int_lo;
       a.ghi = g.int_hi;

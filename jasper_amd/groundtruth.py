@@ -7,8 +7,9 @@ Same arithmetic as the reference utility: L2 distances as
 
 fp16 inputs with k <= 64 and dim <= 512 run on the matrix-core kernel of the
 HIP library (`jasperx_bruteforce_knn`), with the whole base resident in HBM.
-Other inputs (fp32 data, larger k or dim, or device="cpu") use the
-reference's formulation in torch, streaming vector batches.
+Other inputs (fp32 data, larger k or dim, or device="cpu") take a torch
+path that streams query and base blocks with the same arithmetic and keeps
+the k nearest of each query as (distance, id) keys.
 """
 
 from __future__ import annotations
@@ -74,45 +75,67 @@ def generate_groundtruth(vectors: torch.Tensor, queries: torch.Tensor, k: int = 
             print(f"[groundtruth] done — {nq} queries, {n} vectors, k={k}")
         return ids.cpu(), d.cpu()
 
-    use_fp16 = vectors.dtype == torch.float16 and queries.dtype == torch.float16
-    compute_dtype = torch.float16 if (use_fp16 and distance == "ip") else torch.float32
-    final_ids = torch.empty(nq, k, dtype=torch.int32)
-    final_dists = torch.empty(nq, k, dtype=torch.float32)
-    for q_start in range(0, nq, query_batch_size):
-        q_end = min(q_start + query_batch_size, nq)
-        q_batch = queries[q_start:q_end].to(device=device, dtype=compute_dtype)
-        qbs = q_batch.size(0)
-        if distance == "l2":
-            q_sq = (q_batch * q_batch).sum(dim=1, keepdim=True)
-        top_dists = torch.full((qbs, k), float("inf"), dtype=torch.float32, device=device)
-        top_ids = torch.zeros((qbs, k), dtype=torch.int64, device=device)
-        for v_start in range(0, n, vector_batch_size):
-            v_end = min(v_start + vector_batch_size, n)
-            v_batch = vectors[v_start:v_end].to(device=device, dtype=compute_dtype)
-            if distance == "l2":
-                v_sq = (v_batch * v_batch).sum(dim=1)
-                dists = q_sq + v_sq.unsqueeze(0) - 2.0 * (q_batch @ v_batch.T)
-                dists.clamp_(min=0.0)
-            elif distance == "ip":
-                dists = -(q_batch @ v_batch.T)
-            else:
-                raise ValueError(f"Unknown distance: {distance}")
-            dists = dists.float()
-            local_ids = torch.arange(v_start, v_end, device=device).unsqueeze(0).expand(qbs, -1)
-            merged_d = torch.cat([top_dists, dists], dim=1)
-            merged_i = torch.cat([top_ids, local_ids], dim=1)
-            # (distance, id) order: stable sort by id, then by distance
-            order = torch.argsort(merged_i, dim=1, stable=True)
-            merged_d = merged_d.gather(1, order)
-            merged_i = merged_i.gather(1, order)
-            order = torch.argsort(merged_d, dim=1, stable=True)[:, :k]
-            top_dists = merged_d.gather(1, order)
-            top_ids = merged_i.gather(1, order)
-            del v_batch, dists, local_ids, merged_d, merged_i, order
-        final_ids[q_start:q_end] = top_ids.to(torch.int32).cpu()
-        final_dists[q_start:q_end] = top_dists.cpu()
+    return _keyed_knn(vectors, queries, k, distance, torch.device(device), query_batch_size,
+                      vector_batch_size, verbose)
+
+
+# Keys for the (distance, id) order: the float's bits mapped to a signed int32
+# that orders like the float (negative values have their magnitude bits
+# flipped), shifted above the 32-bit id. Keys are unique, so the k smallest
+# keys are the k nearest rows in (distance, id) order whatever order topk
+# visits ties in.
+_NO_KEY = torch.iinfo(torch.int64).max
+
+
+def _to_keys(d: torch.Tensor, first_id: int) -> torch.Tensor:
+    bits = (d + 0.0).contiguous().view(torch.int32)  # + 0.0 folds -0.0 into +0.0
+    bits = torch.where(bits < 0, bits ^ 0x7FFFFFFF, bits).to(torch.int64)
+    ids = torch.arange(first_id, first_id + d.size(1), dtype=torch.int64, device=d.device)
+    return (bits << 32) | ids.unsqueeze(0)
+
+
+def _from_keys(keys: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    missing = keys == _NO_KEY
+    bits = (keys >> 32).to(torch.int32)
+    bits = torch.where(bits < 0, bits ^ 0x7FFFFFFF, bits)
+    d = bits.view(torch.float32).masked_fill(missing, torch.finfo(torch.float32).max)
+    ids = (keys & 0xFFFFFFFF).to(torch.int32).masked_fill(missing, -1)
+    return ids, d
+
+
+def _block_distances(q: torch.Tensor, q_sq, v: torch.Tensor, distance: str) -> torch.Tensor:
+    """Distances of a query block to a base block with the ground-truth
+    arithmetic: L2 = (|q|^2 + |v|^2) - 2 q.v in float32 clamped at 0;
+    IP = -(q.v) in the operands' precision (an fp16 product for fp16
+    inputs), then widened to float32."""
+    if distance == "l2":
+        v_sq = (v * v).sum(dim=1)
+        return (q_sq + v_sq[None, :] - 2.0 * (q @ v.T)).clamp_(min=0.0)
+    return (-(q @ v.T)).float()
+
+
+def _keyed_knn(vectors, queries, k, distance, dev, q_step, v_step, verbose):
+    if distance not in ("l2", "ip"):
+        raise ValueError(f"Unknown distance: {distance}")
+    # fp16 inner products stay fp16, everything else is computed in float32
+    fp16_ip = distance == "ip" and vectors.dtype == queries.dtype == torch.float16
+    dtype = torch.float16 if fp16_ip else torch.float32
+    n, nq = vectors.size(0), queries.size(0)
+    out_ids = torch.empty((nq, k), dtype=torch.int32)
+    out_d = torch.empty((nq, k), dtype=torch.float32)
+    for q0 in range(0, nq, q_step):
+        q = queries[q0:q0 + q_step].to(device=dev, dtype=dtype)
+        q_sq = (q * q).sum(dim=1, keepdim=True) if distance == "l2" else None
+        best = torch.full((q.size(0), k), _NO_KEY, dtype=torch.int64, device=dev)
+        for v0 in range(0, n, v_step):
+            v = vectors[v0:v0 + v_step].to(device=dev, dtype=dtype)
+            keys = torch.cat([best, _to_keys(_block_distances(q, q_sq, v, distance), v0)], dim=1)
+            best = torch.topk(keys, k, dim=1, largest=False, sorted=True).values
+        ids, d = _from_keys(best)
+        out_ids[q0:q0 + q.size(0)] = ids.cpu()
+        out_d[q0:q0 + q.size(0)] = d.cpu()
         if verbose:
-            print(f"\r[groundtruth] {q_end}/{nq} queries", end="", flush=True)
+            print(f"\r[groundtruth] {q0 + q.size(0)}/{nq} queries", end="", flush=True)
     if verbose:
         print()
-    return final_ids, final_dists
+    return out_ids, out_d

@@ -70,6 +70,8 @@ def lib():
         _lib.jo_max_batch_size.argtypes = [i64, i32, i64]
         _lib.jo_build.restype = i32
         _lib.jo_build.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, P, P, P, i32, P]
+        _lib.jo_last_capped_groups.restype = i64
+        _lib.jo_last_capped_groups.argtypes = []
         _lib.jo_append.restype = i32
         _lib.jo_append.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, i64, ctypes.c_uint32, P, P, P, P, i32, P]
         _lib.jo_consolidate.restype = i64
@@ -225,6 +227,8 @@ def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
     g = OracleGraph(vecs16, edges, edist, counts, R, dim, distance)
     g.n_batches = nb.value
     g.max_batch = max_batch
+    # reverse-step groups cut at the 256 + R candidate cap (test counter)
+    g.capped_groups = int(lib().jo_last_capped_groups())
     return g
 
 

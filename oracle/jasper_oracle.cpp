@@ -17,6 +17,7 @@
 // is off so that the only fused multiply-adds are the explicit fmaf() calls.
 
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 #include <cmath>
 #include <cstdint>
@@ -363,6 +364,11 @@ namespace {
 // sorted by (distance, id), then RobustPrune. Also the repair step of
 // consolidate (graph_ops.cuh:151-258), whose pairs are (live vertex, repair
 // candidate).
+// Target groups whose candidate list reached the 256 + R cap with sources
+// left over, since the last jo_build (read by jo_last_capped_groups; a
+// test counter, so tests can show the cap was exercised).
+std::atomic<int64_t> g_capped_groups{0};
+
 void reverse_step(const Graph& g, int dim_for_prune, float alpha, const std::vector<uint64_t>& pairs,
                   uint32_t* edges, uint16_t* edge_dist, uint8_t* counts) {
   const int R = g.R, max_cands = 256 + R;
@@ -386,7 +392,10 @@ void reverse_step(const Graph& g, int dim_for_prune, float alpha, const std::vec
       }
       const uint16_t* wv = g.vecs + (size_t)w * g.dp;
       for (size_t p = heads[(size_t)h]; p < heads[(size_t)h + 1]; ++p) {
-        if ((int)C.size() >= max_cands) break;
+        if ((int)C.size() >= max_cands) {
+          g_capped_groups.fetch_add(1, std::memory_order_relaxed);
+          break;
+        }
         const uint32_t v = (uint32_t)(pairs[p] & 0xFFFFFFFFu);
         if (v == kInvalid32 || v == w) continue;
         C.push_back({v, dist(g.metric, wv, g.vecs + (size_t)v * g.dp, dim_for_prune)});
@@ -477,6 +486,7 @@ int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, 
   if (n <= 0) return 0;
   if (max_batch < 1) return -1;
   if (nthreads > 0) omp_set_num_threads(nthreads);
+  g_capped_groups.store(0);
   std::fill(counts, counts + n, (uint8_t)0);
   std::fill(edges, edges + (size_t)n * R, kInvalid32);
   std::fill(edge_dist, edge_dist + (size_t)n * R, (uint16_t)0);
@@ -485,6 +495,8 @@ int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, 
   if (n_batches_out) *n_batches_out = nb;
   return 0;
 }
+
+int64_t jo_last_capped_groups() { return g_capped_groups.load(); }
 
 // append_batch (construct.cuh:1169-1265): the rows [first, n) were appended
 // to a graph of `first` vertices (their counts must be 0); wires them in with

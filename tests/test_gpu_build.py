@@ -4,7 +4,10 @@ On inputs where the reverse-candidate cap cannot bind (batch <= 256, so no
 target receives more than 256 + R candidates in one batch) the reference
 build is deterministic up to its arithmetic, and the oracle restates that
 arithmetic. The GPU graph must then equal the oracle graph: same edge counts,
-same neighbour ids in the same slots, same bf16 edge distances.
+same neighbour ids in the same slots, same bf16 edge distances. Where the cap
+binds, the reference keeps an arrival-order subset; the oracle and the GPU
+both keep the target's existing edges, then its sources in ascending id,
+and the graphs must still be equal (test_build_matches_oracle_reverse_cap).
 """
 
 import numpy as np
@@ -12,7 +15,7 @@ import pytest
 import torch
 
 import oracle
-from tests.helpers import gaussian, integer_clustered, unit
+from tests.helpers import gaussian, hub_mix, integer_clustered, unit
 
 pytestmark = pytest.mark.gpu
 
@@ -92,18 +95,38 @@ def test_build_tiny_inputs(jasper, oracle_lib):
         _compare(gg, og)
 
 
-def test_build_then_search_recall_c1(jasper, oracle_lib):
-    """Config 1 end to end: GPU build + GPU search recall equals the oracle's."""
+@pytest.mark.parametrize("integer", [False, True])
+def test_build_matches_oracle_reverse_cap(jasper, oracle_lib, integer):
+    """Batches of 400 (n = 20000): row 0 is a hub that nearly every row of a
+    batch links to, so its reverse candidates are cut at 256 + R (the cap of
+    construct.cuh:642-658) in dozens of batches. Non-integer rows take the
+    Gram prune with proof; integer rows (span 220) the exact integer paths."""
+    base = hub_mix(20000, 64, 5, scale=32.0 if integer else 8.0, integer=integer)
+    og = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    print(f"max batch {og.max_batch}, reverse groups cut at 256 + R: {og.capped_groups}")
+    assert og.max_batch == 400 and og.capped_groups >= 20
+    gg = _gpu_build(jasper, base, 32, "l2")
+    _compare(gg, og)
+
+
+def test_build_then_search_c1(jasper, oracle_lib):
+    """Config 1 end to end: the GPU graph equals the oracle's bit for bit
+    (batches of at most 200, so no cap binds) and the GPU search on it
+    returns the oracle's ids and distances."""
     from jasper_amd import datasets
     base, q, p = datasets.config("c1")
     gg = _gpu_build(jasper, base, 32, "l2")
     og = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    assert og.max_batch == 200 and og.capped_groups == 0
+    _compare(gg, og)
     gt, _ = oracle.bruteforce_exact(base, q, k=10)
-    ids, _ = gg.search(torch.from_numpy(q).cuda(), k=10, beam_width=64)
+    ids, d = gg.search(torch.from_numpy(q).cuda(), k=10, beam_width=64)
+    rid, rd = oracle.beam_search(og, q, k=10, beam_width=64)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.array_equal(d.cpu().numpy().view(np.uint32), rd.view(np.uint32))
     r_gpu = oracle.recall(gt, ids.cpu().numpy(), 10)
-    rid, _ = oracle.beam_search(og, q, k=10, beam_width=64)
-    r_ref = oracle.recall(gt, rid, 10)
-    assert abs(r_gpu - r_ref) <= 0.005, (r_gpu, r_ref)
+    print(f"config 1 recall@10 at bw 64: {r_gpu:.3f}")   # 0.813: N(0,1) rows at d = 128
+    assert r_gpu > 0.75
 
 
 def test_build_host_resident_matches_oracle(jasper, oracle_lib):

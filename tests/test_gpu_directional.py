@@ -58,12 +58,13 @@ def _check_unique(gg, g, fn, q, q_rows, bw, **art):
 
 
 def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, bws=(16, 64),
-          lsh_samples=4000, pq_train=3000, pq_iters=4):
+          lsh_samples=4000, pq_train=3000, pq_iters=4, pq_m=None):
     n, dim = x.shape
+    M = pq_m or k_ranks
     xt = torch.from_numpy(x.astype(np.float16)).cuda()
     gg = jasper.Graph.build(xt, n_neighbors=R, distance=distance, build_lsh=lsh, build_pq=pq, k_ranks=k_ranks,
                             prerotate=prerotate, lsh_samples=lsh_samples, lsh_seed=7, pq_train=pq_train,
-                            pq_kmeans_iter=pq_iters, pq_seed=11)
+                            pq_kmeans_iter=pq_iters, pq_seed=11, pq_m=pq_m)
     path = tmp_path / "dir.bin"
     gg.save(str(path))
     g = oracle.load_graph(path, dim, R, distance)
@@ -106,13 +107,14 @@ def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, b
             _check_unique(gg, g, "directional_search", q, q_rows, bw, lsh=art)
     if pq:
         cent, codes, norms = gg.export_pq()
-        rcent, _ = oracle.pq_train(g, k_ranks, n_train=pq_train, iters=pq_iters, seed=11)
+        rcent, _ = oracle.pq_train(g, M, n_train=pq_train, iters=pq_iters, seed=11)
         assert np.array_equal(cent.view(np.uint32), rcent.view(np.uint32)), "PQ centroids differ"
-        rcodes = oracle.pq_encode(g, k_ranks, rcent)
+        rcodes = oracle.pq_encode(g, M, rcent)
+        assert codes.shape == rcodes.shape == (n, M * R)
         assert np.array_equal(codes, rcodes), "PQ codes differ"
         rnorms = oracle.vector_norms(g.vecs16)
         assert np.array_equal(norms.view(np.uint32), rnorms.view(np.uint32)), "vector norms differ"
-        art = oracle.PqArtifacts(k_ranks, g.dp // k_ranks, cent, codes, norms)
+        art = oracle.PqArtifacts(M, g.dp // M, cent, codes, norms)
         for bw in bws:
             ids, d = _search(gg, "pq_search", q, 10, bw)
             rid, rd = oracle.directional_search(g, q_rows, pq=art, k=10, beam_width=bw)
@@ -124,6 +126,8 @@ def _case(jasper, tmp_path, x, q, *, R, distance, k_ranks, prerotate, lsh, pq, b
     # save -> load round trip keeps the artifacts and the results
     g2 = jasper.Graph.load(str(path), dim=dim, n_neighbors=R, distance=distance, k_ranks=k_ranks,
                            prerotate=prerotate)
+    if pq:
+        assert np.array_equal(g2.export_pq()[1], codes), "PQ codes changed in the file round trip"
     for (kind, bw), (ids, d) in out.items():
         ids2, d2 = _search(g2, "directional_search" if kind == "lsh" else "pq_search", q, 10, bw)
         msg = compare_search(ids2, d2, ids, d)
@@ -153,6 +157,47 @@ def test_lsh_pq_long_rows(jasper, oracle_lib, tmp_path):
     q = datasets.sparse_abs(24, 960, 27)
     _case(jasper, tmp_path, x, q, R=32, distance="l2", k_ranks=16, prerotate=True, lsh=True, pq=True,
           bws=(16, 64), pq_train=1500, pq_iters=3)
+
+
+def test_config3_shape(jasper, oracle_lib, tmp_path):
+    """Config 3's parameters at reduced n: unit-sphere d = 96, inner
+    product, R = 64, LSH k_ranks = 4 with u8 words, prerotated, 32768
+    calibration samples, beam widths 32..128."""
+    x = unit(3000, 96, 40)
+    q = unit(40, 96, 41)
+    _case(jasper, tmp_path, x, q, R=64, distance="ip", k_ranks=4, prerotate=True, lsh=True, pq=False,
+          bws=(32, 64, 128), lsh_samples=32768)
+
+
+@pytest.mark.parametrize("pq_m", [16, 120])
+def test_config4_shape(jasper, oracle_lib, tmp_path, pq_m):
+    """Config 4's parameters at reduced n: sparse non-negative d = 960, L2,
+    R = 64, prerotated, PQ with 8-bit codebooks; M = 16 (the largest the
+    reference's configs offer, dsub = 60) and M = 120 (one subspace per
+    8 dims as the config asks, a 120 KB table per query)."""
+    from jasper_amd import datasets
+    x = datasets.sparse_abs(1500, 960, 42)
+    q = datasets.sparse_abs(24, 960, 43)
+    _case(jasper, tmp_path, x, q, R=64, distance="l2", k_ranks=16, prerotate=True, lsh=False, pq=True,
+          bws=(32, 64), pq_train=2000, pq_iters=3, pq_m=pq_m)
+
+
+@pytest.mark.parametrize("pq_m", [8, 12, 24, 32])
+def test_pq_subspace_counts(jasper, oracle_lib, tmp_path, pq_m):
+    """PQ at subspace counts between the reference's 4 and 16 and beyond:
+    8-code groups (m = 8), a partly filled 16-code group (12), two and
+    three groups (24, 32), and dsub = 12, 8, 4, 3 for the table kernels."""
+    x = gaussian(1500, 96, 44)
+    q = gaussian(32, 96, 45)
+    _case(jasper, tmp_path, x, q, R=32, distance="l2", k_ranks=4, prerotate=False, lsh=False, pq=True,
+          bws=(16, 64), pq_m=pq_m)
+
+
+def test_pq_ip_wide(jasper, oracle_lib, tmp_path):
+    x = unit(1500, 64, 46)
+    q = unit(32, 64, 47)
+    _case(jasper, tmp_path, x, q, R=32, distance="ip", k_ranks=4, prerotate=True, lsh=False, pq=True,
+          bws=(32,), pq_m=32)
 
 
 def test_lsh_ip(jasper, oracle_lib, tmp_path):

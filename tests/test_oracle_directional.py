@@ -316,6 +316,86 @@ def test_pq_estimate_exact_on_grid(distance):
     assert np.array_equal(ids, want_ids)
 
 
+def _grid_dsub8(distance, dim, swap=False):
+    """The grid with its coordinates at dims 0, 9 and 18 (subspaces 0, 1
+    and 2 at dsub = 8) and the queries' extra value at dim 27, and a PQ of
+    M = dim / 8 whose codebooks hold the zero vector and +-1 steps along
+    each of the subspace's 8 axes. swap=True exchanges the +1 and -1 steps of
+    axis 0 (a wrong codebook, for the sensitivity check)."""
+    x0, g0 = grid_graph(distance=distance)
+    at = [0, 9, 18, 27]
+    x = np.zeros((len(x0), dim), dtype=np.float32)
+    x[:, at] = x0[:, :4]
+    g = oracle.OracleGraph(oracle.as_padded_f16(x), g0.edges, g0.edge_dist, g0.counts, g0.R, dim, distance,
+                           medoid=0)
+    M, dsub = dim // 8, 8
+    cent = np.full((M, 256, dsub), 1000.0, dtype=np.float32) + np.arange(256, dtype=np.float32)[None, :, None]
+    cent[:, 0] = 0.0
+    for t in range(dsub):
+        cent[:, 1 + 2 * t] = 0.0
+        cent[:, 1 + 2 * t, t] = 1.0
+        cent[:, 2 + 2 * t] = 0.0
+        cent[:, 2 + 2 * t, t] = -1.0
+    codes = oracle.pq_encode(g, M, cent.ravel())
+    if swap:
+        cent[:, [1, 2]] = cent[:, [2, 1]]
+    pq = oracle.PqArtifacts(M, dsub, cent.ravel(), codes, oracle.vector_norms(g.vecs16))
+    q0 = grid_queries()
+    q = np.zeros((len(q0), dim), dtype=np.float32)
+    q[:, at] = q0[:, :4]
+    return x, g, pq, q, codes
+
+
+@pytest.mark.parametrize("distance", ["l2", "ip"])
+@pytest.mark.parametrize("dim", [32, 960])
+def test_pq_estimate_exact_on_grid_dsub8(distance, dim):
+    """One subspace per 8 dims (M = 4 and 120): every edge residual's PQ
+    reconstruction is exact, so a wide search returns the exact top-k."""
+    x, g, pq, q, codes = _grid_dsub8(distance, dim)
+    M, dsub = pq.M, pq.dsub
+    for u, e, dd in _edge_diffs(g):
+        for j in range(M):
+            sub = dd[j * dsub:(j + 1) * dsub]
+            nz = np.nonzero(sub)[0]
+            want = 0 if len(nz) == 0 else (1 if sub[nz[0]] > 0 else 2) + 2 * int(nz[0])
+            assert codes[u, j * g.R + e] == want
+    ids, d = oracle.directional_search(g, q, pq=pq, k=8, beam_width=g.n, limit=2 * g.n)
+    want_ids, want_d = exact_topk(x, q, 8, distance)
+    assert np.array_equal(d.astype(np.float64), want_d)
+    assert np.array_equal(ids, want_ids)
+
+
+@pytest.mark.parametrize("distance", ["l2", "ip"])
+def test_exact_estimators_visit_in_the_same_order(distance):
+    """At a narrow beam the pop order is the order of the estimates. On the
+    grid the LSH estimate (c = (1, 0)), the one-coordinate PQ and the
+    8-dim-subspace PQ (d = 32 and 960) all equal the exact distance, so
+    their visit sequences (ids and exact distances) must be identical; a
+    codebook with the +-1 steps of one axis swapped must change it."""
+    x, g = grid_graph(distance=distance)
+    q = grid_queries()
+    lsh = oracle.build_lsh(g, K=2, pbytes=1, n_samples=4000, seed=3)
+    M = g.dp
+    cent = np.full((M, 256, 1), 1000.0, dtype=np.float32) + np.arange(256, dtype=np.float32)[None, :, None]
+    cent[:, 0, 0], cent[:, 1, 0], cent[:, 2, 0] = 0.0, 1.0, -1.0
+    pq1 = oracle.PqArtifacts(M, 1, cent.ravel(), oracle.pq_encode(g, M, cent.ravel()),
+                             oracle.vector_norms(g.vecs16))
+    runs = [oracle.directional_search(g, q, lsh=lsh, k=8, beam_width=4, limit=40, get_visited=True),
+            oracle.directional_search(g, q, pq=pq1, k=8, beam_width=4, limit=40, get_visited=True)]
+    for dim in (32, 960):
+        _, g8, pq8, q8, _ = _grid_dsub8(distance, dim)
+        runs.append(oracle.directional_search(g8, q8, pq=pq8, k=8, beam_width=4, limit=40, get_visited=True))
+    _, _, vi0, vd0, vc0 = runs[0]
+    assert vc0.min() >= 5 and vc0.sum() > 60
+    for _, _, vi, vd, vc in runs[1:]:
+        assert np.array_equal(vc, vc0)
+        assert np.array_equal(vi, vi0)
+        assert np.array_equal(vd.view(np.uint32), vd0.view(np.uint32))
+    _, gs, pqs, qs, _ = _grid_dsub8(distance, 32, swap=True)
+    _, _, vis, _, vcs = oracle.directional_search(gs, qs, pq=pqs, k=8, beam_width=4, limit=40, get_visited=True)
+    assert not (np.array_equal(vcs, vc0) and np.array_equal(vis, vi0))
+
+
 def test_output_is_stable_topk_of_visits():
     _, g = _small_graph(n=800, dim=32, R=16)
     lsh = oracle.build_lsh(g, K=4, pbytes=1, n_samples=2000, seed=1)

@@ -78,3 +78,29 @@ def test_groundtruth_cpu_matches_oracle():
     rid, rd = oracle.bruteforce_ref(x.astype("float32"), q.astype("float32"), k=10)
     # integer-valued data: distances are exact, ids agree up to ties
     assert (d.numpy() == rd).all()
+
+
+def test_groundtruth_cpu_orders_by_distance_then_id():
+    """The CPU path returns (distance, id) order: duplicated rows tie and
+    must come out by id; IP distances are negative and zero rows give -0.0;
+    k above n pads with (-1, FLT_MAX)."""
+    import numpy as np
+    rng = np.random.default_rng(5)
+    base = rng.integers(-3, 4, size=(40, 8)).astype(np.float32)
+    base[20:30] = base[0:10]          # exact ties
+    base[35] = 0.0                    # IP distance -0.0 / 0.0
+    q = rng.integers(-3, 4, size=(6, 8)).astype(np.float32)
+    for dist in ("l2", "ip"):
+        ids, d = jasper_amd.generate_groundtruth(torch.from_numpy(base), torch.from_numpy(q), k=12,
+                                                 distance=dist, device="cpu", vector_batch_size=7)
+        if dist == "l2":
+            full = ((q[:, None, :] - base[None, :, :]) ** 2).sum(-1)
+        else:
+            full = -(q @ base.T)
+        for i in range(len(q)):
+            order = np.lexsort((np.arange(len(base)), full[i] + 0.0))[:12]
+            assert ids[i].tolist() == order.tolist()
+            assert np.array_equal(d[i].numpy(), full[i][order].astype(np.float32))
+    ids, d = jasper_amd.generate_groundtruth(torch.from_numpy(base[:5]), torch.from_numpy(q), k=8, device="cpu")
+    assert (ids[:, 5:] == -1).all() and (d[:, 5:] == np.finfo(np.float32).max).all()
+    assert sorted(ids[0, :5].tolist()) == list(range(5))
