@@ -207,6 +207,24 @@ int64_t jasperx_build_pq_m(int64_t handle, int64_t m, int64_t n_train, int64_t k
 int64_t jasperx_directional_search_ex(int64_t handle, int32_t use_pq, const void* queries, int64_t n_queries,
                                       int64_t dim, int32_t* out_ids, float* out_dists, int64_t k,
                                       int64_t beam_width, int64_t limit, uint32_t flags, void* stream);
+/* No reference counterpart; for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The same search as jasperx_directional_search_ex (same
+ * arguments, flags and results) with its scratch -- the padded query rows,
+ * their rotation for prerotated graphs and pq_search's per-query tables --
+ * in a static 64 MiB device buffer per GPU instead of stream-ordered
+ * allocations; nothing is allocated or freed. A call takes 2 * padded_dim
+ * bytes per query for the rows (twice that on a prerotated graph) plus
+ * m * 1 KB per query for pq_search, each part rounded up to 256 bytes; one
+ * that needs more than 64 MiB is rejected before anything runs (split such
+ * batches: e.g. at most ~4,000 queries for pq_search with m = 16 at d = 128,
+ * ~540 with m = 120 at d = 960). Queries must be device memory.
+ * Every call on a GPU shares that GPU's buffer, so calls that overlap on one
+ * GPU (other streams, other threads) race. */
+int64_t jasperx_directional_search_noalloc(int64_t handle, int32_t use_pq, const void* queries,
+                                           int64_t n_queries, int64_t dim, int32_t* out_ids, float* out_dists,
+                                           int64_t k, int64_t beam_width, int64_t limit, uint32_t flags,
+                                           void* stream);
 /* Measurement run of directional_search (use_pq = 0) or pq_search
  * (use_pq = 1), flags as above: the same traversal, writing per-query work
  * counters to host memory out_stats[n_queries * 3] = {visits, hops

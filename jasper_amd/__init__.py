@@ -96,6 +96,8 @@ _AGNOSTIC = {
     "jasperx_directional_stats": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_uint32,
                                   _ptr, _ptr],
     "jasperx_build_pq_m": [_i64, _i64, _i64, _i64, _i64],
+    "jasperx_directional_search_noalloc": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64,
+                                           _i64, ctypes.c_uint32, _ptr],
     "jasperx_directional_search_ex": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
                                       ctypes.c_uint32, _ptr],
     "jasperx_bruteforce_knn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, ctypes.c_int32, _ptr, _ptr, _ptr],

@@ -574,6 +574,17 @@ extern "C" int64_t jasperx_directional_search_ex(int64_t h, int32_t use_pq, cons
   });
 }
 
+extern "C" int64_t jasperx_directional_search_noalloc(int64_t h, int32_t use_pq, const void* q, int64_t nq,
+                                                      int64_t dim, int32_t* out_ids, float* out_dists, int64_t k,
+                                                      int64_t bw, int64_t limit, uint32_t flags, void* stream) {
+  return guarded([&]() -> int64_t {
+    if (flags & ~kDirFlagsKnown) throw std::invalid_argument("unknown directional search flags");
+    directional_search_noalloc(lookup(h, nullptr), use_pq != 0, q, nq, dim, out_ids, out_dists, k, bw, limit,
+                               (flags & kDirUnique) != 0, (hipStream_t)stream);
+    return 0;
+  });
+}
+
 extern "C" int64_t jasperx_directional_stats(int64_t h, int32_t use_pq, const void* q, int64_t nq, int64_t dim,
                                              int64_t k, int64_t bw, int64_t limit, uint32_t flags,
                                              uint32_t* out_stats, void* stream) {

@@ -26,6 +26,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <mutex>
 #include <stdexcept>
 #include <vector>
 
@@ -1472,6 +1473,45 @@ void directional_search_fixed(Graph& g, bool use_pq, const void* queries, int64_
   SearchScratch scratch(stream, scratch_base, scratch_bytes);
   directional_search_run(g, use_pq, queries, nq, dim, out_ids, out_dists, k, bw, limit, false, stream, nullptr,
                          unique, scratch);
+}
+
+// ------------------------------------------------- allocation-free search --
+// Scratch of directional_search_noalloc: a file-scope device array, so each
+// GPU the library runs on holds one copy from module load until the process
+// ends. Host code never passes the array's name to a kernel or copy (on the
+// host it is only a stand-in for the symbol): the device address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+void* scratch_address() {
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "current device");
+  if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("device index out of range for the static scratch");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "address of the static search scratch");
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+size_t directional_noalloc_scratch_bytes() { return kNoAllocScratchBytes; }
+
+void directional_search_noalloc(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim,
+                                int32_t* out_ids, float* out_dists, int64_t k, int64_t bw, int64_t limit,
+                                bool unique, hipStream_t stream) {
+  // every byte a call reads from the scratch it has written first (the
+  // padded query rows, their rotation, the PQ tables), so nothing is cleared
+  directional_search_fixed(g, use_pq, queries, nq, dim, out_ids, out_dists, k, bw, limit, unique, stream,
+                           scratch_address(), kNoAllocScratchBytes);
 }
 
 // ---------------------------------------------------------------- files --

@@ -45,6 +45,13 @@ size_t directional_scratch_bytes(const Graph& g, bool use_pq, int64_t nq);
 void directional_search_fixed(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                               float* out_dists, int64_t k, int64_t bw, int64_t limit, bool unique, hipStream_t stream,
                               void* scratch_base, size_t scratch_bytes);
+// directional_search_fixed on a static device scratch of
+// directional_noalloc_scratch_bytes() per GPU (no allocation at all). Calls
+// that overlap on one GPU share that scratch and race.
+size_t directional_noalloc_scratch_bytes();
+void directional_search_noalloc(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim,
+                                int32_t* out_ids, float* out_dists, int64_t k, int64_t bw, int64_t limit,
+                                bool unique, hipStream_t stream);
 // The query rows the directional kernels read (padded, rotated when the
 // graph was prerotated), copied to host memory [nq, padded_dim].
 void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t nq, int64_t dim, uint16_t* out,
