@@ -127,6 +127,7 @@ def main() -> int:
                          "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search), updates "
                          "(config 2: mark_deleted 10%, consolidate, append 100k)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
+    ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -369,6 +370,7 @@ def run_directional(args, torch, jasper_amd, datasets, dev, log, use_pq=False):
     ids, _ = fn(q_t, k=10, beam_width=chosen)
     rec = _recall(gt, ids.cpu().numpy())
     st = g.directional_stats(q_t, k=10, beam_width=chosen, pq=use_pq).astype(np.int64)
+    plain = _plain_curve(torch, jasper_amd, base_t, q_t, gt, "ip", (32, 64, 128), log, "c3")
     dp, R = 96, 64
     visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
     # per edge: PQ reads M = 4 code bytes (IP: no norm gather); LSH K*P + 2 = 6 (u8 words + bf16 m^2)
@@ -381,7 +383,7 @@ def run_directional(args, torch, jasper_amd, datasets, dev, log, use_pq=False):
                 {"workload": f"config 3: {n} x {dim} unit-norm N(0,1) fp16, IP, R=64 alpha=1.2, "
                              f"{'PQ M=4' if use_pq else 'LSH k_ranks=4 u8 words'}, prerotate, {nq} queries, k=10",
                  "beam_width": chosen, "recall_at_10": rec, "build_s": build_s,
-                 "build_vectors_per_s": n / build_s, "curve": curve},
+                 "build_vectors_per_s": n / build_s, "curve": curve, "curve_plain_graph": plain},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
                  "traffic": None, "kernel": f"directional_kernel<IP,{'PQ' if use_pq else 'LSH'}>",
                  "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
@@ -571,55 +573,94 @@ def _c5_plain(args, torch, jasper_amd, base, queries, gt, log):
             "achieved_gbs": ach, "frac": ach / PEAK_HBM_GBS, "curve": curve}
 
 
+def _plain_curve(torch, jasper_amd, base, queries, gt, distance, bws, log, tag):
+    """Recall of the plain beam search on a plain Vamana graph of the same
+    rows (no estimator), to separate what the graph allows from what the
+    directional estimator finds."""
+    t0 = time.perf_counter()
+    pg = jasper_amd.Graph.build(base, n_neighbors=64, distance=distance, alpha=1.2)
+    torch.cuda.synchronize()
+    log(f"{tag} plain graph built in {time.perf_counter() - t0:.1f}s")
+    nq = queries.size(0)
+    curve = []
+    for bw in bws:
+        ids, _ = pg.search(queries, k=10, beam_width=bw)
+        r = _recall(gt, ids.cpu().numpy())
+        wall, _, _ = _timed(torch, lambda bw=bw: pg.search(queries, k=10, beam_width=bw), 3, 1)
+        curve.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
+        log(f"{tag} plain search bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+    pg.free()
+    return curve
+
+
 def run_c4(args, torch, jasper_amd, datasets, dev, log):
     """Config 4: 1M x 960 non-negative sparse vectors (|N(0,1)| * 0.05, 192
     dims zeroed per row) generated in HBM, L2, R=64, alpha=1.2, PQ with
-    M=16 subspaces of 60 dims (8-bit codebooks), prerotated (the Python
-    default with build_pq); 1,000 queries, k=10, pq_search at bw=64."""
+    8-bit codebooks and one subspace per 8 dims (M = 120, --c4-m), prerotated
+    (the Python default with build_pq); 1,000 queries, k=10, pq_search at
+    bw=64. Also: the same graph's PQ retrained at M = 16 (the largest the
+    reference's configs offer), and the plain search on a plain graph of the
+    same rows."""
     n, nq, dim = args.n, min(args.nq, 1000), 960
+    M = args.c4_m
     base = datasets.sparse_abs_device(n, dim, 0, dev)
     queries = datasets.sparse_abs_device(nq, dim, 1, dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2, build_pq=True, k_ranks=16,
-                               prerotate=True)
+                               prerotate=True, pq_m=M)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
     bst = jasper_amd.last_build_stats()
-    log(f"c4 build (prerotation + Vamana + PQ) {build_s:.1f}s = {n / build_s:,.0f} vec/s")
+    log(f"c4 build (prerotation + Vamana + PQ M={M}) {build_s:.1f}s = {n / build_s:,.0f} vec/s")
     t0 = time.perf_counter()
     gt_ids, _ = jasper_amd.generate_groundtruth(base, queries, k=10, distance="l2")
     gt = gt_ids.numpy()
     log(f"c4 ground truth {time.perf_counter() - t0:.1f}s")
-    curve, chosen = [], None
-    for unique in (False, True):
-        for bw in (32, 64, 128, 256):
-            run = lambda bw=bw, unique=unique: g.pq_search(queries, k=10, beam_width=bw, unique=unique)
-            ids, _ = run()
-            r = _recall(gt, ids.cpu().numpy())
-            wall, ev, _ = _timed(torch, run, 3, 1)
-            curve.append({"unique": unique, "beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
-            log(f"c4 unique={unique} bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+
+    def sweep(tag, bws):
+        out = []
+        for unique in (False, True):
+            for bw in bws:
+                run = lambda bw=bw, unique=unique: g.pq_search(queries, k=10, beam_width=bw, unique=unique)
+                ids, _ = run()
+                r = _recall(gt, ids.cpu().numpy())
+                wall, ev, _ = _timed(torch, run, 3, 1)
+                out.append({"unique": unique, "beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
+                log(f"c4 {tag} unique={unique} bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+        return out
+
+    curve = sweep(f"M={M}", (32, 64, 128, 256))
     # the configured point: beam width 64, reference traversal
-    bw, unique = 64, False
+    bw = 64
     wall, ev, _ = _timed(torch, lambda: g.pq_search(queries, k=10, beam_width=bw), args.steps, args.warmup)
     ids, _ = g.pq_search(queries, k=10, beam_width=bw)
     rec = _recall(gt, ids.cpu().numpy())
     st = g.directional_stats(queries, k=10, beam_width=bw, pq=True).astype(np.int64)
     visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
-    M = 16
     # per hop: count byte, vector 2*dp; per edge: id 4, M code bytes, L2 norm 4
     alg = int(visits * 2 * dim + hops + adj * (4 + M + 4) + nq * (2 * dim + 80))
     ach = alg / (ev / 1000.0) / 1e9
+    log(f"c4 M={M} bw={bw}: {wall:.3f} ms/step (events {ev:.3f} ms), {nq / (wall / 1000.0):,.0f} QPS, "
+        f"recall {rec:.4f}, {alg / nq / 1e3:.1f} KB/query, {ach:.0f} GB/s")
+    m16 = None
+    if M != 16:
+        t0 = time.perf_counter()
+        jasper_amd._agnostic("jasperx_build_pq_m")(g.handle, 16, 40000, 12, 123)
+        torch.cuda.synchronize()
+        log(f"c4 PQ retrained at M=16 in {time.perf_counter() - t0:.1f}s")
+        m16 = sweep("M=16", (64, 256))
+    plain = _plain_curve(torch, jasper_amd, base, queries, gt, "l2", (32, 64, 128), log, "c4")
     res = _line(args, "config 4: QPS @ bw=64 and build vectors/s, PQ-ADC directional search (1M x 960, L2)",
                 nq / (wall / 1000.0), "queries/s", wall, "f16",
                 {"workload": f"config 4: {n} x {dim} |N(0,1)|*0.05 with 192 zero dims (generated in HBM), L2, "
-                             f"R=64 alpha=1.2, PQ M=16 dsub=60, prerotate, {nq} queries, k=10, bw=64",
+                             f"R=64 alpha=1.2, PQ M={M} dsub={dim // M}, prerotate, {nq} queries, k=10, bw=64",
                  "build_vectors_per_s": n / build_s, "build_s": build_s, "build_max_batch": int(bst["max_batch"]),
-                 "beam_width": bw, "recall_at_10": rec, "curve": curve},
+                 "beam_width": bw, "recall_at_10": rec, "curve": curve, "curve_pq_m16": m16,
+                 "curve_plain_graph": plain},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
-                 "traffic": None, "kernel": "directional_kernel<L2,PQ>", "kernel_ms": ev,
-                 "algorithmic_bytes_per_launch": alg,
+                 "traffic": None, "kernel": f"directional_kernel<L2,PQ{' wide' if M > 16 else ''}>",
+                 "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
                  "lut_centroid_bytes_per_query": M * 256 * (dim // M) * 4,
                  "per_query": {"visits": float(st[:, 0].mean()), "hops": float(st[:, 1].mean()),
                                "adjacency_entries": float(st[:, 2].mean())}})

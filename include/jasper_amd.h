@@ -107,7 +107,8 @@ extern "C" {
   /* GetVectorDirectional_ :735-763 */                                                        \
   int64_t jasper_get_vector_directional_##id(int64_t handle, int64_t index, void* out,        \
                                              void* stream);                                   \
-  /* GetDirectionalFlags_ :765-775: bit 0 = LSH, bit 1 = PQ; bit 3 = prerotated rows */       \
+  /* GetDirectionalFlags_ :765-775: bit 0 = LSH, bit 1 = PQ; bit 3 = prerotated rows,        \
+   * bit 4 = RaBitQ codes (both extensions) */                                                \
   int64_t jasper_get_directional_flags_##id(int64_t handle);
 
 JASPER_PLAIN_CONFIGS(JASPER_DECLARE_PLAIN)
@@ -195,8 +196,22 @@ int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t
  * reads it back. Otherwise as jasper_build_pq_<cfg> (BuildPq_,
  * ffi/jasper_ffi_common.cuh:507-528). No reference counterpart. */
 int64_t jasperx_build_pq_m(int64_t handle, int64_t m, int64_t n_train, int64_t kmeans_iter, int64_t seed);
-/* directional_search (use_pq = 0) or pq_search (use_pq = 1) with option
- * flags; no reference counterpart. JASPERX_DIR_UNIQUE skips every pop of a
+/* One-bit RaBitQ codes of a directional graph's stored rows (rotated rows
+ * when prerotated): the reference's quantizer (rabitq/quantize.cuh:322-354)
+ * on the rows as stored, against their mean; they feed the RaBitQ estimator
+ * (estimator 2 below) and are saved in the trailer (flag 16). No reference
+ * counterpart (the reference has no RaBitQ estimator: rabitq/distance.cuh
+ * holds only the metric enum). */
+int64_t jasperx_build_rabitq(int64_t handle);
+/* Host copies of the RaBitQ codes: centroid [dim] f32 and nodes
+ * [n, node_bytes] (code bytes, f_add, f_rescale); returns node_bytes. NULL
+ * skips a part. */
+int64_t jasperx_export_rabitq(int64_t handle, float* centroid, uint8_t* nodes);
+/* The directional search with estimator 0 = LSH (directional_search),
+ * 1 = PQ (pq_search) or 2 = RaBitQ (an extension: the one-bit estimator
+ * est = f_add + g_add + f_rescale * <b - 1/2, q'> over the neighbour's
+ * code b and the query quantized to 4 bits, inner product by popcounts),
+ * with option flags; no reference counterpart. JASPERX_DIR_UNIQUE skips every pop of a
  * node already in the exact top-k list: the reference's traversal
  * (graph_beam_search.cuh:160-206) re-visits such nodes and inserts them
  * into that list again, so one node can fill several of the k slots. With
@@ -204,7 +219,7 @@ int64_t jasperx_build_pq_m(int64_t handle, int64_t m, int64_t n_train, int64_t k
  * traversal, identical to jasper_directional_search_<cfg>. Queries, outputs
  * and stream as for jasper_directional_search_<cfg>. */
 #define JASPERX_DIR_UNIQUE 1u
-int64_t jasperx_directional_search_ex(int64_t handle, int32_t use_pq, const void* queries, int64_t n_queries,
+int64_t jasperx_directional_search_ex(int64_t handle, int32_t estimator, const void* queries, int64_t n_queries,
                                       int64_t dim, int32_t* out_ids, float* out_dists, int64_t k,
                                       int64_t beam_width, int64_t limit, uint32_t flags, void* stream);
 /* No reference counterpart; for callers that cannot allocate device memory
@@ -221,15 +236,15 @@ int64_t jasperx_directional_search_ex(int64_t handle, int32_t use_pq, const void
  * ~540 with m = 120 at d = 960). Queries must be device memory.
  * Every call on a GPU shares that GPU's buffer, so calls that overlap on one
  * GPU (other streams, other threads) race. */
-int64_t jasperx_directional_search_noalloc(int64_t handle, int32_t use_pq, const void* queries,
+int64_t jasperx_directional_search_noalloc(int64_t handle, int32_t estimator, const void* queries,
                                            int64_t n_queries, int64_t dim, int32_t* out_ids, float* out_dists,
                                            int64_t k, int64_t beam_width, int64_t limit, uint32_t flags,
                                            void* stream);
-/* Measurement run of directional_search (use_pq = 0) or pq_search
- * (use_pq = 1), flags as above: the same traversal, writing per-query work
+/* Measurement run of the directional search with an estimator as above
+ * (0 LSH, 1 PQ, 2 RaBitQ), flags as above: the same traversal, writing per-query work
  * counters to host memory out_stats[n_queries * 3] = {visits, hops
  * expanded, adjacency entries read}. Not a search entry point. */
-int64_t jasperx_directional_stats(int64_t handle, int32_t use_pq, const void* queries, int64_t n_queries,
+int64_t jasperx_directional_stats(int64_t handle, int32_t estimator, const void* queries, int64_t n_queries,
                                   int64_t dim, int64_t k, int64_t beam_width, int64_t limit, uint32_t flags,
                                   uint32_t* out_stats, void* stream);
 /* The prerotation seed of a directional graph (-1 when its rows are not

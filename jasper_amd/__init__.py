@@ -96,6 +96,8 @@ _AGNOSTIC = {
     "jasperx_directional_stats": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_uint32,
                                   _ptr, _ptr],
     "jasperx_build_pq_m": [_i64, _i64, _i64, _i64, _i64],
+    "jasperx_build_rabitq": [_i64],
+    "jasperx_export_rabitq": [_i64, _ptr, _ptr],
     "jasperx_directional_search_noalloc": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64,
                                            _i64, ctypes.c_uint32, _ptr],
     "jasperx_directional_search_ex": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
@@ -234,7 +236,7 @@ class Graph:
     def __init__(self, handle: int, config_id: str, data_type: DataType, distance: DistanceFunc,
                  n_neighbors: int, dim: int, *, is_directional: bool = False,
                  k_ranks: int | None = None, has_lsh: bool = False, has_pq: bool = False,
-                 prerotate: bool = False, prerotate_seed: int = 42):
+                 prerotate: bool = False, prerotate_seed: int = 42, has_rabitq: bool = False):
         self._handle = handle
         self._config_id = config_id
         self._data_type = data_type
@@ -246,6 +248,7 @@ class Graph:
         self._k_ranks = k_ranks
         self._has_lsh = has_lsh
         self._has_pq = has_pq
+        self._has_rabitq = has_rabitq
         self._prerotate = prerotate
         self._prerotate_seed = prerotate_seed
         if is_directional:
@@ -291,7 +294,8 @@ class Graph:
             prerotate, prerotate_seed = True, int(_agnostic("jasperx_prerotate_seed")(handle))
         return cls(handle, config_id, data_type, distance, n_neighbors, dim,
                    is_directional=True, k_ranks=k_ranks, has_lsh=bool(flags & 1),
-                   has_pq=bool(flags & 2), prerotate=prerotate, prerotate_seed=prerotate_seed)
+                   has_pq=bool(flags & 2), prerotate=prerotate, prerotate_seed=prerotate_seed,
+                   has_rabitq=bool(flags & 16))
 
     def save(self, path: str) -> None:
         """Save to the reference's binary format (reference __init__.py:307-320)."""
@@ -305,13 +309,15 @@ class Graph:
               build_pq: bool = False, k_ranks: int = 4, prerotate: bool | None = None,
               prerotate_seed: int = 42, lsh_samples: int = 32768, lsh_seed: int = 42,
               pq_train: int = 40000, pq_kmeans_iter: int = 12, pq_seed: int = 123,
-              pq_m: int | None = None) -> "Graph":
+              pq_m: int | None = None, build_rabitq: bool = False) -> "Graph":
         """Construct a Vamana graph on the GPU (reference __init__.py:322-428).
 
         pq_m (an extension, no reference counterpart) sets the number of PQ
         subspaces; None keeps the reference's pq_m = k_ranks. Any value that
         divides the padded dim, up to 128, e.g. 120 for one subspace per 8
-        dims at d = 960."""
+        dims at d = 960. build_rabitq (an extension) adds one-bit RaBitQ codes
+        of the stored rows for rabitq_search; it makes the graph directional
+        like build_lsh / build_pq."""
         if isinstance(distance, str):
             distance = DistanceFunc(distance)
         workspace_budget_bytes = parse_storage_size(workspace_budget)
@@ -325,7 +331,7 @@ class Graph:
             raise ValueError(f"Unsupported tensor dtype: {vectors.dtype}. Use torch.float16.")
         n = vectors.size(0)
         stream = _stream_ptr(vectors.device if vectors.is_cuda else None)
-        if not (build_lsh or build_pq):
+        if not (build_lsh or build_pq or build_rabitq):
             config_id = _resolve_config(data_type, n_neighbors, distance)
             handle = _op("construct", config_id)(_tensor_ptr(vectors), n, dim, float(alpha),
                                                  workspace_budget_bytes, on_host, stream)
@@ -342,8 +348,11 @@ class Graph:
                 _op("build_pq", config_id)(handle, pq_train, pq_kmeans_iter, pq_seed)
             else:
                 _agnostic("jasperx_build_pq_m")(handle, pq_m, pq_train, pq_kmeans_iter, pq_seed)
+        if build_rabitq:
+            _agnostic("jasperx_build_rabitq")(handle)
         return cls(handle, config_id, data_type, distance, n_neighbors, dim,
                    is_directional=True, k_ranks=k_ranks, has_lsh=build_lsh, has_pq=build_pq,
+                   has_rabitq=build_rabitq,
                    prerotate=resolved_prerotate, prerotate_seed=prerotate_seed)
 
     # -- properties ---------------------------------------------------------
@@ -406,15 +415,18 @@ class Graph:
         return self._run_search(self._search_fn, queries, k, beam_width, beam_width * 2,
                                 print_throughput)
 
-    def _run_unique(self, use_pq, queries, k, beam_width, limit):
+    def _run_ex(self, estimator, queries, k, beam_width, limit, unique):
         n_queries = queries.size(0)
         out_indices = torch.empty(n_queries, k, dtype=torch.int32, device=queries.device)
         out_distances = torch.empty(n_queries, k, dtype=torch.float32, device=queries.device)
         _agnostic("jasperx_directional_search_ex")(
-            self._handle, 1 if use_pq else 0, _tensor_ptr(queries), n_queries, self._dim,
-            _tensor_ptr(out_indices), _tensor_ptr(out_distances), k, beam_width, limit, DIR_UNIQUE,
-            _stream_ptr(queries.device))
+            self._handle, estimator, _tensor_ptr(queries), n_queries, self._dim,
+            _tensor_ptr(out_indices), _tensor_ptr(out_distances), k, beam_width, limit,
+            DIR_UNIQUE if unique else 0, _stream_ptr(queries.device))
         return out_indices, out_distances
+
+    def _run_unique(self, use_pq, queries, k, beam_width, limit):
+        return self._run_ex(1 if use_pq else 0, queries, k, beam_width, limit, True)
 
     def directional_search(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
                            limit: int | None = None, print_throughput: bool = False,
@@ -453,6 +465,22 @@ class Graph:
             return self._run_unique(True, queries, k, beam_width, resolved_limit)
         return self._run_search(self._pq_search_fn, queries, k, beam_width, resolved_limit,
                                 print_throughput)
+
+    def rabitq_search(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
+                      limit: int | None = None, unique: bool = False):
+        """Directional search with the one-bit RaBitQ estimator (an
+        extension, no reference counterpart): the traversal of
+        directional_search, with each neighbour estimated from its RaBitQ
+        code (built with build_rabitq=True) and the query quantized to 4 bits;
+        unique as for directional_search."""
+        self._check_alive()
+        if not self._is_directional or not self._has_rabitq:
+            raise RuntimeError(
+                "rabitq_search() requires a graph built with build_rabitq=True "
+                "(or loaded with RaBitQ codes present)")
+        queries = self._query_check(queries)
+        resolved_limit = limit if limit is not None else beam_width * 2
+        return self._run_ex(2, queries, k, beam_width, resolved_limit, unique)
 
     # -- misc (reference __init__.py:623-766) -------------------------------
     def get_vector(self, stable_id: int) -> torch.Tensor:
@@ -555,20 +583,33 @@ class Graph:
         return out
 
     def directional_stats(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
-                          limit: int | None = None, pq: bool = False, unique: bool = False) -> np.ndarray:
-        """Per-query work counters of directional_search (pq=False) or
-        pq_search (pq=True) [n_queries, 3]: visits, hops expanded, adjacency
-        entries read. A measurement extension."""
+                          limit: int | None = None, pq: bool = False, unique: bool = False,
+                          estimator: int | None = None) -> np.ndarray:
+        """Per-query work counters of directional_search (pq=False),
+        pq_search (pq=True) or another estimator (estimator = 0 LSH, 1 PQ,
+        2 RaBitQ) [n_queries, 3]: visits, hops expanded, adjacency entries
+        read. A measurement extension."""
         self._check_alive()
         queries = self._query_check(queries)
         nq = queries.size(0)
         out = np.zeros((nq, 3), dtype=np.uint32)
         lim = limit if limit is not None else 2 * beam_width
-        _agnostic("jasperx_directional_stats")(self._handle, 1 if pq else 0, _tensor_ptr(queries), nq, self._dim,
+        est = estimator if estimator is not None else (1 if pq else 0)
+        _agnostic("jasperx_directional_stats")(self._handle, est, _tensor_ptr(queries), nq, self._dim,
                                                k, beam_width, lim, DIR_UNIQUE if unique else 0,
                                                out.ctypes.data_as(_ptr),
                                                _stream_ptr(queries.device))
         return out
+
+    def export_rabitq(self):
+        """(centroid f32 [dim], nodes u8 [n, node_bytes]); a test extension."""
+        self._check_alive()
+        fn = _agnostic("jasperx_export_rabitq")
+        nb = fn(self._handle, None, None)
+        c = np.empty(self._dim, dtype=np.float32)
+        nodes = np.empty((self.n_vectors, nb), dtype=np.uint8)
+        fn(self._handle, c.ctypes.data_as(_ptr), nodes.ctypes.data_as(_ptr))
+        return c, nodes
 
     def export_lsh(self):
         """(c_per_rank f32 [k_ranks], norm_denom, rows u8 [n, row_bytes]); a
@@ -634,7 +675,7 @@ class Graph:
         extra = ""
         if self._is_directional:
             extra = (f", k_ranks={self._k_ranks}, lsh={self._has_lsh}, "
-                     f"pq={self._has_pq}, prerotate={self._prerotate}")
+                     f"pq={self._has_pq}, rabitq={self._has_rabitq}, prerotate={self._prerotate}")
         return (f"Graph(n_vectors={self.n_vectors}, dim={self.dim}, "
                 f"R={self._n_neighbors}, dtype={self._data_type.value}, "
                 f"dist={self._distance.value}{extra})")

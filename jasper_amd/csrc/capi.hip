@@ -373,7 +373,7 @@ JASPER_PLAIN_CONFIGS(JA_DEFINE_PLAIN)
     return guarded([&]() -> int64_t {                                                                          \
       const Config c = config_of(#id);                                                                         \
       Graph& g = lookup(h, &c);                                                                                \
-      return (int64_t)((g.lsh ? 1 : 0) | (g.pq ? 2 : 0) | (g.prerotate ? 8 : 0));                             \
+      return (int64_t)((g.lsh ? 1 : 0) | (g.pq ? 2 : 0) | (g.prerotate ? 8 : 0) | (g.rabitq ? 16 : 0));                             \
     });                                                                                                        \
   }
 
@@ -563,29 +563,50 @@ extern "C" int64_t jasperx_build_pq_m(int64_t h, int64_t m, int64_t n_train, int
   });
 }
 
-extern "C" int64_t jasperx_directional_search_ex(int64_t h, int32_t use_pq, const void* q, int64_t nq, int64_t dim,
+extern "C" int64_t jasperx_build_rabitq(int64_t h) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (g.k_ranks == 0) throw std::invalid_argument("build_rabitq needs a directional graph");
+    build_rabitq(g);
+    return 0;
+  });
+}
+
+extern "C" int64_t jasperx_export_rabitq(int64_t h, float* centroid, uint8_t* nodes) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (!g.rabitq) throw std::runtime_error("graph has no RaBitQ codes");
+    const RabitqArtifacts& a = *g.rabitq;
+    if (centroid) hip_check(hipMemcpy(centroid, a.centroid, (size_t)a.dim * 4, hipMemcpyDefault), "download centroid");
+    if (nodes && g.n > 0)
+      hip_check(hipMemcpy(nodes, a.nodes, (size_t)g.n * (a.code_bytes + 8), hipMemcpyDefault), "download nodes");
+    return (int64_t)(a.code_bytes + 8);
+  });
+}
+
+extern "C" int64_t jasperx_directional_search_ex(int64_t h, int32_t estimator, const void* q, int64_t nq, int64_t dim,
                                                  int32_t* out_ids, float* out_dists, int64_t k, int64_t bw,
                                                  int64_t limit, uint32_t flags, void* stream) {
   return guarded([&]() -> int64_t {
     if (flags & ~kDirFlagsKnown) throw std::invalid_argument("unknown directional search flags");
-    directional_search(lookup(h, nullptr), use_pq != 0, q, nq, dim, out_ids, out_dists, k, bw, limit, false,
+    directional_search(lookup(h, nullptr), estimator, q, nq, dim, out_ids, out_dists, k, bw, limit, false,
                        (hipStream_t)stream, nullptr, (flags & kDirUnique) != 0);
     return 0;
   });
 }
 
-extern "C" int64_t jasperx_directional_search_noalloc(int64_t h, int32_t use_pq, const void* q, int64_t nq,
+extern "C" int64_t jasperx_directional_search_noalloc(int64_t h, int32_t estimator, const void* q, int64_t nq,
                                                       int64_t dim, int32_t* out_ids, float* out_dists, int64_t k,
                                                       int64_t bw, int64_t limit, uint32_t flags, void* stream) {
   return guarded([&]() -> int64_t {
     if (flags & ~kDirFlagsKnown) throw std::invalid_argument("unknown directional search flags");
-    directional_search_noalloc(lookup(h, nullptr), use_pq != 0, q, nq, dim, out_ids, out_dists, k, bw, limit,
+    directional_search_noalloc(lookup(h, nullptr), estimator, q, nq, dim, out_ids, out_dists, k, bw, limit,
                                (flags & kDirUnique) != 0, (hipStream_t)stream);
     return 0;
   });
 }
 
-extern "C" int64_t jasperx_directional_stats(int64_t h, int32_t use_pq, const void* q, int64_t nq, int64_t dim,
+extern "C" int64_t jasperx_directional_stats(int64_t h, int32_t estimator, const void* q, int64_t nq, int64_t dim,
                                              int64_t k, int64_t bw, int64_t limit, uint32_t flags,
                                              uint32_t* out_stats, void* stream) {
   return guarded([&]() -> int64_t {
@@ -600,7 +621,7 @@ extern "C" int64_t jasperx_directional_stats(int64_t h, int32_t use_pq, const vo
     hip_check(hipMalloc(&st, (size_t)nq * 12), "alloc stats");
     try {
       if (flags & ~kDirFlagsKnown) throw std::invalid_argument("unknown directional search flags");
-      directional_search(g, use_pq != 0, q, nq, dim, ids, d, k, bw, limit, false, s, st, (flags & kDirUnique) != 0);
+      directional_search(g, estimator, q, nq, dim, ids, d, k, bw, limit, false, s, st, (flags & kDirUnique) != 0);
       hip_check(hipMemcpyAsync(out_stats, st, (size_t)nq * 12, hipMemcpyDeviceToHost, s), "download stats");
       hip_check(hipStreamSynchronize(s), "sync stats");
     } catch (...) {

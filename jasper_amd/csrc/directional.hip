@@ -17,6 +17,7 @@
 #include "common.hpp"
 #include "directional.hpp"
 #include "directional_api.hpp"
+#include "rabitq.hpp"
 #include "rotation.hpp"
 #include "search.hpp"
 
@@ -39,6 +40,11 @@ LshArtifacts::~LshArtifacts() {
 PqArtifacts::~PqArtifacts() {
   if (centroids) (void)hipFree(centroids);
   if (codes) (void)hipFree(codes);
+}
+
+RabitqArtifacts::~RabitqArtifacts() {
+  if (nodes) (void)hipFree(nodes);
+  if (centroid) (void)hipFree(centroid);
 }
 
 constexpr uint32_t kInv31 = 0x7FFFFFFFu;
@@ -575,32 +581,44 @@ __global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* __restrict__
                lut + (size_t)blockIdx.x * total);
 }
 
-// dsub <= 32: one table entry per thread; a 256-thread block builds the 256
-// entries of subspace j = blockIdx.y for query blockIdx.x. In the 32-lane
-// form above, lane t holds the leaf v_t = fma(q_t, C_t, +0.0) for t < dsub
-// and +0.0 beyond, and the butterfly leaves the writing lane with the tree
-// v_l + v_(l+16), then + the partner 8 lanes away, 4, 2, 1. The thread sums
-// its own leaves in that tree. Leaves past DS are left out, which is exact:
-// no leaf is -0.0 (fma(a, b, +0.0) of a zero product is +0.0) and
-// x + 0.0 == x for every other x.
+// dsub <= 32: one table entry per thread. Block (b, j) holds the 256
+// centroids of subspace j in registers, one per thread, and builds their
+// entries for queries b * kLutQueries ... (the queries' slices are the same
+// address across the block, so they are broadcast reads); each query's 256
+// entries are one coalesced 1 KB store. In the 32-lane form above, lane t
+// holds the leaf v_t = fma(q_t, C_t, +0.0) for t < dsub and +0.0 beyond, and
+// the butterfly leaves the writing lane with the tree v_l + v_(l+16), then
+// + the partner 8 lanes away, 4, 2, 1. The thread sums its own leaves in
+// that tree. Leaves past DS are left out, which is exact: no leaf is -0.0
+// (fma(a, b, +0.0) of a zero product is +0.0) and x + 0.0 == x for every
+// other x.
+constexpr uint32_t kLutQueries = 32;
 template <int DS>
-__global__ __launch_bounds__(256) void pq_lut_small_kernel(const uint16_t* __restrict__ queries, uint32_t dp,
-                                                           uint32_t M, uint32_t dsub,
+__global__ __launch_bounds__(256) void pq_lut_small_kernel(const uint16_t* __restrict__ queries, int64_t nq,
+                                                           uint32_t dp, uint32_t M, uint32_t dsub,
                                                            const float* __restrict__ centroids,
                                                            float* __restrict__ lut) {
-  const uint32_t e = blockIdx.y * 256 + threadIdx.x;
-  const uint16_t* qj = queries + (size_t)blockIdx.x * dp + (size_t)blockIdx.y * dsub;
+  const uint32_t j = blockIdx.y;
+  const uint32_t e = j * 256 + threadIdx.x;
   const float* C = centroids + (size_t)e * dsub;
-  float v[DS];
+  float c[DS];
 #pragma unroll
-  for (int t = 0; t < DS; ++t) v[t] = (uint32_t)t < dsub ? __builtin_fmaf(h2f16(qj[t]), C[t], 0.0f) : 0.0f;
+  for (int t = 0; t < DS; ++t) c[t] = (uint32_t)t < dsub ? C[t] : 0.0f;
+  const int64_t q0 = (int64_t)blockIdx.x * kLutQueries;
+  const int64_t q1 = min(nq, q0 + (int64_t)kLutQueries);
+  for (int64_t qi = q0; qi < q1; ++qi) {
+    const uint16_t* qj = queries + (size_t)qi * dp + (size_t)j * dsub;
+    float v[DS];
 #pragma unroll
-  for (int h = 16; h >= 1; h >>= 1) {
+    for (int t = 0; t < DS; ++t) v[t] = (uint32_t)t < dsub ? __builtin_fmaf(h2f16(qj[t]), c[t], 0.0f) : 0.0f;
 #pragma unroll
-    for (int t = 0; t < h; ++t)
-      if (t + h < DS) v[t] = v[t] + v[t + h];
+    for (int h = 16; h >= 1; h >>= 1) {
+#pragma unroll
+      for (int t = 0; t < h; ++t)
+        if (t + h < DS) v[t] = v[t] + v[t + h];
+    }
+    lut[(size_t)qi * M * 256 + e] = v[0];
   }
-  lut[(size_t)blockIdx.x * M * 256 + e] = v[0];
 }
 
 struct DirArgs {
@@ -627,6 +645,10 @@ struct DirArgs {
   uint32_t code_row_bytes, pq_w, pq_groups;
   const float* norms;
   const float* luts;  // [nq, M * 256] from pq_lut_kernel
+  // RaBitQ
+  const uint8_t* rq_nodes;     // [n, rq_node_bytes]: code dwords, f_add, f_rescale
+  const float* rq_centroid;    // [rq_dim]
+  uint32_t rq_node_bytes, rq_words, rq_dim;
   // optional work counters per query: {visits, hops expanded, adjacency entries}
   uint32_t* stats;
   // skip pops of ids already in the frontier (distinct results; an extension)
@@ -674,14 +696,15 @@ __device__ __forceinline__ uint32_t lsh_word(const uint32_t* w, int r) {
 }
 
 // K = 0: the PQ estimator, with up to 16 * P subspaces (the edge's codes are
-// P groups of 16 bytes in registers); K in {4, 16} with P-byte words: the
-// LSH estimator.
+// P groups of 16 bytes in registers); K = 1: the RaBitQ estimator with codes
+// of up to 32 * P dims; K in {4, 16} with P-byte words: the LSH estimator.
 template <int METRIC, int K, int P>
 __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
   constexpr bool L2 = METRIC == kL2;
   constexpr bool PQ = K == 0;
-  constexpr int KW = PQ ? 1 : K * P / 4;  // dwords of LSH words per edge
+  constexpr bool RQ = K == 1;
+  constexpr int KW = (PQ || RQ) ? 1 : K * P / 4;  // dwords of LSH words per edge
   const uint32_t lane = threadIdx.x;
   const uint32_t qid = blockIdx.x;
   const uint32_t nchunks = a.dp / 8;
@@ -720,6 +743,66 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       q_sq = block128_sum(p0, p1);
     }
     wave_sync();
+  }
+
+  // RaBitQ query factors (the estimator of directional_oracle.cpp,
+  // rq_prepare): the query quantized to 4 bits over its first rq_dim values,
+  // as bit planes (uniform: plane j, dword w at rq_planes[j * P + w]), the
+  // sum of the 4-bit values, delta / 2, lo / 2 and g_add
+  uint32_t rq_planes[RQ ? 4 * P : 1];
+  int32_t rq_sumq = 0;
+  float rq_hd = 0.0f, rq_hl = 0.0f, rq_gadd = 0.0f;
+  if constexpr (RQ) {
+    float lo = FLT_MAX, hi = -FLT_MAX;
+    for (uint32_t i = lane; i < a.rq_dim; i += 64) {
+      const float v = h2f16(q16[i]);
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      lo = fminf(lo, __shfl_xor(lo, m, 64));
+      hi = fmaxf(hi, __shfl_xor(hi, m, 64));
+    }
+    lo = lo + 0.0f;  // one zero for -0.0 and +0.0
+    hi = hi + 0.0f;
+    const float delta = div_rn(hi - lo, 15.0f);
+    int32_t sq = 0;
+    float g = 0.0f;
+#pragma unroll
+    for (int m = 0; m < P / 2; ++m) {
+      const uint32_t i = 64u * m + lane;
+      uint32_t qb = 0;
+      if (i < a.rq_dim) {
+        const float qi = h2f16(q16[i]), ci = a.rq_centroid[i];
+        if (delta > 0.0f) {
+          const float t = rintf(div_rn(qi - lo, delta));
+          qb = (uint32_t)fminf(15.0f, fmaxf(0.0f, t));
+        }
+        if constexpr (L2) {
+          const float d = qi - ci;
+          g = __builtin_fmaf(d, d, g);
+        } else {
+          g = __builtin_fmaf(qi, ci, g);
+        }
+      }
+      sq += (int32_t)qb;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint64_t bits = ballot(((qb >> j) & 1u) != 0u);
+        rq_planes[j * P + 2 * m] = (uint32_t)bits;
+        rq_planes[j * P + 2 * m + 1] = (uint32_t)(bits >> 32);
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      sq += __shfl_xor(sq, m, 64);
+      g = g + __shfl_xor(g, m, 64);
+    }
+    rq_sumq = sq;
+    rq_hd = 0.5f * delta;
+    rq_hl = 0.5f * lo;
+    rq_gadd = L2 ? g : -1.0f - g;
   }
 
   // B = [(medoid, est 0.0, unvisited)], F empty (graph_beam_search.cuh:141-149)
@@ -766,7 +849,9 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     uint32_t wl[KW];
     uint32_t mag_bits = 0;
     uint4 cw[PQ ? P : 1];  // PQ: codes of subspaces 16g .. 16g + 15 in cw[g]
-    if constexpr (!PQ) {
+    if constexpr (RQ) {
+      // nothing of u's row: the estimator reads the neighbours' codes below
+    } else if constexpr (!PQ) {
       const uint8_t* row = a.lsh_rows + (size_t)u * a.row_bytes;
       if (slot) {
         const uint8_t* wp = row + (size_t)lane * (K * P);
@@ -810,6 +895,20 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     const bool valid_v = has && (int64_t)v_raw < a.n;
     float vnorm = 0.0f;
     if constexpr (PQ && L2) vnorm = valid_v ? a.norms[v_raw] : 0.0f;
+    // RaBitQ: the neighbour's code dwords and factors (a gather per edge,
+    // issued before the visit so the two overlap)
+    uint32_t rq_code[RQ ? P : 1];
+    float rq_fadd = 0.0f, rq_fres = 0.0f;
+    if constexpr (RQ) {
+      const uint32_t* node = reinterpret_cast<const uint32_t*>(a.rq_nodes + (size_t)(valid_v ? v_raw : 0u) *
+                                                                                 a.rq_node_bytes);
+#pragma unroll
+      for (int w = 0; w < P; ++w) rq_code[w] = (valid_v && (uint32_t)w < a.rq_words) ? node[w] : 0u;
+      if (valid_v) {
+        rq_fadd = __uint_as_float(node[a.rq_words]);
+        rq_fres = __uint_as_float(node[a.rq_words + 1]);
+      }
+    }
     const uint4* urow = reinterpret_cast<const uint4*>(a.vecs) + (size_t)u * nchunks;
 
     // visit: exact distance of u (the one vector fetch per hop)
@@ -881,7 +980,19 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     if (has) {
       if (valid_v) {
         float est;
-        if constexpr (PQ) {
+        if constexpr (RQ) {
+          int32_t dot = 0, pc = 0;
+#pragma unroll
+          for (int w = 0; w < P; ++w) {
+            const uint32_t c = rq_code[w];
+            pc += __builtin_popcount(c);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dot += __builtin_popcount(c & rq_planes[j * P + w]) << j;
+          }
+          const float t1 = (float)(2 * dot - rq_sumq), t2 = (float)(2 * pc - (int32_t)a.rq_dim);
+          const float ipq = __builtin_fmaf(rq_hd, t1, rq_hl * t2);
+          est = __builtin_fmaf(rq_fres, ipq, rq_fadd + rq_gadd);
+        } else if constexpr (PQ) {
           // acc = <q,u> + sum over j = 0, 1, ..., M - 1 of LUT[j][code_j], in
           // that order (pq_beam_search.cuh:97-100)
           float acc = qu_dot;
@@ -1200,6 +1311,84 @@ void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed, uint32_t 
   g.pq = std::move(art);
 }
 
+// ----------------------------------------------------------- RaBitQ build --
+
+// Column sums of the stored rows in a fixed order (so the centroid is the
+// same on every run): block b adds rows [b * chunk, (b + 1) * chunk) of each
+// column (thread = column, four rows per step), then rabitq_mean_kernel adds
+// the block sums in block order and divides by n.
+__global__ __launch_bounds__(256) void column_partial_kernel(const uint16_t* __restrict__ vecs, int64_t n,
+                                                             uint32_t dp, uint32_t dim, int64_t chunk,
+                                                             float* __restrict__ partial) {
+  const int64_t r0 = (int64_t)blockIdx.x * chunk, r1 = min(n, r0 + chunk);
+  for (uint32_t c = threadIdx.x; c < dim; c += blockDim.x) {
+    float s = 0.0f;
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+      const float v0 = h2f16(vecs[(size_t)r * dp + c]), v1 = h2f16(vecs[(size_t)(r + 1) * dp + c]);
+      const float v2 = h2f16(vecs[(size_t)(r + 2) * dp + c]), v3 = h2f16(vecs[(size_t)(r + 3) * dp + c]);
+      s = s + v0;
+      s = s + v1;
+      s = s + v2;
+      s = s + v3;
+    }
+    for (; r < r1; ++r) s = s + h2f16(vecs[(size_t)r * dp + c]);
+    partial[(size_t)blockIdx.x * dim + c] = s;
+  }
+}
+
+__global__ void rabitq_mean_kernel(const float* __restrict__ partial, uint32_t blocks, uint32_t dim, int64_t n,
+                                   float* __restrict__ out) {
+  for (uint32_t c = threadIdx.x; c < dim; c += blockDim.x) {
+    float s = 0.0f;
+    for (uint32_t b = 0; b < blocks; ++b) s = s + partial[(size_t)b * dim + c];
+    out[c] = div_rn(s, (float)n);
+  }
+}
+
+__global__ void identity_kernel(float* __restrict__ P, uint32_t dim) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < (uint64_t)dim * dim) P[t] = (t % (dim + 1u) == 0) ? 1.0f : 0.0f;
+}
+
+void build_rabitq(Graph& g) {
+  if (g.n <= 0) throw std::runtime_error("build_rabitq: graph is empty");
+  if (g.dim == 0 || g.dim > 256) throw std::invalid_argument("RaBitQ codes support 1 <= dim <= 256");
+  if (g.on_host) throw std::invalid_argument("build_rabitq requires the graph on device");
+  auto art = std::make_unique<RabitqArtifacts>();
+  art->dim = g.dim;
+  art->code_bytes = rabitq_code_bytes(g.dim);
+  const size_t node = art->code_bytes + 8;
+  const uint32_t blocks = (uint32_t)std::max<int64_t>(1, std::min<int64_t>(8192, (g.n + 255) / 256));
+  const int64_t chunk = (g.n + blocks - 1) / blocks;
+  float* partial = nullptr;
+  float* eye = nullptr;
+  hip_check(hipMalloc(&art->nodes, (size_t)g.n * node), "alloc rabitq nodes");
+  hip_check(hipMalloc((void**)&art->centroid, (size_t)g.dim * 4), "alloc rabitq centroid");
+  try {
+    hip_check(hipMalloc((void**)&partial, (size_t)blocks * g.dim * 4), "alloc column sums");
+    hip_check(hipMalloc((void**)&eye, (size_t)g.dim * g.dim * 4), "alloc identity");
+    hipLaunchKernelGGL(column_partial_kernel, dim3(blocks), dim3(256), 0, nullptr, (const uint16_t*)g.vecs, g.n, g.dp,
+                       g.dim, chunk, partial);
+    hipLaunchKernelGGL(rabitq_mean_kernel, dim3(1), dim3(256), 0, nullptr, (const float*)partial, blocks, g.dim, g.n,
+                       art->centroid);
+    const uint64_t pe = (uint64_t)g.dim * g.dim;
+    hipLaunchKernelGGL(identity_kernel, dim3((uint32_t)((pe + 255) / 256)), dim3(256), 0, nullptr, eye, g.dim);
+    hip_check(hipGetLastError(), "launch rabitq centroid");
+    // the rows are already rotated when the graph was prerotated: quantize
+    // them as stored (identity rotation: one product per output, exact)
+    rabitq_quantize(g.vecs, true, g.n, g.dim, g.dp, eye, art->centroid, g.metric, art->nodes, nullptr);
+    hip_check(hipDeviceSynchronize(), "rabitq build");
+  } catch (...) {
+    (void)hipFree(partial);
+    (void)hipFree(eye);
+    throw;
+  }
+  (void)hipFree(partial);
+  (void)hipFree(eye);
+  g.rabitq = std::move(art);
+}
+
 // Query rows [nq, dim] (device memory) into rows of stride dp, zero padded.
 __global__ void pad_rows_kernel(const uint16_t* __restrict__ src, int64_t nq, uint32_t dim, uint32_t dp,
                                 uint16_t* __restrict__ dst) {
@@ -1291,18 +1480,22 @@ const uint16_t* directional_query_rows(const Graph& g, const void* queries, int6
   return rot;
 }
 
-size_t directional_lds_bytes(const Graph& g, bool use_pq, int64_t k, int64_t bw) {
+size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
   size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
-  if (use_pq) lds += (size_t)g.pq->m * 256 * 4;
+  if (est == kEstPq) lds += (size_t)g.pq->m * 256 * 4;
   return lds;
 }
 
 // Every argument check of directional_search, before anything is allocated
 // or launched.
-void check_directional_search(const Graph& g, bool use_pq, int64_t nq, int64_t dim, int64_t k, int64_t bw,
+void check_directional_search(const Graph& g, int est, int64_t nq, int64_t dim, int64_t k, int64_t bw,
                               int64_t limit) {
+  if (est < kEstLsh || est > kEstRabitq) throw std::invalid_argument("unknown directional estimator");
+  const bool use_pq = est == kEstPq;
   if (use_pq && !g.pq) throw std::runtime_error("graph has no PQ artifacts built — call build_pq() first");
-  if (!use_pq && !g.lsh) throw std::runtime_error("graph has no LSH artifacts built — call build_lsh() first");
+  if (est == kEstLsh && !g.lsh) throw std::runtime_error("graph has no LSH artifacts built — call build_lsh() first");
+  if (est == kEstRabitq && !g.rabitq)
+    throw std::runtime_error("graph has no RaBitQ codes built — call build_rabitq() first");
   if (dim != (int64_t)g.dim)
     throw std::invalid_argument("query dim (" + std::to_string(dim) + ") != graph dim (" + std::to_string(g.dim) + ")");
   if (nq < 0 || k < 0 || bw <= 0 || limit < 0) throw std::invalid_argument("negative size argument");
@@ -1316,11 +1509,13 @@ void check_directional_search(const Graph& g, bool use_pq, int64_t nq, int64_t d
     if (g.metric == kL2 && !g.vector_norms) throw std::runtime_error("graph has no vector norms");
     if (g.pq->m == 0 || g.pq->m > kPqMaxM)
       throw std::invalid_argument("pq_search supports at most " + std::to_string(kPqMaxM) + " subspaces");
-  } else if (!((g.lsh->k_ranks == 4 || g.lsh->k_ranks == 16) &&
-               (g.lsh->packed_bytes == 1 || g.lsh->packed_bytes == 2))) {
+  } else if (est == kEstLsh && !((g.lsh->k_ranks == 4 || g.lsh->k_ranks == 16) &&
+                                  (g.lsh->packed_bytes == 1 || g.lsh->packed_bytes == 2))) {
     throw std::invalid_argument("k_ranks must be 4 or 16 with 1- or 2-byte words");
+  } else if (est == kEstRabitq && (g.rabitq->dim != g.dim || g.rabitq->code_bytes > 32)) {
+    throw std::invalid_argument("RaBitQ codes do not match the graph");
   }
-  if (directional_lds_bytes(g, use_pq, k, bw) > 160 * 1024)
+  if (directional_lds_bytes(g, est, k, bw) > 160 * 1024)
     throw std::invalid_argument("beam_width, k and dim need more than 160 KB of LDS");
 }
 
@@ -1335,9 +1530,10 @@ void launch_directional(const DirArgs& a, uint32_t nq, size_t lds, hipStream_t s
 
 // The search after check_directional_search, with its device buffers taken
 // from `scratch`.
-void directional_search_run(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+void directional_search_run(Graph& g, int est, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                             float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
                             uint32_t* stats, bool unique, SearchScratch& scratch) {
+  const bool use_pq = est == kEstPq;
   EventPair ev;
   if (print) {
     hip_check(hipEventCreate(&ev.e0), "event");
@@ -1363,9 +1559,23 @@ void directional_search_run(Graph& g, bool use_pq, const void* queries, int64_t 
   a.out_dists = out_dists;
   a.stats = stats;
   a.unique = unique ? 1u : 0u;
-  const size_t lds = directional_lds_bytes(g, use_pq, k, bw);
+  const size_t lds = directional_lds_bytes(g, est, k, bw);
   const bool l2 = g.metric == kL2;
-  if (use_pq) {
+  if (est == kEstRabitq) {
+    const RabitqArtifacts& rq = *g.rabitq;
+    a.rq_nodes = (const uint8_t*)rq.nodes;
+    a.rq_centroid = rq.centroid;
+    a.rq_node_bytes = rq.code_bytes + 8;
+    a.rq_words = rq.code_bytes / 4;
+    a.rq_dim = rq.dim;
+    if (a.rq_words <= 4) {
+      if (l2) launch_directional<kL2, 1, 4>(a, (uint32_t)nq, lds, stream);
+      else launch_directional<kIP, 1, 4>(a, (uint32_t)nq, lds, stream);
+    } else {
+      if (l2) launch_directional<kL2, 1, 8>(a, (uint32_t)nq, lds, stream);
+      else launch_directional<kIP, 1, 8>(a, (uint32_t)nq, lds, stream);
+    }
+  } else if (use_pq) {
     a.M = g.pq->m;
     a.dsub = g.pq->dsub;
     a.centroids = g.pq->centroids;
@@ -1376,8 +1586,8 @@ void directional_search_run(Graph& g, bool use_pq, const void* queries, int64_t 
     a.norms = g.vector_norms;
     float* luts = (float*)scratch.take((size_t)nq * a.M * 256 * 4);
     const auto small_lut = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3((uint32_t)nq, a.M), dim3(256), 0, stream, qsrc, a.dp, a.M, a.dsub, a.centroids,
-                         luts);
+      const dim3 lgrid((uint32_t)((nq + kLutQueries - 1) / kLutQueries), a.M);
+      hipLaunchKernelGGL(kern, lgrid, dim3(256), 0, stream, qsrc, nq, a.dp, a.M, a.dsub, a.centroids, luts);
     };
     if (a.dsub <= 8) small_lut(pq_lut_small_kernel<8>);
     else if (a.dsub <= 16) small_lut(pq_lut_small_kernel<16>);
@@ -1423,7 +1633,8 @@ void directional_search_run(Graph& g, bool use_pq, const void* queries, int64_t 
     hip_check(hipEventSynchronize(ev.e1), "event sync");
     float ms = 0;
     (void)hipEventElapsedTime(&ms, ev.e0, ev.e1);
-    std::printf("[%s] duration=%gms, throughput=%g\n", use_pq ? "pq_search" : "directional_search", ms,
+    std::printf("[%s] duration=%gms, throughput=%g\n",
+                use_pq ? "pq_search" : (est == kEstRabitq ? "rabitq_search" : "directional_search"), ms,
                 nq * 1000.0 / ms);
     std::fflush(stdout);
   }
@@ -1431,11 +1642,11 @@ void directional_search_run(Graph& g, bool use_pq, const void* queries, int64_t 
 
 }  // namespace
 
-size_t directional_scratch_bytes(const Graph& g, bool use_pq, int64_t nq) {
+size_t directional_scratch_bytes(const Graph& g, int est, int64_t nq) {
   if (nq <= 0) return 0;
   const size_t rows = round256((size_t)nq * g.dp * 2);
   size_t b = rows + (g.prerotate ? rows : 0);
-  if (use_pq && g.pq) b += round256((size_t)nq * g.pq->m * 256 * 4);
+  if (est == kEstPq && g.pq) b += round256((size_t)nq * g.pq->m * 256 * 4);
   return b;
 }
 
@@ -1449,30 +1660,30 @@ void directional_query_rows_to_host(const Graph& g, const void* queries, int64_t
   hip_check(hipStreamSynchronize(stream), "sync query rows");
 }
 
-void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+void directional_search(Graph& g, int est, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                         float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
                         uint32_t* stats, bool unique) {
-  check_directional_search(g, use_pq, nq, dim, k, bw, limit);
+  check_directional_search(g, est, nq, dim, k, bw, limit);
   if (nq == 0 || k == 0) return;
   SearchScratch scratch(stream);
-  directional_search_run(g, use_pq, queries, nq, dim, out_ids, out_dists, k, bw, limit, print, stream, stats,
-                         unique, scratch);
+  directional_search_run(g, est, queries, nq, dim, out_ids, out_dists, k, bw, limit, print, stream, stats, unique,
+                         scratch);
 }
 
-void directional_search_fixed(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+void directional_search_fixed(Graph& g, int est, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                               float* out_dists, int64_t k, int64_t bw, int64_t limit, bool unique, hipStream_t stream,
                               void* scratch_base, size_t scratch_bytes) {
-  check_directional_search(g, use_pq, nq, dim, k, bw, limit);
+  check_directional_search(g, est, nq, dim, k, bw, limit);
   if (nq == 0 || k == 0) return;
-  const size_t need = directional_scratch_bytes(g, use_pq, nq);
+  const size_t need = directional_scratch_bytes(g, est, nq);
   if (need > scratch_bytes)
     throw std::invalid_argument("directional search of " + std::to_string(nq) + " queries needs " +
                                 std::to_string(need) + " bytes of scratch; at most " + std::to_string(scratch_bytes) +
                                 " are available (search fewer queries per call)");
   if (!device_rows(queries)) throw std::invalid_argument("queries must be device memory");
   SearchScratch scratch(stream, scratch_base, scratch_bytes);
-  directional_search_run(g, use_pq, queries, nq, dim, out_ids, out_dists, k, bw, limit, false, stream, nullptr,
-                         unique, scratch);
+  directional_search_run(g, est, queries, nq, dim, out_ids, out_dists, k, bw, limit, false, stream, nullptr, unique,
+                         scratch);
 }
 
 // ------------------------------------------------- allocation-free search --
@@ -1505,12 +1716,12 @@ void* scratch_address() {
 
 size_t directional_noalloc_scratch_bytes() { return kNoAllocScratchBytes; }
 
-void directional_search_noalloc(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim,
+void directional_search_noalloc(Graph& g, int est, const void* queries, int64_t nq, int64_t dim,
                                 int32_t* out_ids, float* out_dists, int64_t k, int64_t bw, int64_t limit,
                                 bool unique, hipStream_t stream) {
   // every byte a call reads from the scratch it has written first (the
   // padded query rows, their rotation, the PQ tables), so nothing is cleared
-  directional_search_fixed(g, use_pq, queries, nq, dim, out_ids, out_dists, k, bw, limit, unique, stream,
+  directional_search_fixed(g, est, queries, nq, dim, out_ids, out_dists, k, bw, limit, unique, stream,
                            scratch_address(), kNoAllocScratchBytes);
 }
 
@@ -1519,8 +1730,9 @@ void directional_search_noalloc(Graph& g, bool use_pq, const void* queries, int6
 // version, u8 flags (1 LSH, 2 PQ, 4 norms); LSH: u8 K, u8 sizeof(packed_t),
 // K floats c_per_rank + float norm_denom, N rows; PQ: u32 M, u32 256,
 // u32 dsub, centroids, N code rows; norms: N floats. This build adds flag 8
-// (prerotated rows) with a u64 seed after the other sections: readers that
-// know flags 1, 2 and 4 only stop before it. Read back at the end of
+// (prerotated rows) with a u64 seed after the other sections, then flag 16
+// (RaBitQ codes: u32 dim, u32 code bytes, dim floats of centroid, N nodes):
+// readers that know flags 1, 2 and 4 only stop before them. Read back at the end of
 // the base section (total_file_size), where the saver puts it; the
 // reference loader looks elsewhere (graph.cuh:1959-1964) and never finds it.
 
@@ -1581,11 +1793,12 @@ void save_directional_file(const Graph& g, const std::string& path) {
   save_graph_file(g, path);
   if (g.n == 0) return;
   const bool has_lsh = (bool)g.lsh, has_pq = (bool)g.pq, has_norms = g.vector_norms != nullptr;
-  if (!has_lsh && !has_pq && !has_norms && !g.prerotate) return;
+  const bool has_rq = (bool)g.rabitq;
+  if (!has_lsh && !has_pq && !has_norms && !g.prerotate && !has_rq) return;
   std::ofstream f(path, std::ios::binary | std::ios::app);
   if (!f.is_open()) throw std::runtime_error("save_directional_graph_to_file: cannot reopen " + path);
-  const uint8_t flags =
-      (has_lsh ? 1u : 0u) | (has_pq ? 2u : 0u) | (has_norms ? 4u : 0u) | (g.prerotate ? 8u : 0u);
+  const uint8_t flags = (has_lsh ? 1u : 0u) | (has_pq ? 2u : 0u) | (has_norms ? 4u : 0u) | (g.prerotate ? 8u : 0u) |
+                        (has_rq ? 16u : 0u);
   f.write((const char*)&kTrailerMagic, 4);
   f.write((const char*)&kTrailerVersion, 4);
   f.write((const char*)&flags, 1);
@@ -1620,6 +1833,17 @@ void save_directional_file(const Graph& g, const std::string& path) {
   if (g.prerotate) {
     const uint64_t seed = g.prerotate_seed;
     f.write((const char*)&seed, 8);
+  }
+  if (has_rq) {
+    const RabitqArtifacts& rq = *g.rabitq;
+    f.write((const char*)&rq.dim, 4);
+    f.write((const char*)&rq.code_bytes, 4);
+    std::vector<float> c(rq.dim);
+    hip_check(hipMemcpy(c.data(), rq.centroid, (size_t)rq.dim * 4, hipMemcpyDeviceToHost), "download centroid");
+    f.write((const char*)c.data(), (std::streamsize)c.size() * 4);
+    std::vector<uint8_t> h((size_t)g.n * (rq.code_bytes + 8));
+    hip_check(hipMemcpy(h.data(), rq.nodes, h.size(), hipMemcpyDeviceToHost), "download rabitq nodes");
+    f.write((const char*)h.data(), (std::streamsize)h.size());
   }
   if (!f.good()) throw std::runtime_error("short write while saving " + path);
 }
@@ -1698,6 +1922,23 @@ static void read_directional_trailer(Graph& gr, const std::string& path, uint64_
     if (f.gcount() != 8) throw std::runtime_error("truncated prerotation record in " + path);
     g->prerotate = true;
     g->prerotate_seed = s;
+  }
+  if (flags & 16u) {
+    auto art = std::make_unique<RabitqArtifacts>();
+    f.read((char*)&art->dim, 4);
+    f.read((char*)&art->code_bytes, 4);
+    if (art->dim != g->dim || art->code_bytes != rabitq_code_bytes(g->dim))
+      throw std::runtime_error("RaBitQ trailer does not match the graph in " + path);
+    std::vector<float> c(art->dim);
+    f.read((char*)c.data(), (std::streamsize)c.size() * 4);
+    std::vector<uint8_t> h((size_t)g->n * (art->code_bytes + 8));
+    f.read((char*)h.data(), (std::streamsize)h.size());
+    if ((size_t)f.gcount() != h.size()) throw std::runtime_error("truncated RaBitQ trailer in " + path);
+    hip_check(hipMalloc((void**)&art->centroid, c.size() * 4), "alloc rabitq centroid");
+    hip_check(hipMemcpy(art->centroid, c.data(), c.size() * 4, hipMemcpyHostToDevice), "upload rabitq centroid");
+    hip_check(hipMalloc(&art->nodes, h.size()), "alloc rabitq nodes");
+    hip_check(hipMemcpy(art->nodes, h.data(), h.size(), hipMemcpyHostToDevice), "upload rabitq nodes");
+    g->rabitq = std::move(art);
   }
   return;
 }

@@ -37,6 +37,18 @@ struct PqArtifacts {
   ~PqArtifacts();
 };
 
+// RaBitQ one-bit codes of the stored rows, in the reference's node layout
+// (rabitq_data_store<float>, rabitq/layout.cuh:43-143: code bytes =
+// ceil(dim/8) rounded up to 4, bits LSB-first, then f_add and f_rescale),
+// taken against `centroid` (the mean of the stored rows) with no further
+// rotation: on a prerotated graph the rows already went through P^T.
+struct RabitqArtifacts {
+  uint32_t dim = 0, code_bytes = 0;
+  void* nodes = nullptr;             // device [n, code_bytes + 8]
+  float* centroid = nullptr;         // device [dim]
+  ~RabitqArtifacts();
+};
+
 // (constexpr: usable in host and device code)
 constexpr uint32_t pq_group_width(uint32_t m) { return m <= 4 ? 4u : m <= 8 ? 8u : 16u; }
 constexpr uint32_t pq_groups(uint32_t m) { return (m + pq_group_width(m) - 1) / pq_group_width(m); }

@@ -25,6 +25,11 @@ void build_lsh(Graph& g, int64_t n_samples, uint64_t seed);
 // m = number of subspaces (0: the config's k_ranks, as the reference, whose
 // pq_m equals k_ranks); any m dividing the padded dim, up to kPqMaxM.
 void build_pq(Graph& g, int64_t n_train, int64_t iters, uint64_t seed, uint32_t m = 0);
+// RaBitQ one-bit codes of the stored rows (the reference's quantizer,
+// rabitq/quantize.cuh:322-354, on the rows as stored) against their mean.
+void build_rabitq(Graph& g);
+// directional estimators (jasperx_directional_search_ex's estimator id)
+constexpr int kEstLsh = 0, kEstPq = 1, kEstRabitq = 2;
 // option flags of jasperx_directional_search_ex
 constexpr uint32_t kDirUnique = 1u;
 constexpr uint32_t kDirFlagsKnown = kDirUnique;
@@ -32,24 +37,24 @@ constexpr uint32_t kDirFlagsKnown = kDirUnique;
 // stats (optional, device [nq * 3]): per query visits, hops expanded and
 // adjacency entries read. unique: skip pops of ids already in the frontier,
 // so the k results are distinct (an extension; the reference re-visits them).
-void directional_search(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+void directional_search(Graph& g, int est, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                         float* out_dists, int64_t k, int64_t bw, int64_t limit, bool print, hipStream_t stream,
                         uint32_t* stats = nullptr, bool unique = false);
 // Device scratch bytes a directional search of nq queries takes (query
 // rows, their rotation, PQ tables).
-size_t directional_scratch_bytes(const Graph& g, bool use_pq, int64_t nq);
+size_t directional_scratch_bytes(const Graph& g, int est, int64_t nq);
 // The same search with its scratch carved from [scratch_base,
 // scratch_base + scratch_bytes): it allocates nothing and throws before
 // launching anything when the call needs more. Queries must be device
 // memory; there is no print_throughput and no work counters.
-void directional_search_fixed(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
+void directional_search_fixed(Graph& g, int est, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,
                               float* out_dists, int64_t k, int64_t bw, int64_t limit, bool unique, hipStream_t stream,
                               void* scratch_base, size_t scratch_bytes);
 // directional_search_fixed on a static device scratch of
 // directional_noalloc_scratch_bytes() per GPU (no allocation at all). Calls
 // that overlap on one GPU share that scratch and race.
 size_t directional_noalloc_scratch_bytes();
-void directional_search_noalloc(Graph& g, bool use_pq, const void* queries, int64_t nq, int64_t dim,
+void directional_search_noalloc(Graph& g, int est, const void* queries, int64_t nq, int64_t dim,
                                 int32_t* out_ids, float* out_dists, int64_t k, int64_t bw, int64_t limit,
                                 bool unique, hipStream_t stream);
 // The query rows the directional kernels read (padded, rotated when the

@@ -170,6 +170,7 @@ void Graph::release() {
   vector_norms = nullptr;
   lsh.reset();
   pq.reset();
+  rabitq.reset();
 }
 
 // out = {non-integer flag, min, max} over fp16 values (infinities and NaN

@@ -61,6 +61,7 @@ struct Graph {
   std::unique_ptr<RotationMatrix> rotation;  // prerotation (MFMA layout)
   std::unique_ptr<LshArtifacts> lsh;
   std::unique_ptr<PqArtifacts> pq;
+  std::unique_ptr<RabitqArtifacts> rabitq;
   float* vector_norms = nullptr;  // [n] ||x||^2
 
   Graph();

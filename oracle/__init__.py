@@ -99,7 +99,10 @@ def lib():
         _lib.jo_directional_search.argtypes = [i32, P, i64, i32, P, P, i32, P, i32,
                                                i32, i32, P, f32, P,
                                                i32, i32, P, P, P,
+                                               i32, P, P,
                                                P, i64, ctypes.c_uint32, i32, i32, i32, i32, P, P, P, P, P, P, i32, i32]
+        _lib.jo_rq_estimates.restype = None
+        _lib.jo_rq_estimates.argtypes = [P, i64, i32, P, i32, P, i64, i32, P, P, P, P]
         _lib.jo_populate_lsh.restype = None
         _lib.jo_populate_lsh.argtypes = [P, i64, i32, P, P, i32, i32, i32, P, i32]
         _lib.jo_lsh_globals.restype = i64
@@ -523,12 +526,15 @@ def build_pq(g: OracleGraph, M: int, n_train: int = 40000, iters: int = 12, seed
 
 def directional_search(g: OracleGraph, queries, lsh: LshArtifacts | None = None, pq: PqArtifacts | None = None,
                        k: int = 10, beam_width: int = 64, limit: int | None = None, max_result: int = 2048,
-                       get_visited: bool = False, unique: bool = False, nthreads: int = 0):
-    """graph_beam_search_kernel (graph_beam_search.cuh:55-270) with the LSH or
-    PQ estimator; returns (ids, dists[, visited ids, visited dists, counts]).
-    unique=True is this build's extension: pops of a node already in the
-    frontier are skipped, so the results hold distinct ids."""
-    assert (lsh is None) != (pq is None)
+                       get_visited: bool = False, unique: bool = False, nthreads: int = 0,
+                       rq: "RqArtifacts | None" = None):
+    """graph_beam_search_kernel (graph_beam_search.cuh:55-270) with the LSH,
+    PQ or RaBitQ estimator; returns (ids, dists[, visited ids, visited dists,
+    counts]). unique=True is this build's extension: pops of a node already
+    in the frontier are skipped, so the results hold distinct ids. The
+    RaBitQ estimator is this build's too (directional_oracle.cpp, rq_estimate)."""
+    assert sum(a is not None for a in (lsh, pq, rq)) == 1
+    mode = 0 if lsh is not None else (1 if pq is not None else 2)
     q16 = queries if (isinstance(queries, np.ndarray) and queries.dtype == np.uint16) else as_padded_f16(queries)
     nq = q16.shape[0]
     if limit is None:
@@ -542,10 +548,12 @@ def directional_search(g: OracleGraph, queries, lsh: LshArtifacts | None = None,
         vc = np.zeros(nq, dtype=np.uint32)
     L = lsh or LshArtifacts(0, 1, np.zeros(1, np.float32), 1.0, np.zeros(1, np.uint8))
     Q = pq or PqArtifacts(0, 0, np.zeros(1, np.float32), np.zeros(1, np.uint8), np.zeros(1, np.float32))
-    lib().jo_directional_search(0 if lsh is not None else 1, _ptr(g.vecs16), g.n, g.dp, _ptr(g.edges),
+    Z = rq or RqArtifacts(0, np.zeros(1, np.uint8), np.zeros(1, np.float32))
+    lib().jo_directional_search(mode, _ptr(g.vecs16), g.n, g.dp, _ptr(g.edges),
                                 _ptr(g.counts), g.R, _ptr(g.deleted_bits), metric_code(g.distance),
                                 L.K, L.pbytes, _ptr(L.c_per_rank), ctypes.c_float(L.norm_denom), _ptr(L.rows),
                                 Q.M, Q.dsub, _ptr(Q.centroids), _ptr(Q.codes), _ptr(Q.norms),
+                                Z.dim, _ptr(Z.nodes), _ptr(Z.centroid),
                                 _ptr(q16), nq, g.medoid, k, beam_width, limit, max_result, _ptr(ids), _ptr(d),
                                 _ptr(vi), _ptr(vd), _ptr(vc), None, 1 if unique else 0, nthreads)
     out = (ids, d)
@@ -588,6 +596,33 @@ def rabitq_quantize(x, P, centroid=None, metric: str = "l2", nthreads: int = 0, 
     f_rescale = np.ascontiguousarray(out[:, cb + 4:cb + 8]).view(np.float32).ravel()
     r = (out, out[:, :cb].copy(), f_add, f_rescale)
     return r + (res,) if return_residuals else r
+
+
+class RqArtifacts:
+    """RaBitQ one-bit codes of a graph's stored rows: nodes u8 [n,
+    code_bytes + 8] (code, f_add, f_rescale) taken against centroid f32
+    [dim]."""
+
+    def __init__(self, dim, nodes, centroid):
+        self.dim = int(dim)
+        self.nodes = np.ascontiguousarray(nodes, dtype=np.uint8)
+        self.centroid = np.ascontiguousarray(centroid, dtype=np.float32)
+
+
+def rq_estimates(rq: RqArtifacts, queries16: np.ndarray, metric: str = "l2", with_factors: bool = False):
+    """The RaBitQ estimate of every node for every query row (fp16 bits
+    [nq, dp]): f32 [nq, n]; with_factors also returns each query's (sumq,
+    (delta/2, lo/2, g_add), bit planes u32 [nq, 4, 8])."""
+    q16 = np.ascontiguousarray(queries16, dtype=np.uint16)
+    nq, dp = q16.shape
+    n = rq.nodes.shape[0]
+    out = np.zeros((nq, n), dtype=np.float32)
+    sumq = np.zeros(nq, dtype=np.int32)
+    hhg = np.zeros((nq, 3), dtype=np.float32)
+    planes = np.zeros((nq, 4, 8), dtype=np.uint32)
+    lib().jo_rq_estimates(_ptr(rq.nodes), n, rq.dim, _ptr(rq.centroid), metric_code(metric), _ptr(q16), nq, dp,
+                          _ptr(out), _ptr(sumq), _ptr(hhg), _ptr(planes))
+    return (out, sumq, hhg, planes) if with_factors else out
 
 
 # ------------------------------------------------------------- file format --

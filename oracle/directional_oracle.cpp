@@ -207,6 +207,101 @@ struct Pq {
   const float* norms;      // [n]
 };
 
+// RaBitQ one-bit codes of the stored rows, as rabitq_quantize<1> writes them
+// (rabitq/layout.cuh:43-143): per vertex code bytes (bit i = [r_i >= 0],
+// LSB-first, rounded up to 4 bytes) then f_add and f_rescale (fp32), taken
+// against the centroid c (the codes' residuals are r = x - c).
+struct Rq {
+  int dim;
+  uint32_t code_bytes;
+  const uint8_t* nodes;    // [n, code_bytes + 8]
+  const float* centroid;   // [dim]
+};
+
+// The RaBitQ estimator (this build's; the reference stops at the quantizer:
+// rabitq/distance.cuh:1-10 is only the metric enum and RabitqQueryFactor,
+// layout.cuh:146-150, is unused). It is the published one-bit estimator
+// (Gao and Long, SIGMOD 2024) in the factor form the quantizer's f_add and
+// f_rescale encode:
+//   est = f_add + g_add + f_rescale * <b - 1/2, q'>
+// with b the code bits and q' the query row, g_add = ||q' - c||^2 (L2) or
+// -1 - <c, q'> (IP: the estimate is then of -<x, q'>, the IP distance).
+// <b - 1/2, q'> uses the query quantized to 4 bits: lo = min q'_i, delta =
+// (max - lo) / 15, qbar_i = rint((q'_i - lo) / delta) in [0, 15], so that
+//   <b - 1/2, q'> ~ (delta / 2) (2 <b, qbar> - sum qbar) + (lo / 2) (2 |b| - dim)
+// where <b, qbar> = sum_j 2^j popcount(b & plane_j) over the qbar bit planes.
+struct RqQuery {
+  uint32_t planes[4][8];   // plane j, dword w: bit i of dword w is bit j of qbar_(32w + i)
+  int32_t sumq;
+  float hd, hl, g_add;
+};
+
+// g_add's sum runs in the device's order: lane l accumulates i = l, l + 64,
+// ... with an fma chain, then the 64 lane sums meet in the xor butterfly
+// 32, 16, 8, 4, 2, 1 (lane 0's tree).
+RqQuery rq_prepare(const uint16_t* q, const Rq& rq, bool l2) {
+  RqQuery Q{};
+  const int dim = rq.dim;
+  float lo = h2f(q[0]), hi = lo;
+  for (int i = 1; i < dim; ++i) {
+    lo = std::min(lo, h2f(q[i]));
+    hi = std::max(hi, h2f(q[i]));
+  }
+  lo = lo + 0.0f;  // one zero for -0.0 and +0.0
+  hi = hi + 0.0f;
+  const float delta = (hi - lo) / 15.0f;
+  int32_t sumq = 0;
+  for (int i = 0; i < dim; ++i) {
+    uint32_t qb = 0;
+    if (delta > 0.0f) {
+      const float t = std::rint((h2f(q[i]) - lo) / delta);
+      qb = (uint32_t)std::min(15.0f, std::max(0.0f, t));
+    }
+    sumq += (int32_t)qb;
+    for (int j = 0; j < 4; ++j)
+      if ((qb >> j) & 1u) Q.planes[j][i >> 5] |= 1u << (i & 31);
+  }
+  Q.sumq = sumq;
+  Q.hd = 0.5f * delta;
+  Q.hl = 0.5f * lo;
+  float lanes[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int i = l; i < dim; i += 64) {
+      const float qi = h2f(q[i]), ci = rq.centroid[i];
+      if (l2) {
+        const float d = qi - ci;
+        acc = std::fmaf(d, d, acc);
+      } else {
+        acc = std::fmaf(qi, ci, acc);
+      }
+    }
+    lanes[l] = acc;
+  }
+  float half[32];
+  for (int l = 0; l < 32; ++l) half[l] = lanes[l] + lanes[l + 32];
+  const float s = warp32(half);
+  Q.g_add = l2 ? s : -1.0f - s;
+  return Q;
+}
+
+float rq_estimate(const uint8_t* node, const RqQuery& Q, const Rq& rq) {
+  const uint32_t words = rq.code_bytes / 4;
+  int32_t dot = 0, pc = 0;
+  for (uint32_t w = 0; w < words && w < 8; ++w) {
+    uint32_t c;
+    std::memcpy(&c, node + 4 * w, 4);
+    pc += __builtin_popcount(c);
+    for (int j = 0; j < 4; ++j) dot += __builtin_popcount(c & Q.planes[j][w]) << j;
+  }
+  float f_add, f_rescale;
+  std::memcpy(&f_add, node + rq.code_bytes, 4);
+  std::memcpy(&f_rescale, node + rq.code_bytes + 4, 4);
+  const float t1 = (float)(2 * dot - Q.sumq), t2 = (float)(2 * pc - rq.dim);
+  const float ipq = std::fmaf(Q.hd, t1, Q.hl * t2);
+  return std::fmaf(f_rescale, ipq, f_add + Q.g_add);
+}
+
 // frontier_insert_sorted, beam_search_common.cuh:156-185.
 void frontier_insert(std::vector<DEntry>& F, DEntry e, uint32_t k) {
   if (k == 0) return;
@@ -232,7 +327,8 @@ void frontier_insert(std::vector<DEntry>& F, DEntry e, uint32_t k) {
 // expansion; the hop still counts against `limit`), so the results hold
 // distinct ids. The reference re-visits such nodes and re-inserts them into
 // F, which lets one node fill several of the k result slots.
-void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const uint16_t* q, uint32_t medoid,
+void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const Rq* rq, const uint16_t* q,
+                     uint32_t medoid,
                      uint32_t k, uint32_t bw, uint32_t limit, uint32_t max_result, int32_t* out_ids,
                      float* out_d, uint32_t* vis_ids, float* vis_d, uint32_t* vis_count, uint64_t* stats,
                      bool unique) {
@@ -263,6 +359,8 @@ void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const uint16
     }
     if (l2) q_sq = norm_sq(q, g.dp);
   }
+  RqQuery rqq{};
+  if (rq) rqq = rq_prepare(q, *rq, l2);
   uint32_t vc = 0, loop = 0;
   uint64_t hops = 0, visits = 0;
   while (loop <= limit) {
@@ -280,7 +378,7 @@ void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const uint16
     }
     const uint16_t* uv = g.vecs + (size_t)u * g.dp;
     float stored, exact_u = 0.0f, qu_dot = 0.0f;
-    if (lsh) {
+    if (lsh || rq) {
       exact_u = visit_exact(q, uv, g.dp, l2, l2 ? diff.data() : nullptr);
       stored = l2 ? exact_u : -exact_u;
     } else {
@@ -332,6 +430,8 @@ void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const uint16
         const float mag = std::sqrt(mag_sq);
         if (l2) x.dist = std::fmaf(-(2.0f * mag), dot_est, exact_u + mag_sq);
         else x.dist = -std::fmaf(mag, dot_est, exact_u);
+      } else if (rq) {
+        x.dist = rq_estimate(rq->nodes + (size_t)x.id * (rq->code_bytes + 8), rqq, *rq);
       } else {
         const uint8_t* code = pq->codes + (size_t)u * pq->M * g.R;
         float acc = qu_dot;
@@ -438,6 +538,22 @@ void jo_frontier_insert_seq(const float* d, const uint32_t* ids, int m, int k, f
   for (size_t i = 0; i < F.size(); ++i) { out_d[i] = F[i].dist; out_ids[i] = F[i].id; }
   *out_count = (int)F.size();
 }
+// RaBitQ estimates of every node for every query row (test access to the
+// estimator): out[nq, n]; also each query's prepared factors when asked
+// (q_sumq [nq], q_hd_hl_g [nq, 3], q_planes [nq, 4, 8]).
+void jo_rq_estimates(const uint8_t* nodes, int64_t n, int dim, const float* centroid, int metric,
+                     const uint16_t* queries, int64_t nq, int dp, float* out, int32_t* q_sumq, float* q_hd_hl_g,
+                     uint32_t* q_planes) {
+  Rq rq{dim, (((uint32_t)dim + 7u) / 8u + 3u) / 4u * 4u, nodes, centroid};
+  for (int64_t i = 0; i < nq; ++i) {
+    const RqQuery Q = rq_prepare(queries + (size_t)i * dp, rq, metric == 0);
+    if (q_sumq) q_sumq[i] = Q.sumq;
+    if (q_hd_hl_g) { q_hd_hl_g[3 * i] = Q.hd; q_hd_hl_g[3 * i + 1] = Q.hl; q_hd_hl_g[3 * i + 2] = Q.g_add; }
+    if (q_planes) std::memcpy(q_planes + (size_t)i * 32, Q.planes, sizeof(Q.planes));
+    for (int64_t v = 0; v < n; ++v) out[(size_t)i * n + v] = rq_estimate(nodes + (size_t)v * (rq.code_bytes + 8), Q, rq);
+  }
+}
+
 uint16_t jo_hsub(uint16_t a, uint16_t b) { return hsub(a, b); }
 uint16_t jo_hmul(uint16_t a, uint16_t b) { return hmul(a, b); }
 
@@ -451,23 +567,27 @@ void jo_vector_norms(const uint16_t* vecs, int64_t n, int dp, float* out, int nt
   for (int64_t i = 0; i < n; ++i) out[i] = norm_sq(vecs + (size_t)i * dp, dp);
 }
 
-// Batched directional search. mode 0 = LSH, 1 = PQ.
+// Batched directional search. mode 0 = LSH, 1 = PQ, 2 = RaBitQ.
 int jo_directional_search(int mode, const uint16_t* vecs, int64_t n, int dp, const uint32_t* edges,
                           const uint8_t* counts, int R, const uint32_t* deleted, int metric,
                           // LSH
                           int K, int pbytes, const float* c_per_rank, float norm_denom, const uint8_t* lsh_rows,
                           // PQ
                           int M, int dsub, const float* centroids, const uint8_t* codes, const float* norms,
+                          // RaBitQ
+                          int rq_dim, const uint8_t* rq_nodes, const float* rq_centroid,
                           const uint16_t* queries, int64_t nq, uint32_t medoid, int k, int bw, int limit,
                           int max_result, int32_t* out_ids, float* out_d, uint32_t* vis_ids, float* vis_d,
                           uint32_t* vis_counts, uint64_t* stats, int unique, int nthreads) {
   DGraph g{vecs, n, dp, edges, counts, R, deleted, metric};
   Lsh lsh{K, pbytes, c_per_rank, norm_denom, lsh_rows, (size_t)R * K * pbytes + 2 * (size_t)R};
   Pq pq{M, dsub, centroids, codes, norms};
+  Rq rq{rq_dim, rq_dim > 0 ? (((uint32_t)rq_dim + 7u) / 8u + 3u) / 4u * 4u : 0u, rq_nodes, rq_centroid};
   if (nthreads > 0) omp_set_num_threads(nthreads);
 #pragma omp parallel for schedule(dynamic, 2)
   for (int64_t i = 0; i < nq; ++i) {
-    directional_one(g, mode == 0 ? &lsh : nullptr, mode == 1 ? &pq : nullptr, queries + (size_t)i * dp, medoid,
+    directional_one(g, mode == 0 ? &lsh : nullptr, mode == 1 ? &pq : nullptr, mode == 2 ? &rq : nullptr,
+                    queries + (size_t)i * dp, medoid,
                     (uint32_t)k, (uint32_t)bw, (uint32_t)limit, (uint32_t)max_result, out_ids + i * k,
                     out_d + i * k, vis_ids ? vis_ids + i * max_result : nullptr,
                     vis_d ? vis_d + i * max_result : nullptr, vis_counts ? vis_counts + i : nullptr,

@@ -280,3 +280,77 @@ def test_prerotation_recorded_in_file(jasper, oracle_lib, tmp_path):
     assert np.array_equal(g.vecs16, gg.export_vectors())
     g2.free()
     gg.free()
+
+
+# ---------------------------------------------------------------- RaBitQ --
+
+def _rq_case(jasper, tmp_path, x, q, *, R, distance, prerotate, bws):
+    """build_rabitq on a directional graph: the codes are the oracle
+    quantizer's on the stored rows against the stored rows' mean (codes
+    bit-exact, factors within the fp32 reduction-order bound), and
+    rabitq_search returns the oracle traversal's ids and distances bit for
+    bit on the exported codes; a file round trip keeps them."""
+    n, dim = x.shape
+    xt = torch.from_numpy(x.astype(np.float16)).cuda()
+    gg = jasper.Graph.build(xt, n_neighbors=R, distance=distance, build_lsh=True, build_rabitq=True, k_ranks=4,
+                            prerotate=prerotate, lsh_samples=2000)
+    rows = gg.export_vectors()
+    stored = rows.view(np.float16)[:, :dim].astype(np.float32)
+    cent, nodes = gg.export_rabitq()
+    mean = stored.astype(np.float64).mean(0)
+    assert np.abs(cent - mean).max() <= 1e-5 * (np.abs(mean).max() + 1.0)
+    ref_nodes, ref_codes, ref_add, ref_res = oracle.rabitq_quantize(stored, np.eye(dim, dtype=np.float32).ravel(),
+                                                                    centroid=cent, metric=distance)
+    cb = oracle.rabitq_code_bytes(dim)
+    assert nodes.shape == ref_nodes.shape
+    assert np.array_equal(nodes[:, :cb], ref_codes), "RaBitQ codes differ"
+    f = np.ascontiguousarray(nodes[:, cb:]).view(np.float32)
+    assert np.allclose(f[:, 0], ref_add, rtol=2e-5, atol=1e-5 * np.abs(ref_add).max())
+    assert np.allclose(f[:, 1], ref_res, rtol=2e-5)
+
+    path = tmp_path / "rq.bin"
+    gg.save(str(path))
+    g = oracle.load_graph(path, dim, R, distance)
+    rq = oracle.RqArtifacts(dim, nodes, cent)
+    q_rows = gg.directional_query_rows(torch.from_numpy(q.astype(np.float16)).cuda())
+    qt = torch.from_numpy(np.ascontiguousarray(q.astype(np.float16))).cuda()
+    out = {}
+    for bw in bws:
+        for unique in (False, True):
+            ids, d = gg.rabitq_search(qt, k=10, beam_width=bw, unique=unique)
+            torch.cuda.synchronize()
+            ids, d = ids.cpu().numpy(), d.cpu().numpy()
+            rid, rd = oracle.directional_search(g, q_rows, rq=rq, k=10, beam_width=bw, unique=unique)
+            msg = compare_search(ids, d, rid, rd)
+            assert msg is None, f"rabitq bw={bw} unique={unique}: {msg}"
+            out[(bw, unique)] = (ids, d)
+    g2 = jasper.Graph.load(str(path), dim=dim, n_neighbors=R, distance=distance, k_ranks=4, prerotate=prerotate)
+    assert g2._has_rabitq and g2._has_lsh
+    c2, n2 = g2.export_rabitq()
+    assert np.array_equal(c2.view(np.uint32), cent.view(np.uint32)) and np.array_equal(n2, nodes)
+    for (bw, unique), (ids, d) in out.items():
+        ids2, d2 = g2.rabitq_search(qt, k=10, beam_width=bw, unique=unique)
+        torch.cuda.synchronize()
+        assert compare_search(ids2.cpu().numpy(), d2.cpu().numpy(), ids, d) is None
+    g2.free()
+    gg.free()
+
+
+def test_rabitq_l2_prerotated(jasper, oracle_lib, tmp_path):
+    x = integer_clustered(3000, 128, 50)
+    q = integer_clustered(40, 128, 51)
+    _rq_case(jasper, tmp_path, x, q, R=64, distance="l2", prerotate=True, bws=(16, 64, 160))
+
+
+def test_rabitq_ip_d96(jasper, oracle_lib, tmp_path):
+    # d = 96: 12 code bytes, 20-byte nodes (4-byte aligned only)
+    x = unit(2500, 96, 52)
+    q = unit(32, 96, 53)
+    _rq_case(jasper, tmp_path, x, q, R=32, distance="ip", prerotate=True, bws=(32, 96))
+
+
+def test_rabitq_l2_d200_unrotated(jasper, oracle_lib, tmp_path):
+    # d = 200: 28 code bytes (seven code words, the eight-word kernel)
+    x = gaussian(2000, 200, 54)
+    q = gaussian(32, 200, 55)
+    _rq_case(jasper, tmp_path, x, q, R=32, distance="l2", prerotate=False, bws=(32,))

@@ -120,3 +120,111 @@ def test_reference_quantizer_properties():       # test_rabitq.cu:264-440
     _, _, fa_l2, _ = oracle.rabitq_quantize(x, eye, metric="l2")
     _, _, fa_ip, _ = oracle.rabitq_quantize(x, eye, metric="ip")
     assert np.any(np.abs(fa_l2 - fa_ip) > 1e-6)
+
+
+# ------------------------------------------------ the one-bit RaBitQ estimator
+# (this build's; the reference stops at the quantizer). Pinned by closed
+# forms where every step is exact, by properties of the 4-bit query, and by
+# its statistics against exact distances.
+
+def _sign_case(dim, metric, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.choice([-1.0, 1.0], size=(300, dim)).astype(np.float32)
+    nodes, codes, f_add, f_rescale = oracle.rabitq_quantize(x, np.eye(dim, dtype=np.float32).ravel(),
+                                                             metric=metric)
+    # integer queries spanning exactly [-7, 8]: delta = 1, lo = -7, qbar = q + 7
+    q = rng.integers(-7, 9, size=(12, dim)).astype(np.float32)
+    q[:, 0], q[:, 1] = -7.0, 8.0
+    rq = oracle.RqArtifacts(dim, nodes, np.zeros(dim, np.float32))
+    return x, q, rq, f_add, f_rescale
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+@pytest.mark.parametrize("dim", [16, 64, 256])
+def test_estimate_exact_on_sign_vectors(metric, dim):
+    """x in {-1, +1}^dim, zero centroid, dim a perfect square: f_add = dim
+    (L2) or 1 (IP), f_rescale = -4 (L2) or -2 (IP) exactly; integer queries
+    in [-7, 8] are exact at 4 bits; every term of the estimate is then an
+    exact fp32 value and it equals the exact distance: ||x - q||^2 (L2),
+    -<x, q> (IP)."""
+    x, q, rq, f_add, f_rescale = _sign_case(dim, metric, dim)
+    if metric == "l2":
+        assert (f_add == dim).all() and (f_rescale == -4.0).all()
+    else:
+        assert (f_add == 1.0).all() and (f_rescale == -2.0).all()
+    est, sumq, hhg, planes = oracle.rq_estimates(rq, oracle.as_padded_f16(q), metric, with_factors=True)
+    assert (hhg[:, 0] == 0.5).all() and (hhg[:, 1] == -3.5).all()
+    assert np.array_equal(sumq, (q + 7).sum(1).astype(np.int32))
+    xd, qd = x.astype(np.float64), q.astype(np.float64)
+    exact = ((qd[:, None, :] - xd[None]) ** 2).sum(-1) if metric == "l2" else -(qd @ xd.T)
+    assert np.array_equal(est.astype(np.float64), exact)
+
+
+def test_query_bit_planes():
+    """Plane j holds bit j of qbar_i at dword i // 32, bit i % 32."""
+    x, q, rq, _, _ = _sign_case(64, "l2", 3)
+    _, _, _, planes = oracle.rq_estimates(rq, oracle.as_padded_f16(q), "l2", with_factors=True)
+    qbar = (q + 7).astype(np.int64)
+    for r in range(len(q)):
+        for j in range(4):
+            for i in range(64):
+                assert ((int(planes[r, j, i // 32]) >> (i % 32)) & 1) == ((qbar[r, i] >> j) & 1)
+        assert not planes[r, :, 2:].any()
+
+
+def test_query_quantization_properties():
+    """Real-valued queries: qbar in [0, 15] with lo + delta * qbar within
+    delta / 2 (plus rounding) of q; sumq = sum qbar; g_add = ||q - c||^2 to
+    fp32 accuracy."""
+    rng = np.random.default_rng(4)
+    dim = 100
+    q = rng.standard_normal((20, dim)).astype(np.float16).astype(np.float32)
+    c = rng.standard_normal(dim).astype(np.float32)
+    nodes, *_ = oracle.rabitq_quantize(rng.standard_normal((5, dim)).astype(np.float32),
+                                       np.eye(dim, dtype=np.float32).ravel())
+    rq = oracle.RqArtifacts(dim, nodes, c)
+    _, sumq, hhg, planes = oracle.rq_estimates(rq, oracle.as_padded_f16(q), "l2", with_factors=True)
+    for r in range(len(q)):
+        qbar = np.zeros(dim, np.int64)
+        for j in range(4):
+            bits = np.array([(int(planes[r, j, i // 32]) >> (i % 32)) & 1 for i in range(dim)])
+            qbar |= bits << j
+        delta, lo = 2.0 * hhg[r, 0], 2.0 * hhg[r, 1]
+        assert lo == q[r].min() and abs(delta - (q[r].max() - lo) / 15) <= 1e-6 * abs(delta)
+        assert qbar.min() == 0 and qbar.max() == 15 and sumq[r] == qbar.sum()
+        assert np.abs(lo + delta * qbar - q[r]).max() <= 0.5 * delta * (1 + 1e-5)
+        g = ((q[r].astype(np.float64) - c) ** 2).sum()
+        assert abs(hhg[r, 2] - g) <= 1e-5 * g
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_estimate_tracks_exact_distance(metric):
+    """On rotated Gaussian data with the data mean as centroid the estimate
+    is unbiased and its error has the one-bit estimator's known scale: the
+    estimate of <r^, q^> has standard deviation sqrt(1 - a^2) / a / sqrt(dim)
+    with a = <x_bar, r^> ~ 0.8 (about 0.75 / sqrt(dim)), so in units of
+    ||x - c|| ||q - c|| / sqrt(dim) the error of -2<r, q_r> (L2) is ~1.5 and
+    of -<r, q'> (IP) ~0.75. A lost rescale factor or a wrong sign fails it."""
+    rng = np.random.default_rng(5)
+    dim = 128
+    P = oracle.rotation_matrix(dim, 42)[0]
+    x = rng.standard_normal((2000, dim)).astype(np.float32)
+    q = rng.standard_normal((40, dim)).astype(np.float32)
+    Pm = colmajor_to_P(P, dim)
+    xr = (x.astype(np.float64) @ Pm).astype(np.float16).astype(np.float32)    # rows P^T x
+    qr = (q.astype(np.float64) @ Pm).astype(np.float16).astype(np.float32)
+    if metric == "ip":
+        xr /= np.linalg.norm(xr, axis=1, keepdims=True)
+        qr /= np.linalg.norm(qr, axis=1, keepdims=True)
+        xr, qr = xr.astype(np.float16).astype(np.float32), qr.astype(np.float16).astype(np.float32)
+    c = xr.mean(0).astype(np.float32)
+    nodes, *_ = oracle.rabitq_quantize(xr, np.eye(dim, dtype=np.float32).ravel(), centroid=c, metric=metric)
+    est = oracle.rq_estimates(oracle.RqArtifacts(dim, nodes, c), oracle.as_padded_f16(qr), metric).astype(np.float64)
+    xd, qd = xr.astype(np.float64), qr.astype(np.float64)
+    exact = ((qd[:, None, :] - xd[None]) ** 2).sum(-1) if metric == "l2" else -(qd @ xd.T)
+    err = est - exact
+    scale = (np.linalg.norm(qd - c, axis=1)[:, None] * np.linalg.norm(xd - c, axis=1)[None]) / np.sqrt(dim)
+    f = 2.0 if metric == "l2" else 1.0
+    assert abs(err.mean()) < 0.02 * scale.mean()
+    assert 0.6 * f < np.sqrt((err ** 2).mean()) / scale.mean() < 0.9 * f
+    assert np.corrcoef(est.ravel(), exact.ravel())[0, 1] > 0.75

@@ -2,8 +2,8 @@
 allocates nothing (its scratch is a static device buffer of 64 MiB per GPU).
 
 Called through the C ABI, it must return exactly what the allocating
-jasperx_directional_search_ex returns for the same graph and queries: LSH and
-PQ estimators on a prerotated graph (so the rotated query rows live in the
+jasperx_directional_search_ex returns for the same graph and queries: LSH, PQ
+and RaBitQ estimators on a prerotated graph (so the rotated query rows live in the
 scratch too), two calls in a row with the second on fewer queries (the
 buffer keeps the first call's contents), and the unique flag. A call whose
 scratch would exceed the buffer is rejected with a clear error.
@@ -35,10 +35,11 @@ def test_noalloc_matches_allocating_search(jasper):
     dim = 120                                                   # padded to 120: rows need no padding kernel work
     x = gaussian(3000, dim, 91)
     g = jasper.Graph.build(torch.from_numpy(x).cuda(), n_neighbors=32, build_lsh=True, build_pq=True, k_ranks=4,
-                           prerotate=True, lsh_samples=4000, pq_train=3000, pq_kmeans_iter=3, pq_m=24)
+                           prerotate=True, lsh_samples=4000, pq_train=3000, pq_kmeans_iter=3, pq_m=24,
+                           build_rabitq=True)
     for nq in (1500, 300):                                      # the second call is smaller
         q = torch.from_numpy(gaussian(nq, dim, 92 + nq)).cuda()
-        for use_pq in (0, 1):
+        for use_pq in (0, 1, 2):                                # estimators: LSH, PQ, RaBitQ
             for flags in (0, 1):
                 want = _call(jasper, "jasperx_directional_search_ex", g, use_pq, q, 10, 48, flags)
                 got = _call(jasper, "jasperx_directional_search_noalloc", g, use_pq, q, 10, 48, flags)
