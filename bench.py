@@ -370,7 +370,7 @@ def run_directional(args, torch, jasper_amd, datasets, dev, log, use_pq=False):
     ids, _ = fn(q_t, k=10, beam_width=chosen)
     rec = _recall(gt, ids.cpu().numpy())
     st = g.directional_stats(q_t, k=10, beam_width=chosen, pq=use_pq).astype(np.int64)
-    plain = _plain_curve(torch, jasper_amd, base_t, q_t, gt, "ip", (32, 64, 128), log, "c3")
+    plain = _sweep(torch, g.exact_search, q_t, gt, (32, 64, 128, 256), log, "c3 exact search on the graph")
     dp, R = 96, 64
     visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
     # per edge: PQ reads M = 4 code bytes (IP: no norm gather); LSH K*P + 2 = 6 (u8 words + bf16 m^2)
@@ -383,7 +383,7 @@ def run_directional(args, torch, jasper_amd, datasets, dev, log, use_pq=False):
                 {"workload": f"config 3: {n} x {dim} unit-norm N(0,1) fp16, IP, R=64 alpha=1.2, "
                              f"{'PQ M=4' if use_pq else 'LSH k_ranks=4 u8 words'}, prerotate, {nq} queries, k=10",
                  "beam_width": chosen, "recall_at_10": rec, "build_s": build_s,
-                 "build_vectors_per_s": n / build_s, "curve": curve, "curve_plain_graph": plain},
+                 "build_vectors_per_s": n / build_s, "curve": curve, "curve_exact_search": plain},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
                  "traffic": None, "kernel": f"directional_kernel<IP,{'PQ' if use_pq else 'LSH'}>",
                  "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
@@ -449,28 +449,54 @@ def run_rabitq(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
+def _sweep(torch, fn, queries, gt, bws, log, tag, **kw):
+    nq = queries.size(0)
+    out = []
+    for bw in bws:
+        run = lambda bw=bw: fn(queries, k=10, beam_width=bw, **kw)
+        ids, _ = run()
+        r = _recall(gt, ids.cpu().numpy())
+        wall, _, _ = _timed(torch, run, 3, 1)
+        out.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0), **kw})
+        log(f"{tag} bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
+    return out
+
+
 def run_c5(args, torch, jasper_amd, datasets, dev, log):
     """Config 5: 100M x 128 clustered integer vectors (10,000 clusters)
-    generated in HBM, R=64, alpha=1.2, prerotated, LSH k_ranks=16 (u8 words),
-    32768 samples; RaBitQ one-bit codes of the base; 10k queries, k=10,
-    directional search, QPS at recall@10 >= 0.9."""
+    generated in HBM, R=64, alpha=1.2, prerotated, RaBitQ one-bit codes for
+    the build's distance estimation (build_search="rabitq": the
+    construction's search pops by the RaBitQ estimate), LSH k_ranks=16 (u8
+    words), 32768 samples; 10k queries, k=10, directional search, QPS at
+    recall@10 >= 0.9 (swept up to the API's beam-width limit, 1983). Beside
+    it: the exact (reference) construction of the same rows, and the exact
+    beam search on both graphs (what each graph allows without an
+    estimator)."""
     n, nq, dim = args.c5_n, args.nq, 128
     t0 = time.perf_counter()
     base = datasets.clustered_device(n, dim, 0, dev)
     queries = datasets.clustered_device(nq, dim, 1, dev)
     torch.cuda.synchronize()
     log(f"c5 data {n} x {dim} generated in HBM in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    gt_ids, _ = jasper_amd.bruteforce_knn(base, queries, 10, "l2")
+    gt = gt_ids.cpu().numpy()
+    log(f"c5 ground truth {time.perf_counter() - t0:.1f}s")
     cfg = jasper_amd._resolve_directional_config(jasper_amd.DataType.FLOAT16, 64, jasper_amd.DistanceFunc.L2,
                                                   16, dim)
     stream = jasper_amd._stream_ptr(dev)
+    budget = jasper_amd.parse_storage_size("10GB")
+    exact_bws = (64, 128, 256, 384, 512)
+
+    # config 5 as configured: RaBitQ build search, then the LSH artifacts
     t0 = time.perf_counter()
-    handle = jasper_amd._op("construct_directional", cfg)(
-        jasper_amd._tensor_ptr(base), n, dim, 1.2, jasper_amd.parse_storage_size("10GB"), False, True, 42, stream)
+    handle = jasper_amd._agnostic("jasperx_construct_directional_ex")(
+        cfg.encode(), jasper_amd._tensor_ptr(base), n, dim, 1.2, budget, False, True, 42, 1, stream)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
     bst = jasper_amd.last_build_stats()
-    log(f"c5 construct (prerotation + Vamana) {build_s:.1f}s = {n / build_s:,.0f} vec/s, "
-        f"batches={int(bst['batches'])} max_batch={int(bst['max_batch'])}")
+    log(f"c5 construct with the RaBitQ build search (prerotation + codes + Vamana) {build_s:.1f}s = "
+        f"{n / build_s:,.0f} vec/s, batches={int(bst['batches'])} max_batch={int(bst['max_batch'])}")
     t0 = time.perf_counter()
     jasper_amd._op("build_lsh", cfg)(handle, 32768, 42)
     torch.cuda.synchronize()
@@ -478,33 +504,19 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
     log(f"c5 LSH artifacts {lsh_s:.1f}s")
     g = jasper_amd.Graph(handle, cfg, jasper_amd.DataType.FLOAT16, jasper_amd.DistanceFunc.L2, 64, dim,
                          is_directional=True, k_ranks=16, has_lsh=True, has_pq=False, prerotate=True,
-                         prerotate_seed=42)
-    rot = torch.from_numpy(jasper_amd.rotation_matrix(dim, 42)).to(dev)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    codes = jasper_amd.rabitq_quantize(base, rotation=rot)
-    torch.cuda.synchronize()
-    rabitq_s = time.perf_counter() - t0
-    del codes
-    log(f"c5 RaBitQ one-bit codes {rabitq_s:.2f}s")
-    t0 = time.perf_counter()
-    gt_ids, _ = jasper_amd.bruteforce_knn(base, queries, 10, "l2")
-    gt = gt_ids.cpu().numpy()
-    log(f"c5 ground truth {time.perf_counter() - t0:.1f}s")
+                         prerotate_seed=42, has_rabitq=True)
     free, total = torch.cuda.mem_get_info()
-    # reference traversal (repeats ids, cannot reach the target here) and the
-    # distinct-results traversal (unique=True, an extension)
+    exact_rq = _sweep(torch, g.exact_search, queries, gt, exact_bws, log, "c5 rabitq-built graph, exact search")
     curve, chosen = [], None
-    for unique, bws in ((False, [32, 64, 128, 256]), (True, [32, 64, 96, 128, 192, 256, 384, 512])):
-        for bw in bws:
-            run = lambda bw=bw, unique=unique: g.directional_search(queries, k=10, beam_width=bw, unique=unique)
-            ids, _ = run()
-            r = _recall(gt, ids.cpu().numpy())
-            wall, ev, _ = _timed(torch, run, 3, 1)
-            curve.append({"unique": unique, "beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
-            log(f"c5 unique={unique} bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
-            if r >= 0.9 and (chosen is None or curve[-1]["qps"] > chosen["qps"]):
-                chosen = curve[-1]
+    for unique, bws in ((False, [32, 64, 128, 256, 512, 1024]),
+                        (True, [32, 64, 128, 256, 512, 768, 1024, 1536, 1983])):
+        for c in _sweep(torch, g.directional_search, queries, gt, bws, log, f"c5 LSH unique={unique}",
+                        unique=unique):
+            curve.append(c)
+            if c["recall_at_10"] >= 0.9 and (chosen is None or c["qps"] > chosen["qps"]):
+                chosen = c
+    rq_curve = _sweep(torch, g.rabitq_search, queries, gt, [64, 256, 1024], log, "c5 RaBitQ unique=True",
+                      unique=True)
     if chosen is None:
         chosen = max(curve, key=lambda c: c["recall_at_10"])
     bw, unique = chosen["beam_width"], chosen["unique"]
@@ -516,17 +528,32 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
     visits, hops, adj = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
     alg = int(visits * 2 * dim + hops + adj * (4 + 16 + 2) + nq * (2 * dim + 80))
     ach = alg / (ev / 1000.0) / 1e9
+    log(f"c5 LSH bw={bw} unique={unique}: recall {rec:.4f}, {nq / (wall / 1000.0):,.0f} QPS, kernel {ev:.3f} ms, "
+        f"{ach:.0f} GB/s")
     g.free()
-    plain = _c5_plain(args, torch, jasper_amd, base, queries, gt, log)
+
+    # the exact (reference) construction of the same rows
+    t0 = time.perf_counter()
+    handle = jasper_amd._op("construct_directional", cfg)(
+        jasper_amd._tensor_ptr(base), n, dim, 1.2, budget, False, True, 42, stream)
+    torch.cuda.synchronize()
+    exact_build_s = time.perf_counter() - t0
+    log(f"c5 exact construct (prerotation + Vamana) {exact_build_s:.1f}s = {n / exact_build_s:,.0f} vec/s")
+    ge = jasper_amd.Graph(handle, cfg, jasper_amd.DataType.FLOAT16, jasper_amd.DistanceFunc.L2, 64, dim,
+                          is_directional=True, k_ranks=16, prerotate=True, prerotate_seed=42)
+    exact_ex = _sweep(torch, ge.exact_search, queries, gt, exact_bws, log, "c5 exact-built graph, exact search")
+    ge.free()
     res = _line(args, "config 5: build vectors/s (100M x 128 in HBM) and QPS @ recall@10>=0.9, directional LSH",
                 nq / (wall / 1000.0), "queries/s", wall, "f16",
                 {"workload": f"config 5: {n} x {dim} clustered integer fp16 (10,000 clusters, generated in HBM), "
-                             "R=64 alpha=1.2, prerotate, LSH k_ranks=16 u8 words, 32768 samples, "
-                             f"{nq} queries, k=10",
+                             "R=64 alpha=1.2, prerotate, RaBitQ build search, LSH k_ranks=16 u8 words, "
+                             f"32768 samples, {nq} queries, k=10",
                  "build_vectors_per_s": n / build_s, "build_s": build_s, "lsh_s": lsh_s,
-                 "rabitq_vectors_per_s": n / rabitq_s, "build_max_batch": int(bst["max_batch"]),
+                 "build_max_batch": int(bst["max_batch"]),
+                 "exact_build_vectors_per_s": n / exact_build_s, "exact_build_s": exact_build_s,
                  "beam_width": bw, "unique": unique, "recall_at_10": rec, "target_recall": 0.9,
-                 "curve": curve, "hbm_used_gb": (total - free) / 1e9, "plain_search": plain},
+                 "curve": curve, "curve_rabitq_search": rq_curve, "curve_exact_search_rabitq_built": exact_rq,
+                 "curve_exact_search_exact_built": exact_ex, "hbm_used_gb": (total - free) / 1e9},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
                  "traffic": None, "kernel": "directional_kernel<L2,LSH>", "kernel_ms": ev,
                  "algorithmic_bytes_per_launch": alg,
@@ -536,71 +563,14 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
-def _c5_plain(args, torch, jasper_amd, base, queries, gt, log):
-    """The same 100M base as a plain graph (Graph.build + search, no
-    prerotation): build vectors/s and the smallest swept beam width whose
-    recall@10 reaches 0.9, with its QPS and HBM roofline."""
-    n, nq = base.size(0), queries.size(0)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2)
-    torch.cuda.synchronize()
-    build_s = time.perf_counter() - t0
-    log(f"c5 plain build {build_s:.1f}s = {n / build_s:,.0f} vec/s")
-    curve, chosen = [], None
-    for bw in (32, 64, 128, 192, 256, 384, 512, 768, 1024):
-        ids, _ = g.search(queries, k=10, beam_width=bw)
-        r = _recall(gt, ids.cpu().numpy())
-        wall, ev, _ = _timed(torch, lambda bw=bw: g.search(queries, k=10, beam_width=bw), 3, 1)
-        curve.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
-        log(f"c5 plain bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
-        if r >= 0.9:
-            chosen = bw
-            break
-    if chosen is None:
-        chosen = max(curve, key=lambda c: c["recall_at_10"])["beam_width"]
-    wall, ev, _ = _timed(torch, lambda: g.search(queries, k=10, beam_width=chosen), args.steps, args.warmup)
-    ids, _ = g.search(queries, k=10, beam_width=chosen)
-    rec = _recall(gt, ids.cpu().numpy())
-    st = g.search_stats(queries, k=10, beam_width=chosen).astype(np.int64)
-    alg = algorithmic_bytes(st, 128, nq)
-    ach = alg / (ev / 1000.0) / 1e9
-    log(f"c5 plain bw={chosen}: recall={rec:.4f} qps={nq / (wall / 1000.0):,.0f} kernel {ev:.3f} ms "
-        f"{ach:.0f} GB/s")
-    g.free()
-    return {"build_s": build_s, "build_vectors_per_s": n / build_s, "beam_width": chosen, "recall_at_10": rec,
-            "qps": nq / (wall / 1000.0), "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
-            "achieved_gbs": ach, "frac": ach / PEAK_HBM_GBS, "curve": curve}
-
-
-def _plain_curve(torch, jasper_amd, base, queries, gt, distance, bws, log, tag):
-    """Recall of the plain beam search on a plain Vamana graph of the same
-    rows (no estimator), to separate what the graph allows from what the
-    directional estimator finds."""
-    t0 = time.perf_counter()
-    pg = jasper_amd.Graph.build(base, n_neighbors=64, distance=distance, alpha=1.2)
-    torch.cuda.synchronize()
-    log(f"{tag} plain graph built in {time.perf_counter() - t0:.1f}s")
-    nq = queries.size(0)
-    curve = []
-    for bw in bws:
-        ids, _ = pg.search(queries, k=10, beam_width=bw)
-        r = _recall(gt, ids.cpu().numpy())
-        wall, _, _ = _timed(torch, lambda bw=bw: pg.search(queries, k=10, beam_width=bw), 3, 1)
-        curve.append({"beam_width": bw, "recall_at_10": r, "qps": nq / (wall / 1000.0)})
-        log(f"{tag} plain search bw={bw} recall={r:.4f} qps={nq / (wall / 1000.0):,.0f}")
-    pg.free()
-    return curve
-
-
 def run_c4(args, torch, jasper_amd, datasets, dev, log):
     """Config 4: 1M x 960 non-negative sparse vectors (|N(0,1)| * 0.05, 192
     dims zeroed per row) generated in HBM, L2, R=64, alpha=1.2, PQ with
     8-bit codebooks and one subspace per 8 dims (M = 120, --c4-m), prerotated
     (the Python default with build_pq); 1,000 queries, k=10, pq_search at
     bw=64. Also: the same graph's PQ retrained at M = 16 (the largest the
-    reference's configs offer), and the plain search on a plain graph of the
-    same rows."""
+    reference's configs offer), and the exact beam search on the graph (what
+    it allows without an estimator)."""
     n, nq, dim = args.n, min(args.nq, 1000), 960
     M = args.c4_m
     base = datasets.sparse_abs_device(n, dim, 0, dev)
@@ -650,14 +620,14 @@ def run_c4(args, torch, jasper_amd, datasets, dev, log):
         torch.cuda.synchronize()
         log(f"c4 PQ retrained at M=16 in {time.perf_counter() - t0:.1f}s")
         m16 = sweep("M=16", (64, 256))
-    plain = _plain_curve(torch, jasper_amd, base, queries, gt, "l2", (32, 64, 128), log, "c4")
+    plain = _sweep(torch, g.exact_search, queries, gt, (32, 64, 128, 256), log, "c4 exact search on the graph")
     res = _line(args, "config 4: QPS @ bw=64 and build vectors/s, PQ-ADC directional search (1M x 960, L2)",
                 nq / (wall / 1000.0), "queries/s", wall, "f16",
                 {"workload": f"config 4: {n} x {dim} |N(0,1)|*0.05 with 192 zero dims (generated in HBM), L2, "
                              f"R=64 alpha=1.2, PQ M={M} dsub={dim // M}, prerotate, {nq} queries, k=10, bw=64",
                  "build_vectors_per_s": n / build_s, "build_s": build_s, "build_max_batch": int(bst["max_batch"]),
                  "beam_width": bw, "recall_at_10": rec, "curve": curve, "curve_pq_m16": m16,
-                 "curve_plain_graph": plain},
+                 "curve_exact_search": plain},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
                  "traffic": None, "kernel": f"directional_kernel<L2,PQ{' wide' if M > 16 else ''}>",
                  "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,

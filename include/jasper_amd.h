@@ -196,6 +196,26 @@ int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t
  * reads it back. Otherwise as jasper_build_pq_<cfg> (BuildPq_,
  * ffi/jasper_ffi_common.cuh:507-528). No reference counterpart. */
 int64_t jasperx_build_pq_m(int64_t handle, int64_t m, int64_t n_train, int64_t kmeans_iter, int64_t seed);
+/* The plain beam search (Search_, ffi/jasper_ffi_common.cuh:302-369) on any
+ * graph, directional ones included: exact distances over the stored rows,
+ * the queries padded and, on a prerotated graph, rotated as the directional
+ * search rotates them. It shows what a directional graph allows without an
+ * estimator; the reference offers no search() on directional graphs
+ * (python/jasper/__init__.py:469-475). Outputs as jasper_search_<cfg>. */
+int64_t jasperx_exact_search(int64_t handle, const void* queries, int64_t n_queries, int64_t dim, int32_t* out_ids,
+                             float* out_dists, int64_t k, int64_t beam_width, int64_t limit, void* stream);
+/* jasper_construct_directional_<config> (ConstructDirectionalGraph_,
+ * ffi/jasper_ffi_common.cuh:444-486) with the config named by its id (e.g.
+ * "f16_r64_l2_k16_d128") and option bits; no reference counterpart.
+ * JASPERX_BUILD_RABITQ_SEARCH computes the RaBitQ codes of the stored rows
+ * first (jasperx_build_rabitq) and lets the construction's search stage pop
+ * by the RaBitQ estimate (each popped row is scored exactly, as the plain
+ * build search does); forward prune, grouping and reverse prune are
+ * unchanged. options = 0 is the reference construction. */
+#define JASPERX_BUILD_RABITQ_SEARCH 1u
+int64_t jasperx_construct_directional_ex(const char* config, const void* vectors, int64_t n_vectors, int64_t dim,
+                                         double alpha, int64_t workspace_budget_bytes, bool on_host,
+                                         bool prerotate, int64_t prerotate_seed, uint32_t options, void* stream);
 /* One-bit RaBitQ codes of a directional graph's stored rows (rotated rows
  * when prerotated): the reference's quantizer (rabitq/quantize.cuh:322-354)
  * on the rows as stored, against their mean; they feed the RaBitQ estimator

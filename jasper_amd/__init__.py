@@ -97,6 +97,9 @@ _AGNOSTIC = {
                                   _ptr, _ptr],
     "jasperx_build_pq_m": [_i64, _i64, _i64, _i64, _i64],
     "jasperx_build_rabitq": [_i64],
+    "jasperx_exact_search": [_i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64, _ptr],
+    "jasperx_construct_directional_ex": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, ctypes.c_bool,
+                                         ctypes.c_bool, _i64, ctypes.c_uint32, _ptr],
     "jasperx_export_rabitq": [_i64, _ptr, _ptr],
     "jasperx_directional_search_noalloc": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64,
                                            _i64, ctypes.c_uint32, _ptr],
@@ -309,7 +312,8 @@ class Graph:
               build_pq: bool = False, k_ranks: int = 4, prerotate: bool | None = None,
               prerotate_seed: int = 42, lsh_samples: int = 32768, lsh_seed: int = 42,
               pq_train: int = 40000, pq_kmeans_iter: int = 12, pq_seed: int = 123,
-              pq_m: int | None = None, build_rabitq: bool = False) -> "Graph":
+              pq_m: int | None = None, build_rabitq: bool = False,
+              build_search: str = "exact") -> "Graph":
         """Construct a Vamana graph on the GPU (reference __init__.py:322-428).
 
         pq_m (an extension, no reference counterpart) sets the number of PQ
@@ -317,7 +321,12 @@ class Graph:
         divides the padded dim, up to 128, e.g. 120 for one subspace per 8
         dims at d = 960. build_rabitq (an extension) adds one-bit RaBitQ codes
         of the stored rows for rabitq_search; it makes the graph directional
-        like build_lsh / build_pq."""
+        like build_lsh / build_pq. build_search="rabitq" (an extension) makes
+        the construction's search stage pop by the RaBitQ estimate of the
+        stored rows (their codes are computed first and kept) instead of the
+        exact plain search; "exact" is the reference construction."""
+        if build_search not in ("exact", "rabitq"):
+            raise ValueError(f"build_search must be 'exact' or 'rabitq', got {build_search!r}")
         if isinstance(distance, str):
             distance = DistanceFunc(distance)
         workspace_budget_bytes = parse_storage_size(workspace_budget)
@@ -331,6 +340,8 @@ class Graph:
             raise ValueError(f"Unsupported tensor dtype: {vectors.dtype}. Use torch.float16.")
         n = vectors.size(0)
         stream = _stream_ptr(vectors.device if vectors.is_cuda else None)
+        if build_search == "rabitq":
+            build_rabitq = True
         if not (build_lsh or build_pq or build_rabitq):
             config_id = _resolve_config(data_type, n_neighbors, distance)
             handle = _op("construct", config_id)(_tensor_ptr(vectors), n, dim, float(alpha),
@@ -338,9 +349,14 @@ class Graph:
             return cls(handle, config_id, data_type, distance, n_neighbors, dim)
         config_id = _resolve_directional_config(data_type, n_neighbors, distance, k_ranks, dim)
         resolved_prerotate = prerotate if prerotate is not None else True
-        handle = _op("construct_directional", config_id)(
-            _tensor_ptr(vectors), n, dim, float(alpha), workspace_budget_bytes, on_host,
-            resolved_prerotate, prerotate_seed, stream)
+        if build_search == "rabitq":
+            handle = _agnostic("jasperx_construct_directional_ex")(
+                config_id.encode(), _tensor_ptr(vectors), n, dim, float(alpha), workspace_budget_bytes, on_host,
+                resolved_prerotate, prerotate_seed, 1, stream)
+        else:
+            handle = _op("construct_directional", config_id)(
+                _tensor_ptr(vectors), n, dim, float(alpha), workspace_budget_bytes, on_host,
+                resolved_prerotate, prerotate_seed, stream)
         if build_lsh:
             _op("build_lsh", config_id)(handle, lsh_samples, lsh_seed)
         if build_pq:
@@ -348,7 +364,7 @@ class Graph:
                 _op("build_pq", config_id)(handle, pq_train, pq_kmeans_iter, pq_seed)
             else:
                 _agnostic("jasperx_build_pq_m")(handle, pq_m, pq_train, pq_kmeans_iter, pq_seed)
-        if build_rabitq:
+        if build_rabitq and build_search != "rabitq":
             _agnostic("jasperx_build_rabitq")(handle)
         return cls(handle, config_id, data_type, distance, n_neighbors, dim,
                    is_directional=True, k_ranks=k_ranks, has_lsh=build_lsh, has_pq=build_pq,
@@ -465,6 +481,24 @@ class Graph:
             return self._run_unique(True, queries, k, beam_width, resolved_limit)
         return self._run_search(self._pq_search_fn, queries, k, beam_width, resolved_limit,
                                 print_throughput)
+
+    def exact_search(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
+                     limit: int | None = None):
+        """The plain beam search with exact distances on any graph,
+        directional ones included (an extension: the reference's search()
+        refuses directional graphs); queries are rotated as for
+        directional_search on a prerotated graph. Shows what the graph
+        itself allows, without an estimator."""
+        self._check_alive()
+        queries = self._query_check(queries)
+        nq = queries.size(0)
+        out_indices = torch.empty(nq, k, dtype=torch.int32, device=queries.device)
+        out_distances = torch.empty(nq, k, dtype=torch.float32, device=queries.device)
+        lim = limit if limit is not None else 2 * beam_width
+        _agnostic("jasperx_exact_search")(self._handle, _tensor_ptr(queries), nq, self._dim,
+                                          _tensor_ptr(out_indices), _tensor_ptr(out_distances), k, beam_width,
+                                          lim, _stream_ptr(queries.device))
+        return out_indices, out_distances
 
     def rabitq_search(self, queries: torch.Tensor, k: int = 10, beam_width: int = 64,
                       limit: int | None = None, unique: bool = False):

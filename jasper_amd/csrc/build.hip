@@ -22,6 +22,7 @@
 // sources in ascending id order. It is one of the orders the reference can
 // produce, and it makes the build deterministic.
 #include "build.hpp"
+#include "directional_api.hpp"
 #include "common.hpp"
 #include "prune.hpp"
 #include "search.hpp"
@@ -391,12 +392,13 @@ struct EventTimer {
 };
 
 void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, bool time_stages,
-                 BuildStats* stats) {
-  build_range(g, alpha, 0, g.n, max_batch, true, stream, time_stages, stats);
+                 BuildStats* stats, bool rabitq_search) {
+  build_range(g, alpha, 0, g.n, max_batch, true, stream, time_stages, stats, rabitq_search);
 }
 
 void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max_batch, bool doubling,
-                 hipStream_t stream, bool time_stages, BuildStats* stats) {
+                 hipStream_t stream, bool time_stages, BuildStats* stats, bool rabitq_search) {
+  if (rabitq_search && !g.rabitq) throw std::invalid_argument("RaBitQ build search needs the RaBitQ codes");
   if (last <= first) return;
   if (first < 0 || last > g.n) throw std::invalid_argument("vertex range outside the graph");
   if (max_batch < 1) max_batch = 1;  // the reference loops forever here (n < 50); clamp instead
@@ -504,7 +506,11 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       // took the search stage from 11.4 s to 10.6 s)
       r.hash_bits = seen_cache_hash_bits(g.n);
       timer.start();
-      launch_beam_search(g, r, stream);
+      if (rabitq_search)
+        rabitq_build_search(g, (uint32_t)count, (uint32_t)bs, kBuildL, kBuildLimit, kBuildMaxResult, visited, vcounts,
+                            stream);
+      else
+        launch_beam_search(g, r, stream);
       timer.stop(st.search_ms);
       // 2. forward merge + prune + reverse pairs
       pa.batch_offset = (uint32_t)count;

@@ -22,14 +22,17 @@ int64_t reference_max_batch(int64_t n, uint32_t R, int64_t budget_bytes);
 // Builds the edges of `g` (vectors already resident) with the reference's
 // batch schedule: batches of 1, 2, 4, ... up to max_batch over ids in order.
 // `time_stages` records per-stage HIP-event times (adds stream syncs).
+// rabitq_search: the search stage pops by the RaBitQ estimate (the graph's
+// RaBitQ codes must exist; rabitq_build_search) instead of running the plain
+// search; the rest of each batch is unchanged.
 void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, bool time_stages,
-                 BuildStats* stats);
+                 BuildStats* stats, bool rabitq_search = false);
 
 // The same per-batch steps over the vertices [first, last) only, in batches
 // of 1, 2, 4, ... up to max_batch (doubling) or of max_batch; the rows of
 // [first, last) must hold no edges yet.
 void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max_batch, bool doubling,
-                 hipStream_t stream, bool time_stages, BuildStats* stats);
+                 hipStream_t stream, bool time_stages, BuildStats* stats, bool rabitq_search = false);
 
 // Live updates (reference construct.cuh:1169-1265, graph_ops.cuh:94-258).
 // append_rows: copies `count` rows (host or device fp16 [count, dim]) into

@@ -563,6 +563,36 @@ extern "C" int64_t jasperx_build_pq_m(int64_t h, int64_t m, int64_t n_train, int
   });
 }
 
+extern "C" int64_t jasperx_construct_directional_ex(const char* config, const void* vectors, int64_t n, int64_t dim,
+                                                    double alpha, int64_t budget, bool on_host, bool prerotate,
+                                                    int64_t seed, uint32_t options, void* stream) {
+  return guarded([&]() -> int64_t {
+    if (!config) throw std::invalid_argument("null config id");
+    static const char* const kNames[] = {
+#define JA_DIR_NAME(id) #id,
+        JASPER_DIRECTIONAL_CONFIGS(JA_DIR_NAME)
+#undef JA_DIR_NAME
+    };
+    bool known = false;
+    for (const char* name : kNames) known = known || std::strcmp(name, config) == 0;
+    if (!known) throw std::invalid_argument(std::string("unknown directional config ") + config);
+    if (options & ~kBuildOptionsKnown) throw std::invalid_argument("unknown construction options");
+    const Config c = config_of(config);
+    check_directional_dim(c.small_dim, dim);
+    auto g = construct_directional(c.R, c.metric, c.k_ranks, c.small_dim, vectors, n, dim, alpha, budget, on_host,
+                                   prerotate, (uint64_t)seed, (hipStream_t)stream, &g_last_build, options);
+    return insert(std::move(g), true);
+  });
+}
+
+extern "C" int64_t jasperx_exact_search(int64_t h, const void* q, int64_t nq, int64_t dim, int32_t* out_ids,
+                                        float* out_dists, int64_t k, int64_t bw, int64_t limit, void* stream) {
+  return guarded([&]() -> int64_t {
+    exact_search(lookup(h, nullptr), q, nq, dim, out_ids, out_dists, k, bw, limit, (hipStream_t)stream);
+    return 0;
+  });
+}
+
 extern "C" int64_t jasperx_build_rabitq(int64_t h) {
   return guarded([&]() -> int64_t {
     Graph& g = lookup(h, nullptr);

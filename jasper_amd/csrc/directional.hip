@@ -651,6 +651,13 @@ struct DirArgs {
   uint32_t rq_node_bytes, rq_words, rq_dim;
   // optional work counters per query: {visits, hops expanded, adjacency entries}
   uint32_t* stats;
+  // build mode (RaBitQ only): queries are the graph's rows [q_start,
+  // q_start + nq); each visit is scored with the plain search's distance and
+  // recorded as a key in visited[qid * max_result + i], with the count in
+  // visited_counts[qid]
+  uint64_t* visited;
+  uint32_t* visited_counts;
+  uint32_t q_start;
   // skip pops of ids already in the frontier (distinct results; an extension)
   uint32_t unique;
 };
@@ -718,7 +725,8 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   uint4* xv = qv + nchunks;  // L2 LSH: fp16 q - u
   float* lut = reinterpret_cast<float*>(xv + nchunks);
 
-  const uint4* qsrc = reinterpret_cast<const uint4*>(a.queries) + (size_t)qid * nchunks;
+  const uint4* qsrc = a.visited ? reinterpret_cast<const uint4*>(a.vecs) + (size_t)(a.q_start + qid) * nchunks
+                               : reinterpret_cast<const uint4*>(a.queries) + (size_t)qid * nchunks;
   for (uint32_t i = lane; i < nchunks; i += 64) qv[i] = qsrc[i];
   wave_sync();
   const uint16_t* q16 = reinterpret_cast<const uint16_t*>(qv);
@@ -916,6 +924,13 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     if constexpr (PQ) {
       qu_dot = visit_exact<false>(qv, urow, nchunks, nullptr);
       stored = L2 ? (q_sq - 2.0f * qu_dot) + a.norms[u] : -qu_dot;
+    } else if (RQ && a.visited) {
+      // build mode: the plain search's distance (distance.cuh's 4-lane
+      // order), so visits carry the values the plain build search records
+      const float part = L2 ? stream_partial_l2(qv, urow, lane & 3u, nchunks)
+                            : stream_partial_ip(qv, urow, lane & 3u, nchunks, a.dp);
+      stored = __shfl(quad_finish<METRIC>(part), 0, 64);
+      if (lane == 0) a.visited[(size_t)qid * a.max_result + vc] = make_key(stored, u);
     } else {
       exact_u = visit_exact<L2>(qv, urow, nchunks, xv);
       stored = L2 ? exact_u : -exact_u;
@@ -1098,6 +1113,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     wave_sync();
   }
 
+  if (a.visited_counts && lane == 0) a.visited_counts[qid] = vc;
   if (a.stats && lane == 0) {
     a.stats[(size_t)qid * 3] = vc;
     a.stats[(size_t)qid * 3 + 1] = n_hops;
@@ -1136,7 +1152,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
 std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_ranks, bool small_dim,
                                              const void* vectors, int64_t n, int64_t dim, double alpha,
                                              int64_t budget, bool on_host, bool prerotate, uint64_t seed,
-                                             hipStream_t stream, BuildStats* stats) {
+                                             hipStream_t stream, BuildStats* stats, uint32_t options) {
   if (n <= 0) throw std::invalid_argument("vectors must contain at least one row");
   if (n > 0x7FFFFFFF) throw std::invalid_argument("too many vectors for 31-bit ids");
   auto g = std::make_unique<Graph>();
@@ -1162,7 +1178,9 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
   const bool time_stages = timing && timing[0] == '1';
   BuildStats local;
   BuildStats* st = stats ? stats : &local;
-  build_graph(*g, (float)alpha, mbs, stream, time_stages, st);
+  const bool rq_search = (options & kBuildRabitqSearch) != 0;
+  if (rq_search) build_rabitq(*g);  // codes of the stored (prerotated) rows, before any edge exists
+  build_graph(*g, (float)alpha, mbs, stream, time_stages, st, rq_search);
   if (time_stages) {
     std::printf("[construct] n=%lld batches=%lld max_batch=%lld search=%.1fms prune=%.1fms group=%.1fms "
                 "reverse=%.1fms total=%.1fms\n",
@@ -1642,6 +1660,46 @@ void directional_search_run(Graph& g, int est, const void* queries, int64_t nq, 
 
 }  // namespace
 
+void rabitq_build_search(const Graph& g, uint32_t q_start, uint32_t nq, uint32_t bw, uint32_t limit,
+                         uint32_t max_result, uint64_t* visited, uint32_t* visited_counts, hipStream_t stream) {
+  if (!g.rabitq) throw std::runtime_error("RaBitQ build search needs the RaBitQ codes");
+  if (nq == 0) return;
+  if ((int64_t)q_start + nq > g.n) throw std::invalid_argument("query range out of bounds");
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  DirArgs a{};
+  a.vecs = (const uint16_t*)g.vecs;
+  a.n = g.n;
+  a.dp = g.dp;
+  a.R = g.R;
+  a.edges = g.edges;
+  a.counts = g.counts;
+  a.deleted = g.deleted;
+  a.medoid = g.medoid;
+  a.k = 0;
+  a.bw = bw;
+  a.limit = limit;
+  a.max_result = max_result;
+  a.visited = visited;
+  a.visited_counts = visited_counts;
+  a.q_start = q_start;
+  const RabitqArtifacts& rq = *g.rabitq;
+  a.rq_nodes = (const uint8_t*)rq.nodes;
+  a.rq_centroid = rq.centroid;
+  a.rq_node_bytes = rq.code_bytes + 8;
+  a.rq_words = rq.code_bytes / 4;
+  a.rq_dim = rq.dim;
+  const size_t lds = directional_lds_bytes(g, kEstRabitq, 0, bw);
+  const bool l2 = g.metric == kL2;
+  if (a.rq_words <= 4) {
+    if (l2) launch_directional<kL2, 1, 4>(a, nq, lds, stream);
+    else launch_directional<kIP, 1, 4>(a, nq, lds, stream);
+  } else {
+    if (l2) launch_directional<kL2, 1, 8>(a, nq, lds, stream);
+    else launch_directional<kIP, 1, 8>(a, nq, lds, stream);
+  }
+  hip_check(hipGetLastError(), "launch directional_kernel (build search)");
+}
+
 size_t directional_scratch_bytes(const Graph& g, int est, int64_t nq) {
   if (nq <= 0) return 0;
   const size_t rows = round256((size_t)nq * g.dp * 2);
@@ -1668,6 +1726,30 @@ void directional_search(Graph& g, int est, const void* queries, int64_t nq, int6
   SearchScratch scratch(stream);
   directional_search_run(g, est, queries, nq, dim, out_ids, out_dists, k, bw, limit, print, stream, stats, unique,
                          scratch);
+}
+
+void exact_search(Graph& g, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids, float* out_dists,
+                  int64_t k, int64_t bw, int64_t limit, hipStream_t stream) {
+  if (dim != (int64_t)g.dim)
+    throw std::invalid_argument("query dim (" + std::to_string(dim) + ") != graph dim (" + std::to_string(g.dim) + ")");
+  if (nq < 0 || k < 0 || bw <= 0 || limit < 0) throw std::invalid_argument("negative size argument");
+  if (nq > 0x7FFFFFFF) throw std::invalid_argument("too many queries");
+  if (nq == 0 || k == 0) return;
+  if (bw + 64 >= 2048)
+    throw std::invalid_argument("beam_width " + std::to_string(bw) + " is too large (beam_width + 64 must be < 2048)");
+  SearchScratch scratch(stream);
+  const uint16_t* rows = directional_query_rows(g, queries, nq, dim, stream, scratch);
+  SearchRequest r;
+  r.queries = rows;
+  r.nq = (uint32_t)nq;
+  r.medoid = g.medoid;
+  r.k = (uint32_t)k;
+  r.beam_width = (uint32_t)bw;
+  r.limit = (uint32_t)limit;
+  r.max_result = 2048;
+  r.out_ids = out_ids;
+  r.out_dists = out_dists;
+  launch_beam_search(g, r, stream);
 }
 
 void directional_search_fixed(Graph& g, int est, const void* queries, int64_t nq, int64_t dim, int32_t* out_ids,

@@ -70,6 +70,8 @@ def lib():
         _lib.jo_max_batch_size.argtypes = [i64, i32, i64]
         _lib.jo_build.restype = i32
         _lib.jo_build.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, P, P, P, i32, P]
+        _lib.jo_build_rq.restype = i32
+        _lib.jo_build_rq.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, i32, P, P, P, P, P, i32, P]
         _lib.jo_last_capped_groups.restype = i64
         _lib.jo_last_capped_groups.argtypes = []
         _lib.jo_append.restype = i32
@@ -211,8 +213,10 @@ def max_batch_size(n: int, R: int, budget_bytes: int = 10 ** 10) -> int:
 
 def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
           workspace_budget: int = 10 ** 10, max_batch: int | None = None,
-          nthreads: int = 0) -> OracleGraph:
-    """Vamana construction, reference index/construct.cuh:992-1160."""
+          nthreads: int = 0, rq: "RqArtifacts | None" = None) -> OracleGraph:
+    """Vamana construction, reference index/construct.cuh:992-1160. With rq
+    (this build's extension) the search stage pops by the RaBitQ estimate of
+    those codes (rabitq_build_search) instead of the plain search."""
     vecs16 = as_padded_f16(vectors)
     n, dp = vecs16.shape
     dim = np.asarray(vectors).shape[1]
@@ -222,9 +226,14 @@ def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
     edist = np.empty((n, R), dtype=np.uint16)
     counts = np.empty(n, dtype=np.uint8)
     nb = ctypes.c_int64(0)
-    rc = lib().jo_build(_ptr(vecs16), n, dp, dim, R, metric_code(distance), ctypes.c_float(alpha),
-                        int(max_batch), _ptr(edges), _ptr(edist), _ptr(counts), nthreads,
-                        ctypes.byref(nb))
+    if rq is None:
+        rc = lib().jo_build(_ptr(vecs16), n, dp, dim, R, metric_code(distance), ctypes.c_float(alpha),
+                            int(max_batch), _ptr(edges), _ptr(edist), _ptr(counts), nthreads,
+                            ctypes.byref(nb))
+    else:
+        rc = lib().jo_build_rq(_ptr(vecs16), n, dp, dim, R, metric_code(distance), ctypes.c_float(alpha),
+                               int(max_batch), rq.dim, _ptr(rq.nodes), _ptr(rq.centroid), _ptr(edges),
+                               _ptr(edist), _ptr(counts), nthreads, ctypes.byref(nb))
     if rc != 0:
         raise RuntimeError(f"oracle build failed ({rc})")
     g = OracleGraph(vecs16, edges, edist, counts, R, dim, distance)

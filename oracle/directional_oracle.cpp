@@ -327,11 +327,17 @@ void frontier_insert(std::vector<DEntry>& F, DEntry e, uint32_t k) {
 // expansion; the hop still counts against `limit`), so the results hold
 // distinct ids. The reference re-visits such nodes and re-inserts them into
 // F, which lets one node fill several of the k result slots.
+extern "C" float jo_l2(const uint16_t* a, const uint16_t* b, int dim);  // jasper_oracle.cpp (distance.cuh)
+extern "C" float jo_ip(const uint16_t* a, const uint16_t* b, int dim);
+
+// plain_visit (the RaBitQ build search, this build's extension): a visit is
+// scored with the plain search's distance (distance.cuh's lane order over
+// the padded row) instead of compute_qu_diff_and_exact.
 void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const Rq* rq, const uint16_t* q,
                      uint32_t medoid,
                      uint32_t k, uint32_t bw, uint32_t limit, uint32_t max_result, int32_t* out_ids,
                      float* out_d, uint32_t* vis_ids, float* vis_d, uint32_t* vis_count, uint64_t* stats,
-                     bool unique) {
+                     bool unique, bool plain_visit = false) {
   const bool l2 = g.metric == 0;
   std::vector<DEntry> B, tail, merged;
   std::vector<DEntry> F;
@@ -378,7 +384,9 @@ void directional_one(const DGraph& g, const Lsh* lsh, const Pq* pq, const Rq* rq
     }
     const uint16_t* uv = g.vecs + (size_t)u * g.dp;
     float stored, exact_u = 0.0f, qu_dot = 0.0f;
-    if (lsh || rq) {
+    if (rq && plain_visit) {
+      stored = l2 ? jo_l2(q, uv, g.dp) : jo_ip(q, uv, g.dp);
+    } else if (lsh || rq) {
       exact_u = visit_exact(q, uv, g.dp, l2, l2 ? diff.data() : nullptr);
       stored = l2 ? exact_u : -exact_u;
     } else {
@@ -538,6 +546,20 @@ void jo_frontier_insert_seq(const float* d, const uint32_t* ids, int m, int k, f
   for (size_t i = 0; i < F.size(); ++i) { out_d[i] = F[i].dist; out_ids[i] = F[i].id; }
   *out_count = (int)F.size();
 }
+// The RaBitQ build search of one row (rabitq_build_search): directional
+// traversal from the medoid with k = 0, visits scored by the plain distance;
+// writes the visits (ids, distances) and returns their count.
+int jo_rq_visit(const uint16_t* vecs, int64_t n, int dp, const uint32_t* edges, const uint8_t* counts, int R,
+                int metric, int rq_dim, const uint8_t* rq_nodes, const float* rq_centroid, const uint16_t* q,
+                uint32_t medoid, int bw, int limit, int max_result, uint32_t* vis_ids, float* vis_d) {
+  DGraph g{vecs, n, dp, edges, counts, R, nullptr, metric};
+  Rq rq{rq_dim, (((uint32_t)rq_dim + 7u) / 8u + 3u) / 4u * 4u, rq_nodes, rq_centroid};
+  uint32_t vc = 0;
+  directional_one(g, nullptr, nullptr, &rq, q, medoid, 0, (uint32_t)bw, (uint32_t)limit, (uint32_t)max_result,
+                  nullptr, nullptr, vis_ids, vis_d, &vc, nullptr, false, true);
+  return (int)vc;
+}
+
 // RaBitQ estimates of every node for every query row (test access to the
 // estimator): out[nq, n]; also each query's prepared factors when asked
 // (q_sumq [nq], q_hd_hl_g [nq, 3], q_planes [nq, 4, 8]).

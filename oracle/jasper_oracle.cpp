@@ -414,9 +414,21 @@ void reverse_step(const Graph& g, int dim_for_prune, float alpha, const std::vec
 // process_batch (construct.cuh:743-911) over the vertices [first, last), in
 // batches of 1, 2, 4, ... up to max_batch (construction) or of max_batch
 // (append_batch, construct.cuh:1226-1241), searching from `medoid`.
+int jo_rq_visit(const uint16_t* vecs, int64_t n, int dp, const uint32_t* edges, const uint8_t* counts, int R,
+                int metric, int rq_dim, const uint8_t* rq_nodes, const float* rq_centroid, const uint16_t* q,
+                uint32_t medoid, int bw, int limit, int max_result, uint32_t* vis_ids,
+                float* vis_d);  // directional_oracle.cpp
+
+// RaBitQ codes for the build search (jo_build_rq); null: the plain search.
+struct RqBuild {
+  int dim;
+  const uint8_t* nodes;
+  const float* centroid;
+};
+
 int64_t process_batches(const Graph& g, int dim_for_prune, float alpha, int64_t first, int64_t last,
                         int64_t max_batch, bool doubling, uint32_t medoid, uint32_t* edges,
-                        uint16_t* edge_dist, uint8_t* counts) {
+                        uint16_t* edge_dist, uint8_t* counts, const RqBuild* rqb = nullptr) {
   const uint16_t* vecs = g.vecs;
   const int dp = g.dp, R = g.R;
   const int L = 64, LIMIT = 256, MAX_RESULT = 256;
@@ -432,8 +444,17 @@ int64_t process_batches(const Graph& g, int dim_for_prune, float alpha, int64_t 
     // (i) beam search of every batch vector against the pre-batch graph
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t i = 0; i < bs; ++i) {
-      search_one(g, vecs + (size_t)(s + i) * dp, medoid, (uint32_t)L, (uint32_t)LIMIT,
-                 (uint32_t)MAX_RESULT, true, &visited[(size_t)i], nullptr, nullptr);
+      if (rqb) {
+        // the RaBitQ build search (directional_oracle.cpp, jo_rq_visit)
+        uint32_t ids[MAX_RESULT];
+        float ds[MAX_RESULT];
+        const int nv = jo_rq_visit(vecs, g.n, dp, g.edges, g.counts, R, g.metric, rqb->dim, rqb->nodes,
+                                   rqb->centroid, vecs + (size_t)(s + i) * dp, medoid, L, LIMIT, MAX_RESULT, ids, ds);
+        for (int j = 0; j < nv; ++j) visited[(size_t)i].push_back({ids[j], ds[j], true});
+      } else {
+        search_one(g, vecs + (size_t)(s + i) * dp, medoid, (uint32_t)L, (uint32_t)LIMIT,
+                   (uint32_t)MAX_RESULT, true, &visited[(size_t)i], nullptr, nullptr);
+      }
     }
     // (ii)+(iii) merge_candidates_kernel + robust_prune_kernel
 #pragma omp parallel
@@ -497,6 +518,27 @@ int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, 
 }
 
 int64_t jo_last_capped_groups() { return g_capped_groups.load(); }
+
+// jo_build with the RaBitQ build search (rabitq_build_search): the search
+// stage pops by the RaBitQ estimate of the given codes (nodes [n,
+// code_bytes + 8] of the rows as stored, centroid [rq_dim]).
+int jo_build_rq(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, int metric, float alpha,
+                int64_t max_batch, int rq_dim, const uint8_t* rq_nodes, const float* rq_centroid, uint32_t* edges,
+                uint16_t* edge_dist, uint8_t* counts, int nthreads, int64_t* n_batches_out) {
+  if (n <= 0) return 0;
+  if (max_batch < 1 || rq_dim <= 0 || rq_dim > 256) return -1;
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  g_capped_groups.store(0);
+  std::fill(counts, counts + n, (uint8_t)0);
+  std::fill(edges, edges + (size_t)n * R, kInvalid32);
+  std::fill(edge_dist, edge_dist + (size_t)n * R, (uint16_t)0);
+  Graph g{vecs, n, dp, edges, counts, R, nullptr, metric};
+  const RqBuild rqb{rq_dim, rq_nodes, rq_centroid};
+  const int64_t nb =
+      process_batches(g, dim_for_prune, alpha, 0, n, max_batch, true, 0u, edges, edge_dist, counts, &rqb);
+  if (n_batches_out) *n_batches_out = nb;
+  return 0;
+}
 
 // append_batch (construct.cuh:1169-1265): the rows [first, n) were appended
 // to a graph of `first` vertices (their counts must be 0); wires them in with

@@ -179,3 +179,33 @@ def test_build_gram_proof_path_matches_oracle(jasper, oracle_lib, tmp_path):
         mask = np.arange(32)[None, :] < counts[:, None]
         assert np.array_equal(edges[mask], og.edges[mask]), name
         assert np.array_equal(edist[mask], og.edge_dist[mask]), name
+
+
+def test_build_hand_computed_line(jasper, oracle_lib):
+    """The six points of the hand-computed construction (test_oracle_build):
+    n < 50 gives batches of one, and the device graph (R = 8, the smallest
+    config) must be the one worked out by hand."""
+    from tests.test_oracle_build import HAND_BATCH1, check_hand_graph, line_points
+    g = _gpu_build(jasper, line_points().astype(np.float16), 8, "l2")
+    edges, edist, counts = g.export_edges()
+    check_hand_graph(edges, edist, counts, HAND_BATCH1)
+    g.free()
+
+
+@pytest.mark.parametrize("distance,dim,n", [("l2", 128, 6000), ("ip", 96, 4000)])
+def test_build_rabitq_search_matches_oracle(jasper, oracle_lib, distance, dim, n):
+    """build_search="rabitq": the RaBitQ codes of the stored (prerotated)
+    rows, then construction whose search stage pops by their estimate; the
+    graph equals the oracle's construction with the same codes (exported
+    from the device), edges, order and bf16 distances."""
+    x = integer_clustered(n, dim, 73) if distance == "l2" else unit(n, dim, 74)
+    t = torch.from_numpy(np.ascontiguousarray(x.astype(np.float16))).cuda()
+    g = jasper.Graph.build(t, n_neighbors=32, distance=distance, alpha=1.2, build_lsh=True, k_ranks=4,
+                           prerotate=True, lsh_samples=2000, build_search="rabitq")
+    torch.cuda.synchronize()
+    assert g._has_rabitq
+    rows = g.export_vectors().view(np.float16)[:, :dim]
+    cent, nodes = g.export_rabitq()
+    og = oracle.build(rows, R=32, distance=distance, alpha=1.2, rq=oracle.RqArtifacts(dim, nodes, cent))
+    _compare(g, og)
+    g.free()

@@ -354,3 +354,32 @@ def test_rabitq_l2_d200_unrotated(jasper, oracle_lib, tmp_path):
     x = gaussian(2000, 200, 54)
     q = gaussian(32, 200, 55)
     _rq_case(jasper, tmp_path, x, q, R=32, distance="l2", prerotate=False, bws=(32,))
+
+
+def test_exact_search_on_directional_and_plain_graphs(jasper, oracle_lib, tmp_path):
+    """exact_search (an extension): the plain beam search on the stored rows
+    with the queries rotated as directional_search rotates them; on a
+    prerotated directional graph it equals the oracle's plain search of the
+    saved graph with the rotated query rows, on a plain graph it equals
+    search()."""
+    x = integer_clustered(3000, 128, 60)
+    q = integer_clustered(40, 128, 61)
+    qt = torch.from_numpy(q.astype(np.float16)).cuda()
+    gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=32, build_lsh=True,
+                            k_ranks=4, prerotate=True, lsh_samples=2000)
+    path = tmp_path / "ex.bin"
+    gg.save(str(path))
+    g = oracle.load_graph(path, 128, 32, "l2")
+    q_rows = gg.directional_query_rows(qt)
+    for bw in (16, 64):
+        ids, d = gg.exact_search(qt, k=10, beam_width=bw)
+        torch.cuda.synchronize()
+        rid, rd = oracle.beam_search(g, q_rows, k=10, beam_width=bw)
+        assert compare_search(ids.cpu().numpy(), d.cpu().numpy(), rid, rd) is None
+    gg.free()
+    pg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=32)
+    a, ad = pg.search(qt, k=10, beam_width=48)
+    b, bd = pg.exact_search(qt, k=10, beam_width=48)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(ad, bd)
+    pg.free()

@@ -122,3 +122,71 @@ def test_tiny_inputs_build():
         assert (g.counts <= min(n - 1, 8)).all()
         if n > 1:
             assert (g.counts >= 1).all()
+
+
+# ---------------------------------------------------- hand-computed tiny build
+# Six points on a line (coordinate 0 of d = 8) at 0, 10, 3, 20, 21, 12;
+# alpha = 1.2, L2 (squared distances), R = 2 or 8 (no row keeps more than two
+# candidates after the alpha prune, so both give the same graph). The expected graphs below were worked
+# out by hand from the contract (batched search from the medoid 0 against the
+# pre-batch graph, forward RobustPrune of existing edges + visited nodes,
+# reverse merge of the target's existing edges with its new sources, then
+# RobustPrune; prune c when d(c, s) * alpha < d_c). Batches of two (schedule
+# 1, 2, 2, 1) make the result sensitive to three plausible mistakes:
+#   * leaving the target's existing edges out of the reverse merge gives row
+#     2 = [3] after the third batch (and changes rows 2, 3, 5 at the end);
+#   * searching the graph as it stands after earlier members of the batch
+#     were inserted lets row 4 see row 3: [3, 2] instead of [2];
+#   * applying alpha to the other side (d_c * alpha < d(c, s)) keeps 2 in
+#     row 3: [5, 2] instead of [5].
+# With batches of one (n < 50 forces them on the device) every search sees
+# the previous insertions, and the graph is the second one.
+LINE = [0.0, 10.0, 3.0, 20.0, 21.0, 12.0]
+HAND_BATCH2 = {0: [(2, 9)], 1: [(0, 100)], 2: [(0, 9), (5, 81)], 3: [(5, 64)], 4: [(2, 324)],
+               5: [(3, 64), (2, 81)]}
+HAND_BATCH1 = {0: [(2, 9)], 1: [(5, 4), (2, 49)], 2: [(0, 9), (1, 49)], 3: [(4, 1), (5, 64)],
+               4: [(3, 1), (2, 324)], 5: [(1, 4), (3, 64)]}
+
+
+def line_points():
+    x = np.zeros((6, 8), dtype=np.float32)
+    x[:, 0] = LINE
+    return x
+
+
+def check_hand_graph(edges, edist, counts, want):
+    for v, row in want.items():
+        assert int(counts[v]) == len(row), (v, counts[v], row)
+        assert edges[v, :len(row)].tolist() == [w for w, _ in row], (v, edges[v, :counts[v]], row)
+        got = (np.asarray(edist[v, :len(row)], dtype=np.uint32) << 16).view(np.float32).tolist()
+        assert got == [float(d) for _, d in row], (v, got, row)
+
+
+@pytest.mark.parametrize("R", [2, 8])
+@pytest.mark.parametrize("max_batch,want", [(2, HAND_BATCH2), (1, HAND_BATCH1)])
+def test_hand_computed_line_build(max_batch, want, R):
+    g = oracle.build(line_points(), R=R, distance="l2", alpha=1.2, max_batch=max_batch)
+    assert g.n_batches == (4 if max_batch == 2 else 6)
+    check_hand_graph(g.edges, g.edge_dist, g.counts, want)
+
+
+def test_rabitq_search_build_quality():
+    """The construction with the RaBitQ build search (an extension) keeps
+    the build's invariants and a graph whose plain-search recall is near the
+    exact construction's on clustered data."""
+    dim = 64
+    x = datasets.clustered(4000, dim, 31, n_clusters=40).astype(np.float32)
+    q = datasets.clustered(60, dim, 32, n_clusters=40).astype(np.float32)
+    c = x.mean(0).astype(np.float32)
+    nodes, *_ = oracle.rabitq_quantize(x, np.eye(dim, dtype=np.float32).ravel(), centroid=c)
+    g_rq = oracle.build(x, R=32, rq=oracle.RqArtifacts(dim, nodes, c))
+    g_ex = oracle.build(x, R=32)
+    R = 32
+    for g in (g_rq, g_ex):
+        assert (g.counts <= R).all() and g.counts.min() >= 1
+        for v in range(g.n):
+            row = g.edges[v, :g.counts[v]]
+            assert v not in row and (row < g.n).all()
+    gt, _ = oracle.bruteforce_exact(x, q, k=10)
+    rec = [oracle.recall(gt, oracle.beam_search(g, q, k=10, beam_width=32)[0], 10) for g in (g_rq, g_ex)]
+    assert rec[0] >= rec[1] - 0.05, rec
