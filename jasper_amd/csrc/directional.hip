@@ -87,14 +87,27 @@ __device__ __forceinline__ float warp32_sum(float v) {
   return v;
 }
 
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
 // The reference 128-thread reduction, p0 = virtual thread lane, p1 =
-// virtual thread lane + 64. Every lane receives the result.
+// virtual thread lane + 64. Every lane receives the result (the four warp
+// sums are read from lanes 0 and 32 without the LDS crossbar).
 __device__ __forceinline__ float block128_sum(float p0, float p1) {
   p0 = warp32_sum(p0);
   p1 = warp32_sum(p1);
-  const float w0 = __shfl(p0, 0, 64), w1 = __shfl(p0, 32, 64);
-  const float w2 = __shfl(p1, 0, 64), w3 = __shfl(p1, 32, 64);
+  const float w0 = readlane_f(p0, 0), w1 = readlane_f(p0, 32);
+  const float w2 = readlane_f(p1, 0), w3 = readlane_f(p1, 32);
   return (w0 + w2) + (w1 + w3);
+}
+
+// The same tree when virtual threads 64..127 hold nothing (their warp sums
+// are +0.0): (w0 + 0) + (w1 + 0).
+__device__ __forceinline__ float block128_sum_low(float p0) {
+  p0 = warp32_sum(p0);
+  const float w0 = readlane_f(p0, 0), w1 = readlane_f(p0, 32);
+  return (w0 + 0.0f) + (w1 + 0.0f);
 }
 
 // splitmix64 counter sampler, identical to the oracle's
@@ -691,7 +704,7 @@ __device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4* uro
     }
     p[h] = local;
   }
-  return block128_sum(p[0], p[1]);
+  return nchunks <= 64 ? block128_sum_low(p[0]) : block128_sum(p[0], p[1]);
 }
 
 // One LSH word (sign in the MSB, coordinate below) of rank r from the
@@ -701,6 +714,10 @@ __device__ __forceinline__ uint32_t lsh_word(const uint32_t* w, int r) {
   if constexpr (P == 1) return (w[r >> 2] >> (8 * (r & 3))) & 0xFFu;
   else return (w[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
 }
+
+// Largest number of new keys a hop merges by counting (larger ones take
+// the binary searches).
+constexpr uint32_t kCountMerge = 16;
 
 // K = 0: the PQ estimator, with up to 16 * P subspaces (the edge's codes are
 // P groups of 16 bytes in registers); K = 1: the RaBitQ estimator with codes
@@ -823,14 +840,19 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   while (loop <= a.limit) {
     loop += 1;
     int p = -1;
+    uint64_t pk = 0;
     for (uint32_t base = hint; base < cnt; base += 64) {
       const uint32_t i = base + lane;
-      const bool unv = i < cnt && !key_visited(B[i]);
-      const uint64_t m = ballot(unv);
-      if (m) { p = (int)(base + (uint32_t)__builtin_ctzll(m)); break; }
+      const uint64_t bv = i < cnt ? B[i] : 1ull;
+      const uint64_t m = ballot(!key_visited(bv));
+      if (m) {
+        const int l = __builtin_ctzll(m);
+        p = (int)base + l;
+        pk = readlane64(bv, l);
+        break;
+      }
     }
     if (p < 0) break;
-    const uint64_t pk = B[p];
     wave_sync();
     if (lane == 0) B[p] = pk | 1ull;
     hint = (uint32_t)p + 1u;
@@ -1071,42 +1093,70 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     t = wave_sort_upto(t, nt);
     if (lane < nt) T[lane] = t;
     wave_sync();
-    // positions below the smallest key's insertion point lo0 keep their
-    // entries; the merge and the dedup start there
-    const uint32_t top = pow2_ceil(cnt);
-    uint32_t lo = 0;
-    if (lane < nt) {
-      // upper bound: head entries with rank <= rank(t) precede t
-      for (uint32_t step = top; step > 0; step >>= 1) {
-        const uint32_t probe = lo + step;
-        if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
+    // Merge by rank: new key t_i (sorted, lane i) lands at lo_i + i, where
+    // lo_i = the number of head entries ranked <= t_i (head first on ties),
+    // and head entry j moves to j + #{i : lo_i <= j}. Positions below the
+    // smallest key's insertion point lo0 keep their entries; the merge and
+    // the dedup start there.
+    uint32_t lo0;
+    if (nt <= kCountMerge && cnt <= 128) {
+      // few new keys and a head of at most two rows: count with ballots
+      // against the head held in registers (no dependent LDS reads)
+      const uint64_t h0 = lane < cnt ? B[lane] : ~0ull;
+      const uint64_t h1 = lane + 64u < cnt ? B[lane + 64u] : ~0ull;
+      uint32_t lo_v = 0;
+      for (uint32_t i = 0; i < nt; ++i) {
+        const uint64_t ti = readlane64(t, (int)i) | 1ull;  // rank(h) <= rank(t) <=> h <= t | 1
+        uint32_t c = (uint32_t)__builtin_popcountll(ballot(h0 <= ti));
+        if (cnt > 64) c += (uint32_t)__builtin_popcountll(ballot(h1 <= ti));
+        lo_v = lane == i ? c : lo_v;
       }
-      NB[lane + lo] = t;
-    }
-    const uint32_t lo0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
-    const uint32_t ttop = pow2_ceil(nt);
-    for (uint32_t j = lo0 + lane; j < cnt; j += 64) {
-      const uint64_t bk = B[j];
-      const uint32_t c = lds_lower_bound(T, nt, ttop, key_rank(bk));
-      NB[j + c] = bk;
+      if (lane < nt) NB[lane + lo_v] = t;
+      lo0 = (uint32_t)__builtin_amdgcn_readlane((int)lo_v, 0);
+      uint32_t s0 = 0, s1 = 0;
+      for (uint32_t i = 0; i < nt; ++i) {
+        const uint32_t li = (uint32_t)__builtin_amdgcn_readlane((int)lo_v, (int)i);
+        s0 += li <= lane ? 1u : 0u;
+        s1 += li <= lane + 64u ? 1u : 0u;
+      }
+      if (lane >= lo0 && lane < cnt) NB[lane + s0] = h0;
+      if (lane + 64u >= lo0 && lane + 64u < cnt) NB[lane + 64u + s1] = h1;
+    } else {
+      const uint32_t top = pow2_ceil(cnt);
+      uint32_t lo = 0;
+      if (lane < nt) {
+        // upper bound: head entries with rank <= rank(t) precede t
+        for (uint32_t step = top; step > 0; step >>= 1) {
+          const uint32_t probe = lo + step;
+          if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
+        }
+        NB[lane + lo] = t;
+      }
+      lo0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
+      const uint32_t ttop = pow2_ceil(nt);
+      for (uint32_t j = lo0 + lane; j < cnt; j += 64) {
+        const uint64_t bk = B[j];
+        const uint32_t c = lds_lower_bound(T, nt, ttop, key_rank(bk));
+        NB[j + c] = bk;
+      }
     }
     wave_sync();
     const uint32_t total = cnt + nt;
-    const uint32_t id0 = lo0 == 0 ? kInv31 : key_id(B[lo0 - 1u]);
+    // the previous entry's id: the lane below (DPP wave shift), or for lane
+    // 0 the last id of the previous row (the head's entry below lo0 at first)
+    uint32_t carry = lo0 == 0 ? kInv31 : key_id(B[lo0 - 1u]);
     uint32_t kept = lo0;
     for (uint32_t base = lo0; base < total; base += 64) {
       const uint32_t m = base + lane;
-      bool keep = false;
-      uint64_t cur = 0;
-      if (m < total) {
-        cur = NB[m];
-        const uint32_t prev_id = m == lo0 ? id0 : key_id(NB[m - 1]);
-        keep = key_id(cur) != prev_id;
-      }
+      const uint64_t cur = m < total ? NB[m] : 0ull;
+      const uint32_t cid = key_id(cur);
+      const uint32_t prev_id = (uint32_t)__builtin_amdgcn_update_dpp((int)carry, (int)cid, 0x138, 0xF, 0xF, false);
+      const bool keep = m < total && cid != prev_id;
       const uint64_t kmask = ballot(keep);
       const uint32_t pos = kept + mbcnt(kmask);
       if (keep && pos < a.bw) B[pos] = cur;
       kept += (uint32_t)__builtin_popcountll(kmask);
+      carry = (uint32_t)__builtin_amdgcn_readlane((int)cid, 63);
     }
     cnt = min(kept, a.bw);
     hint = min(hint, lo0);
