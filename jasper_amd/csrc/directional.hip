@@ -678,15 +678,18 @@ struct DirArgs {
 // Exact distance of the popped node (compute_qu_diff_and_exact,
 // beam_search_common.cuh:87-154). L2: fp16 q - u, stored to diff, sum of
 // f0^2 + f1^2 per half2; IP: sum of fp16 products per half2.
+// qreg: the query's chunks lane and lane + 64 in registers, used when the
+// row has at most 128 chunks (longer rows read qrow).
 template <bool L2>
-__device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4* urow, uint32_t nchunks, uint4* diff) {
+__device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4 (&qreg)[2], const uint4* urow,
+                                             uint32_t nchunks, uint4* diff) {
   const uint32_t lane = lane_id();
   float p[2] = {0.0f, 0.0f};
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     float local = 0.0f;
     for (uint32_t i = lane + 64u * h; i < nchunks; i += 128) {
-      const uint4 q = qrow[i], u = urow[i];
+      const uint4 q = nchunks <= 128 ? qreg[h] : qrow[i], u = urow[i];
       const uint32_t qw[4] = {q.x, q.y, q.z, q.w}, uw[4] = {u.x, u.y, u.z, u.w};
       uint32_t dw[4];
 #pragma unroll
@@ -745,7 +748,10 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   const uint4* qsrc = a.visited ? reinterpret_cast<const uint4*>(a.vecs) + (size_t)(a.q_start + qid) * nchunks
                                : reinterpret_cast<const uint4*>(a.queries) + (size_t)qid * nchunks;
   for (uint32_t i = lane; i < nchunks; i += 64) qv[i] = qsrc[i];
-  wave_sync();
+  uint4 qreg[2];
+  qreg[0] = lane < nchunks ? qsrc[lane] : make_uint4(0u, 0u, 0u, 0u);
+  qreg[1] = lane + 64u < nchunks ? qsrc[lane + 64u] : make_uint4(0u, 0u, 0u, 0u);
+  lds_wave_sync();
   const uint16_t* q16 = reinterpret_cast<const uint16_t*>(qv);
 
   float q_sq = 0.0f;
@@ -767,7 +773,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       }
       q_sq = block128_sum(p0, p1);
     }
-    wave_sync();
+    lds_wave_sync();
   }
 
   // RaBitQ query factors (the estimator of directional_oracle.cpp,
@@ -835,8 +841,10 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   uint64_t* NB = buf1;
   if (lane == 0) B[0] = make_key(0.0f, a.medoid);
   uint32_t cnt = 1, fc = 0, vc = 0, loop = 0, n_hops = 0, n_adj = 0;
+  float fdr = FLT_MAX;     // F's distances and ids in registers when k <= 64
+  uint32_t fir = kInv31;
   uint32_t hint = 0;  // every entry of B before `hint` is visited
-  wave_sync();
+  lds_wave_sync();
   while (loop <= a.limit) {
     loop += 1;
     int p = -1;
@@ -853,7 +861,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       }
     }
     if (p < 0) break;
-    wave_sync();
+    lds_wave_sync();
     if (lane == 0) B[p] = pk | 1ull;
     hint = (uint32_t)p + 1u;
     const uint32_t u = key_id(pk);
@@ -861,12 +869,16 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       // u already in F: its exact distance and its neighbours' estimates are
       // those of its first visit, so the hop would only duplicate F entries
       bool in_f = false;
-      for (uint32_t base = 0; base < fc && !in_f; base += 64) {
-        const uint32_t i = base + lane;
-        in_f = ballot(i < fc && Fi[i] == u) != 0;
+      if (a.k <= 64) {
+        in_f = ballot(lane < fc && fir == u) != 0;
+      } else {
+        for (uint32_t base = 0; base < fc && !in_f; base += 64) {
+          const uint32_t i = base + lane;
+          in_f = ballot(i < fc && Fi[i] == u) != 0;
+        }
       }
       if (in_f) {
-        wave_sync();
+        lds_wave_sync();
         continue;
       }
     }
@@ -944,7 +956,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     // visit: exact distance of u (the one vector fetch per hop)
     float exact_u = 0.0f, qu_dot = 0.0f, stored;
     if constexpr (PQ) {
-      qu_dot = visit_exact<false>(qv, urow, nchunks, nullptr);
+      qu_dot = visit_exact<false>(qv, qreg, urow, nchunks, nullptr);
       stored = L2 ? (q_sq - 2.0f * qu_dot) + a.norms[u] : -qu_dot;
     } else if (RQ && a.visited) {
       // build mode: the plain search's distance (distance.cuh's 4-lane
@@ -954,7 +966,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       stored = __shfl(quad_finish<METRIC>(part), 0, 64);
       if (lane == 0) a.visited[(size_t)qid * a.max_result + vc] = make_key(stored, u);
     } else {
-      exact_u = visit_exact<L2>(qv, urow, nchunks, xv);
+      exact_u = visit_exact<L2>(qv, qreg, urow, nchunks, xv);
       stored = L2 ? exact_u : -exact_u;
     }
     // frontier_insert_sorted (beam_search_common.cuh:156-185): the new entry
@@ -963,26 +975,24 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     // below the last entry, which drops out
     if (a.k > 0) {
       if (a.k <= 64) {
+        // F in registers (lane i holds entry i): entries pos .. lim - 1 move
+        // up one lane (DPP wave shift), the new one lands at pos
         const bool full = fc == a.k;
         const uint32_t lim = full ? a.k - 1 : fc;
-        float fdl = 0.0f;
-        uint32_t fil = 0;
-        if (lane < fc) {
-          fdl = Fd[lane];
-          fil = Fi[lane];
-        }
-        const bool enter = !full || stored < __shfl(fdl, (int)(a.k - 1), 64);
-        const uint64_t le = ballot(lane < lim && !(fdl > stored));
-        const uint32_t pos = le ? 64u - (uint32_t)__builtin_clzll(le) : 0u;
-        wave_sync();
+        const bool enter = !full || stored < readlane_f(fdr, (int)(a.k - 1));
         if (enter) {
-          if (lane >= pos && lane < lim) {
-            Fd[lane + 1] = fdl;
-            Fi[lane + 1] = fil;
+          const uint64_t le = ballot(lane < lim && !(fdr > stored));
+          const uint32_t pos = le ? 64u - (uint32_t)__builtin_clzll(le) : 0u;
+          const float sd = __int_as_float(
+              __builtin_amdgcn_update_dpp(__float_as_int(fdr), __float_as_int(fdr), 0x138, 0xF, 0xF, false));
+          const uint32_t si = (uint32_t)__builtin_amdgcn_update_dpp((int)fir, (int)fir, 0x138, 0xF, 0xF, false);
+          if (lane > pos && lane <= lim) {
+            fdr = sd;
+            fir = si;
           }
           if (lane == pos) {
-            Fd[pos] = stored;
-            Fi[pos] = u;
+            fdr = stored;
+            fir = u;
           }
           if (!full) fc += 1;
         }
@@ -1008,7 +1018,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     }
     vc += 1;
     if (vc == a.max_result) break;
-    wave_sync();
+    lds_wave_sync();
 
     // estimate u's neighbours from the data read above (no neighbour vector fetches)
     n_hops += 1;
@@ -1084,15 +1094,15 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     const uint64_t km = ballot(kt);
     const uint32_t nt = (uint32_t)__builtin_popcountll(km);
     if (nt == 0) {
-      wave_sync();
+      lds_wave_sync();
       continue;
     }
     if (kt) T[mbcnt(km)] = t;
-    wave_sync();
+    lds_wave_sync();
     t = lane < nt ? T[lane] : kEmptyKey;
     t = wave_sort_upto(t, nt);
     if (lane < nt) T[lane] = t;
-    wave_sync();
+    lds_wave_sync();
     // Merge by rank: new key t_i (sorted, lane i) lands at lo_i + i, where
     // lo_i = the number of head entries ranked <= t_i (head first on ties),
     // and head entry j moves to j + #{i : lo_i <= j}. Positions below the
@@ -1140,7 +1150,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         NB[j + c] = bk;
       }
     }
-    wave_sync();
+    lds_wave_sync();
     const uint32_t total = cnt + nt;
     // the previous entry's id: the lane below (DPP wave shift), or for lane
     // 0 the last id of the previous row (the head's entry below lo0 at first)
@@ -1160,7 +1170,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     }
     cnt = min(kept, a.bw);
     hint = min(hint, lo0);
-    wave_sync();
+    lds_wave_sync();
   }
 
   if (a.visited_counts && lane == 0) a.visited_counts[qid] = vc;
@@ -1171,7 +1181,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   }
   // output: F in order, skipping invalid / deleted, pad (0x7FFFFFFF, FLT_MAX)
   // (graph_beam_search.cuh:246-266)
-  wave_sync();
+  lds_wave_sync();
   uint32_t out = 0;
   for (uint32_t base = 0; base < fc && out < a.k; base += 64) {
     const uint32_t i = base + lane;
@@ -1179,8 +1189,8 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     float dist = 0.0f;
     uint32_t id = 0;
     if (ok) {
-      dist = Fd[i];
-      id = Fi[i];
+      dist = a.k <= 64 ? fdr : Fd[i];
+      id = a.k <= 64 ? fir : Fi[i];
       ok = (int64_t)id < a.n && ((a.deleted[id >> 5] >> (id & 31u)) & 1u) == 0u;
     }
     const uint64_t m = ballot(ok);
