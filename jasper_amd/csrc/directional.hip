@@ -102,12 +102,82 @@ __device__ __forceinline__ float block128_sum(float p0, float p1) {
   return (w0 + w2) + (w1 + w3);
 }
 
-// The same tree when virtual threads 64..127 hold nothing (their warp sums
-// are +0.0): (w0 + 0) + (w1 + 0).
-__device__ __forceinline__ float block128_sum_low(float p0) {
-  p0 = warp32_sum(p0);
+// Lane 0 of each row of 16 lanes receives the row's butterfly sum (xor 8,
+// 4, 2, 1): lane l adds lane l + j by a DPP row shift, and since a + b and
+// b + a are the same float, lane 0 holds exactly the butterfly's value. The
+// other lanes hold partial sums.
+template <int J>
+__device__ __forceinline__ float row_shl_f(float v) {
+  // lanes past the row's end read 0 (bound_ctrl), which lets the shift fold
+  // into the add as one DPP instruction
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + J, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float row_sum_first(float v) {
+  v = v + row_shl_f<8>(v);
+  v = v + row_shl_f<4>(v);
+  v = v + row_shl_f<2>(v);
+  v = v + row_shl_f<1>(v);
+  return v;
+}
+
+// Lanes 0 and 32 receive the butterfly sums of lanes 0..31 and 32..63
+// (warp32_sum's values there): rows 0 and 2 first add the row above them.
+__device__ __forceinline__ float warp32_sum_first(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return row_sum_first(v + __uint_as_float(r[1]));
+}
+
+// block128_sum for the visit, by rows: with at most 16 virtual threads
+// holding values the other three warp sums are +0.0 and the tree reduces to
+// (row 0's sum + 0) + 0, which is row 0's sum + 0 (a sum tree whose leaves
+// differ only in the signs of zeros gives the same value or a zero, and
+// adding +0.0 makes either zero +0.0).
+__device__ __forceinline__ float block128_sum_rows(float p0, float p1, uint32_t nthreads) {
+  if (nthreads <= 16) return readlane_f(row_sum_first(p0), 0) + 0.0f;
+  p0 = warp32_sum_first(p0);
   const float w0 = readlane_f(p0, 0), w1 = readlane_f(p0, 32);
-  return (w0 + 0.0f) + (w1 + 0.0f);
+  if (nthreads <= 64) return (w0 + 0.0f) + (w1 + 0.0f);
+  p1 = warp32_sum_first(p1);
+  const float w2 = readlane_f(p1, 0), w3 = readlane_f(p1, 32);
+  return (w0 + w2) + (w1 + w3);
+}
+
+// Sums of an fp16 pair with one rounding, the halves read by v_fma_mix_f32.
+// h2_sq_sum: f0^2 + f1^2 (each square of an fp16 value is exact in fp32, 22
+// significant bits, so fma(f1, f1, f0 * f0) is the rounded sum of squares);
+// h2_sum: f0 + f1 as fma(f0, 1, f1).
+__device__ __forceinline__ float h2_sq_sum(uint32_t w) {
+  const float f0 = h2f_lo(w), f1 = h2f_hi(w);
+  return __builtin_fmaf(f1, f1, __builtin_fmaf(f0, f0, 0.0f));
+}
+
+__device__ __forceinline__ float h2_sum(uint32_t w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(w), "s"(1.0f));
+  return r;
+}
+
+// Square root of a bf16 value through a 256-entry table in LDS: for sign 0
+// and exponent field E in 1..254 the value is (1 + m / 128) * 2^e, e = E -
+// 127, and its root is sqrt((1 + m / 128) * 2^p) * 2^((e - p) / 2) with p =
+// e mod 2. tab[(p << 7) | m] holds the correctly rounded first factor (in
+// [1, 2)), and the power of two scales it exactly (the result is normal).
+// Index bit 7 is p = 1 - (E mod 2), i.e. bit 7 of the bf16 bits inverted.
+// Zeros, subnormals, infinities, NaNs and negative values take sqrt_rn.
+__device__ __forceinline__ float bf16_sqrt(const float* tab, uint32_t bits) {
+  if (bits - 0x80u < 0x7F00u) {
+    const int e = (int)((bits >> 7) & 0xFFu) - 127;
+    return __builtin_ldexpf(tab[(bits & 0xFFu) ^ 0x80u], e >> 1);
+  }
+  return sqrt_rn(bf2f((uint16_t)bits));
+}
+
+__device__ __forceinline__ void fill_sqrt_table(float* tab, uint32_t lane) {
+  for (uint32_t i = lane; i < 256; i += 64) {
+    const uint32_t p = i >> 7, m = i & 127u;
+    tab[i] = sqrt_rn(bf2f((uint16_t)(((127u + p) << 7) | m)));
+  }
 }
 
 // splitmix64 counter sampler, identical to the oracle's
@@ -696,18 +766,16 @@ __device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4 (&qr
       for (int j = 0; j < 4; ++j) {
         if constexpr (L2) {
           dw[j] = hsub2_bits(qw[j], uw[j]);
-          const float f0 = h2f_lo(dw[j]), f1 = h2f_hi(dw[j]);
-          local = local + (f0 * f0 + f1 * f1);
+          local = local + h2_sq_sum(dw[j]);
         } else {
-          const uint32_t pw = hmul2_bits(qw[j], uw[j]);
-          local = local + (h2f_lo(pw) + h2f_hi(pw));
+          local = local + h2_sum(hmul2_bits(qw[j], uw[j]));
         }
       }
       if constexpr (L2) diff[i] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
     }
     p[h] = local;
   }
-  return nchunks <= 64 ? block128_sum_low(p[0]) : block128_sum(p[0], p[1]);
+  return block128_sum_rows(p[0], p[1], nchunks);
 }
 
 // One LSH word (sign in the MSB, coordinate below) of rank r from the
@@ -741,13 +809,24 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   uint64_t* T = buf1 + cap;
   float* Fd = reinterpret_cast<float*>(T + 64);  // frontier distances (exact bits)
   uint32_t* Fi = reinterpret_cast<uint32_t*>(Fd + a.k);
+  // LSH with 1-byte words (dp <= 128): q and q - u take 16 chunks each,
+  // zero past dp, so any 7-bit coordinate reads inside them
+  constexpr bool LSH8 = !PQ && !RQ && P == 1;
+  const uint32_t qchunks = LSH8 ? 16u : nchunks;
   uint4* qv = reinterpret_cast<uint4*>(smem + ((2 * cap + 64 + a.k + 1) & ~1u));  // 16-byte aligned
-  uint4* xv = qv + nchunks;  // L2 LSH: fp16 q - u
-  float* lut = reinterpret_cast<float*>(xv + nchunks);
+  uint4* xv = qv + qchunks;  // L2 LSH: fp16 q - u
+  float* lut = reinterpret_cast<float*>(xv + qchunks);  // PQ: the query's LUT; LSH: the bf16 sqrt table
 
   const uint4* qsrc = a.visited ? reinterpret_cast<const uint4*>(a.vecs) + (size_t)(a.q_start + qid) * nchunks
                                : reinterpret_cast<const uint4*>(a.queries) + (size_t)qid * nchunks;
   for (uint32_t i = lane; i < nchunks; i += 64) qv[i] = qsrc[i];
+  if constexpr (LSH8) {
+    for (uint32_t i = nchunks + lane; i < 16u; i += 64) {
+      qv[i] = make_uint4(0u, 0u, 0u, 0u);
+      xv[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  if constexpr (!PQ && !RQ) fill_sqrt_table(lut, lane);
   uint4 qreg[2];
   qreg[0] = lane < nchunks ? qsrc[lane] : make_uint4(0u, 0u, 0u, 0u);
   qreg[1] = lane + 64u < nchunks ? qsrc[lane + 64u] : make_uint4(0u, 0u, 0u, 0u);
@@ -1066,13 +1145,16 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
           for (int r = 0; r < K; ++r) {
             const uint32_t w = lsh_word<P>(wl, r);
             const uint32_t coord = w & (kSign - 1u);
-            const float cs = (w & kSign) ? -a.c[r] : a.c[r];
-            const float xc = coord < a.dp ? h2f16(x16[coord]) : 0.0f;  // guards a corrupt row
+            // -c_r when the sign bit is set: the bit moved to the float's sign
+            const float cs = __uint_as_float(__float_as_uint(a.c[r]) ^ ((w & kSign) << (P == 1 ? 24 : 16)));
+            // 1-byte words: coord < 128 and x16 is zero past dp; 2-byte
+            // words: the bound guards a corrupt row
+            const float xc = (P == 1 || coord < a.dp) ? h2f16(x16[coord]) : 0.0f;
             dot_acc = __builtin_fmaf(cs, xc, dot_acc);
           }
           const float mag_sq = bf2f((uint16_t)mag_bits);
           const float dot_est = dot_acc * a.inv_norm_denom;
-          const float mag = sqrt_rn(mag_sq);
+          const float mag = bf16_sqrt(lut, mag_bits);
           est = L2 ? __builtin_fmaf(-(2.0f * mag), dot_est, exact_u + mag_sq)
                    : -__builtin_fmaf(mag, dot_est, exact_u);
         }
@@ -1559,7 +1641,14 @@ const uint16_t* directional_query_rows(const Graph& g, const void* queries, int6
 }
 
 size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
-  size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8 + (size_t)2 * g.dp * 2;
+  size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8;
+  if (est == kEstLsh) {
+    // q and q - u (16 chunks each with 1-byte words), the sqrt table
+    const size_t chunks = g.lsh->packed_bytes == 1 ? 16 : g.dp / 8;
+    lds += 2 * chunks * 16 + 256 * 4;
+  } else {
+    lds += (size_t)2 * g.dp * 2;
+  }
   if (est == kEstPq) lds += (size_t)g.pq->m * 256 * 4;
   return lds;
 }
@@ -1590,6 +1679,8 @@ void check_directional_search(const Graph& g, int est, int64_t nq, int64_t dim, 
   } else if (est == kEstLsh && !((g.lsh->k_ranks == 4 || g.lsh->k_ranks == 16) &&
                                   (g.lsh->packed_bytes == 1 || g.lsh->packed_bytes == 2))) {
     throw std::invalid_argument("k_ranks must be 4 or 16 with 1- or 2-byte words");
+  } else if (est == kEstLsh && g.lsh->packed_bytes == 1 && g.dp > 128) {
+    throw std::invalid_argument("1-byte LSH words address at most 128 dims");
   } else if (est == kEstRabitq && (g.rabitq->dim != g.dim || g.rabitq->code_bytes > 32)) {
     throw std::invalid_argument("RaBitQ codes do not match the graph");
   }
