@@ -85,6 +85,16 @@ __device__ __forceinline__ void wave_sync() { __syncthreads(); }
 // compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// v with lane l replaced by s (v_writelane_b32); s and l are wave-uniform.
+// The lane select goes through m0: an SGPR data operand and an SGPR lane
+// select together exceed gfx9's one scalar operand per VALU instruction.
+__device__ __forceinline__ uint32_t writelane(uint32_t v, uint32_t s, uint32_t l) {
+  asm("v_writelane_b32 %0, %1, m0"
+      : "+v"(v)
+      : "s"(__builtin_amdgcn_readfirstlane(s)), "{m0}"(__builtin_amdgcn_readfirstlane(l)));
+  return v;
+}
+
 // Per-lane select by a wave-uniform lane mask held in SGPRs: bit set -> b.
 __device__ __forceinline__ uint32_t select_by_mask(uint32_t a, uint32_t b, uint64_t mask) {
   uint32_t r;

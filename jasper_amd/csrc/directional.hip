@@ -1191,28 +1191,40 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     // smallest key's insertion point lo0 keep their entries; the merge and
     // the dedup start there.
     uint32_t lo0;
+    uint32_t lo_v = 0;       // counting path: lane i < nt holds lo_i
+    bool in_place = false;   // the counting path merged into B itself
     if (nt <= kCountMerge && cnt <= 128) {
-      // few new keys and a head of at most two rows: count with ballots
-      // against the head held in registers (no dependent LDS reads)
+      // few new keys and a head of at most two rows: the head is held in
+      // registers, so the merge writes B in place. Key i is counted against
+      // the head with ballots: g0 / g1 mark the head entries ranked after
+      // it, lo_i = the rest, and each marked entry moves up one slot (the
+      // head is sorted, so lo_i <= j exactly when entry j is marked).
       const uint64_t h0 = lane < cnt ? B[lane] : ~0ull;
       const uint64_t h1 = lane + 64u < cnt ? B[lane + 64u] : ~0ull;
-      uint32_t lo_v = 0;
-      for (uint32_t i = 0; i < nt; ++i) {
-        const uint64_t ti = readlane64(t, (int)i) | 1ull;  // rank(h) <= rank(t) <=> h <= t | 1
-        uint32_t c = (uint32_t)__builtin_popcountll(ballot(h0 <= ti));
-        if (cnt > 64) c += (uint32_t)__builtin_popcountll(ballot(h1 <= ti));
-        lo_v = lane == i ? c : lo_v;
-      }
-      if (lane < nt) NB[lane + lo_v] = t;
-      lo0 = (uint32_t)__builtin_amdgcn_readlane((int)lo_v, 0);
       uint32_t s0 = 0, s1 = 0;
-      for (uint32_t i = 0; i < nt; ++i) {
-        const uint32_t li = (uint32_t)__builtin_amdgcn_readlane((int)lo_v, (int)i);
-        s0 += li <= lane ? 1u : 0u;
-        s1 += li <= lane + 64u ? 1u : 0u;
+      // rank(h) <= rank(t) <=> h <= t | 1
+      if ((uint32_t)__builtin_amdgcn_readfirstlane(cnt) > 64u) {
+        for (uint32_t i = 0; i < nt; ++i) {
+          const uint64_t ti = readlane64(t, (int)i) | 1ull;
+          const bool g0 = h0 > ti, g1 = h1 > ti;
+          s0 += g0 ? 1u : 0u;
+          s1 += g1 ? 1u : 0u;
+          lo_v = writelane(lo_v, 128u - (uint32_t)__builtin_popcountll(ballot(g0)) -
+                                     (uint32_t)__builtin_popcountll(ballot(g1)), i);
+        }
+      } else {
+        for (uint32_t i = 0; i < nt; ++i) {
+          const uint64_t ti = readlane64(t, (int)i) | 1ull;
+          const bool g0 = h0 > ti;
+          s0 += g0 ? 1u : 0u;
+          lo_v = writelane(lo_v, 64u - (uint32_t)__builtin_popcountll(ballot(g0)), i);
+        }
       }
-      if (lane >= lo0 && lane < cnt) NB[lane + s0] = h0;
-      if (lane + 64u >= lo0 && lane + 64u < cnt) NB[lane + 64u + s1] = h1;
+      lo0 = (uint32_t)__builtin_amdgcn_readlane((int)lo_v, 0);
+      if (lane < nt) B[lane + lo_v] = t;
+      if (lane >= lo0 && lane < cnt) B[lane + s0] = h0;
+      if (lane + 64u >= lo0 && lane + 64u < cnt) B[lane + 64u + s1] = h1;
+      in_place = true;
     } else {
       const uint32_t top = pow2_ceil(cnt);
       uint32_t lo = 0;
@@ -1234,21 +1246,44 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     }
     lds_wave_sync();
     const uint32_t total = cnt + nt;
-    // the previous entry's id: the lane below (DPP wave shift), or for lane
-    // 0 the last id of the previous row (the head's entry below lo0 at first)
-    uint32_t carry = lo0 == 0 ? kInv31 : key_id(B[lo0 - 1u]);
-    uint32_t kept = lo0;
-    for (uint32_t base = lo0; base < total; base += 64) {
-      const uint32_t m = base + lane;
-      const uint64_t cur = m < total ? NB[m] : 0ull;
-      const uint32_t cid = key_id(cur);
-      const uint32_t prev_id = (uint32_t)__builtin_amdgcn_update_dpp((int)carry, (int)cid, 0x138, 0xF, 0xF, false);
-      const bool keep = m < total && cid != prev_id;
-      const uint64_t kmask = ballot(keep);
-      const uint32_t pos = kept + mbcnt(kmask);
-      if (keep && pos < a.bw) B[pos] = cur;
-      kept += (uint32_t)__builtin_popcountll(kmask);
-      carry = (uint32_t)__builtin_amdgcn_readlane((int)cid, 63);
+    // Dedup: drop each entry whose id equals the previous entry's. Merging
+    // never makes two head entries adjacent that were not, and B holds no
+    // adjacent equal ids, so an entry can only be dropped at a new key or
+    // right after one. The in-place merge checks those two places and is
+    // done when neither drops anything (the usual case).
+    bool dedup = true;
+    if (in_place) {
+      bool d = false;
+      if (lane < nt) {
+        const uint32_t pos = lane + lo_v, id = key_id(t);
+        const uint32_t prev_id = pos == 0 ? kInv31 : key_id(B[pos - 1u]);
+        d = prev_id == id || (pos + 1u < total && key_id(B[pos + 1u]) == id);
+      }
+      dedup = ballot(d) != 0;
+    }
+    uint32_t kept = total;
+    if (dedup) {
+      // in order from lo0, reading the merged entries (B itself after the
+      // in-place merge: each row is read before any of its slots is written,
+      // and writes only go to slots at or below the ones read)
+      const uint64_t* src = in_place ? B : NB;
+      // the previous entry's id: the lane below (DPP wave shift), or for
+      // lane 0 the last id of the previous row (the head's entry below lo0
+      // at first)
+      uint32_t carry = lo0 == 0 ? kInv31 : key_id(B[lo0 - 1u]);
+      kept = lo0;
+      for (uint32_t base = lo0; base < total; base += 64) {
+        const uint32_t m = base + lane;
+        const uint64_t cur = m < total ? src[m] : 0ull;
+        const uint32_t cid = key_id(cur);
+        const uint32_t prev_id = (uint32_t)__builtin_amdgcn_update_dpp((int)carry, (int)cid, 0x138, 0xF, 0xF, false);
+        const bool keep = m < total && cid != prev_id;
+        const uint64_t kmask = ballot(keep);
+        const uint32_t pos = kept + mbcnt(kmask);
+        if (keep && pos < a.bw) B[pos] = cur;
+        kept += (uint32_t)__builtin_popcountll(kmask);
+        carry = (uint32_t)__builtin_amdgcn_readlane((int)cid, 63);
+      }
     }
     cnt = min(kept, a.bw);
     hint = min(hint, lo0);
