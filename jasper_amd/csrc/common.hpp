@@ -85,6 +85,10 @@ __device__ __forceinline__ void wave_sync() { __syncthreads(); }
 // compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// A value every lane holds alike, marked as such for the compiler (it is
+// then kept in an SGPR and branches on it are scalar branches).
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+
 // v with lane l replaced by s (v_writelane_b32); s and l are wave-uniform.
 // The lane select goes through m0: an SGPR data operand and an SGPR lane
 // select together exceed gfx9's one scalar operand per VALU instruction.

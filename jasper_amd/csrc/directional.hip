@@ -745,35 +745,54 @@ struct DirArgs {
   uint32_t unique;
 };
 
+// One thread's share of the visit for one chunk of 8 fp16 values, summed
+// in order from 0 (L2 also stores the fp16 differences to *d).
+template <bool L2>
+__device__ __forceinline__ float chunk_sum(uint4 q, uint4 u, uint4* d, float local) {
+  const uint32_t qw[4] = {q.x, q.y, q.z, q.w}, uw[4] = {u.x, u.y, u.z, u.w};
+  uint32_t dw[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (L2) {
+      dw[j] = hsub2_bits(qw[j], uw[j]);
+      local = local + h2_sq_sum(dw[j]);
+    } else {
+      local = local + h2_sum(hmul2_bits(qw[j], uw[j]));
+    }
+  }
+  if constexpr (L2) *d = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+  return local;
+}
+
 // Exact distance of the popped node (compute_qu_diff_and_exact,
 // beam_search_common.cuh:87-154). L2: fp16 q - u, stored to diff, sum of
 // f0^2 + f1^2 per half2; IP: sum of fp16 products per half2.
 // qreg: the query's chunks lane and lane + 64 in registers, used when the
 // row has at most 128 chunks (longer rows read qrow).
-template <bool L2>
+// ureg: u's chunks lane and lane + 64, loaded by the caller, when the row
+// has at most 128 chunks.
+// kMaxChunks: a bound on nchunks known to the caller at compile time.
+template <bool L2, uint32_t kMaxChunks>
 __device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4 (&qreg)[2], const uint4* urow,
-                                             uint32_t nchunks, uint4* diff) {
+                                             const uint4 (&ureg)[2], uint32_t nchunks, uint4* diff) {
   const uint32_t lane = lane_id();
   float p[2] = {0.0f, 0.0f};
+  if (kMaxChunks <= 16) {
+    if (lane < nchunks) p[0] = chunk_sum<L2>(qreg[0], ureg[0], diff + lane, 0.0f);
+    return readlane_f(row_sum_first(p[0]), 0) + 0.0f;  // block128_sum_rows with nthreads <= 16
+  }
+  if (nchunks <= 128) {
+    // at most one chunk per virtual thread: lane and lane + 64
+    if (lane < nchunks) p[0] = chunk_sum<L2>(qreg[0], ureg[0], diff + lane, 0.0f);
+    if (kMaxChunks > 64 && nchunks > 64 && lane + 64u < nchunks)
+      p[1] = chunk_sum<L2>(qreg[1], ureg[1], diff + lane + 64u, 0.0f);
+  } else {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    float local = 0.0f;
-    for (uint32_t i = lane + 64u * h; i < nchunks; i += 128) {
-      const uint4 q = nchunks <= 128 ? qreg[h] : qrow[i], u = urow[i];
-      const uint32_t qw[4] = {q.x, q.y, q.z, q.w}, uw[4] = {u.x, u.y, u.z, u.w};
-      uint32_t dw[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (L2) {
-          dw[j] = hsub2_bits(qw[j], uw[j]);
-          local = local + h2_sq_sum(dw[j]);
-        } else {
-          local = local + h2_sum(hmul2_bits(qw[j], uw[j]));
-        }
-      }
-      if constexpr (L2) diff[i] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    for (int h = 0; h < 2; ++h) {
+      float local = 0.0f;
+      for (uint32_t i = lane + 64u * h; i < nchunks; i += 128) local = chunk_sum<L2>(qrow[i], urow[i], diff + i, local);
+      p[h] = local;
     }
-    p[h] = local;
   }
   return block128_sum_rows(p[0], p[1], nchunks);
 }
@@ -943,7 +962,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     lds_wave_sync();
     if (lane == 0) B[p] = pk | 1ull;
     hint = (uint32_t)p + 1u;
-    const uint32_t u = key_id(pk);
+    const uint32_t u = uniform(key_id(pk));
     if (a.unique) {
       // u already in F: its exact distance and its neighbours' estimates are
       // those of its first visit, so the hop would only duplicate F entries
@@ -964,9 +983,23 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     // every read that depends only on u, issued before the visit: the edge
     // count, the adjacency row, and u's estimator data for edge slot `lane`
     // (slots past the count are read and ignored; they lie inside u's rows)
-    const bool slot = lane < a.R;
+    // u's row first (rows of at most 128 chunks): the visit's arithmetic
+    // then overlaps the gathers below
+    const uint4* urow = reinterpret_cast<const uint4*>(a.vecs) + (size_t)u * nchunks;
+    // Loads below are issued by every lane, at clamped indexes, so that the
+    // wait for the visited row does not also wait for later loads; lanes
+    // past the row or the degree ignore what they read.
+    // a compile-time bound on the row's chunks: 1-byte LSH words address at
+    // most 128 dims, RaBitQ codes at most 256
+    constexpr uint32_t kMaxChunks = LSH8 ? 16u : RQ ? 32u : 0xFFFFFFFFu;
+    const bool short_row = nchunks <= 128 && !(RQ && a.visited);
+    uint4 ureg[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+    // adjacency slot `lane` (slots past R read slot R - 1 and are never used:
+    // only lanes below the degree are)
+    const uint32_t el = min(lane, a.R - 1u);
     const uint32_t deg_raw = a.counts[u];
-    const uint32_t v_raw = slot ? a.edges[(size_t)u * a.R + lane] : 0u;
+    const uint32_t* erow = a.edges + (size_t)u * a.R;
+    const uint32_t v_raw = erow[el];
     uint32_t wl[KW];
     uint32_t mag_bits = 0;
     uint4 cw[PQ ? P : 1];  // PQ: codes of subspaces 16g .. 16g + 15 in cw[g]
@@ -974,30 +1007,24 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       // nothing of u's row: the estimator reads the neighbours' codes below
     } else if constexpr (!PQ) {
       const uint8_t* row = a.lsh_rows + (size_t)u * a.row_bytes;
-      if (slot) {
-        const uint8_t* wp = row + (size_t)lane * (K * P);
-        if constexpr (KW == 1) wl[0] = *reinterpret_cast<const uint32_t*>(wp);
-        else if constexpr (KW == 2) {
-          const uint2 t2 = *reinterpret_cast<const uint2*>(wp);
-          wl[0] = t2.x; wl[1] = t2.y;
-        } else {
-#pragma unroll
-          for (int c = 0; c < KW / 4; ++c) {
-            const uint4 t4 = reinterpret_cast<const uint4*>(wp)[c];
-            wl[4 * c] = t4.x; wl[4 * c + 1] = t4.y; wl[4 * c + 2] = t4.z; wl[4 * c + 3] = t4.w;
-          }
-        }
-        mag_bits = *reinterpret_cast<const uint16_t*>(row + (size_t)a.R * (K * P) + 2 * (size_t)lane);
+      if constexpr (KW == 1) wl[0] = reinterpret_cast<const uint32_t*>(row)[el];
+      else if constexpr (KW == 2) {
+        const uint2 t2 = reinterpret_cast<const uint2*>(row)[el];
+        wl[0] = t2.x; wl[1] = t2.y;
       } else {
 #pragma unroll
-        for (int c = 0; c < KW; ++c) wl[c] = 0;
+        for (int c = 0; c < KW / 4; ++c) {
+          const uint4 t4 = reinterpret_cast<const uint4*>(row)[el * (KW / 4) + c];
+          wl[4 * c] = t4.x; wl[4 * c + 1] = t4.y; wl[4 * c + 2] = t4.z; wl[4 * c + 3] = t4.w;
+        }
       }
+      mag_bits = reinterpret_cast<const uint16_t*>(row + (size_t)a.R * (K * P))[el];
     } else {
-      const uint8_t* crow = a.codes + (size_t)u * a.code_row_bytes + (size_t)lane * a.pq_w;
+      const uint8_t* crow = a.codes + (size_t)u * a.code_row_bytes + (size_t)el * a.pq_w;
 #pragma unroll
       for (int g = 0; g < (PQ ? P : 1); ++g) {
         cw[g] = make_uint4(0u, 0u, 0u, 0u);
-        if (slot && (uint32_t)g < a.pq_groups) {
+        if ((uint32_t)g < a.pq_groups) {
           const uint8_t* cp = crow + (size_t)g * a.R * a.pq_w;
           if (a.pq_w == 16) {
             cw[g] = *reinterpret_cast<const uint4*>(cp);
@@ -1011,9 +1038,17 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         }
       }
     }
-    const uint32_t deg = min(deg_raw, a.R);
-    const bool has = lane < deg;
-    const bool valid_v = has && (int64_t)v_raw < a.n;
+    if (short_row) ureg[0] = urow[min(lane, nchunks - 1u)];
+    if (kMaxChunks > 64 && short_row && nchunks > 64) ureg[1] = urow[min(lane + 64u, nchunks - 1u)];
+    // the degree and edge validity: before the visit where gathers depend
+    // on them (PQ norms, RaBitQ codes), after it for LSH
+    uint32_t deg = 0;
+    bool has = false, valid_v = false;
+    if constexpr (PQ || RQ) {
+      deg = uniform(min(deg_raw, a.R));
+      has = lane < deg;
+      valid_v = has && (int64_t)v_raw < a.n;
+    }
     float vnorm = 0.0f;
     if constexpr (PQ && L2) vnorm = valid_v ? a.norms[v_raw] : 0.0f;
     // RaBitQ: the neighbour's code dwords and factors (a gather per edge,
@@ -1030,12 +1065,11 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         rq_fres = __uint_as_float(node[a.rq_words + 1]);
       }
     }
-    const uint4* urow = reinterpret_cast<const uint4*>(a.vecs) + (size_t)u * nchunks;
 
     // visit: exact distance of u (the one vector fetch per hop)
     float exact_u = 0.0f, qu_dot = 0.0f, stored;
     if constexpr (PQ) {
-      qu_dot = visit_exact<false>(qv, qreg, urow, nchunks, nullptr);
+      qu_dot = visit_exact<false, kMaxChunks>(qv, qreg, urow, ureg, nchunks, nullptr);
       stored = L2 ? (q_sq - 2.0f * qu_dot) + a.norms[u] : -qu_dot;
     } else if (RQ && a.visited) {
       // build mode: the plain search's distance (distance.cuh's 4-lane
@@ -1045,7 +1079,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       stored = __shfl(quad_finish<METRIC>(part), 0, 64);
       if (lane == 0) a.visited[(size_t)qid * a.max_result + vc] = make_key(stored, u);
     } else {
-      exact_u = visit_exact<L2>(qv, qreg, urow, nchunks, xv);
+      exact_u = visit_exact<L2, kMaxChunks>(qv, qreg, urow, ureg, nchunks, xv);
       stored = L2 ? exact_u : -exact_u;
     }
     // frontier_insert_sorted (beam_search_common.cuh:156-185): the new entry
@@ -1094,6 +1128,12 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         }
       }
       if (a.k > 64) fc = (uint32_t)__shfl((int)fc, 0, 64);
+      fc = uniform(fc);
+    }
+    if constexpr (!PQ && !RQ) {
+      deg = uniform(min(deg_raw, a.R));
+      has = lane < deg;
+      valid_v = has && (int64_t)v_raw < a.n;
     }
     vc += 1;
     if (vc == a.max_result) break;
@@ -1102,6 +1142,14 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     // estimate u's neighbours from the data read above (no neighbour vector fetches)
     n_hops += 1;
     n_adj += deg;
+    // every lane takes the gathered words here, on every path, so no load of
+    // this hop is still in flight when the next hop reuses its registers
+    if constexpr (!PQ && !RQ) {
+#pragma unroll
+      for (int c = 0; c < KW; ++c) asm volatile("" ::"v"(wl[c]));
+      asm volatile("" ::"v"(mag_bits));
+    }
+    asm volatile("" ::"v"(v_raw));
     uint64_t t = kEmptyKey;
     if (has) {
       if (valid_v) {
@@ -1285,8 +1333,8 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         carry = (uint32_t)__builtin_amdgcn_readlane((int)cid, 63);
       }
     }
-    cnt = min(kept, a.bw);
-    hint = min(hint, lo0);
+    cnt = uniform(min(kept, a.bw));
+    hint = uniform(min(hint, lo0));
     lds_wave_sync();
   }
 
