@@ -125,7 +125,7 @@ def main() -> int:
                          "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
                          "rabitq (one-bit codes), c4 (config 4: 1M x 960 build + PQ search), c5 "
                          "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search), updates "
-                         "(config 2: mark_deleted 10%, consolidate, append 100k)")
+                         "(config 2: mark_deleted 10%%, consolidate, append 100k)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
     args = ap.parse_args()

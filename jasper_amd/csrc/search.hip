@@ -223,7 +223,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   const uint32_t nlimit = METRIC == kL2 ? a.nchunks : a.dp;
   bool intx = false;
   if constexpr (METRIC == kL2 && CPL > 0 && !STATS) {
-    if (a.gint) intx = query_int_exact<CPL>(a, qf.h);
+    if (a.gint) intx = uniform(query_int_exact<CPL>(a, qf.h) ? 1u : 0u) != 0u;
   }
 
   // B = [(medoid, d(q, medoid))]; at bw <= 64 B lives in registers, one key
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       const uint32_t p = (uint32_t)__builtin_ctzll(m);
       const uint64_t m2 = m & (m - 1u);
       pk = readlane64(b, (int)p) | 1ull;
-      next_u = m2 ? key_id(readlane64(b, (int)__builtin_ctzll(m2))) : kInvalid32;
+      next_u = uniform(m2 ? key_id(readlane64(b, (int)__builtin_ctzll(m2))) : kInvalid32);
       if (lane == p) b = pk;
       if (a.visited && lane == 0) a.visited[(size_t)qid * a.max_result + vc] = pk;
     } else {
@@ -285,20 +285,20 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       }
       if (p < 0) break;
       pk = B[p] | 1ull;
-      next_u = p2 >= 0 ? key_id(B[p2]) : kInvalid32;
+      next_u = uniform(p2 >= 0 ? key_id(B[p2]) : kInvalid32);
       wave_sync();
       if (lane == 0) {
         B[p] = pk;
         if (a.visited) a.visited[(size_t)qid * a.max_result + vc] = pk;
       }
-      hint = (uint32_t)p + 1;
+      hint = uniform((uint32_t)p + 1);
     }
-    vc += 1;
+    vc = uniform(vc + 1u);
     if (vc == a.max_result) break;
 
     // ---- expand: one coalesced row read (degree and row issued together,
     //      or taken from the prediction), filter through the seen cache
-    const uint32_t u = key_id(pk);
+    const uint32_t u = uniform(key_id(pk));
     uint32_t cu, v;
     if (u == spec_u) {
       cu = spec_c;
@@ -378,7 +378,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       const bool dup = (lane < 63u && x0 != kEmptyKey && key_rank(x0) == key_rank(nx)) ||
                        (last != kEmptyKey && key_rank(x1) == key_rank(last));
       if (ballot(dup) == 0) {
-        cnt = min(cnt + nt, bw);
+        cnt = uniform(min(cnt + nt, bw));
         b = lane < cnt ? x0 : kEmptyKey;
         lds_wave_sync();
         continue;
@@ -412,7 +412,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     //      smallest kept key's position lb0 keep their places; only
     //      positions from lb0 on are merged, and the shorter of the
     //      unchanged prefix and the merged tail is copied across
-    const uint32_t lb0 = (uint32_t)__shfl((int)lb, (int)__builtin_ctzll(km), 64);
+    const uint32_t lb0 = uniform((uint32_t)__shfl((int)lb, (int)__builtin_ctzll(km), 64));
     if (keep) {
       const uint32_t pos = ti + lb;
       if (pos < bw) NB[pos] = t;
@@ -434,8 +434,8 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       wave_sync();
       for (uint32_t j = lb0 + lane; j < ncnt; j += 64) B[j] = NB[j];
     }
-    hint = min(hint, lb0);
-    cnt = ncnt;
+    hint = uniform(min(hint, lb0));
+    cnt = uniform(ncnt);
     wave_sync();
     if (regb) b = lane < cnt ? B[lane] : kEmptyKey;
   }
