@@ -103,6 +103,75 @@ def cpu_baseline(base: np.ndarray, queries: np.ndarray, target_s: float) -> dict
     }
 
 
+def _median_time(fn, runs: int = 3) -> float:
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def cpu_routines(cores: int) -> list:
+    """The rest of the reference's CPU path, each on a bounded sample, median
+    of 3 warm runs on `cores` threads (the rotation-matrix factorisation and
+    best_rescale_factor are sequential in the reference and run on one):
+    the config 1 exact scan in full, the host distance routines at d = 128,
+    96 and 960 (2M, 2M and 0.5M pairs from fixed pools), RaBitQ one-bit
+    quantisation of 250,000 of 1M x 128 rows, the best_rescale_factor loop of
+    get_const_scaling_factors (1,000 unit rows) and set_rotation_matrix at
+    d = 96, 128 and 960."""
+    import oracle
+    from jasper_amd import datasets
+    oracle.ensure_built()
+    items = []
+    base1, q1, _ = datasets.config("c1")
+    b1, qf = base1.astype(np.float32), q1.astype(np.float32)
+    oracle.bruteforce_ref(b1, qf, k=10, nthreads=cores)
+    t = _median_time(lambda: oracle.bruteforce_ref(b1, qf, k=10, nthreads=cores))
+    items.append({"routine": "exact kNN scan, config 1 in full (100 queries x 10,000 x 128, L2, top-10)",
+                  "value": len(q1) / t, "unit": "queries/s", "gflops": 2.0 * len(q1) * len(base1) * 128 / t / 1e9,
+                  "cores": cores})
+    rng = np.random.default_rng(7)
+    for d in (128, 96, 960):
+        pool = 1 << 17 if d <= 128 else 1 << 14
+        total = 2_000_000 if d <= 128 else 500_000
+        a = rng.standard_normal((pool, d)).astype(np.float16).view(np.uint16)
+        b = rng.standard_normal((pool, d)).astype(np.float16).view(np.uint16)
+        reps = (total + pool - 1) // pool
+
+        def run():
+            for _ in range(reps):
+                oracle.distance_pairs(a, b, "l2", nthreads=cores)
+        run_pairs = reps * pool
+        oracle.distance_pairs(a, b, "l2", nthreads=cores)
+        t = _median_time(run)
+        items.append({"routine": f"host L2 distance routine (distance.cuh l2_distance order), d={d}",
+                      "value": run_pairs / t, "unit": "distances/s",
+                      "gb_per_s": run_pairs * 4.0 * d / t / 1e9, "sample": f"{run_pairs} pairs from two "
+                      f"{pool}-row fp16 pools", "cores": cores})
+    x = rng.standard_normal((1_000_000, 128)).astype(np.float32)
+    P, _ = oracle.rotation_matrix(128, 42)
+    c = x.mean(axis=0)
+    xs = x[:250_000]
+    oracle.rabitq_quantize(x[:10000], P, c, nthreads=cores)
+    t = _median_time(lambda: oracle.rabitq_quantize(xs, P, c, nthreads=cores))
+    items.append({"routine": "RaBitQ one-bit quantize (rotation, residual, sign code, f_add, f_rescale) of "
+                             "250,000 rows of a 1,000,000 x 128 set (centroid = its mean)",
+                  "value": len(xs) / t, "unit": "vectors/s", "cores": cores})
+    del x, xs
+    o = rng.standard_normal((1000, 128)).astype(np.float32)
+    o = np.abs(o / np.linalg.norm(o, axis=1, keepdims=True)).astype(np.float32)
+    t = _median_time(lambda: oracle.const_scaling_factor(o, 1))
+    items.append({"routine": "best_rescale_factor over get_const_scaling_factors' 1,000 unit rows, d=128, 1 bit",
+                  "value": t * 1e3, "unit": "ms", "cores": 1})
+    for d in (96, 128, 960):
+        t = _median_time(lambda: oracle.rotation_matrix(d, 42), runs=3 if d <= 128 else 1)
+        items.append({"routine": f"set_rotation_matrix (N(0,1) matrix, Householder QR, sign fix), d={d}",
+                      "value": t * 1e3, "unit": "ms", "cores": 1})
+    return items
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,7 +181,7 @@ def main() -> int:
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--target-recall", type=float, default=0.95)
     ap.add_argument("--sweep", default="16,24,32,40,44,48,64,96,128,192,256")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--curve-out", default=None, help="also write the QPS/recall curve as JSON here")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -281,6 +350,9 @@ def main() -> int:
         t0 = time.perf_counter()
         result["cpu_baseline"] = cpu_baseline(base, queries, args.cpu_seconds)
         log(f"cpu baseline in {time.perf_counter() - t0:.1f}s: {result['cpu_baseline']['value']:.1f} q/s")
+        t0 = time.perf_counter()
+        result["cpu_baseline"]["routines"] = cpu_routines(result["cpu_baseline"]["cores"])
+        log(f"cpu routines in {time.perf_counter() - t0:.1f}s")
     if args.curve_out:
         with open(args.curve_out, "w") as f:
             json.dump(result, f, indent=1)

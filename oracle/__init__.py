@@ -121,6 +121,10 @@ def lib():
         _lib.jo_rabitq_code_bytes.argtypes = [i32]
         _lib.jo_rabitq_quantize.restype = None
         _lib.jo_rabitq_quantize.argtypes = [P, i64, i32, P, P, i32, P, P, i32]
+        _lib.jo_best_rescale_factor.restype = ctypes.c_double
+        _lib.jo_best_rescale_factor.argtypes = [P, i64, i32]
+        _lib.jo_const_scaling_factor.restype = ctypes.c_double
+        _lib.jo_const_scaling_factor.argtypes = [P, i64, i64, i32]
         _lib.jo_frontier_insert_seq.restype = None
         _lib.jo_frontier_insert_seq.argtypes = [P, P, i32, i32, P, P, P]
         _lib.jo_pq_encode.restype = None
@@ -605,6 +609,19 @@ def rabitq_quantize(x, P, centroid=None, metric: str = "l2", nthreads: int = 0, 
     f_rescale = np.ascontiguousarray(out[:, cb + 4:cb + 8]).view(np.float32).ravel()
     r = (out, out[:, :cb].copy(), f_add, f_rescale)
     return r + (res,) if return_residuals else r
+
+
+def best_rescale_factor(o_abs, ex_bits: int) -> float:
+    """best_rescale_factor (reference quantize.cuh:22-82) of one row o = |x|."""
+    o = np.ascontiguousarray(o_abs, dtype=np.float32).ravel()
+    return float(lib().jo_best_rescale_factor(_ptr(o), o.shape[0], int(ex_bits)))
+
+
+def const_scaling_factor(rows_abs, ex_bits: int) -> float:
+    """Mean of best_rescale_factor over rows (get_const_scaling_factors'
+    host loop, quantize.cuh:124-130)."""
+    r = np.ascontiguousarray(rows_abs, dtype=np.float32)
+    return float(lib().jo_const_scaling_factor(_ptr(r), r.shape[0], r.shape[1], int(ex_bits)))
 
 
 class RqArtifacts:

@@ -24,10 +24,12 @@
 // Sums run in index order in fp32 (the reference's cuBLAS and cg::reduce
 // orders are unspecified); parity with the device is a tolerance.
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <limits>
+#include <utility>
 #include <vector>
 
 #include <omp.h>
@@ -98,6 +100,68 @@ void jo_rabitq_quantize(const float* x, int64_t n, int dim, const float* P, cons
       if (resid_out) std::memcpy(resid_out + (size_t)v * dim, r.data(), (size_t)dim * 4);
     }
   }
+}
+
+// best_rescale_factor (reference quantize.cuh:22-82), the host routine behind
+// get_const_scaling_factors (:89-131). For o = |x| of a unit vector and
+// ex_bits bits it returns the scale t at which o_bar(t) = the per-dimension
+// counters, stepped one at a time in increasing order of their step
+// thresholds (o_bar_i + 1) / o_i, maximise <o_bar + 1/2, o> / |o_bar + 1/2|.
+// Counters start at floor(t0 * o_i + 1e-5), t0 = t_end * tight[ex_bits],
+// t_end = (2^ex_bits - 1 + 10) / max(o). Every dimension's first step is
+// taken; a later one only while the counter is below 2^ex_bits - 1 and its
+// threshold below t_end. Here all steps are listed first and swept in
+// (threshold, dimension) order, which is the order the reference's min-heap
+// pops them in. Sums are in double, as the reference's.
+double jo_best_rescale_factor(const float* o, int64_t dim, int ex_bits) {
+  static const double kTight[9] = {0, 0.15, 0.20, 0.52, 0.59, 0.71, 0.75, 0.77, 0.81};
+  const int top = (1 << ex_bits) - 1;
+  double mx = 0.0;
+  for (int64_t i = 0; i < dim; ++i) mx = std::max(mx, (double)o[i]);
+  const double t_end = (double)(top + 10) / mx;
+  const double t0 = t_end * kTight[ex_bits];
+  std::vector<int> bar((size_t)dim);
+  double num = 0.0, den = 0.25 * (double)dim;
+  for (int64_t i = 0; i < dim; ++i) {
+    const int b = (int)(t0 * (double)o[i] + 1e-5);
+    bar[(size_t)i] = b;
+    den += (double)b * b + b;
+    num += (b + 0.5) * (double)o[i];
+  }
+  // every step: the first one per dimension, then the ones its counter
+  // takes while below top with a threshold below t_end
+  std::vector<std::pair<double, int64_t>> steps;
+  for (int64_t i = 0; i < dim; ++i) {
+    int b = bar[(size_t)i] + 1;
+    steps.emplace_back((double)b / (double)o[i], i);
+    while (b < top) {
+      const double t = (double)(b + 1) / (double)o[i];
+      if (!(t < t_end)) break;
+      steps.emplace_back(t, i);
+      ++b;
+    }
+  }
+  std::sort(steps.begin(), steps.end());
+  double best_ip = 0.0, best_t = 0.0;
+  for (const auto& st : steps) {
+    const int b = ++bar[(size_t)st.second];
+    den += 2.0 * b;
+    num += (double)o[st.second];
+    const double ip = num / std::sqrt(den);
+    if (ip > best_ip) {
+      best_ip = ip;
+      best_t = st.first;
+    }
+  }
+  return best_t;
+}
+
+// get_const_scaling_factors' host loop (quantize.cuh:124-130): the mean of
+// best_rescale_factor over n rows of o = |x| (rows of length dim).
+double jo_const_scaling_factor(const float* rows, int64_t n, int64_t dim, int ex_bits) {
+  double sum = 0.0;
+  for (int64_t r = 0; r < n; ++r) sum += jo_best_rescale_factor(rows + (size_t)r * dim, dim, ex_bits);
+  return sum / (double)n;
 }
 
 }  // extern "C"

@@ -228,3 +228,62 @@ def test_estimate_tracks_exact_distance(metric):
     assert abs(err.mean()) < 0.02 * scale.mean()
     assert 0.6 * f < np.sqrt((err ** 2).mean()) / scale.mean() < 0.9 * f
     assert np.corrcoef(est.ravel(), exact.ravel())[0, 1] > 0.75
+
+
+# ------------------------------------------------ best_rescale_factor (host) --
+# The reference's host routine behind get_const_scaling_factors
+# (quantize.cuh:22-131). Pinned by a closed form and by an independent
+# restatement: a binary heap of step thresholds (the reference's structure)
+# with the ratio recomputed from scratch at every step.
+
+def _rescale_by_heap(o, ex_bits):
+    import heapq
+    tight = [0, 0.15, 0.20, 0.52, 0.59, 0.71, 0.75, 0.77, 0.81]
+    top = (1 << ex_bits) - 1
+    o = [float(v) for v in np.asarray(o, dtype=np.float32)]
+    t_end = (top + 10) / max(o)
+    t0 = t_end * tight[ex_bits]
+    bar = [int(t0 * v + 1e-5) for v in o]
+    heap = [((b + 1) / v, i) for i, (b, v) in enumerate(zip(bar, o))]
+    heapq.heapify(heap)
+    best, best_t = 0.0, 0.0
+    while heap:
+        t, i = heapq.heappop(heap)
+        bar[i] += 1
+        num = sum((b + 0.5) * v for b, v in zip(bar, o))
+        den = sum((b + 0.5) ** 2 for b in bar)
+        ip = num / np.sqrt(den)
+        if ip > best:
+            best, best_t = ip, t
+        if bar[i] < top:
+            tn = (bar[i] + 1) / o[i]
+            if tn < t_end:
+                heapq.heappush(heap, (tn, i))
+    return best_t
+
+
+def test_best_rescale_factor_one_dim_closed_form(oracle_lib):
+    # dim 1, one bit: t_end = 11 / x, the counter starts at floor(1.65) = 1
+    # and its one step (threshold 2 / x) raises the ratio from 0 to x
+    for x in (0.7, 0.05, 1.0):
+        xf = float(np.float32(x))
+        assert oracle.best_rescale_factor(np.array([x], np.float32), 1) == pytest.approx(2.0 / xf, rel=1e-15)
+
+
+@pytest.mark.parametrize("dim,ex_bits", [(8, 1), (16, 2), (32, 3), (24, 4), (128, 1)])
+def test_best_rescale_factor_matches_heap_restatement(oracle_lib, dim, ex_bits):
+    rng = np.random.default_rng(dim * 10 + ex_bits)
+    for _ in range(5):
+        x = rng.standard_normal(dim).astype(np.float32)
+        o = np.abs(x / np.linalg.norm(x)).astype(np.float32)
+        got = oracle.best_rescale_factor(o, ex_bits)
+        want = _rescale_by_heap(o, ex_bits)
+        assert got == pytest.approx(want, rel=1e-12), (got, want)
+
+
+def test_const_scaling_factor_is_the_mean(oracle_lib):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((20, 64)).astype(np.float32)
+    o = np.abs(x / np.linalg.norm(x, axis=1, keepdims=True)).astype(np.float32)
+    want = np.mean([oracle.best_rescale_factor(r, 1) for r in o])
+    assert oracle.const_scaling_factor(o, 1) == pytest.approx(want, rel=1e-12)
