@@ -172,6 +172,27 @@ def cpu_routines(cores: int) -> list:
     return items
 
 
+def general_path_run(args, bw: int, log) -> dict:
+    """The same build and search with the integer-row shortcuts off (the
+    packed-difference distances and the exact integer Gram prune), in a child
+    process (the switch is read once per process): config 2's numbers on the
+    path every other dataset takes."""
+    import subprocess
+    cmd = [sys.executable, "-u", os.path.abspath(__file__), "--int-exact", "0", "--sweep", str(bw), "--steps",
+           str(args.steps), "--warmup", str(args.warmup), "--n", str(args.n), "--nq", str(args.nq),
+           "--no-cpu-baseline"]
+    log(f"general path (JASPER_INT_EXACT=0) at bw={bw} in a child process")
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=1200)
+    if r.returncode != 0:
+        raise RuntimeError(f"general-path run failed with exit code {r.returncode}")
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    cfg = line["config"]
+    return {"beam_width": cfg["beam_width"], "qps": line["value"], "recall_at_10": cfg["recall_at_10"],
+            "ms_per_step": line["ms_per_step"], "kernel_ms": line["roofline"]["kernel_ms"],
+            "roofline_frac": line["roofline"]["frac"], "build_vectors_per_s": cfg["build_vectors_per_s"],
+            "build_s": cfg["build_s"], "kernel": line["roofline"]["kernel"]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,7 +218,13 @@ def main() -> int:
                          "(config 2: mark_deleted 10%%, consolidate, append 100k)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
+    ap.add_argument("--int-exact", type=int, default=1, choices=[0, 1],
+                    help="0: run with the integer-row shortcuts off (JASPER_INT_EXACT=0), the general "
+                         "distance and prune paths; the default search run also measures this in a child "
+                         "process at its chosen beam width")
     args = ap.parse_args()
+    if args.int_exact == 0:
+        os.environ["JASPER_INT_EXACT"] = "0"  # read by the library at its first range scan
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); every "
@@ -346,6 +373,8 @@ def main() -> int:
                           "vectors_scored": scored / args.nq},
         },
     }
+    if args.int_exact == 1 and args.path == "search":
+        result["config"]["general_path"] = general_path_run(args, chosen, log)
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
         result["cpu_baseline"] = cpu_baseline(base, queries, args.cpu_seconds)
@@ -768,6 +797,30 @@ def run_updates(args, torch, jasper_amd, datasets, dev, log):
     out = out.cpu().numpy()
     nid = new_ids.numpy()
     self_recall = float(np.mean([nid[i] in out[i] for i in range(min(nq, n_add))]))
+    g.free()
+    # The reference's append gate (cmd/test_append.cu:66-121): construct on the
+    # n rows, append the n_add new ones, search all appended rows themselves
+    # (limit 2 * bw) and count those found in their own top 10. Beside it the
+    # same rows searched in a graph built on all n + n_add rows at once: the
+    # gap between the two is what the append costs, the rest is the data.
+    def self_recall_of(graph, rows, want, bws=(64, 128)):
+        res = {}
+        for b in bws:
+            o, _ = graph.search(rows, k=10, beam_width=b)
+            o = o.cpu().numpy()
+            res[b] = float(np.mean((o == want[:, None]).any(axis=1)))
+        return res
+    want = np.arange(n, n + n_add)
+    ga = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2)
+    ga_ids = ga.append(extra, 1.2).numpy()
+    assert np.array_equal(ga_ids, want)
+    gate_append = self_recall_of(ga, extra, want)
+    ga.free()
+    gb = jasper_amd.Graph.build(torch.cat([base, extra]).contiguous(), n_neighbors=64, distance="l2", alpha=1.2)
+    gate_built = self_recall_of(gb, extra, want)
+    gb.free()
+    log(f"reference append gate: appended rows' self-recall@10 at bw 64 / 128: {gate_append[64]:.4f} / "
+        f"{gate_append[128]:.4f}; the same rows built in from the start: {gate_built[64]:.4f} / {gate_built[128]:.4f}")
     log(f"build {build_s:.2f}s; recall@10 bw={bw}: {r0:.4f} -> after deleting {n_del}: {r1:.4f} "
         f"(mark_deleted {del_ms:.1f} ms, viol={viol}) -> consolidate {cons_ms:.1f} ms: {r2:.4f} -> "
         f"append {n_add} in {add_ms:.1f} ms ({n_add / (add_ms / 1000.0):,.0f} vec/s): {r3:.4f}; "
@@ -780,7 +833,12 @@ def run_updates(args, torch, jasper_amd, datasets, dev, log):
                  "build_s": build_s, "mark_deleted_ms": del_ms, "consolidate_ms": cons_ms, "append_ms": add_ms,
                  "recall_built": r0, "recall_after_delete": r1, "recall_after_consolidate": r2,
                  "recall_after_append": r3, "viol": viol, "appended_self_recall_at_10": self_recall,
-                 "built_self_recall_at_10": base_self},
+                 "built_self_recall_at_10": base_self,
+                 "append_gate": {"protocol": f"build {n}, append {n_add}, search the {n_add} appended rows "
+                                             "(k 10, limit 2 bw) as cmd/test_append.cu does",
+                                 "self_recall_at_10_bw64": gate_append[64], "self_recall_at_10_bw128": gate_append[128],
+                                 "same_rows_built_in_bw64": gate_built[64],
+                                 "same_rows_built_in_bw128": gate_built[128]}},
                 None)
     res["steps"], res["warmup"] = 1, 0
     print(json.dumps(res), flush=True)
