@@ -1026,7 +1026,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         cw[g] = make_uint4(0u, 0u, 0u, 0u);
         if ((uint32_t)g < a.pq_groups) {
           const uint8_t* cp = crow + (size_t)g * a.R * a.pq_w;
-          if (a.pq_w == 16) {
+          if (P > 1 || a.pq_w == 16) {  // more than one group: M > 16, groups of 16
             cw[g] = *reinterpret_cast<const uint4*>(cp);
           } else if (a.pq_w == 8) {
             const uint2 t2 = *reinterpret_cast<const uint2*>(cp);
