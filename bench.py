@@ -44,11 +44,11 @@ METRIC = "QPS @ recall@10≥0.95, 1M×128 fp16 synthetic; build vectors/sec"
 PEAK_HBM_GBS = 8000.0
 
 
-def measured_traffic(beam_width: int, n: int, nq: int):
-    """HBM bytes per launch of the search kernel from the committed rocprofv3
+def measured_traffic(beam_width: int, n: int, nq: int, profile: str = "beam_search_c2_1M_pmc.md"):
+    """HBM bytes per launch of a kernel from a committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary, when it covers this exact workload;
     None otherwise (the counters cannot be read from inside this process)."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "beam_search_c2_1M_pmc.md")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
     try:
         with open(path) as f:
             text = f.read()
@@ -371,6 +371,11 @@ def main() -> int:
             "algorithmic_bytes_per_launch": alg_bytes,
             "per_query": {"hops": hops / args.nq, "adjacency_entries": deg / args.nq,
                           "vectors_scored": scored / args.nq},
+            # what a kernel that fetches every adjacency entry's vector would
+            # move (2 dp bytes per entry, the reference-equivalent figure),
+            # and the rate it would need to match this launch's time
+            "reference_equivalent_bytes_per_launch": int(deg * 2 * 128),
+            "reference_equivalent_gbs": deg * 2 * 128 / (kernel_ms / 1000.0) / 1e9,
         },
     }
     if args.int_exact == 1 and args.path == "search":
@@ -486,7 +491,8 @@ def run_directional(args, torch, jasper_amd, datasets, dev, log, use_pq=False):
                  "beam_width": chosen, "recall_at_10": rec, "build_s": build_s,
                  "build_vectors_per_s": n / build_s, "curve": curve, "curve_exact_search": plain},
                 {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
-                 "traffic": None, "kernel": f"directional_kernel<IP,{'PQ' if use_pq else 'LSH'}>",
+                 "traffic": None if use_pq else measured_traffic(chosen, n, nq, "directional_c3_1M_pmc.md"),
+                 "kernel": f"directional_kernel<IP,{'PQ' if use_pq else 'LSH'}>",
                  "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
                  "per_query": {"visits": float(st[:, 0].mean()), "hops": float(st[:, 1].mean()),
                                "adjacency_entries": float(st[:, 2].mean())}})
