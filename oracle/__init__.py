@@ -70,6 +70,13 @@ def lib():
         _lib.jo_max_batch_size.argtypes = [i64, i32, i64]
         _lib.jo_build.restype = i32
         _lib.jo_build.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, P, P, P, i32, P]
+        _lib.jo_build_scale.restype = i32
+        _lib.jo_build_scale.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, i64, i64, P, P, P, i32]
+        _lib.jo_scale_merge_order.restype = i64
+        _lib.jo_scale_merge_order.argtypes = [i64, P]
+        _lib.jo_prune_scale.restype = i32
+        _lib.jo_prune_scale.argtypes = [P, i32, i32, i32, f32, i32, i64, i64, i64, i64, ctypes.c_uint32, P, P,
+                                        i32, P, P]
         _lib.jo_build_rq.restype = i32
         _lib.jo_build_rq.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, i32, P, P, P, P, P, i32, P]
         _lib.jo_last_capped_groups.restype = i64
@@ -622,6 +629,65 @@ def const_scaling_factor(rows_abs, ex_bits: int) -> float:
     host loop, quantize.cuh:124-130)."""
     r = np.ascontiguousarray(rows_abs, dtype=np.float32)
     return float(lib().jo_const_scaling_factor(_ptr(r), r.shape[0], r.shape[1], int(ex_bits)))
+
+
+def build_scale(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2, n_parts: int = 2,
+                workspace_budget: int = 10 ** 10, part_batch: int | None = None,
+                merge_batch: int | None = None, nthreads: int = 0) -> OracleGraph:
+    """The partitioned build (reference index/construct_scale.cuh:68-450):
+    n_parts contiguous partitions of ceil(n / n_parts) rows built on their own
+    (batches doubling up to part_batch), their edges offset to global ids,
+    then every pair of partitions merged once in the reference's cyclic order
+    with B1 in batches of merge_batch. Defaults follow the reference
+    (construct_scale.cuh:96-99 and 383-385, cmd/create_scale_index.cu:84):
+    part_batch = min(budget batch, n / n_parts / 20), merge_batch = budget
+    batch. Global ids; medoid 0."""
+    v16 = as_padded_f16(vectors)
+    n, dp = v16.shape
+    dim = np.asarray(vectors).shape[1]
+    # max_batch_size_for_budget (construct.cuh:238-262), without the FFI's n / 50 cap
+    per_item = 8 * 64 + 8 * 256 + 4 + 8 * (256 + R) + 4 + 8 * R + 4 * R + 4 * R
+    budget_batch = max(1, (workspace_budget - 4) // per_item)
+    if part_batch is None:
+        part_batch = max(1, min(budget_batch, n // n_parts // 20))
+    if merge_batch is None:
+        merge_batch = budget_batch
+    edges = np.empty((n, R), dtype=np.uint32)
+    edist = np.empty((n, R), dtype=np.uint16)
+    counts = np.empty(n, dtype=np.uint8)
+    rc = lib().jo_build_scale(_ptr(v16), n, dp, dim, R, metric_code(distance), float(alpha), n_parts,
+                              part_batch, merge_batch, _ptr(edges), _ptr(edist), _ptr(counts), nthreads)
+    if rc != 0:
+        raise ValueError("build_scale: bad arguments (empty partition or batch < 1)")
+    g = OracleGraph(v16, edges, edist, counts, R, dim, distance)
+    g.n_parts = n_parts
+    g.part_batch = part_batch
+    g.merge_batch = merge_batch
+    return g
+
+
+def scale_merge_order(n_parts: int) -> list:
+    """The (B1, B2) partition pairs in the order the partitioned build merges
+    them (reference index/construct_scale.cuh:386-445)."""
+    out = np.empty(max(1, n_parts * (n_parts - 1)), dtype=np.int64)
+    m = int(lib().jo_scale_merge_order(n_parts, _ptr(out)))
+    return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(m)]
+
+
+def prune_scale(vectors, b1: tuple, b2: tuple, self_id: int, cand_ids, cand_dists, R: int,
+                alpha: float = 1.2, distance: str = "l2"):
+    """The merge prune on one sorted candidate list (reference
+    index/construct_scale_kernels.cuh:22-139): b1 / b2 are (first, count)
+    row ranges whose vectors are resolvable. Returns (ids, dists)."""
+    v16 = as_padded_f16(vectors)
+    dim = np.asarray(vectors).shape[1]
+    ids = np.ascontiguousarray(cand_ids, dtype=np.uint32)
+    dists = np.ascontiguousarray(cand_dists, dtype=np.float32)
+    out_i = np.empty(R, dtype=np.uint32)
+    out_d = np.empty(R, dtype=np.float32)
+    ns = lib().jo_prune_scale(_ptr(v16), v16.shape[1], dim, metric_code(distance), float(alpha), R, b1[0], b1[1],
+                              b2[0], b2[1], self_id, _ptr(ids), _ptr(dists), len(ids), _ptr(out_i), _ptr(out_d))
+    return out_i[:ns].copy(), out_d[:ns].copy()
 
 
 class RqArtifacts:

@@ -17,6 +17,7 @@
 // is off so that the only fused multiply-adds are the explicit fmaf() calls.
 
 #include <algorithm>
+#include <numeric>
 #include <atomic>
 #include <cfloat>
 #include <cmath>
@@ -538,6 +539,239 @@ int jo_build_rq(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int 
       process_batches(g, dim_for_prune, alpha, 0, n, max_batch, true, 0u, edges, edge_dist, counts, &rqb);
   if (n_batches_out) *n_batches_out = nb;
   return 0;
+}
+
+// ------------------------------------------------------- partitioned build --
+// intermediate_graph (reference index/construct_scale.cuh:68-330 with
+// construct_scale_kernels.cuh:23-330): the rows are cut into n_parts
+// contiguous partitions of ceil(n / n_parts) rows, each built on its own
+// (construct_graph with batches doubling up to part_batch), its edge ids
+// shifted to global ids; then every unordered pair of partitions is merged
+// once, in the reference's cyclic order (merge(), :391-450). A merge (B1,
+// B2) walks B1 in batches of merge_batch (not crossing a 2^20-row segment
+// boundary of B1, :358-365) and per batch:
+//   (i)   searches B2's graph with each batch row (k = L = 64, beam width
+//         64, limit 256, 256 visits kept); B2's edges to other partitions
+//         are out of its range and skipped;
+//   (ii)  per batch row: its edges and the visits (as global ids), sorted by
+//         (distance, id), then the merge prune below, into B1;
+//   (iii) reverse pairs (neighbour, row) of the batch's new rows whose
+//         neighbour is in B2, grouped by neighbour; per B2 target: its
+//         edges, then the sources (distances computed; this restatement
+//         takes them in ascending id), capped at 256 + R, sorted, then the
+//         merge prune, into B2.
+// The merge prune (robust_prune_kernel_scale, :23-139) keeps a candidate
+// whose vector is in neither partition without testing it, and tests
+// candidates only against selected members whose vectors are in B1 or B2.
+namespace {
+
+struct ScaleRange {
+  const uint16_t* vecs;
+  int dp;
+  int64_t b1s, n1, b2s, n2;
+  const uint16_t* row(uint32_t id) const {
+    if ((int64_t)id >= b1s && (int64_t)id < b1s + n1) return vecs + (size_t)id * dp;
+    if ((int64_t)id >= b2s && (int64_t)id < b2s + n2) return vecs + (size_t)id * dp;
+    return nullptr;
+  }
+};
+
+int robust_prune_scale(const ScaleRange& sr, int metric, int dim_for_prune, uint32_t self,
+                       const std::vector<Cand>& C, float alpha, int R, Cand* sel) {
+  int ns = 0;
+  for (const Cand& c : C) {
+    if (ns >= R) break;
+    if (c.id == self || c.id == kInvalid32) continue;
+    const uint16_t* cv = sr.row(c.id);
+    if (!cv) {  // "we cant prune this, but we need to keep it"
+      sel[ns++] = c;
+      continue;
+    }
+    bool pruned = false;
+    for (int j = 0; j < ns && !pruned; ++j) {
+      const uint16_t* sv = sr.row(sel[j].id);
+      if (!sv) continue;
+      if (dist(metric, cv, sv, dim_for_prune) * alpha < c.dist) pruned = true;
+    }
+    if (!pruned) sel[ns++] = c;
+  }
+  return ns;
+}
+
+void scale_merge(const uint16_t* vecs, int dp, int dim_for_prune, int R, int metric, float alpha, int64_t b1s,
+                 int64_t n1, int64_t b2s, int64_t n2, int64_t merge_batch, uint32_t* edges, uint16_t* edge_dist,
+                 uint8_t* counts) {
+  const int L = 64, LIMIT = 256, MAX_RESULT = 256, max_cands = MAX_RESULT + R;
+  const int64_t kSegment = (int64_t)1 << 20;
+  const ScaleRange sr{vecs, dp, b1s, n1, b2s, n2};
+  std::vector<uint32_t> local((size_t)n2 * R);
+  std::vector<std::vector<Entry>> visited;
+  std::vector<uint64_t> pairs;
+  int64_t count = 0;
+  while (count < n1) {
+    const int64_t bs = std::min({merge_batch, n1 - count, kSegment - count % kSegment});
+    // B2's adjacency with ids local to B2 (others past its range)
+    for (int64_t w = 0; w < n2; ++w)
+      for (int e = 0; e < R; ++e) {
+        const uint32_t x = edges[(size_t)(b2s + w) * R + e];
+        local[(size_t)w * R + e] = ((int64_t)x >= b2s && (int64_t)x < b2s + n2) ? (uint32_t)(x - b2s) : kInvalid32;
+      }
+    const Graph g2{vecs + (size_t)b2s * dp, n2, dp, local.data(), counts + b2s, R, nullptr, metric};
+    visited.assign((size_t)bs, {});
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t i = 0; i < bs; ++i)
+      search_one(g2, vecs + (size_t)(b1s + count + i) * dp, 0u, (uint32_t)L, (uint32_t)LIMIT, (uint32_t)MAX_RESULT,
+                 true, &visited[(size_t)i], nullptr, nullptr);
+#pragma omp parallel
+    {
+      std::vector<Cand> C;
+      std::vector<Cand> sel((size_t)R);
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t i = 0; i < bs; ++i) {
+        const uint32_t v = (uint32_t)(b1s + count + i);
+        C.clear();
+        for (uint32_t e = 0; e < counts[v]; ++e) {
+          const uint32_t w = edges[(size_t)v * R + e];
+          if (w == kInvalid32) continue;
+          C.push_back({w, bf2f(edge_dist[(size_t)v * R + e])});
+        }
+        for (const Entry& x : visited[(size_t)i]) {
+          const uint32_t gid = x.id == kInvalid31 ? kInvalid32 : (uint32_t)(b2s + x.id);
+          if (gid != v && gid != kInvalid32) C.push_back({gid, x.dist});
+        }
+        if ((int)C.size() > max_cands) C.resize((size_t)max_cands);
+        std::sort(C.begin(), C.end(), cand_less);
+        const int ns = robust_prune_scale(sr, metric, dim_for_prune, v, C, alpha, R, sel.data());
+        for (int j = 0; j < ns; ++j) {
+          edges[(size_t)v * R + j] = sel[(size_t)j].id;
+          edge_dist[(size_t)v * R + j] = f2bf(sel[(size_t)j].dist);
+        }
+        counts[v] = (uint8_t)ns;
+      }
+    }
+    pairs.clear();
+    for (int64_t i = 0; i < bs; ++i) {
+      const uint32_t v = (uint32_t)(b1s + count + i);
+      for (uint32_t e = 0; e < counts[v]; ++e) {
+        const uint32_t w = edges[(size_t)v * R + e];
+        if ((int64_t)w >= b2s && (int64_t)w < b2s + n2) pairs.push_back(((uint64_t)w << 32) | v);
+      }
+    }
+    std::sort(pairs.begin(), pairs.end());
+    std::vector<size_t> heads;
+    for (size_t q = 0; q < pairs.size(); ++q)
+      if (q == 0 || (pairs[q] >> 32) != (pairs[q - 1] >> 32)) heads.push_back(q);
+    heads.push_back(pairs.size());
+#pragma omp parallel
+    {
+      std::vector<Cand> C;
+      std::vector<Cand> sel((size_t)R);
+      const int64_t n_groups = (int64_t)heads.size() - 1;
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t h = 0; h < n_groups; ++h) {
+        const uint32_t w = (uint32_t)(pairs[heads[(size_t)h]] >> 32);
+        C.clear();
+        for (uint32_t e = 0; e < counts[w]; ++e) {
+          const uint32_t x = edges[(size_t)w * R + e];
+          if (x == kInvalid32) continue;
+          C.push_back({x, bf2f(edge_dist[(size_t)w * R + e])});
+        }
+        const uint16_t* wv = vecs + (size_t)w * dp;
+        for (size_t q = heads[(size_t)h]; q < heads[(size_t)h + 1]; ++q) {
+          if ((int)C.size() >= max_cands) break;
+          const uint32_t v = (uint32_t)(pairs[q] & 0xFFFFFFFFu);
+          if (v == w) continue;
+          const uint16_t* vv = sr.row(v);
+          if (!vv) continue;
+          C.push_back({v, dist(metric, wv, vv, dim_for_prune)});
+        }
+        std::sort(C.begin(), C.end(), cand_less);
+        const int ns = robust_prune_scale(sr, metric, dim_for_prune, w, C, alpha, R, sel.data());
+        for (int j = 0; j < ns; ++j) {
+          edges[(size_t)w * R + j] = sel[(size_t)j].id;
+          edge_dist[(size_t)w * R + j] = f2bf(sel[(size_t)j].dist);
+        }
+        counts[w] = (uint8_t)ns;
+      }
+    }
+    count += bs;
+  }
+}
+
+}  // namespace
+
+// The merge order of intermediate_graph::merge (construct_scale.cuh:386-445):
+// for each interval itv = 1 .. P/2 the pairs (B1, B1 + itv mod P) walk
+// cycles of P / gcd(itv, P) calls (one call when the cycle has length 2), B1
+// taking the previous call's B2, and the next cycle starting one partition
+// further on. Writes (B1, B2) pairs to out; returns the number of merges.
+int64_t jo_scale_merge_order(int64_t P, int64_t* out) {
+  int64_t B1 = 0, m = 0;
+  for (int64_t itv = 1; itv <= P / 2; ++itv) {
+    const int64_t gg = std::gcd(itv, P), cycle_len = P / gg;
+    const int64_t calls = cycle_len == 2 ? 1 : cycle_len;
+    for (int64_t cyc = 0; cyc < gg; ++cyc) {
+      if (cyc > 0) B1 = (B1 + 1) % P;
+      for (int64_t step = 0; step < calls; ++step) {
+        const int64_t B2 = (B1 + itv) % P;
+        out[2 * m] = B1;
+        out[2 * m + 1] = B2;
+        ++m;
+        B1 = B2;
+      }
+    }
+  }
+  return m;
+}
+
+// The partitioned build above. Outputs as jo_build (global ids); medoid = 0.
+// Returns -1 on bad arguments (a partition would be empty).
+int jo_build_scale(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, int metric, float alpha,
+                   int64_t n_parts, int64_t part_batch, int64_t merge_batch, uint32_t* edges, uint16_t* edge_dist,
+                   uint8_t* counts, int nthreads) {
+  if (n <= 0) return 0;
+  if (n_parts < 1 || part_batch < 1 || merge_batch < 1) return -1;
+  const int64_t part = (n + n_parts - 1) / n_parts;
+  if (part * (n_parts - 1) >= n) return -1;
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  g_capped_groups.store(0);
+  std::fill(counts, counts + n, (uint8_t)0);
+  std::fill(edges, edges + (size_t)n * R, kInvalid32);
+  std::fill(edge_dist, edge_dist + (size_t)n * R, (uint16_t)0);
+  for (int64_t p = 0; p < n_parts; ++p) {
+    const int64_t s = p * part, c = std::min(part, n - s);
+    uint32_t* e = edges + (size_t)s * R;
+    Graph g{vecs + (size_t)s * dp, c, dp, e, counts + s, R, nullptr, metric};
+    process_batches(g, dim_for_prune, alpha, 0, c, part_batch, true, 0u, e, edge_dist + (size_t)s * R, counts + s);
+    for (int64_t i = 0; i < c; ++i)
+      for (uint32_t j = 0; j < counts[s + i]; ++j) e[(size_t)i * R + j] += (uint32_t)s;
+  }
+  std::vector<int64_t> order((size_t)(n_parts * (n_parts - 1)));
+  const int64_t n_merges = jo_scale_merge_order(n_parts, order.data());
+  for (int64_t m = 0; m < n_merges; ++m) {
+    const int64_t b1s = order[(size_t)(2 * m)] * part, b2s = order[(size_t)(2 * m + 1)] * part;
+    scale_merge(vecs, dp, dim_for_prune, R, metric, alpha, b1s, std::min(part, n - b1s), b2s,
+                std::min(part, n - b2s), merge_batch, edges, edge_dist, counts);
+  }
+  return 0;
+}
+
+// The merge prune on one hand-made candidate list (test hook): B1 = rows
+// [b1s, b1s + n1), B2 = rows [b2s, b2s + n2) of vecs; candidates already
+// sorted. Returns the number selected.
+int jo_prune_scale(const uint16_t* vecs, int dp, int dim_for_prune, int metric, float alpha, int R, int64_t b1s,
+                   int64_t n1, int64_t b2s, int64_t n2, uint32_t self, const uint32_t* cand_ids,
+                   const float* cand_dists, int n_cands, uint32_t* out_ids, float* out_dists) {
+  const ScaleRange sr{vecs, dp, b1s, n1, b2s, n2};
+  std::vector<Cand> C((size_t)n_cands);
+  for (int i = 0; i < n_cands; ++i) C[(size_t)i] = {cand_ids[i], cand_dists[i]};
+  std::vector<Cand> sel((size_t)R);
+  const int ns = robust_prune_scale(sr, metric, dim_for_prune, self, C, alpha, R, sel.data());
+  for (int j = 0; j < ns; ++j) {
+    out_ids[j] = sel[(size_t)j].id;
+    out_dists[j] = sel[(size_t)j].dist;
+  }
+  return ns;
 }
 
 // append_batch (construct.cuh:1169-1265): the rows [first, n) were appended
