@@ -216,6 +216,25 @@ int64_t jasperx_exact_search(int64_t handle, const void* queries, int64_t n_quer
 int64_t jasperx_construct_directional_ex(const char* config, const void* vectors, int64_t n_vectors, int64_t dim,
                                          double alpha, int64_t workspace_budget_bytes, bool on_host,
                                          bool prerotate, int64_t prerotate_seed, uint32_t options, void* stream);
+/* The partitioned build of cmd/create_scale_index.cu:57-98 (the reference
+ * exposes it only as that command; no FFI binding): include/jasper/index/
+ * construct_scale.cuh intermediate_graph::allocate_and_construct (:83-128)
+ * with n_parts partitions of ceil(n / n_parts) rows, then merge() (:378-446).
+ * config: a plain config id (e.g. "f16_r64_l2"); vectors [n_vectors, dim]
+ * fp16 (host or device); partitions are built in batches of up to
+ * min(budget batch, max_batch_size), max_batch_size <= 0 meaning the
+ * command's n / n_parts / 20; merges in batches of the budget batch. The
+ * graph is resident in device memory (the reference stages partitions
+ * through host memory; the result is the same); returns a plain-config
+ * handle (search / save / updates as for jasper_construct_<config>).
+ * Errors: a partition would be empty, a budget below one batch item. */
+int64_t jasperx_construct_scale(const char* config, const void* vectors, int64_t n_vectors, int64_t dim,
+                                double alpha, int64_t n_parts, int64_t workspace_budget_bytes,
+                                int64_t max_batch_size, void* stream);
+/* Times of the last partitioned build: {partition builds ms, merges ms,
+ * total ms, merges, merge batches, partition batch size, merge batch
+ * size}. */
+int64_t jasperx_last_scale_stats(double* out7);
 /* One-bit RaBitQ codes of a directional graph's stored rows (rotated rows
  * when prerotated): the reference's quantizer (rabitq/quantize.cuh:322-354)
  * on the rows as stored, against their mean; they feed the RaBitQ estimator

@@ -101,6 +101,8 @@ _AGNOSTIC = {
     "jasperx_construct_directional_ex": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, ctypes.c_bool,
                                          ctypes.c_bool, _i64, ctypes.c_uint32, _ptr],
     "jasperx_export_rabitq": [_i64, _ptr, _ptr],
+    "jasperx_construct_scale": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, _i64, _i64, _ptr],
+    "jasperx_last_scale_stats": [_ptr],
     "jasperx_directional_search_noalloc": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64,
                                            _i64, ctypes.c_uint32, _ptr],
     "jasperx_directional_search_ex": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
@@ -370,6 +372,31 @@ class Graph:
                    is_directional=True, k_ranks=k_ranks, has_lsh=build_lsh, has_pq=build_pq,
                    has_rabitq=build_rabitq,
                    prerotate=resolved_prerotate, prerotate_seed=prerotate_seed)
+
+    @classmethod
+    def build_scale(cls, vectors: torch.Tensor, n_neighbors: int = 32,
+                    distance: DistanceFunc | str = DistanceFunc.L2, alpha: float = 1.2, n_parts: int = 2,
+                    workspace_budget: str = "10GB", max_batch_size: int | None = None) -> "Graph":
+        """The partitioned build of the reference's create_scale_index command
+        (cmd/create_scale_index.cu:57-98; include/jasper/index/
+        construct_scale.cuh): n_parts partitions built on their own, then
+        every pair merged. max_batch_size caps the partitions' batches (None:
+        n / n_parts / 20, as the command sets it); merges use the workspace
+        budget's batch. Returns a plain graph (search, save, updates)."""
+        if isinstance(distance, str):
+            distance = DistanceFunc(distance)
+        if vectors.ndim != 2:
+            raise ValueError(f"vectors must be 2D, got {vectors.ndim}D")
+        if vectors.dtype != torch.float16:
+            raise ValueError(f"Unsupported tensor dtype: {vectors.dtype}. Use torch.float16.")
+        vectors = vectors.contiguous()
+        n, dim = vectors.shape
+        config_id = _resolve_config(DataType.FLOAT16, n_neighbors, distance)
+        stream = _stream_ptr(vectors.device if vectors.is_cuda else None)
+        handle = _agnostic("jasperx_construct_scale")(
+            config_id.encode(), _tensor_ptr(vectors), n, dim, float(alpha), int(n_parts),
+            parse_storage_size(workspace_budget), int(max_batch_size or 0), stream)
+        return cls(handle, config_id, DataType.FLOAT16, distance, n_neighbors, dim)
 
     # -- properties ---------------------------------------------------------
     @property
@@ -724,6 +751,14 @@ def last_build_stats() -> dict:
     return dict(zip(keys, out.tolist()))
 
 
+def last_scale_stats() -> dict:
+    """Times and batch counts of the last partitioned build (Graph.build_scale)."""
+    out = np.zeros(7, dtype=np.float64)
+    _agnostic("jasperx_last_scale_stats")(out.ctypes.data_as(_ptr))
+    keys = ["partition_ms", "merge_ms", "total_ms", "merges", "merge_batches", "part_batch", "merge_batch"]
+    return dict(zip(keys, out.tolist()))
+
+
 # ── Utilities (reference __init__.py:770-946) ─────────────────────────
 
 def read_bin(path: str, dtype: str = "f32", max_vectors: int = 0) -> torch.Tensor:
@@ -778,7 +813,7 @@ from .groundtruth import bruteforce_knn, generate_groundtruth  # noqa: E402
 __all__ = [
     "Graph", "DistanceFunc", "DataType", "JasperError", "read_bin", "read_groundtruth",
     "get_recall", "generate_groundtruth", "bruteforce_knn", "save_groundtruth", "parse_storage_size",
-    "last_build_stats", "library_path",
+    "last_build_stats", "last_scale_stats", "library_path",
 ]
 
 

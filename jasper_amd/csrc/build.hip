@@ -30,6 +30,7 @@
 #include <rocprim/device/device_scan.hpp>
 
 #include <algorithm>
+#include <numeric>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -41,14 +42,17 @@ constexpr uint32_t kBuildLimit = 256;     // BEAM_SEARCH_LIMIT (construct.cuh:57
 constexpr uint32_t kBuildMaxResult = 256; // beam_search_max_result_size (construct.cuh:62)
 constexpr uint32_t kCandBuf = 512;        // >= 256 + R, power of two
 
-int64_t reference_max_batch(int64_t n, uint32_t R, int64_t budget_bytes) {
+int64_t budget_max_batch(uint32_t R, int64_t budget_bytes) {
   const int64_t L = kBuildL, max_result = kBuildMaxResult, max_cands = max_result + R;
   const int64_t per_item = 8 * L + 8 * max_result + 4 + 8 * max_cands + 4 + 8 * (int64_t)R + 4 * (int64_t)R +
                            4 * (int64_t)R;
   const int64_t fixed = 4;
-  int64_t b = budget_bytes <= fixed ? 0 : (budget_bytes - fixed) / per_item;
-  b = std::min<int64_t>(b, 0xFFFFFFFFll);
-  return std::min<int64_t>(b, n / 50);
+  const int64_t b = budget_bytes <= fixed ? 0 : (budget_bytes - fixed) / per_item;
+  return std::min<int64_t>(b, 0xFFFFFFFFll);
+}
+
+int64_t reference_max_batch(int64_t n, uint32_t R, int64_t budget_bytes) {
+  return std::min<int64_t>(budget_max_batch(R, budget_bytes), n / 50);
 }
 
 struct PruneKernelArgs {
@@ -169,7 +173,11 @@ static float gram_margin_scale() {
 static size_t prune_lds_bytes() { return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4; }
 static_assert(kGramLdsWords <= kCandBuf, "the Gram prune's scratch reuses the source list");
 
-template <int CPL, int METRIC, bool INTX>
+// SCALE: a merge of the partitioned build (B1 batch against B2): the merge
+// prune, and reverse pairs only for targets in B2 (r2 of the prune context;
+// process_reverse_edges_kernel_scale skips the others,
+// index/construct_scale_kernels.cuh:193-194).
+template <int CPL, int METRIC, bool INTX, bool SCALE>
 __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
@@ -195,10 +203,12 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   }
   wave_sync();
   sort_candidates(l.C, nc);
-  const uint32_t ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  const uint32_t ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   write_selection(a, v, ns, l.S_ids, l.S_dist);
   if (lane < R) {
-    a.pairs[(size_t)bid * R + lane] = lane < ns ? (((uint64_t)l.S_ids[lane] << a.pair_shift) | bid) : kEmptyKey;
+    const uint32_t t = lane < ns ? l.S_ids[lane] : 0u;
+    const bool pair = lane < ns && (!SCALE || t - a.pc.r2_lo < a.pc.r2_n);
+    a.pairs[(size_t)bid * R + lane] = pair ? (((uint64_t)t << a.pair_shift) | bid) : kEmptyKey;
   }
 }
 
@@ -244,7 +254,7 @@ constexpr int reverse_waves_per_simd() {
   return CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
 }
 
-template <int CPL, int METRIC, bool INTX>
+template <int CPL, int METRIC, bool INTX, bool SCALE>
 __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void reverse_prune_kernel(PruneKernelArgs a) {
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
@@ -302,7 +312,9 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
     const uint32_t nc = nE + taken;
     sort_candidates(l.C, nc);
     uint32_t ns;
-    if constexpr (CPL >= 1 && CPL <= 4) {
+    if constexpr (SCALE) {
+      ns = robust_prune_wave<CPL, METRIC, INTX, true>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+    } else if constexpr (CPL >= 1 && CPL <= 4) {
       // up to 96 candidates of rows of up to 128 values: pair distances on
       // the matrix cores, exact for integer rows, proved otherwise
       const uint32_t climit = METRIC == kL2 ? a.pc.nlimit : (a.pc.nlimit + 7u) / 8u;
@@ -330,30 +342,30 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
   }
 }
 
-template <int CPL, int METRIC, bool INTX>
+template <int CPL, int METRIC, bool INTX, bool SCALE>
 static void launch_forward(const PruneKernelArgs& a, uint32_t bs, size_t lds, hipStream_t s) {
-  auto k = forward_prune_kernel<CPL, METRIC, INTX>;
+  auto k = forward_prune_kernel<CPL, METRIC, INTX, SCALE>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
   hipLaunchKernelGGL(k, dim3(bs), dim3(64), lds, s, a);
 }
 
-template <int CPL, int METRIC, bool INTX>
+template <int CPL, int METRIC, bool INTX, bool SCALE>
 static void launch_reverse(const PruneKernelArgs& a, uint32_t grid, size_t lds, hipStream_t s) {
-  auto k = reverse_prune_kernel<CPL, METRIC, INTX>;
+  auto k = reverse_prune_kernel<CPL, METRIC, INTX, SCALE>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
   hipLaunchKernelGGL(k, dim3(grid), dim3(64), lds, s, a);
 }
 
-template <int METRIC, bool INTX>
+template <int METRIC, bool INTX, bool SCALE = false>
 static void dispatch_prune(bool reverse, uint32_t cpl, const PruneKernelArgs& a, uint32_t grid, size_t lds,
                            hipStream_t s) {
   switch (cpl) {
-#define JA_CASE(C)                                                   \
-  case C:                                                            \
-    if (reverse) launch_reverse<C, METRIC, INTX && C != 0>(a, grid, lds, s); \
-    else launch_forward<C, METRIC, INTX && C != 0>(a, grid, lds, s);         \
+#define JA_CASE(C)                                                                  \
+  case C:                                                                           \
+    if (reverse) launch_reverse<C, METRIC, INTX && C != 0, SCALE>(a, grid, lds, s); \
+    else launch_forward<C, METRIC, INTX && C != 0, SCALE>(a, grid, lds, s);         \
     break;
     JA_CASE(0)
     JA_CASE(1)
@@ -396,20 +408,10 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
   build_range(g, alpha, 0, g.n, max_batch, true, stream, time_stages, stats, rabitq_search);
 }
 
-void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max_batch, bool doubling,
-                 hipStream_t stream, bool time_stages, BuildStats* stats, bool rabitq_search) {
-  if (rabitq_search && !g.rabitq) throw std::invalid_argument("RaBitQ build search needs the RaBitQ codes");
-  if (last <= first) return;
-  if (first < 0 || last > g.n) throw std::invalid_argument("vertex range outside the graph");
-  if (max_batch < 1) max_batch = 1;  // the reference loops forever here (n < 50); clamp instead
-  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
-  const uint32_t nchunks = g.dp / 8;
-  // chunks per quad lane held in registers; 0 streams rows longer than 32 chunks
-  const uint32_t cpl = (nchunks + 3) / 4 > 8 ? 0u : (nchunks + 3) / 4;
-  const int64_t mb = std::min<int64_t>(max_batch, last - first);
-  const uint32_t R = g.R;
-
-  // workspace
+// Device workspace of one build pass for batches of up to mb vertices:
+// the search's popped keys, reverse pairs (unsorted and sorted), group
+// heads and the radix sort's temporary storage. Freed on destruction.
+struct BuildWorkspace {
   uint64_t* visited = nullptr;
   uint32_t* vcounts = nullptr;
   uint64_t* pairs = nullptr;
@@ -417,9 +419,28 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
   uint32_t* heads = nullptr;
   uint32_t* nheads = nullptr;
   void* temp = nullptr;
-  const size_t max_pairs = (size_t)mb * R;
-  const size_t temp_bytes = sort_u64_temp_bytes(max_pairs);
-  auto cleanup = [&]() {
+  size_t temp_bytes = 0;
+
+  BuildWorkspace(int64_t mb, uint32_t R) {
+    const size_t max_pairs = (size_t)mb * R;
+    temp_bytes = sort_u64_temp_bytes(max_pairs);
+    try {
+      hip_check(hipMalloc(&visited, (size_t)mb * kBuildMaxResult * 8), "alloc build visited");
+      hip_check(hipMalloc(&vcounts, (size_t)mb * 4), "alloc build visited counts");
+      hip_check(hipMalloc(&pairs, max_pairs * 8), "alloc reverse pairs");
+      hip_check(hipMalloc(&sorted, max_pairs * 8), "alloc sorted pairs");
+      hip_check(hipMalloc(&heads, max_pairs * 4), "alloc heads");
+      hip_check(hipMalloc(&nheads, 4), "alloc head count");
+      hip_check(hipMalloc(&temp, std::max<size_t>(temp_bytes, 16)), "alloc sort temp");
+    } catch (...) {
+      release();
+      throw;
+    }
+  }
+  ~BuildWorkspace() { release(); }
+  BuildWorkspace(const BuildWorkspace&) = delete;
+  BuildWorkspace& operator=(const BuildWorkspace&) = delete;
+  void release() {
     (void)hipFree(visited);
     (void)hipFree(vcounts);
     (void)hipFree(pairs);
@@ -427,56 +448,112 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
     (void)hipFree(heads);
     (void)hipFree(nheads);
     (void)hipFree(temp);
-  };
-  try {
-    hip_check(hipMalloc(&visited, (size_t)mb * kBuildMaxResult * 8), "alloc build visited");
-    hip_check(hipMalloc(&vcounts, (size_t)mb * 4), "alloc build visited counts");
-    hip_check(hipMalloc(&pairs, max_pairs * 8), "alloc reverse pairs");
-    hip_check(hipMalloc(&sorted, max_pairs * 8), "alloc sorted pairs");
-    hip_check(hipMalloc(&heads, max_pairs * 4), "alloc heads");
-    hip_check(hipMalloc(&nheads, 4), "alloc head count");
-    hip_check(hipMalloc(&temp, std::max<size_t>(temp_bytes, 16)), "alloc sort temp");
-  } catch (...) {
-    cleanup();
-    throw;
+    visited = nullptr;
+    vcounts = nullptr;
+    pairs = sorted = nullptr;
+    heads = nheads = nullptr;
+    temp = nullptr;
   }
+};
 
-  // pair keys: target << sb | (source - batch start); the radix sort covers
-  // the bits of both
-  uint32_t sb = 1;
-  while (((uint64_t)1 << sb) < (uint64_t)mb) ++sb;
-  int end_bit = (int)sb;
-  while (end_bit < 64 && ((uint64_t)1 << (end_bit - sb)) <= (uint64_t)g.n) ++end_bit;
+// Reverse pair keys are target << sb | (source - batch start) with sb the
+// bits of the largest batch; the radix sort covers the bits of both.
+struct PairBits {
+  uint32_t sb;
+  int end_bit;
+};
+static PairBits pair_bits(int64_t mb, int64_t n) {
+  PairBits b;
+  b.sb = 1;
+  while (((uint64_t)1 << b.sb) < (uint64_t)mb) ++b.sb;
+  b.end_bit = (int)b.sb;
+  while (b.end_bit < 64 && ((uint64_t)1 << (b.end_bit - b.sb)) <= (uint64_t)n) ++b.end_bit;
+  return b;
+}
 
+// Kernel arguments of the prune passes over g with workspace ws. *intx
+// tells whether the rows are integers in the exact range (int_exact_l2:
+// packed-difference distances, the same bits as the fp32 chain).
+static PruneKernelArgs prune_args(Graph& g, float alpha, const BuildWorkspace& ws, uint32_t sb, hipStream_t stream,
+                                  bool* intx) {
   PruneKernelArgs pa{};
   pa.pair_shift = sb;
   pa.pair_mask = (1u << sb) - 1u;
   pa.pc.vecs = (const uint4*)g.vecs;
-  pa.pc.nchunks = nchunks;
+  pa.pc.nchunks = g.dp / 8;
   pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;  // the reference prunes with `dim`
-  pa.pc.R = R;
+  pa.pc.R = g.R;
   pa.pc.alpha = alpha;
   pa.pc.margin_scale = gram_margin_scale();
   pa.edges = g.edges;
   pa.edist = g.edist;
   pa.counts = g.counts;
-  pa.visited = visited;
-  pa.visited_counts = vcounts;
-  pa.pairs = pairs;
-  pa.sorted_pairs = sorted;
-  pa.heads = heads;
-  pa.n_heads = nheads;
-  const size_t plds = prune_lds_bytes();
-  // integer-valued rows in the exact range: packed-difference distances,
-  // the same bits as the fp32 chain (int_exact_l2)
+  pa.visited = ws.visited;
+  pa.visited_counts = ws.vcounts;
+  pa.pairs = ws.pairs;
+  pa.sorted_pairs = ws.sorted;
+  pa.heads = ws.heads;
+  pa.n_heads = ws.nheads;
   int32_t int_lo = 0;
-  const bool intx = int_exact_l2(g, stream, &int_lo);
-  {
-    const _Float16 lo = (_Float16)int_lo;  // exact: an fp16 value of the rows
-    uint16_t bits;
-    std::memcpy(&bits, &lo, 2);
-    pa.pc.lo2 = (uint32_t)bits * 0x10001u;
+  *intx = int_exact_l2(g, stream, &int_lo);
+  const _Float16 lo = (_Float16)int_lo;  // exact: an fp16 value of the rows
+  uint16_t bits;
+  std::memcpy(&bits, &lo, 2);
+  pa.pc.lo2 = (uint32_t)bits * 0x10001u;
+  return pa;
+}
+
+// chunks per quad lane held in registers; 0 streams rows longer than 32 chunks
+static uint32_t prune_cpl(const Graph& g) {
+  const uint32_t nchunks = g.dp / 8;
+  return (nchunks + 3) / 4 > 8 ? 0u : (nchunks + 3) / 4;
+}
+
+// Steps 3 and 4 of a batch: group the reverse pairs of its bs vertices by
+// target, then the reverse merge + prune (SCALE: the merge prune).
+template <bool SCALE>
+static void reverse_step(const Graph& g, PruneKernelArgs& pa, const BuildWorkspace& ws, const PairBits& pb,
+                         int64_t bs, bool intx, uint32_t cpl, EventTimer& timer, BuildStats& st,
+                         hipStream_t stream) {
+  const size_t plds = prune_lds_bytes();
+  const uint32_t np = (uint32_t)(bs * g.R);
+  timer.start();
+  sort_u64(ws.temp, ws.temp_bytes, ws.pairs, ws.sorted, np, pb.end_bit, stream);
+  hip_check(hipMemsetAsync(ws.nheads, 0, 4, stream), "clear head count");
+  hipLaunchKernelGGL(mark_heads_kernel, dim3((np + kMarkHeadsBlock - 1) / kMarkHeadsBlock), dim3(kMarkHeadsBlock), 0,
+                     stream, ws.sorted, np, pb.sb, ws.heads, ws.nheads);
+  hip_check(hipGetLastError(), "launch mark_heads_kernel");
+  timer.stop(st.sort_ms);
+  pa.n_pairs = np;
+  const uint32_t grid = (uint32_t)std::min<int64_t>(std::max<int64_t>(np, 1), 16384);
+  timer.start();
+  if (SCALE) {
+    if (g.metric == kL2) dispatch_prune<kL2, false, true>(true, cpl, pa, grid, plds, stream);
+    else dispatch_prune<kIP, false, true>(true, cpl, pa, grid, plds, stream);
+  } else {
+    if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
+    else if (g.metric == kL2) dispatch_prune<kL2, false>(true, cpl, pa, grid, plds, stream);
+    else dispatch_prune<kIP, false>(true, cpl, pa, grid, plds, stream);
   }
+  hip_check(hipGetLastError(), "launch reverse_prune_kernel");
+  timer.stop(st.reverse_ms);
+}
+
+void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max_batch, bool doubling,
+                 hipStream_t stream, bool time_stages, BuildStats* stats, bool rabitq_search) {
+  if (rabitq_search && !g.rabitq) throw std::invalid_argument("RaBitQ build search needs the RaBitQ codes");
+  if (last <= first) return;
+  if (first < 0 || last > g.n) throw std::invalid_argument("vertex range outside the graph");
+  if (max_batch < 1) max_batch = 1;  // the reference loops forever here (n < 50); clamp instead
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  const uint32_t cpl = prune_cpl(g);
+  const int64_t mb = std::min<int64_t>(max_batch, last - first);
+
+  BuildWorkspace ws(mb, g.R);
+  const PairBits pb = pair_bits(mb, g.n);
+  bool intx = false;
+  PruneKernelArgs pa = prune_args(g, alpha, ws, pb.sb, stream, &intx);
+  const size_t plds = prune_lds_bytes();
 
   BuildStats st;
   st.max_batch = mb;
@@ -500,15 +577,15 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       r.beam_width = kBuildL;
       r.limit = kBuildLimit;
       r.max_result = kBuildMaxResult;
-      r.visited = visited;
-      r.visited_counts = vcounts;
+      r.visited = ws.visited;
+      r.visited_counts = ws.vcounts;
       // the queries' seen-cache size (at 100M vectors the 8 KB 16-bit form
       // took the search stage from 11.4 s to 10.6 s)
       r.hash_bits = seen_cache_hash_bits(g.n);
       timer.start();
       if (rabitq_search)
-        rabitq_build_search(g, (uint32_t)count, (uint32_t)bs, kBuildL, kBuildLimit, kBuildMaxResult, visited, vcounts,
-                            stream);
+        rabitq_build_search(g, (uint32_t)count, (uint32_t)bs, kBuildL, kBuildLimit, kBuildMaxResult, ws.visited,
+                            ws.vcounts, stream);
       else
         launch_beam_search(g, r, stream);
       timer.stop(st.search_ms);
@@ -520,24 +597,8 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       else dispatch_prune<kIP, false>(false, cpl, pa, (uint32_t)bs, plds, stream);
       hip_check(hipGetLastError(), "launch forward_prune_kernel");
       timer.stop(st.prune_ms);
-      // 3. group reverse pairs by target
-      const uint32_t np = (uint32_t)(bs * R);
-      timer.start();
-      sort_u64(temp, temp_bytes, pairs, sorted, np, end_bit, stream);
-      hip_check(hipMemsetAsync(nheads, 0, 4, stream), "clear head count");
-      hipLaunchKernelGGL(mark_heads_kernel, dim3((np + kMarkHeadsBlock - 1) / kMarkHeadsBlock), dim3(kMarkHeadsBlock),
-                         0, stream, sorted, np, sb, heads, nheads);
-      hip_check(hipGetLastError(), "launch mark_heads_kernel");
-      timer.stop(st.sort_ms);
-      // 4. reverse merge + prune
-      pa.n_pairs = np;
-      const uint32_t grid = (uint32_t)std::min<int64_t>(std::max<int64_t>(np, 1), 16384);
-      timer.start();
-      if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
-      else if (g.metric == kL2) dispatch_prune<kL2, false>(true, cpl, pa, grid, plds, stream);
-      else dispatch_prune<kIP, false>(true, cpl, pa, grid, plds, stream);
-      hip_check(hipGetLastError(), "launch reverse_prune_kernel");
-      timer.stop(st.reverse_ms);
+      // 3-4. group reverse pairs by target, reverse merge + prune
+      reverse_step<false>(g, pa, ws, pb, bs, intx, cpl, timer, st, stream);
       count += bs;
       st.batches += 1;
       if (doubling && bs < mb) bs = std::min<int64_t>(mb, bs * 2);
@@ -551,12 +612,138 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
     (void)hipStreamSynchronize(stream);
     (void)hipEventDestroy(t0);
     (void)hipEventDestroy(t1);
-    cleanup();
     throw;
   }
   (void)hipEventDestroy(t0);
   (void)hipEventDestroy(t1);
-  cleanup();
+  if (stats) *stats = st;
+}
+
+// ------------------------------------------------------ partitioned build
+
+std::vector<std::pair<int64_t, int64_t>> scale_merge_order(int64_t P) {
+  std::vector<std::pair<int64_t, int64_t>> order;
+  int64_t B1 = 0;
+  for (int64_t itv = 1; itv <= P / 2; ++itv) {
+    const int64_t gg = std::gcd(itv, P), cycle_len = P / gg;
+    const int64_t calls = cycle_len == 2 ? 1 : cycle_len;
+    for (int64_t cyc = 0; cyc < gg; ++cyc) {
+      if (cyc > 0) B1 = (B1 + 1) % P;
+      for (int64_t step = 0; step < calls; ++step) {
+        const int64_t B2 = (B1 + itv) % P;
+        order.emplace_back(B1, B2);
+        B1 = B2;
+      }
+    }
+  }
+  return order;
+}
+
+void build_scale(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int64_t merge_batch,
+                 hipStream_t stream, ScaleStats* stats) {
+  const int64_t n = g.n;
+  if (n <= 0) throw std::invalid_argument("graph is empty");
+  if (n_parts < 1) throw std::invalid_argument("n_parts must be positive");
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  const int64_t part = (n + n_parts - 1) / n_parts;
+  if (part * (n_parts - 1) >= n)
+    throw std::invalid_argument("n_parts must be smaller: " + std::to_string(n_parts) +
+                                " partitions of " + std::to_string(n) + " vectors leave one empty");
+  if (part_batch < 1) part_batch = 1;
+  if (merge_batch < 1) merge_batch = 1;
+  ScaleStats st;
+  st.part_batch = part_batch;
+  hipEvent_t t0, t1, t2;
+  hip_check(hipEventCreate(&t0), "event");
+  hip_check(hipEventCreate(&t1), "event");
+  hip_check(hipEventCreate(&t2), "event");
+  struct Events {
+    hipEvent_t* e[3];
+    ~Events() { for (hipEvent_t* x : e) (void)hipEventDestroy(*x); }
+  } ev{{&t0, &t1, &t2}};
+  hip_check(hipEventRecord(t0, stream), "event record");
+
+  // 1. each partition on its own: its rows start without edges and its
+  //    search starts at its first row, so no edge leaves the partition --
+  //    the reference's separate construct_graph plus apply_global_offset
+  //    (construct_scale.cuh:107-124, graph.cuh:804-827), in place
+  const uint32_t medoid = g.medoid;
+  try {
+    for (int64_t p = 0; p < n_parts; ++p) {
+      const int64_t s = p * part, c = std::min(part, n - s);
+      g.medoid = (uint32_t)s;
+      build_range(g, alpha, s, s + c, part_batch, true, stream, false, nullptr);
+    }
+  } catch (...) {
+    g.medoid = medoid;
+    throw;
+  }
+  g.medoid = medoid;
+  hip_check(hipEventRecord(t1, stream), "event record");
+
+  // 2. merge every pair once (construct_scale.cuh:378-446), B1 in batches
+  //    cut at 2^20-row segment boundaries (:362-364)
+  const auto order = scale_merge_order(n_parts);
+  if (!order.empty()) {
+    const int64_t mb = std::min<int64_t>(merge_batch, part);
+    st.merge_batch = mb;
+    const uint32_t cpl = prune_cpl(g);
+    BuildWorkspace ws(mb, g.R);
+    const PairBits pb = pair_bits(mb, n);
+    bool intx = false;
+    PruneKernelArgs pa = prune_args(g, alpha, ws, pb.sb, stream, &intx);
+    const size_t plds = prune_lds_bytes();
+    EventTimer timer(false, stream);
+    BuildStats bst;
+    constexpr int64_t kSegment = (int64_t)1 << 20;
+    for (const auto& m : order) {
+      const int64_t b1s = m.first * part, n1 = std::min(part, n - b1s);
+      const int64_t b2s = m.second * part, n2 = std::min(part, n - b2s);
+      pa.pc.r1_lo = (uint32_t)b1s;
+      pa.pc.r1_n = (uint32_t)n1;
+      pa.pc.r2_lo = (uint32_t)b2s;
+      pa.pc.r2_n = (uint32_t)n2;
+      int64_t count = 0;
+      while (count < n1) {
+        const int64_t bs = std::min({mb, n1 - count, kSegment - count % kSegment});
+        // 1. B1's batch searched in B2 alone, from B2's first row
+        //    (construct_scale.cuh:190-213): edges leaving B2 are dropped
+        SearchRequest r;
+        r.use_range = true;
+        r.q_start = (uint32_t)(b1s + count);
+        r.nq = (uint32_t)bs;
+        r.medoid = (uint32_t)b2s;
+        r.id_lo = (uint32_t)b2s;
+        r.id_n = n2;
+        r.k = kBuildL;
+        r.beam_width = kBuildL;
+        r.limit = kBuildLimit;
+        r.max_result = kBuildMaxResult;
+        r.visited = ws.visited;
+        r.visited_counts = ws.vcounts;
+        r.hash_bits = seen_cache_hash_bits(n);
+        launch_beam_search(g, r, stream);
+        // 2. forward merge + merge prune into B1, pairs for B2 targets
+        pa.batch_offset = (uint32_t)(b1s + count);
+        if (g.metric == kL2) dispatch_prune<kL2, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        else dispatch_prune<kIP, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        hip_check(hipGetLastError(), "launch forward_prune_kernel (merge)");
+        // 3-4. reverse edges into B2 (process_reverse_edges_kernel_scale)
+        reverse_step<true>(g, pa, ws, pb, bs, intx, cpl, timer, bst, stream);
+        count += bs;
+        st.merge_batches += 1;
+      }
+      st.merges += 1;
+    }
+  }
+  hip_check(hipEventRecord(t2, stream), "event record");
+  hip_check(hipStreamSynchronize(stream), "scale build synchronize");
+  float a = 0, b = 0;
+  hip_check(hipEventElapsedTime(&a, t0, t1), "event elapsed");
+  hip_check(hipEventElapsedTime(&b, t1, t2), "event elapsed");
+  st.partition_ms = a;
+  st.merge_ms = b;
+  st.total_ms = (double)a + b;
   if (stats) *stats = st;
 }
 

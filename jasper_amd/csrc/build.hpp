@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+#include <vector>
+
 #include "graph.hpp"
 
 namespace jasper_amd {
@@ -18,6 +21,8 @@ struct BuildStats {
 // (graph_construct_workspace::max_batch_size_for_budget, index/construct.cuh:
 // 238-262, capped at n/50 by ffi/jasper_ffi_common.cuh:245-248).
 int64_t reference_max_batch(int64_t n, uint32_t R, int64_t budget_bytes);
+// The same without the n/50 cap (the partitioned build's merges use it).
+int64_t budget_max_batch(uint32_t R, int64_t budget_bytes);
 
 // Builds the edges of `g` (vectors already resident) with the reference's
 // batch schedule: batches of 1, 2, 4, ... up to max_batch over ids in order.
@@ -33,6 +38,25 @@ void build_graph(Graph& g, float alpha, int64_t max_batch, hipStream_t stream, b
 // [first, last) must hold no edges yet.
 void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max_batch, bool doubling,
                  hipStream_t stream, bool time_stages, BuildStats* stats, bool rabitq_search = false);
+
+// The partitioned build (reference index/construct_scale.cuh:68-446, driven
+// by cmd/create_scale_index.cu:57-98): the n rows of g (no edges yet) split
+// into n_parts contiguous partitions of ceil(n / n_parts) rows, each built
+// on its own (batches doubling to part_batch, search from its first row),
+// then every pair merged once in scale_merge_order: B1 in batches of up to
+// merge_batch searched in B2 alone (from B2's first row, edges leaving B2
+// dropped), the forward merge prune into B1 and the reverse merge prune into
+// B2, where a vector outside B1 and B2 is kept untested and prunes nothing
+// (construct_scale_kernels.cuh:22-310). The whole graph stays in HBM: the
+// reference stages partitions through host memory two at a time, which
+// changes where rows live, not the result.
+struct ScaleStats {
+  double partition_ms = 0, merge_ms = 0, total_ms = 0;
+  int64_t merges = 0, merge_batches = 0, part_batch = 0, merge_batch = 0;
+};
+std::vector<std::pair<int64_t, int64_t>> scale_merge_order(int64_t n_parts);
+void build_scale(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int64_t merge_batch,
+                 hipStream_t stream, ScaleStats* stats);
 
 // Live updates (reference construct.cuh:1169-1265, graph_ops.cuh:94-258).
 // append_rows: copies `count` rows (host or device fp16 [count, dim]) into

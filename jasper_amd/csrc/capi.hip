@@ -40,6 +40,7 @@ std::unordered_map<int64_t, Entry> g_table;
 std::mutex g_mutex;
 int64_t g_next_handle = 0;
 BuildStats g_last_build;
+ScaleStats g_last_scale;
 
 struct Config {
   uint32_t R;
@@ -582,6 +583,57 @@ extern "C" int64_t jasperx_construct_directional_ex(const char* config, const vo
     auto g = construct_directional(c.R, c.metric, c.k_ranks, c.small_dim, vectors, n, dim, alpha, budget, on_host,
                                    prerotate, (uint64_t)seed, (hipStream_t)stream, &g_last_build, options);
     return insert(std::move(g), true);
+  });
+}
+
+extern "C" int64_t jasperx_construct_scale(const char* config, const void* vectors, int64_t n, int64_t dim,
+                                           double alpha, int64_t n_parts, int64_t budget, int64_t max_batch_size,
+                                           void* stream) {
+  return guarded([&]() -> int64_t {
+    if (!config) throw std::invalid_argument("null config id");
+    static const char* const kNames[] = {
+#define JA_PLAIN_NAME(id) #id,
+        JASPER_PLAIN_CONFIGS(JA_PLAIN_NAME)
+#undef JA_PLAIN_NAME
+    };
+    bool known = false;
+    for (const char* name : kNames) known = known || std::strcmp(name, config) == 0;
+    if (!known) throw std::invalid_argument(std::string("unknown plain config ") + config);
+    if (n <= 0) throw std::invalid_argument("vectors must contain at least one row");
+    if (n > 0x7FFFFFFF) throw std::invalid_argument("too many vectors for 31-bit ids");
+    if (dim <= 0) throw std::invalid_argument("dim must be positive");
+    if (n_parts < 1) throw std::invalid_argument("n_parts must be positive");
+    const Config c = config_of(config);
+    hipStream_t s = (hipStream_t)stream;
+    // partitions: min(budget batch, max_batch_size), the caller's cap
+    // defaulting to n / n_parts / 20 (cmd/create_scale_index.cu:84,
+    // construct_scale.cuh:96-99); merges: the budget batch (:383-385)
+    const int64_t budget_batch = budget_max_batch(c.R, budget);
+    if (budget_batch < 1) throw std::invalid_argument("workspace budget below one batch item");
+    const int64_t cap = max_batch_size > 0 ? max_batch_size : std::max<int64_t>(1, n / n_parts / 20);
+    const int64_t part_batch = std::min(budget_batch, cap);
+    auto g = std::make_unique<Graph>();
+    g->allocate(n, (uint32_t)dim, c.R, c.metric, false);
+    upload_vectors(*g, vectors, n, (uint32_t)dim, s);
+    ScaleStats st;
+    build_scale(*g, (float)alpha, n_parts, part_batch, budget_batch, s, &st);
+    g->next_id = (uint64_t)n;
+    {
+      std::lock_guard<std::mutex> lock(g_mutex);
+      g_last_scale = st;
+    }
+    return insert(std::move(g), false);
+  });
+}
+
+extern "C" int64_t jasperx_last_scale_stats(double* out7) {
+  return guarded([&]() -> int64_t {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    const ScaleStats& s = g_last_scale;
+    const double v[7] = {s.partition_ms, s.merge_ms, s.total_ms, (double)s.merges, (double)s.merge_batches,
+                         (double)s.part_batch, (double)s.merge_batch};
+    std::memcpy(out7, v, sizeof(v));
+    return 0;
   });
 }
 

@@ -25,7 +25,17 @@ struct PruneCtx {
   float alpha;
   uint32_t lo2;      // integer-valued rows: the smallest value, as two fp16
   float margin_scale;  // >= 1: widens the Gram prune's proof margin (testing)
+  // partitioned build merges: the two id ranges whose vectors the merge may
+  // read ([r1_lo, r1_lo + r1_n) and [r2_lo, r2_lo + r2_n))
+  uint32_t r1_lo, r1_n, r2_lo, r2_n;
 };
+
+// Whether the merge prune resolves id's vector (robust_prune_kernel_scale,
+// reference index/construct_scale_kernels.cuh:69-74: b1_graph.is_valid or
+// b2_graph.is_valid).
+__device__ __forceinline__ bool resolvable(const PruneCtx& p, uint32_t id) {
+  return id - p.r1_lo < p.r1_n || id - p.r2_lo < p.r2_n;
+}
 
 // The left operand of a loaded row: L2 keeps the fp16 chunks; IP converts
 // the load layout (lane l: chunks l, l+4, ...) to quad_partial's fp32
@@ -77,7 +87,11 @@ __device__ __forceinline__ void load_member(const PruneCtx& p, const uint32_t* S
 // C: sorted keys [0, nc) in LDS. Writes the selection to S_ids / S_dist.
 // Returns |S|. INTX: rows are integer-valued within the exact range
 // (int_exact_l2), so pair distances take the packed-difference form.
-template <int CPL, int METRIC, bool INTX>
+// SCALE: the merge prune of the partitioned build (reference
+// index/construct_scale_kernels.cuh:54-126): a candidate whose vector is
+// not resolvable is selected without a test, and a selected member that is
+// not resolvable prunes nothing.
+template <int CPL, int METRIC, bool INTX, bool SCALE = false>
 __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
                                       uint32_t* S_ids, float* S_dist) {
   const uint32_t lane = lane_id();
@@ -90,6 +104,8 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     const uint32_t cid = key_id(ck);
     const float cd = key_dist(ck);
     valid = valid && cid != self;
+    // tested against members (SCALE: only when its vector is resolvable)
+    const bool tested = !SCALE || resolvable(p, cid);
     RowFrag<CPL> xc;
     load_row_frag<CPL>(p.vecs + (size_t)(valid ? cid : 0u) * p.nchunks, ql, p.nchunks, valid, xc);
     LeftFrag<CPL, METRIC> cf;
@@ -109,8 +125,11 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
           load_row_frag<CPL>(p.vecs + (size_t)(uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)(s + 1)) *
                                           p.nchunks,
                              ql, p.nchunks, true, xn);
+        if constexpr (SCALE) {
+          if (!resolvable(p, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)s))) continue;
+        }
         const float d = left_distance<CPL, METRIC, INTX>(cf, xs, ql, p.nchunks, p.nlimit);
-        if (d * p.alpha < cd) pruned = true;
+        if (tested && d * p.alpha < cd) pruned = true;
         if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
       }
     }
@@ -118,6 +137,8 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     uint64_t live = ballot(valid && !pruned && ql == 0);
     while (live && ns < p.R) {
       const uint32_t g = (uint32_t)__builtin_ctzll(live) >> 2;
+      // SCALE: the new member prunes only when its vector is resolvable
+      const bool g_prunes = !SCALE || (ballot(tested && qg == g) != 0);
       if (qg == g) {
         if (ql == 0) {
           S_ids[ns] = cid;
@@ -139,8 +160,10 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
           xs.x[t].w = (uint32_t)__shfl((int)xc.x[t].w, src, 64);
         }
       }
-      const float d = left_distance<CPL, METRIC, INTX>(cf, xs, ql, p.nchunks, p.nlimit);
-      if (qg > g && d * p.alpha < cd) pruned = true;
+      if (g_prunes) {
+        const float d = left_distance<CPL, METRIC, INTX>(cf, xs, ql, p.nchunks, p.nlimit);
+        if (qg > g && tested && d * p.alpha < cd) pruned = true;
+      }
       ns += 1;
       live = ballot(valid && !pruned && ql == 0 && qg > g);
     }

@@ -31,6 +31,9 @@ namespace jasper_amd {
 struct SearchArgs {
   const uint4* vecs;
   int64_t n;
+  // neighbours are followed only when their id is in [id_lo, id_lo + id_n)
+  // (the whole graph unless the request narrows it)
+  uint32_t id_lo, id_n;
   uint32_t dp, nchunks, R;
   const uint32_t* edges;
   const uint8_t* counts;
@@ -316,7 +319,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
       spec_v = a.edges[(size_t)su * a.R + elane];
     }
     const uint32_t deg = min(cu, a.R);
-    bool isnew = lane < deg && (int64_t)v < a.n;
+    bool isnew = lane < deg && v - a.id_lo < a.id_n;
     if constexpr (STATS) {
       // exact filter: first time this query sees v
       if (isnew) {
@@ -543,9 +546,15 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
   if (g.n <= 0) throw std::invalid_argument("graph is empty");
   if ((int64_t)r.medoid >= g.n) throw std::invalid_argument("medoid out of range");
   if (r.use_range && (int64_t)r.q_start + r.nq > g.n) throw std::invalid_argument("query range out of bounds");
+  const int64_t win_n = r.id_n < 0 ? g.n : r.id_n;
+  if ((int64_t)r.id_lo + win_n > g.n || win_n == 0) throw std::invalid_argument("id window outside the graph");
+  if (r.medoid < r.id_lo || (int64_t)r.medoid >= (int64_t)r.id_lo + win_n)
+    throw std::invalid_argument("medoid outside the id window");
   SearchArgs a{};
   a.vecs = (const uint4*)g.vecs;
   a.n = g.n;
+  a.id_lo = r.id_lo;
+  a.id_n = (uint32_t)win_n;
   a.dp = g.dp;
   a.nchunks = g.dp / 8;
   a.R = g.R;

@@ -20,6 +20,12 @@ struct SearchRequest {
   uint64_t* visited = nullptr;     // [nq, max_result] popped keys in pop order (may be null)
   uint32_t* visited_counts = nullptr;
   uint32_t hash_bits = 0;          // 0 = choose from beam width
+  // id window: neighbours outside [id_lo, id_lo + id_n) are dropped as the
+  // reference drops ids past a graph's range (beam_search/device_kernels.cuh:
+  // 95-129); id_n < 0 = the whole graph. The partitioned build's merge
+  // searches one partition of the full graph this way.
+  uint32_t id_lo = 0;
+  int64_t id_n = -1;
   // measurement mode (exact seen set, work counters); both or neither
   uint32_t* seen_bits = nullptr;   // [nq, ceil(n/32)], zeroed by the caller
   uint32_t* stats = nullptr;       // [nq, 4]: hops, sum of degrees, vectors scored,
