@@ -209,13 +209,16 @@ def main() -> int:
                     help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--path", default="search",
-                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5", "updates"],
+                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5", "updates",
+                             "scale"],
                     help="search (default, the headline metric) or one of the other hot-path rows, each "
                          "printing its own JSON line: directional (config 3, LSH), pq (PQ-ADC on "
                          "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
                          "rabitq (one-bit codes), c4 (config 4: 1M x 960 build + PQ search), c5 "
                          "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search), updates "
-                         "(config 2: mark_deleted 10%%, consolidate, append 100k)")
+                         "(config 2: mark_deleted 10%%, consolidate, append 100k), scale (config 2: the "
+                         "partitioned build)")
+    ap.add_argument("--scale-parts", default="4,2,8", help="partition counts of --path scale (first = the line's value)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
     ap.add_argument("--int-exact", type=int, default=1, choices=[0, 1],
@@ -851,8 +854,67 @@ def run_updates(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
+def run_scale(args, torch, jasper_amd, datasets, dev, log):
+    """The partitioned build (construct_scale.cuh, cmd/create_scale_index.cu)
+    on config 2 (1M x 128 clustered, R=64, L2, budget 10 GB): --scale-parts
+    partitions built on their own, every pair merged. Timed once per
+    partition count; recall@10 of the 10k queries at a few beam widths beside
+    the plain build's, on the same data."""
+    n, nq, dim = args.n, args.nq, 128
+    base = torch.from_numpy(datasets.clustered(n, dim, 0)).to(dev)
+    q = torch.from_numpy(datasets.clustered(nq, dim, 1)).to(dev)
+    gt, _ = jasper_amd.bruteforce_knn(base, q, 10, "l2")
+    gt = gt.cpu().numpy()
+    bws = (32, 44, 64, 128)
+
+    def recalls(g):
+        out = {}
+        for b in bws:
+            ids, _ = g.search(q, k=10, beam_width=b)
+            torch.cuda.synchronize()
+            out[b] = _recall(gt, ids.cpu().numpy())
+        return out
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2)
+    torch.cuda.synchronize()
+    plain_s = time.perf_counter() - t0
+    plain_r = recalls(g)
+    g.free()
+    log(f"plain build {plain_s:.2f}s, recall@10 {plain_r}")
+    runs = []
+    for P in [int(x) for x in args.scale_parts.split(",")]:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g = jasper_amd.Graph.build_scale(base, n_neighbors=64, distance="l2", alpha=1.2, n_parts=P,
+                                         workspace_budget="10GB")
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        st = jasper_amd.last_scale_stats()
+        r = recalls(g)
+        g.free()
+        runs.append({"n_parts": P, "build_s": wall, "partition_s": st["partition_ms"] / 1e3,
+                     "merge_s": st["merge_ms"] / 1e3, "merges": int(st["merges"]),
+                     "merge_batches": int(st["merge_batches"]), "part_batch": int(st["part_batch"]),
+                     "merge_batch": int(st["merge_batch"]), "recall_at_10": {str(b): v for b, v in r.items()}})
+        log(f"n_parts={P}: {wall:.2f}s (partitions {st['partition_ms'] / 1e3:.2f}s, {int(st['merges'])} merges "
+            f"{st['merge_ms'] / 1e3:.2f}s), recall@10 {r}")
+    head = runs[0]
+    res = _line(args, f"partitioned build, config 2: vectors/s ({head['n_parts']} partitions)", n / head["build_s"],
+                "vectors/s", head["build_s"] * 1000.0, "f32",
+                {"workload": f"config 2 ({n} x 128 clustered, R=64, L2, alpha 1.2), budget 10 GB: partitions "
+                             f"built on their own (batches min(budget batch, n / n_parts / 20)), every pair "
+                             f"merged (batches of the budget batch); recall@10 of {nq} queries",
+                 "plain_build_s": plain_s, "plain_recall_at_10": {str(b): v for b, v in plain_r.items()},
+                 "runs": runs}, None)
+    res["steps"], res["warmup"] = 1, 0
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 OTHER_PATHS = {"c4": run_c4, "c5": run_c5, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
-               "rotate": run_rotate, "rabitq": run_rabitq, "updates": run_updates}
+               "rotate": run_rotate, "rabitq": run_rabitq, "updates": run_updates, "scale": run_scale}
 
 
 if __name__ == "__main__":
