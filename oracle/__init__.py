@@ -77,6 +77,11 @@ def lib():
         _lib.jo_prune_scale.restype = i32
         _lib.jo_prune_scale.argtypes = [P, i32, i32, i32, f32, i32, i64, i64, i64, i64, ctypes.c_uint32, P, P,
                                         i32, P, P]
+        _lib.jo_diskann_assign.restype = i32
+        _lib.jo_diskann_assign.argtypes = [P, i64, i32, i32, i32, i32, u64, P, P]
+        _lib.jo_build_diskann.restype = i32
+        _lib.jo_build_diskann.argtypes = [P, i64, i32, i32, i32, i32, i32, f32, i32, i32, u64, i64, P, P, P, P,
+                                          i32]
         _lib.jo_build_rq.restype = i32
         _lib.jo_build_rq.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, i32, P, P, P, P, P, i32, P]
         _lib.jo_last_capped_groups.restype = i64
@@ -688,6 +693,56 @@ def prune_scale(vectors, b1: tuple, b2: tuple, self_id: int, cand_ids, cand_dist
     ns = lib().jo_prune_scale(_ptr(v16), v16.shape[1], dim, metric_code(distance), float(alpha), R, b1[0], b1[1],
                               b2[0], b2[1], self_id, _ptr(ids), _ptr(dists), len(ids), _ptr(out_i), _ptr(out_d))
     return out_i[:ns].copy(), out_d[:ns].copy()
+
+
+def diskann_assign(vectors, n_parts: int, n_dup: int = 2, seed: int = 42):
+    """Shard assignment of the DiskANN build (reference
+    index/construct_diskann.cuh:104-276): per row, n_dup shards (INVALID =
+    0xFFFFFFFF where a rank repeats a shard). Returns (shard_of [n, n_dup]
+    uint32, mean [dim] fp16 bits)."""
+    v16 = as_padded_f16(vectors)
+    n, dp = v16.shape
+    dim = np.asarray(vectors).shape[1]
+    out = np.empty((n, n_dup), dtype=np.uint32)
+    mean = np.empty(dim, dtype=np.uint16)
+    rc = lib().jo_diskann_assign(_ptr(v16), n, dp, dim, n_parts, n_dup, seed, _ptr(out), _ptr(mean))
+    if rc != 0:
+        raise ValueError("diskann_assign: bad arguments")
+    return out, mean
+
+
+def diskann_batch_cap(n: int, R_int: int, n_parts: int, workspace_budget: int = 10 ** 10) -> int:
+    """min(budget batch at R_int, max(1, n / n_parts / 20)) (construct_diskann.cuh:373-375,
+    cmd/create_diskann_index.cu:84)."""
+    per_item = 8 * 64 + 8 * 256 + 4 + 8 * (256 + R_int) + 4 + 8 * R_int + 4 * R_int + 4 * R_int
+    budget_batch = (workspace_budget - 4) // per_item
+    return max(1, min(budget_batch, max(1, n // n_parts // 20)))
+
+
+def build_diskann(vectors, R_int: int = 32, R_fin: int = 32, distance: str = "l2", alpha: float = 1.2,
+                  n_parts: int = 4, n_dup: int = 2, seed: int = 42, workspace_budget: int = 10 ** 10,
+                  batch_cap: int | None = None, nthreads: int = 0) -> OracleGraph:
+    """The DiskANN build (reference index/construct_diskann.cuh:328-613): LSH
+    shards with duplication, one graph of degree R_int per shard, then the
+    distance-only merge into rows of R_fin. Global ids; medoid 0."""
+    v16 = as_padded_f16(vectors)
+    n, dp = v16.shape
+    dim = np.asarray(vectors).shape[1]
+    if batch_cap is None:
+        batch_cap = diskann_batch_cap(n, R_int, n_parts, workspace_budget)
+    edges = np.empty((n, R_fin), dtype=np.uint32)
+    edist = np.empty((n, R_fin), dtype=np.uint16)
+    counts = np.empty(n, dtype=np.uint8)
+    shard_of = np.empty((n, n_dup), dtype=np.uint32)
+    rc = lib().jo_build_diskann(_ptr(v16), n, dp, dim, R_int, R_fin, metric_code(distance), float(alpha), n_parts,
+                                n_dup, seed, batch_cap, _ptr(edges), _ptr(edist), _ptr(counts), _ptr(shard_of),
+                                nthreads)
+    if rc != 0:
+        raise ValueError("build_diskann: bad arguments")
+    g = OracleGraph(v16, edges, edist, counts, R_fin, dim, distance)
+    g.shard_of = shard_of
+    g.batch_cap = batch_cap
+    return g
 
 
 class RqArtifacts:

@@ -999,4 +999,159 @@ void jo_rotation_matrix(int d, uint64_t seed, float* m, float* mt) {
   }
 }
 
+// --------------------------------------------------------- DiskANN build --
+// construct_diskann.cuh (driven by cmd/create_diskann_index.cu:59-103).
+//
+// assign_shards (:104-276, kernels construct_diskann_kernels.cuh:15-139):
+//   mean: rows 0, s, 2s, ... with s = max(1, n / min(n, 2,000,000)), summed
+//     per coordinate in double, divided by the row count, rounded to fp16;
+//   each row centred in fp16 (v - mean, one rounding), rotated by P (the
+//     rotation matrix for `seed` rounded to fp16): r_i = fp16(sum_k
+//     P[k + i*dim] * c_k) with fp32 accumulation (cublasGemmEx, op T; its
+//     summation order is unspecified: here k ascending, one fma per term);
+//   keys (|bits(r_i)| << 16) | i; n_dup times: the largest key wins, its
+//     coordinate and sign give bucket 2 coord + sign and shard bucket mod
+//     n_parts (INVALID when an earlier rank chose the same shard), then the
+//     winner's key is cleared.
+// Shard lists hold global ids in ascending order.
+static uint16_t hsub16(uint16_t a, uint16_t b) { return jo_d2h((double)h2f(a) - (double)h2f(b)); }
+
+int jo_diskann_assign(const uint16_t* vecs, int64_t n, int dp, int dim, int n_parts, int n_dup, uint64_t seed,
+                      uint32_t* shard_of, uint16_t* mean_out) {
+  if (n <= 0 || dim <= 0 || n_parts < 1 || n_dup < 1 || dp < dim || dp > 65536) return -1;
+  const int64_t target = std::min<int64_t>(n, 2000000);
+  const int64_t stride = std::max<int64_t>(1, n / target);
+  std::vector<double> acc((size_t)dim, 0.0);
+  int64_t sampled = 0;
+  for (int64_t i = 0; i < n; i += stride) {
+    for (int d = 0; d < dim; ++d) acc[(size_t)d] += (double)h2f(vecs[(size_t)i * dp + d]);
+    ++sampled;
+  }
+  std::vector<uint16_t> mean((size_t)dim);
+  for (int d = 0; d < dim; ++d) mean[(size_t)d] = jo_d2h(acc[(size_t)d] / (double)std::max<int64_t>(1, sampled));
+  if (mean_out) std::copy(mean.begin(), mean.end(), mean_out);
+  std::vector<float> P((size_t)dim * dim), Pt((size_t)dim * dim);
+  jo_rotation_matrix(dim, seed, P.data(), Pt.data());
+  std::vector<float> P16((size_t)dim * dim);
+  for (size_t i = 0; i < P.size(); ++i) P16[i] = h2f(jo_d2h((double)P[i]));
+#pragma omp parallel
+  {
+    std::vector<float> c((size_t)dim);
+    std::vector<uint16_t> rot((size_t)dim);
+    std::vector<uint32_t> keys((size_t)dp);
+#pragma omp for schedule(static)
+    for (int64_t v = 0; v < n; ++v) {
+      const uint16_t* x = vecs + (size_t)v * dp;
+      for (int k = 0; k < dim; ++k) c[(size_t)k] = h2f(hsub16(x[k], mean[(size_t)k]));
+      for (int i = 0; i < dim; ++i) {
+        float a = 0.0f;
+        const float* col = P16.data() + (size_t)i * dim;
+        for (int k = 0; k < dim; ++k) a = std::fmaf(col[k], c[(size_t)k], a);
+        rot[(size_t)i] = jo_d2h((double)a);
+      }
+      for (int i = 0; i < dp; ++i)
+        keys[(size_t)i] = i < dim ? ((uint32_t)(rot[(size_t)i] & 0x7FFFu) << 16) | (uint32_t)i : 0u;
+      uint32_t* out = shard_of + (size_t)v * n_dup;
+      for (int r = 0; r < n_dup; ++r) {
+        uint32_t win = 0;
+        for (int i = 0; i < dp; ++i) win = std::max(win, keys[(size_t)i]);
+        const uint32_t coord = win & 0xFFFFu;
+        const uint32_t sign = (rot[coord] >> 15) & 1u;
+        const uint32_t shard = (2u * coord + sign) % (uint32_t)n_parts;
+        bool dup = false;
+        for (int t = 0; t < r; ++t) dup = dup || out[t] == shard;
+        out[r] = dup ? kInvalid32 : shard;
+        keys[coord] = 0;
+      }
+    }
+  }
+  return 0;
+}
+
+// diskann_intermediate_graph::build (:328-613): shards that are not empty
+// become tasks, largest first (the reference's std::sort leaves equal sizes
+// in an unspecified order: here ascending shard index). Each task: its rows
+// (ascending global id) built as their own graph of degree R_int (the plain
+// construction, batches doubling to max(1, min(batch_cap, count)), search
+// from its first row), neighbour ids mapped to global ids, then merge_row
+// (:278-325) for every row: the final row's entries then the shard row's,
+// stably sorted by stored (bf16) distance, the first R_fin distinct ids
+// kept. Merges run one task after another. medoid = 0.
+int jo_build_diskann(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R_int, int R_fin, int metric,
+                     float alpha, int n_parts, int n_dup, uint64_t seed, int64_t batch_cap, uint32_t* edges,
+                     uint16_t* edge_dist, uint8_t* counts, uint32_t* shard_of_out, int nthreads) {
+  if (n <= 0 || R_int < 1 || R_fin < 1 || R_int > 255 || R_fin > 255 || batch_cap < 1) return -1;
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+  std::vector<uint32_t> shard_of((size_t)n * n_dup);
+  if (jo_diskann_assign(vecs, n, dp, dim_for_prune, n_parts, n_dup, seed, shard_of.data(), nullptr) != 0)
+    return -1;
+  if (shard_of_out) std::copy(shard_of.begin(), shard_of.end(), shard_of_out);
+  std::vector<std::vector<uint32_t>> shard_ids((size_t)n_parts);
+  for (int64_t v = 0; v < n; ++v)
+    for (int r = 0; r < n_dup; ++r) {
+      const uint32_t s = shard_of[(size_t)v * n_dup + r];
+      if (s != kInvalid32) shard_ids[s].push_back((uint32_t)v);
+    }
+  std::vector<int> tasks;
+  for (int p = 0; p < n_parts; ++p)
+    if (!shard_ids[(size_t)p].empty()) tasks.push_back(p);
+  std::stable_sort(tasks.begin(), tasks.end(),
+                   [&](int a, int b) { return shard_ids[(size_t)a].size() > shard_ids[(size_t)b].size(); });
+  std::fill(counts, counts + n, (uint8_t)0);
+  std::fill(edges, edges + (size_t)n * R_fin, kInvalid32);
+  std::fill(edge_dist, edge_dist + (size_t)n * R_fin, (uint16_t)0);
+  g_capped_groups.store(0);
+  for (int p : tasks) {
+    const std::vector<uint32_t>& ids = shard_ids[(size_t)p];
+    const int64_t c = (int64_t)ids.size();
+    std::vector<uint16_t> sv((size_t)c * dp);
+    for (int64_t i = 0; i < c; ++i)
+      std::copy(vecs + (size_t)ids[(size_t)i] * dp, vecs + (size_t)(ids[(size_t)i] + 1) * dp, sv.begin() + i * dp);
+    std::vector<uint32_t> se((size_t)c * R_int, kInvalid32);
+    std::vector<uint16_t> sd((size_t)c * R_int, 0);
+    std::vector<uint8_t> sc((size_t)c, 0);
+    Graph g{sv.data(), c, dp, se.data(), sc.data(), R_int, nullptr, metric};
+    process_batches(g, dim_for_prune, alpha, 0, c, std::max<int64_t>(1, std::min<int64_t>(batch_cap, c)), true, 0u,
+                    se.data(), sd.data(), sc.data());
+#pragma omp parallel
+    {
+      std::vector<std::pair<float, uint32_t>> C;  // (distance, slot in ids/bits)
+      std::vector<uint32_t> cid;
+      std::vector<uint16_t> cbits;
+#pragma omp for schedule(static)
+      for (int64_t i = 0; i < c; ++i) {
+        const uint32_t gid = ids[(size_t)i];
+        uint32_t* fe = edges + (size_t)gid * R_fin;
+        uint16_t* fd = edge_dist + (size_t)gid * R_fin;
+        cid.clear();
+        cbits.clear();
+        for (int j = 0; j < counts[gid]; ++j)
+          if (fe[j] != kInvalid32) { cid.push_back(fe[j]); cbits.push_back(fd[j]); }
+        for (int j = 0; j < sc[(size_t)i]; ++j) {
+          const uint32_t nb = se[(size_t)i * R_int + j];
+          if (nb == kInvalid32) continue;
+          cid.push_back(ids[nb]);
+          cbits.push_back(sd[(size_t)i * R_int + j]);
+        }
+        C.clear();
+        for (size_t t = 0; t < cid.size(); ++t) C.push_back({bf2f(cbits[t]), (uint32_t)t});
+        std::stable_sort(C.begin(), C.end(), [](const std::pair<float, uint32_t>& a,
+                                                const std::pair<float, uint32_t>& b) { return a.first < b.first; });
+        int sel = 0;
+        for (size_t t = 0; t < C.size() && sel < R_fin; ++t) {
+          const uint32_t id = cid[C[t].second];
+          bool dup = false;
+          for (int u = 0; u < sel && !dup; ++u) dup = fe[u] == id;
+          if (dup) continue;
+          fe[sel] = id;
+          fd[sel] = f2bf(C[t].first);
+          ++sel;
+        }
+        counts[gid] = (uint8_t)sel;
+      }
+    }
+  }
+  return 0;
+}
+
 }  // extern "C"
