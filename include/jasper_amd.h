@@ -235,6 +235,30 @@ int64_t jasperx_construct_scale(const char* config, const void* vectors, int64_t
  * total ms, merges, merge batches, partition batch size, merge batch
  * size}. */
 int64_t jasperx_last_scale_stats(double* out7);
+/* The DiskANN build of cmd/create_diskann_index.cu:59-103 (no FFI binding in
+ * the reference): include/jasper/index/construct_diskann.cuh
+ * diskann_intermediate_graph::build (:328-613). Rows go to n_dup shards by
+ * cross-polytope LSH (centred on the sampled mean, rotated by the seed's
+ * orthogonal matrix; the reference uses seed 42), each shard is built as its
+ * own graph of degree r_int (batches doubling to min(budget batch,
+ * max_batch_size); max_batch_size <= 0 takes the command's n / n_parts / 20),
+ * and the shards' rows are merged by stored distance into rows of the
+ * config's R (the reference's configs: r_int 32 with R 32 or 64). config: a
+ * plain config id; vectors [n_vectors, dim] fp16 (host or device), dim <=
+ * 1024; n_dup <= 16. Returns a plain-config handle. Shards of equal size are
+ * merged in shard order (the reference leaves that order unspecified). */
+int64_t jasperx_construct_diskann(const char* config, const void* vectors, int64_t n_vectors, int64_t dim,
+                                  double alpha, int64_t r_int, int64_t n_parts, int64_t n_dup,
+                                  int64_t workspace_budget_bytes, int64_t max_batch_size, int64_t seed,
+                                  void* stream);
+/* The shard assignment alone (assign_shards, construct_diskann.cuh:104-276)
+ * for tests: out_shard_of [n_vectors * n_dup] (0xFFFFFFFF where a rank
+ * repeats a shard) and out_mean [dim] fp16 bits, host memory, either NULL. */
+int64_t jasperx_diskann_assign(const void* vectors, int64_t n_vectors, int64_t dim, int64_t n_parts, int64_t n_dup,
+                               int64_t seed, uint32_t* out_shard_of, uint16_t* out_mean, void* stream);
+/* Times of the last DiskANN build: {assignment ms, shard builds ms, merges
+ * ms, total ms, shards, largest shard}. */
+int64_t jasperx_last_diskann_stats(double* out6);
 /* One-bit RaBitQ codes of a directional graph's stored rows (rotated rows
  * when prerotated): the reference's quantizer (rabitq/quantize.cuh:322-354)
  * on the rows as stored, against their mean; they feed the RaBitQ estimator

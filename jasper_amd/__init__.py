@@ -103,6 +103,10 @@ _AGNOSTIC = {
     "jasperx_export_rabitq": [_i64, _ptr, _ptr],
     "jasperx_construct_scale": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, _i64, _i64, _ptr],
     "jasperx_last_scale_stats": [_ptr],
+    "jasperx_construct_diskann": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, _i64, _i64, _i64, _i64,
+                                  _i64, _ptr],
+    "jasperx_diskann_assign": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr],
+    "jasperx_last_diskann_stats": [_ptr],
     "jasperx_directional_search_noalloc": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64,
                                            _i64, ctypes.c_uint32, _ptr],
     "jasperx_directional_search_ex": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64,
@@ -396,6 +400,32 @@ class Graph:
         handle = _agnostic("jasperx_construct_scale")(
             config_id.encode(), _tensor_ptr(vectors), n, dim, float(alpha), int(n_parts),
             parse_storage_size(workspace_budget), int(max_batch_size or 0), stream)
+        return cls(handle, config_id, DataType.FLOAT16, distance, n_neighbors, dim)
+
+    @classmethod
+    def build_diskann(cls, vectors: torch.Tensor, n_neighbors: int = 32, r_int: int = 32,
+                      distance: DistanceFunc | str = DistanceFunc.L2, alpha: float = 1.2, n_parts: int = 4,
+                      n_dup: int = 2, workspace_budget: str = "10GB", max_batch_size: int | None = None,
+                      seed: int = 42) -> "Graph":
+        """The DiskANN build of the reference's create_diskann_index command
+        (cmd/create_diskann_index.cu:59-103; include/jasper/index/
+        construct_diskann.cuh): rows sharded by cross-polytope LSH into n_dup
+        of n_parts shards, each shard built at degree r_int, rows merged by
+        stored distance into n_neighbors (the final degree). Returns a plain
+        graph (search, save, updates)."""
+        if isinstance(distance, str):
+            distance = DistanceFunc(distance)
+        if vectors.ndim != 2:
+            raise ValueError(f"vectors must be 2D, got {vectors.ndim}D")
+        if vectors.dtype != torch.float16:
+            raise ValueError(f"Unsupported tensor dtype: {vectors.dtype}. Use torch.float16.")
+        vectors = vectors.contiguous()
+        n, dim = vectors.shape
+        config_id = _resolve_config(DataType.FLOAT16, n_neighbors, distance)
+        stream = _stream_ptr(vectors.device if vectors.is_cuda else None)
+        handle = _agnostic("jasperx_construct_diskann")(
+            config_id.encode(), _tensor_ptr(vectors), n, dim, float(alpha), int(r_int), int(n_parts), int(n_dup),
+            parse_storage_size(workspace_budget), int(max_batch_size or 0), int(seed), stream)
         return cls(handle, config_id, DataType.FLOAT16, distance, n_neighbors, dim)
 
     # -- properties ---------------------------------------------------------
@@ -759,6 +789,27 @@ def last_scale_stats() -> dict:
     return dict(zip(keys, out.tolist()))
 
 
+def last_diskann_stats() -> dict:
+    """Times of the last DiskANN build (Graph.build_diskann)."""
+    out = np.zeros(6, dtype=np.float64)
+    _agnostic("jasperx_last_diskann_stats")(out.ctypes.data_as(_ptr))
+    keys = ["assign_ms", "build_ms", "merge_ms", "total_ms", "shards", "max_shard"]
+    return dict(zip(keys, out.tolist()))
+
+
+def diskann_assign(vectors: torch.Tensor, n_parts: int, n_dup: int = 2, seed: int = 42):
+    """Shard assignment of the DiskANN build on the GPU: (shard_of [n, n_dup]
+    uint32 with 0xFFFFFFFF for repeated shards, mean [dim] fp16 bits)."""
+    vectors = vectors.contiguous()
+    n, dim = vectors.shape
+    so = np.empty((n, n_dup), dtype=np.uint32)
+    mean = np.empty(dim, dtype=np.uint16)
+    _agnostic("jasperx_diskann_assign")(_tensor_ptr(vectors), n, dim, int(n_parts), int(n_dup), int(seed),
+                                        so.ctypes.data_as(_ptr), mean.ctypes.data_as(_ptr),
+                                        _stream_ptr(vectors.device if vectors.is_cuda else None))
+    return so, mean
+
+
 # ── Utilities (reference __init__.py:770-946) ─────────────────────────
 
 def read_bin(path: str, dtype: str = "f32", max_vectors: int = 0) -> torch.Tensor:
@@ -813,7 +864,7 @@ from .groundtruth import bruteforce_knn, generate_groundtruth  # noqa: E402
 __all__ = [
     "Graph", "DistanceFunc", "DataType", "JasperError", "read_bin", "read_groundtruth",
     "get_recall", "generate_groundtruth", "bruteforce_knn", "save_groundtruth", "parse_storage_size",
-    "last_build_stats", "last_scale_stats", "library_path",
+    "last_build_stats", "last_scale_stats", "last_diskann_stats", "diskann_assign", "library_path",
 ]
 
 

@@ -18,6 +18,7 @@
 #include "../../include/jasper_amd.h"
 #include "bruteforce.hpp"
 #include "build.hpp"
+#include "diskann.hpp"
 #include "common.hpp"
 #include "directional.hpp"
 #include "directional_api.hpp"
@@ -41,6 +42,7 @@ std::mutex g_mutex;
 int64_t g_next_handle = 0;
 BuildStats g_last_build;
 ScaleStats g_last_scale;
+DiskannStats g_last_diskann;
 
 struct Config {
   uint32_t R;
@@ -623,6 +625,72 @@ extern "C" int64_t jasperx_construct_scale(const char* config, const void* vecto
       g_last_scale = st;
     }
     return insert(std::move(g), false);
+  });
+}
+
+extern "C" int64_t jasperx_construct_diskann(const char* config, const void* vectors, int64_t n, int64_t dim,
+                                             double alpha, int64_t r_int, int64_t n_parts, int64_t n_dup,
+                                             int64_t budget, int64_t max_batch_size, int64_t seed, void* stream) {
+  return guarded([&]() -> int64_t {
+    if (!config) throw std::invalid_argument("null config id");
+    static const char* const kNames[] = {
+#define JA_PLAIN_NAME(id) #id,
+        JASPER_PLAIN_CONFIGS(JA_PLAIN_NAME)
+#undef JA_PLAIN_NAME
+    };
+    bool known = false;
+    for (const char* name : kNames) known = known || std::strcmp(name, config) == 0;
+    if (!known) throw std::invalid_argument(std::string("unknown plain config ") + config);
+    if (n <= 0) throw std::invalid_argument("vectors must contain at least one row");
+    if (n > 0x7FFFFFFF) throw std::invalid_argument("too many vectors for 31-bit ids");
+    if (dim <= 0) throw std::invalid_argument("dim must be positive");
+    if (n_parts < 1) throw std::invalid_argument("n_parts must be positive");
+    if (r_int < 1 || r_int > 64) throw std::invalid_argument("r_int must be between 1 and 64");
+    const Config c = config_of(config);
+    hipStream_t s = (hipStream_t)stream;
+    // min(budget batch at R_int, the command's n / n_parts / 20)
+    // (construct_diskann.cuh:373-375, cmd/create_diskann_index.cu:84)
+    const int64_t budget_batch = budget_max_batch((uint32_t)r_int, budget);
+    if (budget_batch < 1) throw std::invalid_argument("workspace budget below one batch item");
+    const int64_t cap = max_batch_size > 0 ? max_batch_size : std::max<int64_t>(1, n / n_parts / 20);
+    auto g = std::make_unique<Graph>();
+    g->allocate(n, (uint32_t)dim, c.R, c.metric, false);
+    upload_vectors(*g, vectors, n, (uint32_t)dim, s);
+    DiskannStats st;
+    build_diskann(*g, (uint32_t)r_int, (float)alpha, n_parts, n_dup, (uint64_t)seed, std::min(budget_batch, cap), s,
+                  &st);
+    g->next_id = (uint64_t)n;
+    {
+      std::lock_guard<std::mutex> lock(g_mutex);
+      g_last_diskann = st;
+    }
+    return insert(std::move(g), false);
+  });
+}
+
+extern "C" int64_t jasperx_diskann_assign(const void* vectors, int64_t n, int64_t dim, int64_t n_parts,
+                                          int64_t n_dup, int64_t seed, uint32_t* out_shard_of, uint16_t* out_mean,
+                                          void* stream) {
+  return guarded([&]() -> int64_t {
+    if (n <= 0) throw std::invalid_argument("vectors must contain at least one row");
+    if (n > 0x7FFFFFFF) throw std::invalid_argument("too many vectors for 31-bit ids");
+    if (dim <= 0) throw std::invalid_argument("dim must be positive");
+    hipStream_t s = (hipStream_t)stream;
+    Graph g;
+    g.allocate(n, (uint32_t)dim, 1, kL2, false);
+    upload_vectors(g, vectors, n, (uint32_t)dim, s);
+    diskann_assign(g, n_parts, n_dup, (uint64_t)seed, out_shard_of, out_mean, s);
+    return 0;
+  });
+}
+
+extern "C" int64_t jasperx_last_diskann_stats(double* out6) {
+  return guarded([&]() -> int64_t {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    const DiskannStats& s = g_last_diskann;
+    const double v[6] = {s.assign_ms, s.build_ms, s.merge_ms, s.total_ms, (double)s.shards, (double)s.max_shard};
+    std::memcpy(out6, v, sizeof(v));
+    return 0;
   });
 }
 

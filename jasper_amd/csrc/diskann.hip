@@ -1,0 +1,437 @@
+// diskann.hip -- the DiskANN build (reference index/construct_diskann.cuh,
+// construct_diskann_kernels.cuh; driven by cmd/create_diskann_index.cu).
+//
+//   1. Shards by cross-polytope LSH (assign_shards, :104-276): each row,
+//      centred on the sampled mean and rotated by the seed's orthogonal
+//      matrix, goes to the shards of its n_dup largest |coordinates| (bucket
+//      2 coord + sign, shard bucket mod n_parts). One wave per row: the
+//      centred row sits in LDS, each lane accumulates the rotated
+//      coordinates lane, lane + 64, ... in fp32 (k ascending, one fma per
+//      term; cuBLAS's order in the reference is unspecified), and n_dup wave
+//      max-reductions over the packed keys (|bits| << 16 | coord) pick the
+//      ranks. The (shard, row) pairs are radix-sorted, which lists every
+//      shard's rows in ascending order, and counted per shard.
+//   2. Each shard, largest first, is gathered into a shard graph of degree
+//      R_int and built with the plain construction (build_graph: batches
+//      doubling to min(batch cap, shard size), search from its first row).
+//   3. Distance-only merge (merge_row, :278-325), one wave per shard row:
+//      the final row's entries and the shard row's (ids mapped to global),
+//      the shard's duplicates of ids already in the final row dropped (the
+//      same id carries the same stored distance: distances are symmetric
+//      bit for bit), a 128-key bitonic sort by (distance, position), and the
+//      first R_fin kept.
+// The reference stages shards through host memory and merges on the CPU in
+// a worker thread, one shard after another; here the whole graph stays in
+// HBM and the merges run as kernels on the build stream in the same order.
+#include "build.hpp"
+#include "common.hpp"
+#include "diskann.hpp"
+#include "rotation.hpp"
+
+#include <algorithm>
+#include <numeric>
+#include <vector>
+
+namespace jasper_amd {
+
+namespace {
+
+constexpr uint32_t kMaxDup = 16;
+
+__device__ __forceinline__ float h2f_bits(uint16_t b) { return __half2float(__ushort_as_half(b)); }
+
+// binary64 -> binary16 bits, round to nearest even (one rounding).
+__device__ uint16_t d2h_rn(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+  const double a = fabs(x);
+  if (a != a) return (uint16_t)(sign | 0x7E00u);
+  if (a >= 65520.0) return (uint16_t)(sign | 0x7C00u);  // rounds to infinity
+  if (a < 6.103515625e-05) {                            // below 2^-14: subnormal step 2^-24
+    const double q = rint(a * 16777216.0);               // exact scaling, rint = RNE
+    return (uint16_t)(sign | (uint16_t)q);
+  }
+  int e = 0;
+  const double m = frexp(a, &e);  // a = m 2^e, m in [0.5, 1)
+  double q = rint((m * 2.0 - 1.0) * 1024.0);
+  int E = e - 1;
+  if (q >= 1024.0) {
+    q = 0.0;
+    E += 1;
+  }
+  if (E + 15 >= 31) return (uint16_t)(sign | 0x7C00u);
+  return (uint16_t)(sign | (uint16_t)((E + 15) << 10) | (uint16_t)q);
+}
+
+__global__ void mean_partial_kernel(const uint16_t* vecs, uint32_t dp, uint32_t dim, int64_t stride,
+                                    int64_t sampled, int64_t per_block, double* partial) {
+  const int64_t s0 = (int64_t)blockIdx.x * per_block;
+  const int64_t s1 = min(sampled, s0 + per_block);
+  for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x) {
+    double acc = 0.0;
+    for (int64_t s = s0; s < s1; ++s) acc += (double)h2f_bits(vecs[(size_t)(s * stride) * dp + d]);
+    partial[(size_t)blockIdx.x * dim + d] = acc;
+  }
+}
+
+__global__ void mean_final_kernel(const double* partial, uint32_t blocks, uint32_t dim, int64_t sampled,
+                                  uint16_t* mean) {
+  for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x) {
+    double acc = 0.0;
+    for (uint32_t b = 0; b < blocks; ++b) acc += partial[(size_t)b * dim + d];
+    mean[d] = d2h_rn(acc / (double)(sampled > 0 ? sampled : 1));
+  }
+}
+
+struct AssignArgs {
+  const uint16_t* vecs;
+  int64_t n;
+  uint32_t dp, dim;
+  const uint16_t* mean;  // [dim] fp16
+  const float* pt;       // [dim][dim]: pt[k * dim + i] = fp16(P[k + i * dim]) as f32
+  uint32_t n_parts, n_dup;
+  uint32_t* shard_of;    // [n, n_dup]
+  uint64_t* pairs;       // [n, n_dup]: shard << 32 | row, empty for repeats
+  uint32_t* shard_counts;  // [n_parts]
+};
+
+// One wave (one 64-thread block) per row, grid-stride.
+template <int T>
+__global__ __launch_bounds__(64) void assign_kernel(AssignArgs a) {
+  extern __shared__ float crow[];  // [dim] centred row
+  const uint32_t lane = lane_id();
+  for (int64_t row = blockIdx.x; row < a.n; row += gridDim.x) {
+    const uint16_t* x = a.vecs + (size_t)row * a.dp;
+    for (uint32_t k = lane; k < a.dim; k += 64) {
+      // subtract_mean_kernel: v - mean in fp16, one rounding
+      const _Float16 c = (_Float16)(__builtin_bit_cast(_Float16, x[k]) - __builtin_bit_cast(_Float16, a.mean[k]));
+      crow[k] = (float)c;
+    }
+    wave_sync();
+    float acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = 0.0f;
+    for (uint32_t k = 0; k < a.dim; ++k) {
+      const float ck = crow[k];
+      const float* p = a.pt + (size_t)k * a.dim;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint32_t i = lane + 64u * (uint32_t)t;
+        const float pk = i < a.dim ? p[i] : 0.0f;
+        acc[t] = __builtin_fmaf(pk, ck, acc[t]);
+      }
+    }
+    uint32_t rbits[T], key[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t i = lane + 64u * (uint32_t)t;
+      const _Float16 h = (_Float16)acc[t];
+      rbits[t] = (uint32_t)__builtin_bit_cast(uint16_t, h);
+      key[t] = i < a.dim ? (((rbits[t] & 0x7FFFu) << 16) | i) : 0u;
+    }
+    uint32_t prev[kMaxDup];
+    for (uint32_t r = 0; r < a.n_dup; ++r) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int t = 0; t < T; ++t) m = max(m, key[t]);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+      const uint32_t win = uniform(m);
+      const uint32_t coord = win & 0xFFFFu;
+      const uint32_t owner = coord & 63u, slot = coord >> 6;
+      uint32_t rb = 0;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        if ((uint32_t)t == slot) rb = rbits[t];
+      const uint32_t sign = (uniform((uint32_t)__shfl((int)rb, (int)owner, 64)) >> 15) & 1u;
+      const uint32_t shard = (2u * coord + sign) % a.n_parts;
+      bool dup = false;
+      for (uint32_t t = 0; t < r; ++t) dup = dup || prev[t] == shard;
+      prev[r] = dup ? kInvalid32 : shard;
+      if (lane == 0) {
+        a.shard_of[(size_t)row * a.n_dup + r] = dup ? kInvalid32 : shard;
+        a.pairs[(size_t)row * a.n_dup + r] = dup ? kEmptyKey : (((uint64_t)shard << 32) | (uint64_t)row);
+        if (!dup) atomicAdd(&a.shard_counts[shard], 1u);
+      }
+      if (lane == owner) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          if ((uint32_t)t == slot) key[t] = 0u;
+      }
+    }
+    wave_sync();
+  }
+}
+
+// Shard rows from the graph: row i of the shard is graph row ids[i] (the low
+// 32 bits of the sorted pairs).
+__global__ void gather_rows_kernel(const uint4* src, const uint64_t* ids, int64_t count, uint32_t words, uint4* dst) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= count * words) return;
+  const int64_t i = t / words, w = t % words;
+  dst[t] = src[(size_t)(uint32_t)ids[i] * words + w];
+}
+
+struct MergeArgs {
+  const uint64_t* ids;  // shard row -> global id (low 32 bits)
+  int64_t count;
+  const uint32_t* s_edges;
+  const uint16_t* s_edist;
+  const uint8_t* s_counts;
+  uint32_t R_int;
+  uint32_t* f_edges;
+  uint16_t* f_edist;
+  uint8_t* f_counts;
+  uint32_t R_fin;
+};
+
+// Order of a bf16 distance as the float comparison sees it (-0 = +0).
+__device__ __forceinline__ uint32_t bf16_order(uint32_t b) {
+  if ((b & 0x7FFFu) == 0u) b = 0u;
+  return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+}
+
+__global__ __launch_bounds__(64) void merge_rows_kernel(MergeArgs a) {
+  __shared__ uint32_t ids_l[128];
+  __shared__ uint16_t bits_l[128];
+  const uint32_t lane = lane_id();
+  for (int64_t i = blockIdx.x; i < a.count; i += gridDim.x) {
+    const uint32_t gid = (uint32_t)a.ids[i];
+    const uint32_t cf = uniform(a.f_counts[gid]);
+    const uint32_t cs = uniform(a.s_counts[i]);
+    const uint32_t el = min(lane, a.R_fin - 1u), sl = min(lane, a.R_int - 1u);
+    const uint32_t e_id = a.f_edges[(size_t)gid * a.R_fin + el];
+    const uint16_t e_bits = a.f_edist[(size_t)gid * a.R_fin + el];
+    const uint32_t s_loc = a.s_edges[(size_t)i * a.R_int + sl];
+    const uint16_t s_bits = a.s_edist[(size_t)i * a.R_int + sl];
+    const bool ve = lane < cf && lane < a.R_fin && e_id != kInvalid32;
+    bool vs = lane < cs && lane < a.R_int && s_loc != kInvalid32;
+    const uint32_t s_id = vs ? (uint32_t)a.ids[s_loc] : kInvalid32;
+    ids_l[lane] = ve ? e_id : kInvalid32;
+    bits_l[lane] = e_bits;
+    ids_l[64 + lane] = s_id;
+    bits_l[64 + lane] = s_bits;
+    wave_sync();
+    // a shard entry whose id the final row holds already: the final row's
+    // copy (same distance, earlier position) is the one kept
+    for (uint32_t j = 0; j < cf && j < 64; ++j) vs = vs && ids_l[j] != s_id;
+    uint64_t x0 = ve ? (((uint64_t)bf16_order(e_bits) << 32) | lane) : kEmptyKey;
+    uint64_t x1 = vs ? (((uint64_t)bf16_order(s_bits) << 32) | (64u + lane)) : kEmptyKey;
+    const uint32_t nv = (uint32_t)__builtin_popcountll(ballot(ve)) + (uint32_t)__builtin_popcountll(ballot(vs));
+    wave_bitonic_sort128(x0, x1);
+    const uint32_t keep = min(nv, a.R_fin);
+    if (lane < keep) {
+      const uint32_t pos = (uint32_t)x0 & 0xFFu;
+      a.f_edges[(size_t)gid * a.R_fin + lane] = ids_l[pos];
+      a.f_edist[(size_t)gid * a.R_fin + lane] = bits_l[pos];
+    }
+    if (lane == 0) a.f_counts[gid] = (uint8_t)keep;
+    wave_sync();
+  }
+}
+
+template <int T>
+void launch_assign(const AssignArgs& a, uint32_t grid, hipStream_t s) {
+  hipLaunchKernelGGL(assign_kernel<T>, dim3(grid), dim3(64), (size_t)a.dim * 4, s, a);
+}
+
+struct DeviceBuf {
+  void* p = nullptr;
+  explicit DeviceBuf(size_t bytes, const char* what) { hip_check(hipMalloc(&p, std::max<size_t>(bytes, 16)), what); }
+  ~DeviceBuf() { (void)hipFree(p); }
+  DeviceBuf(const DeviceBuf&) = delete;
+  DeviceBuf& operator=(const DeviceBuf&) = delete;
+  template <typename X>
+  X* as() const { return static_cast<X*>(p); }
+};
+
+// Steps of assign_shards on the device rows of g. Leaves the sorted pairs in
+// sorted[0, n * n_dup) and the shard sizes in counts_out.
+void assign_device(const Graph& g, uint32_t n_parts, uint32_t n_dup, uint64_t seed, uint32_t* shard_of,
+                   uint64_t* pairs, uint64_t* sorted, uint16_t* mean, std::vector<uint32_t>& counts_out,
+                   hipStream_t s) {
+  const int64_t n = g.n;
+  const uint32_t dim = g.dim;
+  // mean over rows 0, stride, 2 stride, ...
+  const int64_t target = std::min<int64_t>(n, 2000000);
+  const int64_t stride = std::max<int64_t>(1, n / target);
+  const int64_t sampled = (n + stride - 1) / stride;
+  const uint32_t blocks = (uint32_t)std::min<int64_t>(sampled, 4096);
+  const int64_t per_block = (sampled + blocks - 1) / blocks;
+  DeviceBuf partial((size_t)blocks * dim * 8, "alloc mean partials");
+  hipLaunchKernelGGL(mean_partial_kernel, dim3(blocks), dim3(256), 0, s, (const uint16_t*)g.vecs, g.dp, dim, stride,
+                     sampled, per_block, partial.as<double>());
+  hip_check(hipGetLastError(), "launch mean_partial_kernel");
+  hipLaunchKernelGGL(mean_final_kernel, dim3(1), dim3(256), 0, s, partial.as<const double>(), blocks, dim, sampled,
+                     mean);
+  hip_check(hipGetLastError(), "launch mean_final_kernel");
+  // the rotation matrix rounded to fp16, transposed for coalesced reads
+  const std::vector<float> P = rotation_matrix(dim, seed);
+  std::vector<float> pt((size_t)dim * dim);
+  for (uint32_t i = 0; i < dim; ++i)
+    for (uint32_t k = 0; k < dim; ++k) {
+      const uint16_t h = f2h_rn(P[(size_t)k + (size_t)i * dim]);
+      _Float16 hv;
+      std::memcpy(&hv, &h, 2);
+      pt[(size_t)k * dim + i] = (float)hv;
+    }
+  DeviceBuf dpt(pt.size() * 4, "alloc rotation");
+  DeviceBuf dcounts((size_t)n_parts * 4, "alloc shard counts");
+  hip_check(hipMemcpyAsync(dpt.p, pt.data(), pt.size() * 4, hipMemcpyHostToDevice, s), "upload rotation");
+  hip_check(hipMemsetAsync(dcounts.p, 0, (size_t)n_parts * 4, s), "clear shard counts");
+  AssignArgs a{};
+  a.vecs = (const uint16_t*)g.vecs;
+  a.n = n;
+  a.dp = g.dp;
+  a.dim = dim;
+  a.mean = mean;
+  a.pt = dpt.as<const float>();
+  a.n_parts = n_parts;
+  a.n_dup = n_dup;
+  a.shard_of = shard_of;
+  a.pairs = pairs;
+  a.shard_counts = dcounts.as<uint32_t>();
+  const uint32_t grid = (uint32_t)std::min<int64_t>(n, 65536);
+  const uint32_t T = (dim + 63) / 64;
+  if (T <= 1) launch_assign<1>(a, grid, s);
+  else if (T <= 2) launch_assign<2>(a, grid, s);
+  else if (T <= 4) launch_assign<4>(a, grid, s);
+  else if (T <= 8) launch_assign<8>(a, grid, s);
+  else if (T <= 16) launch_assign<16>(a, grid, s);
+  else throw std::invalid_argument("DiskANN shard assignment supports dim <= 1024");
+  hip_check(hipGetLastError(), "launch assign_kernel");
+  // group by shard, rows ascending within a shard
+  const size_t np = (size_t)n * n_dup;
+  int sbits = 1;
+  while ((1u << sbits) < n_parts) ++sbits;
+  const size_t tb = sort_u64_temp_bytes(np);
+  DeviceBuf temp(tb, "alloc sort temp");
+  sort_u64(temp.p, tb, pairs, sorted, np, 32 + sbits, s);
+  counts_out.assign(n_parts, 0);
+  hip_check(hipMemcpyAsync(counts_out.data(), dcounts.p, (size_t)n_parts * 4, hipMemcpyDeviceToHost, s),
+            "read shard counts");
+  hip_check(hipStreamSynchronize(s), "shard assignment");
+}
+
+void check_assign_args(const Graph& g, int64_t n_parts, int64_t n_dup) {
+  if (g.n <= 0) throw std::invalid_argument("graph is empty");
+  if (n_parts < 1 || n_parts > 0x7FFFFFFF) throw std::invalid_argument("n_parts must be positive");
+  if (n_dup < 1 || n_dup > (int64_t)kMaxDup)
+    throw std::invalid_argument("n_dup must be between 1 and " + std::to_string(kMaxDup));
+  if (g.dim > 1024) throw std::invalid_argument("DiskANN shard assignment supports dim <= 1024");
+}
+
+}  // namespace
+
+void diskann_assign(const Graph& g, int64_t n_parts, int64_t n_dup, uint64_t seed, uint32_t* shard_of_host,
+                    uint16_t* mean_host, hipStream_t s) {
+  check_assign_args(g, n_parts, n_dup);
+  const size_t np = (size_t)g.n * n_dup;
+  DeviceBuf shard_of(np * 4, "alloc shard ids");
+  DeviceBuf pairs(np * 8, "alloc shard pairs");
+  DeviceBuf sorted(np * 8, "alloc sorted shard pairs");
+  DeviceBuf mean((size_t)g.dim * 2, "alloc mean");
+  std::vector<uint32_t> counts;
+  assign_device(g, (uint32_t)n_parts, (uint32_t)n_dup, seed, shard_of.as<uint32_t>(), pairs.as<uint64_t>(),
+                sorted.as<uint64_t>(), mean.as<uint16_t>(), counts, s);
+  if (shard_of_host)
+    hip_check(hipMemcpy(shard_of_host, shard_of.p, np * 4, hipMemcpyDeviceToHost), "read shard ids");
+  if (mean_host) hip_check(hipMemcpy(mean_host, mean.p, (size_t)g.dim * 2, hipMemcpyDeviceToHost), "read mean");
+}
+
+void build_diskann(Graph& g, uint32_t R_int, float alpha, int64_t n_parts, int64_t n_dup, uint64_t seed,
+                   int64_t batch_cap, hipStream_t s, DiskannStats* stats) {
+  check_assign_args(g, n_parts, n_dup);
+  if (R_int < 1 || R_int > 64) throw std::invalid_argument("R_int must be between 1 and 64");
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  if (batch_cap < 1) batch_cap = 1;
+  DiskannStats st;
+  // events: 0 start, 1 shards assigned, 2 a shard's gather, 3 its build
+  // done, 4 its merge done
+  hipEvent_t e[5];
+  for (hipEvent_t& x : e) hip_check(hipEventCreate(&x), "event");
+  struct Events {
+    hipEvent_t* e;
+    ~Events() { for (int i = 0; i < 5; ++i) (void)hipEventDestroy(e[i]); }
+  } ev{e};
+  hip_check(hipEventRecord(e[0], s), "event record");
+
+  const size_t np = (size_t)g.n * n_dup;
+  DeviceBuf shard_of(np * 4, "alloc shard ids");
+  DeviceBuf pairs(np * 8, "alloc shard pairs");
+  DeviceBuf sorted(np * 8, "alloc sorted shard pairs");
+  DeviceBuf mean((size_t)g.dim * 2, "alloc mean");
+  std::vector<uint32_t> counts;
+  assign_device(g, (uint32_t)n_parts, (uint32_t)n_dup, seed, shard_of.as<uint32_t>(), pairs.as<uint64_t>(),
+                sorted.as<uint64_t>(), mean.as<uint16_t>(), counts, s);
+  hip_check(hipEventRecord(e[1], s), "event record");
+
+  // tasks: non-empty shards, largest first, equal sizes by shard index
+  std::vector<int64_t> offset((size_t)n_parts + 1, 0);
+  for (int64_t p = 0; p < n_parts; ++p) offset[(size_t)p + 1] = offset[(size_t)p] + counts[(size_t)p];
+  std::vector<int64_t> tasks;
+  for (int64_t p = 0; p < n_parts; ++p)
+    if (counts[(size_t)p]) tasks.push_back(p);
+  std::stable_sort(tasks.begin(), tasks.end(),
+                   [&](int64_t a, int64_t b) { return counts[(size_t)a] > counts[(size_t)b]; });
+  st.shards = (int64_t)tasks.size();
+  int64_t max_count = 0;
+  for (int64_t p : tasks) max_count = std::max<int64_t>(max_count, counts[(size_t)p]);
+  st.max_shard = max_count;
+
+  Graph sg;
+  sg.allocate(max_count, g.dim, R_int, g.metric, false);
+  const uint32_t words = g.dp / 8;
+  double build_ms = 0, merge_ms = 0;
+  for (int64_t p : tasks) {
+    const int64_t c = counts[(size_t)p];
+    const uint64_t* ids = sorted.as<uint64_t>() + offset[(size_t)p];
+    hip_check(hipEventRecord(e[2], s), "event record");
+    const int64_t threads = c * words;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s,
+                       (const uint4*)g.vecs, ids, c, words, (uint4*)sg.vecs);
+    hip_check(hipGetLastError(), "launch gather_rows_kernel");
+    hip_check(hipMemsetAsync(sg.counts, 0, (size_t)c, s), "clear shard degrees");
+    sg.n = c;
+    sg.medoid = 0;
+    // the shard's values lie in the graph's recorded range
+    sg.int_state = g.int_state;
+    sg.int_lo = g.int_lo;
+    sg.int_hi = g.int_hi;
+    build_graph(sg, alpha, std::max<int64_t>(1, std::min<int64_t>(batch_cap, c)), s, false, nullptr);
+    hip_check(hipEventRecord(e[3], s), "event record");
+    MergeArgs m{};
+    m.ids = ids;
+    m.count = c;
+    m.s_edges = sg.edges;
+    m.s_edist = sg.edist;
+    m.s_counts = sg.counts;
+    m.R_int = R_int;
+    m.f_edges = g.edges;
+    m.f_edist = g.edist;
+    m.f_counts = g.counts;
+    m.R_fin = g.R;
+    hipLaunchKernelGGL(merge_rows_kernel, dim3((uint32_t)std::min<int64_t>(c, 1 << 20)), dim3(64), 0, s, m);
+    hip_check(hipGetLastError(), "launch merge_rows_kernel");
+    hip_check(hipEventRecord(e[4], s), "event record");
+    hip_check(hipEventSynchronize(e[4]), "diskann shard");
+    float b = 0, mm = 0;
+    hip_check(hipEventElapsedTime(&b, e[2], e[3]), "event elapsed");
+    hip_check(hipEventElapsedTime(&mm, e[3], e[4]), "event elapsed");
+    build_ms += b;
+    merge_ms += mm;
+  }
+  hip_check(hipEventRecord(e[4], s), "event record");
+  hip_check(hipStreamSynchronize(s), "diskann build");
+  float assign = 0, total = 0;
+  hip_check(hipEventElapsedTime(&assign, e[0], e[1]), "event elapsed");
+  hip_check(hipEventElapsedTime(&total, e[0], e[4]), "event elapsed");
+  st.assign_ms = assign;
+  st.build_ms = build_ms;
+  st.merge_ms = merge_ms;
+  st.total_ms = total;
+  g.medoid = 0;
+  if (stats) *stats = st;
+}
+
+}  // namespace jasper_amd
