@@ -210,15 +210,16 @@ def main() -> int:
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--path", default="search",
                     choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5", "updates",
-                             "scale"],
+                             "scale", "diskann"],
                     help="search (default, the headline metric) or one of the other hot-path rows, each "
                          "printing its own JSON line: directional (config 3, LSH), pq (PQ-ADC on "
                          "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
                          "rabitq (one-bit codes), c4 (config 4: 1M x 960 build + PQ search), c5 "
                          "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search), updates "
                          "(config 2: mark_deleted 10%%, consolidate, append 100k), scale (config 2: the "
-                         "partitioned build)")
+                         "partitioned build), diskann (config 2: the DiskANN build)")
     ap.add_argument("--scale-parts", default="4,2,8", help="partition counts of --path scale (first = the line's value)")
+    ap.add_argument("--diskann-parts", default="8,4,16", help="shard counts of --path diskann (first = the line's value)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
     ap.add_argument("--int-exact", type=int, default=1, choices=[0, 1],
@@ -913,8 +914,70 @@ def run_scale(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
+def run_diskann(args, torch, jasper_amd, datasets, dev, log):
+    """The DiskANN build (construct_diskann.cuh, cmd/create_diskann_index.cu)
+    on config 2 (1M x 128 clustered, L2, budget 10 GB): cross-polytope LSH
+    shards with 2 copies, shards built at R_int = 32, merged to R = 64 (the
+    reference's f16_r32_64_l2) and to R = 32; timed once each, recall@10 of
+    the 10k queries beside the plain build's."""
+    n, nq, dim = args.n, args.nq, 128
+    base = torch.from_numpy(datasets.clustered(n, dim, 0)).to(dev)
+    q = torch.from_numpy(datasets.clustered(nq, dim, 1)).to(dev)
+    gt, _ = jasper_amd.bruteforce_knn(base, q, 10, "l2")
+    gt = gt.cpu().numpy()
+    bws = (32, 44, 64, 128)
+
+    def recalls(g):
+        out = {}
+        for b in bws:
+            ids, _ = g.search(q, k=10, beam_width=b)
+            torch.cuda.synchronize()
+            out[b] = _recall(gt, ids.cpu().numpy())
+        return out
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2)
+    torch.cuda.synchronize()
+    plain_s = time.perf_counter() - t0
+    plain_r = recalls(g)
+    g.free()
+    log(f"plain build (R 64) {plain_s:.2f}s, recall@10 {plain_r}")
+    runs = []
+    for R_fin in (64, 32):
+        for P in [int(x) for x in args.diskann_parts.split(",")]:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            g = jasper_amd.Graph.build_diskann(base, n_neighbors=R_fin, r_int=32, distance="l2", alpha=1.2,
+                                               n_parts=P, n_dup=2, workspace_budget="10GB")
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            st = jasper_amd.last_diskann_stats()
+            r = recalls(g)
+            g.free()
+            runs.append({"R_fin": R_fin, "n_parts": P, "build_s": wall, "assign_s": st["assign_ms"] / 1e3,
+                         "shard_builds_s": st["build_ms"] / 1e3, "merges_s": st["merge_ms"] / 1e3,
+                         "shards": int(st["shards"]), "max_shard": int(st["max_shard"]),
+                         "recall_at_10": {str(b): v for b, v in r.items()}})
+            log(f"R_fin={R_fin} n_parts={P}: {wall:.2f}s (assign {st['assign_ms']:.1f} ms, shard builds "
+                f"{st['build_ms'] / 1e3:.2f}s, merges {st['merge_ms']:.1f} ms, largest shard "
+                f"{int(st['max_shard'])}), recall@10 {r}")
+    head = runs[0]
+    res = _line(args, f"DiskANN build, config 2: vectors/s (R_int 32 -> R 64, {head['n_parts']} shards, 2 copies)",
+                n / head["build_s"], "vectors/s", head["build_s"] * 1000.0, "f32",
+                {"workload": f"config 2 ({n} x 128 clustered, L2, alpha 1.2), budget 10 GB: cross-polytope LSH "
+                             f"shards (seed 42, 2 copies), shards built at R_int 32 (batches min(budget batch, "
+                             f"n / n_parts / 20)), merged by stored distance; recall@10 of {nq} queries",
+                 "plain_build_s": plain_s, "plain_recall_at_10": {str(b): v for b, v in plain_r.items()},
+                 "runs": runs}, None)
+    res["steps"], res["warmup"] = 1, 0
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 OTHER_PATHS = {"c4": run_c4, "c5": run_c5, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
-               "rotate": run_rotate, "rabitq": run_rabitq, "updates": run_updates, "scale": run_scale}
+               "rotate": run_rotate, "rabitq": run_rabitq, "updates": run_updates, "scale": run_scale,
+               "diskann": run_diskann}
 
 
 if __name__ == "__main__":
