@@ -528,7 +528,8 @@ static void reverse_step(const Graph& g, PruneKernelArgs& pa, const BuildWorkspa
   const uint32_t grid = (uint32_t)std::min<int64_t>(std::max<int64_t>(np, 1), 16384);
   timer.start();
   if (SCALE) {
-    if (g.metric == kL2) dispatch_prune<kL2, false, true>(true, cpl, pa, grid, plds, stream);
+    if (intx) dispatch_prune<kL2, true, true>(true, cpl, pa, grid, plds, stream);
+    else if (g.metric == kL2) dispatch_prune<kL2, false, true>(true, cpl, pa, grid, plds, stream);
     else dispatch_prune<kIP, false, true>(true, cpl, pa, grid, plds, stream);
   } else {
     if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
@@ -725,7 +726,8 @@ void build_scale(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int
         launch_beam_search(g, r, stream);
         // 2. forward merge + merge prune into B1, pairs for B2 targets
         pa.batch_offset = (uint32_t)(b1s + count);
-        if (g.metric == kL2) dispatch_prune<kL2, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        if (intx) dispatch_prune<kL2, true, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        else if (g.metric == kL2) dispatch_prune<kL2, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
         else dispatch_prune<kIP, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
         hip_check(hipGetLastError(), "launch forward_prune_kernel (merge)");
         // 3-4. reverse edges into B2 (process_reverse_edges_kernel_scale)

@@ -4,13 +4,15 @@
 //   1. Shards by cross-polytope LSH (assign_shards, :104-276): each row,
 //      centred on the sampled mean and rotated by the seed's orthogonal
 //      matrix, goes to the shards of its n_dup largest |coordinates| (bucket
-//      2 coord + sign, shard bucket mod n_parts). One wave per row: the
-//      centred row sits in LDS, each lane accumulates the rotated
-//      coordinates lane, lane + 64, ... in fp32 (k ascending, one fma per
-//      term; cuBLAS's order in the reference is unspecified), and n_dup wave
+//      2 coord + sign, shard bucket mod n_parts). One wave per row: each
+//      lane holds the centred coordinates lane, lane + 64, ... and
+//      accumulates the rotated ones with the same indexes in fp32 (k
+//      ascending, coordinate k broadcast by v_readlane, one fma per term;
+//      cuBLAS's order in the reference is unspecified), and n_dup wave
 //      max-reductions over the packed keys (|bits| << 16 | coord) pick the
 //      ranks. The (shard, row) pairs are radix-sorted, which lists every
-//      shard's rows in ascending order, and counted per shard.
+//      shard's rows in ascending order; shard sizes come from the run
+//      boundaries.
 //   2. Each shard, largest first, is gathered into a shard graph of degree
 //      R_int and built with the plain construction (build_graph: batches
 //      doubling to min(batch cap, shard size), search from its first row).
@@ -74,13 +76,21 @@ __global__ void mean_partial_kernel(const uint16_t* vecs, uint32_t dp, uint32_t 
   }
 }
 
-__global__ void mean_final_kernel(const double* partial, uint32_t blocks, uint32_t dim, int64_t sampled,
-                                  uint16_t* mean) {
-  for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x) {
-    double acc = 0.0;
-    for (uint32_t b = 0; b < blocks; ++b) acc += partial[(size_t)b * dim + d];
-    mean[d] = d2h_rn(acc / (double)(sampled > 0 ? sampled : 1));
+// One block per coordinate: the partial sums in any order (they are exact),
+// a tree in LDS, one rounding to fp16.
+__global__ __launch_bounds__(256) void mean_final_kernel(const double* partial, uint32_t blocks, uint32_t dim,
+                                                         int64_t sampled, uint16_t* mean) {
+  __shared__ double red[256];
+  const uint32_t d = blockIdx.x;
+  double acc = 0.0;
+  for (uint32_t b = threadIdx.x; b < blocks; b += 256) acc += partial[(size_t)b * dim + d];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (uint32_t w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
   }
+  if (threadIdx.x == 0) mean[d] = d2h_rn(red[0] / (double)(sampled > 0 ? sampled : 1));
 }
 
 struct AssignArgs {
@@ -92,33 +102,67 @@ struct AssignArgs {
   uint32_t n_parts, n_dup;
   uint32_t* shard_of;    // [n, n_dup]
   uint64_t* pairs;       // [n, n_dup]: shard << 32 | row, empty for repeats
-  uint32_t* shard_counts;  // [n_parts]
 };
 
-// One wave (one 64-thread block) per row, grid-stride.
-template <int T>
-__global__ __launch_bounds__(64) void assign_kernel(AssignArgs a) {
-  extern __shared__ float crow[];  // [dim] centred row
+// Shard sizes from the sorted pairs: each shard's run [start, end) is
+// found at its boundaries (no atomics: one shard's counter would be hit by
+// every row that lands in it).
+__global__ void shard_bounds_kernel(const uint64_t* sorted, int64_t np, uint32_t* start, uint32_t* end) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= np) return;
+  const uint64_t k = sorted[i];
+  if (k == kEmptyKey) return;
+  const uint32_t sh = (uint32_t)(k >> 32);
+  if (i == 0 || (uint32_t)(sorted[i - 1] >> 32) != sh) start[sh] = (uint32_t)i;
+  if (i + 1 == np || sorted[i + 1] == kEmptyKey || (uint32_t)(sorted[i + 1] >> 32) != sh) end[sh] = (uint32_t)(i + 1);
+}
+
+// Four waves per block, one row per wave at a time (grid-stride). The
+// rotation (f32 values of the fp16 matrix, pt[k * dim + i]) is staged in LDS
+// when it fits (dim <= 128: 64 KB); lane l owns output coordinates l, l + 64,
+// ... and input coordinates likewise, and coordinate k of the centred row
+// reaches every lane by v_readlane, k ascending.
+constexpr uint32_t kAssignWaves = 4;
+
+template <int T, bool LDS_P>
+__global__ __launch_bounds__(64 * kAssignWaves) void assign_kernel(AssignArgs a) {
+  extern __shared__ float pt_l[];
   const uint32_t lane = lane_id();
-  for (int64_t row = blockIdx.x; row < a.n; row += gridDim.x) {
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t dim = a.dim;
+  if constexpr (LDS_P) {
+    for (uint32_t j = threadIdx.x; j < dim * dim; j += 64 * kAssignWaves) pt_l[j] = a.pt[j];
+    __syncthreads();
+  }
+  const int64_t step = (int64_t)gridDim.x * kAssignWaves;
+  for (int64_t row = (int64_t)blockIdx.x * kAssignWaves + wave; row < a.n; row += step) {
     const uint16_t* x = a.vecs + (size_t)row * a.dp;
-    for (uint32_t k = lane; k < a.dim; k += 64) {
+    float c[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t k = lane + 64u * (uint32_t)t;
       // subtract_mean_kernel: v - mean in fp16, one rounding
-      const _Float16 c = (_Float16)(__builtin_bit_cast(_Float16, x[k]) - __builtin_bit_cast(_Float16, a.mean[k]));
-      crow[k] = (float)c;
+      c[t] = k < dim ? (float)(_Float16)(__builtin_bit_cast(_Float16, x[k]) -
+                                         __builtin_bit_cast(_Float16, a.mean[k]))
+                     : 0.0f;
     }
-    wave_sync();
     float acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = 0.0f;
-    for (uint32_t k = 0; k < a.dim; ++k) {
-      const float ck = crow[k];
-      const float* p = a.pt + (size_t)k * a.dim;
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const uint32_t i = lane + 64u * (uint32_t)t;
-        const float pk = i < a.dim ? p[i] : 0.0f;
-        acc[t] = __builtin_fmaf(pk, ck, acc[t]);
+    for (int tk = 0; tk < T; ++tk) {
+      const uint32_t k0 = 64u * (uint32_t)tk;
+      const uint32_t kend = dim > k0 ? min(64u, dim - k0) : 0u;
+      for (uint32_t kk = 0; kk < kend; ++kk) {
+        const float ck = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c[tk]), (int)kk));
+        const size_t base = (size_t)(k0 + kk) * dim;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint32_t i = lane + 64u * (uint32_t)t;
+          float pk = 0.0f;
+          if (i < dim) pk = LDS_P ? pt_l[base + i] : a.pt[base + i];
+          acc[t] = __builtin_fmaf(pk, ck, acc[t]);
+        }
       }
     }
     uint32_t rbits[T], key[T];
@@ -127,7 +171,7 @@ __global__ __launch_bounds__(64) void assign_kernel(AssignArgs a) {
       const uint32_t i = lane + 64u * (uint32_t)t;
       const _Float16 h = (_Float16)acc[t];
       rbits[t] = (uint32_t)__builtin_bit_cast(uint16_t, h);
-      key[t] = i < a.dim ? (((rbits[t] & 0x7FFFu) << 16) | i) : 0u;
+      key[t] = i < dim ? (((rbits[t] & 0x7FFFu) << 16) | i) : 0u;
     }
     uint32_t prev[kMaxDup];
     for (uint32_t r = 0; r < a.n_dup; ++r) {
@@ -151,7 +195,6 @@ __global__ __launch_bounds__(64) void assign_kernel(AssignArgs a) {
       if (lane == 0) {
         a.shard_of[(size_t)row * a.n_dup + r] = dup ? kInvalid32 : shard;
         a.pairs[(size_t)row * a.n_dup + r] = dup ? kEmptyKey : (((uint64_t)shard << 32) | (uint64_t)row);
-        if (!dup) atomicAdd(&a.shard_counts[shard], 1u);
       }
       if (lane == owner) {
 #pragma unroll
@@ -159,7 +202,6 @@ __global__ __launch_bounds__(64) void assign_kernel(AssignArgs a) {
           if ((uint32_t)t == slot) key[t] = 0u;
       }
     }
-    wave_sync();
   }
 }
 
@@ -231,8 +273,15 @@ __global__ __launch_bounds__(64) void merge_rows_kernel(MergeArgs a) {
 }
 
 template <int T>
-void launch_assign(const AssignArgs& a, uint32_t grid, hipStream_t s) {
-  hipLaunchKernelGGL(assign_kernel<T>, dim3(grid), dim3(64), (size_t)a.dim * 4, s, a);
+void launch_assign(const AssignArgs& a, hipStream_t s) {
+  const uint32_t grid = (uint32_t)std::min<int64_t>((a.n + kAssignWaves - 1) / kAssignWaves, 2048);
+  if ((size_t)a.dim * a.dim * 4 <= 64 * 1024) {
+    auto k = assign_kernel<T, true>;
+    hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024), "LDS");
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * kAssignWaves), (size_t)a.dim * a.dim * 4, s, a);
+  } else {
+    hipLaunchKernelGGL((assign_kernel<T, false>), dim3(grid), dim3(64 * kAssignWaves), 0, s, a);
+  }
 }
 
 struct DeviceBuf {
@@ -262,7 +311,7 @@ void assign_device(const Graph& g, uint32_t n_parts, uint32_t n_dup, uint64_t se
   hipLaunchKernelGGL(mean_partial_kernel, dim3(blocks), dim3(256), 0, s, (const uint16_t*)g.vecs, g.dp, dim, stride,
                      sampled, per_block, partial.as<double>());
   hip_check(hipGetLastError(), "launch mean_partial_kernel");
-  hipLaunchKernelGGL(mean_final_kernel, dim3(1), dim3(256), 0, s, partial.as<const double>(), blocks, dim, sampled,
+  hipLaunchKernelGGL(mean_final_kernel, dim3(dim), dim3(256), 0, s, partial.as<const double>(), blocks, dim, sampled,
                      mean);
   hip_check(hipGetLastError(), "launch mean_final_kernel");
   // the rotation matrix rounded to fp16, transposed for coalesced reads
@@ -276,9 +325,9 @@ void assign_device(const Graph& g, uint32_t n_parts, uint32_t n_dup, uint64_t se
       pt[(size_t)k * dim + i] = (float)hv;
     }
   DeviceBuf dpt(pt.size() * 4, "alloc rotation");
-  DeviceBuf dcounts((size_t)n_parts * 4, "alloc shard counts");
+  DeviceBuf bounds((size_t)n_parts * 8, "alloc shard bounds");
   hip_check(hipMemcpyAsync(dpt.p, pt.data(), pt.size() * 4, hipMemcpyHostToDevice, s), "upload rotation");
-  hip_check(hipMemsetAsync(dcounts.p, 0, (size_t)n_parts * 4, s), "clear shard counts");
+  hip_check(hipMemsetAsync(bounds.p, 0, (size_t)n_parts * 8, s), "clear shard bounds");
   AssignArgs a{};
   a.vecs = (const uint16_t*)g.vecs;
   a.n = n;
@@ -290,14 +339,12 @@ void assign_device(const Graph& g, uint32_t n_parts, uint32_t n_dup, uint64_t se
   a.n_dup = n_dup;
   a.shard_of = shard_of;
   a.pairs = pairs;
-  a.shard_counts = dcounts.as<uint32_t>();
-  const uint32_t grid = (uint32_t)std::min<int64_t>(n, 65536);
   const uint32_t T = (dim + 63) / 64;
-  if (T <= 1) launch_assign<1>(a, grid, s);
-  else if (T <= 2) launch_assign<2>(a, grid, s);
-  else if (T <= 4) launch_assign<4>(a, grid, s);
-  else if (T <= 8) launch_assign<8>(a, grid, s);
-  else if (T <= 16) launch_assign<16>(a, grid, s);
+  if (T <= 1) launch_assign<1>(a, s);
+  else if (T <= 2) launch_assign<2>(a, s);
+  else if (T <= 4) launch_assign<4>(a, s);
+  else if (T <= 8) launch_assign<8>(a, s);
+  else if (T <= 16) launch_assign<16>(a, s);
   else throw std::invalid_argument("DiskANN shard assignment supports dim <= 1024");
   hip_check(hipGetLastError(), "launch assign_kernel");
   // group by shard, rows ascending within a shard
@@ -307,10 +354,16 @@ void assign_device(const Graph& g, uint32_t n_parts, uint32_t n_dup, uint64_t se
   const size_t tb = sort_u64_temp_bytes(np);
   DeviceBuf temp(tb, "alloc sort temp");
   sort_u64(temp.p, tb, pairs, sorted, np, 32 + sbits, s);
-  counts_out.assign(n_parts, 0);
-  hip_check(hipMemcpyAsync(counts_out.data(), dcounts.p, (size_t)n_parts * 4, hipMemcpyDeviceToHost, s),
-            "read shard counts");
+  uint32_t* start = bounds.as<uint32_t>();
+  uint32_t* end = start + n_parts;
+  hipLaunchKernelGGL(shard_bounds_kernel, dim3((uint32_t)((np + 255) / 256)), dim3(256), 0, s, sorted, (int64_t)np,
+                     start, end);
+  hip_check(hipGetLastError(), "launch shard_bounds_kernel");
+  std::vector<uint32_t> be((size_t)n_parts * 2);
+  hip_check(hipMemcpyAsync(be.data(), bounds.p, (size_t)n_parts * 8, hipMemcpyDeviceToHost, s), "read shard bounds");
   hip_check(hipStreamSynchronize(s), "shard assignment");
+  counts_out.assign(n_parts, 0);
+  for (uint32_t p = 0; p < n_parts; ++p) counts_out[p] = be[(size_t)n_parts + p] - be[p];
 }
 
 void check_assign_args(const Graph& g, int64_t n_parts, int64_t n_dup) {
