@@ -25,6 +25,7 @@
 
 #include <algorithm>
 #include <cfloat>
+#include <cstdlib>
 #include <stdexcept>
 
 namespace jasper_amd {
@@ -276,6 +277,7 @@ __global__ __launch_bounds__(64) void bf_merge_kernel(const uint64_t* __restrict
 constexpr int64_t kBfSample = 65536;
 constexpr int64_t kBfTwoPassMin = 4 * kBfSample;
 constexpr uint32_t kBfCandCap = 1024;
+constexpr uint32_t kBfLocal = 16;  // candidates a filter work-group stages per query before appending to HBM
 
 // Appends a candidate key to query q's list (a rare path, kept out of line
 // so that its address arithmetic does not occupy registers in the loop).
@@ -285,10 +287,10 @@ __device__ __noinline__ void bf_append(uint32_t* qcount, uint64_t* qcand, uint32
 }
 
 // Cooperative base-tile staging of bf_filter_kernel: thread element i is
-// (row srow[i], chunk scol[i]) of the 32-row tile starting at v0.
+// (row srow[i], chunk scol[i]) of the ROWS-row tile starting at v0.
 // (native vector registers: a uint4 struct copied under a condition stays in
 // private memory)
-template <int PER, int METRIC>
+template <int PER, int ROWS, int METRIC>
 __device__ __forceinline__ void bf_gload(const uint4* base4, const float* vsq, int64_t v0, int64_t v_begin,
                                          int64_t v_end, uint32_t nck, uint32_t nel, uint32_t tid,
                                          const uint32_t (&srow)[PER], const uint32_t (&scol)[PER],
@@ -301,45 +303,83 @@ __device__ __forceinline__ void bf_gload(const uint4* base4, const float* vsq, i
     stage[i] = *reinterpret_cast<const u32x4*>(base4 + (size_t)(vv < v_end ? vv : v_begin) * nck + (in ? scol[i] : 0u));
   }
   if constexpr (METRIC == kL2) {
-    const int64_t vv = v0 + (tid & 31u);
+    const int64_t vv = v0 + (tid & (uint32_t)(ROWS - 1));
     svs = vsq[vv < v_end ? vv : v_begin];
   }
 }
 
-template <int PER>
+// The filter's cheap test reads ||v||^2 shrunk by 2^-20 (see bf_filter_kernel).
+constexpr float kBfVsShrink = 1.0f - 0x1p-20f;
+
+template <int PER, int ROWS>
 __device__ __forceinline__ void bf_sstore(uint4* tile, float* tvs, uint32_t buf, uint32_t rs, uint32_t nel,
                                           uint32_t tid, const uint32_t (&srow)[PER], const uint32_t (&scol)[PER],
                                           const u32x4 (&stage)[PER], float svs) {
 #pragma unroll
   for (int i = 0; i < PER; ++i)
     if (tid + 256u * (uint32_t)i < nel)
-      *reinterpret_cast<u32x4*>(tile + buf * 32 * rs + srow[i] * rs + scol[i]) = stage[i];
-  if (tid < 32) tvs[buf * 32 + tid] = svs;
+      *reinterpret_cast<u32x4*>(tile + buf * ROWS * rs + srow[i] * rs + scol[i]) = stage[i];
+  if (tid < (uint32_t)ROWS) {
+    tvs[buf * ROWS + tid] = svs;
+    tvs[2 * ROWS + buf * ROWS + tid] = svs * kBfVsShrink;
+  }
 }
 
-template <int KS, int TILES, int METRIC>
+// TILES: 32-query tiles per wave; SUB: 32-row base tiles per step (one
+// barrier per SUB tiles, SUB independent matrix-core chains per query tile).
+template <int KS, int TILES, int SUB, int METRIC>
 __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restrict__ base, int64_t n, uint32_t dp,
                                                         const uint16_t* __restrict__ queries, int64_t nq,
                                                         const float* __restrict__ vsq, const float* __restrict__ qsq,
                                                         const float* __restrict__ qthr, uint32_t thr_stride,
-                                                        int64_t chunk, uint32_t* __restrict__ qcount,
+                                                        int64_t chunk, uint32_t qblocks,
+                                                        uint32_t* __restrict__ qcount,
                                                         uint64_t* __restrict__ qcand) {
-  // LDS: two base tiles of 32 rows, row stride nck + 1 chunks (the extra
+  // XCD-aware work order: work-groups are dealt to the 8 XCDs round-robin
+  // by id, so work-group p runs on XCD p % 8. Logical item L = (the items of
+  // the XCDs before it) + p / 8, with query block L % qblocks and base chunk
+  // L / qblocks: the query blocks of one chunk run on one XCD together and
+  // read its base tiles through that XCD's L2 (dealt round-robin they would
+  // fetch every tile into all eight L2s).
+  const uint32_t G = gridDim.x, p = blockIdx.x, xcd = p & 7u, per = G >> 3, extra = G & 7u;
+  const uint32_t L = xcd * per + min(xcd, extra) + (p >> 3);
+  const uint32_t qblock = L % qblocks, cblock = L / qblocks;
+  // LDS: two base tiles of ROWS rows, row stride nck + 1 chunks (the extra
   // chunk is zero: it is the K slot past the row when dp % 16 == 8, and it
-  // staggers the rows across banks); two sets of 32 squared norms; per wave
-  // and query tile the 32 query norms and thresholds
+  // staggers the rows across banks); two sets of ROWS squared norms (and
+  // their shrunk copies); per wave and query tile the 32 query norms,
+  // thresholds and cheap-test bounds.
+  //
+  // L2 scores first take a cheap conservative test: y = fl(2 q.v - vs')
+  // >= c_q, with vs' = fl(||v||^2 (1 - 2^-20)) and c_q <= (||q||^2 - T_q) -
+  // 2^-19 (||q||^2 + T_q). Whenever the exact score d = fl(fl(||q||^2 +
+  // ||v||^2) - 2 q.v) satisfies d <= T_q (T_q >= 0), y passes: with u =
+  // 2^-24 and |2 q.v| <= (||q||^2 + ||v||^2)(1 + 128u), d <= T_q gives
+  // 2 q.v - ||v||^2 >= ||q||^2 - T_q - (||q||^2 + ||v||^2 + 2 T_q) u, and y
+  // exceeds 2 q.v - ||v||^2 by at least 11.9 u ||v||^2 - 2.1 u ||q||^2. Only
+  // a 32 x 32 block in which some lane's test passes computes the exact
+  // scores and their appends; the others cost one fma and one compare per
+  // score.
+  constexpr int ROWS = 32 * SUB;
   extern __shared__ uint4 bf_tile[];
   const uint32_t nck = dp / 8, rs = nck + 1;
-  float* tvs = reinterpret_cast<float*>(bf_tile + 2 * 32 * rs);  // [2][32]
-  float* sqs = tvs + 64;              // [4 waves][TILES][32]
+  float* tvs = reinterpret_cast<float*>(bf_tile + 2 * ROWS * rs);  // [2][ROWS] norms, then [2][ROWS] shrunk
+  float* sqs = tvs + 4 * ROWS;         // [4 waves][TILES][32]
   float* sth = sqs + 4 * TILES * 32;   // [4 waves][TILES][32]
+  float* scr = sth + 4 * TILES * 32;   // [4 waves][TILES][32] c_q of the cheap test
+  // per wave and query row: a count and kBfLocal staged candidate keys
+  // (wave-private; flushed to the query's HBM list once, at the end)
+  uint32_t* lcnt = reinterpret_cast<uint32_t*>(scr + 4 * TILES * 32);  // [4 waves][TILES * 32]
+  uint64_t* lbuf = reinterpret_cast<uint64_t*>(lcnt + 4 * TILES * 32); // [4 waves][TILES * 32][kBfLocal]
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u, am = lane & 31u, ah = lane >> 5;
-  const int64_t qbase = (int64_t)blockIdx.x * (128 * TILES) + (int64_t)w * (32 * TILES);
-  const int64_t v_begin = (int64_t)blockIdx.y * chunk;
+  const int64_t qbase = (int64_t)qblock * (128 * TILES) + (int64_t)w * (32 * TILES);
+  for (uint32_t r = lane; r < 32u * TILES; r += 64) lcnt[w * TILES * 32 + r] = 0u;
+  const int64_t v_begin = (int64_t)cblock * chunk;
   const int64_t v_end = min(n, v_begin + chunk);
   const uint4* base4 = reinterpret_cast<const uint4*>(base);
 
-  if (tid < 64) bf_tile[(tid >> 5) * 32 * rs + (tid & 31u) * rs + nck] = make_uint4(0, 0, 0, 0);
+  for (uint32_t r = tid; r < 2u * ROWS; r += 256) bf_tile[(r / ROWS) * ROWS * rs + (r % ROWS) * rs + nck] =
+      make_uint4(0, 0, 0, 0);
   uint4 af[TILES][KS];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
@@ -352,14 +392,19 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
     }
     if (ah == 0) {
       // a NaN threshold passes nothing (rows past the last query)
-      sqs[(w * TILES + t) * 32 + am] = (METRIC == kL2 && aq < nq) ? qsq[aq] : 0.0f;
-      sth[(w * TILES + t) * 32 + am] = aq < nq ? qthr[(size_t)aq * thr_stride] : __builtin_nanf("");
+      const float qn = (METRIC == kL2 && aq < nq) ? qsq[aq] : 0.0f;
+      const float th = aq < nq ? qthr[(size_t)aq * thr_stride] : __builtin_nanf("");
+      sqs[(w * TILES + t) * 32 + am] = qn;
+      sth[(w * TILES + t) * 32 + am] = th;
+      // c_q in double, pushed below its own rounding to fp32
+      const double c = ((double)qn - (double)th) - ((double)qn + fabs((double)th)) * 0x1p-19;
+      scr[(w * TILES + t) * 32 + am] = (float)(c - fabs(c) * 0x1p-22);
     }
   }
 
   // cooperative tile loads: thread element i is (row srow[i], chunk scol[i])
-  constexpr int kPer = (32 * 2 * KS + 255) / 256;
-  const uint32_t nel = 32 * nck;
+  constexpr int kPer = (ROWS * 2 * KS + 255) / 256;
+  const uint32_t nel = ROWS * nck;
   uint32_t srow[kPer], scol[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -373,9 +418,9 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
   u32x4 sta[kPer], stb[kPer];
   float sva = 0.0f, svb = 0.0f;
   if (v_begin < v_end) {
-    bf_gload<kPer, METRIC>(base4, vsq, v_begin, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
-    bf_sstore<kPer>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
-    bf_gload<kPer, METRIC>(base4, vsq, v_begin + 32, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v_begin, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
+    bf_sstore<kPer, ROWS>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v_begin + ROWS, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
   }
   __syncthreads();
   // every load issued so far (query fragments, first tiles) completes here:
@@ -383,60 +428,98 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
   // iteration, the prefetched tile included
   __builtin_amdgcn_s_waitcnt(0);
   auto step = [&](int64_t v0, uint32_t buf) {
-    const uint4* brow = bf_tile + buf * 32 * rs + am * rs;
-    uint4 b[KS];
+    // the chains of every (query tile, base sub-tile) interleaved; each
+    // accumulates over s in order, as bf_scan_kernel does: the distances
+    // must match it bit for bit
+    float16v accs[TILES][SUB];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) b[s] = brow[(uint32_t)s * 2 + ah];
-    const float vs = tvs[buf * 32 + am];
-    const int64_t v = v0 + am;
-    const bool vok = v < v_end;
-    // the tiles' MFMA chains interleaved (each tile accumulates over s in
-    // order, as bf_scan_kernel does: the distances must match it bit for bit)
-    float16v accs[TILES];
+    for (int t = 0; t < TILES; ++t)
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) accs[t] = float16v{};
+      for (int u = 0; u < SUB; ++u) accs[t][u] = float16v{};
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+    for (int s = 0; s < KS; ++s) {
+      uint4 b[SUB];
+#pragma unroll
+      for (int u = 0; u < SUB; ++u) b[u] = bf_tile[buf * ROWS * rs + (32u * u + am) * rs + (uint32_t)s * 2 + ah];
 #pragma unroll
       for (int t = 0; t < TILES; ++t)
-        accs[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[t][s]), u4_as_h8(b[s]), accs[t], 0, 0, 0);
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      const float16v acc = accs[t];
+        for (int u = 0; u < SUB; ++u)
+          accs[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[t][s]), u4_as_h8(b[u]), accs[t][u], 0, 0, 0);
+    }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        // rows 8g + 4ah + j, j = 0..3
-        const uint32_t row0 = 8u * (uint32_t)g + 4u * ah;
-        const float4 q4 = *reinterpret_cast<const float4*>(sqs + (w * TILES + t) * 32 + row0);
-        const float4 t4 = *reinterpret_cast<const float4*>(sth + (w * TILES + t) * 32 + row0);
-        const float qsv[4] = {q4.x, q4.y, q4.z, q4.w}, thv[4] = {t4.x, t4.y, t4.z, t4.w};
+    for (int u = 0; u < SUB; ++u) {
+      const float vs = tvs[buf * ROWS + 32u * u + am];
+      const float vsm = tvs[2 * ROWS + buf * ROWS + 32u * u + am];
+      const int64_t v = v0 + 32 * u + am;
+      const bool vok = v < v_end;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float d;
-          if constexpr (METRIC == kL2) d = __builtin_fmaf(-2.0f, acc[4 * g + j], qsv[j] + vs);
-          else d = -__half2float(__float2half_rn(acc[4 * g + j]));
-          if (vok && d <= thv[j]) {
-            if constexpr (METRIC == kL2) d = d < 0.0f ? 0.0f : d;
-            bf_append(qcount, qcand, (uint32_t)qbase + (uint32_t)(32 * t + j) + row0, bf_key(d, (uint32_t)v));
+      for (int t = 0; t < TILES; ++t) {
+        const float16v acc = accs[t][u];
+        if constexpr (METRIC == kL2) {
+          uint64_t any = 0;  // lanes with a passing score, one compare mask per score
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const uint32_t row0 = 8u * (uint32_t)g + 4u * ah;
+            const float4 c4 = *reinterpret_cast<const float4*>(scr + (w * TILES + t) * 32 + row0);
+            const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) any |= ballot(__builtin_fmaf(2.0f, acc[4 * g + j], -vsm) >= cv[j]);
+          }
+          if (any == 0) continue;
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          // rows 8g + 4ah + j, j = 0..3
+          const uint32_t row0 = 8u * (uint32_t)g + 4u * ah;
+          const float4 q4 = *reinterpret_cast<const float4*>(sqs + (w * TILES + t) * 32 + row0);
+          const float4 t4 = *reinterpret_cast<const float4*>(sth + (w * TILES + t) * 32 + row0);
+          const float qsv[4] = {q4.x, q4.y, q4.z, q4.w}, thv[4] = {t4.x, t4.y, t4.z, t4.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float d;
+            if constexpr (METRIC == kL2) d = __builtin_fmaf(-2.0f, acc[4 * g + j], qsv[j] + vs);
+            else d = -__half2float(__float2half_rn(acc[4 * g + j]));
+            if (vok && d <= thv[j]) {
+              if constexpr (METRIC == kL2) d = d < 0.0f ? 0.0f : d;
+              // staged in LDS (an LDS atomic); a full stage appends to HBM
+              const uint32_t r = (uint32_t)(32 * t + j) + row0;
+              const uint64_t key = bf_key(d, (uint32_t)v);
+              const uint32_t slot = atomicAdd(&lcnt[w * TILES * 32 + r], 1u);
+              if (slot < kBfLocal) lbuf[(size_t)(w * TILES * 32 + r) * kBfLocal + slot] = key;
+              else bf_append(qcount, qcand, (uint32_t)qbase + r, key);
+            }
           }
         }
       }
     }
   };
-  for (int64_t v0 = v_begin; v0 < v_end; v0 += 64) {
-    // tile v0 in buffer 0, tile v0 + 32 in stb, tile v0 + 64 loads into sta
-    // loads are unconditional (rows past the chunk are clamped and never
-    // stored), so the wait counts before each store are static
-    bf_gload<kPer, METRIC>(base4, vsq, v0 + 64, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
+  for (int64_t v0 = v_begin; v0 < v_end; v0 += 2 * ROWS) {
+    // tile v0 in buffer 0, tile v0 + ROWS in stb, tile v0 + 2 ROWS loads into sta.
+    // Loads and stores are unconditional (rows past the chunk are clamped
+    // reads, stored but never scored): with a conditional store the
+    // compiler cannot prove the staging registers free at the loop head and
+    // waits there for every load in flight, the prefetch included.
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v0 + 2 * ROWS, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
     step(v0, 0u);
-    if (v0 + 32 < v_end) bf_sstore<kPer>(bf_tile, tvs, 1u, rs, nel, tid, srow, scol, stb, svb);
+    bf_sstore<kPer, ROWS>(bf_tile, tvs, 1u, rs, nel, tid, srow, scol, stb, svb);
     __syncthreads();
-    if (v0 + 32 >= v_end) break;
-    // tile v0 + 32 in buffer 1, tile v0 + 64 in sta, tile v0 + 96 loads into stb
-    bf_gload<kPer, METRIC>(base4, vsq, v0 + 96, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
-    step(v0 + 32, 1u);
-    if (v0 + 64 < v_end) bf_sstore<kPer>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
+    if (v0 + ROWS >= v_end) break;
+    // tile v0 + ROWS in buffer 1, tile v0 + 2 ROWS in sta, tile v0 + 3 ROWS loads into stb
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v0 + 3 * ROWS, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
+    step(v0 + ROWS, 1u);
+    bf_sstore<kPer, ROWS>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
     __syncthreads();
+  }
+  // flush the staged candidates: one HBM slot reservation per query row
+  lds_wave_sync();
+  for (uint32_t r = lane; r < 32u * TILES; r += 64) {
+    const int64_t q = qbase + r;
+    const uint32_t c = min(lcnt[w * TILES * 32 + r], kBfLocal);
+    if (q >= nq || c == 0) continue;
+    const uint32_t at = atomicAdd(&qcount[q], c);
+    for (uint32_t i = 0; i < c && at + i < kBfCandCap; ++i)
+      qcand[(size_t)q * kBfCandCap + at + i] = lbuf[(size_t)(w * TILES * 32 + r) * kBfLocal + i];
   }
 }
 
@@ -513,28 +596,47 @@ static void bf_one_pass(const void* base, int64_t n, uint32_t dp, const void* qu
   (void)hipFreeAsync(lists, s);
 }
 
-template <int KS, int METRIC>
-static void launch_filter(const void* base, int64_t n, uint32_t dp, const void* queries, int64_t nq,
-                          const float* vsq, const float* qsq, const float* qthr, uint32_t thr_stride,
-                          uint32_t* qcount, uint64_t* qcand, hipStream_t s) {
+template <int KS, int SUB, int METRIC>
+static void launch_filter_sub(const void* base, int64_t n, uint32_t dp, const void* queries, int64_t nq,
+                              const float* vsq, const float* qsq, const float* qthr, uint32_t thr_stride,
+                              uint32_t* qcount, uint64_t* qcand, hipStream_t s) {
   // one 32-query tile per wave: two (208 VGPRs) and three (272) measured
   // 7.48 and 11.7 ms against 7.15 ms on config 2's 10k x 1M ground truth
   constexpr int TILES = 1;
   const int64_t qblocks = (nq + 128 * TILES - 1) / (128 * TILES);
-  // about 2,500 work-groups; the query block is the fast grid index so the
-  // work-groups running at once share base tiles in L2
+  // about 2,500 work-groups in a 1-D grid that the kernel maps to (query
+  // block, chunk) so that one chunk's query blocks share an XCD
   int64_t want = std::max<int64_t>(1, 2560 / qblocks);
   want = std::min<int64_t>(want, (n + 31) / 32);
   const int64_t chunk = ((n + want - 1) / want + 31) / 32 * 32;
   const uint32_t n_chunks = (uint32_t)((n + chunk - 1) / chunk);
   const uint32_t rs = dp / 8 + 1;
-  const size_t lds = (size_t)2 * 32 * rs * 16 + 2 * 32 * 4 + (size_t)2 * 4 * TILES * 32 * 4;
-  auto kern = bf_filter_kernel<KS, TILES, METRIC>;
+  const size_t lds = (size_t)2 * 32 * SUB * rs * 16 + 4 * 32 * SUB * 4 + (size_t)3 * 4 * TILES * 32 * 4 +
+                     (size_t)4 * TILES * 32 * (4 + 8 * kBfLocal);
+  auto kern = bf_filter_kernel<KS, TILES, SUB, METRIC>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
-  hipLaunchKernelGGL(kern, dim3((uint32_t)qblocks, n_chunks), dim3(256), lds, s, (const uint16_t*)base, n, dp,
-                     (const uint16_t*)queries, nq, vsq, qsq, qthr, thr_stride, chunk, qcount, qcand);
+  hipLaunchKernelGGL(kern, dim3((uint32_t)qblocks * n_chunks), dim3(256), lds, s, (const uint16_t*)base, n, dp,
+                     (const uint16_t*)queries, nq, vsq, qsq, qthr, thr_stride, chunk, (uint32_t)qblocks, qcount,
+                     qcand);
   hip_check(hipGetLastError(), "launch bf_filter_kernel");
+}
+
+template <int KS, int METRIC>
+static void launch_filter(const void* base, int64_t n, uint32_t dp, const void* queries, int64_t nq,
+                          const float* vsq, const float* qsq, const float* qthr, uint32_t thr_stride,
+                          uint32_t* qcount, uint64_t* qcand, hipStream_t s) {
+  // 64-row steps (two 32-row tiles, two chains per wave): 6.25 ms against
+  // 6.73 ms with 32-row steps on config 2's ground truth; JASPER_BF_SUB=1
+  // selects the latter (tuning)
+  static const int sub = [] {
+    const char* e = std::getenv("JASPER_BF_SUB");
+    return e ? std::atoi(e) : 2;
+  }();
+  if (sub == 1 || KS > 16)
+    launch_filter_sub<KS, 1, METRIC>(base, n, dp, queries, nq, vsq, qsq, qthr, thr_stride, qcount, qcand, s);
+  else
+    launch_filter_sub<KS, 2, METRIC>(base, n, dp, queries, nq, vsq, qsq, qthr, thr_stride, qcount, qcand, s);
 }
 
 template <int METRIC>
