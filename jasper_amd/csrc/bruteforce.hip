@@ -559,10 +559,18 @@ static void bf_one_pass(const void* base, int64_t n, uint32_t dp, const void* qu
                         int metric, const float* vsq, const float* qsq, int32_t* out_ids, float* out_d,
                         const uint8_t* tile_flags, const uint8_t* q_flags, hipStream_t s) {
   const uint32_t ks = (dp + 15) / 16;  // 16-wide K steps (the last may be half empty)
-  // chunks: about 8192 work-groups (single waves) in all, each chunk a
-  // multiple of 64 vectors (a whole number of 32-vector steps)
+  // chunks: each a multiple of 64 vectors (a whole number of 32-vector steps)
+  // about 2,048 work-groups (single waves): longer chunks spend fewer of
+  // their steps filling and compacting the buffers before the threshold
+  // settles (config 2's 65,536-row sample: 8,192 work-groups 6.24 ms per
+  // ground-truth call, 4,096 5.62, 2,048 5.44, 1,024 5.77);
+  // JASPER_BF_SCAN_WGS overrides it (tuning)
   const int64_t qtiles = (nq + 31) / 32;
-  int64_t want = std::max<int64_t>(1, 8192 / qtiles);
+  static const int64_t target = [] {
+    const char* e = std::getenv("JASPER_BF_SCAN_WGS");
+    return e ? std::max<int64_t>(1, std::atoll(e)) : 2048;
+  }();
+  int64_t want = std::max<int64_t>(1, target / qtiles);
   want = std::min<int64_t>(want, (n + 63) / 64);
   int64_t chunk = ((n + want - 1) / want + 63) / 64 * 64;
   const uint32_t n_chunks = (uint32_t)((n + chunk - 1) / chunk);
