@@ -206,16 +206,17 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   const uint32_t lane = threadIdx.x;
   const uint32_t qid = blockIdx.x;
   const uint32_t bw = a.bw;
-  uint64_t* buf0 = smem;
-  uint64_t* buf1 = smem + bw;
-  uint64_t* T = smem + 2 * bw;
-  uint32_t* cand = reinterpret_cast<uint32_t*>(T + 64);
-  uint32_t* H = cand + 64;
+  uint64_t* B = smem;                                     // [bw] the candidate list
+  uint64_t* T = smem + bw;                                // [64] new keys
+  uint32_t* cand = reinterpret_cast<uint32_t*>(T + 64);   // [64] new neighbour ids
+  uint32_t* TAG = cand + 64;                              // [bw] merge position tags
+  uint32_t* H = TAG + bw;                                 // seen cache
   {
     // 32-bit words of the cache: empty = all ones (ids) or zero (tags)
     const uint32_t words = a.tag_bits ? (1u << a.hash_bits) / 2u : 1u << a.hash_bits;
     const uint32_t fill = a.tag_bits ? 0u : kInvalid32;
     for (uint32_t i = lane; i < words; i += 64) H[i] = fill;
+    for (uint32_t i = lane; i < bw; i += 64) TAG[i] = 0u;  // no position marked
   }
 
   const uint32_t ql = lane & 3u, qg = lane >> 2;
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     if (lane == 0) b = make_key(d, a.medoid);
     wave_sync();  // hash table initialised
     if (lane == 0) {
-      buf0[0] = make_key(d, a.medoid);
+      B[0] = make_key(d, a.medoid);
       seen_test_insert(a, H, a.medoid);
       if constexpr (STATS) atomicOr(&a.seen_bits[(size_t)qid * a.seen_words + (a.medoid >> 5)], 1u << (a.medoid & 31u));
     }
@@ -250,8 +251,6 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   wave_sync();
   uint32_t st_hops = 0, st_deg = 0, st_scored = 1, st_pred = 0;
 
-  uint64_t* B = buf0;
-  uint64_t* NB = buf1;
   uint32_t hint = 0, vc = 0, loop = 0;
   // adjacency (degree, row) of the predicted next pop, loaded one hop ahead
   // so that a correct prediction takes the adjacency read off the hop's
@@ -411,32 +410,37 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     if (keep) T[ti] = t;
     wave_sync();
 
-    // ---- merge by rank into NB, clip to bw. Entries of B below the
-    //      smallest kept key's position lb0 keep their places; only
-    //      positions from lb0 on are merged, and the shorter of the
-    //      unchanged prefix and the merged tail is copied across
+    // ---- merge in place, clipped to bw. Entries of B below the smallest
+    //      kept key's position lb0 keep their places. Kept key i (compacted
+    //      to T[i]) lands at p_i = lb_i + i, and that position is marked
+    //      with i (cleared again after the merge); every other output
+    //      position o >= lb0 takes B[o - (placed keys below o)]. The 64-entry
+    //      chunks of [lb0, ncnt) run from the top down, so a chunk reads only
+    //      entries that are not yet overwritten (its own reads precede its
+    //      writes).
     const uint32_t lb0 = uniform((uint32_t)__shfl((int)lb, (int)__builtin_ctzll(km), 64));
-    if (keep) {
-      const uint32_t pos = ti + lb;
-      if (pos < bw) NB[pos] = t;
-    }
-    const uint32_t ttop = pow2_ceil(nk);
-    for (uint32_t j = lb0 + lane; j < cnt; j += 64) {
-      const uint64_t bk = B[j];
-      const uint32_t c = lds_lower_bound(T, nk, ttop, key_rank(bk));
-      const uint32_t pos = j + c;
-      if (pos < bw) NB[pos] = bk;
-    }
     const uint32_t ncnt = min(cnt + nk, bw);
-    if (lb0 <= ncnt - lb0) {
-      for (uint32_t j = lane; j < lb0; j += 64) NB[j] = B[j];
-      uint64_t* tmp = B;
-      B = NB;
-      NB = tmp;
-    } else {
-      wave_sync();
-      for (uint32_t j = lb0 + lane; j < ncnt; j += 64) B[j] = NB[j];
+    const bool placed = keep && ti + lb < ncnt;
+    if (placed) TAG[ti + lb] = 0x100u | ti;
+    // kept keys that land inside the clipped list (the others fall past it)
+    const uint32_t np = (uint32_t)__builtin_popcountll(ballot(placed));
+    wave_sync();
+    uint32_t above = 0;  // kept keys above the current chunk
+    for (int32_t o0 = (int32_t)(lb0 + ((ncnt - 1u - lb0) & ~63u)); o0 >= (int32_t)lb0; o0 -= 64) {
+      const uint32_t o = (uint32_t)o0 + lane;
+      const bool valid = o < ncnt;
+      const uint32_t tg = valid ? TAG[o] : 0u;
+      const bool isnew = tg != 0u;
+      const uint64_t m = ballot(isnew);
+      // kept keys at positions >= o: above, plus this chunk's from lane on
+      const uint32_t ge = above + (uint32_t)__builtin_popcountll(m >> lane);
+      uint64_t v = 0;
+      if (isnew) v = T[tg & 0xFFu];
+      else if (valid) v = B[o - (np - ge)];
+      if (valid) B[o] = v;
+      above = uniform(above + (uint32_t)__builtin_popcountll(m));
     }
+    if (placed) TAG[ti + lb] = 0u;
     hint = uniform(min(hint, lb0));
     cnt = uniform(ncnt);
     wave_sync();
@@ -524,7 +528,8 @@ static uint32_t default_hash_bits(uint32_t bw, int64_t n) {
 size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {
   const uint32_t hb = r.hash_bits ? r.hash_bits : default_hash_bits(r.beam_width, g.n);
   const size_t entry = seen_tag_bits(g.n, hb) ? 2 : 4;
-  return (size_t)2 * r.beam_width * 8 + 64 * 8 + 64 * 4 + std::max<size_t>(((size_t)1 << hb) * entry, 4);
+  return (size_t)r.beam_width * 8 + 64 * 8 + 64 * 4 + (size_t)r.beam_width * 4 +
+         std::max<size_t>(((size_t)1 << hb) * entry, 4);
 }
 
 template <int CPL, int METRIC, bool STATS>
