@@ -19,7 +19,8 @@
 //    lanes scores one new neighbour with the reference's accumulation order
 //    (lane l: chunks l, l+4, ...; quad sum (l0+l2)+(l1+l3)).
 //  * New keys are sorted with a register bitonic network, deduplicated and
-//    merged into B by rank (binary searches in LDS), then clipped to bw.
+//    merged into B (in registers at bw <= 64, else in place in LDS), then
+//    clipped to bw.
 #include "common.hpp"
 #include "search.hpp"
 
