@@ -812,6 +812,10 @@ constexpr uint32_t kCountMerge = 16;
 // K = 0: the PQ estimator, with up to 16 * P subspaces (the edge's codes are
 // P groups of 16 bytes in registers); K = 1: the RaBitQ estimator with codes
 // of up to 32 * P dims; K in {4, 16} with P-byte words: the LSH estimator.
+// 8-byte words of the merge's position marks (one byte per slot of the
+// candidate buffer, rounded to 16 bytes).
+__host__ __device__ __forceinline__ uint32_t dir_mark_words(uint32_t cap) { return ((cap + 15u) & ~15u) / 8u; }
+
 template <int METRIC, int K, int P>
 __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
@@ -828,11 +832,14 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   uint64_t* T = buf1 + cap;
   float* Fd = reinterpret_cast<float*>(T + 64);  // frontier distances (exact bits)
   uint32_t* Fi = reinterpret_cast<uint32_t*>(Fd + a.k);
+  // marks of the new keys' positions in the general merge (nonzero = new)
+  uint8_t* MK = reinterpret_cast<uint8_t*>(smem + ((2 * cap + 64 + a.k + 1) & ~1u));
   // LSH with 1-byte words (dp <= 128): q and q - u take 16 chunks each,
   // zero past dp, so any 7-bit coordinate reads inside them
   constexpr bool LSH8 = !PQ && !RQ && P == 1;
   const uint32_t qchunks = LSH8 ? 16u : nchunks;
-  uint4* qv = reinterpret_cast<uint4*>(smem + ((2 * cap + 64 + a.k + 1) & ~1u));  // 16-byte aligned
+  uint4* qv = reinterpret_cast<uint4*>(smem + ((2 * cap + 64 + a.k + 1) & ~1u) + dir_mark_words(cap));  // 16-byte aligned
+  for (uint32_t i = lane; i < dir_mark_words(cap) * 2u; i += 64) reinterpret_cast<uint32_t*>(MK)[i] = 0u;
   uint4* xv = qv + qchunks;  // L2 LSH: fp16 q - u
   float* lut = reinterpret_cast<float*>(xv + qchunks);  // PQ: the query's LUT; LSH: the bf16 sqrt table
 
@@ -1283,14 +1290,23 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
           if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
         }
         NB[lane + lo] = t;
+        MK[lane + lo] = 1u;
       }
       lo0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
-      const uint32_t ttop = pow2_ceil(nt);
-      for (uint32_t j = lo0 + lane; j < cnt; j += 64) {
-        const uint64_t bk = B[j];
-        const uint32_t c = lds_lower_bound(T, nt, ttop, key_rank(bk));
-        NB[j + c] = bk;
+      lds_wave_sync();
+      // every other position o >= lo0 takes head entry o - (new keys below
+      // o): a ballot over the marks counts them per 64-entry row
+      const uint32_t tot = cnt + nt;
+      uint32_t below = 0;
+      for (uint32_t o0 = lo0; o0 < tot; o0 += 64) {
+        const uint32_t o = o0 + lane;
+        const bool valid = o < tot;
+        const bool isnew = valid && MK[o] != 0u;
+        const uint64_t m = ballot(isnew);
+        if (valid && !isnew) NB[o] = B[o - below - mbcnt(m)];
+        below = uniform(below + (uint32_t)__builtin_popcountll(m));
       }
+      if (lane < nt) MK[lane + lo] = 0u;
     }
     lds_wave_sync();
     const uint32_t total = cnt + nt;
@@ -1724,7 +1740,7 @@ const uint16_t* directional_query_rows(const Graph& g, const void* queries, int6
 }
 
 size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
-  size_t lds = (size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) * 8;
+  size_t lds = ((size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) + dir_mark_words((uint32_t)(bw + g.R))) * 8;
   if (est == kEstLsh) {
     // q and q - u (16 chunks each with 1-byte words), the sqrt table
     const size_t chunks = g.lsh->packed_bytes == 1 ? 16 : g.dp / 8;
