@@ -10,7 +10,8 @@
 //      batch start, sb = bits of the largest batch)
 //      are written in the same kernel (merge_candidates_kernel,
 //      robust_prune_kernel and fill_reverse_edges, :280-501);
-//   3. radix sort of the reverse pairs and a head-marking pass, which groups
+//   3. a stable radix sort of the reverse pairs on their target bits (they
+//      are written in source order) and a head-marking pass, which groups
 //      them by target with sources ascending (:846-879);
 //   4. reverse merge + RobustPrune, one wave per target
 //      (process_reverse_edges_kernel, :560-741).
@@ -518,7 +519,9 @@ static void reverse_step(const Graph& g, PruneKernelArgs& pa, const BuildWorkspa
   const size_t plds = prune_lds_bytes();
   const uint32_t np = (uint32_t)(bs * g.R);
   timer.start();
-  sort_u64(ws.temp, ws.temp_bytes, ws.pairs, ws.sorted, np, pb.end_bit, stream);
+  // the pairs are written in source order (pair index = source * R + slot),
+  // so a stable sort of the target bits groups them with sources ascending
+  sort_u64(ws.temp, ws.temp_bytes, ws.pairs, ws.sorted, np, (int)pb.sb, pb.end_bit, stream);
   hip_check(hipMemsetAsync(ws.nheads, 0, 4, stream), "clear head count");
   hipLaunchKernelGGL(mark_heads_kernel, dim3((np + kMarkHeadsBlock - 1) / kMarkHeadsBlock), dim3(kMarkHeadsBlock), 0,
                      stream, ws.sorted, np, pb.sb, ws.heads, ws.nheads);
@@ -1038,7 +1041,7 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
       if (np == 0) continue;
       total_pairs += (int64_t)np;
       const uint32_t np32 = (uint32_t)np;
-      sort_u64(temp, temp_bytes, pairs, sorted, np32, end_bit, stream);
+      sort_u64(temp, temp_bytes, pairs, sorted, np32, 0, end_bit, stream);
       hip_check(hipMemsetAsync(nheads, 0, 4, stream), "clear head count");
       hipLaunchKernelGGL(mark_heads_kernel, dim3((np32 + kMarkHeadsBlock - 1) / kMarkHeadsBlock),
                          dim3(kMarkHeadsBlock), 0, stream, sorted, np32, 32u, heads, nheads);

@@ -349,11 +349,14 @@ void assign_device(const Graph& g, uint32_t n_parts, uint32_t n_dup, uint64_t se
   hip_check(hipGetLastError(), "launch assign_kernel");
   // group by shard, rows ascending within a shard
   const size_t np = (size_t)n * n_dup;
+  // shard bits: an empty key's field (all ones) must not be a shard number
   int sbits = 1;
-  while ((1u << sbits) < n_parts) ++sbits;
+  while ((1u << sbits) <= n_parts) ++sbits;
   const size_t tb = sort_u64_temp_bytes(np);
   DeviceBuf temp(tb, "alloc sort temp");
-  sort_u64(temp.p, tb, pairs, sorted, np, 32 + sbits, s);
+  // pairs are written in row order: a stable sort of the shard bits keeps
+  // each shard's rows ascending
+  sort_u64(temp.p, tb, pairs, sorted, np, 32, 32 + sbits, s);
   uint32_t* start = bounds.as<uint32_t>();
   uint32_t* end = start + n_parts;
   hipLaunchKernelGGL(shard_bounds_kernel, dim3((uint32_t)((np + 255) / 256)), dim3(256), 0, s, sorted, (int64_t)np,
@@ -363,7 +366,16 @@ void assign_device(const Graph& g, uint32_t n_parts, uint32_t n_dup, uint64_t se
   hip_check(hipMemcpyAsync(be.data(), bounds.p, (size_t)n_parts * 8, hipMemcpyDeviceToHost, s), "read shard bounds");
   hip_check(hipStreamSynchronize(s), "shard assignment");
   counts_out.assign(n_parts, 0);
-  for (uint32_t p = 0; p < n_parts; ++p) counts_out[p] = be[(size_t)n_parts + p] - be[p];
+  uint64_t total = 0, expect = 0;
+  for (uint32_t p = 0; p < n_parts; ++p) {
+    counts_out[p] = be[(size_t)n_parts + p] - be[p];
+    if (be[(size_t)n_parts + p] < be[p] || counts_out[p] > (uint64_t)n)
+      throw std::logic_error("shard assignment: inconsistent shard runs");
+    if (counts_out[p] && be[p] != expect) throw std::logic_error("shard assignment: shard runs out of order");
+    expect += counts_out[p];
+    total += counts_out[p];
+  }
+  if (total > np) throw std::logic_error("shard assignment: more shard rows than pairs");
 }
 
 void check_assign_args(const Graph& g, int64_t n_parts, int64_t n_dup) {
