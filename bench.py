@@ -380,6 +380,15 @@ def main() -> int:
             # and the rate it would need to match this launch's time
             "reference_equivalent_bytes_per_launch": int(deg * 2 * 128),
             "reference_equivalent_gbs": deg * 2 * 128 / (kernel_ms / 1000.0) / 1e9,
+            # what the two figures are: achieved counts the bytes the
+            # algorithm must read; traffic is what rocprofv3's FETCH_SIZE and
+            # WRITE_SIZE count leaving L2 for the memory fabric, which
+            # includes reads served by the 256 MB Infinity Cache (config 2's
+            # 256 MB vector table fits it), scaled by factors measured on a
+            # streaming copy
+            "notes": "achieved = algorithmic bytes / kernel time; traffic = L2-to-fabric bytes per launch "
+                     "(FETCH_SIZE x 2 + WRITE_SIZE, factors from a streaming copy), which counts Infinity "
+                     "Cache hits as well as DRAM reads, so neither figure is a DRAM-only measurement",
         },
     }
     if args.int_exact == 1 and args.path == "search":
