@@ -28,7 +28,6 @@
 #include "prune.hpp"
 #include "search.hpp"
 
-#include <rocprim/device/device_scan.hpp>
 
 #include <algorithm>
 #include <numeric>
@@ -973,9 +972,7 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
     hip_check(hipMalloc(&per_vertex, (size_t)(chunk + 1) * 8), "alloc repair counts");
     hip_check(hipMalloc(&offsets, (size_t)(chunk + 1) * 8), "alloc repair offsets");
     hip_check(hipMalloc(&nheads, 4), "alloc head count");
-    hip_check(rocprim::exclusive_scan(nullptr, scan_bytes, per_vertex, offsets, (uint64_t)0, (size_t)chunk + 1,
-                                      rocprim::plus<uint64_t>(), stream),
-              "scan temp size");
+    scan_bytes = scan_u64_temp_bytes((size_t)chunk + 1);
     hip_check(hipMalloc(&scan_temp, std::max<size_t>(scan_bytes, 16)), "alloc scan temp");
     int end_bit = 32;
     while (end_bit < 64 && ((uint64_t)1 << (end_bit - 32)) <= (uint64_t)n) ++end_bit;
@@ -1008,9 +1005,7 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
                          n, R, n_min, n_max, per_vertex, (uint64_t*)nullptr);
       hip_check(hipGetLastError(), "launch repair_candidates_kernel");
       hip_check(hipMemsetAsync(per_vertex + cn, 0, 8, stream), "clear scan tail");
-      hip_check(rocprim::exclusive_scan(scan_temp, scan_bytes, per_vertex, offsets, (uint64_t)0, (size_t)cn + 1,
-                                        rocprim::plus<uint64_t>(), stream),
-                "scan repair counts");
+      exclusive_scan_u64(scan_temp, scan_bytes, per_vertex, offsets, (size_t)cn + 1, stream);
       uint64_t np = 0;
       hip_check(hipMemcpyAsync(&np, offsets + cn, 8, hipMemcpyDeviceToHost, stream), "read repair count");
       hip_check(hipStreamSynchronize(stream), "repair count");

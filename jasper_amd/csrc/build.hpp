@@ -74,7 +74,12 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream);
 // Radix sort of u64 keys (defined in sort.hip).
 size_t sort_u64_temp_bytes(size_t max_items);
 // Stable: keys equal in bits [begin_bit, end_bit) keep their input order.
+// in and out must differ; in is not written.
 void sort_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, size_t n, int begin_bit,
               int end_bit, hipStream_t stream);
+// Exclusive prefix sums of n u64 values (defined in sort.hip).
+size_t scan_u64_temp_bytes(size_t max_items);
+void exclusive_scan_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, size_t n,
+                        hipStream_t stream);
 
 }  // namespace jasper_amd

@@ -109,6 +109,21 @@ def test_build_matches_oracle_reverse_cap(jasper, oracle_lib, integer):
     _compare(gg, og)
 
 
+@pytest.mark.parametrize("groups", ["3", "1"])
+def test_build_reverse_grouping_several_tiles_per_group(jasper, oracle_lib, monkeypatch, groups):
+    """The reverse pairs of a 400-row batch at R = 32 fill four 4,096-key
+    sort tiles. With the sort's work-groups capped at 3 (tiles split 1, 1, 2)
+    or 1 (one work-group walks all four), each work-group carries its digit
+    offsets from tile to tile -- the path that otherwise runs only above
+    8M keys -- and the graph must stay the oracle's."""
+    monkeypatch.setenv("JASPER_SORT_GROUPS", groups)
+    base = hub_mix(20000, 64, 5, scale=32.0, integer=True)
+    og = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    assert og.max_batch == 400
+    gg = _gpu_build(jasper, base, 32, "l2")
+    _compare(gg, og)
+
+
 def test_build_then_search_c1(jasper, oracle_lib):
     """Config 1 end to end: the GPU graph equals the oracle's bit for bit
     (batches of at most 200, so no cap binds) and the GPU search on it

@@ -103,13 +103,15 @@ def test_mark_deleted_filters_results_and_moves_medoid(jasper, oracle_lib, tmp_p
         assert not (set(ids.cpu().numpy().ravel().tolist()) & gone)  # viol == 0
 
 
-@pytest.mark.parametrize("kind,frac", [("integer", 0.1), ("integer", 0.5), ("gaussian", 0.2)])
-def test_consolidate_matches_oracle(jasper, oracle_lib, tmp_path, kind, frac):
-    base = integer_clustered(3000, 128, 35) if kind == "integer" else gaussian(3000, 96, 35)
+# n = 9000: the repair-count scan spans three 4,096-value tiles
+@pytest.mark.parametrize("kind,frac,n", [("integer", 0.1, 3000), ("integer", 0.5, 3000), ("gaussian", 0.2, 3000),
+                                         ("integer", 0.2, 9000)])
+def test_consolidate_matches_oracle(jasper, oracle_lib, tmp_path, kind, frac, n):
+    base = integer_clustered(n, 128, 35) if kind == "integer" else gaussian(n, 96, 35)
     g = oracle.build(base, R=32)
     gg = _load(jasper, g, tmp_path)
     rng = np.random.default_rng(36)
-    dels = rng.choice(3000, size=int(3000 * frac), replace=False).astype(np.int32)
+    dels = rng.choice(n, size=int(n * frac), replace=False).astype(np.int32)
     gg.mark_deleted(torch.from_numpy(dels))
     oracle.mark_deleted(g, dels)
     gg.consolidate(alpha=1.2)
@@ -117,7 +119,7 @@ def test_consolidate_matches_oracle(jasper, oracle_lib, tmp_path, kind, frac):
     assert gg.n_tombstoned == 0
     got = _state(gg, g, tmp_path)
     _compare(got, g)
-    dead = np.zeros(3000, bool)
+    dead = np.zeros(n, bool)
     dead[dels] = True
     mask = np.arange(32)[None, :] < got.counts[:, None]
     assert not dead[got.edges[mask]].any()  # no edge into a deleted vertex
