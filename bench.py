@@ -545,7 +545,7 @@ def run_rotate(args, torch, jasper_amd, datasets, dev, log):
                 {"workload": f"{args.n} x 128 fp16 rows times a 128 x 128 fp16 rotation, fp32 accumulation",
                  "tflops": 2.0 * args.n * 128 * 128 / (ev / 1000.0) / 1e12},
                 {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
-                 "traffic": None, "kernel": "rotate_tile_kernel<4>", "kernel_ms": ev,
+                 "traffic": None, "kernel": "rotate_tile_kernel<4,8>", "kernel_ms": ev,
                  "algorithmic_bytes_per_launch": nbytes})
     print(json.dumps(res), flush=True)
     return 0

@@ -13,6 +13,7 @@
 #include "rotation.hpp"
 
 #include <cmath>
+#include <cstdlib>
 #include <random>
 #include <stdexcept>
 #include <vector>
@@ -106,54 +107,78 @@ __global__ __launch_bounds__(256) void rotate_mfma_kernel(const uint16_t* __rest
   }
 }
 
-// The common case (P and four 16-row output tiles fit in LDS): every wave of
-// the block iterates the same number of times, so block barriers are safe.
-// Each wave rounds its 16 x dim results to fp16 into an LDS tile (row stride
-// dp_out + 8 halves, 16-byte aligned, 2-way bank conflicts at most), then
-// writes whole rows with 16-byte stores.
-template <int KS>
-__global__ __launch_bounds__(256) void rotate_tile_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t dp_in,
-                                                          const uint16_t* __restrict__ pt, uint32_t kp,
-                                                          uint32_t dim, uint16_t* __restrict__ out,
-                                                          uint32_t dp_out) {
+// The common case (P and four 16-row output tiles fit in LDS). P is staged
+// once per block; after that each wave works alone: tiles gw, gw + stride,
+// ... (gw its index in the grid), the next tile's rows loaded before the
+// current tile's MFMAs. Each wave rounds its 16 x dim results to fp16 into
+// its own LDS tile (row stride dp_out + 8 halves, 16-byte aligned, 2-way bank
+// conflicts at most) and writes whole rows with 16-byte stores; a wave's LDS
+// operations execute in order, so the tile needs no block barrier.
+template <int KS, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void rotate_tile_kernel(const uint16_t* __restrict__ x, int64_t n,
+                                                                 uint32_t dp_in, const uint16_t* __restrict__ pt,
+                                                                 uint32_t kp, uint32_t dim,
+                                                                 uint16_t* __restrict__ out, uint32_t dp_out) {
   extern __shared__ uint4 lds4[];
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t mp = (dim + 15u) & ~15u;
   const uint32_t kc = kp / 8;
+  // Pt rows in LDS one chunk apart from 256-byte alignment: the 16 lanes that
+  // read one K slice of 16 rows then hit 16 different bank groups (with rows
+  // kc chunks apart, kc a multiple of 16 at d = 128, they all hit one; the
+  // kernel ran 1.5x slower)
+  const uint32_t kcl = kc + 1;
   const uint32_t ostride = dp_out + 8;  // halves
   uint4* pt_lds = lds4;
-  uint16_t* otile = reinterpret_cast<uint16_t*>(lds4 + (size_t)mp * kc) + (size_t)wave * 16 * ostride;
+  uint16_t* otile = reinterpret_cast<uint16_t*>(lds4 + (size_t)mp * kcl) + (size_t)wave * 16 * ostride;
   const uint4* ptg = reinterpret_cast<const uint4*>(pt);
-  for (uint32_t i = threadIdx.x; i < mp * kc; i += blockDim.x) pt_lds[i] = ptg[i];
+  for (uint32_t i = threadIdx.x; i < mp * kc; i += blockDim.x) pt_lds[(i / kc) * kcl + i % kc] = ptg[i];
   __syncthreads();
   const uint32_t col = lane & 15u, kq = lane >> 4;
   const uint32_t in_chunks = dp_in / 8, out_chunks = dp_out / 8;
   const int64_t tiles = (n + 15) / 16;
-  for (int64_t tb = (int64_t)blockIdx.x * 4; tb < tiles; tb += (int64_t)gridDim.x * 4) {
-    const int64_t tile = tb + wave;
+  const int64_t stride = (int64_t)gridDim.x * WAVES;
+  auto load_tile = [&](int64_t tile, uint4 (&xf)[KS]) {
     const int64_t row = tile * 16 + col;
-    const bool row_ok = row < n;
+    const bool row_ok = tile < tiles && row < n;
     const uint4* xr = reinterpret_cast<const uint4*>(x) + (size_t)(row_ok ? row : 0) * in_chunks;
-    uint4 xf[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const uint32_t c = (uint32_t)s * 4 + kq;
       xf[s] = (row_ok && c < in_chunks) ? xr[c] : make_uint4(0, 0, 0, 0);
     }
+  };
+  uint4 xf[KS];
+  int64_t tile = (int64_t)blockIdx.x * WAVES + wave;
+  load_tile(tile, xf);
+  for (; tile < tiles; tile += stride) {
+    uint4 xn[KS];
+    load_tile(tile + stride, xn);
     for (uint32_t m0 = 0; m0 < mp; m0 += 16) {
       float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const uint4 pf = pt_lds[(size_t)(m0 + col) * kc + (uint32_t)s * 4 + kq];
+        const uint4 pf = pt_lds[(size_t)(m0 + col) * kcl + (uint32_t)s * 4 + kq];
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(pf), as_half8(xf[s]), acc, 0, 0, 0);
       }
       const uint32_t i0 = m0 + 4 * kq;
+      if (i0 + 3 < dp_out) {
+        // one 8-byte write of the lane's four outputs: a half wave's 32
+        // lanes cover the 64 banks once
+        uint2 w;
+        w.x = (uint32_t)__half_as_ushort(__float2half_rn(acc[0])) |
+              ((uint32_t)__half_as_ushort(__float2half_rn(acc[1])) << 16);
+        w.y = (uint32_t)__half_as_ushort(__float2half_rn(acc[2])) |
+              ((uint32_t)__half_as_ushort(__float2half_rn(acc[3])) << 16);
+        *reinterpret_cast<uint2*>(otile + col * ostride + i0) = w;
+      } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (i0 + j < dp_out) otile[col * ostride + i0 + j] = __half_as_ushort(__float2half_rn(acc[j]));
+        for (int j = 0; j < 4; ++j)
+          if (i0 + j < dp_out) otile[col * ostride + i0 + j] = __half_as_ushort(__float2half_rn(acc[j]));
+      }
     }
-    __syncthreads();
+    lds_wave_sync();
     const int64_t row0 = tile * 16;
     for (uint32_t idx = lane; idx < 16 * out_chunks; idx += 64) {
       const uint32_t r = idx / out_chunks, c = idx % out_chunks;
@@ -164,7 +189,9 @@ __global__ __launch_bounds__(256) void rotate_tile_kernel(const uint16_t* __rest
             *reinterpret_cast<const uint4*>(otile + r * ostride + c * 8);
       }
     }
-    __syncthreads();
+    lds_wave_sync();
+#pragma unroll
+    for (int s = 0; s < KS; ++s) xf[s] = xn[s];
   }
 }
 
@@ -254,20 +281,48 @@ void rotate_rows(const RotationMatrix& r, const void* x, int64_t n, uint32_t dp_
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), shm, s, xi, n, dp_in, (const uint16_t*)r.pt, r.kp, r.dim, o,
                        dp_out);
   };
-  const size_t tile_lds = lds + (size_t)4 * 16 * (dp_out + 8) * 2;
-  if (tile_lds <= 64 * 1024 && dp_out <= r.mp && ks <= 6) {
-    const uint32_t g2 = (uint32_t)std::min<int64_t>((tiles + 3) / 4, 1024);
+  // eight waves share one staged P where the LDS allows (1M x 128: 98 us
+  // against 105 us with four; two blocks of 69.6 KB per CU)
+  auto lds_for = [&](int w) { return (size_t)r.mp * (r.kp / 8 + 1) * 16 + (size_t)w * 16 * (dp_out + 8) * 2; };
+  const int waves = lds_for(8) <= 96 * 1024 ? 8 : 4;
+  const size_t tile_lds = lds_for(waves);
+  if (tile_lds <= 96 * 1024 && dp_out <= r.mp && ks <= 6) {
+    // whole rounds of resident blocks (LDS allows floor(160 KB / tile_lds)
+    // per CU): every wave then walks the same number of tiles, give or take one
+    static const int cus = [] {
+      int dev = 0, c = 256;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+        c = 256;
+      return c;
+    }();
+    const int64_t per_cu = std::max<int64_t>(1, (int64_t)(160 * 1024) / (int64_t)tile_lds);
+    const uint32_t g2 = (uint32_t)std::min<int64_t>((tiles + waves - 1) / waves, per_cu * cus);
     auto go = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3(g2), dim3(256), tile_lds, s, xi, n, dp_in, (const uint16_t*)r.pt, r.kp, r.dim,
-                         o, dp_out);
+      if (tile_lds > 64 * 1024)
+        hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)tile_lds),
+                  "rotation LDS");
+      hipLaunchKernelGGL(kern, dim3(g2), dim3(64 * waves), tile_lds, s, xi, n, dp_in, (const uint16_t*)r.pt, r.kp,
+                         r.dim, o, dp_out);
     };
-    switch (ks) {
-      case 1: go(rotate_tile_kernel<1>); break;
-      case 2: go(rotate_tile_kernel<2>); break;
-      case 3: go(rotate_tile_kernel<3>); break;
-      case 4: go(rotate_tile_kernel<4>); break;
-      case 5: go(rotate_tile_kernel<5>); break;
-      default: go(rotate_tile_kernel<6>); break;
+    if (waves == 8) {
+      switch (ks) {
+        case 1: go(rotate_tile_kernel<1, 8>); break;
+        case 2: go(rotate_tile_kernel<2, 8>); break;
+        case 3: go(rotate_tile_kernel<3, 8>); break;
+        case 4: go(rotate_tile_kernel<4, 8>); break;
+        case 5: go(rotate_tile_kernel<5, 8>); break;
+        default: go(rotate_tile_kernel<6, 8>); break;
+      }
+    } else {
+      switch (ks) {
+        case 1: go(rotate_tile_kernel<1, 4>); break;
+        case 2: go(rotate_tile_kernel<2, 4>); break;
+        case 3: go(rotate_tile_kernel<3, 4>); break;
+        case 4: go(rotate_tile_kernel<4, 4>); break;
+        case 5: go(rotate_tile_kernel<5, 4>); break;
+        default: go(rotate_tile_kernel<6, 4>); break;
+      }
     }
   } else if (use_lds) {
     switch (ks) {

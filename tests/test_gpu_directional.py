@@ -245,10 +245,11 @@ def test_prerotated_build_rows(jasper, oracle_lib, dim):
     gg.free()
 
 
-@pytest.mark.parametrize("dim,n", [(8, 5), (33, 70), (96, 1000), (128, 4099), (250, 64), (960, 300)])
+@pytest.mark.parametrize("dim,n", [(8, 5), (33, 70), (96, 1000), (128, 4099), (160, 500), (250, 64), (960, 300)])
 def test_rotate_operator(jasper, oracle_lib, dim, n):
     """The stand-alone rotation (device and host inputs, unaligned strides,
-    the global-memory path for dim 960)."""
+    more than 64 KB of LDS per block at dim 160, the global-memory path for
+    dim 960)."""
     x = (gaussian(n, dim, 32) * 4).astype(np.float16)
     got = jasper.rotate(torch.from_numpy(x).cuda(), seed=42)
     torch.cuda.synchronize()
