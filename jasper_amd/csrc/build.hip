@@ -169,6 +169,9 @@ static float gram_margin_scale() {
 #ifndef JASPER_GRAM_WAVES
 #define JASPER_GRAM_WAVES 2
 #endif
+#ifndef JASPER_GRAM8_WAVES
+#define JASPER_GRAM8_WAVES 3
+#endif
 
 static size_t prune_lds_bytes() { return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4; }
 static_assert(kGramLdsWords <= kCandBuf, "the Gram prune's scratch reuses the source list");
@@ -247,15 +250,20 @@ __global__ __launch_bounds__(kMarkHeadsBlock) void mark_heads_kernel(const uint6
 }
 
 // The Gram prune holds 96 candidate rows of up to 128 values in registers
-// (96 VGPRs) beside its accumulators; two waves per SIMD keep it unspilled (three
-// spill, and measured slower).
-template <int CPL, bool INTX>
+// (96 VGPRs as fp16) beside its accumulators; two waves per SIMD keep it
+// unspilled (three spill, and measured slower). As bytes (I8) the rows take
+// 48 VGPRs.
+template <int CPL, bool INTX, bool I8>
 constexpr int reverse_waves_per_simd() {
-  return CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
+  return I8 ? JASPER_GRAM8_WAVES : CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
 }
 
-template <int CPL, int METRIC, bool INTX, bool SCALE>
-__global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void reverse_prune_kernel(PruneKernelArgs a) {
+// I8 (integer rows spanning at most 255 values, CPL 1..4, L2): the Gram
+// prune on bytes; the rest of the kernel is the INTX kernel's.
+template <int CPL, int METRIC, bool INTX, bool SCALE, bool I8 = false>
+__global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void reverse_prune_kernel(
+    PruneKernelArgs a) {
+  static_assert(!I8 || (INTX && METRIC == kL2 && CPL >= 1 && CPL <= 4 && !SCALE), "byte rows: integer L2 only");
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
   const uint32_t lane = lane_id();
@@ -321,9 +329,9 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX>())) void rev
       if (nc <= kGramMaxCands && climit <= kGramMaxChunks) {
         float* gn = reinterpret_cast<float*>(l.srcs);
         if constexpr (INTX) {
-          if (nc <= 32) ns = robust_prune_gram<1>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
-          else if (nc <= 64) ns = robust_prune_gram<2>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
-          else ns = robust_prune_gram<3>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+          if (nc <= 32) ns = robust_prune_gram<1, I8>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+          else if (nc <= 64) ns = robust_prune_gram<2, I8>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
+          else ns = robust_prune_gram<3, I8>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
         } else {
           if (nc <= 32) ns = robust_prune_gram_f<1, CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
           else if (nc <= 64) ns = robust_prune_gram_f<2, CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
@@ -350,9 +358,9 @@ static void launch_forward(const PruneKernelArgs& a, uint32_t bs, size_t lds, hi
   hipLaunchKernelGGL(k, dim3(bs), dim3(64), lds, s, a);
 }
 
-template <int CPL, int METRIC, bool INTX, bool SCALE>
+template <int CPL, int METRIC, bool INTX, bool SCALE, bool I8 = false>
 static void launch_reverse(const PruneKernelArgs& a, uint32_t grid, size_t lds, hipStream_t s) {
-  auto k = reverse_prune_kernel<CPL, METRIC, INTX, SCALE>;
+  auto k = reverse_prune_kernel<CPL, METRIC, INTX, SCALE, I8>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
   hipLaunchKernelGGL(k, dim3(grid), dim3(64), lds, s, a);
@@ -379,6 +387,29 @@ static void dispatch_prune(bool reverse, uint32_t cpl, const PruneKernelArgs& a,
 #undef JA_CASE
     default:
       throw std::logic_error("unreachable chunks-per-lane case");
+  }
+}
+
+// Integer rows (int_exact_l2 holds) whose values span at most 255: the
+// reverse prune's Gram step can take them as bytes. JASPER_GRAM8=0 turns
+// that off (the fp16 Gram kernel then runs; the results are the same).
+static bool int8_rows(const Graph& g) {
+  static const bool on = [] {
+    const char* e = std::getenv("JASPER_GRAM8");
+    return !(e && std::atoi(e) == 0);
+  }();
+  return on && g.int_state == 1 && (int64_t)g.int_hi - (int64_t)g.int_lo <= 255;
+}
+
+// The reverse prune on integer rows spanning at most 255 values: rows of up
+// to 128 values take the byte Gram kernel, longer ones the INTX kernel.
+static void dispatch_reverse_i8(uint32_t cpl, const PruneKernelArgs& a, uint32_t grid, size_t lds, hipStream_t s) {
+  switch (cpl) {
+    case 1: launch_reverse<1, kL2, true, false, true>(a, grid, lds, s); break;
+    case 2: launch_reverse<2, kL2, true, false, true>(a, grid, lds, s); break;
+    case 3: launch_reverse<3, kL2, true, false, true>(a, grid, lds, s); break;
+    case 4: launch_reverse<4, kL2, true, false, true>(a, grid, lds, s); break;
+    default: dispatch_prune<kL2, true>(true, cpl, a, grid, lds, s); break;
   }
 }
 
@@ -534,7 +565,8 @@ static void reverse_step(const Graph& g, PruneKernelArgs& pa, const BuildWorkspa
     else if (g.metric == kL2) dispatch_prune<kL2, false, true>(true, cpl, pa, grid, plds, stream);
     else dispatch_prune<kIP, false, true>(true, cpl, pa, grid, plds, stream);
   } else {
-    if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
+    if (intx && int8_rows(g)) dispatch_reverse_i8(cpl, pa, grid, plds, stream);
+    else if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
     else if (g.metric == kL2) dispatch_prune<kL2, false>(true, cpl, pa, grid, plds, stream);
     else dispatch_prune<kIP, false>(true, cpl, pa, grid, plds, stream);
   }
@@ -1046,7 +1078,8 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
       pa.heads = heads;
       pa.n_heads = nheads;
       const uint32_t grid = (uint32_t)std::min<uint64_t>(np, 16384);
-      if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
+      if (intx && int8_rows(g)) dispatch_reverse_i8(cpl, pa, grid, plds, stream);
+      else if (intx) dispatch_prune<kL2, true>(true, cpl, pa, grid, plds, stream);
       else if (g.metric == kL2) dispatch_prune<kL2, false>(true, cpl, pa, grid, plds, stream);
       else dispatch_prune<kIP, false>(true, cpl, pa, grid, plds, stream);
       hip_check(hipGetLastError(), "launch reverse_prune_kernel");

@@ -207,6 +207,15 @@ __device__ __forceinline__ gram_h8 as_gram_h8(const uint4& x) {
   return r;
 }
 
+typedef int gram_i4 __attribute__((ext_vector_type(4)));
+typedef int gram_i16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ gram_i4 as_gram_i4(const uint4& x) {
+  gram_i4 r;
+  __builtin_memcpy(&r, &x, 16);
+  return r;
+}
+
 // C: sorted keys [0, nc) in LDS, nc <= 32 * T; p.nlimit <= kGramMaxChunks.
 // gn: LDS scratch of kGramLdsWords words. Writes the selection to S_ids /
 // S_dist and returns |S| (the selection robust_prune_wave makes).
@@ -217,52 +226,101 @@ __device__ __forceinline__ uint32_t spread_nibbles(uint32_t w) {
   return (w & 0xFu) | ((w & 0xF0u) << 4) | ((w & 0xF00u) << 8) | ((w & 0xF000u) << 12);
 }
 
-template <int T>
+// I8: rows whose values span at most 255 (int8_rows) as bytes v - 128,
+// v = x - lo in [0, 255], on v_mfma_i32_32x32x32_i8: half the operand
+// registers of the fp16 form and half its MFMA steps. The Gram form's pair
+// distance is the same exact integer (|a_i - a_j|^2 does not depend on the
+// shift, and stays below 2^24), so the decisions are the fp16 form's.
+template <int T, bool I8 = false>
 __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
                                       uint32_t* S_ids, float* S_dist, float* gn) {
   static_assert(T >= 1 && T <= 3, "one to three tiles");
-  constexpr int KS = kGramMaxChunks / 2;  // 16 fp16 values per step
+  // fp16: 16 values per step, lane half h holds chunk 2s + h; int8: 32
+  // values per step, lane half h holds chunks 4s + 2h and 4s + 2h + 1
+  constexpr int KS = I8 ? kGramMaxChunks / 4 : kGramMaxChunks / 2;
   const uint32_t lane = lane_id();
   const uint32_t r = lane & 31u, h = lane >> 5;
   float* gcd = gn + kGramMaxCands;
 
-  // MFMA operand of tile t, step s: lane (r, h) holds values 16s + 8h .. +8
-  // of candidate 32t + r, shifted; steps past the summed length are zero
+  // MFMA operand of tile t, step s for candidate 32t + r, shifted; chunks
+  // past the summed length are zero
   uint4 fr[T][KS];
   float nrm[T];
+  if constexpr (I8) {
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const uint32_t i = 32u * (uint32_t)t + r;
-    const uint64_t key = i < nc ? C[i] : kEmptyKey;
-    const uint32_t id = i < nc ? key_id(key) : self;
-    const uint4* row = p.vecs + (size_t)id * p.nchunks;
+    for (int t = 0; t < T; ++t) {
+      const uint32_t i = 32u * (uint32_t)t + r;
+      const uint64_t key = i < nc ? C[i] : kEmptyKey;
+      const uint32_t id = i < nc ? key_id(key) : self;
+      const uint4* row = p.vecs + (size_t)id * p.nchunks;
+      uint4 raw[2 * KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const uint32_t c = 2u * (uint32_t)s + h;
-      fr[t][s] = row[min(c, p.nchunks - 1u)];
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t c = 4u * (uint32_t)s + 2u * h;
+        raw[2 * s] = row[min(c, p.nchunks - 1u)];
+        raw[2 * s + 1] = row[min(c + 1u, p.nchunks - 1u)];
+      }
+      if (h == 0) gcd[i] = key_dist(key);
+      int acc = 0;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint32_t c = 4u * (uint32_t)s + 2u * h + (uint32_t)u;
+          const uint32_t keep = c < p.nlimit ? ~0u : 0u;
+          const uint4 x = raw[2 * s + u];
+          // x - lo + 1024 = 0x6400 | v exactly (v < 1024): v is the low byte
+          const uint32_t a0 = sub_half2(sub_half2(x.x, p.lo2), 0xE400E400u);
+          const uint32_t a1 = sub_half2(sub_half2(x.y, p.lo2), 0xE400E400u);
+          const uint32_t a2 = sub_half2(sub_half2(x.z, p.lo2), 0xE400E400u);
+          const uint32_t a3 = sub_half2(sub_half2(x.w, p.lo2), 0xE400E400u);
+          wd[2 * u] = (__builtin_amdgcn_perm(a1, a0, 0x06040200u) ^ 0x80808080u) & keep;
+          wd[2 * u + 1] = (__builtin_amdgcn_perm(a3, a2, 0x06040200u) ^ 0x80808080u) & keep;
+        }
+        fr[t][s] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
+      }
+      const int tot = acc + __shfl_xor(acc, 32, 64);
+      nrm[t] = (float)tot;  // exact: below 2^24
+      if (h == 0) gn[i] = nrm[t];
     }
-    if (h == 0) gcd[i] = key_dist(key);
-  }
+  } else {
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    float acc = 0.0f;
+    for (int t = 0; t < T; ++t) {
+      const uint32_t i = 32u * (uint32_t)t + r;
+      const uint64_t key = i < nc ? C[i] : kEmptyKey;
+      const uint32_t id = i < nc ? key_id(key) : self;
+      const uint4* row = p.vecs + (size_t)id * p.nchunks;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const uint32_t c = 2u * (uint32_t)s + h;
-      const uint32_t keep = c < p.nlimit ? ~0u : 0u;  // per word: no struct select
-      uint4 x = fr[t][s];
-      x.x = sub_half2(x.x, p.lo2) & keep;
-      x.y = sub_half2(x.y, p.lo2) & keep;
-      x.z = sub_half2(x.z, p.lo2) & keep;
-      x.w = sub_half2(x.w, p.lo2) & keep;
-      fr[t][s] = x;
-      acc = dot2_sqdiff(x.x, 0u, acc);
-      acc = dot2_sqdiff(x.y, 0u, acc);
-      acc = dot2_sqdiff(x.z, 0u, acc);
-      acc = dot2_sqdiff(x.w, 0u, acc);
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t c = 2u * (uint32_t)s + h;
+        fr[t][s] = row[min(c, p.nchunks - 1u)];
+      }
+      if (h == 0) gcd[i] = key_dist(key);
     }
-    nrm[t] = acc + xor_lane_f<32>(acc);  // exact: integers below 2^24
-    if (h == 0) gn[32u * (uint32_t)t + r] = nrm[t];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t c = 2u * (uint32_t)s + h;
+        const uint32_t keep = c < p.nlimit ? ~0u : 0u;  // per word: no struct select
+        uint4 x = fr[t][s];
+        x.x = sub_half2(x.x, p.lo2) & keep;
+        x.y = sub_half2(x.y, p.lo2) & keep;
+        x.z = sub_half2(x.z, p.lo2) & keep;
+        x.w = sub_half2(x.w, p.lo2) & keep;
+        fr[t][s] = x;
+        acc = dot2_sqdiff(x.x, 0u, acc);
+        acc = dot2_sqdiff(x.y, 0u, acc);
+        acc = dot2_sqdiff(x.z, 0u, acc);
+        acc = dot2_sqdiff(x.w, 0u, acc);
+      }
+      nrm[t] = acc + xor_lane_f<32>(acc);  // exact: integers below 2^24
+      if (h == 0) gn[32u * (uint32_t)t + r] = nrm[t];
+    }
   }
   wave_sync();
 
@@ -278,10 +336,20 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   for (int t = 0; t < T; ++t) {
 #pragma unroll
     for (int t2 = 0; t2 <= t; ++t2) {
-      gram_f16 acc = {};
+      gram_f16 acc;
+      if constexpr (I8) {
+        gram_i16 ai = {};
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_gram_h8(fr[t][s]), as_gram_h8(fr[t2][s]), acc, 0, 0, 0);
+        for (int s = 0; s < KS; ++s)
+          ai = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_gram_i4(fr[t][s]), as_gram_i4(fr[t2][s]), ai, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = (float)ai[e];  // exact: |a_i . a_j| < 2^24
+      } else {
+        acc = gram_f16{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_gram_h8(fr[t][s]), as_gram_h8(fr[t2][s]), acc, 0, 0, 0);
+      }
       // lane holds column j = 32 t2 + r (whose norm it holds) and rows
       // 32 t + 8g + 4h + q
       const float nj = nrm[t2];

@@ -55,11 +55,13 @@ def test_build_matches_oracle_integer_r64(jasper, oracle_lib):
     _compare(gg, og)
 
 
-@pytest.mark.parametrize("hi", [362, 363])
+@pytest.mark.parametrize("hi", [255, 256, 362, 363])
 def test_build_matches_oracle_integer_range_limit(jasper, oracle_lib, hi):
     # values {0, hi} at dim 128: hi = 362 keeps dim * hi^2 just under 2^24
     # (packed fp16 differences with v_dot2), 363 just over (fp32 chain);
-    # distances reach the limit, and the many ties test the (dist, id) order
+    # hi = 255 is the widest span the reverse prune takes as bytes (int8
+    # Gram), 256 the narrowest it takes as fp16; distances reach the limit,
+    # and the many ties test the (dist, id) order
     rng = np.random.default_rng(14)
     base = (rng.integers(0, 2, size=(1500, 128)) * hi).astype(np.float16)
     base[:, :16] = rng.integers(0, hi + 1, size=(1500, 16)).astype(np.float16)
@@ -107,6 +109,37 @@ def test_build_matches_oracle_reverse_cap(jasper, oracle_lib, integer):
     assert og.max_batch == 400 and og.capped_groups >= 20
     gg = _gpu_build(jasper, base, 32, "l2")
     _compare(gg, og)
+
+
+@pytest.mark.parametrize("gram8", ["0", "1"])
+def test_build_byte_and_half_gram_agree(jasper, oracle_lib, gram8, tmp_path):
+    """Integer rows of span 207 build the same graph with the reverse prune's
+    Gram step on bytes (default) and on fp16 (JASPER_GRAM8=0, read once per
+    process, hence the child process), both the oracle's."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    base = integer_clustered(6000, 128, 41)
+    og = oracle.build(base, R=64, distance="l2", alpha=1.2)
+    np.save(tmp_path / "base.npy", base)
+    code = f"""
+import sys, numpy as np, torch
+sys.path.insert(0, {str(Path(__file__).resolve().parents[1])!r})
+import jasper_amd
+base = np.load({str(tmp_path / 'base.npy')!r})
+g = jasper_amd.Graph.build(torch.from_numpy(base).cuda(), n_neighbors=64, distance='l2', alpha=1.2)
+e, d, c = g.export_edges()
+np.savez({str(tmp_path / 'out.npz')!r}, e=e, d=d, c=c)
+"""
+    env = dict(os.environ, JASPER_GRAM8=gram8)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = np.load(tmp_path / "out.npz")
+    assert np.array_equal(out["c"], og.counts)
+    mask = np.arange(64)[None, :] < og.counts[:, None]
+    assert np.array_equal(out["e"][mask], og.edges[mask])
+    assert np.array_equal(out["d"][mask], og.edge_dist[mask])
 
 
 @pytest.mark.parametrize("groups", ["3", "1"])
