@@ -19,8 +19,10 @@ Procedure
      device synchronisations;
   6. roofline of the search kernel: algorithmic bytes per launch from the
      kernel's own exact work counters (hops, adjacency entries read,
-     distinct vectors scored) divided by the kernel time measured with HIP
-     events on the stream the kernel runs on;
+     distinct vectors scored, each at the bytes of the row format the query
+     reads: the graph's byte rows, dim bytes, or its fp16 rows, 2 dim bytes)
+     divided by the kernel time measured with HIP events on the stream the
+     kernel runs on;
   7. CPU baseline (rank 0, N = 1): the exact kNN scan restated from the
      reference's ground-truth arithmetic, on a bounded query sample, all
      host cores.
@@ -44,18 +46,21 @@ METRIC = "QPS @ recall@10≥0.95, 1M×128 fp16 synthetic; build vectors/sec"
 PEAK_HBM_GBS = 8000.0
 
 
-def measured_traffic(beam_width: int, n: int, nq: int, profile: str = "beam_search_c2_1M_pmc.md"):
+def measured_traffic(beam_width: int, n: int, nq: int, row_bytes: int = 256,
+                     profile: str = "beam_search_c2_1M_pmc.md"):
     """HBM bytes per launch of a kernel from a committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary, when it covers this exact workload;
-    None otherwise (the counters cannot be read from inside this process)."""
+    FETCH_SIZE / WRITE_SIZE summary, when it covers this exact workload and
+    row format; None otherwise (the counters cannot be read from inside this
+    process)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
     try:
         with open(path) as f:
             text = f.read()
     except OSError:
         return None
-    m = re.search(r"machine-readable: traffic_bytes_per_launch=(\d+) beam_width=(\d+) n=(\d+) nq=(\d+)", text)
-    if not m or (int(m.group(2)), int(m.group(3)), int(m.group(4))) != (beam_width, n, nq):
+    m = re.search(r"machine-readable: traffic_bytes_per_launch=(\d+) beam_width=(\d+) n=(\d+) nq=(\d+) "
+                  r"row_bytes=(\d+)", text)
+    if not m or tuple(int(m.group(i)) for i in range(2, 6)) != (beam_width, n, nq, row_bytes):
         return None
     return int(m.group(1))
 
@@ -330,7 +335,9 @@ def main() -> int:
     # ---- algorithmic bytes per launch (exact work counters of the same traversal)
     st = g.search_stats(q_t, k=10, beam_width=chosen).astype(np.int64)
     hops, deg, scored = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
-    alg_bytes = algorithmic_bytes(st, 128, args.nq)
+    fmt = g.row_format()
+    rows_b = query_row_bytes(fmt, queries, 128)
+    alg_bytes = algorithmic_bytes(st, 128, args.nq, rows_b)
     achieved = alg_bytes / (kernel_ms / 1000.0) / 1e9
     log(f"bw={chosen}: {ms_per_step:.3f} ms/step, kernel {kernel_ms:.3f} ms, qps={qps:,.0f}, "
         f"recall={final_recall:.4f}, hops/q={hops / args.nq:.1f}, scored/q={scored / args.nq:.1f}, "
@@ -360,7 +367,9 @@ def main() -> int:
             "build_vectors_per_s": args.n / build_s,
             "build_s": build_s,
             "build_max_batch": int(bst["max_batch"]),
-            "storage": "fp16 vectors, fp32 distance arithmetic",
+            "storage": ("fp16 vectors; the search reads byte rows (value - lo) for integer rows spanning "
+                        "<= 255 values" if fmt["byte_rows"] else "fp16 vectors") + ", fp32 distance arithmetic",
+            "row_bytes_per_scored_vector": float(rows_b.mean()),
             "curve": curve,
         },
         "roofline": {
@@ -369,7 +378,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBS,
-            "traffic": measured_traffic(chosen, args.n, args.nq),
+            "traffic": measured_traffic(chosen, args.n, args.nq, int(rows_b.mean())),
             "kernel": "beam_search_kernel<4,0,false>",
             "kernel_ms": kernel_ms,
             "algorithmic_bytes_per_launch": alg_bytes,
@@ -410,13 +419,31 @@ def main() -> int:
 
 # ------------------------------------------------------------------ other rows
 
-def algorithmic_bytes(st, dp, nq):
+def algorithmic_bytes(st, dp, nq, row_bytes=None):
     """Bytes one plain-search launch must move, from its exact work counters
     [nq, 4] (hops, adjacency entries, vectors scored): a 1-byte degree per
-    hop, 4 bytes per adjacency entry, 2*dp bytes per distinct vector scored,
-    plus the query rows and the k=10 (id, distance) outputs."""
-    hops, deg, scored = st[:, 0].sum(), st[:, 1].sum(), st[:, 2].sum()
-    return int(hops * 1 + deg * 4 + scored * 2 * dp + nq * (2 * dp + 8 * 10))
+    hop, 4 bytes per adjacency entry, row_bytes[q] per distinct vector query q
+    scores (2*dp for fp16 rows, dim for byte rows), plus the fp16 query rows
+    and the k=10 (id, distance) outputs."""
+    hops, deg = st[:, 0].sum(), st[:, 1].sum()
+    rb = np.full(len(st), 2 * dp, dtype=np.int64) if row_bytes is None else np.asarray(row_bytes, dtype=np.int64)
+    return int(hops * 1 + deg * 4 + (st[:, 2] * rb).sum() + nq * (2 * dp + 8 * 10))
+
+
+def query_row_bytes(fmt, queries, dim):
+    """Bytes per scored row for each query: the byte rows (dim bytes) when
+    the graph keeps them and the query is integer-valued with its values and
+    the rows' spanning at most the exact span (the search's per-query
+    test), else the fp16 rows (2*dim at dim 128)."""
+    smax = 2048
+    while smax > 0 and dim * smax * smax >= 16777216:
+        smax -= 1
+    q = queries.astype(np.float32)
+    if not fmt["byte_rows"]:
+        return np.full(len(q), 2 * dim, dtype=np.int64)
+    integer = (q == np.rint(q)).all(axis=1)
+    span = np.maximum(q.max(axis=1), fmt["hi"]) - np.minimum(q.min(axis=1), fmt["lo"])
+    return np.where(integer & (span <= smax), dim, 2 * dim).astype(np.int64)
 
 
 def _timed(torch, fn, steps, warmup):

@@ -316,6 +316,12 @@ int64_t jasperx_directional_stats(int64_t handle, int32_t estimator, const void*
  * readers of flags 1, 2 and 4 stop before it), and loading them restores it
  * whatever prerotate/seed the caller passed. No reference counterpart. */
 int64_t jasperx_prerotate_seed(int64_t handle);
+/* The row formats the graph keeps: out4 = {value state (0 no rows, 1 all
+ * values integers in [lo, hi], 2 otherwise), lo, hi, byte rows (1 when the
+ * search reads the rows as bytes value - lo: L2, integers spanning at most
+ * 255 values, dim 112 or 128; JASPER_SEARCH_BYTES=0 turns them off)}. No
+ * reference counterpart (an inspection call for tests and tooling). */
+int64_t jasperx_row_format(int64_t handle, int64_t* out4);
 /* Library build identifier (git-independent), for load checks. */
 const char* jasperx_version(void);
 

@@ -85,6 +85,7 @@ _AGNOSTIC = {
     "jasperx_export_graph": [_i64, _ptr, _ptr, _ptr],
     "jasperx_last_build_stats": [_ptr],
     "jasperx_prerotate_seed": [_i64],
+    "jasperx_row_format": [_i64, _ptr],
     "jasperx_search_stats": [_i64, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr],
     "jasperx_export_vectors": [_i64, _ptr],
     "jasperx_export_lsh": [_i64, _ptr, _ptr, _ptr],
@@ -759,6 +760,14 @@ class Graph:
             self.free()
         except Exception:
             pass
+
+    def row_format(self) -> dict:
+        """The row formats the graph keeps (jasperx_row_format): whether all
+        values are integers, their range, and whether the search reads the
+        rows as bytes."""
+        out = np.zeros(4, dtype=np.int64)
+        _agnostic("jasperx_row_format")(self._handle, out.ctypes.data_as(_ptr))
+        return {"integer": int(out[0]) == 1, "lo": int(out[1]), "hi": int(out[2]), "byte_rows": bool(out[3])}
 
     def __repr__(self) -> str:
         if self._handle is None:

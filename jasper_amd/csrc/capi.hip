@@ -389,6 +389,18 @@ extern "C" int64_t jasperx_prerotate_seed(int64_t h) {
   });
 }
 
+extern "C" int64_t jasperx_row_format(int64_t h, int64_t* out4) {
+  return guarded([&]() -> int64_t {
+    Graph& g = lookup(h, nullptr);
+    if (!out4) throw std::invalid_argument("null output");
+    out4[0] = g.int_state;
+    out4[1] = g.int_lo;
+    out4[2] = g.int_hi;
+    out4[3] = g.vecs8 && g.vecs8_lo == g.int_lo && g.vecs8_cap >= g.n && byte_rows_eligible(g) ? 1 : 0;
+    return 0;
+  });
+}
+
 extern "C" int64_t jasper_free_graph(int64_t h) {
   return guarded([&]() -> int64_t {
     std::unique_ptr<Graph> victim;

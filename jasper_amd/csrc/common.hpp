@@ -547,6 +547,17 @@ __device__ __forceinline__ float stream_partial_ip(const uint4* a, const uint4* 
 // two, and the same bits as quad_partial_l2h on such data.
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
+// a - b on two fp16 values at once (v_pk_add_f16)
+__device__ __forceinline__ uint32_t sub_half2(uint32_t a, uint32_t b) {
+  half2_t x, y;
+  __builtin_memcpy(&x, &a, 4);
+  __builtin_memcpy(&y, &b, 4);
+  const half2_t d = x - y;
+  uint32_t r;
+  __builtin_memcpy(&r, &d, 4);
+  return r;
+}
+
 __device__ __forceinline__ float dot2_sqdiff(uint32_t a, uint32_t b, float acc) {
   half2_t x, y;
   __builtin_memcpy(&x, &a, 4);

@@ -165,6 +165,9 @@ void Graph::release() {
   counts = nullptr;
   deleted = nullptr;
   slot_to_id = nullptr;
+  if (vecs8) (void)hipFree(vecs8);
+  vecs8 = nullptr;
+  vecs8_cap = 0;
   rotation.reset();
   if (vector_norms) (void)hipFree(vector_norms);
   vector_norms = nullptr;
@@ -219,7 +222,90 @@ static bool int_exact_enabled() {
   return enabled;
 }
 
+// rows [row0, row0 + rows) to bytes: value - lo, one thread per 8 values
+__global__ void byte_rows_kernel(const uint4* __restrict__ vecs, uint32_t dp8, uint32_t dim8, int64_t row0,
+                                 int64_t rows, int32_t lo, uint2* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= rows * (int64_t)dim8) return;
+  const int64_t r = row0 + t / dim8;
+  const uint32_t c = (uint32_t)(t % dim8);
+  const uint4 v = vecs[(size_t)r * dp8 + c];
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t b[2] = {0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    _Float16 hv;
+    const uint16_t bits = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+    __builtin_memcpy(&hv, &bits, 2);
+    const int32_t x = (int32_t)(float)hv;  // an integer in [lo, lo + 255]
+    b[k >> 2] |= (uint32_t)(x - lo) << (8 * (k & 3));
+  }
+  out[(size_t)r * dim8 + c] = make_uint2(b[0], b[1]);
+}
+
+static bool byte_rows_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("JASPER_SEARCH_BYTES");
+    return !(e && std::atoi(e) == 0);
+  }();
+  return on;
+}
+
+// an integer s is an fp16 value when |s| <= 2048, or |s| <= 65504 and s is
+// a multiple of the fp16 spacing at |s|
+static bool fp16_integer(int64_t s) {
+  const int64_t m = s < 0 ? -s : s;
+  if (m <= 2048) return true;
+  if (m > 65504) return false;
+  int64_t spacing = 1;
+  while ((int64_t)2048 * spacing <= m) spacing *= 2;
+  return m % spacing == 0;
+}
+
+bool byte_rows_eligible(const Graph& g) {
+  if (!byte_rows_enabled() || g.on_host || g.metric != 0 || g.int_state != 1) return false;
+  if ((int64_t)g.int_hi - (int64_t)g.int_lo > 255) return false;
+  if (g.dim % 16 != 0 || g.dim < 112 || g.dim > 128 || g.dp != g.dim) return false;
+  return fp16_integer((int64_t)g.int_lo - 1024);
+}
+
+// After rows [row0, end) were written and scanned: keep the byte rows of
+// [0, end) current, or drop them when the rows no longer qualify.
+static void update_byte_rows(Graph& g, int64_t row0, int64_t end, hipStream_t stream) {
+  if (!byte_rows_eligible(g)) {
+    if (g.vecs8) (void)hipFree(g.vecs8);
+    g.vecs8 = nullptr;
+    g.vecs8_cap = 0;
+    return;
+  }
+  if (end <= 0) return;
+  int64_t from = row0;
+  if (!g.vecs8 || g.vecs8_lo != g.int_lo || g.vecs8_cap < end) {
+    if (g.vecs8) (void)hipFree(g.vecs8);
+    g.vecs8 = nullptr;
+    const int64_t cap = std::max<int64_t>(g.capacity, end);
+    hip_check(hipMalloc((void**)&g.vecs8, (size_t)cap * g.dim), "alloc byte rows");
+    g.vecs8_cap = cap;
+    g.vecs8_lo = g.int_lo;
+    from = 0;
+  }
+  const int64_t rows = end - from;
+  if (rows <= 0) return;
+  const uint32_t dim8 = g.dim / 8;
+  const int64_t total = rows * dim8;
+  hipLaunchKernelGGL(byte_rows_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, stream,
+                     (const uint4*)g.vecs, g.dp / 8, dim8, from, rows, g.int_lo, (uint2*)g.vecs8);
+  hip_check(hipGetLastError(), "launch byte_rows_kernel");
+}
+
+static void scan_int_range_only(Graph& g, int64_t row0, int64_t n, hipStream_t stream);
+
 void scan_int_range(Graph& g, int64_t row0, int64_t n, hipStream_t stream) {
+  scan_int_range_only(g, row0, n, stream);
+  update_byte_rows(g, row0, row0 + n, stream);
+}
+
+static void scan_int_range_only(Graph& g, int64_t row0, int64_t n, hipStream_t stream) {
   if (!int_exact_enabled() || !g.vecs || g.on_host) {
     g.int_state = 2;
     return;

@@ -49,6 +49,12 @@ struct Graph {
   // 2 = some value is not an integer (or the scan is off)
   int int_state = 0;
   int32_t int_lo = 0, int_hi = -1;
+  // byte rows for the search: value - vecs8_lo per value, u8 [vecs8_cap,
+  // dim], kept by scan_int_range while the rows are integers spanning at
+  // most 255 values (update_byte_rows); null otherwise
+  uint8_t* vecs8 = nullptr;
+  int64_t vecs8_cap = 0;
+  int32_t vecs8_lo = 0;
   uint32_t* edges = nullptr;
   uint16_t* edist = nullptr;
   uint8_t* counts = nullptr;
@@ -108,6 +114,11 @@ int32_t int_exact_span(uint32_t dim);
 // there, so searches only read the result. JASPER_INT_EXACT=0 (measurement)
 // records "not integers".
 void scan_int_range(Graph& g, int64_t row0, int64_t n, hipStream_t stream);
+// Whether the graph's rows qualify for byte rows: L2, device-resident,
+// integers spanning at most 255 values, dim 112 or 128 (16-value byte
+// chunks, four fp16 chunks per quad lane), and lo - 1024 an fp16 value (the
+// search's query shift).
+bool byte_rows_eligible(const Graph& g);
 
 // The recorded result: true when every stored value is an integer in
 // [int_lo, int_hi].

@@ -191,16 +191,6 @@ constexpr uint32_t kGramMaxChunks = 16;   // rows of up to 128 fp16 values
 typedef _Float16 gram_h8 __attribute__((ext_vector_type(8)));
 typedef float gram_f16 __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ uint32_t sub_half2(uint32_t a, uint32_t b) {
-  half2_t x, y;
-  __builtin_memcpy(&x, &a, 4);
-  __builtin_memcpy(&y, &b, 4);
-  const half2_t d = x - y;
-  uint32_t r;
-  __builtin_memcpy(&r, &d, 4);
-  return r;
-}
-
 __device__ __forceinline__ gram_h8 as_gram_h8(const uint4& x) {
   gram_h8 r;
   __builtin_memcpy(&r, &x, 16);

@@ -57,6 +57,10 @@ struct SearchArgs {
   uint32_t* seen_bits;      // [nq, seen_words]
   uint32_t seen_words;
   uint32_t* stats;          // [nq, 4]: hops, sum of degrees, vectors scored, predicted hops
+  // byte rows (value - glo, 16 * nb8 bytes per row) when the graph keeps
+  // them, and the query shift glo - 1024 as two fp16 (qsh2)
+  const uint4* vecs8;
+  uint32_t nb8, qsh2;
   // the graph's rows are integers in [glo, ghi] (gint); queries that are
   // integers too, with the union spanning at most smax, take the packed form
   uint32_t gint;
@@ -147,6 +151,71 @@ __device__ __forceinline__ float score(const SearchArgs& a, const QueryFrag<CPL,
   return left_distance<CPL, METRIC, false>(q, x, ql, a.nchunks, nlimit);
 }
 
+// ---- byte rows. A query that qualifies for the packed-difference form
+// (intx) is scored against the graph's byte rows b = x - glo instead of its
+// fp16 rows, reading half the bytes. Quad lane ql takes byte chunks ql and
+// ql + 4 (16 values each). The query is held shifted, q' = q - glo + 1024,
+// and a byte b becomes the fp16 value 1024 + b by placing 0x64 above it
+// (one v_perm_b32 per two values), so q' - (1024 + b) = q - x: the same
+// exact fp16 difference, and with it the same exact sum of squares, as the
+// fp16 rows give.
+struct RowBytes {
+  uint4 x[2];
+};
+
+// q: byte chunk ql in q[0..1], byte chunk ql + 4 in q[2..3] (fp16 q')
+__device__ __forceinline__ void load_query_bytes(const SearchArgs& a, const uint4* qrow, uint32_t ql,
+                                                 uint4 (&q)[4]) {
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    const uint32_t c = ql + 4u * u;
+    const uint32_t c0 = c < a.nb8 ? 2u * c : 0u;
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+      uint4 w = qrow[c0 + h];
+      w.x = sub_half2(w.x, a.qsh2);
+      w.y = sub_half2(w.y, a.qsh2);
+      w.z = sub_half2(w.z, a.qsh2);
+      w.w = sub_half2(w.w, a.qsh2);
+      q[2 * u + h] = w;
+    }
+  }
+}
+
+__device__ __forceinline__ void load_row_bytes(const SearchArgs& a, uint32_t v, uint32_t ql, RowBytes& r) {
+  const uint4* row = a.vecs8 + (size_t)v * a.nb8;
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    const uint32_t c = ql + 4u * u;
+    r.x[u] = row[c < a.nb8 ? c : 0u];
+  }
+}
+
+// bytes b0..b3 of w to fp16 pairs (1024 + b0, 1024 + b1) and (1024 + b2, 1024 + b3)
+__device__ __forceinline__ uint32_t bytes_lo_pair(uint32_t w) { return __builtin_amdgcn_perm(w, 0x64646464u, 0x00050004u); }
+__device__ __forceinline__ uint32_t bytes_hi_pair(uint32_t w) { return __builtin_amdgcn_perm(w, 0x64646464u, 0x00070006u); }
+
+__device__ __forceinline__ float score_bytes(const SearchArgs& a, const uint4 (&q)[4], const RowBytes& r,
+                                             uint32_t ql) {
+  float acc = 0.0f;
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    if (ql + 4u * u < a.nb8) {
+      const uint4 b = r.x[u];
+      const uint4 q0 = q[2 * u], q1 = q[2 * u + 1];
+      acc = dot2_sqdiff(q0.x, bytes_lo_pair(b.x), acc);
+      acc = dot2_sqdiff(q0.y, bytes_hi_pair(b.x), acc);
+      acc = dot2_sqdiff(q0.z, bytes_lo_pair(b.y), acc);
+      acc = dot2_sqdiff(q0.w, bytes_hi_pair(b.y), acc);
+      acc = dot2_sqdiff(q1.x, bytes_lo_pair(b.z), acc);
+      acc = dot2_sqdiff(q1.y, bytes_hi_pair(b.z), acc);
+      acc = dot2_sqdiff(q1.z, bytes_lo_pair(b.w), acc);
+      acc = dot2_sqdiff(q1.w, bytes_hi_pair(b.w), acc);
+    }
+  }
+  return quad_finish<kL2>(acc);
+}
+
 // Appends the key of a scored row to T[nt..) when its rank is below thr
 // (the quad's first lane writes); returns the new count (wave-uniform).
 __device__ __forceinline__ uint32_t append_key(uint64_t* T, uint32_t nt, bool act, uint32_t ql, float d, uint32_t v,
@@ -182,6 +251,32 @@ __device__ __forceinline__ uint32_t score_pass(const SearchArgs& a, const QueryF
     return append_key(T, nt, act1, ql, d1, v1, thr);
   } else {
     const float d0 = score<CPL, METRIC>(a, qf, x0, ql, nlimit, intx);
+    return append_key(T, nt, act0, ql, d0, v0, thr);
+  }
+}
+
+// score_pass on the byte rows
+template <bool TWO>
+__device__ __forceinline__ uint32_t score_pass_bytes(const SearchArgs& a, const uint4 (&q8)[4], const uint32_t* cand,
+                                                     uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql,
+                                                     uint32_t qg, uint64_t thr, uint32_t nt) {
+  const uint32_t j0 = base + qg;
+  const bool act0 = j0 < nm;
+  const uint32_t v0 = act0 ? cand[j0] : 0u;
+  RowBytes x0;
+  load_row_bytes(a, v0, ql, x0);
+  if constexpr (TWO) {
+    const uint32_t j1 = base + 16u + qg;
+    const bool act1 = j1 < nm;
+    const uint32_t v1 = act1 ? cand[j1] : 0u;
+    RowBytes x1;
+    load_row_bytes(a, v1, ql, x1);
+    const float d0 = score_bytes(a, q8, x0, ql);
+    const float d1 = score_bytes(a, q8, x1, ql);
+    nt = append_key(T, nt, act0, ql, d0, v0, thr);
+    return append_key(T, nt, act1, ql, d1, v1, thr);
+  } else {
+    const float d0 = score_bytes(a, q8, x0, ql);
     return append_key(T, nt, act0, ql, d0, v0, thr);
   }
 }
@@ -230,6 +325,14 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   if constexpr (METRIC == kL2 && CPL > 0 && !STATS) {
     if (a.gint) intx = uniform(query_int_exact<CPL>(a, qf.h) ? 1u : 0u) != 0u;
   }
+  // byte rows for this query (wave-uniform; rows of 112 or 128 values).
+  // From here on such a query is held shifted, in byte-chunk order, in the
+  // registers of its fp16 fragment, which it no longer uses.
+  bool bytes = false;
+  if constexpr (METRIC == kL2 && CPL == 4 && !STATS) {
+    bytes = intx && a.vecs8 != nullptr;
+    if (bytes) load_query_bytes(a, qrow, ql, qf.h.x);
+  }
 
   // B = [(medoid, d(q, medoid))]; at bw <= 64 B lives in registers, one key
   // per lane (`b`), and is written to LDS only for the merge's general path
@@ -238,9 +341,16 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   uint32_t cnt = 1;
   uint64_t b = kEmptyKey;
   {
-    RowFrag<CPL> x;
-    load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
-    const float d = score<CPL, METRIC>(a, qf, x, ql, nlimit, intx);
+    float d = 0.0f;
+    if (bytes) {
+      RowBytes xb;
+      load_row_bytes(a, a.medoid, ql, xb);
+      if constexpr (CPL == 4 && METRIC == kL2) d = score_bytes(a, qf.h.x, xb, ql);
+    } else {
+      RowFrag<CPL> x;
+      load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
+      d = score<CPL, METRIC>(a, qf, x, ql, nlimit, intx);
+    }
     if (lane == 0) b = make_key(d, a.medoid);
     wave_sync();  // hash table initialised
     if (lane == 0) {
@@ -348,13 +458,21 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     uint64_t thr = ~0ull;
     if (cnt == bw) thr = key_rank(regb ? readlane64(b, (int)(bw - 1u)) : B[bw - 1u]);
     uint32_t nt = 0, base = 0;
+    if (bytes) {
+      if constexpr (CPL == 4 && METRIC == kL2) {
+        for (; base + 16 < nm; base += 32)
+          nt = score_pass_bytes<true>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
+        if (base < nm) nt = score_pass_bytes<false>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
+      }
+    } else {
 #if JASPER_SEARCH_TWO_ROWS
-    for (; base + 16 < nm; base += 32)
-      nt = score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+      for (; base + 16 < nm; base += 32)
+        nt = score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
 #endif
-    for (; base + 16 < nm; base += 16)
-      nt = score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
-    if (base < nm) nt = score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+      for (; base + 16 < nm; base += 16)
+        nt = score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+      if (base < nm) nt = score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+    }
     if (nt == 0) {
       lds_wave_sync();
       continue;
@@ -607,6 +725,15 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
       a.ghi = g.int_hi;
       a.smax = int_exact_span(g.dim);
     }
+  }
+  a.vecs8 = nullptr;
+  a.nb8 = 0;
+  a.qsh2 = 0;
+  if (a.gint && g.vecs8 && g.vecs8_lo == g.int_lo && g.vecs8_cap >= g.n && byte_rows_eligible(g)) {
+    a.vecs8 = (const uint4*)g.vecs8;
+    a.nb8 = g.dim / 16;
+    const uint32_t h = f2h_rn((float)g.int_lo - 1024.0f);  // exact (byte_rows_eligible)
+    a.qsh2 = h | (h << 16);
   }
   a.seen_bits = r.seen_bits;
   a.seen_words = (uint32_t)((g.n + 31) / 32);

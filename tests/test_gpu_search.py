@@ -231,11 +231,74 @@ def test_search_integer_queries_exact_span(jasper, oracle_lib, tmp_path):
     q = np.concatenate([q, q[:8] + 0.5]).astype(np.float16)  # non-integer queries
     g = oracle.build(base, R=32, distance="l2", alpha=1.2)
     gg = _load(jasper, g, tmp_path)
+    # rows span 39 values: the search reads them as bytes (queries that take
+    # the packed form), the other queries read the fp16 rows
+    assert gg.row_format() == {"integer": True, "lo": 260, "hi": 299, "byte_rows": True}
     for bw in (16, 64, 128):
         ids, d = _run(jasper, gg, q, 10, bw)
         rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
         msg = compare_search(ids, d, rid, rd)
         assert msg is None, f"bw={bw}: {msg}"
+
+
+@pytest.mark.parametrize("dim,lo,hi,byte_rows", [(128, 0, 255, True), (128, 0, 256, False), (112, -40, 200, True),
+                                                 (96, 0, 100, False)])
+def test_search_byte_rows_match_oracle(jasper, oracle_lib, tmp_path, dim, lo, hi, byte_rows):
+    """Byte rows are kept for integer rows spanning at most 255 values at
+    dim 112 or 128; with and without them the results are the oracle's.
+    Queries: in-range integers (bytes), integers up to the exact span's edge,
+    and non-integers (fp16 rows)."""
+    rng = np.random.default_rng(dim + hi)
+    base = rng.integers(lo, hi + 1, size=(2500, dim))
+    base[:, 0] = np.where(rng.random(2500) < 0.5, lo, hi)  # both ends present
+    base = base.astype(np.float16)
+    q = np.concatenate([rng.integers(lo, hi + 1, size=(24, dim)),
+                        rng.integers(lo - 100, hi + 100, size=(8, dim))]).astype(np.float32)
+    q = np.concatenate([q, q[:8] + 0.25]).astype(np.float16)
+    g = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    assert gg.row_format()["byte_rows"] is byte_rows
+    for bw in (24, 96):
+        ids, d = _run(jasper, gg, q, 10, bw)
+        rid, rd = oracle.beam_search(g, q, k=10, beam_width=bw)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"bw={bw}: {msg}"
+
+
+def test_search_byte_rows_off_same_results(jasper, oracle_lib, tmp_path):
+    """JASPER_SEARCH_BYTES=0 (read once per process, hence the child): no
+    byte rows, and the same ids and distance bits as with them."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    base = integer_clustered(4000, 128, 71)
+    q = integer_clustered(64, 128, 72)
+    g = oracle.build(base, R=64, distance="l2", alpha=1.2)
+    path = tmp_path / "g.bin"
+    oracle.save_graph(g, path)
+    np.save(tmp_path / "q.npy", q)
+    code = f"""
+import sys, numpy as np, torch
+sys.path.insert(0, {str(Path(__file__).resolve().parents[1])!r})
+import jasper_amd
+gg = jasper_amd.Graph.load({str(path)!r}, dim=128, n_neighbors=64, distance='l2')
+q = torch.from_numpy(np.load({str(tmp_path / 'q.npy')!r})).cuda()
+ids, d = gg.search(q, k=10, beam_width=64)
+np.savez({str(tmp_path / 'out.npz')!r}, ids=ids.cpu().numpy(), d=d.cpu().numpy(), b=gg.row_format()['byte_rows'])
+"""
+    r = subprocess.run([sys.executable, "-c", code], env=dict(os.environ, JASPER_SEARCH_BYTES="0"),
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    off = np.load(tmp_path / "out.npz")
+    assert not bool(off["b"])
+    gg = jasper.Graph.load(str(path), dim=128, n_neighbors=64, distance="l2")
+    assert gg.row_format()["byte_rows"]
+    ids, d = _run(jasper, gg, q, 10, 64)
+    assert np.array_equal(ids, off["ids"])
+    assert np.array_equal(d.view(np.uint32), off["d"].view(np.uint32))
+    rid, rd = oracle.beam_search(g, q, k=10, beam_width=64)
+    assert compare_search(ids, d, rid, rd) is None
 
 
 def test_search_host_resident_graph_matches_oracle(jasper, oracle_lib, tmp_path):

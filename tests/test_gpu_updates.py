@@ -65,6 +65,29 @@ def test_append_matches_oracle(jasper, oracle_lib, tmp_path, kind):
         assert self_recall >= 0.99, self_recall
 
 
+def test_append_lower_values_rewrites_byte_rows(jasper, oracle_lib, tmp_path):
+    """Rows in [50, 200] are kept as bytes from 50; appended rows reach 0,
+    so the byte rows are rewritten from 0 (the append also grows the
+    storage). Construction and search stay the oracle's."""
+    rng = np.random.default_rng(33)
+    data = rng.integers(50, 201, size=(2600, 128)).astype(np.float16)
+    data[2000:, :8] = rng.integers(0, 60, size=(600, 8)).astype(np.float16)
+    g = oracle.build(data[:2000], R=32, distance="l2", alpha=1.2)
+    gg = _load(jasper, g, tmp_path)
+    assert gg.row_format() == {"integer": True, "lo": 50, "hi": 200, "byte_rows": True}
+    ids = gg.append(torch.from_numpy(np.ascontiguousarray(data[2000:])).cuda(), alpha=1.2)
+    ref, ref_ids = oracle.append(g, data[2000:], alpha=1.2)
+    assert np.array_equal(ids.numpy(), ref_ids)
+    fmt = gg.row_format()
+    assert fmt["byte_rows"] and fmt["lo"] == int(data.min()) and fmt["hi"] == 200
+    _compare(_state(gg, ref, tmp_path), ref)
+    q = data[1990:2100].copy()
+    out, d = gg.search(torch.from_numpy(q).cuda(), k=10, beam_width=48)
+    rid, rd = oracle.beam_search(ref, q, k=10, beam_width=48)
+    assert np.array_equal(out.cpu().numpy(), rid)
+    assert np.array_equal(d.cpu().numpy().view(np.uint32), rd.view(np.uint32))
+
+
 def test_append_twice_ids_and_growth(jasper, oracle_lib, tmp_path):
     data = integer_clustered(2600, 128, 32)
     g = oracle.build(data[:1000], R=32)
