@@ -253,17 +253,20 @@ __global__ __launch_bounds__(kMarkHeadsBlock) void mark_heads_kernel(const uint6
 // (96 VGPRs as fp16) beside its accumulators; two waves per SIMD keep it
 // unspilled (three spill, and measured slower). As bytes (I8) the rows take
 // 48 VGPRs.
-template <int CPL, bool INTX, bool I8>
+template <int CPL, bool INTX, int I8>
 constexpr int reverse_waves_per_simd() {
   return I8 ? JASPER_GRAM8_WAVES : CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1;
 }
 
 // I8 (integer rows spanning at most 255 values, CPL 1..4, L2): the Gram
-// prune on bytes; the rest of the kernel is the INTX kernel's.
-template <int CPL, int METRIC, bool INTX, bool SCALE, bool I8 = false>
+// prune on bytes, converted from the fp16 rows (1) or read from the graph's
+// byte rows (2, CPL 4), which then also give the sources' distances to the
+// target; the rest of the kernel is the INTX kernel's.
+template <int CPL, int METRIC, bool INTX, bool SCALE, int I8 = 0>
 __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void reverse_prune_kernel(
     PruneKernelArgs a) {
   static_assert(!I8 || (INTX && METRIC == kL2 && CPL >= 1 && CPL <= 4 && !SCALE), "byte rows: integer L2 only");
+  static_assert(I8 != 2 || CPL == 4, "byte rows hold rows of 112 or 128 values");
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
   const uint32_t lane = lane_id();
@@ -281,7 +284,8 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
     // values, the first 64 pairs of its group, and the next head
     const ExistingRow er = load_existing(a, w);
     RowFrag<CPL> xw;
-    load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
+    if constexpr (I8 == 2) load_query_bytes(a.pc.vecs + (size_t)w * a.pc.nchunks, a.pc.nb8, a.pc.qsh2, ql, xw.x);
+    else load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
     uint64_t key = a.sorted_pairs[min(start + lane, a.n_pairs - 1u)];
     if (start + lane >= a.n_pairs) key = kEmptyKey;
     const uint32_t start_next = a.heads[min(h + gridDim.x, nh - 1u)];
@@ -305,16 +309,29 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
     const uint32_t w_next = (uint32_t)(a.sorted_pairs[start_next] >> a.pair_shift);
     wave_sync();
     // d(w, v) for every source (compute_distance(src_vec = w, sink_vec = v))
-    LeftFrag<CPL, METRIC> wf;
-    left_from_row<CPL, METRIC>(xw, ql, wf);
-    for (uint32_t base = 0; base < taken; base += 16) {
-      const uint32_t j = base + qg;
-      const bool act = j < taken;
-      const uint32_t sid = act ? l.srcs[j] : 0u;
-      RowFrag<CPL> xs;
-      load_row_frag<CPL>(a.pc.vecs + (size_t)sid * a.pc.nchunks, ql, a.pc.nchunks, act, xs);
-      const float d = left_distance<CPL, METRIC, INTX>(wf, xs, ql, a.pc.nchunks, a.pc.nlimit);
-      if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
+    if constexpr (I8 == 2) {
+      // xw holds w shifted in byte-chunk order: the sources' byte rows
+      for (uint32_t base = 0; base < taken; base += 16) {
+        const uint32_t j = base + qg;
+        const bool act = j < taken;
+        const uint32_t sid = act ? l.srcs[j] : 0u;
+        RowBytes xs;
+        load_row_bytes(a.pc.vecs8, a.pc.nb8, sid, ql, xs);
+        const float d = score_bytes(a.pc.nb8, xw.x, xs, ql);
+        if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
+      }
+    } else {
+      LeftFrag<CPL, METRIC> wf;
+      left_from_row<CPL, METRIC>(xw, ql, wf);
+      for (uint32_t base = 0; base < taken; base += 16) {
+        const uint32_t j = base + qg;
+        const bool act = j < taken;
+        const uint32_t sid = act ? l.srcs[j] : 0u;
+        RowFrag<CPL> xs;
+        load_row_frag<CPL>(a.pc.vecs + (size_t)sid * a.pc.nchunks, ql, a.pc.nchunks, act, xs);
+        const float d = left_distance<CPL, METRIC, INTX>(wf, xs, ql, a.pc.nchunks, a.pc.nlimit);
+        if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
+      }
     }
     wave_sync();
     const uint32_t nc = nE + taken;
@@ -358,7 +375,7 @@ static void launch_forward(const PruneKernelArgs& a, uint32_t bs, size_t lds, hi
   hipLaunchKernelGGL(k, dim3(bs), dim3(64), lds, s, a);
 }
 
-template <int CPL, int METRIC, bool INTX, bool SCALE, bool I8 = false>
+template <int CPL, int METRIC, bool INTX, bool SCALE, int I8 = 0>
 static void launch_reverse(const PruneKernelArgs& a, uint32_t grid, size_t lds, hipStream_t s) {
   auto k = reverse_prune_kernel<CPL, METRIC, INTX, SCALE, I8>;
   if (lds > 64 * 1024)
@@ -390,6 +407,20 @@ static void dispatch_prune(bool reverse, uint32_t cpl, const PruneKernelArgs& a,
   }
 }
 
+// The graph's byte rows, when it keeps them current, for the reverse
+// prune's byte mode (null otherwise).
+static void set_byte_rows(PruneCtx& pc, const Graph& g) {
+  pc.vecs8 = nullptr;
+  pc.nb8 = 0;
+  pc.qsh2 = 0;
+  if (g.vecs8 && g.vecs8_lo == g.int_lo && g.vecs8_cap >= g.n && byte_rows_eligible(g)) {
+    pc.vecs8 = (const uint4*)g.vecs8;
+    pc.nb8 = g.dim / 16;
+    const uint32_t h = f2h_rn((float)g.int_lo - 1024.0f);  // exact (byte_rows_eligible)
+    pc.qsh2 = h | (h << 16);
+  }
+}
+
 // Integer rows (int_exact_l2 holds) whose values span at most 255: the
 // reverse prune's Gram step can take them as bytes. JASPER_GRAM8=0 turns
 // that off (the fp16 Gram kernel then runs; the results are the same).
@@ -405,10 +436,13 @@ static bool int8_rows(const Graph& g) {
 // to 128 values take the byte Gram kernel, longer ones the INTX kernel.
 static void dispatch_reverse_i8(uint32_t cpl, const PruneKernelArgs& a, uint32_t grid, size_t lds, hipStream_t s) {
   switch (cpl) {
-    case 1: launch_reverse<1, kL2, true, false, true>(a, grid, lds, s); break;
-    case 2: launch_reverse<2, kL2, true, false, true>(a, grid, lds, s); break;
-    case 3: launch_reverse<3, kL2, true, false, true>(a, grid, lds, s); break;
-    case 4: launch_reverse<4, kL2, true, false, true>(a, grid, lds, s); break;
+    case 1: launch_reverse<1, kL2, true, false, 1>(a, grid, lds, s); break;
+    case 2: launch_reverse<2, kL2, true, false, 1>(a, grid, lds, s); break;
+    case 3: launch_reverse<3, kL2, true, false, 1>(a, grid, lds, s); break;
+    case 4:
+      if (a.pc.vecs8) launch_reverse<4, kL2, true, false, 2>(a, grid, lds, s);
+      else launch_reverse<4, kL2, true, false, 1>(a, grid, lds, s);
+      break;
     default: dispatch_prune<kL2, true>(true, cpl, a, grid, lds, s); break;
   }
 }
@@ -531,6 +565,7 @@ static PruneKernelArgs prune_args(Graph& g, float alpha, const BuildWorkspace& w
   uint16_t bits;
   std::memcpy(&bits, &lo, 2);
   pa.pc.lo2 = (uint32_t)bits * 0x10001u;
+  set_byte_rows(pa.pc, g);
   return pa;
 }
 
@@ -1022,6 +1057,7 @@ int64_t consolidate(Graph& g, float alpha, hipStream_t stream) {
       std::memcpy(&bits, &lo, 2);
       pa.pc.lo2 = (uint32_t)bits * 0x10001u;
     }
+    set_byte_rows(pa.pc, g);
     pa.edges = g.edges;
     pa.edist = g.edist;
     pa.counts = g.counts;

@@ -583,6 +583,72 @@ __device__ __forceinline__ float quad_partial_l2_int(const RowFrag<CPL>& qf, con
   return acc;
 }
 
+// ---- byte rows. A row of integers that spans at most 255 values can be
+// held as bytes b = x - lo; an operand that qualifies for the packed-difference
+// form is scored against the bytes instead of the fp16 row, reading half the
+// bytes. Quad lane ql takes byte chunks ql and ql + 4 (16 values each). The
+// left operand (a query) is held shifted, q' = q - lo + 1024,
+// and a byte b becomes the fp16 value 1024 + b by placing 0x64 above it
+// (one v_perm_b32 per two values), so q' - (1024 + b) = q - x: the same
+// exact fp16 difference, and with it the same exact sum of squares, as the
+// fp16 rows give.
+struct RowBytes {
+  uint4 x[2];
+};
+
+// q: byte chunk ql in q[0..1], byte chunk ql + 4 in q[2..3] (fp16 q')
+__device__ __forceinline__ void load_query_bytes(const uint4* qrow, uint32_t nb8, uint32_t qsh2, uint32_t ql,
+                                                 uint4 (&q)[4]) {
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    const uint32_t c = ql + 4u * u;
+    const uint32_t c0 = c < nb8 ? 2u * c : 0u;
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+      uint4 w = qrow[c0 + h];
+      w.x = sub_half2(w.x, qsh2);
+      w.y = sub_half2(w.y, qsh2);
+      w.z = sub_half2(w.z, qsh2);
+      w.w = sub_half2(w.w, qsh2);
+      q[2 * u + h] = w;
+    }
+  }
+}
+
+__device__ __forceinline__ void load_row_bytes(const uint4* vecs8, uint32_t nb8, uint32_t v, uint32_t ql,
+                                               RowBytes& r) {
+  const uint4* row = vecs8 + (size_t)v * nb8;
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    const uint32_t c = ql + 4u * u;
+    r.x[u] = row[c < nb8 ? c : 0u];
+  }
+}
+
+// bytes b0..b3 of w to fp16 pairs (1024 + b0, 1024 + b1) and (1024 + b2, 1024 + b3)
+__device__ __forceinline__ uint32_t bytes_lo_pair(uint32_t w) { return __builtin_amdgcn_perm(w, 0x64646464u, 0x00050004u); }
+__device__ __forceinline__ uint32_t bytes_hi_pair(uint32_t w) { return __builtin_amdgcn_perm(w, 0x64646464u, 0x00070006u); }
+
+__device__ __forceinline__ float score_bytes(uint32_t nb8, const uint4 (&q)[4], const RowBytes& r, uint32_t ql) {
+  float acc = 0.0f;
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    if (ql + 4u * u < nb8) {
+      const uint4 b = r.x[u];
+      const uint4 q0 = q[2 * u], q1 = q[2 * u + 1];
+      acc = dot2_sqdiff(q0.x, bytes_lo_pair(b.x), acc);
+      acc = dot2_sqdiff(q0.y, bytes_hi_pair(b.x), acc);
+      acc = dot2_sqdiff(q0.z, bytes_lo_pair(b.y), acc);
+      acc = dot2_sqdiff(q0.w, bytes_hi_pair(b.y), acc);
+      acc = dot2_sqdiff(q1.x, bytes_lo_pair(b.z), acc);
+      acc = dot2_sqdiff(q1.y, bytes_hi_pair(b.z), acc);
+      acc = dot2_sqdiff(q1.z, bytes_lo_pair(b.w), acc);
+      acc = dot2_sqdiff(q1.w, bytes_hi_pair(b.w), acc);
+    }
+  }
+  return quad_finish<kL2>(acc);
+}
+
 // ----------------------------------------------------------- left operands
 // The operand a row is compared against (a query, or a pruning candidate):
 // L2 keeps its fp16 chunks (v_fma_mix converts them), IP its fp32 elements

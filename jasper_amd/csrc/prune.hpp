@@ -28,6 +28,10 @@ struct PruneCtx {
   // partitioned build merges: the two id ranges whose vectors the merge may
   // read ([r1_lo, r1_lo + r1_n) and [r2_lo, r2_lo + r2_n))
   uint32_t r1_lo, r1_n, r2_lo, r2_n;
+  // the graph's byte rows (value - lo, nb8 16-byte chunks per row) and the
+  // shift lo - 1024 as two fp16, when it keeps them; null otherwise
+  const uint4* vecs8;
+  uint32_t nb8, qsh2;
 };
 
 // Whether the merge prune resolves id's vector (robust_prune_kernel_scale,
@@ -221,12 +225,13 @@ __device__ __forceinline__ uint32_t spread_nibbles(uint32_t w) {
 // registers of the fp16 form and half its MFMA steps. The Gram form's pair
 // distance is the same exact integer (|a_i - a_j|^2 does not depend on the
 // shift, and stays below 2^24), so the decisions are the fp16 form's.
-template <int T, bool I8 = false>
+template <int T, int I8 = 0>
 __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
                                       uint32_t* S_ids, float* S_dist, float* gn) {
   static_assert(T >= 1 && T <= 3, "one to three tiles");
   // fp16: 16 values per step, lane half h holds chunk 2s + h; int8: 32
-  // values per step, lane half h holds chunks 4s + 2h and 4s + 2h + 1
+  // values per step, lane half h holds chunks 4s + 2h and 4s + 2h + 1 (byte
+  // chunk 2s + h of a byte row)
   constexpr int KS = I8 ? kGramMaxChunks / 4 : kGramMaxChunks / 2;
   const uint32_t lane = lane_id();
   const uint32_t r = lane & 31u, h = lane >> 5;
@@ -236,7 +241,38 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   // past the summed length are zero
   uint4 fr[T][KS];
   float nrm[T];
-  if constexpr (I8) {
+  if constexpr (I8 == 2) {
+    // the byte rows already hold v = x - lo: one 16-byte load per step
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t i = 32u * (uint32_t)t + r;
+      const uint64_t key = i < nc ? C[i] : kEmptyKey;
+      const uint32_t id = i < nc ? key_id(key) : self;
+      const uint4* row8 = p.vecs8 + (size_t)id * p.nb8;
+      uint4 raw[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t c = 2u * (uint32_t)s + h;  // fp16 chunks 2c and 2c + 1
+        raw[s] = row8[min(c, p.nb8 - 1u)];
+      }
+      if (h == 0) gcd[i] = key_dist(key);
+      int acc = 0;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t c = 2u * (uint32_t)s + h;
+        const uint32_t keep = 2u * c + 1u < p.nlimit ? ~0u : 0u;
+        const uint4 x = raw[s];
+        const uint32_t wd[4] = {(x.x ^ 0x80808080u) & keep, (x.y ^ 0x80808080u) & keep,
+                                (x.z ^ 0x80808080u) & keep, (x.w ^ 0x80808080u) & keep};
+        fr[t][s] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
+      }
+      const int tot = acc + __shfl_xor(acc, 32, 64);
+      nrm[t] = (float)tot;  // exact: below 2^24
+      if (h == 0) gn[i] = nrm[t];
+    }
+  } else if constexpr (I8 == 1) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const uint32_t i = 32u * (uint32_t)t + r;
@@ -327,7 +363,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
 #pragma unroll
     for (int t2 = 0; t2 <= t; ++t2) {
       gram_f16 acc;
-      if constexpr (I8) {
+      if constexpr (I8 != 0) {
         gram_i16 ai = {};
 #pragma unroll
         for (int s = 0; s < KS; ++s)

@@ -151,69 +151,17 @@ __device__ __forceinline__ float score(const SearchArgs& a, const QueryFrag<CPL,
   return left_distance<CPL, METRIC, false>(q, x, ql, a.nchunks, nlimit);
 }
 
-// ---- byte rows. A query that qualifies for the packed-difference form
-// (intx) is scored against the graph's byte rows b = x - glo instead of its
-// fp16 rows, reading half the bytes. Quad lane ql takes byte chunks ql and
-// ql + 4 (16 values each). The query is held shifted, q' = q - glo + 1024,
-// and a byte b becomes the fp16 value 1024 + b by placing 0x64 above it
-// (one v_perm_b32 per two values), so q' - (1024 + b) = q - x: the same
-// exact fp16 difference, and with it the same exact sum of squares, as the
-// fp16 rows give.
-struct RowBytes {
-  uint4 x[2];
-};
-
-// q: byte chunk ql in q[0..1], byte chunk ql + 4 in q[2..3] (fp16 q')
+// ---- byte rows (common.hpp: load_query_bytes, load_row_bytes, score_bytes)
 __device__ __forceinline__ void load_query_bytes(const SearchArgs& a, const uint4* qrow, uint32_t ql,
                                                  uint4 (&q)[4]) {
-#pragma unroll
-  for (uint32_t u = 0; u < 2; ++u) {
-    const uint32_t c = ql + 4u * u;
-    const uint32_t c0 = c < a.nb8 ? 2u * c : 0u;
-#pragma unroll
-    for (uint32_t h = 0; h < 2; ++h) {
-      uint4 w = qrow[c0 + h];
-      w.x = sub_half2(w.x, a.qsh2);
-      w.y = sub_half2(w.y, a.qsh2);
-      w.z = sub_half2(w.z, a.qsh2);
-      w.w = sub_half2(w.w, a.qsh2);
-      q[2 * u + h] = w;
-    }
-  }
+  load_query_bytes(qrow, a.nb8, a.qsh2, ql, q);
 }
-
 __device__ __forceinline__ void load_row_bytes(const SearchArgs& a, uint32_t v, uint32_t ql, RowBytes& r) {
-  const uint4* row = a.vecs8 + (size_t)v * a.nb8;
-#pragma unroll
-  for (uint32_t u = 0; u < 2; ++u) {
-    const uint32_t c = ql + 4u * u;
-    r.x[u] = row[c < a.nb8 ? c : 0u];
-  }
+  load_row_bytes(a.vecs8, a.nb8, v, ql, r);
 }
-
-// bytes b0..b3 of w to fp16 pairs (1024 + b0, 1024 + b1) and (1024 + b2, 1024 + b3)
-__device__ __forceinline__ uint32_t bytes_lo_pair(uint32_t w) { return __builtin_amdgcn_perm(w, 0x64646464u, 0x00050004u); }
-__device__ __forceinline__ uint32_t bytes_hi_pair(uint32_t w) { return __builtin_amdgcn_perm(w, 0x64646464u, 0x00070006u); }
-
 __device__ __forceinline__ float score_bytes(const SearchArgs& a, const uint4 (&q)[4], const RowBytes& r,
                                              uint32_t ql) {
-  float acc = 0.0f;
-#pragma unroll
-  for (uint32_t u = 0; u < 2; ++u) {
-    if (ql + 4u * u < a.nb8) {
-      const uint4 b = r.x[u];
-      const uint4 q0 = q[2 * u], q1 = q[2 * u + 1];
-      acc = dot2_sqdiff(q0.x, bytes_lo_pair(b.x), acc);
-      acc = dot2_sqdiff(q0.y, bytes_hi_pair(b.x), acc);
-      acc = dot2_sqdiff(q0.z, bytes_lo_pair(b.y), acc);
-      acc = dot2_sqdiff(q0.w, bytes_hi_pair(b.y), acc);
-      acc = dot2_sqdiff(q1.x, bytes_lo_pair(b.z), acc);
-      acc = dot2_sqdiff(q1.y, bytes_hi_pair(b.z), acc);
-      acc = dot2_sqdiff(q1.z, bytes_lo_pair(b.w), acc);
-      acc = dot2_sqdiff(q1.w, bytes_hi_pair(b.w), acc);
-    }
-  }
-  return quad_finish<kL2>(acc);
+  return score_bytes(a.nb8, q, r, ql);
 }
 
 // Appends the key of a scored row to T[nt..) when its rank is below thr
@@ -291,13 +239,24 @@ __device__ __forceinline__ uint32_t score_pass_bytes(const SearchArgs& a, const 
 #ifndef JASPER_SEARCH_WAVES_L2
 #define JASPER_SEARCH_WAVES_L2 6
 #endif
-template <int CPL, int METRIC>
+// graphs with byte rows: two byte rows (16 VGPRs) in flight, the fp16 rows of
+// the few queries outside the exact span one at a time (72 VGPRs: seven waves
+// fit, but measured 0.445 ms against 0.436 ms at six on config 2, bw 44: the
+// hop's chain of dependent reads, not residency, sets the pace)
+#ifndef JASPER_SEARCH_WAVES_BYTES
+#define JASPER_SEARCH_WAVES_BYTES 6
+#endif
+template <int CPL, int METRIC, bool BYTES>
 constexpr int search_waves_per_simd() {
-  return CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? JASPER_SEARCH_WAVES_L2 : 1;
+  return BYTES ? JASPER_SEARCH_WAVES_BYTES
+               : CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? JASPER_SEARCH_WAVES_L2 : 1;
 }
 
-template <int CPL, int METRIC, bool STATS>
-__global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void beam_search_kernel(SearchArgs a) {
+// BYTES: the graph keeps byte rows (CPL 4, L2, no measurement mode)
+template <int CPL, int METRIC, bool STATS, bool BYTES = false>
+__global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC, BYTES>())) void beam_search_kernel(
+    SearchArgs a) {
+  static_assert(!BYTES || (CPL == 4 && METRIC == kL2 && !STATS), "byte rows: L2 rows of 112 or 128 values");
   extern __shared__ uint64_t smem[];
   const uint32_t lane = threadIdx.x;
   const uint32_t qid = blockIdx.x;
@@ -329,8 +288,8 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   // From here on such a query is held shifted, in byte-chunk order, in the
   // registers of its fp16 fragment, which it no longer uses.
   bool bytes = false;
-  if constexpr (METRIC == kL2 && CPL == 4 && !STATS) {
-    bytes = intx && a.vecs8 != nullptr;
+  if constexpr (BYTES) {
+    bytes = intx;
     if (bytes) load_query_bytes(a, qrow, ql, qf.h.x);
   }
 
@@ -343,9 +302,11 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
   {
     float d = 0.0f;
     if (bytes) {
-      RowBytes xb;
-      load_row_bytes(a, a.medoid, ql, xb);
-      if constexpr (CPL == 4 && METRIC == kL2) d = score_bytes(a, qf.h.x, xb, ql);
+      if constexpr (BYTES) {
+        RowBytes xb;
+        load_row_bytes(a, a.medoid, ql, xb);
+        d = score_bytes(a, qf.h.x, xb, ql);
+      }
     } else {
       RowFrag<CPL> x;
       load_row_frag<CPL>(a.vecs + (size_t)a.medoid * a.nchunks, ql, a.nchunks, true, x);
@@ -459,15 +420,17 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC>())) void be
     if (cnt == bw) thr = key_rank(regb ? readlane64(b, (int)(bw - 1u)) : B[bw - 1u]);
     uint32_t nt = 0, base = 0;
     if (bytes) {
-      if constexpr (CPL == 4 && METRIC == kL2) {
+      if constexpr (BYTES) {
         for (; base + 16 < nm; base += 32)
           nt = score_pass_bytes<true>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
         if (base < nm) nt = score_pass_bytes<false>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
       }
     } else {
 #if JASPER_SEARCH_TWO_ROWS
-      for (; base + 16 < nm; base += 32)
-        nt = score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+      if constexpr (!BYTES) {
+        for (; base + 16 < nm; base += 32)
+          nt = score_pass<CPL, METRIC, true>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
+      }
 #endif
       for (; base + 16 < nm; base += 16)
         nt = score_pass<CPL, METRIC, false>(a, qf, cand, T, base, nm, ql, qg, intx, thr, nt);
@@ -651,9 +614,9 @@ size_t beam_search_lds_bytes(const Graph& g, const SearchRequest& r) {
          std::max<size_t>(((size_t)1 << hb) * entry, 4);
 }
 
-template <int CPL, int METRIC, bool STATS>
+template <int CPL, int METRIC, bool STATS, bool BYTES = false>
 static void launch_one(const SearchArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  auto kern = beam_search_kernel<CPL, METRIC, STATS>;
+  auto kern = beam_search_kernel<CPL, METRIC, STATS, BYTES>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
               "set LDS size");
@@ -743,6 +706,11 @@ void launch_beam_search(const Graph& g, const SearchRequest& r, hipStream_t stre
   const size_t lds = beam_search_lds_bytes(g, r);
   const uint32_t cpl = (a.nchunks + 3) / 4;
   const dim3 grid(r.nq);
+  if (a.vecs8 && !stats && g.metric == kL2 && cpl == 4) {
+    launch_one<4, kL2, false, true>(a, grid, lds, stream);
+    hip_check(hipGetLastError(), "launch beam_search_kernel");
+    return;
+  }
 #define JA_LAUNCH(C)                                                                                   \
   case C: {                                                                                            \
     if (g.metric == kL2) {                                                                             \
