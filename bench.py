@@ -379,7 +379,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBS,
             "traffic": measured_traffic(chosen, args.n, args.nq, int(rows_b.mean())),
-            "kernel": "beam_search_kernel<4,0,false>",
+            "kernel": "beam_search_kernel<4,0,false,true>" if fmt["byte_rows"] else "beam_search_kernel<4,0,false>",
             "kernel_ms": kernel_ms,
             "algorithmic_bytes_per_launch": alg_bytes,
             "per_query": {"hops": hops / args.nq, "adjacency_entries": deg / args.nq,
