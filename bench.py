@@ -214,13 +214,14 @@ def main() -> int:
                     help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--path", default="search",
-                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5", "updates",
-                             "scale", "diskann"],
+                    choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5", "c5plain",
+                             "updates", "scale", "diskann"],
                     help="search (default, the headline metric) or one of the other hot-path rows, each "
                          "printing its own JSON line: directional (config 3, LSH), pq (PQ-ADC on "
                          "config 3's data), bruteforce (exact k-NN, config 2), rotate (prerotation), "
                          "rabitq (one-bit codes), c4 (config 4: 1M x 960 build + PQ search), c5 "
-                         "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search), updates "
+                         "(config 5: 100M x 128 in-HBM build + LSH k=16 directional search), c5plain (config 5's rows "
+                         "without prerotation: plain build and search on byte rows), updates "
                          "(config 2: mark_deleted 10%%, consolidate, append 100k), scale (config 2: the "
                          "partitioned build), diskann (config 2: the DiskANN build)")
     ap.add_argument("--scale-parts", default="4,2,8", help="partition counts of --path scale (first = the line's value)")
@@ -1011,7 +1012,55 @@ def run_diskann(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
-OTHER_PATHS = {"c4": run_c4, "c5": run_c5, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
+def run_c5plain(args, torch, jasper_amd, datasets, dev, log):
+    """Config 5's 100M x 128 clustered integer rows without prerotation:
+    the plain construction (the exact build search) and the plain beam
+    search on that graph, QPS at the first swept beam width with recall@10
+    >= 0.9. The rows are integers in [0, 218], so the graph keeps byte rows
+    and both the build's searches and the queries read them. The roofline's
+    algorithmic bytes come from the exact work counters of a 256-query
+    sample (the counters' per-query seen bitmap is n / 8 bytes), scaled to
+    the batch."""
+    n, nq, dim = args.c5_n, args.nq, 128
+    base = datasets.clustered_device(n, dim, 0, dev)
+    queries = datasets.clustered_device(nq, dim, 1, dev)
+    torch.cuda.synchronize()
+    gt_ids, _ = jasper_amd.bruteforce_knn(base, queries, 10, "l2")
+    gt = gt_ids.cpu().numpy()
+    t0 = time.perf_counter()
+    g = jasper_amd.Graph.build(base, n_neighbors=64, distance="l2", alpha=1.2)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    bst = jasper_amd.last_build_stats()
+    fmt = g.row_format()
+    log(f"c5 plain build {build_s:.1f}s = {n / build_s:,.0f} vec/s, batches={int(bst['batches'])}, rows {fmt}")
+    curve = _sweep(torch, g.search, queries, gt, (64, 128, 256, 384, 512), log, "c5 plain graph search")
+    chosen = next((c for c in curve if c["recall_at_10"] >= 0.9), curve[-1])
+    bw = chosen["beam_width"]
+    wall, ev, _ = _timed(torch, lambda: g.search(queries, k=10, beam_width=bw), args.steps, args.warmup)
+    sample = queries[:256].contiguous()
+    st = g.search_stats(sample, k=10, beam_width=bw).astype(np.int64)
+    rows_b = query_row_bytes(fmt, sample.cpu().numpy(), dim)
+    alg = algorithmic_bytes(st, dim, len(st), rows_b) * nq / len(st)
+    gbs = alg / (ev / 1000.0) / 1e9
+    res = _line(args, "QPS @ recall@10>=0.9, config 5 data (100M x 128) plain graph", nq / (wall / 1000.0),
+                "queries/s", wall, "f32",
+                {"workload": f"{n} x {dim} clustered integer fp16 (10,000 clusters), not prerotated, R=64 "
+                             f"alpha=1.2, plain construction and beam search, {nq} queries, k=10",
+                 "beam_width": bw, "recall_at_10": chosen["recall_at_10"], "build_s": build_s,
+                 "build_vectors_per_s": n / build_s, "byte_rows": fmt["byte_rows"], "curve": curve},
+                {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                 "traffic": None, "kernel": "beam_search_kernel<4,0,false,true>" if fmt["byte_rows"]
+                 else "beam_search_kernel<4,0,false>", "kernel_ms": ev, "algorithmic_bytes_per_launch": alg,
+                 "per_query": {"hops": float(st[:, 0].mean()), "adjacency_entries": float(st[:, 1].mean()),
+                               "vectors_scored": float(st[:, 2].mean())},
+                 "notes": "algorithmic bytes from a 256-query sample of the exact work counters"})
+    print(json.dumps(res), flush=True)
+    g.free()
+    return 0
+
+
+OTHER_PATHS = {"c4": run_c4, "c5": run_c5, "c5plain": run_c5plain, "directional": run_directional, "pq": run_pq, "bruteforce": run_bruteforce,
                "rotate": run_rotate, "rabitq": run_rabitq, "updates": run_updates, "scale": run_scale,
                "diskann": run_diskann}
 
