@@ -463,6 +463,7 @@ void build_diskann(Graph& g, uint32_t R_int, float alpha, int64_t n_parts, int64
     sg.int_state = g.int_state;
     sg.int_lo = g.int_lo;
     sg.int_hi = g.int_hi;
+    refresh_byte_rows(sg, c, s);  // the shard's byte rows, when the graph's rows qualify
     build_graph(sg, alpha, std::max<int64_t>(1, std::min<int64_t>(batch_cap, c)), s, false, nullptr);
     hip_check(hipEventRecord(e[3], s), "event record");
     MergeArgs m{};

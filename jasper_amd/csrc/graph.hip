@@ -298,6 +298,8 @@ static void update_byte_rows(Graph& g, int64_t row0, int64_t end, hipStream_t st
   hip_check(hipGetLastError(), "launch byte_rows_kernel");
 }
 
+void refresh_byte_rows(Graph& g, int64_t rows, hipStream_t stream) { update_byte_rows(g, 0, rows, stream); }
+
 static void scan_int_range_only(Graph& g, int64_t row0, int64_t n, hipStream_t stream);
 
 void scan_int_range(Graph& g, int64_t row0, int64_t n, hipStream_t stream) {

@@ -119,6 +119,10 @@ void scan_int_range(Graph& g, int64_t row0, int64_t n, hipStream_t stream);
 // chunks, four fp16 chunks per quad lane), and lo - 1024 an fp16 value (the
 // search's query shift).
 bool byte_rows_eligible(const Graph& g);
+// Rewrites the byte rows of rows [0, rows) (or drops them) from the value
+// range already recorded in g, for rows written without a range scan whose
+// values lie in that range (the DiskANN build's shard graphs).
+void refresh_byte_rows(Graph& g, int64_t rows, hipStream_t stream);
 
 // The recorded result: true when every stored value is an integer in
 // [int_lo, int_hi].
