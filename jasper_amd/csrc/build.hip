@@ -310,14 +310,19 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
     wave_sync();
     // d(w, v) for every source (compute_distance(src_vec = w, sink_vec = v))
     if constexpr (I8 == 2) {
-      // xw holds w shifted in byte-chunk order: the sources' byte rows
+      // xw holds w shifted in byte-chunk order; a graph row's values lie in
+      // the byte range, so w becomes bytes and the sources' byte rows are
+      // scored with v_dot4_u32_u8
+      uint4 wb[2];
+      uint32_t wn;
+      (void)left_bytes_u8(a.pc.nb8, xw.x, ql, wb, wn);
       for (uint32_t base = 0; base < taken; base += 16) {
         const uint32_t j = base + qg;
         const bool act = j < taken;
         const uint32_t sid = act ? l.srcs[j] : 0u;
         RowBytes xs;
         load_row_bytes(a.pc.vecs8, a.pc.nb8, sid, ql, xs);
-        const float d = score_bytes(a.pc.nb8, xw.x, xs, ql);
+        const float d = score_bytes_u8(a.pc.nb8, wb[0], wb[1], wn, xs, ql);
         if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
       }
     } else {

@@ -649,6 +649,60 @@ __device__ __forceinline__ float score_bytes(uint32_t nb8, const uint4 (&q)[4], 
   return quad_finish<kL2>(acc);
 }
 
+// A left operand whose own values also lie in [lo, lo + 255] (every half of
+// its q' words is 0x64bb) becomes bytes b_q = q - lo in the byte rows'
+// layout (qb[0]: byte chunk ql, qb[1]: byte chunk ql + 4), with qn the sum
+// of b_q^2 over the lane's values. Then per lane sum (q - x)^2 = qn + sum
+// b_x^2 - 2 sum b_q b_x, all exact in u32 with v_dot4_u32_u8 (four values
+// per instruction, against one v_perm, v_pk_add_f16 and v_dot2 per two values
+// of score_bytes), and the quad sum of these integers (each below 2^24, their
+// total too) is the same float. Returns whether the operand qualifies
+// (wave-uniform).
+__device__ __forceinline__ bool left_bytes_u8(uint32_t nb8, const uint4 (&q)[4], uint32_t ql, uint4 (&qb)[2],
+                                              uint32_t& qn) {
+  bool ok = true;
+  qn = 0;
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    const uint4 q0 = q[2 * u], q1 = q[2 * u + 1];
+    qb[u] = make_uint4(__builtin_amdgcn_perm(q0.y, q0.x, 0x06040200u), __builtin_amdgcn_perm(q0.w, q0.z, 0x06040200u),
+                       __builtin_amdgcn_perm(q1.y, q1.x, 0x06040200u), __builtin_amdgcn_perm(q1.w, q1.z, 0x06040200u));
+    if (ql + 4u * u < nb8) {
+      // every half's high byte is 0x64: the and of the words has all of
+      // 0x64's bits there and their or no other bit
+      const uint32_t wa = q0.x & q0.y & q0.z & q0.w & q1.x & q1.y & q1.z & q1.w;
+      const uint32_t wo = q0.x | q0.y | q0.z | q0.w | q1.x | q1.y | q1.z | q1.w;
+      ok = ok && (wa & 0xFF00FF00u) == 0x64006400u && (wo & 0xFF00FF00u) == 0x64006400u;
+      qn = __builtin_amdgcn_udot4(qb[u].x, qb[u].x, qn, false);
+      qn = __builtin_amdgcn_udot4(qb[u].y, qb[u].y, qn, false);
+      qn = __builtin_amdgcn_udot4(qb[u].z, qb[u].z, qn, false);
+      qn = __builtin_amdgcn_udot4(qb[u].w, qb[u].w, qn, false);
+    }
+  }
+  return ballot(!ok) == 0;
+}
+
+__device__ __forceinline__ float score_bytes_u8(uint32_t nb8, const uint4& qb0, const uint4& qb1, uint32_t qn,
+                                                const RowBytes& r, uint32_t ql) {
+  uint32_t qx = 0, xx = 0;
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    if (ql + 4u * u < nb8) {
+      const uint4 b = r.x[u];
+      const uint4 q = u == 0 ? qb0 : qb1;
+      qx = __builtin_amdgcn_udot4(q.x, b.x, qx, false);
+      qx = __builtin_amdgcn_udot4(q.y, b.y, qx, false);
+      qx = __builtin_amdgcn_udot4(q.z, b.z, qx, false);
+      qx = __builtin_amdgcn_udot4(q.w, b.w, qx, false);
+      xx = __builtin_amdgcn_udot4(b.x, b.x, xx, false);
+      xx = __builtin_amdgcn_udot4(b.y, b.y, xx, false);
+      xx = __builtin_amdgcn_udot4(b.z, b.z, xx, false);
+      xx = __builtin_amdgcn_udot4(b.w, b.w, xx, false);
+    }
+  }
+  return quad_finish<kL2>((float)(qn + xx - 2u * qx));  // the lane's exact sum of (q - x)^2
+}
+
 // ----------------------------------------------------------- left operands
 // The operand a row is compared against (a query, or a pruning candidate):
 // L2 keeps its fp16 chunks (v_fma_mix converts them), IP its fp32 elements

@@ -203,8 +203,8 @@ __device__ __forceinline__ uint32_t score_pass(const SearchArgs& a, const QueryF
   }
 }
 
-// score_pass on the byte rows
-template <bool TWO>
+// score_pass on the byte rows (U8: the query held as bytes, left_bytes_u8)
+template <bool TWO, bool U8 = false>
 __device__ __forceinline__ uint32_t score_pass_bytes(const SearchArgs& a, const uint4 (&q8)[4], const uint32_t* cand,
                                                      uint64_t* T, uint32_t base, uint32_t nm, uint32_t ql,
                                                      uint32_t qg, uint64_t thr, uint32_t nt) {
@@ -219,12 +219,12 @@ __device__ __forceinline__ uint32_t score_pass_bytes(const SearchArgs& a, const 
     const uint32_t v1 = act1 ? cand[j1] : 0u;
     RowBytes x1;
     load_row_bytes(a, v1, ql, x1);
-    const float d0 = score_bytes(a, q8, x0, ql);
-    const float d1 = score_bytes(a, q8, x1, ql);
+    const float d0 = (U8 ? score_bytes_u8(a.nb8, q8[0], q8[1], q8[2].x, x0, ql) : score_bytes(a, q8, x0, ql));
+    const float d1 = (U8 ? score_bytes_u8(a.nb8, q8[0], q8[1], q8[2].x, x1, ql) : score_bytes(a, q8, x1, ql));
     nt = append_key(T, nt, act0, ql, d0, v0, thr);
     return append_key(T, nt, act1, ql, d1, v1, thr);
   } else {
-    const float d0 = score_bytes(a, q8, x0, ql);
+    const float d0 = (U8 ? score_bytes_u8(a.nb8, q8[0], q8[1], q8[2].x, x0, ql) : score_bytes(a, q8, x0, ql));
     return append_key(T, nt, act0, ql, d0, v0, thr);
   }
 }
@@ -287,10 +287,23 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC, BYTES>())) 
   // byte rows for this query (wave-uniform; rows of 112 or 128 values).
   // From here on such a query is held shifted, in byte-chunk order, in the
   // registers of its fp16 fragment, which it no longer uses.
-  bool bytes = false;
+  // A query whose values also lie in [glo, glo + 255] then moves on to its
+  // bytes (u8q): qf.h.x[0..1] its byte chunks, qf.h.x[2].x the lane's sum of
+  // their squares (left_bytes_u8).
+  bool bytes = false, u8q = false;
   if constexpr (BYTES) {
     bytes = intx;
-    if (bytes) load_query_bytes(a, qrow, ql, qf.h.x);
+    if (bytes) {
+      load_query_bytes(a, qrow, ql, qf.h.x);
+      uint4 qb[2];
+      uint32_t qn;
+      u8q = left_bytes_u8(a.nb8, qf.h.x, ql, qb, qn);
+      if (u8q) {
+        qf.h.x[0] = qb[0];
+        qf.h.x[1] = qb[1];
+        qf.h.x[2].x = qn;
+      }
+    }
   }
 
   // B = [(medoid, d(q, medoid))]; at bw <= 64 B lives in registers, one key
@@ -305,7 +318,7 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC, BYTES>())) 
       if constexpr (BYTES) {
         RowBytes xb;
         load_row_bytes(a, a.medoid, ql, xb);
-        d = score_bytes(a, qf.h.x, xb, ql);
+        d = u8q ? score_bytes_u8(a.nb8, qf.h.x[0], qf.h.x[1], qf.h.x[2].x, xb, ql) : score_bytes(a, qf.h.x, xb, ql);
       }
     } else {
       RowFrag<CPL> x;
@@ -421,9 +434,15 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC, BYTES>())) 
     uint32_t nt = 0, base = 0;
     if (bytes) {
       if constexpr (BYTES) {
-        for (; base + 16 < nm; base += 32)
-          nt = score_pass_bytes<true>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
-        if (base < nm) nt = score_pass_bytes<false>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
+        if (u8q) {
+          for (; base + 16 < nm; base += 32)
+            nt = score_pass_bytes<true, true>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
+          if (base < nm) nt = score_pass_bytes<false, true>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
+        } else {
+          for (; base + 16 < nm; base += 32)
+            nt = score_pass_bytes<true>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
+          if (base < nm) nt = score_pass_bytes<false>(a, qf.h.x, cand, T, base, nm, ql, qg, thr, nt);
+        }
       }
     } else {
 #if JASPER_SEARCH_TWO_ROWS
