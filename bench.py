@@ -356,7 +356,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": search_dtype(fmt, queries),
         "data": "synthetic",
         "config": {
             "workload": (f"config 2: {args.n} x 128 clustered integer-valued fp16 (1000 clusters, "
@@ -369,7 +369,8 @@ def main() -> int:
             "build_s": build_s,
             "build_max_batch": int(bst["max_batch"]),
             "storage": ("fp16 vectors; the search reads byte rows (value - lo) for integer rows spanning "
-                        "<= 255 values" if fmt["byte_rows"] else "fp16 vectors") + ", fp32 distance arithmetic",
+                        "<= 255 values, and queries in that range as bytes (exact u8 dot products, u32 sums)"
+                        if fmt["byte_rows"] else "fp16 vectors, fp32 distance arithmetic"),
             "row_bytes_per_scored_vector": float(rows_b.mean()),
             "curve": curve,
         },
@@ -445,6 +446,18 @@ def query_row_bytes(fmt, queries, dim):
     integer = (q == np.rint(q)).all(axis=1)
     span = np.maximum(q.max(axis=1), fmt["hi"]) - np.minimum(q.min(axis=1), fmt["lo"])
     return np.where(integer & (span <= smax), dim, 2 * dim).astype(np.int64)
+
+
+def search_dtype(fmt, queries):
+    """The arithmetic the plain search uses for these queries: u8 (v_dot4_u32_u8
+    with u32 sums, exact) when the graph keeps byte rows and every query's
+    values are integers in the rows' byte range [lo, lo + 255], f32 when none
+    is, both names otherwise."""
+    q = queries.astype(np.float32)
+    if not fmt["byte_rows"]:
+        return "f32"
+    inb = ((q == np.rint(q)) & (q >= fmt["lo"]) & (q <= fmt["lo"] + 255)).all(axis=1)
+    return "u8" if inb.all() else ("f32" if not inb.any() else "u8+f32")
 
 
 def _timed(torch, fn, steps, warmup):
@@ -1044,7 +1057,7 @@ def run_c5plain(args, torch, jasper_amd, datasets, dev, log):
     alg = algorithmic_bytes(st, dim, len(st), rows_b) * nq / len(st)
     gbs = alg / (ev / 1000.0) / 1e9
     res = _line(args, "QPS @ recall@10>=0.9, config 5 data (100M x 128) plain graph", nq / (wall / 1000.0),
-                "queries/s", wall, "f32",
+                "queries/s", wall, search_dtype(fmt, queries.cpu().numpy()),
                 {"workload": f"{n} x {dim} clustered integer fp16 (10,000 clusters), not prerotated, R=64 "
                              f"alpha=1.2, plain construction and beam search, {nq} queries, k=10",
                  "beam_width": bw, "recall_at_10": chosen["recall_at_10"], "build_s": build_s,
