@@ -180,8 +180,11 @@ static_assert(kGramLdsWords <= kCandBuf, "the Gram prune's scratch reuses the so
 // prune, and reverse pairs only for targets in B2 (r2 of the prune context;
 // process_reverse_edges_kernel_scale skips the others,
 // index/construct_scale_kernels.cuh:193-194).
-template <int CPL, int METRIC, bool INTX, bool SCALE>
+// BYTES: the graph keeps byte rows (CPL 4, L2, integer rows): the prune
+// works on them (robust_prune_wave_u8)
+template <int CPL, int METRIC, bool INTX, bool SCALE, bool BYTES = false>
 __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
+  static_assert(!BYTES || (CPL == 4 && METRIC == kL2 && INTX && !SCALE), "byte rows: integer L2 rows of 112/128");
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
   const uint32_t lane = lane_id();
@@ -206,7 +209,9 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   }
   wave_sync();
   sort_candidates(l.C, nc);
-  const uint32_t ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  uint32_t ns;
+  if constexpr (BYTES) ns = robust_prune_wave_u8(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  else ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   write_selection(a, v, ns, l.S_ids, l.S_dist);
   if (lane < R) {
     const uint32_t t = lane < ns ? l.S_ids[lane] : 0u;
@@ -372,9 +377,9 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
   }
 }
 
-template <int CPL, int METRIC, bool INTX, bool SCALE>
+template <int CPL, int METRIC, bool INTX, bool SCALE, bool BYTES = false>
 static void launch_forward(const PruneKernelArgs& a, uint32_t bs, size_t lds, hipStream_t s) {
-  auto k = forward_prune_kernel<CPL, METRIC, INTX, SCALE>;
+  auto k = forward_prune_kernel<CPL, METRIC, INTX, SCALE, BYTES>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds), "LDS");
   hipLaunchKernelGGL(k, dim3(bs), dim3(64), lds, s, a);
@@ -667,7 +672,8 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       // 2. forward merge + prune + reverse pairs
       pa.batch_offset = (uint32_t)count;
       timer.start();
-      if (intx) dispatch_prune<kL2, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+      if (intx && pa.pc.vecs8 && cpl == 4) launch_forward<4, kL2, true, false, true>(pa, (uint32_t)bs, plds, stream);
+      else if (intx) dispatch_prune<kL2, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
       else if (g.metric == kL2) dispatch_prune<kL2, false>(false, cpl, pa, (uint32_t)bs, plds, stream);
       else dispatch_prune<kIP, false>(false, cpl, pa, (uint32_t)bs, plds, stream);
       hip_check(hipGetLastError(), "launch forward_prune_kernel");

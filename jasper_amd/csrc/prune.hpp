@@ -176,6 +176,80 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
   return ns;
 }
 
+// robust_prune_wave on byte rows (CPL 4, L2, pc.vecs8 set: integer rows
+// spanning at most 255 values): candidates and members are read as byte
+// rows and every pair distance is sum b_c^2 + sum b_m^2 - 2 sum b_c b_m in
+// u32 (score_bytes_u8: two independent chains of eight v_dot4_u32_u8 per
+// lane instead of one chain of sixteen v_dot2), the exact integer of the
+// packed-difference form, so the selection is the same. A member selected
+// in this block is taken from its quad's registers.
+__device__ uint32_t robust_prune_wave_u8(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
+                                         uint32_t* S_ids, float* S_dist) {
+  const uint32_t lane = lane_id();
+  const uint32_t ql = lane & 3u, qg = lane >> 2;
+  uint32_t ns = 0;
+  for (uint32_t b = 0; b < nc && ns < p.R; b += 16) {
+    const uint32_t j = b + qg;
+    bool valid = j < nc;
+    const uint64_t ck = valid ? C[j] : kEmptyKey;
+    const uint32_t cid = key_id(ck);
+    const float cd = key_dist(ck);
+    valid = valid && cid != self;
+    RowBytes cb;
+    load_row_bytes(p.vecs8, p.nb8, valid ? cid : 0u, ql, cb);
+    uint32_t cn = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) {
+      if (ql + 4u * u < p.nb8) {
+        cn = __builtin_amdgcn_udot4(cb.x[u].x, cb.x[u].x, cn, false);
+        cn = __builtin_amdgcn_udot4(cb.x[u].y, cb.x[u].y, cn, false);
+        cn = __builtin_amdgcn_udot4(cb.x[u].z, cb.x[u].z, cn, false);
+        cn = __builtin_amdgcn_udot4(cb.x[u].w, cb.x[u].w, cn, false);
+      }
+    }
+    bool pruned = false;
+    const uint32_t ns0 = ns;
+    if (ns0) {
+      const uint32_t sid_lane = lane < ns0 ? S_ids[lane] : 0u;
+      RowBytes xn;
+      load_row_bytes(p.vecs8, p.nb8, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, 0), ql, xn);
+      for (uint32_t s = 0; s < ns0; ++s) {
+        const RowBytes xs = xn;
+        if (s + 1 < ns0)
+          load_row_bytes(p.vecs8, p.nb8, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)(s + 1)), ql, xn);
+        const float d = score_bytes_u8(p.nb8, cb.x[0], cb.x[1], cn, xs, ql);
+        if (d * p.alpha < cd) pruned = true;
+        if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
+      }
+    }
+    // resolve the block in candidate order
+    uint64_t live = ballot(valid && !pruned && ql == 0);
+    while (live && ns < p.R) {
+      const uint32_t g = (uint32_t)__builtin_ctzll(live) >> 2;
+      if (qg == g && ql == 0) {
+        S_ids[ns] = cid;
+        S_dist[ns] = cd;
+      }
+      wave_sync();
+      const int src = (int)(g * 4u + ql);
+      RowBytes xs;
+#pragma unroll
+      for (uint32_t u = 0; u < 2; ++u) {
+        xs.x[u].x = (uint32_t)__shfl((int)cb.x[u].x, src, 64);
+        xs.x[u].y = (uint32_t)__shfl((int)cb.x[u].y, src, 64);
+        xs.x[u].z = (uint32_t)__shfl((int)cb.x[u].z, src, 64);
+        xs.x[u].w = (uint32_t)__shfl((int)cb.x[u].w, src, 64);
+      }
+      const float d = score_bytes_u8(p.nb8, cb.x[0], cb.x[1], cn, xs, ql);
+      if (qg > g && d * p.alpha < cd) pruned = true;
+      ns += 1;
+      live = ballot(valid && !pruned && ql == 0 && qg > g);
+    }
+  }
+  wave_sync();
+  return ns;
+}
+
 // ------------------------------------------------ integer rows: Gram form
 // On integer-valued rows within the exact range (int_exact_l2), shifted by
 // their smallest value lo to a' = a - lo in [0, span] (exact in fp16), every
