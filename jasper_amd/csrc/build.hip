@@ -184,7 +184,7 @@ static_assert(kGramLdsWords <= kCandBuf, "the Gram prune's scratch reuses the so
 // works on them (robust_prune_wave_u8)
 template <int CPL, int METRIC, bool INTX, bool SCALE, bool BYTES = false>
 __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
-  static_assert(!BYTES || (CPL == 4 && METRIC == kL2 && INTX && !SCALE), "byte rows: integer L2 rows of 112/128");
+  static_assert(!BYTES || (CPL == 4 && METRIC == kL2 && INTX), "byte rows: integer L2 rows of 112/128");
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
   const uint32_t lane = lane_id();
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   wave_sync();
   sort_candidates(l.C, nc);
   uint32_t ns;
-  if constexpr (BYTES) ns = robust_prune_wave_u8(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  if constexpr (BYTES) ns = robust_prune_wave_u8<SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   else ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   write_selection(a, v, ns, l.S_ids, l.S_dist);
   if (lane < R) {
@@ -348,7 +348,12 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
     sort_candidates(l.C, nc);
     uint32_t ns;
     if constexpr (SCALE) {
-      ns = robust_prune_wave<CPL, METRIC, INTX, true>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+      if constexpr (CPL == 4 && METRIC == kL2 && INTX) {
+        if (a.pc.vecs8) ns = robust_prune_wave_u8<true>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+        else ns = robust_prune_wave<CPL, METRIC, INTX, true>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+      } else {
+        ns = robust_prune_wave<CPL, METRIC, INTX, true>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
+      }
     } else if constexpr (CPL >= 1 && CPL <= 4) {
       // up to 96 candidates of rows of up to 128 values: pair distances on
       // the matrix cores, exact for integer rows, proved otherwise
@@ -806,7 +811,8 @@ void build_scale(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int
         launch_beam_search(g, r, stream);
         // 2. forward merge + merge prune into B1, pairs for B2 targets
         pa.batch_offset = (uint32_t)(b1s + count);
-        if (intx) dispatch_prune<kL2, true, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        if (intx && pa.pc.vecs8 && cpl == 4) launch_forward<4, kL2, true, true, true>(pa, (uint32_t)bs, plds, stream);
+        else if (intx) dispatch_prune<kL2, true, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
         else if (g.metric == kL2) dispatch_prune<kL2, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
         else dispatch_prune<kIP, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
         hip_check(hipGetLastError(), "launch forward_prune_kernel (merge)");

@@ -182,7 +182,9 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
 // u32 (score_bytes_u8: two independent chains of eight v_dot4_u32_u8 per
 // lane instead of one chain of sixteen v_dot2), the exact integer of the
 // packed-difference form, so the selection is the same. A member selected
-// in this block is taken from its quad's registers.
+// in this block is taken from its quad's registers. SCALE: the merge prune's
+// rule, as robust_prune_wave's.
+template <bool SCALE = false>
 __device__ uint32_t robust_prune_wave_u8(const PruneCtx& p, const uint64_t* C, uint32_t nc, uint32_t self,
                                          uint32_t* S_ids, float* S_dist) {
   const uint32_t lane = lane_id();
@@ -195,6 +197,7 @@ __device__ uint32_t robust_prune_wave_u8(const PruneCtx& p, const uint64_t* C, u
     const uint32_t cid = key_id(ck);
     const float cd = key_dist(ck);
     valid = valid && cid != self;
+    const bool tested = !SCALE || resolvable(p, cid);
     RowBytes cb;
     load_row_bytes(p.vecs8, p.nb8, valid ? cid : 0u, ql, cb);
     uint32_t cn = 0;
@@ -217,8 +220,11 @@ __device__ uint32_t robust_prune_wave_u8(const PruneCtx& p, const uint64_t* C, u
         const RowBytes xs = xn;
         if (s + 1 < ns0)
           load_row_bytes(p.vecs8, p.nb8, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)(s + 1)), ql, xn);
+        if constexpr (SCALE) {
+          if (!resolvable(p, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)s))) continue;
+        }
         const float d = score_bytes_u8(p.nb8, cb.x[0], cb.x[1], cn, xs, ql);
-        if (d * p.alpha < cd) pruned = true;
+        if (tested && d * p.alpha < cd) pruned = true;
         if ((s & 7u) == 7u && ballot(valid && !pruned) == 0) break;
       }
     }
@@ -226,6 +232,8 @@ __device__ uint32_t robust_prune_wave_u8(const PruneCtx& p, const uint64_t* C, u
     uint64_t live = ballot(valid && !pruned && ql == 0);
     while (live && ns < p.R) {
       const uint32_t g = (uint32_t)__builtin_ctzll(live) >> 2;
+      // SCALE: the new member prunes only when its vector is resolvable
+      const bool g_prunes = !SCALE || (ballot(tested && qg == g) != 0);
       if (qg == g && ql == 0) {
         S_ids[ns] = cid;
         S_dist[ns] = cd;
@@ -240,8 +248,10 @@ __device__ uint32_t robust_prune_wave_u8(const PruneCtx& p, const uint64_t* C, u
         xs.x[u].z = (uint32_t)__shfl((int)cb.x[u].z, src, 64);
         xs.x[u].w = (uint32_t)__shfl((int)cb.x[u].w, src, 64);
       }
-      const float d = score_bytes_u8(p.nb8, cb.x[0], cb.x[1], cn, xs, ql);
-      if (qg > g && d * p.alpha < cd) pruned = true;
+      if (g_prunes) {
+        const float d = score_bytes_u8(p.nb8, cb.x[0], cb.x[1], cn, xs, ql);
+        if (qg > g && tested && d * p.alpha < cd) pruned = true;
+      }
       ns += 1;
       live = ballot(valid && !pruned && ql == 0 && qg > g);
     }
