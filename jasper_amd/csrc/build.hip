@@ -369,6 +369,8 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
           else if (nc <= 64) ns = robust_prune_gram_f<2, CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
           else ns = robust_prune_gram_f<3, CPL, METRIC>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
         }
+      } else if constexpr (I8 == 2) {
+        ns = robust_prune_wave_u8(a.pc, l.C, nc, w, l.S_ids, l.S_dist);  // more than 96 candidates
       } else {
         ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
       }

@@ -111,6 +111,20 @@ def test_build_matches_oracle_reverse_cap(jasper, oracle_lib, integer):
     _compare(gg, og)
 
 
+def test_build_reverse_cap_byte_rows(jasper, oracle_lib):
+    """The hub case at dim 128 on integer rows (span under 255): the graph
+    keeps byte rows, so the reverse prune runs its byte mode, and the hub's
+    groups of more than 96 candidates take that mode's u8 wave prune."""
+    base = hub_mix(20000, 128, 6, scale=32.0, integer=True)
+    og = oracle.build(base, R=32, distance="l2", alpha=1.2)
+    assert og.max_batch == 400 and og.capped_groups >= 20
+    gg = _gpu_build(jasper, base, 32, "l2")
+    fmt = gg.row_format()
+    print(f"row format {fmt}, reverse groups cut at 256 + R: {og.capped_groups}")
+    assert fmt["byte_rows"]
+    _compare(gg, og)
+
+
 @pytest.mark.parametrize("gram8", ["0", "1"])
 def test_build_byte_and_half_gram_agree(jasper, oracle_lib, gram8, tmp_path):
     """Integer rows of span 207 build the same graph with the reverse prune's
