@@ -228,6 +228,12 @@ def main() -> int:
     ap.add_argument("--diskann-parts", default="8,4,16", help="shard counts of --path diskann (first = the line's value)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
+    ap.add_argument("--no-general-path", action="store_true",
+                    help="skip the child-process run with the integer-row shortcuts off (profiler runs)")
+    ap.add_argument("--nq-sweep", default="",
+                    help="comma-separated query counts: after the headline measurement, time the search "
+                         "kernel at the chosen beam width on that many queries of the same mixture "
+                         "(config.nq_sweep: kernel ms and QPS per count)")
     ap.add_argument("--int-exact", type=int, default=1, choices=[0, 1],
                     help="0: run with the integer-row shortcuts off (JASPER_INT_EXACT=0), the general "
                          "distance and prune paths; the default search run also measures this in a child "
@@ -402,7 +408,9 @@ def main() -> int:
                      "Cache hits as well as DRAM reads, so neither figure is a DRAM-only measurement",
         },
     }
-    if args.int_exact == 1 and args.path == "search":
+    if args.nq_sweep:
+        result["config"]["nq_sweep"] = nq_sweep(args, torch, g, datasets, dev, chosen, log)
+    if args.int_exact == 1 and args.path == "search" and not args.no_general_path:
         result["config"]["general_path"] = general_path_run(args, chosen, log)
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
@@ -479,6 +487,23 @@ def _timed(torch, fn, steps, warmup):
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
     ev_ms = float(np.median([a.elapsed_time(b) for a, b in evs]))
     return wall_ms, ev_ms, out
+
+
+def nq_sweep(args, torch, g, datasets, dev, bw, log) -> list:
+    """Kernel time of one search launch against the number of queries in it
+    (same graph, same beam width, queries of the same mixture from seed 1):
+    one wave per query, so the counts around the resident-wave limit show
+    whether a launch's last partial round of waves costs a full round."""
+    counts = [int(x) for x in args.nq_sweep.split(",") if x]
+    q_all = torch.from_numpy(datasets.clustered(max(counts), 128, 1)).to(dev)
+    out = []
+    for nq in counts:
+        q = q_all[:nq].contiguous()
+        _, ev_ms, _ = _timed(torch, lambda: g.search(q, k=10, beam_width=bw), 10, 2)
+        out.append({"nq": nq, "kernel_ms": ev_ms, "qps": nq / (ev_ms / 1000.0),
+                    "us_per_query": ev_ms * 1000.0 / nq})
+        log(f"nq={nq:6d} bw={bw}: {ev_ms:.3f} ms, {nq / (ev_ms / 1000.0):,.0f} QPS")
+    return out
 
 
 def _line(args, metric, value, unit, ms, dtype, config, roofline, higher=True):

@@ -292,10 +292,10 @@ __host__ __device__ __forceinline__ uint32_t pow2_ceil(uint32_t x) {
 
 // -------------------------------------------------------------- distances --
 // Quad layout: the 4 lanes of a quad evaluate one distance. For L2, quad
-// lane l owns the 16-byte chunks l, l+4, l+8, ... (distance.cuh:108-143) and
+// lane l owns the 16-byte chunks l, l+4, l+8, ... (distance.cuh:40-84) and
 // accumulates fma(d, d, acc), d = f32(a) - f32(b), over the 8 halves of each
 // chunk in order; the quad sum is (l0 + l2) + (l1 + l3). For IP, reference
-// lane l owns the elements l, l+4, l+8, ... (distance.cuh:155-167); chunks
+// lane l owns the elements l, l+4, l+8, ... (distance.cuh:94-106); chunks
 // are loaded as for L2 and every chunk is broadcast across the quad so that
 // lane l can accumulate its two elements of each chunk in element order.
 

@@ -176,7 +176,7 @@ def f2bf(x: float) -> int:
 
 
 def distance(a: np.ndarray, b: np.ndarray, distance: str = "l2", dim: int | None = None) -> float:
-    """Single distance between two fp16 vectors (reference distance.cuh:93-167)."""
+    """Single distance between two fp16 vectors (reference distance/distance.cuh:33-106)."""
     pa = as_padded_f16(np.asarray(a).reshape(1, -1))
     pb = as_padded_f16(np.asarray(b).reshape(1, -1))
     d = pa.shape[1] if dim is None else dim

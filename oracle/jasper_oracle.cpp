@@ -77,7 +77,7 @@ inline float bf2f(uint16_t b) {
   return f;
 }
 
-// Squared L2 distance, distance/distance.cuh:93-153 (l2_distance::compute)
+// Squared L2 distance, distance/distance.cuh:33-92 (l2_distance::compute)
 // with DATA_T = __half, TILE_SIZE = 4, loads_per_round = 2.
 // Lane l of the 4-lane tile owns the 16-byte chunks w = l + 4j + 8i, i.e. the
 // chunks congruent to l mod 4 in ascending order, and accumulates
@@ -101,7 +101,7 @@ float l2_dist(const uint16_t* a, const uint16_t* b, int dim) {
   return (lane[0] + lane[2]) + (lane[1] + lane[3]);
 }
 
-// Negated inner product, distance/distance.cuh:155-167. Lane l sums elements
+// Negated inner product, distance/distance.cuh:94-106. Lane l sums elements
 // i = l, l+4, ... (products of two halves are exact in fp32, so fma and
 // mul+add agree); same butterfly; negated.
 float ip_dist(const uint16_t* a, const uint16_t* b, int dim) {
