@@ -284,6 +284,9 @@ def main() -> int:
     log(f"build {args.n} vectors in {build_s:.2f}s ({args.n / build_s:.0f} vec/s), "
         f"batches={int(bst['batches'])} max_batch={int(bst['max_batch'])}")
 
+    build_total_ms = bst["total_ms"]
+    build_roof = build_roofline(jasper_amd, base_t, 64, build_s, build_total_ms, log)
+
     # ---- ground truth
     t0 = time.perf_counter()
     gt_ids, _ = jasper_amd.generate_groundtruth(base_t, q_t, k=10, distance="l2",
@@ -374,6 +377,7 @@ def main() -> int:
             "build_vectors_per_s": args.n / build_s,
             "build_s": build_s,
             "build_max_batch": int(bst["max_batch"]),
+            "build_roofline": build_roof,
             "storage": ("fp16 vectors; the search reads byte rows (value - lo) for integer rows spanning "
                         "<= 255 values, and queries in that range as bytes (exact u8 dot products, u32 sums)"
                         if fmt["byte_rows"] else "fp16 vectors, fp32 distance arithmetic"),
@@ -487,6 +491,77 @@ def _timed(torch, fn, steps, warmup):
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
     ev_ms = float(np.median([a.elapsed_time(b) for a, b in evs]))
     return wall_ms, ev_ms, out
+
+
+def build_algorithmic_bytes(w: dict, R: int, dp: int, row_bytes: int) -> dict:
+    """Bytes a Vamana build must move, per stage, from its work counters
+    (jasper_amd.last_build_work): every distinct vector a stage reads at the
+    bytes of the row format it reads (row_bytes), adjacency rows at 6 B per
+    edge (u32 id + bf16 distance) plus the 1-byte count, visited keys and
+    reverse pairs at 8 B.
+      search : per row its fp16 query row (2 dp), per pop the count byte, 4 B
+               per adjacency entry, row_bytes per distinct vector scored, 8 B
+               per popped key written;
+      forward: per row its count (read and write) and its R reverse-pair
+               slots (8 B each, written), its existing edges (6 B), its
+               visited keys (8 B), row_bytes per candidate row, 6 B per edge
+               written;
+      group  : the reverse pairs read and written once by the sort (16 B each)
+               and a 4-byte head per target;
+      reverse: per target its count (read and write), its own row and head,
+               its existing edges (6 B + the edge's row), its sources (the
+               8-byte pair + the source's row), 6 B per edge written."""
+    search = (w["search_rows"] * 2 * dp + w["search_hops"] + w["search_adjacency"] * 4
+              + w["search_scored"] * row_bytes + w["search_visited"] * 8)
+    forward = (w["forward_rows"] * (2 + 8 * R) + w["forward_existing"] * 6 + w["forward_visited"] * 8
+               + w["forward_candidates"] * row_bytes + w["forward_selected"] * 6)
+    group = w["forward_selected"] * 16 + w["reverse_targets"] * 4
+    reverse = (w["reverse_targets"] * (2 + row_bytes + 4) + w["reverse_existing"] * (6 + row_bytes)
+               + w["reverse_sources"] * (8 + row_bytes) + w["reverse_selected"] * 6)
+    return {"search": search, "forward": forward, "group": group, "reverse": reverse,
+            "total": search + forward + group + reverse}
+
+
+def build_roofline(jasper_amd, base_t, R, build_s, build_total_ms, log) -> dict:
+    """Roofline of the build: two more builds of the same rows (the same
+    graph), one with work counting (exact per-stage counts) and one with
+    per-stage HIP-event times; achieved = algorithmic bytes / time."""
+    import torch
+    n, dim = base_t.shape
+    dp = (dim + 7) // 8 * 8
+    jasper_amd.set_build_work_counting(True)
+    try:
+        g2 = jasper_amd.Graph.build(base_t, n_neighbors=R, distance="l2", alpha=1.2)
+        torch.cuda.synchronize()
+        w = jasper_amd.last_build_work()
+    finally:
+        jasper_amd.set_build_work_counting(False)
+    fmt = g2.row_format()
+    g2.free()
+    os.environ["JASPER_BUILD_TIMING"] = "1"
+    try:
+        g3 = jasper_amd.Graph.build(base_t, n_neighbors=R, distance="l2", alpha=1.2)
+        torch.cuda.synchronize()
+        st = jasper_amd.last_build_stats()
+    finally:
+        del os.environ["JASPER_BUILD_TIMING"]
+    g3.free()
+    row_b = dim if fmt["byte_rows"] else 2 * dp
+    b = build_algorithmic_bytes(w, R, dp, row_b)
+    stage_ms = {"search": st["search_ms"], "forward": st["prune_ms"], "group": st["group_ms"],
+                "reverse": st["reverse_ms"]}
+    stages = {k: {"bytes": b[k], "ms": stage_ms[k],
+                  "achieved_gbs": b[k] / (stage_ms[k] / 1e3) / 1e9 if stage_ms[k] > 0 else None,
+                  "frac": b[k] / (stage_ms[k] / 1e3) / 1e9 / PEAK_HBM_GBS if stage_ms[k] > 0 else None}
+              for k in stage_ms}
+    ach = b["total"] / (build_total_ms / 1e3) / 1e9
+    log(f"build roofline: {b['total'] / n / 1e3:.1f} KB per inserted vector, {b['total'] / 1e9:.2f} GB in "
+        f"{build_total_ms:.1f} ms of GPU time: {ach:.0f} GB/s ({ach / PEAK_HBM_GBS:.1%}); stages " +
+        ", ".join(f"{k} {v['ms']:.1f} ms {v['achieved_gbs'] or 0:.0f} GB/s" for k, v in stages.items()))
+    return {"bound": "hbm", "algorithmic_bytes": b["total"], "bytes_per_vector": b["total"] / n,
+            "row_bytes": row_b, "gpu_ms": build_total_ms, "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": ach / PEAK_HBM_GBS, "wall_achieved": b["total"] / build_s / 1e9, "stages": stages,
+            "work": w}
 
 
 def nq_sweep(args, torch, g, datasets, dev, bw, log) -> list:
@@ -736,6 +811,7 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
                              f"32768 samples, {nq} queries, k=10",
                  "build_vectors_per_s": n / build_s, "build_s": build_s, "lsh_s": lsh_s,
                  "build_max_batch": int(bst["max_batch"]),
+            "build_roofline": build_roof,
                  "exact_build_vectors_per_s": n / exact_build_s, "exact_build_s": exact_build_s,
                  "beam_width": bw, "unique": unique, "recall_at_10": rec, "target_recall": 0.9,
                  "curve": curve, "curve_rabitq_search": rq_curve, "curve_exact_search_rabitq_built": exact_rq,

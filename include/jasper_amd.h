@@ -134,6 +134,16 @@ const char* jasper_last_error(void);
  * plus batches and max batch size) when JASPER_BUILD_TIMING=1 was set. */
 int64_t jasperx_export_graph(int64_t handle, uint32_t* edges, uint16_t* edge_dist, uint8_t* counts);
 int64_t jasperx_last_build_stats(double* out7);
+/* Build work counting (measurement; no reference counterpart): while on != 0,
+ * constructions count their work and jasperx_last_build_work copies the 16
+ * counters of the last one: rows searched, search pops, adjacency entries,
+ * distinct vectors scored, visited keys written, forward-prune rows, their
+ * existing edges, visited keys read, candidate rows, edges written, reverse
+ * targets, their existing edges, reverse pairs read, edges written (the rest
+ * zero). The search stage then runs with an exact per-query seen bitmap
+ * (n bits per row of a batch; refused above 8 GiB); the graph is the same. */
+int64_t jasperx_build_work_counting(int64_t on);
+int64_t jasperx_last_build_work(uint64_t* out16);
 /* Measurement run of the plain search: same traversal with an exact
  * per-query seen set, writing per-query work counters to host memory
  * out_stats[n_queries * 4] = {hops, sum of degrees read, vectors scored,

@@ -84,6 +84,8 @@ _AGNOSTIC = {
     "jasper_get_dim": [_i64],
     "jasperx_export_graph": [_i64, _ptr, _ptr, _ptr],
     "jasperx_last_build_stats": [_ptr],
+    "jasperx_build_work_counting": [_i64],
+    "jasperx_last_build_work": [_ptr],
     "jasperx_prerotate_seed": [_i64],
     "jasperx_row_format": [_i64, _ptr],
     "jasperx_search_stats": [_i64, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr],
@@ -788,6 +790,24 @@ def last_build_stats() -> dict:
     _agnostic("jasperx_last_build_stats")(out.ctypes.data_as(_ptr))
     keys = ["search_ms", "prune_ms", "group_ms", "reverse_ms", "total_ms", "batches", "max_batch"]
     return dict(zip(keys, out.tolist()))
+
+
+BUILD_WORK_KEYS = ["search_rows", "search_hops", "search_adjacency", "search_scored", "search_visited",
+                   "forward_rows", "forward_existing", "forward_visited", "forward_candidates", "forward_selected",
+                   "reverse_targets", "reverse_existing", "reverse_sources", "reverse_selected"]
+
+
+def set_build_work_counting(on: bool) -> None:
+    """Count the work of the following constructions (measurement mode: the
+    search stage runs with an exact per-query seen bitmap; same graph)."""
+    _agnostic("jasperx_build_work_counting")(ctypes.c_int64(1 if on else 0))
+
+
+def last_build_work() -> dict:
+    """Work counters of the last construction made with counting on."""
+    out = np.zeros(16, dtype=np.uint64)
+    _agnostic("jasperx_last_build_work")(out.ctypes.data_as(_ptr))
+    return {k: int(v) for k, v in zip(BUILD_WORK_KEYS, out.tolist())}
 
 
 def last_scale_stats() -> dict:

@@ -72,7 +72,42 @@ struct PruneKernelArgs {
   uint32_t n_pairs;
   const uint32_t* heads;
   const uint32_t* n_heads;
+  // work counters (BuildWork indices) or null
+  unsigned long long* work;
 };
+
+static bool g_build_work = false;
+void set_build_work_counting(bool on) { g_build_work = on; }
+bool build_work_counting() { return g_build_work; }
+
+__device__ __forceinline__ void add_work(unsigned long long* w, int i, uint32_t v) {
+  if (v) atomicAdd(&w[i], (unsigned long long)v);
+}
+
+// Sums the search stage's per-query counters (hops, degrees, scored) and
+// visited counts of a batch into the work counters.
+__global__ __launch_bounds__(256) void search_work_kernel(const uint32_t* st, const uint32_t* vcounts, uint32_t nq,
+                                                          unsigned long long* work) {
+  unsigned long long h = 0, d = 0, s = 0, v = 0;
+  for (uint32_t q = blockIdx.x * 256 + threadIdx.x; q < nq; q += gridDim.x * 256) {
+    h += st[(size_t)q * 4 + 0];
+    d += st[(size_t)q * 4 + 1];
+    s += st[(size_t)q * 4 + 2];
+    v += vcounts[q];
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    h += __shfl_xor(h, o, 64);
+    d += __shfl_xor(d, o, 64);
+    s += __shfl_xor(s, o, 64);
+    v += __shfl_xor(v, o, 64);
+  }
+  if (lane_id() == 0) {
+    atomicAdd(&work[kWorkSearchHops], h);
+    atomicAdd(&work[kWorkSearchAdjacency], d);
+    atomicAdd(&work[kWorkSearchScored], s);
+    atomicAdd(&work[kWorkSearchVisited], v);
+  }
+}
 
 // The adjacency row of v as loaded: degree, and per lane one slot (lanes
 // past R read slot R - 1), issued together with no dependence on the degree.
@@ -126,6 +161,44 @@ __device__ __forceinline__ void sort_candidates(uint64_t* C, uint32_t nc) {
   lds_bitonic_sort(C, N);
 }
 
+// Sorts a reverse target's candidates: C[0, nE) its existing edges in slot
+// order (stored bf16 distances), C[nE, nE + taken) its new sources. A stored
+// row is the output of an earlier prune, so its keys are usually ascending
+// already (ties of the rounded distances can break the id order): they are
+// sorted only when a lane finds its predecessor larger, the few sources are
+// sorted apart, and the two lists meet in one bitonic merge (64 wide when
+// they fit, else 128 wide over two registers) in place of a full sort of
+// both. The keys are distinct or identical 64-bit values, so the result is
+// the full sort's.
+__device__ __forceinline__ void sort_reverse_candidates(uint64_t* C, uint32_t nE, uint32_t taken) {
+  const uint32_t nc = nE + taken;
+  if (nE > 64u || taken > 64u) {
+    sort_candidates(C, nc);
+    return;
+  }
+  const uint32_t lane = lane_id();
+  uint64_t e = lane < nE ? C[lane] : kEmptyKey;
+  uint64_t t = lane < taken ? C[nE + lane] : kEmptyKey;
+  const uint64_t prev = __shfl_up(e, 1, 64);
+  if (ballot(lane > 0u && lane < nE && e < prev)) e = wave_bitonic_sort<64>(e);
+  t = wave_sort_upto(t, taken);
+  wave_sync();  // every read of C precedes the writes below
+  // e ascending then the sources descending: a bitonic sequence of 128
+  const uint64_t tr = reverse_lanes64(t);
+  const bool lt = e < tr;
+  uint64_t x0 = lt ? e : tr;
+  if (nc <= 64u) {
+    x0 = bitonic_merge_steps<64, 32>(x0, lane);
+    C[lane] = x0;
+  } else {
+    uint64_t x1 = lt ? tr : e;
+    bitonic_stage128<128, 32>(x0, x1);
+    C[lane] = x0;
+    C[lane + 64] = x1;
+  }
+  wave_sync();
+}
+
 __device__ __forceinline__ void write_selection(const PruneKernelArgs& a, uint32_t v, uint32_t ns,
                                                 const uint32_t* S_ids, const float* S_dist) {
   const uint32_t lane = lane_id();
@@ -170,7 +243,11 @@ static float gram_margin_scale() {
 #define JASPER_GRAM_WAVES 2
 #endif
 #ifndef JASPER_GRAM8_WAVES
-#define JASPER_GRAM8_WAVES 3
+#define JASPER_GRAM8_WAVES 4
+#endif
+// The forward prune on byte rows takes the Gram form for up to 96 candidates.
+#ifndef JASPER_FWD_GRAM
+#define JASPER_FWD_GRAM 1
 #endif
 
 static size_t prune_lds_bytes() { return kCandBuf * 8 + 64 * 4 + 64 * 4 + kCandBuf * 4; }
@@ -183,7 +260,8 @@ static_assert(kGramLdsWords <= kCandBuf, "the Gram prune's scratch reuses the so
 // BYTES: the graph keeps byte rows (CPL 4, L2, integer rows): the prune
 // works on them (robust_prune_wave_u8)
 template <int CPL, int METRIC, bool INTX, bool SCALE, bool BYTES = false>
-__global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
+__global__ __launch_bounds__(64, (BYTES && !SCALE && JASPER_FWD_GRAM ? JASPER_GRAM8_WAVES : 1)) void
+forward_prune_kernel(PruneKernelArgs a) {
   static_assert(!BYTES || (CPL == 4 && METRIC == kL2 && INTX), "byte rows: integer L2 rows of 112/128");
   extern __shared__ uint64_t smem[];
   const PruneLds l = carve_prune_lds(smem, a.pc.R);
@@ -195,6 +273,7 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   const ExistingRow er = load_existing(a, v);
   const uint32_t nv = a.visited_counts[bid];
   uint32_t nc = append_existing(er, R, l.C);
+  const uint32_t n_existing = nc;
   for (uint32_t base = 0; base < nv; base += 64) {
     const uint32_t i = base + lane;
     bool ok = i < nv;
@@ -210,9 +289,28 @@ __global__ __launch_bounds__(64) void forward_prune_kernel(PruneKernelArgs a) {
   wave_sync();
   sort_candidates(l.C, nc);
   uint32_t ns;
-  if constexpr (BYTES) ns = robust_prune_wave_u8<SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
-  else ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  if constexpr (BYTES && !SCALE && JASPER_FWD_GRAM) {
+    // up to 96 candidates: the byte-row Gram prune (all candidate rows read
+    // at once, pair distances on the matrix cores); longer lists the wave prune
+    float* gn = reinterpret_cast<float*>(l.srcs);
+    if (nc <= 32 && a.pc.alpha >= 0.0f) ns = robust_prune_gram<1, 2>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+    else if (nc <= 64 && a.pc.alpha >= 0.0f) ns = robust_prune_gram<2, 2>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+    else if (nc <= kGramMaxCands && a.pc.alpha >= 0.0f)
+      ns = robust_prune_gram<3, 2>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+    else ns = robust_prune_wave_u8<SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  } else if constexpr (BYTES) {
+    ns = robust_prune_wave_u8<SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  } else {
+    ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  }
   write_selection(a, v, ns, l.S_ids, l.S_dist);
+  if (a.work && lane == 0) {
+    add_work(a.work, kWorkForwardRows, 1u);
+    add_work(a.work, kWorkForwardExisting, n_existing);
+    add_work(a.work, kWorkForwardVisited, nv);
+    add_work(a.work, kWorkForwardCandidates, nc);
+    add_work(a.work, kWorkForwardSelected, ns);
+  }
   if (lane < R) {
     const uint32_t t = lane < ns ? l.S_ids[lane] : 0u;
     const bool pair = lane < ns && (!SCALE || t - a.pc.r2_lo < a.pc.r2_n);
@@ -345,7 +443,7 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
     }
     wave_sync();
     const uint32_t nc = nE + taken;
-    sort_candidates(l.C, nc);
+    sort_reverse_candidates(l.C, nE, taken);
     uint32_t ns;
     if constexpr (SCALE) {
       if constexpr (CPL == 4 && METRIC == kL2 && INTX) {
@@ -358,7 +456,8 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
       // up to 96 candidates of rows of up to 128 values: pair distances on
       // the matrix cores, exact for integer rows, proved otherwise
       const uint32_t climit = METRIC == kL2 ? a.pc.nlimit : (a.pc.nlimit + 7u) / 8u;
-      if (nc <= kGramMaxCands && climit <= kGramMaxChunks) {
+      // (the integer Gram prune's thresholds need alpha >= 0)
+      if (nc <= kGramMaxCands && climit <= kGramMaxChunks && (!INTX || a.pc.alpha >= 0.0f)) {
         float* gn = reinterpret_cast<float*>(l.srcs);
         if constexpr (INTX) {
           if (nc <= 32) ns = robust_prune_gram<1, I8>(a.pc, l.C, nc, w, l.S_ids, l.S_dist, gn);
@@ -378,6 +477,12 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
       ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
     }
     write_selection(a, w, ns, l.S_ids, l.S_dist);
+    if (a.work && lane == 0) {
+      add_work(a.work, kWorkReverseTargets, 1u);
+      add_work(a.work, kWorkReverseExisting, nE);
+      add_work(a.work, kWorkReverseSources, taken);
+      add_work(a.work, kWorkReverseSelected, ns);
+    }
     wave_sync();
     start = start_next;
     w = w_next;
@@ -644,6 +749,30 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
 
   BuildStats st;
   st.max_batch = mb;
+  // work counting: counters, the search stage's per-query counters and its
+  // exact seen bitmap (freed when the build returns or throws)
+  struct WorkBuffers {
+    unsigned long long* work = nullptr;
+    uint32_t* qstats = nullptr;
+    uint32_t* seen = nullptr;
+    ~WorkBuffers() {
+      (void)hipFree(work);
+      (void)hipFree(qstats);
+      (void)hipFree(seen);
+    }
+  } wb;
+  const size_t seen_words = (size_t)((g.n + 31) / 32);
+  if (g_build_work) {
+    const size_t seen_bytes = (size_t)mb * seen_words * 4;
+    if (seen_bytes > ((size_t)8 << 30))
+      throw std::invalid_argument("build work counting needs " + std::to_string(seen_bytes >> 20) +
+                                  " MiB of seen bitmap (limit 8 GiB): count a smaller build");
+    hip_check(hipMalloc(&wb.work, kWorkCount * 8), "alloc build work counters");
+    hip_check(hipMemsetAsync(wb.work, 0, kWorkCount * 8, stream), "clear build work counters");
+    hip_check(hipMalloc(&wb.qstats, (size_t)mb * 16), "alloc search counters");
+    hip_check(hipMalloc(&wb.seen, std::max<size_t>(seen_bytes, 4)), "alloc seen bitmap");
+    pa.work = wb.work;
+  }
   EventTimer timer(time_stages, stream);
   hipEvent_t t0, t1;
   hip_check(hipEventCreate(&t0), "event");
@@ -669,6 +798,11 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       // the queries' seen-cache size (at 100M vectors the 8 KB 16-bit form
       // took the search stage from 11.4 s to 10.6 s)
       r.hash_bits = seen_cache_hash_bits(g.n);
+      if (wb.work && !rabitq_search) {
+        hip_check(hipMemsetAsync(wb.seen, 0, (size_t)bs * seen_words * 4, stream), "clear seen bitmap");
+        r.stats = wb.qstats;
+        r.seen_bits = wb.seen;
+      }
       timer.start();
       if (rabitq_search)
         rabitq_build_search(g, (uint32_t)count, (uint32_t)bs, kBuildL, kBuildLimit, kBuildMaxResult, ws.visited,
@@ -676,6 +810,15 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       else
         launch_beam_search(g, r, stream);
       timer.stop(st.search_ms);
+      if (wb.work) {
+        st.work[kWorkSearchQueries] += (uint64_t)bs;
+        if (!rabitq_search) {
+          const uint32_t blocks = (uint32_t)std::min<int64_t>((bs + 255) / 256, 1024);
+          hipLaunchKernelGGL(search_work_kernel, dim3(blocks), dim3(256), 0, stream, wb.qstats, ws.vcounts,
+                             (uint32_t)bs, wb.work);
+          hip_check(hipGetLastError(), "launch search_work_kernel");
+        }
+      }
       // 2. forward merge + prune + reverse pairs
       pa.batch_offset = (uint32_t)count;
       timer.start();
@@ -696,6 +839,12 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
     float total = 0;
     hip_check(hipEventElapsedTime(&total, t0, t1), "event elapsed");
     st.total_ms = total;
+    if (wb.work) {
+      uint64_t w[kWorkCount];
+      hip_check(hipMemcpy(w, wb.work, sizeof(w), hipMemcpyDeviceToHost), "read build work counters");
+      for (int i = 0; i < kWorkCount; ++i)
+        if (i != kWorkSearchQueries) st.work[i] = w[i];
+    }
   } catch (...) {
     (void)hipStreamSynchronize(stream);
     (void)hipEventDestroy(t0);

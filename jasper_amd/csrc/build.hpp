@@ -11,11 +11,40 @@
 
 namespace jasper_amd {
 
+// Work counters of one build (filled only while work counting is on, see
+// set_build_work_counting), indices of BuildStats::work:
+enum BuildWork : int {
+  kWorkSearchQueries = 0,   // rows searched by the search stage
+  kWorkSearchHops,          // pops (one adjacency row each)
+  kWorkSearchAdjacency,     // adjacency entries read (sum of degrees)
+  kWorkSearchScored,        // distinct vectors scored, per query
+  kWorkSearchVisited,       // popped keys written to the visited list
+  kWorkForwardRows,         // vertices through the forward prune
+  kWorkForwardExisting,     // existing edges read (ids + bf16 distances)
+  kWorkForwardVisited,      // visited keys read
+  kWorkForwardCandidates,   // candidate rows the prune reads (existing + visited, self excluded)
+  kWorkForwardSelected,     // edges written (= reverse pairs)
+  kWorkReverseTargets,      // targets through the reverse prune
+  kWorkReverseExisting,     // their existing edges read
+  kWorkReverseSources,      // reverse pairs read (sources taken)
+  kWorkReverseSelected,     // edges written
+  kWorkCount = 16
+};
+
 struct BuildStats {
   double search_ms = 0, prune_ms = 0, sort_ms = 0, reverse_ms = 0, total_ms = 0;
   int64_t batches = 0;
   int64_t max_batch = 0;
+  uint64_t work[kWorkCount] = {};
 };
+
+// While on, builds count their work (BuildStats::work): the search stage
+// runs the plain search's exact-counter instance (a per-query seen bitmap of
+// n bits, so this mode is for measurement at moderate n; it refuses more than
+// 8 GiB of bitmap) and the prune kernels add their counts. The graph built is
+// the same. Process-wide; not for concurrent builds.
+void set_build_work_counting(bool on);
+bool build_work_counting();
 
 // Maximum batch size of the reference for a workspace budget
 // (graph_construct_workspace::max_batch_size_for_budget, index/construct.cuh:

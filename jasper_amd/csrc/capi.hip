@@ -188,11 +188,11 @@ std::unique_ptr<Graph> construct(const Config& cfg, const void* vectors, int64_t
     g_last_build = st;
   }
   if (time_stages) {
-    std::printf("[construct] n=%lld batches=%lld max_batch=%lld search=%.1fms prune=%.1fms group=%.1fms "
+    std::fprintf(stderr, "[construct] n=%lld batches=%lld max_batch=%lld search=%.1fms prune=%.1fms group=%.1fms "
                 "reverse=%.1fms total=%.1fms\n",
                 (long long)n, (long long)st.batches, (long long)st.max_batch, st.search_ms, st.prune_ms, st.sort_ms,
                 st.reverse_ms, st.total_ms);
-    std::fflush(stdout);
+    std::fflush(stderr);
   }
   return g;
 }
@@ -806,6 +806,21 @@ extern "C" int64_t jasperx_last_build_stats(double* out7) {
     const double v[7] = {s.search_ms, s.prune_ms, s.sort_ms, s.reverse_ms, s.total_ms, (double)s.batches,
                          (double)s.max_batch};
     std::memcpy(out7, v, sizeof(v));
+    return 0;
+  });
+}
+
+extern "C" int64_t jasperx_build_work_counting(int64_t on) {
+  return guarded([&]() -> int64_t {
+    set_build_work_counting(on != 0);
+    return 0;
+  });
+}
+
+extern "C" int64_t jasperx_last_build_work(uint64_t* out16) {
+  return guarded([&]() -> int64_t {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    std::memcpy(out16, g_last_build.work, sizeof(g_last_build.work));
     return 0;
   });
 }

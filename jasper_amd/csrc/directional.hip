@@ -1423,11 +1423,11 @@ std::unique_ptr<Graph> construct_directional(uint32_t R, int metric, uint32_t k_
   if (rq_search) build_rabitq(*g);  // codes of the stored (prerotated) rows, before any edge exists
   build_graph(*g, (float)alpha, mbs, stream, time_stages, st, rq_search);
   if (time_stages) {
-    std::printf("[construct] n=%lld batches=%lld max_batch=%lld search=%.1fms prune=%.1fms group=%.1fms "
+    std::fprintf(stderr, "[construct] n=%lld batches=%lld max_batch=%lld search=%.1fms prune=%.1fms group=%.1fms "
                 "reverse=%.1fms total=%.1fms\n",
                 (long long)n, (long long)st->batches, (long long)st->max_batch, st->search_ms, st->prune_ms,
                 st->sort_ms, st->reverse_ms, st->total_ms);
-    std::fflush(stdout);
+    std::fflush(stderr);
   }
   g->next_id = (uint64_t)n;
   return g;

@@ -304,6 +304,21 @@ __device__ __forceinline__ uint32_t spread_nibbles(uint32_t w) {
   return (w & 0xFu) | ((w & 0xF0u) << 4) | ((w & 0xF00u) << 8) | ((w & 0xF000u) << 12);
 }
 
+// The prune test d * alpha < cd (fp32) on an exact integer distance d is
+// d < T for one integer T per candidate: fl(d * alpha) is non-decreasing in
+// d for alpha >= 0, so the passing d form a prefix. T is the smallest d >= 0
+// that fails (found from cd / alpha and stepped to the boundary), or 2^30
+// when every d below it passes. Callers route alpha < 0 and NaN elsewhere.
+__device__ __forceinline__ int prune_int_threshold(float cd, float alpha) {
+  if (!(cd > 0.0f)) return 0;            // 0 * alpha < cd fails, and so does every d
+  if (!(alpha > 0.0f)) return 1 << 30;   // alpha == 0: every d passes
+  const float q = cd / alpha;
+  int d = q >= 1073741824.0f ? (1 << 30) : (int)q;
+  while (d < (1 << 30) && (float)d * alpha < cd) ++d;
+  while (d > 0 && !((float)(d - 1) * alpha < cd)) --d;
+  return d;
+}
+
 // I8: rows whose values span at most 255 (int8_rows) as bytes v - 128,
 // v = x - lo in [0, 255], on v_mfma_i32_32x32x32_i8: half the operand
 // registers of the fp16 form and half its MFMA steps. The Gram form's pair
@@ -319,12 +334,14 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   constexpr int KS = I8 ? kGramMaxChunks / 4 : kGramMaxChunks / 2;
   const uint32_t lane = lane_id();
   const uint32_t r = lane & 31u, h = lane >> 5;
-  float* gcd = gn + kGramMaxCands;
+  // per candidate i: U_i = T_i - |a_i|^2 (prune_int_threshold), so that
+  // "j prunes i" is |a_j|^2 - 2 a_i.a_j < U_i in exact integers
+  int* gu = reinterpret_cast<int*>(gn);
 
   // MFMA operand of tile t, step s for candidate 32t + r, shifted; chunks
   // past the summed length are zero
   uint4 fr[T][KS];
-  float nrm[T];
+  int nrm[T];
   if constexpr (I8 == 2) {
     // the byte rows already hold v = x - lo: one 16-byte load per step
 #pragma unroll
@@ -339,7 +356,6 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         const uint32_t c = 2u * (uint32_t)s + h;  // fp16 chunks 2c and 2c + 1
         raw[s] = row8[min(c, p.nb8 - 1u)];
       }
-      if (h == 0) gcd[i] = key_dist(key);
       int acc = 0;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -352,9 +368,8 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
       }
-      const int tot = acc + __shfl_xor(acc, 32, 64);
-      nrm[t] = (float)tot;  // exact: below 2^24
-      if (h == 0) gn[i] = nrm[t];
+      nrm[t] = acc + __shfl_xor(acc, 32, 64);  // below 2^24
+      if (h == 0) gu[i] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
     }
   } else if constexpr (I8 == 1) {
 #pragma unroll
@@ -370,7 +385,6 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         raw[2 * s] = row[min(c, p.nchunks - 1u)];
         raw[2 * s + 1] = row[min(c + 1u, p.nchunks - 1u)];
       }
-      if (h == 0) gcd[i] = key_dist(key);
       int acc = 0;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -392,9 +406,8 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
       }
-      const int tot = acc + __shfl_xor(acc, 32, 64);
-      nrm[t] = (float)tot;  // exact: below 2^24
-      if (h == 0) gn[i] = nrm[t];
+      nrm[t] = acc + __shfl_xor(acc, 32, 64);  // below 2^24
+      if (h == 0) gu[i] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
     }
   } else {
 #pragma unroll
@@ -408,7 +421,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         const uint32_t c = 2u * (uint32_t)s + h;
         fr[t][s] = row[min(c, p.nchunks - 1u)];
       }
-      if (h == 0) gcd[i] = key_dist(key);
+      if (h == 0) gu[i] = prune_int_threshold(key_dist(key), p.alpha);
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -428,11 +441,19 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         acc = dot2_sqdiff(x.z, 0u, acc);
         acc = dot2_sqdiff(x.w, 0u, acc);
       }
-      nrm[t] = acc + xor_lane_f<32>(acc);  // exact: integers below 2^24
-      if (h == 0) gn[32u * (uint32_t)t + r] = nrm[t];
+      nrm[t] = (int)(acc + xor_lane_f<32>(acc));  // exact: integers below 2^24
     }
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (h == 0) gu[32u * (uint32_t)t + r] -= nrm[t];
   }
   wave_sync();
+  // rows 8g + 4h + q of a diagonal block that follow this lane's column r
+  uint32_t diagm = 0u;
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    if (r < (uint32_t)(8 * (e >> 2) + 4 * (int)h + (e & 3))) diagm |= 1u << e;
 
   // W[t][t2], lane (r, h): bit b set when candidate 32 t + b is pruned by
   // candidate 32 t2 + r (which precedes it): the column of the pair block
@@ -446,39 +467,35 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   for (int t = 0; t < T; ++t) {
 #pragma unroll
     for (int t2 = 0; t2 <= t; ++t2) {
-      gram_f16 acc;
+      gram_i16 ai;
       if constexpr (I8 != 0) {
-        gram_i16 ai = {};
+        ai = gram_i16{};
 #pragma unroll
         for (int s = 0; s < KS; ++s)
           ai = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_gram_i4(fr[t][s]), as_gram_i4(fr[t2][s]), ai, 0, 0, 0);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] = (float)ai[e];  // exact: |a_i . a_j| < 2^24
       } else {
-        acc = gram_f16{};
+        gram_f16 acc = gram_f16{};
 #pragma unroll
         for (int s = 0; s < KS; ++s)
           acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_gram_h8(fr[t][s]), as_gram_h8(fr[t2][s]), acc, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ai[e] = (int)acc[e];  // exact: |a_i . a_j| < 2^24
       }
       // lane holds column j = 32 t2 + r (whose norm it holds) and rows
-      // 32 t + 8g + 4h + q
-      const float nj = nrm[t2];
+      // 32 t + 8g + 4h + q; bit 4g + q: j prunes that row, built from the
+      // top bit down
+      const int nj = nrm[t2];
       uint32_t w16 = 0u;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 ni = *reinterpret_cast<const float4*>(gn + 32 * t + 8 * g + 4 * h);
-        const float4 cd = *reinterpret_cast<const float4*>(gcd + 32 * t + 8 * g + 4 * h);
+      for (int g = 3; g >= 0; --g) {
+        const int4 u = *reinterpret_cast<const int4*>(gu + 32 * t + 8 * g + 4 * h);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float gij = acc[4 * g + q];
-          const float niq = q == 0 ? ni.x : q == 1 ? ni.y : q == 2 ? ni.z : ni.w;
-          const float cdq = q == 0 ? cd.x : q == 1 ? cd.y : q == 2 ? cd.z : cd.w;
-          const float d = (niq - gij) + (nj - gij);
-          bool bit = d * p.alpha < cdq;
-          if (t == t2) bit = bit && r < (uint32_t)(8 * g + 4 * (int)h + q);
-          w16 |= bit ? (1u << (4 * g + q)) : 0u;
+        for (int q = 3; q >= 0; --q) {
+          const int uq = q == 0 ? u.x : q == 1 ? u.y : q == 2 ? u.z : u.w;
+          w16 = (w16 << 1) | (nj - 2 * ai[4 * g + q] < uq ? 1u : 0u);
         }
       }
+      if (t == t2) w16 &= diagm;
       const uint32_t w = spread_nibbles(w16) << (4u * h);  // rows 8g + 4h + q
       W[t][t2] = w | xor_lane<32>(w);
       __builtin_amdgcn_sched_barrier(0);

@@ -55,6 +55,10 @@ def lib():
         _lib = ctypes.CDLL(str(_LIB_PATH))
         P = ctypes.c_void_p
         i32, i64, f32, u64 = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint64
+        _lib.jo_build_work.restype = None
+        _lib.jo_build_work.argtypes = [i32]
+        _lib.jo_last_build_work.restype = None
+        _lib.jo_last_build_work.argtypes = [P]
         _lib.jo_l2.restype = f32
         _lib.jo_l2.argtypes = [P, P, i32]
         _lib.jo_ip.restype = f32
@@ -227,12 +231,22 @@ def max_batch_size(n: int, R: int, budget_bytes: int = 10 ** 10) -> int:
     return int(lib().jo_max_batch_size(n, R, budget_bytes))
 
 
+BUILD_WORK_KEYS = ["search_rows", "search_hops", "search_adjacency", "search_scored", "search_visited",
+                   "forward_rows", "forward_existing", "forward_visited", "forward_candidates", "forward_selected",
+                   "reverse_targets", "reverse_existing", "reverse_sources", "reverse_selected"]
+
+
 def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
           workspace_budget: int = 10 ** 10, max_batch: int | None = None,
-          nthreads: int = 0, rq: "RqArtifacts | None" = None) -> OracleGraph:
+          nthreads: int = 0, rq: "RqArtifacts | None" = None, count_work: bool = False) -> OracleGraph:
     """Vamana construction, reference index/construct.cuh:992-1160. With rq
     (this build's extension) the search stage pops by the RaBitQ estimate of
-    those codes (rabitq_build_search) instead of the plain search."""
+    those codes (rabitq_build_search) instead of the plain search.
+    count_work: also count the build's work (g.work, a dict keyed by
+    BUILD_WORK_KEYS: rows searched, pops, adjacency entries, distinct vectors
+    scored and popped keys of the search stage; the forward and reverse
+    prunes' rows, existing edges, visited keys / sources, candidates and
+    edges written)."""
     vecs16 = as_padded_f16(vectors)
     n, dp = vecs16.shape
     dim = np.asarray(vectors).shape[1]
@@ -242,6 +256,7 @@ def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
     edist = np.empty((n, R), dtype=np.uint16)
     counts = np.empty(n, dtype=np.uint8)
     nb = ctypes.c_int64(0)
+    lib().jo_build_work(1 if count_work else 0)
     if rq is None:
         rc = lib().jo_build(_ptr(vecs16), n, dp, dim, R, metric_code(distance), ctypes.c_float(alpha),
                             int(max_batch), _ptr(edges), _ptr(edist), _ptr(counts), nthreads,
@@ -255,6 +270,11 @@ def build(vectors, R: int = 32, distance: str = "l2", alpha: float = 1.2,
     g = OracleGraph(vecs16, edges, edist, counts, R, dim, distance)
     g.n_batches = nb.value
     g.max_batch = max_batch
+    if count_work:
+        w = np.zeros(16, dtype=np.uint64)
+        lib().jo_last_build_work(_ptr(w))
+        lib().jo_build_work(0)
+        g.work = {k: int(v) for k, v in zip(BUILD_WORK_KEYS, w.tolist())}
     # reverse-step groups cut at the 256 + R candidate cap (test counter)
     g.capped_groups = int(lib().jo_last_capped_groups())
     return g

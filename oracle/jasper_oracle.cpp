@@ -370,6 +370,16 @@ namespace {
 // test counter, so tests can show the cap was exercised).
 std::atomic<int64_t> g_capped_groups{0};
 
+// Work counters of the last build's process_batches while jo_build_work is
+// on (the device build's BuildWork indices): rows searched, pops, adjacency
+// entries, distinct vectors scored, popped keys recorded; forward rows,
+// existing edges, visited keys, candidates, edges written; reverse targets,
+// existing edges, sources taken, edges written. Test infrastructure: the
+// device counts of the same build must equal these.
+std::atomic<bool> g_count_work{false};
+std::atomic<uint64_t> g_work[16];
+
+
 void reverse_step(const Graph& g, int dim_for_prune, float alpha, const std::vector<uint64_t>& pairs,
                   uint32_t* edges, uint16_t* edge_dist, uint8_t* counts) {
   const int R = g.R, max_cands = 256 + R;
@@ -391,6 +401,7 @@ void reverse_step(const Graph& g, int dim_for_prune, float alpha, const std::vec
         if (x == kInvalid32) continue;
         C.push_back({x, bf2f(edge_dist[(size_t)w * R + e])});
       }
+      const size_t n_existing = C.size();
       const uint16_t* wv = g.vecs + (size_t)w * g.dp;
       for (size_t p = heads[(size_t)h]; p < heads[(size_t)h + 1]; ++p) {
         if ((int)C.size() >= max_cands) {
@@ -401,8 +412,15 @@ void reverse_step(const Graph& g, int dim_for_prune, float alpha, const std::vec
         if (v == kInvalid32 || v == w) continue;
         C.push_back({v, dist(g.metric, wv, g.vecs + (size_t)v * g.dp, dim_for_prune)});
       }
+      const size_t n_cands = C.size();
       std::sort(C.begin(), C.end(), cand_less);
       const int ns = robust_prune(g, dim_for_prune, w, C, alpha, R, sel.data());
+      if (g_count_work.load()) {
+        g_work[10] += 1;
+        g_work[11] += n_existing;
+        g_work[12] += n_cands - n_existing;
+        g_work[13] += (uint64_t)ns;
+      }
       for (int j = 0; j < ns; ++j) {
         edges[(size_t)w * R + j] = sel[(size_t)j].id;
         edge_dist[(size_t)w * R + j] = f2bf(sel[(size_t)j].dist);
@@ -442,10 +460,22 @@ int64_t process_batches(const Graph& g, int dim_for_prune, float alpha, int64_t 
     bs = std::min<int64_t>(bs, max_batch);
     const int64_t s = count;
     visited.assign((size_t)bs, {});
+    const bool cw = g_count_work.load();
+    if (cw) g_work[0] += (uint64_t)bs;
     // (i) beam search of every batch vector against the pre-batch graph
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t i = 0; i < bs; ++i) {
-      if (rqb) {
+      if (cw && !rqb) {
+        SearchStats st;
+        std::vector<uint32_t> seen;
+        search_one(g, vecs + (size_t)(s + i) * dp, medoid, (uint32_t)L, (uint32_t)LIMIT,
+                   (uint32_t)MAX_RESULT, true, &visited[(size_t)i], &st, &seen);
+        std::sort(seen.begin(), seen.end());
+        g_work[1] += st.hops;
+        g_work[2] += st.edges_read;
+        g_work[3] += (uint64_t)(std::unique(seen.begin(), seen.end()) - seen.begin());
+        g_work[4] += visited[(size_t)i].size();
+      } else if (rqb) {
         // the RaBitQ build search (directional_oracle.cpp, jo_rq_visit)
         uint32_t ids[MAX_RESULT];
         float ds[MAX_RESULT];
@@ -471,11 +501,19 @@ int64_t process_batches(const Graph& g, int dim_for_prune, float alpha, int64_t 
           if (w == kInvalid32) continue;
           C.push_back({w, bf2f(edge_dist[(size_t)v * R + e])});
         }
+        const size_t n_existing = C.size();
         for (const Entry& x : visited[(size_t)i])
           if (x.id != v && x.id != kInvalid32) C.push_back({x.id, x.dist});
         if ((int)C.size() > max_cands) C.resize((size_t)max_cands);
         std::sort(C.begin(), C.end(), cand_less);
         const int ns = robust_prune(g, dim_for_prune, v, C, alpha, R, sel.data());
+        if (cw) {
+          g_work[5] += 1;
+          g_work[6] += n_existing;
+          g_work[7] += visited[(size_t)i].size();
+          g_work[8] += C.size();
+          g_work[9] += (uint64_t)ns;
+        }
         for (int j = 0; j < ns; ++j) {
           edges[(size_t)v * R + j] = sel[(size_t)j].id;
           edge_dist[(size_t)v * R + j] = f2bf(sel[(size_t)j].dist);
@@ -519,6 +557,18 @@ int jo_build(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R, 
 }
 
 int64_t jo_last_capped_groups() { return g_capped_groups.load(); }
+
+// Work counting of the following builds (see g_work): on != 0 clears the
+// counters and turns counting on, 0 turns it off.
+void jo_build_work(int on) {
+  if (on)
+    for (auto& w : g_work) w.store(0);
+  g_count_work.store(on != 0);
+}
+
+void jo_last_build_work(uint64_t* out16) {
+  for (int i = 0; i < 16; ++i) out16[i] = g_work[i].load();
+}
 
 // jo_build with the RaBitQ build search (rabitq_build_search): the search
 // stage pops by the RaBitQ estimate of the given codes (nodes [n,

@@ -271,3 +271,30 @@ def test_build_rabitq_search_matches_oracle(jasper, oracle_lib, distance, dim, n
     og = oracle.build(rows, R=32, distance=distance, alpha=1.2, rq=oracle.RqArtifacts(dim, nodes, cent))
     _compare(g, og)
     g.free()
+
+
+@pytest.mark.parametrize("kind", ["integer", "gaussian"])
+def test_build_work_counters_match_oracle(jasper, oracle_lib, kind):
+    """Work counting (the build roofline's byte counts): the device build in
+    counting mode makes the same graph, and its counters (search pops,
+    adjacency entries, distinct vectors scored, popped keys; forward and
+    reverse prune rows, existing edges, candidates, sources, edges written)
+    equal the oracle's counts of the same build. Integer rows take the byte
+    prunes, Gaussian rows the fp16 ones."""
+    base = integer_clustered(3000, 128, 31) if kind == "integer" else gaussian(2500, 128, 32)
+    og = oracle.build(base, R=32, distance="l2", alpha=1.2, count_work=True)
+    jasper.set_build_work_counting(True)
+    try:
+        gg = _gpu_build(jasper, base, 32, "l2")
+        work = jasper.last_build_work()
+    finally:
+        jasper.set_build_work_counting(False)
+    _compare(gg, og)
+    assert work == og.work, {k: (work[k], og.work[k]) for k in work if work[k] != og.work[k]}
+    assert work["search_rows"] == work["forward_rows"] == len(base)
+    assert work["reverse_sources"] == work["forward_selected"]
+    gg.free()
+    g2 = _gpu_build(jasper, base, 32, "l2")
+    assert not any(jasper.last_build_work().values())  # counting off: nothing counted
+    _compare(g2, og)
+    g2.free()
