@@ -949,11 +949,16 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   float fdr = FLT_MAX;     // F's distances and ids in registers when k <= 64
   uint32_t fir = kInv31;
   uint32_t hint = 0;  // every entry of B before `hint` is visited
+  // degree of the predicted next pop (the next unvisited entry of B after
+  // the pop), read one hop ahead: when the pop matches, the adjacency and
+  // estimator rows are read only up to the degree
+  uint32_t spec_u = kInvalid32, spec_c = 0;
   lds_wave_sync();
   while (loop <= a.limit) {
     loop += 1;
     int p = -1;
     uint64_t pk = 0;
+    uint32_t next_u = kInvalid32;
     for (uint32_t base = hint; base < cnt; base += 64) {
       const uint32_t i = base + lane;
       const uint64_t bv = i < cnt ? B[i] : 1ull;
@@ -962,9 +967,12 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
         const int l = __builtin_ctzll(m);
         p = (int)base + l;
         pk = readlane64(bv, l);
+        const uint64_t m2 = m & (m - 1u);
+        if (m2) next_u = key_id(readlane64(bv, __builtin_ctzll(m2)));
         break;
       }
     }
+    next_u = uniform(next_u);
     if (p < 0) break;
     lds_wave_sync();
     if (lane == 0) B[p] = pk | 1ull;
@@ -1002,9 +1010,14 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     const bool short_row = nchunks <= 128 && !(RQ && a.visited);
     uint4 ureg[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
     // adjacency slot `lane` (slots past R read slot R - 1 and are never used:
-    // only lanes below the degree are)
-    const uint32_t el = min(lane, a.R - 1u);
-    const uint32_t deg_raw = a.counts[u];
+    // only lanes below the degree are); with the degree read ahead, slots
+    // past it read the last live one, so only the lines the degree covers
+    // are fetched
+    const bool known = u == spec_u;
+    const uint32_t el = known ? min(lane, max(min(spec_c, a.R), 1u) - 1u) : min(lane, a.R - 1u);
+    const uint32_t deg_raw = known ? spec_c : (uint32_t)a.counts[u];
+    spec_u = next_u;
+    spec_c = next_u != kInvalid32 ? (uint32_t)a.counts[next_u] : 0u;
     const uint32_t* erow = a.edges + (size_t)u * a.R;
     const uint32_t v_raw = erow[el];
     uint32_t wl[KW];

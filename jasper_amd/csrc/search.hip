@@ -252,6 +252,86 @@ constexpr int search_waves_per_simd() {
                : CPL == 0 ? 4 : (CPL <= 4 && METRIC == kL2) ? JASPER_SEARCH_WAVES_L2 : 1;
 }
 
+// Merge of the sorted new keys t (nt of them, one per lane) into B held one
+// key per lane (b, cnt entries, bw <= 64): B ascending against the new keys
+// reversed, the lane-wise minima are a bitonic sequence holding the 64
+// smallest keys, sorted by six more stages. Equal ranks (a re-scored member
+// of B, an id scored twice) sit side by side in the merged order, or across
+// its 64th key: then nothing changes and false is returned (the general
+// path takes the hop).
+__device__ __forceinline__ bool merge_regs(uint64_t& b, uint64_t t, uint32_t nt, uint32_t& cnt, uint32_t bw,
+                                           uint32_t lane) {
+  const uint64_t tr = reverse_lanes64(t);
+  const bool lt = b < tr;
+  uint64_t x0 = lt ? b : tr;
+  const uint64_t x1 = lt ? tr : b;
+  x0 = bitonic_merge_steps<64, 32>(x0, lane);
+  const uint64_t nx = __shfl_down(x0, 1, 64);
+  const uint64_t last = readlane64(x0, 63);
+  const bool dup = (lane < 63u && x0 != kEmptyKey && key_rank(x0) == key_rank(nx)) ||
+                   (last != kEmptyKey && key_rank(x1) == key_rank(last));
+  if (ballot(dup) != 0) return false;
+  cnt = uniform(min(cnt + nt, bw));
+  b = lane < cnt ? x0 : kEmptyKey;
+  return true;
+}
+
+// General merge of the sorted new keys t (nt of them) into B[0, cnt) in LDS:
+// equal neighbours are dropped, and so is any key already in B (a binary
+// search in LDS); the rest are merged in place, clipped to bw. Kept key i
+// (compacted to T[i]) lands at p_i = lb_i + i, and that position is marked
+// in TAG with i (cleared again after the merge); entries of B below the
+// smallest kept key's position lb0 keep their places, and every other output
+// position o >= lb0 takes B[o - (placed keys below o)]. The 64-entry chunks
+// of [lb0, ncnt) run from the top down, so a chunk reads only entries that
+// are not yet overwritten (its own reads precede its writes). Returns false
+// when every new key was a repeat or a member of B (B unchanged).
+__device__ __forceinline__ bool merge_general(uint64_t* B, uint64_t* T, uint32_t* TAG, uint64_t t, uint32_t nt,
+                                              uint32_t& cnt, uint32_t& hint, uint32_t bw, uint32_t lane) {
+  const uint64_t prev = __shfl_up(t, 1, 64);
+  bool keep = lane < nt && !(lane > 0 && key_rank(prev) == key_rank(t));
+  uint32_t lb = 0;
+  const uint32_t top = pow2_ceil(cnt);
+  if (lane < nt) {
+    lb = lds_lower_bound(B, cnt, top, key_rank(t));
+    if (lb < cnt && key_rank(B[lb]) == key_rank(t)) keep = false;
+  }
+  const uint64_t km = ballot(keep);
+  const uint32_t nk = (uint32_t)__builtin_popcountll(km);
+  if (nk == 0) return false;
+  const uint32_t ti = mbcnt(km);
+  wave_sync();
+  if (keep) T[ti] = t;
+  wave_sync();
+  const uint32_t lb0 = uniform((uint32_t)__shfl((int)lb, (int)__builtin_ctzll(km), 64));
+  const uint32_t ncnt = min(cnt + nk, bw);
+  const bool placed = keep && ti + lb < ncnt;
+  if (placed) TAG[ti + lb] = 0x100u | ti;
+  // kept keys that land inside the clipped list (the others fall past it)
+  const uint32_t np = (uint32_t)__builtin_popcountll(ballot(placed));
+  wave_sync();
+  uint32_t above = 0;  // kept keys above the current chunk
+  for (int32_t o0 = (int32_t)(lb0 + ((ncnt - 1u - lb0) & ~63u)); o0 >= (int32_t)lb0; o0 -= 64) {
+    const uint32_t o = (uint32_t)o0 + lane;
+    const bool valid = o < ncnt;
+    const uint32_t tg = valid ? TAG[o] : 0u;
+    const bool isnew = tg != 0u;
+    const uint64_t m = ballot(isnew);
+    // kept keys at positions >= o: above, plus this chunk's from lane on
+    const uint32_t ge = above + (uint32_t)__builtin_popcountll(m >> lane);
+    uint64_t v = 0;
+    if (isnew) v = T[tg & 0xFFu];
+    else if (valid) v = B[o - (np - ge)];
+    if (valid) B[o] = v;
+    above = uniform(above + (uint32_t)__builtin_popcountll(m));
+  }
+  if (placed) TAG[ti + lb] = 0u;
+  hint = uniform(min(hint, lb0));
+  cnt = uniform(ncnt);
+  wave_sync();
+  return true;
+}
+
 // BYTES: the graph keeps byte rows (CPL 4, L2, no measurement mode)
 template <int CPL, int METRIC, bool STATS, bool BYTES = false>
 __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC, BYTES>())) void beam_search_kernel(
@@ -461,90 +541,23 @@ __global__ __launch_bounds__(64, (search_waves_per_simd<CPL, METRIC, BYTES>())) 
     }
     wave_sync();
 
-    // ---- sort the new keys
+    // ---- sort the new keys, merge them into B
     uint64_t t = lane < nt ? T[lane] : kEmptyKey;
     t = wave_sort_upto(t, nt);
+    if (regb && merge_regs(b, t, nt, cnt, bw, lane)) {
+      lds_wave_sync();
+      continue;
+    }
     if (regb) {
-      // B one key per lane: bitonic merge in registers. B ascending against
-      // the new keys reversed: the lane-wise minima are a bitonic sequence
-      // holding the 64 smallest keys, sorted by six more stages. Equal ranks
-      // (a re-scored member of B, an id scored twice) are left to the
-      // general path below: they sit side by side in the merged order, or
-      // across its 64th key.
-      const uint64_t tr = reverse_lanes64(t);
-      const bool lt = b < tr;
-      uint64_t x0 = lt ? b : tr;
-      const uint64_t x1 = lt ? tr : b;
-      x0 = bitonic_merge_steps<64, 32>(x0, lane);
-      const uint64_t nx = __shfl_down(x0, 1, 64);
-      const uint64_t last = readlane64(x0, 63);
-      const bool dup = (lane < 63u && x0 != kEmptyKey && key_rank(x0) == key_rank(nx)) ||
-                       (last != kEmptyKey && key_rank(x1) == key_rank(last));
-      if (ballot(dup) == 0) {
-        cnt = uniform(min(cnt + nt, bw));
-        b = lane < cnt ? x0 : kEmptyKey;
-        lds_wave_sync();
-        continue;
-      }
       // B to LDS for the general path
       if (lane < cnt) B[lane] = b;
       hint = 0;
       wave_sync();
     }
-    // ---- general path: drop duplicates and members of B, merge by rank
-    const uint64_t prev = __shfl_up(t, 1, 64);
-    bool keep = lane < nt && !(lane > 0 && key_rank(prev) == key_rank(t));
-    uint32_t lb = 0;
-    const uint32_t top = pow2_ceil(cnt);
-    if (lane < nt) {
-      lb = lds_lower_bound(B, cnt, top, key_rank(t));
-      if (lb < cnt && key_rank(B[lb]) == key_rank(t)) keep = false;
-    }
-    const uint64_t km = ballot(keep);
-    const uint32_t nk = (uint32_t)__builtin_popcountll(km);
-    if (nk == 0) {  // every new key was a repeat or a member of B
+    if (!merge_general(B, T, TAG, t, nt, cnt, hint, bw, lane)) {
       lds_wave_sync();
       continue;
     }
-    const uint32_t ti = mbcnt(km);
-    wave_sync();
-    if (keep) T[ti] = t;
-    wave_sync();
-
-    // ---- merge in place, clipped to bw. Entries of B below the smallest
-    //      kept key's position lb0 keep their places. Kept key i (compacted
-    //      to T[i]) lands at p_i = lb_i + i, and that position is marked
-    //      with i (cleared again after the merge); every other output
-    //      position o >= lb0 takes B[o - (placed keys below o)]. The 64-entry
-    //      chunks of [lb0, ncnt) run from the top down, so a chunk reads only
-    //      entries that are not yet overwritten (its own reads precede its
-    //      writes).
-    const uint32_t lb0 = uniform((uint32_t)__shfl((int)lb, (int)__builtin_ctzll(km), 64));
-    const uint32_t ncnt = min(cnt + nk, bw);
-    const bool placed = keep && ti + lb < ncnt;
-    if (placed) TAG[ti + lb] = 0x100u | ti;
-    // kept keys that land inside the clipped list (the others fall past it)
-    const uint32_t np = (uint32_t)__builtin_popcountll(ballot(placed));
-    wave_sync();
-    uint32_t above = 0;  // kept keys above the current chunk
-    for (int32_t o0 = (int32_t)(lb0 + ((ncnt - 1u - lb0) & ~63u)); o0 >= (int32_t)lb0; o0 -= 64) {
-      const uint32_t o = (uint32_t)o0 + lane;
-      const bool valid = o < ncnt;
-      const uint32_t tg = valid ? TAG[o] : 0u;
-      const bool isnew = tg != 0u;
-      const uint64_t m = ballot(isnew);
-      // kept keys at positions >= o: above, plus this chunk's from lane on
-      const uint32_t ge = above + (uint32_t)__builtin_popcountll(m >> lane);
-      uint64_t v = 0;
-      if (isnew) v = T[tg & 0xFFu];
-      else if (valid) v = B[o - (np - ge)];
-      if (valid) B[o] = v;
-      above = uniform(above + (uint32_t)__builtin_popcountll(m));
-    }
-    if (placed) TAG[ti + lb] = 0u;
-    hint = uniform(min(hint, lb0));
-    cnt = uniform(ncnt);
-    wave_sync();
     if (regb) b = lane < cnt ? B[lane] : kEmptyKey;
   }
   if (regb) {
