@@ -194,8 +194,8 @@ int64_t jasperx_rabitq_quantize(const void* vectors, int32_t dtype, int64_t n, i
  * reference runs in torch): L2 = (||q||^2 + ||v||^2) - 2 q.v in fp32 clamped
  * at 0; IP = -(fp16(q.v)). base [n][stride] and queries [nq][stride] are
  * device fp16 rows padded with zeros to stride = the next multiple of 8 of
- * dim, 16-byte aligned. Results (device) ordered by (distance, id); k <= 64,
- * dim <= 512. Asynchronous on `stream`. */
+ * dim, 16-byte aligned. Results (device) ordered by (distance, id); k <= 128,
+ * padded dim <= 4096. Asynchronous on `stream`. */
 int64_t jasperx_bruteforce_knn(const void* base, int64_t n, int64_t dim, int64_t base_stride, const void* queries,
                                int64_t n_queries, int64_t query_stride, int64_t k, int32_t metric,
                                int32_t* out_ids, float* out_dists, void* stream);

@@ -7,8 +7,9 @@
 // products are exact in fp32, accumulation in fp32); the squared norms are
 // fp32 sums in element order. Ties are ordered by (distance, id).
 //
-// One-pass path, used for bases under 262,144 rows, for the threshold
-// sample of the two-pass path and for queries that overflow it:
+// One-pass path, used for bases under four samples (262,144 rows at k = 10),
+// for rows longer than 512 values, for the threshold sample of the two-pass
+// path and for queries that overflow it:
 // bf_scan_kernel: one wave owns 32 queries and one chunk of the base. It
 // holds the A fragments of its queries in registers and walks the chunk 32
 // vectors at a time (one 32x32 output tile, K over the padded dim), loading
@@ -17,7 +18,9 @@
 // query's current k-th best; a buffer that could overflow in the next step
 // is compacted (sorted, cut to k), which also lowers the threshold. At the
 // end each (query, chunk) writes its best k, sorted. bf_merge_kernel: one
-// wave per query merges the chunk lists.
+// wave per query merges the chunk lists. Rows longer than 32 K steps (512
+// values, config 4's 960) take the same kernel with the query and base
+// fragments read per slice of 8 K steps.
 // The two-pass path for large bases is described before bf_filter_kernel.
 #include "bruteforce.hpp"
 #include "common.hpp"
@@ -34,8 +37,11 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int kBfMaxK = 64;          // k the fused scan supports
+constexpr int kBfMaxK = 128;         // k the fused scan supports
 constexpr int kBfStep = 32;          // vectors per step = most keys a query can gain per step
+constexpr int kBfScratch = 256;      // compaction scratch: holds a full buffer (k + kBfStep <= 160)
+constexpr uint32_t kBfMaxDp = 4096;  // longest padded row
+constexpr int kBfSlice = 8;          // K steps per slice of the long-row scan (KS = 0)
 
 __device__ uint4 kBfZeroChunk = {0u, 0u, 0u, 0u};  // never written
 
@@ -69,9 +75,9 @@ __global__ void row_sqnorm_kernel(const uint16_t* __restrict__ x, int64_t n, uin
 // Sort key: order-preserving distance bits (high) and id (low).
 __device__ __forceinline__ uint64_t bf_key(float d, uint32_t id) { return ((uint64_t)dist_to_ord(d) << 32) | id; }
 
-// Compact one query's buffer through the wave's 128-entry scratch: sort the
-// cnt (<= 128) keys, keep min(cnt, k) in buf; returns that count and the k-th
-// key (~0 when fewer than k remain). Wave-wide.
+// Compact one query's buffer through the wave's kBfScratch-entry scratch:
+// sort the cnt (<= kBfScratch) keys, keep min(cnt, k) in buf; returns that
+// count and the k-th key (~0 when fewer than k remain). Wave-wide.
 __device__ uint32_t bf_compact(uint64_t* buf, uint32_t cnt, uint32_t k, uint64_t* scratch, uint64_t* kth) {
   const uint32_t lane = lane_id();
   if (cnt <= 64) {
@@ -85,12 +91,12 @@ __device__ uint32_t bf_compact(uint64_t* buf, uint32_t cnt, uint32_t k, uint64_t
     lds_wave_sync();
     return keep;
   }
-  scratch[lane] = lane < cnt ? buf[lane] : ~0ull;
-  scratch[lane + 64] = lane + 64 < cnt ? buf[lane + 64] : ~0ull;
+  const uint32_t N = pow2_ceil(cnt);
+  for (uint32_t i = lane; i < N; i += 64) scratch[i] = i < cnt ? buf[i] : ~0ull;
   wave_sync();
-  lds_bitonic_sort(scratch, 128);
+  lds_bitonic_sort(scratch, N);
   const uint32_t keep = min(cnt, k);
-  if (lane < keep) buf[lane] = scratch[lane];
+  for (uint32_t i = lane; i < keep; i += 64) buf[i] = scratch[i];
   *kth = keep == k ? scratch[k - 1] : ~0ull;
   wave_sync();
   return keep;
@@ -103,10 +109,12 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
                                                      uint32_t k, uint32_t cap, int64_t chunk, uint32_t n_chunks,
                                                      uint64_t* __restrict__ out /* [nq][n_chunks][k] */,
                                                      const uint8_t* __restrict__ tile_flags) {
-  // cap = k + kBfStep rounded up to 8: candidate slots per query
+  // cap = k + kBfStep rounded up to 8: candidate slots per query.
+  // KS = 0: rows longer than 32 K steps; the query and base fragments are
+  // read per slice of kBfSlice steps instead of held in registers.
   extern __shared__ uint64_t bf_lds[];
   uint64_t* cand = bf_lds;                 // [32][cap]
-  uint64_t* scratch = bf_lds + 32 * cap;   // [128]
+  uint64_t* scratch = bf_lds + 32 * cap;   // [kBfScratch]
   __shared__ uint32_t cnt[32];
   __shared__ uint64_t thr[32];
   const uint32_t lane = threadIdx.x;
@@ -126,13 +134,19 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
   // A fragments: lane holds query q0 + (lane % 32), K slice 8 * (lane / 32).
   const uint32_t am = lane & 31u, ah = lane >> 5;
   const int64_t aq = q0 + am;
-  uint4 af[KS];
+  constexpr int KR = KS > 0 ? KS : 1;  // K steps held in registers
+  uint4 af[KR];
+  if constexpr (KS > 0) {
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const uint32_t c = (uint32_t)s * 2 + ah;
-    af[s] = (aq < nq && c < nck) ? reinterpret_cast<const uint4*>(queries + (size_t)aq * dp)[c]
-                                 : make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t c = (uint32_t)s * 2 + ah;
+      af[s] = (aq < nq && c < nck) ? reinterpret_cast<const uint4*>(queries + (size_t)aq * dp)[c]
+                                   : make_uint4(0, 0, 0, 0);
+    }
   }
+  // long rows: this lane's query row (a row of zeros past nq)
+  const uint4* qrow = aq < nq ? reinterpret_cast<const uint4*>(queries + (size_t)aq * dp) : nullptr;
+  const uint32_t nks = (dp + 15) / 16;  // K steps (the last may be half empty)
   // the query rows of this lane's accumulators: m = 8g + 4*(lane/32) + j.
   // thd[r] is the distance of row r's current k-th key (+inf until known);
   // a score passes the cheap test d <= thd[r] and then the exact key test.
@@ -150,22 +164,43 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
   // a K slot past the row (dp % 16 == 8) reads the zero chunk: no per-lane
   // branch in the loop, and the product stays an exact 0 (the query side is
   // zero there too)
-  auto load_step = [&](int64_t v0, uint4 (&nb)[KS], float& nvs) {
+  auto load_step = [&](int64_t v0, uint4 (&nb)[KR], float& nvs) {
     const int64_t v = v0 + am;
     const int64_t vr = v < v_end ? v : v_begin;
     if constexpr (METRIC == kL2) nvs = vsq[vr];
-    const uint4* rv = reinterpret_cast<const uint4*>(base + (size_t)vr * dp);
+    if constexpr (KS > 0) {
+      const uint4* rv = reinterpret_cast<const uint4*>(base + (size_t)vr * dp);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const uint32_t c = (uint32_t)s * 2 + ah;
-      nb[s] = *(c < nck ? rv + c : &kBfZeroChunk);
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t c = (uint32_t)s * 2 + ah;
+        nb[s] = *(c < nck ? rv + c : &kBfZeroChunk);
+      }
     }
   };
-  auto step = [&](int64_t v0, const uint4 (&cb)[KS], float vs) {
+  auto step = [&](int64_t v0, const uint4 (&cb)[KR], float vs) {
     float16v acc = {};
+    if constexpr (KS > 0) {
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[s]), u4_as_h8(cb[s]), acc, 0, 0, 0);
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(af[s]), u4_as_h8(cb[s]), acc, 0, 0, 0);
+    } else {
+      // K in slices: both fragments of a slice read together, then its
+      // chain of kBfSlice matrix-core steps (the query rows stay in cache)
+      const int64_t v = v0 + am;
+      const uint4* rv = reinterpret_cast<const uint4*>(base + (size_t)(v < v_end ? v : v_begin) * dp);
+      for (uint32_t s0 = 0; s0 < nks; s0 += kBfSlice) {
+        uint4 a8[kBfSlice], b8[kBfSlice];
+#pragma unroll
+        for (int t = 0; t < kBfSlice; ++t) {
+          const uint32_t c = (s0 + (uint32_t)t) * 2 + ah;
+          a8[t] = qrow && c < nck ? qrow[c] : make_uint4(0u, 0u, 0u, 0u);
+          b8[t] = *(c < nck ? rv + c : &kBfZeroChunk);
+        }
+#pragma unroll
+        for (int t = 0; t < kBfSlice; ++t)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(u4_as_h8(a8[t]), u4_as_h8(b8[t]), acc, 0, 0, 0);
+      }
+    }
     // lane holds column n = lane % 32 (vector) and rows 8g + 4*(lane/32) + j
     const int64_t v = v0 + am;
     if (v < v_end) {
@@ -212,7 +247,7 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
   };
   // two tiles per iteration; tiles past v_end load a clamped row and add no
   // candidates (v < v_end fails), so the loop needs no mid-iteration exit
-  uint4 ba[KS], bb[KS];
+  uint4 ba[KR], bb[KR];
   float vsa = 0.0f, vsb = 0.0f;
   if (v_begin < v_end) load_step(v_begin, ba, vsa);
   for (int64_t v0 = v_begin; v0 < v_end; v0 += 64) {
@@ -262,7 +297,8 @@ __global__ __launch_bounds__(64) void bf_merge_kernel(const uint64_t* __restrict
 
 // ----------------------------------------------------------- two-pass path
 // For large bases the exact top-k is found in two passes over a GEMM:
-//  1. the one-pass kernels above on a sample (the first kBfSample rows) give
+//  1. the one-pass kernels above on a sample (the first rows of the base:
+//     kBfSample, or more when k * n is large) give
 //     each query the k-th smallest distance T_q of that sample. The true
 //     k-th smallest over the whole base is <= T_q (the sample's k nearest are
 //     k base rows), so every true neighbour has d <= T_q;
@@ -274,8 +310,7 @@ __global__ __launch_bounds__(64) void bf_merge_kernel(const uint64_t* __restrict
 // A query whose list would exceed kBfCandCap is flagged and redone with the
 // one-pass kernels (only its 32-query tile runs). Results are identical to
 // the one-pass path: the same distances, the same (distance, id) order.
-constexpr int64_t kBfSample = 65536;
-constexpr int64_t kBfTwoPassMin = 4 * kBfSample;
+constexpr int64_t kBfSample = 65536;  // smallest sample (larger for large k * n)
 constexpr uint32_t kBfCandCap = 1024;
 constexpr uint32_t kBfLocal = 16;  // candidates a filter work-group stages per query before appending to HBM
 
@@ -578,7 +613,7 @@ static void bf_one_pass(const void* base, int64_t n, uint32_t dp, const void* qu
   hip_check(hipMallocAsync((void**)&lists, (size_t)nq * n_chunks * k * 8, s), "alloc chunk lists");
   const dim3 grid((uint32_t)qtiles, n_chunks);
   const uint32_t cap = (k + kBfStep + 7u) & ~7u;
-  const size_t lds = ((size_t)32 * cap + 128) * 8;
+  const size_t lds = ((size_t)32 * cap + kBfScratch) * 8;
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(64), lds, s, (const uint16_t*)base, n, dp, (const uint16_t*)queries, nq,
                        vsq, qsq, k, cap, chunk, n_chunks, lists, tile_flags);
@@ -588,7 +623,8 @@ static void bf_one_pass(const void* base, int64_t n, uint32_t dp, const void* qu
     if (metric == kL2) go(bf_scan_kernel<K, kL2>);                 \
     else go(bf_scan_kernel<K, kIP>);                               \
     break;
-  switch (ks) {
+  switch (ks > 32 ? 0u : ks) {
+    JA_BF_CASE(0)
     JA_BF_CASE(1) JA_BF_CASE(2) JA_BF_CASE(3) JA_BF_CASE(4) JA_BF_CASE(5) JA_BF_CASE(6) JA_BF_CASE(7)
     JA_BF_CASE(8) JA_BF_CASE(9) JA_BF_CASE(10) JA_BF_CASE(11) JA_BF_CASE(12) JA_BF_CASE(13) JA_BF_CASE(14)
     JA_BF_CASE(15) JA_BF_CASE(16) JA_BF_CASE(17) JA_BF_CASE(18) JA_BF_CASE(19) JA_BF_CASE(20) JA_BF_CASE(21)
@@ -665,8 +701,8 @@ static void dispatch_filter(uint32_t ks, const void* base, int64_t n, uint32_t d
 void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, const void* queries, int64_t nq,
                     uint32_t k, int metric, int32_t* out_ids, float* out_d, hipStream_t s) {
   if (k == 0 || nq <= 0) return;
-  if (k > (uint32_t)kBfMaxK) throw std::invalid_argument("bruteforce_knn supports k <= 64");
-  if (dp % 8 != 0 || dp > 512) throw std::invalid_argument("bruteforce_knn supports padded dim <= 512");
+  if (k > (uint32_t)kBfMaxK) throw std::invalid_argument("bruteforce_knn supports k <= 128");
+  if (dp % 8 != 0 || dp > kBfMaxDp) throw std::invalid_argument("bruteforce_knn supports padded dim <= 4096");
   if (n <= 0) throw std::invalid_argument("empty base");
   if (n > 0x7FFFFFFFll) throw std::invalid_argument("too many base vectors");
   if (nq > 0x7FFFFFFFll) throw std::invalid_argument("too many queries");
@@ -680,10 +716,14 @@ void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, cons
     hipLaunchKernelGGL(row_sqnorm_kernel, dim3((uint32_t)((nq + 255) / 256)), dim3(256), 0, s,
                        (const uint16_t*)queries, nq, dp, dim, qsq);
   }
-  if (n < kBfTwoPassMin) {
+  // the two-pass path: rows of up to 32 K steps (512 values), and a sample
+  // large enough that a query's filtered list (about k * n / sample keys)
+  // stays near half of kBfCandCap
+  const int64_t sample = std::max<int64_t>(kBfSample, ((int64_t)2 * k * n / kBfCandCap + 63) / 64 * 64);
+  if (n < 4 * sample || dp > 512) {
     bf_one_pass(base, n, dp, queries, nq, k, metric, vsq, qsq, out_ids, out_d, nullptr, nullptr, s);
   } else {
-    // 1. thresholds from the sample rows [0, kBfSample)
+    // 1. thresholds from the sample rows [0, sample)
     int32_t* sid = nullptr;
     float* sd = nullptr;
     uint32_t* qcount = nullptr;
@@ -697,7 +737,7 @@ void bruteforce_knn(const void* base, int64_t n, uint32_t dim, uint32_t dp, cons
     hip_check(hipMallocAsync((void**)&flags, (size_t)(nq + ntiles), s), "alloc overflow flags");
     hip_check(hipMemsetAsync(qcount, 0, (size_t)nq * 4, s), "clear candidate counts");
     hip_check(hipMemsetAsync(flags, 0, (size_t)(nq + ntiles), s), "clear overflow flags");
-    bf_one_pass(base, kBfSample, dp, queries, nq, k, metric, vsq, qsq, sid, sd, nullptr, nullptr, s);
+    bf_one_pass(base, sample, dp, queries, nq, k, metric, vsq, qsq, sid, sd, nullptr, nullptr, s);
     // 2. every distance against the thresholds (the k-th sample distance)
     const uint32_t ks = (dp + 15) / 16;
     if (metric == kL2) dispatch_filter<kL2>(ks, base, n, dp, queries, nq, vsq, qsq, sd + (k - 1), k, qcount, qcand, s);

@@ -5,8 +5,9 @@ Same arithmetic as the reference utility: L2 distances as
 -(q.v) where fp16 inputs give an fp16 matmul result. Results are ordered by
 (distance, id).
 
-fp16 inputs with k <= 64 and dim <= 512 run on the matrix-core kernel of the
-HIP library (`jasperx_bruteforce_knn`), with the whole base resident in HBM.
+fp16 inputs with k <= 128 and dim <= 4096 (the reference's default k = 100
+and config 4's dim 960 included) run on the matrix-core kernel of the HIP
+library (`jasperx_bruteforce_knn`), with the whole base resident in HBM.
 Other inputs (fp32 data, larger k or dim, or device="cpu") take a torch
 path that streams query and base blocks with the same arithmetic and keeps
 the k nearest of each query as (distance, id) keys.
@@ -16,8 +17,8 @@ from __future__ import annotations
 
 import torch
 
-_HIP_MAX_K = 64
-_HIP_MAX_DIM = 512
+_HIP_MAX_K = 128
+_HIP_MAX_DIM = 4096
 
 
 def _padded_rows(x: torch.Tensor, dp: int, device) -> torch.Tensor:
@@ -32,7 +33,7 @@ def _padded_rows(x: torch.Tensor, dp: int, device) -> torch.Tensor:
 def bruteforce_knn(vectors: torch.Tensor, queries: torch.Tensor, k: int, distance: str = "l2",
                    device: str = "cuda") -> tuple[torch.Tensor, torch.Tensor]:
     """k nearest base rows per query on the matrix cores; fp16 inputs,
-    k <= 64, dim <= 512. Returns device tensors (int32 ids [nq, k], float32
+    k <= 128, dim <= 4096. Returns device tensors (int32 ids [nq, k], float32
     distances [nq, k]); missing neighbours are (-1, FLT_MAX)."""
     from . import _agnostic, _stream_ptr, _tensor_ptr
     if vectors.dtype != torch.float16 or queries.dtype != torch.float16:

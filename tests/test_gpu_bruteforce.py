@@ -36,7 +36,7 @@ def _ref(base, q, k, distance):
 def test_integer_data_bit_exact(jasper, oracle_lib, dim, distance):
     base = integer_clustered(20000, dim, 40)
     q = integer_clustered(300, dim, 41)
-    for k in (1, 10, 64):
+    for k in (1, 10, 64, 100, 128):
         ids, d = _run(jasper, base, q, k, distance)
         rid, rd = _ref(base, q, k, distance)
         if distance == "ip":
@@ -81,10 +81,15 @@ def test_generate_groundtruth_uses_kernel(jasper, oracle_lib):
                                          torch.from_numpy(q.astype(np.float16)), k=10)
     rid, rd = _ref(base, q, 10, "l2")
     assert np.array_equal(ids.numpy(), rid) and np.array_equal(d.numpy(), rd)
+    # the reference's default k = 100 runs on the kernel too
+    ids1, d1 = jasper.generate_groundtruth(torch.from_numpy(base.astype(np.float16)),
+                                           torch.from_numpy(q.astype(np.float16)))
+    rid1, rd1 = _ref(base, q, 100, "l2")
+    assert np.array_equal(ids1.numpy(), rid1) and np.array_equal(d1.numpy(), rd1)
     # k above the kernel's limit takes the torch formulation; same answers
     ids2, d2 = jasper.generate_groundtruth(torch.from_numpy(base.astype(np.float16)),
-                                           torch.from_numpy(q.astype(np.float16)), k=80)
-    rid2, rd2 = _ref(base, q, 80, "l2")
+                                           torch.from_numpy(q.astype(np.float16)), k=200)
+    rid2, rd2 = _ref(base, q, 200, "l2")
     assert np.array_equal(d2.numpy(), rd2)
 
 
@@ -95,11 +100,47 @@ def test_two_pass_integer_exact(jasper, oracle_lib, distance):
     bit for bit, ties ordered by id."""
     base = integer_clustered(300_000, 64, 44)
     q = integer_clustered(100, 64, 45)
-    for k in (10, 64):
+    for k in (10, 64, 100):
         ids, d = _run(jasper, base, q, k, distance)
         rid, rd = _ref(base, q, k, distance)
         assert np.array_equal(d, rd), f"k={k}"
         assert np.array_equal(ids, rid), f"k={k}"
+
+
+@pytest.mark.parametrize("dim", [520, 960, 1000])
+@pytest.mark.parametrize("distance", ["l2", "ip"])
+def test_long_rows_integer_exact(jasper, oracle_lib, dim, distance):
+    """Rows longer than 512 values take the scan with K read in slices (dp
+    1000: a half-empty last K step). Values in [0, 15] keep every sum of
+    products below 2^24, so the results equal the reference arithmetic bit
+    for bit, ties by id; k up to the reference default 100."""
+    rng = np.random.default_rng(dim)
+    base = rng.integers(0, 16, size=(6000, dim)).astype(np.float32)
+    q = rng.integers(0, 16, size=(70, dim)).astype(np.float32)
+    for k in (10, 100):
+        ids, d = _run(jasper, base, q, k, distance)
+        rid, rd = _ref(base, q, k, distance)
+        assert np.array_equal(d, rd), f"k={k}"
+        assert np.array_equal(ids, rid), f"k={k}"
+
+
+def test_long_rows_config4_data(jasper, oracle_lib):
+    """Config 4's generator (|N(0,1)| * 0.05, 20 % zeros, dim 960): the
+    reference arithmetic within 1e-5 relative, ids wherever the reference's
+    neighbouring distances are separated by more than the tolerance."""
+    from jasper_amd import datasets
+    base = datasets.sparse_abs(8000, 960, 60)
+    q = datasets.sparse_abs(40, 960, 61)
+    k = 10
+    ids, d = _run(jasper, base, q, k, "l2")
+    rid, rd = _ref(base, q, k + 1, "l2")
+    scale = np.abs(rd[:, :k]) + 1e-3
+    assert np.all(np.abs(d - rd[:, :k]) <= 1e-5 * scale)
+    gap = (rd[:, 1:] - rd[:, :-1]) > 2e-5 * (np.abs(rd[:, 1:]) + 1e-3)
+    for i in range(len(q)):
+        for j in range(k):
+            if gap[i, j] and (j == 0 or gap[i, j - 1]):
+                assert ids[i, j] == rid[i, j], (i, j)
 
 
 def test_two_pass_overflow_falls_back(jasper, oracle_lib):
