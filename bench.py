@@ -228,6 +228,7 @@ def main() -> int:
     ap.add_argument("--diskann-parts", default="8,4,16", help="shard counts of --path diskann (first = the line's value)")
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
+    ap.add_argument("--rotate-dim", type=int, default=128, help="row dimension of --path rotate (128 or 960)")
     ap.add_argument("--no-general-path", action="store_true",
                     help="skip the child-process run with the integer-row shortcuts off (profiler runs)")
     ap.add_argument("--nq-sweep", default="",
@@ -676,18 +677,36 @@ def run_bruteforce(args, torch, jasper_amd, datasets, dev, log):
     return 0
 
 
+PEAK_MFMA_F16_TFLOPS = 2500.0
+
+
 def run_rotate(args, torch, jasper_amd, datasets, dev, log):
-    """Prerotation of 1M x 128 fp16 rows (the construct-time GEMM)."""
-    x = torch.from_numpy(datasets.clustered(args.n, 128, 0)).to(dev)
+    """Prerotation of 1M fp16 rows (the construct-time GEMM): d = 128 (config
+    2's rows; HBM-bound, 64 flop/byte) or --rotate-dim 960 (config 4's rows;
+    480 flop/byte, above the MI355X ridge of about 310: matrix-core bound)."""
+    d = args.rotate_dim
+    rows = datasets.sparse_abs(args.n, d, 0) if d == 960 else datasets.clustered(args.n, d, 0)
+    x = torch.from_numpy(rows).to(dev)
     wall, ev, _ = _timed(torch, lambda: jasper_amd.rotate(x, 42), args.steps, args.warmup)
-    nbytes = 4.0 * args.n * 128 + 2 * 128 * 128
+    nbytes = 4.0 * args.n * d + 2 * d * d
+    flop = 2.0 * args.n * d * d
     gbs = nbytes / (ev / 1000.0) / 1e9
-    res = _line(args, "prerotation GB/s, 1M x 128 fp16", gbs, "GB/s", wall, "f16",
-                {"workload": f"{args.n} x 128 fp16 rows times a 128 x 128 fp16 rotation, fp32 accumulation",
-                 "tflops": 2.0 * args.n * 128 * 128 / (ev / 1000.0) / 1e12},
-                {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
-                 "traffic": None, "kernel": "rotate_tile_kernel<4,8>", "kernel_ms": ev,
-                 "algorithmic_bytes_per_launch": nbytes})
+    tf = flop / (ev / 1000.0) / 1e12
+    kernel = "rotate_tile_kernel" if d <= 192 else "rotate_gemm_kernel"
+    if flop / nbytes < PEAK_MFMA_F16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
+        roof = {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                "traffic": None, "kernel": kernel, "kernel_ms": ev, "algorithmic_bytes_per_launch": nbytes}
+        res = _line(args, f"prerotation GB/s, {args.n} x {d} fp16", gbs, "GB/s", wall, "f16",
+                    {"workload": f"{args.n} x {d} fp16 rows times a {d} x {d} fp16 rotation, fp32 accumulation",
+                     "tflops": tf}, roof)
+    else:
+        roof = {"bound": "mfma", "achieved": tf, "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": tf / PEAK_MFMA_F16_TFLOPS, "traffic": None, "kernel": kernel, "kernel_ms": ev,
+                "algorithmic_flop_per_launch": flop}
+        res = _line(args, f"prerotation TFLOP/s, {args.n} x {d} fp16", tf, "TFLOP/s", wall, "f16",
+                    {"workload": f"{args.n} x {d} fp16 rows (config 4's generator) times a {d} x {d} fp16 rotation, "
+                                 "fp32 accumulation", "hbm_gbs": gbs}, roof)
+    log(f"rotate {args.n} x {d}: {ev:.3f} ms, {tf:.1f} TFLOP/s, {gbs:.0f} GB/s")
     print(json.dumps(res), flush=True)
     return 0
 

@@ -195,6 +195,124 @@ __global__ __launch_bounds__(64 * WAVES) void rotate_tile_kernel(const uint16_t*
   }
 }
 
+// Long rows (P too large for LDS, d > 192; config 4's d = 960): an
+// LDS-tiled GEMM out[r][i] = sum_k Pt[i][k] x[r][k]. A block of 4 waves owns
+// 128 outputs i x 128 rows r; each wave 64 x 64 as 2 x 2 tiles of
+// v_mfma_f32_32x32x16_f16 (A = Pt: M = outputs, B = x: N = rows, both read
+// along K). K runs in chunks of 64 staged through LDS, the next chunk's
+// global loads in flight while the current one is on the matrix cores.
+// Blocks are mapped so that the output-column blocks of one row block land
+// on one XCD (work-groups are dealt to the 8 XCDs round-robin): they read the
+// same x tile, which that XCD's L2 then serves.
+constexpr uint32_t kRgTile = 128;  // outputs and rows per block
+constexpr uint32_t kRgK = 64;      // K per LDS chunk
+constexpr uint32_t kRgStride = kRgK / 8 + 1;  // uint4 per LDS row (one chunk of padding)
+
+typedef float float16v_r __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void rotate_gemm_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t dp_in,
+                                                          const uint16_t* __restrict__ pt, uint32_t kp,
+                                                          uint32_t dim, uint16_t* __restrict__ out,
+                                                          uint32_t dp_out, uint32_t col_blocks, int64_t row_blocks) {
+  __shared__ uint4 sa[2][kRgTile * kRgStride];  // Pt chunk: [output][k]
+  __shared__ uint4 sb[2][kRgTile * kRgStride];  // x chunk: [row][k]
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t mp = (dim + 15u) & ~15u;
+  // block p runs on XCD p % 8; the col_blocks blocks of one row block are
+  // p = xcd + 8 * (c + col_blocks * j) for c < col_blocks
+  const int64_t p = blockIdx.x;
+  const int64_t xcd = p & 7, q = p >> 3;
+  const uint32_t cb = (uint32_t)(q % col_blocks);
+  const int64_t rb = (q / col_blocks) * 8 + xcd;
+  if (rb >= row_blocks) return;
+  const uint32_t i_base = cb * kRgTile;
+  const int64_t r_base = rb * kRgTile;
+  const uint32_t kc = kp / 8, in_chunks = dp_in / 8;
+  // staging: thread element e = tid + 256 j is (row e / 8, chunk e % 8)
+  auto gload = [&](uint32_t k0, uint4 (&ga)[4], uint4 (&gb)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t e = tid + 256u * (uint32_t)j, rr = e >> 3, c = (k0 / 8) + (e & 7u);
+      const uint32_t i = i_base + rr;
+      ga[j] = (i < mp && c < kc) ? reinterpret_cast<const uint4*>(pt)[(size_t)i * kc + c] : make_uint4(0, 0, 0, 0);
+      const int64_t r = r_base + rr;
+      gb[j] = (r < n && c < in_chunks) ? reinterpret_cast<const uint4*>(x)[(size_t)r * in_chunks + c]
+                                       : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto sstore = [&](uint32_t buf, const uint4 (&ga)[4], const uint4 (&gb)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t e = tid + 256u * (uint32_t)j, rr = e >> 3, c = e & 7u;
+      sa[buf][rr * kRgStride + c] = ga[j];
+      sb[buf][rr * kRgStride + c] = gb[j];
+    }
+  };
+  const uint32_t wm = wave & 1u, wn = wave >> 1;  // the wave's 64 outputs and 64 rows
+  const uint32_t l32 = lane & 31u, lh = lane >> 5;
+  float16v_r acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = float16v_r{};
+  uint4 ga[4], gb[4];
+  gload(0, ga, gb);
+  sstore(0, ga, gb);
+  __syncthreads();
+  const uint32_t nchunk = (kp + kRgK - 1) / kRgK;
+  for (uint32_t ch = 0; ch < nchunk; ++ch) {
+    const uint32_t buf = ch & 1u;
+    if (ch + 1 < nchunk) gload((ch + 1) * kRgK, ga, gb);
+#pragma unroll
+    for (uint32_t ks = 0; ks < kRgK / 16; ++ks) {
+      // lane: row/output l32 of the tile, K slice 8 * lh of the 16-wide step
+      const uint32_t c = ks * 2 + lh;
+      uint4 fa[2], fb[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) fa[a] = sa[buf][(wm * 64 + 32 * a + l32) * kRgStride + c];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) fb[b] = sb[buf][(wn * 64 + 32 * b + l32) * kRgStride + c];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_half8(fa[a]), as_half8(fb[b]), acc[a][b], 0, 0, 0);
+    }
+    if (ch + 1 < nchunk) {
+      sstore(buf ^ 1u, ga, gb);
+      __syncthreads();
+    }
+  }
+  // acc[a][b][4g + e]: output i_base + 64 wm + 32 a + 8 g + 4 lh + e, row
+  // r_base + 64 wn + 32 b + l32; four consecutive outputs per 8-byte store
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int64_t r = r_base + wn * 64 + 32 * b + l32;
+    if (r >= n) continue;
+    uint16_t* orow = out + (size_t)r * dp_out;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t i0 = i_base + wm * 64 + 32 * a + 8 * g + 4 * lh;
+        const float v[4] = {acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+        if (i0 + 3 < mp && i0 + 3 < dp_out) {
+          uint2 w;
+          w.x = (uint32_t)__half_as_ushort(__float2half_rn(v[0])) |
+                ((uint32_t)__half_as_ushort(__float2half_rn(v[1])) << 16);
+          w.y = (uint32_t)__half_as_ushort(__float2half_rn(v[2])) |
+                ((uint32_t)__half_as_ushort(__float2half_rn(v[3])) << 16);
+          *reinterpret_cast<uint2*>(orow + i0) = w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (i0 + e < mp && i0 + e < dp_out) orow[i0 + e] = __half_as_ushort(__float2half_rn(v[e]));
+        }
+      }
+    }
+  }
+}
+
 // Zero the output pad columns [dim, dp_out) that the tiles do not cover.
 __global__ void clear_pad_kernel(uint16_t* out, int64_t n, uint32_t mp, uint32_t dp_out) {
   const uint32_t w = dp_out - mp;
@@ -324,6 +442,13 @@ void rotate_rows(const RotationMatrix& r, const void* x, int64_t n, uint32_t dp_
         default: go(rotate_tile_kernel<6, 4>); break;
       }
     }
+  } else if (ks > 6) {
+    const uint32_t col_blocks = (r.mp + kRgTile - 1) / kRgTile;
+    const int64_t row_blocks = (n + kRgTile - 1) / kRgTile;
+    // grid: col_blocks blocks per row block, row blocks in groups of 8 (one per XCD)
+    const int64_t blocks = ((row_blocks + 7) / 8) * 8 * col_blocks;
+    hipLaunchKernelGGL(rotate_gemm_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, xi, n, dp_in,
+                       (const uint16_t*)r.pt, r.kp, r.dim, o, dp_out, col_blocks, row_blocks);
   } else if (use_lds) {
     switch (ks) {
       case 1: launch(rotate_mfma_kernel<1, true>, lds); break;

@@ -245,11 +245,13 @@ def test_prerotated_build_rows(jasper, oracle_lib, dim):
     gg.free()
 
 
-@pytest.mark.parametrize("dim,n", [(8, 5), (33, 70), (96, 1000), (128, 4099), (160, 500), (250, 64), (960, 300)])
+@pytest.mark.parametrize("dim,n", [(8, 5), (33, 70), (96, 1000), (128, 4099), (160, 500), (200, 777), (250, 64),
+                                   (960, 300), (960, 2100), (1000, 130)])
 def test_rotate_operator(jasper, oracle_lib, dim, n):
     """The stand-alone rotation (device and host inputs, unaligned strides,
-    more than 64 KB of LDS per block at dim 160, the global-memory path for
-    dim 960)."""
+    more than 64 KB of LDS per block at dim 160, the LDS-tiled GEMM above
+    dim 192: partial output and row blocks, dim 1000 with K padded to 1024
+    and outputs past the row's stride)."""
     x = (gaussian(n, dim, 32) * 4).astype(np.float16)
     got = jasper.rotate(torch.from_numpy(x).cuda(), seed=42)
     torch.cuda.synchronize()
