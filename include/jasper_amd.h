@@ -233,14 +233,18 @@ int64_t jasperx_construct_directional_ex(const char* config, const void* vectors
  * config: a plain config id (e.g. "f16_r64_l2"); vectors [n_vectors, dim]
  * fp16 (host or device); partitions are built in batches of up to
  * min(budget batch, max_batch_size), max_batch_size <= 0 meaning the
- * command's n / n_parts / 20; merges in batches of the budget batch. The
- * graph is resident in device memory (the reference stages partitions
- * through host memory; the result is the same); returns a plain-config
- * handle (search / save / updates as for jasper_construct_<config>).
- * Errors: a partition would be empty, a budget below one batch item. */
+ * command's n / n_parts / 20; merges in batches of the budget batch.
+ * on_host = false: the graph is resident in device memory. on_host = true:
+ * the graph lives in pinned host memory and the build stages partitions
+ * through it, two on the device at a time (the reference's staging,
+ * construct_scale.cuh:121-124, 398-445), for indexes larger than HBM; the
+ * graph is the same edge for edge. Returns a plain-config handle (search /
+ * save / updates as for jasper_construct_<config>; an on_host graph as a
+ * graph loaded with on_host). Errors: a partition would be empty, a budget
+ * below one batch item. */
 int64_t jasperx_construct_scale(const char* config, const void* vectors, int64_t n_vectors, int64_t dim,
                                 double alpha, int64_t n_parts, int64_t workspace_budget_bytes,
-                                int64_t max_batch_size, void* stream);
+                                int64_t max_batch_size, bool on_host, void* stream);
 /* Times of the last partitioned build: {partition builds ms, merges ms,
  * total ms, merges, merge batches, partition batch size, merge batch
  * size}. */
@@ -255,12 +259,15 @@ int64_t jasperx_last_scale_stats(double* out7);
  * and the shards' rows are merged by stored distance into rows of the
  * config's R (the reference's configs: r_int 32 with R 32 or 64). config: a
  * plain config id; vectors [n_vectors, dim] fp16 (host or device), dim <=
- * 1024; n_dup <= 16. Returns a plain-config handle. Shards of equal size are
- * merged in shard order (the reference leaves that order unspecified). */
+ * 1024; n_dup <= 16. A shard of more than max_shard rows is built as equal
+ * sub-shards (construct_diskann.cuh:386-417); max_shard <= 0 takes the
+ * largest shard graph the free device memory holds after the workspace and
+ * 4 GB. Returns a plain-config handle. Tasks of equal size are merged in
+ * (shard, sub-shard) order (the reference leaves that order unspecified). */
 int64_t jasperx_construct_diskann(const char* config, const void* vectors, int64_t n_vectors, int64_t dim,
                                   double alpha, int64_t r_int, int64_t n_parts, int64_t n_dup,
                                   int64_t workspace_budget_bytes, int64_t max_batch_size, int64_t seed,
-                                  void* stream);
+                                  int64_t max_shard, void* stream);
 /* The shard assignment alone (assign_shards, construct_diskann.cuh:104-276)
  * for tests: out_shard_of [n_vectors * n_dup] (0xFFFFFFFF where a rank
  * repeats a shard) and out_mean [dim] fp16 bits, host memory, either NULL. */

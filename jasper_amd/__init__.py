@@ -104,10 +104,10 @@ _AGNOSTIC = {
     "jasperx_construct_directional_ex": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, ctypes.c_bool,
                                          ctypes.c_bool, _i64, ctypes.c_uint32, _ptr],
     "jasperx_export_rabitq": [_i64, _ptr, _ptr],
-    "jasperx_construct_scale": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, _i64, _i64, _ptr],
+    "jasperx_construct_scale": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, _i64, _i64, _bool, _ptr],
     "jasperx_last_scale_stats": [_ptr],
     "jasperx_construct_diskann": [ctypes.c_char_p, _ptr, _i64, _i64, ctypes.c_double, _i64, _i64, _i64, _i64, _i64,
-                                  _i64, _ptr],
+                                  _i64, _i64, _ptr],
     "jasperx_diskann_assign": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr],
     "jasperx_last_diskann_stats": [_ptr],
     "jasperx_directional_search_noalloc": [_i64, ctypes.c_int32, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64,
@@ -383,13 +383,17 @@ class Graph:
     @classmethod
     def build_scale(cls, vectors: torch.Tensor, n_neighbors: int = 32,
                     distance: DistanceFunc | str = DistanceFunc.L2, alpha: float = 1.2, n_parts: int = 2,
-                    workspace_budget: str = "10GB", max_batch_size: int | None = None) -> "Graph":
+                    workspace_budget: str = "10GB", max_batch_size: int | None = None,
+                    on_host: bool = False) -> "Graph":
         """The partitioned build of the reference's create_scale_index command
         (cmd/create_scale_index.cu:57-98; include/jasper/index/
         construct_scale.cuh): n_parts partitions built on their own, then
         every pair merged. max_batch_size caps the partitions' batches (None:
         n / n_parts / 20, as the command sets it); merges use the workspace
-        budget's batch. Returns a plain graph (search, save, updates)."""
+        budget's batch. on_host: the graph lives in pinned host memory and
+        partitions are staged through the device two at a time (indexes
+        larger than HBM); the same graph. Returns a plain graph (search,
+        save, updates)."""
         if isinstance(distance, str):
             distance = DistanceFunc(distance)
         if vectors.ndim != 2:
@@ -402,20 +406,22 @@ class Graph:
         stream = _stream_ptr(vectors.device if vectors.is_cuda else None)
         handle = _agnostic("jasperx_construct_scale")(
             config_id.encode(), _tensor_ptr(vectors), n, dim, float(alpha), int(n_parts),
-            parse_storage_size(workspace_budget), int(max_batch_size or 0), stream)
+            parse_storage_size(workspace_budget), int(max_batch_size or 0), bool(on_host), stream)
         return cls(handle, config_id, DataType.FLOAT16, distance, n_neighbors, dim)
 
     @classmethod
     def build_diskann(cls, vectors: torch.Tensor, n_neighbors: int = 32, r_int: int = 32,
                       distance: DistanceFunc | str = DistanceFunc.L2, alpha: float = 1.2, n_parts: int = 4,
                       n_dup: int = 2, workspace_budget: str = "10GB", max_batch_size: int | None = None,
-                      seed: int = 42) -> "Graph":
+                      seed: int = 42, max_shard: int | None = None) -> "Graph":
         """The DiskANN build of the reference's create_diskann_index command
         (cmd/create_diskann_index.cu:59-103; include/jasper/index/
         construct_diskann.cuh): rows sharded by cross-polytope LSH into n_dup
         of n_parts shards, each shard built at degree r_int, rows merged by
-        stored distance into n_neighbors (the final degree). Returns a plain
-        graph (search, save, updates)."""
+        stored distance into n_neighbors (the final degree). A shard of more
+        than max_shard rows is built as equal sub-shards (None: the largest
+        shard graph the free device memory holds). Returns a plain graph
+        (search, save, updates)."""
         if isinstance(distance, str):
             distance = DistanceFunc(distance)
         if vectors.ndim != 2:
@@ -428,7 +434,7 @@ class Graph:
         stream = _stream_ptr(vectors.device if vectors.is_cuda else None)
         handle = _agnostic("jasperx_construct_diskann")(
             config_id.encode(), _tensor_ptr(vectors), n, dim, float(alpha), int(r_int), int(n_parts), int(n_dup),
-            parse_storage_size(workspace_budget), int(max_batch_size or 0), int(seed), stream)
+            parse_storage_size(workspace_budget), int(max_batch_size or 0), int(seed), int(max_shard or 0), stream)
         return cls(handle, config_id, DataType.FLOAT16, distance, n_neighbors, dim)
 
     # -- properties ---------------------------------------------------------

@@ -388,7 +388,7 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
     const ExistingRow er = load_existing(a, w);
     RowFrag<CPL> xw;
     if constexpr (I8 == 2) load_query_bytes(a.pc.vecs + (size_t)w * a.pc.nchunks, a.pc.nb8, a.pc.qsh2, ql, xw.x);
-    else load_row_frag<CPL>(a.pc.vecs + (size_t)w * a.pc.nchunks, ql, a.pc.nchunks, true, xw);
+    else load_row_frag<CPL>(vec_row(a.pc, w), ql, a.pc.nchunks, true, xw);
     uint64_t key = a.sorted_pairs[min(start + lane, a.n_pairs - 1u)];
     if (start + lane >= a.n_pairs) key = kEmptyKey;
     const uint32_t start_next = a.heads[min(h + gridDim.x, nh - 1u)];
@@ -434,9 +434,9 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
       for (uint32_t base = 0; base < taken; base += 16) {
         const uint32_t j = base + qg;
         const bool act = j < taken;
-        const uint32_t sid = act ? l.srcs[j] : 0u;
+        const uint32_t sid = act ? l.srcs[j] : a.pc.r1_lo;
         RowFrag<CPL> xs;
-        load_row_frag<CPL>(a.pc.vecs + (size_t)sid * a.pc.nchunks, ql, a.pc.nchunks, act, xs);
+        load_row_frag<CPL>(vec_row(a.pc, sid), ql, a.pc.nchunks, act, xs);
         const float d = left_distance<CPL, METRIC, INTX>(wf, xs, ql, a.pc.nchunks, a.pc.nlimit);
         if (act && ql == 0) l.C[nE + j] = make_key(d, sid);
       }
@@ -977,6 +977,257 @@ void build_scale(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int
   }
   hip_check(hipEventRecord(t2, stream), "event record");
   hip_check(hipStreamSynchronize(stream), "scale build synchronize");
+  float a = 0, b = 0;
+  hip_check(hipEventElapsedTime(&a, t0, t1), "event elapsed");
+  hip_check(hipEventElapsedTime(&b, t1, t2), "event elapsed");
+  st.partition_ms = a;
+  st.merge_ms = b;
+  st.total_ms = (double)a + b;
+  if (stats) *stats = st;
+}
+
+// ------------------------------------------- staged (out-of-core) scale build
+
+// Adds `off` to the valid edge ids of rows [0, n): a partition built with
+// local ids (its first row is id 0) moves to its global ids (the reference's
+// apply_global_offset, graph.cuh:804-827).
+__global__ void offset_edges_kernel(uint32_t* edges, const uint8_t* counts, int64_t n, uint32_t R, uint32_t off) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * (int64_t)R) return;
+  const int64_t row = t / R;
+  if ((uint32_t)(t % R) < counts[row]) edges[t] += off;
+}
+
+namespace {
+
+// A Graph whose columns point into memory it does not own (a device slot,
+// shifted so that global ids index it): the pointers are dropped before the
+// Graph's destructor could free them.
+struct GraphView {
+  Graph g;
+  ~GraphView() {
+    g.vecs = nullptr;
+    g.vecs8 = nullptr;
+    g.edges = nullptr;
+    g.edist = nullptr;
+    g.counts = nullptr;
+    g.deleted = nullptr;
+    g.slot_to_id = nullptr;
+  }
+};
+
+// One device slot of the staged merge: the columns of one partition.
+struct StageSlot {
+  Graph d;              // device columns for up to `part` rows (ids local)
+  int64_t part_id = -1;
+  int64_t lo = 0, rows = 0;
+  bool dirty = false;   // adjacency changed since it was loaded
+};
+
+}  // namespace
+
+void build_scale_staged(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int64_t merge_batch,
+                        hipStream_t stream, ScaleStats* stats) {
+  if (!g.on_host) throw std::invalid_argument("the staged build keeps the graph in host memory (on_host)");
+  const int64_t n = g.n;
+  if (n <= 0) throw std::invalid_argument("graph is empty");
+  if (n_parts < 1) throw std::invalid_argument("n_parts must be positive");
+  if (g.R > 64) throw std::invalid_argument("R must be <= 64");
+  const int64_t part = (n + n_parts - 1) / n_parts;
+  if (part * (n_parts - 1) >= n)
+    throw std::invalid_argument("n_parts must be smaller: " + std::to_string(n_parts) + " partitions of " +
+                                std::to_string(n) + " vectors leave one empty");
+  if (part_batch < 1) part_batch = 1;
+  if (merge_batch < 1) merge_batch = 1;
+  const uint32_t R = g.R, dp = g.dp;
+  ScaleStats st;
+  st.part_batch = part_batch;
+  hipEvent_t t0, t1, t2;
+  hip_check(hipEventCreate(&t0), "event");
+  hip_check(hipEventCreate(&t1), "event");
+  hip_check(hipEventCreate(&t2), "event");
+  struct Events {
+    hipEvent_t* e[3];
+    ~Events() { for (hipEvent_t* x : e) (void)hipEventDestroy(*x); }
+  } ev{{&t0, &t1, &t2}};
+  hip_check(hipEventRecord(t0, stream), "event record");
+
+  // two device slots of `part` rows; the graph's columns stay in pinned host
+  // memory (construct_scale.cuh:121-124, 398-445)
+  StageSlot slot[2];
+  for (StageSlot& x : slot) x.d.allocate(part, g.dim, R, g.metric, false);
+  auto upload = [&](StageSlot& x, int64_t p) {
+    x.part_id = p;
+    x.lo = p * part;
+    x.rows = std::min(part, n - x.lo);
+    x.dirty = false;
+    const size_t r = (size_t)x.rows;
+    hip_check(hipMemcpyAsync(x.d.vecs, (const char*)g.vecs + (size_t)x.lo * dp * 2, r * dp * 2,
+                             hipMemcpyHostToDevice, stream), "stage vectors in");
+    hip_check(hipMemcpyAsync(x.d.edges, g.edges + (size_t)x.lo * R, r * R * 4, hipMemcpyHostToDevice, stream),
+              "stage edges in");
+    hip_check(hipMemcpyAsync(x.d.edist, g.edist + (size_t)x.lo * R, r * R * 2, hipMemcpyHostToDevice, stream),
+              "stage edge distances in");
+    hip_check(hipMemcpyAsync(x.d.counts, g.counts + x.lo, r, hipMemcpyHostToDevice, stream), "stage counts in");
+  };
+  auto write_back = [&](StageSlot& x) {
+    if (x.part_id < 0 || !x.dirty) return;
+    const size_t r = (size_t)x.rows;
+    hip_check(hipMemcpyAsync(g.edges + (size_t)x.lo * R, x.d.edges, r * R * 4, hipMemcpyDeviceToHost, stream),
+              "stage edges out");
+    hip_check(hipMemcpyAsync(g.edist + (size_t)x.lo * R, x.d.edist, r * R * 2, hipMemcpyDeviceToHost, stream),
+              "stage edge distances out");
+    hip_check(hipMemcpyAsync(g.counts + x.lo, x.d.counts, r, hipMemcpyDeviceToHost, stream), "stage counts out");
+    hip_check(hipStreamSynchronize(stream), "stage out");
+    x.dirty = false;
+  };
+
+  // 1. each partition on its own in slot 0, with local ids (search from its
+  //    first row), then shifted to global ids; the value ranges of all
+  //    partitions together give the merges' integer test
+  int32_t lo = 0, hi = -1;
+  bool all_int = true;
+  for (int64_t p = 0; p < n_parts; ++p) {
+    StageSlot& x = slot[0];
+    upload(x, p);
+    Graph& d = x.d;
+    d.n = x.rows;
+    d.medoid = 0;
+    scan_int_range(d, 0, x.rows, stream);
+    if (int_range(d)) {
+      lo = hi < lo ? d.int_lo : std::min(lo, d.int_lo);
+      hi = hi < lo ? d.int_hi : std::max(hi, d.int_hi);
+    } else {
+      all_int = false;
+    }
+    build_range(d, alpha, 0, x.rows, part_batch, true, stream, false, nullptr);
+    const int64_t total = x.rows * (int64_t)R;
+    hipLaunchKernelGGL(offset_edges_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, stream, d.edges,
+                       (const uint8_t*)d.counts, x.rows, R, (uint32_t)x.lo);
+    hip_check(hipGetLastError(), "launch offset_edges_kernel");
+    x.dirty = true;
+    write_back(x);
+    x.part_id = -1;
+  }
+  hip_check(hipEventRecord(t1, stream), "event record");
+
+  // 2. merge every pair once in scale_merge_order: B1's batches searched in
+  //    B2 alone, the forward prune into B1, the reverse prune into B2, with
+  //    the two partitions in the slots (a partition shared with the previous
+  //    pair stays on the device)
+  const auto order = scale_merge_order(n_parts);
+  if (!order.empty()) {
+    const int64_t mb = std::min<int64_t>(merge_batch, part);
+    st.merge_batch = mb;
+    const uint32_t cpl = prune_cpl(g);
+    BuildWorkspace ws(mb, R);
+    const PairBits pb = pair_bits(mb, n);
+    const bool intx = g.metric == kL2 && all_int && hi >= lo &&
+                      (int64_t)hi - (int64_t)lo <= (int64_t)int_exact_span(g.dim);
+    PruneKernelArgs pa{};
+    pa.pair_shift = pb.sb;
+    pa.pair_mask = (1u << pb.sb) - 1u;
+    pa.pc.nchunks = dp / 8;
+    pa.pc.nlimit = g.metric == kL2 ? g.dim / 8 : g.dim;  // the reference prunes with `dim`
+    pa.pc.R = R;
+    pa.pc.alpha = alpha;
+    pa.pc.margin_scale = gram_margin_scale();
+    pa.pc.staged = 1;
+    pa.visited = ws.visited;
+    pa.visited_counts = ws.vcounts;
+    pa.pairs = ws.pairs;
+    pa.sorted_pairs = ws.sorted;
+    pa.heads = ws.heads;
+    pa.n_heads = ws.nheads;
+    {
+      const _Float16 h = (_Float16)(intx ? lo : 0);  // exact: an fp16 value of the rows
+      uint16_t bits;
+      std::memcpy(&bits, &h, 2);
+      pa.pc.lo2 = (uint32_t)bits * 0x10001u;
+    }
+    const size_t plds = prune_lds_bytes();
+    EventTimer timer(false, stream);
+    BuildStats bst;
+    constexpr int64_t kSegment = (int64_t)1 << 20;
+    for (const auto& m : order) {
+      // slots for B1 and B2: keep whichever is already resident
+      StageSlot* s1 = slot[0].part_id == m.first ? &slot[0] : slot[1].part_id == m.first ? &slot[1] : nullptr;
+      StageSlot* s2 = slot[0].part_id == m.second ? &slot[0] : slot[1].part_id == m.second ? &slot[1] : nullptr;
+      if (!s1) {
+        s1 = s2 == &slot[0] ? &slot[1] : &slot[0];
+        write_back(*s1);
+        upload(*s1, m.first);
+      }
+      if (!s2) {
+        s2 = s1 == &slot[0] ? &slot[1] : &slot[0];
+        write_back(*s2);
+        upload(*s2, m.second);
+      }
+      const int64_t b1s = s1->lo, n1 = s1->rows, b2s = s2->lo, n2 = s2->rows;
+      // B2 as a graph over global ids (only its window is read)
+      GraphView v2;
+      Graph& gv = v2.g;
+      gv.dim = g.dim;
+      gv.dp = dp;
+      gv.R = R;
+      gv.metric = g.metric;
+      gv.n = n;
+      gv.capacity = n;
+      gv.medoid = (uint32_t)b2s;
+      gv.int_state = intx ? 1 : 2;
+      gv.int_lo = lo;
+      gv.int_hi = hi;
+      gv.vecs = (char*)s2->d.vecs - (size_t)b2s * dp * 2;
+      gv.edges = s2->d.edges - (size_t)b2s * R;
+      gv.counts = s2->d.counts - b2s;
+      pa.pc.vecs = (const uint4*)s1->d.vecs;
+      pa.pc.vecs_b = (const uint4*)s2->d.vecs;
+      pa.pc.r1_lo = (uint32_t)b1s;
+      pa.pc.r1_n = (uint32_t)n1;
+      pa.pc.r2_lo = (uint32_t)b2s;
+      pa.pc.r2_n = (uint32_t)n2;
+      int64_t count = 0;
+      while (count < n1) {
+        const int64_t bs = std::min({mb, n1 - count, kSegment - count % kSegment});
+        SearchRequest r;
+        r.queries = (const char*)s1->d.vecs + (size_t)count * dp * 2;
+        r.nq = (uint32_t)bs;
+        r.medoid = (uint32_t)b2s;
+        r.id_lo = (uint32_t)b2s;
+        r.id_n = n2;
+        r.k = kBuildL;
+        r.beam_width = kBuildL;
+        r.limit = kBuildLimit;
+        r.max_result = kBuildMaxResult;
+        r.visited = ws.visited;
+        r.visited_counts = ws.vcounts;
+        r.hash_bits = seen_cache_hash_bits(n);
+        launch_beam_search(gv, r, stream);
+        // forward merge prune into B1 (its adjacency indexed by global id)
+        pa.batch_offset = (uint32_t)(b1s + count);
+        pa.edges = s1->d.edges - (size_t)b1s * R;
+        pa.edist = s1->d.edist - (size_t)b1s * R;
+        pa.counts = s1->d.counts - b1s;
+        if (intx) dispatch_prune<kL2, true, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        else if (g.metric == kL2) dispatch_prune<kL2, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        else dispatch_prune<kIP, false, true>(false, cpl, pa, (uint32_t)bs, plds, stream);
+        hip_check(hipGetLastError(), "launch forward_prune_kernel (staged merge)");
+        // reverse merge prune into B2
+        pa.edges = s2->d.edges - (size_t)b2s * R;
+        pa.edist = s2->d.edist - (size_t)b2s * R;
+        pa.counts = s2->d.counts - b2s;
+        reverse_step<true>(g, pa, ws, pb, bs, intx, cpl, timer, bst, stream);
+        count += bs;
+        st.merge_batches += 1;
+      }
+      s1->dirty = s2->dirty = true;
+      st.merges += 1;
+    }
+    for (StageSlot& x : slot) write_back(x);
+  }
+  hip_check(hipEventRecord(t2, stream), "event record");
+  hip_check(hipStreamSynchronize(stream), "staged scale build synchronize");
+  scan_int_range(g, 0, n, stream);
   float a = 0, b = 0;
   hip_check(hipEventElapsedTime(&a, t0, t1), "event elapsed");
   hip_check(hipEventElapsedTime(&b, t1, t2), "event elapsed");

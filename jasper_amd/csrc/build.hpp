@@ -86,6 +86,14 @@ struct ScaleStats {
 std::vector<std::pair<int64_t, int64_t>> scale_merge_order(int64_t n_parts);
 void build_scale(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int64_t merge_batch,
                  hipStream_t stream, ScaleStats* stats);
+// The same build with the graph in pinned host memory (g.on_host, rows
+// uploaded): each partition is built on the device and written back, and
+// every merge runs with its two partitions in two device slots of ceil(n /
+// n_parts) rows (the reference's staging, construct_scale.cuh:121-124,
+// 398-445), so the device holds two partitions and the workspace, not the
+// index. The graph is the in-HBM build's, edge for edge.
+void build_scale_staged(Graph& g, float alpha, int64_t n_parts, int64_t part_batch, int64_t merge_batch,
+                        hipStream_t stream, ScaleStats* stats);
 
 // Live updates (reference construct.cuh:1169-1265, graph_ops.cuh:94-258).
 // append_rows: copies `count` rows (host or device fp16 [count, dim]) into

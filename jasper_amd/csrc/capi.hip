@@ -602,7 +602,7 @@ extern "C" int64_t jasperx_construct_directional_ex(const char* config, const vo
 
 extern "C" int64_t jasperx_construct_scale(const char* config, const void* vectors, int64_t n, int64_t dim,
                                            double alpha, int64_t n_parts, int64_t budget, int64_t max_batch_size,
-                                           void* stream) {
+                                           bool on_host, void* stream) {
   return guarded([&]() -> int64_t {
     if (!config) throw std::invalid_argument("null config id");
     static const char* const kNames[] = {
@@ -627,10 +627,11 @@ extern "C" int64_t jasperx_construct_scale(const char* config, const void* vecto
     const int64_t cap = max_batch_size > 0 ? max_batch_size : std::max<int64_t>(1, n / n_parts / 20);
     const int64_t part_batch = std::min(budget_batch, cap);
     auto g = std::make_unique<Graph>();
-    g->allocate(n, (uint32_t)dim, c.R, c.metric, false);
+    g->allocate(n, (uint32_t)dim, c.R, c.metric, on_host);
     upload_vectors(*g, vectors, n, (uint32_t)dim, s);
     ScaleStats st;
-    build_scale(*g, (float)alpha, n_parts, part_batch, budget_batch, s, &st);
+    if (on_host) build_scale_staged(*g, (float)alpha, n_parts, part_batch, budget_batch, s, &st);
+    else build_scale(*g, (float)alpha, n_parts, part_batch, budget_batch, s, &st);
     g->next_id = (uint64_t)n;
     {
       std::lock_guard<std::mutex> lock(g_mutex);
@@ -642,7 +643,8 @@ extern "C" int64_t jasperx_construct_scale(const char* config, const void* vecto
 
 extern "C" int64_t jasperx_construct_diskann(const char* config, const void* vectors, int64_t n, int64_t dim,
                                              double alpha, int64_t r_int, int64_t n_parts, int64_t n_dup,
-                                             int64_t budget, int64_t max_batch_size, int64_t seed, void* stream) {
+                                             int64_t budget, int64_t max_batch_size, int64_t seed,
+                                             int64_t max_shard, void* stream) {
   return guarded([&]() -> int64_t {
     if (!config) throw std::invalid_argument("null config id");
     static const char* const kNames[] = {
@@ -669,8 +671,12 @@ extern "C" int64_t jasperx_construct_diskann(const char* config, const void* vec
     g->allocate(n, (uint32_t)dim, c.R, c.metric, false);
     upload_vectors(*g, vectors, n, (uint32_t)dim, s);
     DiskannStats st;
-    build_diskann(*g, (uint32_t)r_int, (float)alpha, n_parts, n_dup, (uint64_t)seed, std::min(budget_batch, cap), s,
-                  &st);
+    // shards larger than the device can build are split (max_shard <= 0:
+    // from the free device memory, as construct_diskann.cuh:386-397)
+    const int64_t shard_cap =
+        max_shard > 0 ? max_shard : diskann_max_shard_for_device((uint32_t)dim, (uint32_t)r_int, budget);
+    build_diskann(*g, (uint32_t)r_int, (float)alpha, n_parts, n_dup, (uint64_t)seed, std::min(budget_batch, cap),
+                  shard_cap, s, &st);
     g->next_id = (uint64_t)n;
     {
       std::lock_guard<std::mutex> lock(g_mutex);

@@ -404,8 +404,19 @@ void diskann_assign(const Graph& g, int64_t n_parts, int64_t n_dup, uint64_t see
   if (mean_host) hip_check(hipMemcpy(mean_host, mean.p, (size_t)g.dim * 2, hipMemcpyDeviceToHost), "read mean");
 }
 
+int64_t diskann_max_shard_for_device(uint32_t dim, uint32_t R_int, int64_t workspace_budget) {
+  size_t free_b = 0, total_b = 0;
+  hip_check(hipMemGetInfo(&free_b, &total_b), "device memory info");
+  // a shard graph row: fp16 vector, R_int ids and bf16 distances, degree,
+  // slot id, deletion bit, and its byte row when the rows qualify
+  const size_t per_vec = (size_t)pad_dim(dim) * 2 + (size_t)R_int * 6 + 1 + 4 + 1 + dim;
+  const size_t reserve = (size_t)std::max<int64_t>(workspace_budget, 0) + ((size_t)4 << 30);
+  const size_t avail = free_b > reserve ? free_b - reserve : free_b / 2;
+  return (int64_t)std::min<size_t>(std::max<size_t>(avail / per_vec, 1), 0x7FFFFFFF);
+}
+
 void build_diskann(Graph& g, uint32_t R_int, float alpha, int64_t n_parts, int64_t n_dup, uint64_t seed,
-                   int64_t batch_cap, hipStream_t s, DiskannStats* stats) {
+                   int64_t batch_cap, int64_t max_shard, hipStream_t s, DiskannStats* stats) {
   check_assign_args(g, n_parts, n_dup);
   if (R_int < 1 || R_int > 64) throw std::invalid_argument("R_int must be between 1 and 64");
   if (g.R > 64) throw std::invalid_argument("R must be <= 64");
@@ -431,26 +442,35 @@ void build_diskann(Graph& g, uint32_t R_int, float alpha, int64_t n_parts, int64
                 sorted.as<uint64_t>(), mean.as<uint16_t>(), counts, s);
   hip_check(hipEventRecord(e[1], s), "event record");
 
-  // tasks: non-empty shards, largest first, equal sizes by shard index
+  // tasks: non-empty shards, each split into equal sub-shards of at most
+  // max_shard rows (max_shard > 0); largest first, equal sizes by shard
+  // index, then sub-shard
   std::vector<int64_t> offset((size_t)n_parts + 1, 0);
   for (int64_t p = 0; p < n_parts; ++p) offset[(size_t)p + 1] = offset[(size_t)p] + counts[(size_t)p];
-  std::vector<int64_t> tasks;
-  for (int64_t p = 0; p < n_parts; ++p)
-    if (counts[(size_t)p]) tasks.push_back(p);
-  std::stable_sort(tasks.begin(), tasks.end(),
-                   [&](int64_t a, int64_t b) { return counts[(size_t)a] > counts[(size_t)b]; });
+  struct Task {
+    int64_t begin, len;  // a run of the sorted (shard, row) pairs
+  };
+  std::vector<Task> tasks;
+  for (int64_t p = 0; p < n_parts; ++p) {
+    const int64_t total = counts[(size_t)p];
+    if (total == 0) continue;
+    const int64_t n_sub = max_shard > 0 ? (total + max_shard - 1) / max_shard : 1;
+    const int64_t sub = (total + n_sub - 1) / n_sub;
+    for (int64_t b = 0; b < total; b += sub) tasks.push_back({offset[(size_t)p] + b, std::min(sub, total - b)});
+  }
+  std::stable_sort(tasks.begin(), tasks.end(), [](const Task& a, const Task& b) { return a.len > b.len; });
   st.shards = (int64_t)tasks.size();
   int64_t max_count = 0;
-  for (int64_t p : tasks) max_count = std::max<int64_t>(max_count, counts[(size_t)p]);
+  for (const Task& t : tasks) max_count = std::max<int64_t>(max_count, t.len);
   st.max_shard = max_count;
 
   Graph sg;
   sg.allocate(max_count, g.dim, R_int, g.metric, false);
   const uint32_t words = g.dp / 8;
   double build_ms = 0, merge_ms = 0;
-  for (int64_t p : tasks) {
-    const int64_t c = counts[(size_t)p];
-    const uint64_t* ids = sorted.as<uint64_t>() + offset[(size_t)p];
+  for (const Task& task : tasks) {
+    const int64_t c = task.len;
+    const uint64_t* ids = sorted.as<uint64_t>() + task.begin;
     hip_check(hipEventRecord(e[2], s), "event record");
     const int64_t threads = c * words;
     hipLaunchKernelGGL(gather_rows_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s,

@@ -22,9 +22,17 @@ void diskann_assign(const Graph& g, int64_t n_parts, int64_t n_dup, uint64_t see
 // The DiskANN build into g (rows uploaded, no edges; g.R = R_final):
 // shards by cross-polytope LSH with n_dup copies, one graph of degree R_int
 // per shard (batches doubling to min(batch_cap, shard size)), then the
-// distance-only merge into g's rows, shards largest first (equal sizes by
-// shard index). medoid 0.
+// distance-only merge into g's rows, largest first (equal sizes by shard
+// index, then sub-shard). A shard of more than max_shard rows (max_shard >
+// 0) is built as equal sub-shards of its ascending ids, each at most
+// max_shard rows (construct_diskann.cuh:386-417), so the shard graph never
+// outgrows the device memory the caller gives it. medoid 0.
 void build_diskann(Graph& g, uint32_t R_int, float alpha, int64_t n_parts, int64_t n_dup, uint64_t seed,
-                   int64_t batch_cap, hipStream_t s, DiskannStats* stats);
+                   int64_t batch_cap, int64_t max_shard, hipStream_t s, DiskannStats* stats);
+
+// Rows of the largest shard graph that fits the device's free memory after
+// the construction workspace and 4 GB of slack (construct_diskann.cuh:
+// 386-397), for rows of dim values and degree R_int.
+int64_t diskann_max_shard_for_device(uint32_t dim, uint32_t R_int, int64_t workspace_budget);
 
 }  // namespace jasper_amd

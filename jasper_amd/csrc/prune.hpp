@@ -32,13 +32,35 @@ struct PruneCtx {
   // shift lo - 1024 as two fp16, when it keeps them; null otherwise
   const uint4* vecs8;
   uint32_t nb8, qsh2;
+  // staged merge (the partitioned build with its partitions in host memory,
+  // two on the device): range 1's rows at vecs, range 2's at vecs_b, each
+  // from its first id; no other rows are on the device (byte rows off)
+  uint32_t staged;
+  const uint4* vecs_b;
 };
+
+// Row of vector id: the flat array, or in a staged merge the device slot of
+// the id's range (callers pass only ids of the two ranges there).
+__device__ __forceinline__ const uint4* vec_row(const PruneCtx& p, uint32_t id) {
+  if (p.staged) {
+    if (id - p.r2_lo < p.r2_n) return p.vecs_b + (size_t)(id - p.r2_lo) * p.nchunks;
+    return p.vecs + (size_t)(id - p.r1_lo) * p.nchunks;
+  }
+  return p.vecs + (size_t)id * p.nchunks;
+}
 
 // Whether the merge prune resolves id's vector (robust_prune_kernel_scale,
 // reference index/construct_scale_kernels.cuh:69-74: b1_graph.is_valid or
 // b2_graph.is_valid).
 __device__ __forceinline__ bool resolvable(const PruneCtx& p, uint32_t id) {
   return id - p.r1_lo < p.r1_n || id - p.r2_lo < p.r2_n;
+}
+
+// id, or range 1's first row for an id the merge does not resolve: rows
+// that are read but whose values are not used (a staged merge has only the
+// two ranges' rows on the device).
+__device__ __forceinline__ uint32_t readable_id(const PruneCtx& p, uint32_t id) {
+  return p.staged && !resolvable(p, id) ? p.r1_lo : id;
 }
 
 // The left operand of a loaded row: L2 keeps the fp16 chunks; IP converts
@@ -85,7 +107,7 @@ __device__ __forceinline__ void left_from_row(const RowFrag<CPL>& xf, uint32_t q
 template <int CPL>
 __device__ __forceinline__ void load_member(const PruneCtx& p, const uint32_t* S_ids, uint32_t s, uint32_t ql,
                                             RowFrag<CPL>& x) {
-  load_row_frag<CPL>(p.vecs + (size_t)S_ids[s] * p.nchunks, ql, p.nchunks, true, x);
+  load_row_frag<CPL>(vec_row(p, readable_id(p, S_ids[s])), ql, p.nchunks, true, x);
 }
 
 // C: sorted keys [0, nc) in LDS. Writes the selection to S_ids / S_dist.
@@ -111,7 +133,7 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     // tested against members (SCALE: only when its vector is resolvable)
     const bool tested = !SCALE || resolvable(p, cid);
     RowFrag<CPL> xc;
-    load_row_frag<CPL>(p.vecs + (size_t)(valid ? cid : 0u) * p.nchunks, ql, p.nchunks, valid, xc);
+    load_row_frag<CPL>(vec_row(p, valid ? readable_id(p, cid) : p.r1_lo), ql, p.nchunks, valid, xc);
     LeftFrag<CPL, METRIC> cf;
     left_from_row<CPL, METRIC>(xc, ql, cf);
     bool pruned = false;
@@ -121,14 +143,14 @@ __device__ uint32_t robust_prune_wave(const PruneCtx& p, const uint64_t* C, uint
     if (ns0) {
       const uint32_t sid_lane = lane < ns0 ? S_ids[lane] : 0u;
       RowFrag<CPL> xn;
-      load_row_frag<CPL>(p.vecs + (size_t)(uint32_t)__builtin_amdgcn_readlane((int)sid_lane, 0) * p.nchunks, ql,
+      load_row_frag<CPL>(vec_row(p, readable_id(p, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, 0))), ql,
                          p.nchunks, true, xn);
       for (uint32_t s = 0; s < ns0; ++s) {
         const RowFrag<CPL> xs = xn;
         if (s + 1 < ns0)
-          load_row_frag<CPL>(p.vecs + (size_t)(uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)(s + 1)) *
-                                          p.nchunks,
-                             ql, p.nchunks, true, xn);
+          load_row_frag<CPL>(
+              vec_row(p, readable_id(p, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)(s + 1)))), ql,
+              p.nchunks, true, xn);
         if constexpr (SCALE) {
           if (!resolvable(p, (uint32_t)__builtin_amdgcn_readlane((int)sid_lane, (int)s))) continue;
         }

@@ -84,7 +84,7 @@ def lib():
         _lib.jo_diskann_assign.restype = i32
         _lib.jo_diskann_assign.argtypes = [P, i64, i32, i32, i32, i32, u64, P, P]
         _lib.jo_build_diskann.restype = i32
-        _lib.jo_build_diskann.argtypes = [P, i64, i32, i32, i32, i32, i32, f32, i32, i32, u64, i64, P, P, P, P,
+        _lib.jo_build_diskann.argtypes = [P, i64, i32, i32, i32, i32, i32, f32, i32, i32, u64, i64, i64, P, P, P, P,
                                           i32]
         _lib.jo_build_rq.restype = i32
         _lib.jo_build_rq.argtypes = [P, i64, i32, i32, i32, i32, f32, i64, i32, P, P, P, P, P, i32, P]
@@ -741,10 +741,11 @@ def diskann_batch_cap(n: int, R_int: int, n_parts: int, workspace_budget: int = 
 
 def build_diskann(vectors, R_int: int = 32, R_fin: int = 32, distance: str = "l2", alpha: float = 1.2,
                   n_parts: int = 4, n_dup: int = 2, seed: int = 42, workspace_budget: int = 10 ** 10,
-                  batch_cap: int | None = None, nthreads: int = 0) -> OracleGraph:
+                  batch_cap: int | None = None, max_shard: int = 0, nthreads: int = 0) -> OracleGraph:
     """The DiskANN build (reference index/construct_diskann.cuh:328-613): LSH
-    shards with duplication, one graph of degree R_int per shard, then the
-    distance-only merge into rows of R_fin. Global ids; medoid 0."""
+    shards with duplication, one graph of degree R_int per shard (a shard
+    above max_shard rows, when max_shard > 0, built as equal sub-shards),
+    then the distance-only merge into rows of R_fin. Global ids; medoid 0."""
     v16 = as_padded_f16(vectors)
     n, dp = v16.shape
     dim = np.asarray(vectors).shape[1]
@@ -755,8 +756,8 @@ def build_diskann(vectors, R_int: int = 32, R_fin: int = 32, distance: str = "l2
     counts = np.empty(n, dtype=np.uint8)
     shard_of = np.empty((n, n_dup), dtype=np.uint32)
     rc = lib().jo_build_diskann(_ptr(v16), n, dp, dim, R_int, R_fin, metric_code(distance), float(alpha), n_parts,
-                                n_dup, seed, batch_cap, _ptr(edges), _ptr(edist), _ptr(counts), _ptr(shard_of),
-                                nthreads)
+                                n_dup, seed, batch_cap, int(max_shard), _ptr(edges), _ptr(edist), _ptr(counts),
+                                _ptr(shard_of), nthreads)
     if rc != 0:
         raise ValueError("build_diskann: bad arguments")
     g = OracleGraph(v16, edges, edist, counts, R_fin, dim, distance)

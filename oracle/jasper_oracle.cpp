@@ -1128,8 +1128,8 @@ int jo_diskann_assign(const uint16_t* vecs, int64_t n, int dp, int dim, int n_pa
 // stably sorted by stored (bf16) distance, the first R_fin distinct ids
 // kept. Merges run one task after another. medoid = 0.
 int jo_build_diskann(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune, int R_int, int R_fin, int metric,
-                     float alpha, int n_parts, int n_dup, uint64_t seed, int64_t batch_cap, uint32_t* edges,
-                     uint16_t* edge_dist, uint8_t* counts, uint32_t* shard_of_out, int nthreads) {
+                     float alpha, int n_parts, int n_dup, uint64_t seed, int64_t batch_cap, int64_t max_shard,
+                     uint32_t* edges, uint16_t* edge_dist, uint8_t* counts, uint32_t* shard_of_out, int nthreads) {
   if (n <= 0 || R_int < 1 || R_fin < 1 || R_int > 255 || R_fin > 255 || batch_cap < 1) return -1;
   if (nthreads > 0) omp_set_num_threads(nthreads);
   std::vector<uint32_t> shard_of((size_t)n * n_dup);
@@ -1142,17 +1142,29 @@ int jo_build_diskann(const uint16_t* vecs, int64_t n, int dp, int dim_for_prune,
       const uint32_t s = shard_of[(size_t)v * n_dup + r];
       if (s != kInvalid32) shard_ids[s].push_back((uint32_t)v);
     }
-  std::vector<int> tasks;
-  for (int p = 0; p < n_parts; ++p)
-    if (!shard_ids[(size_t)p].empty()) tasks.push_back(p);
-  std::stable_sort(tasks.begin(), tasks.end(),
-                   [&](int a, int b) { return shard_ids[(size_t)a].size() > shard_ids[(size_t)b].size(); });
+  // build tasks (construct_diskann.cuh:386-417): a shard above max_shard
+  // rows (max_shard > 0) splits into equal sub-shards of its ascending ids;
+  // largest first, ties in (shard, sub-shard) order
+  struct Task {
+    int part;
+    int64_t begin, len;
+  };
+  std::vector<Task> tasks;
+  for (int p = 0; p < n_parts; ++p) {
+    const int64_t total = (int64_t)shard_ids[(size_t)p].size();
+    if (total == 0) continue;
+    const int64_t n_sub = max_shard > 0 ? (total + max_shard - 1) / max_shard : 1;
+    const int64_t sub = (total + n_sub - 1) / n_sub;
+    for (int64_t b = 0; b < total; b += sub) tasks.push_back({p, b, std::min(sub, total - b)});
+  }
+  std::stable_sort(tasks.begin(), tasks.end(), [](const Task& a, const Task& b) { return a.len > b.len; });
   std::fill(counts, counts + n, (uint8_t)0);
   std::fill(edges, edges + (size_t)n * R_fin, kInvalid32);
   std::fill(edge_dist, edge_dist + (size_t)n * R_fin, (uint16_t)0);
   g_capped_groups.store(0);
-  for (int p : tasks) {
-    const std::vector<uint32_t>& ids = shard_ids[(size_t)p];
+  for (const Task& task : tasks) {
+    const std::vector<uint32_t> ids(shard_ids[(size_t)task.part].begin() + task.begin,
+                                    shard_ids[(size_t)task.part].begin() + task.begin + task.len);
     const int64_t c = (int64_t)ids.size();
     std::vector<uint16_t> sv((size_t)c * dp);
     for (int64_t i = 0; i < c; ++i)

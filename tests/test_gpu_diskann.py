@@ -102,3 +102,22 @@ def test_diskann_bad_arguments(jasper):
         jasper.Graph.build_diskann(t, n_neighbors=8, r_int=8, n_parts=2, n_dup=17)
     with pytest.raises(ValueError):
         jasper.Graph.build_diskann(t, n_neighbors=8, r_int=65, n_parts=2, n_dup=2)
+
+
+@pytest.mark.parametrize("max_shard", [400, 999])
+def test_diskann_build_split_shards_matches_oracle(jasper, oracle_lib, max_shard):
+    """A shard graph cap (the device budget a shard may take) below the
+    shards' sizes: each shard is built as equal sub-shards of its ascending
+    ids, at most max_shard rows each, largest first
+    (construct_diskann.cuh:386-417), and merged as shards are; the graph
+    equals the oracle's with the same cap."""
+    x = integer_clustered(3000, 128, 53)
+    og = oracle.build_diskann(x, R_int=32, R_fin=32, n_parts=4, n_dup=2, batch_cap=25, max_shard=max_shard)
+    gg = jasper.Graph.build_diskann(torch.from_numpy(x).cuda(), n_neighbors=32, r_int=32, n_parts=4, n_dup=2,
+                                    max_batch_size=25, max_shard=max_shard)
+    _compare(gg, og)
+    st = jasper.last_diskann_stats()
+    sizes = np.bincount(og.shard_of[og.shard_of != 0xFFFFFFFF].ravel(), minlength=4)
+    subs = [-(-int(s) // max_shard) for s in sizes if s]
+    assert st["shards"] == sum(subs) and st["shards"] > int((sizes > 0).sum())
+    assert st["max_shard"] <= max_shard

@@ -101,3 +101,37 @@ def test_scale_empty_partition_rejected(jasper):
     t = torch.zeros((9, 8), dtype=torch.float16, device="cuda")
     with pytest.raises(ValueError):
         jasper.Graph.build_scale(t, n_neighbors=8, n_parts=4)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_scale_build_staged_matches_oracle(jasper, oracle_lib, case):
+    """on_host: the graph in pinned host memory, each partition built on the
+    device and written back, every merge with its two partitions staged
+    into two device slots (a partition shared with the previous pair stays
+    resident; five and six partitions switch cycles). The graph equals the
+    oracle's partitioned build edge for edge, as the in-HBM build does."""
+    name, make, R, distance, P, pb, mb = case
+    base = make()
+    print(f"staged case {name}: n={base.shape[0]} dim={base.shape[1]} R={R} {distance} P={P}", flush=True)
+    og = oracle.build_scale(base, R=R, distance=distance, alpha=1.2, n_parts=P, part_batch=pb,
+                            merge_batch=mb)
+    t = torch.from_numpy(np.ascontiguousarray(base))  # host rows
+    gg = jasper.Graph.build_scale(t, n_neighbors=R, distance=distance, alpha=1.2, n_parts=P,
+                                  workspace_budget=_budget(mb, R), max_batch_size=pb, on_host=True)
+    torch.cuda.synchronize()
+    _compare(gg, og)
+    st = jasper.last_scale_stats()
+    assert st["merges"] == P * (P - 1) // 2
+
+
+def test_scale_build_staged_then_search(jasper, oracle_lib):
+    base = integer_clustered(3000, 128, 38)
+    q = integer_clustered(300, 128, 39)
+    og = oracle.build_scale(base, R=32, n_parts=4, part_batch=30, merge_batch=128)
+    gg = jasper.Graph.build_scale(torch.from_numpy(base), n_neighbors=32, n_parts=4,
+                                  workspace_budget=_budget(128, 32), max_batch_size=30, on_host=True)
+    _compare(gg, og)
+    ids, d = gg.search(torch.from_numpy(q).cuda(), k=10, beam_width=64)
+    rid, rd = oracle.beam_search(og, q, k=10, beam_width=64)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.array_equal(d.cpu().numpy().view(np.uint32), rd.view(np.uint32))
