@@ -229,6 +229,8 @@ def main() -> int:
     ap.add_argument("--c5-n", type=int, default=100_000_000, help="base size of --path c5")
     ap.add_argument("--c4-m", type=int, default=120, help="PQ subspaces of --path c4 (120 = one per 8 dims)")
     ap.add_argument("--rotate-dim", type=int, default=128, help="row dimension of --path rotate (128 or 960)")
+    ap.add_argument("--no-build-roofline", action="store_true",
+                    help="skip the two extra builds that count the build's work and time its stages (profiler runs)")
     ap.add_argument("--no-general-path", action="store_true",
                     help="skip the child-process run with the integer-row shortcuts off (profiler runs)")
     ap.add_argument("--nq-sweep", default="",
@@ -286,7 +288,8 @@ def main() -> int:
         f"batches={int(bst['batches'])} max_batch={int(bst['max_batch'])}")
 
     build_total_ms = bst["total_ms"]
-    build_roof = build_roofline(jasper_amd, base_t, 64, build_s, build_total_ms, log)
+    build_roof = None if args.no_build_roofline else build_roofline(jasper_amd, base_t, 64, build_s, build_total_ms,
+                                                                     log)
 
     # ---- ground truth
     t0 = time.perf_counter()

@@ -80,8 +80,12 @@ static bool g_build_work = false;
 void set_build_work_counting(bool on) { g_build_work = on; }
 bool build_work_counting() { return g_build_work; }
 
-__device__ __forceinline__ void add_work(unsigned long long* w, int i, uint32_t v) {
-  if (v) atomicAdd(&w[i], (unsigned long long)v);
+// Work counters are kept in kWorkCopies copies (counter i, copy c at
+// i * kWorkCopies + c), a block adding to copy blockIdx % kWorkCopies, so
+// that a million waves do not serialise on one address; the host sums them.
+constexpr int kWorkCopies = 64;
+__device__ __forceinline__ void add_work(unsigned long long* w, int i, uint64_t v) {
+  if (v) atomicAdd(&w[i * kWorkCopies + (blockIdx.x & (kWorkCopies - 1))], (unsigned long long)v);
 }
 
 // Sums the search stage's per-query counters (hops, degrees, scored) and
@@ -102,10 +106,10 @@ __global__ __launch_bounds__(256) void search_work_kernel(const uint32_t* st, co
     v += __shfl_xor(v, o, 64);
   }
   if (lane_id() == 0) {
-    atomicAdd(&work[kWorkSearchHops], h);
-    atomicAdd(&work[kWorkSearchAdjacency], d);
-    atomicAdd(&work[kWorkSearchScored], s);
-    atomicAdd(&work[kWorkSearchVisited], v);
+    add_work(work, kWorkSearchHops, h);
+    add_work(work, kWorkSearchAdjacency, d);
+    add_work(work, kWorkSearchScored, s);
+    add_work(work, kWorkSearchVisited, v);
   }
 }
 
@@ -379,6 +383,7 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
   const uint32_t max_cands = kBuildMaxResult + R;
   uint32_t h = blockIdx.x;
   if (h >= nh) return;
+  uint64_t wk_targets = 0, wk_existing = 0, wk_sources = 0, wk_selected = 0;  // work counters (a.work)
   // the first pair of the next head is read one target ahead
   uint32_t start = a.heads[h];
   uint32_t w = (uint32_t)(a.sorted_pairs[start] >> a.pair_shift);
@@ -477,15 +482,19 @@ __global__ __launch_bounds__(64, (reverse_waves_per_simd<CPL, INTX, I8>())) void
       ns = robust_prune_wave<CPL, METRIC, INTX>(a.pc, l.C, nc, w, l.S_ids, l.S_dist);
     }
     write_selection(a, w, ns, l.S_ids, l.S_dist);
-    if (a.work && lane == 0) {
-      add_work(a.work, kWorkReverseTargets, 1u);
-      add_work(a.work, kWorkReverseExisting, nE);
-      add_work(a.work, kWorkReverseSources, taken);
-      add_work(a.work, kWorkReverseSelected, ns);
-    }
+    wk_targets += 1;
+    wk_existing += nE;
+    wk_sources += taken;
+    wk_selected += ns;
     wave_sync();
     start = start_next;
     w = w_next;
+  }
+  if (a.work && lane == 0) {
+    add_work(a.work, kWorkReverseTargets, wk_targets);
+    add_work(a.work, kWorkReverseExisting, wk_existing);
+    add_work(a.work, kWorkReverseSources, wk_sources);
+    add_work(a.work, kWorkReverseSelected, wk_selected);
   }
 }
 
@@ -767,8 +776,8 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
     if (seen_bytes > ((size_t)8 << 30))
       throw std::invalid_argument("build work counting needs " + std::to_string(seen_bytes >> 20) +
                                   " MiB of seen bitmap (limit 8 GiB): count a smaller build");
-    hip_check(hipMalloc(&wb.work, kWorkCount * 8), "alloc build work counters");
-    hip_check(hipMemsetAsync(wb.work, 0, kWorkCount * 8, stream), "clear build work counters");
+    hip_check(hipMalloc(&wb.work, kWorkCount * kWorkCopies * 8), "alloc build work counters");
+    hip_check(hipMemsetAsync(wb.work, 0, kWorkCount * kWorkCopies * 8, stream), "clear build work counters");
     hip_check(hipMalloc(&wb.qstats, (size_t)mb * 16), "alloc search counters");
     hip_check(hipMalloc(&wb.seen, std::max<size_t>(seen_bytes, 4)), "alloc seen bitmap");
     pa.work = wb.work;
@@ -840,10 +849,14 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
     hip_check(hipEventElapsedTime(&total, t0, t1), "event elapsed");
     st.total_ms = total;
     if (wb.work) {
-      uint64_t w[kWorkCount];
-      hip_check(hipMemcpy(w, wb.work, sizeof(w), hipMemcpyDeviceToHost), "read build work counters");
-      for (int i = 0; i < kWorkCount; ++i)
-        if (i != kWorkSearchQueries) st.work[i] = w[i];
+      std::vector<uint64_t> w((size_t)kWorkCount * kWorkCopies);
+      hip_check(hipMemcpy(w.data(), wb.work, w.size() * 8, hipMemcpyDeviceToHost), "read build work counters");
+      for (int i = 0; i < kWorkCount; ++i) {
+        if (i == kWorkSearchQueries) continue;
+        uint64_t sum = 0;
+        for (int c = 0; c < kWorkCopies; ++c) sum += w[(size_t)i * kWorkCopies + c];
+        st.work[i] = sum;
+      }
     }
   } catch (...) {
     (void)hipStreamSynchronize(stream);
