@@ -651,17 +651,28 @@ __device__ __forceinline__ void pq_lut_range(const uint16_t* q16, const float* c
   }
 }
 
-// Every query's LUT [nq, M * 256] in one launch, kLutWaveEntries entries per
-// wave, so the whole GPU builds them instead of one wave per query.
+// Rows of 256 entries per query in the tables the search reads: M rows,
+// then rows of -0.0f up to a multiple of 4 (the search adds the last
+// group of subspaces 4 rows at a time; x + (-0.0f) == x for every x under
+// round to nearest).
+__host__ __device__ constexpr uint32_t pq_lut_rows(uint32_t m) { return (m + 3u) / 4u * 4u; }
+
+// Every query's LUT [nq, pq_lut_rows(M) * 256] in one launch,
+// kLutWaveEntries entries per wave, so the whole GPU builds them instead of
+// one wave per query.
 constexpr uint32_t kLutWaveEntries = 64;
 __global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* __restrict__ queries, uint32_t dp, uint32_t M,
                                                     uint32_t dsub, const float* __restrict__ centroids,
                                                     float* __restrict__ lut) {
-  const uint32_t total = M * 256;
+  const uint32_t total = M * 256, stride = pq_lut_rows(M) * 256;
   const uint32_t e_begin = blockIdx.y * kLutWaveEntries;
+  float* out = lut + (size_t)blockIdx.x * stride;
+  if (e_begin >= total) {  // a pad row
+    for (uint32_t e = e_begin + threadIdx.x; e < min(stride, e_begin + kLutWaveEntries); e += 64) out[e] = -0.0f;
+    return;
+  }
   const uint32_t e_end = min(total, e_begin + kLutWaveEntries);
-  pq_lut_range(queries + (size_t)blockIdx.x * dp, centroids, dsub, e_begin, e_end,
-               lut + (size_t)blockIdx.x * total);
+  pq_lut_range(queries + (size_t)blockIdx.x * dp, centroids, dsub, e_begin, e_end, out);
 }
 
 // dsub <= 32: one table entry per thread. Block (b, j) holds the 256
@@ -683,12 +694,17 @@ __global__ __launch_bounds__(256) void pq_lut_small_kernel(const uint16_t* __res
                                                            float* __restrict__ lut) {
   const uint32_t j = blockIdx.y;
   const uint32_t e = j * 256 + threadIdx.x;
+  const size_t stride = (size_t)pq_lut_rows(M) * 256;
+  const int64_t q0 = (int64_t)blockIdx.x * kLutQueries;
+  const int64_t q1 = min(nq, q0 + (int64_t)kLutQueries);
+  if (j >= M) {  // a pad row
+    for (int64_t qi = q0; qi < q1; ++qi) lut[(size_t)qi * stride + e] = -0.0f;
+    return;
+  }
   const float* C = centroids + (size_t)e * dsub;
   float c[DS];
 #pragma unroll
   for (int t = 0; t < DS; ++t) c[t] = (uint32_t)t < dsub ? C[t] : 0.0f;
-  const int64_t q0 = (int64_t)blockIdx.x * kLutQueries;
-  const int64_t q1 = min(nq, q0 + (int64_t)kLutQueries);
   for (int64_t qi = q0; qi < q1; ++qi) {
     const uint16_t* qj = queries + (size_t)qi * dp + (size_t)j * dsub;
     float v[DS];
@@ -700,7 +716,7 @@ __global__ __launch_bounds__(256) void pq_lut_small_kernel(const uint16_t* __res
       for (int t = 0; t < h; ++t)
         if (t + h < DS) v[t] = v[t] + v[t + h];
     }
-    lut[(size_t)qi * M * 256 + e] = v[0];
+    lut[(size_t)qi * stride + e] = v[0];
   }
 }
 
@@ -727,7 +743,7 @@ struct DirArgs {
   const uint8_t* codes;  // edge-interleaved rows of code_row_bytes
   uint32_t code_row_bytes, pq_w, pq_groups;
   const float* norms;
-  const float* luts;  // [nq, M * 256] from pq_lut_kernel
+  const float* luts;  // [nq, pq_lut_rows(M) * 256] from pq_lut_kernel
   // RaBitQ
   const uint8_t* rq_nodes;     // [n, rq_node_bytes]: code dwords, f_add, f_rescale
   const float* rq_centroid;    // [rq_dim]
@@ -816,7 +832,14 @@ constexpr uint32_t kCountMerge = 16;
 // candidate buffer, rounded to 16 bytes).
 __host__ __device__ __forceinline__ uint32_t dir_mark_words(uint32_t cap) { return ((cap + 15u) & ~15u) / 8u; }
 
-template <int METRIC, int K, int P>
+// PQ table layouts in LDS (the last argument of directional_kernel): the
+// whole table; the first 4 groups of 16 subspaces and the last, partly
+// filled group, with the other groups' entries gathered from the table in
+// global memory; the first 4 groups, the rest gathered. The split layouts
+// (P = 8, more than 64 subspaces) let two queries' waves share a CU.
+constexpr int kLutWhole = 0, kLutSplitLast = 1, kLutSplit = 2;
+
+template <int METRIC, int K, int P, int LUT = kLutWhole>
 __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
   constexpr bool L2 = METRIC == kL2;
@@ -827,21 +850,32 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   const uint32_t qid = blockIdx.x;
   const uint32_t nchunks = a.dp / 8;
   const uint32_t cap = a.bw + a.R;
-  uint64_t* buf0 = smem;
+  // PQ: the query's table at the start of LDS, so that a table row's offset
+  // is a constant of the read instruction; the search state after it
+  // (rows: the whole padded table, or 64 and, with kLutSplitLast, the last
+  // group's)
+  const uint32_t lut_tail_rows = LUT == kLutSplitLast ? pq_lut_rows(a.M & 15u) : 0u;
+  const uint32_t lut_words = PQ ? ((LUT == kLutWhole ? pq_lut_rows(a.M) : 64u) + lut_tail_rows) * 128u : 0u;
+  uint64_t* sm = smem + lut_words;
+  uint64_t* buf0 = sm;
   uint64_t* buf1 = buf0 + cap;
   uint64_t* T = buf1 + cap;
   float* Fd = reinterpret_cast<float*>(T + 64);  // frontier distances (exact bits)
   uint32_t* Fi = reinterpret_cast<uint32_t*>(Fd + a.k);
   // marks of the new keys' positions in the general merge (nonzero = new)
-  uint8_t* MK = reinterpret_cast<uint8_t*>(smem + ((2 * cap + 64 + a.k + 1) & ~1u));
+  uint8_t* MK = reinterpret_cast<uint8_t*>(sm + ((2 * cap + 64 + a.k + 1) & ~1u));
   // LSH with 1-byte words (dp <= 128): q and q - u take 16 chunks each,
   // zero past dp, so any 7-bit coordinate reads inside them
   constexpr bool LSH8 = !PQ && !RQ && P == 1;
+  // split PQ layouts: groups 4 .. 7 may be gathered
+  constexpr int kGlobGroups = (PQ && P == 8 && LUT != kLutWhole) ? 4 : 0;
+  static_assert(LUT == kLutWhole || (PQ && P == 8), "split tables need 8 groups");
   const uint32_t qchunks = LSH8 ? 16u : nchunks;
-  uint4* qv = reinterpret_cast<uint4*>(smem + ((2 * cap + 64 + a.k + 1) & ~1u) + dir_mark_words(cap));  // 16-byte aligned
+  uint4* qv = reinterpret_cast<uint4*>(sm + ((2 * cap + 64 + a.k + 1) & ~1u) + dir_mark_words(cap));  // 16-byte aligned
   for (uint32_t i = lane; i < dir_mark_words(cap) * 2u; i += 64) reinterpret_cast<uint32_t*>(MK)[i] = 0u;
   uint4* xv = qv + qchunks;  // L2 LSH: fp16 q - u
-  float* lut = reinterpret_cast<float*>(xv + qchunks);  // PQ: the query's LUT; LSH: the bf16 sqrt table
+  // PQ: the query's LUT; LSH: the bf16 sqrt table
+  float* lut = PQ ? reinterpret_cast<float*>(smem) : reinterpret_cast<float*>(xv + qchunks);
 
   const uint4* qsrc = a.visited ? reinterpret_cast<const uint4*>(a.vecs) + (size_t)(a.q_start + qid) * nchunks
                                : reinterpret_cast<const uint4*>(a.queries) + (size_t)qid * nchunks;
@@ -861,11 +895,15 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
 
   float q_sq = 0.0f;
   if constexpr (PQ) {
-    // the query's LUT, built by pq_lut_kernel, into LDS
-    const uint32_t total4 = a.M * 64;
-    const float4* src = reinterpret_cast<const float4*>(a.luts + (size_t)qid * a.M * 256);
+    // the query's LUT, built by pq_lut_kernel, into LDS: every row, pad
+    // rows included, or the first 64 rows, then the last group's rows with
+    // kLutSplitLast
+    const float4* src = reinterpret_cast<const float4*>(a.luts + (size_t)qid * pq_lut_rows(a.M) * 256);
     float4* dst = reinterpret_cast<float4*>(lut);
-    for (uint32_t i = lane; i < total4; i += 64) dst[i] = src[i];
+    const uint32_t head4 = lut_words / 2u - lut_tail_rows * 64u;  // 16-byte chunks: rows * 64
+    for (uint32_t i = lane; i < head4; i += 64) dst[i] = src[i];
+    const uint32_t tail4 = lut_tail_rows * 64u, from4 = (a.M >> 4) * 16u * 64u;
+    for (uint32_t i = lane; i < tail4; i += 64) dst[head4 + i] = src[from4 + i];
     if constexpr (L2) {
       float p0 = 0.0f, p1 = 0.0f;
       for (uint32_t i = lane; i < a.dp; i += 128) {
@@ -1071,6 +1109,49 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     }
     float vnorm = 0.0f;
     if constexpr (PQ && L2) vnorm = valid_v ? a.norms[v_raw] : 0.0f;
+    // PQ: the table's group counts, re-read every hop so that the compiler
+    // tests them where they are used rather than holding every test's
+    // result in scalar registers across the loop. pq_q4: the last group's
+    // 4-row chunks (the rows past M hold -0.0f)
+    uint32_t pq_full = a.M >> 4, pq_q4 = ((a.M & 15u) + 3u) >> 2;
+    if constexpr (PQ) asm volatile("" : "+s"(pq_full), "+s"(pq_q4));
+    // split layouts, groups 4 .. 7: their entries from the query's LUT in
+    // global memory (the last group's, with kLutSplit, in 4-row chunks),
+    // issued here so that the gathers overlap the visit; group g lands in
+    // gv[(g - 4) * 16 + i]
+    float gv[kGlobGroups > 0 ? kGlobGroups * 16 : 1];
+    if constexpr (kGlobGroups > 0) {
+      if (valid_v) {
+        const float* gl = a.luts + (size_t)qid * pq_lut_rows(a.M) * 256;
+#pragma unroll
+        for (int h = 0; h < kGlobGroups; ++h) {
+          const int g = P - kGlobGroups + h;
+          {
+            const uint32_t w4[4] = {cw[g].x, cw[g].y, cw[g].z, cw[g].w};
+            // rows 4c .. 4c + 3: byte offset of entry (16g + 4c + j, code),
+            // below 512 KB, kept opaque so the load adds it to the table's
+            // base as a 32-bit offset
+            const auto gather = [&](int c) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                uint32_t off = (((uint32_t)g * 16u + 4u * c + j) << 10) + (((w4[c] >> (8 * j)) & 0xFFu) << 2);
+                asm volatile("" : "+v"(off));
+                gv[h * 16 + 4 * c + j] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gl) + off);
+              }
+            };
+            // 4 chunks in a full group, pq_q4 in the last
+            if ((uint32_t)g < pq_full) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) gather(c);
+            } else if (LUT == kLutSplit && (uint32_t)g == pq_full) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                if ((uint32_t)c < pq_q4) gather(c);
+            }
+          }
+        }
+      }
+    }
     // RaBitQ: the neighbour's code dwords and factors (a gather per edge,
     // issued before the visit so the two overlap)
     uint32_t rq_code[RQ ? P : 1];
@@ -1188,20 +1269,38 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
           est = __builtin_fmaf(rq_fres, ipq, rq_fadd + rq_gadd);
         } else if constexpr (PQ) {
           // acc = <q,u> + sum over j = 0, 1, ..., M - 1 of LUT[j][code_j], in
-          // that order (pq_beam_search.cuh:97-100)
+          // that order (pq_beam_search.cuh:97-100): the full groups of 16
+          // subspaces, then the last group's subspaces, each group from LDS
+          // or from the gathers as the layout places it
           float acc = qu_dot;
-          const uint32_t full = a.M >> 4, rem = a.M & 15u;
 #pragma unroll
           for (int g = 0; g < (PQ ? P : 1); ++g) {
             const uint32_t w4[4] = {cw[g].x, cw[g].y, cw[g].z, cw[g].w};
-            const float* lg = lut + g * 16 * 256;
-            if ((uint32_t)g < full) {
+            const bool past_lds = kGlobGroups > 0 && g >= P - kGlobGroups;
+            // a group past the first 4, but the last group with kLutSplitLast,
+            // comes from the gathers
+            const bool from_global = past_lds && (LUT == kLutSplit || (uint32_t)g < pq_full);
+            // with kLutSplitLast the last group's rows follow the first 64
+            const float* lg = lut + (past_lds ? 64u : (uint32_t)g * 16u) * 256u;
+            // rows 4c .. 4c + 3 of the group
+            const auto add4 = [&](int c) {
+              if (from_global) {
+                const int h = kGlobGroups > 0 ? g - (P - kGlobGroups) : 0;
 #pragma unroll
-              for (int i = 0; i < 16; ++i) acc = acc + lg[i * 256 + ((w4[i >> 2] >> (8 * (i & 3))) & 0xFFu)];
-            } else if ((uint32_t)g == full) {
+                for (int j = 0; j < 4; ++j) acc = acc + gv[h * 16 + 4 * c + j];
+              } else {
 #pragma unroll
-              for (int i = 0; i < 15; ++i)
-                if ((uint32_t)i < rem) acc = acc + lg[i * 256 + ((w4[i >> 2] >> (8 * (i & 3))) & 0xFFu)];
+                for (int j = 0; j < 4; ++j) acc = acc + lg[(4 * c + j) * 256 + ((w4[c] >> (8 * j)) & 0xFFu)];
+              }
+            };
+            // 4 chunks in a full group, pq_q4 in the last
+            if ((uint32_t)g < pq_full) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) add4(c);
+            } else if ((uint32_t)g == pq_full) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                if ((uint32_t)c < pq_q4) add4(c);
             }
           }
           est = L2 ? (q_sq - 2.0f * acc) + vnorm : -acc;
@@ -1752,7 +1851,8 @@ const uint16_t* directional_query_rows(const Graph& g, const void* queries, int6
   return rot;
 }
 
-size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
+// LDS of one query's wave, less the PQ table.
+size_t directional_base_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
   size_t lds = ((size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) + dir_mark_words((uint32_t)(bw + g.R))) * 8;
   if (est == kEstLsh) {
     // q and q - u (16 chunks each with 1-byte words), the sqrt table
@@ -1761,7 +1861,43 @@ size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
   } else {
     lds += (size_t)2 * g.dp * 2;
   }
-  if (est == kEstPq) lds += (size_t)g.pq->m * 256 * 4;
+  return lds;
+}
+
+// PQ: the table layout in LDS. A table of more than 64 subspaces leaves
+// room for one query per CU; when a launch has more queries than CUs, the
+// kernel keeps the first 4 groups of 16 subspaces in LDS, which lets two
+// queries share a CU (5 groups would be 80 KB alone), and gathers the
+// entries of the other groups from the table in global memory -- all but
+// the last group's when its rows fit in LDS beside the 4 (a full group and
+// the last group's rows save the same gathers per KB). The sum runs over
+// the subspaces in the same order in every layout.
+int pq_lut_layout(const Graph& g, int64_t k, int64_t bw, int64_t nq) {
+  const uint32_t m = g.pq->m;
+  if (m <= 64) return kLutWhole;
+  static const int cus = [] {
+    int dev = 0, c = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+      c = 256;
+    return c;
+  }();
+  const size_t base = directional_base_lds_bytes(g, kEstPq, k, bw);
+  const size_t half_cu = 80 * 1024, four = 64 * 1024;
+  if (nq <= cus || base + (size_t)pq_lut_rows(m) * 1024 <= half_cu || base + four > half_cu) return kLutWhole;
+  return m % 16 != 0 && base + four + (size_t)pq_lut_rows(m % 16) * 1024 <= half_cu ? kLutSplitLast : kLutSplit;
+}
+
+// LDS of one query's wave, with the PQ table in the given layout.
+size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw, int lut_layout = kLutWhole) {
+  size_t lds = directional_base_lds_bytes(g, est, k, bw);
+  if (est == kEstPq) {
+    const uint32_t m = g.pq->m;
+    const uint32_t rows = lut_layout == kLutWhole ? pq_lut_rows(m)
+                        : lut_layout == kLutSplitLast ? 64 + pq_lut_rows(m % 16)
+                                                      : 64;
+    lds += (size_t)rows * 1024;
+  }
   return lds;
 }
 
@@ -1796,13 +1932,13 @@ void check_directional_search(const Graph& g, int est, int64_t nq, int64_t dim, 
   } else if (est == kEstRabitq && (g.rabitq->dim != g.dim || g.rabitq->code_bytes > 32)) {
     throw std::invalid_argument("RaBitQ codes do not match the graph");
   }
-  if (directional_lds_bytes(g, est, k, bw) > 160 * 1024)
+  if (directional_lds_bytes(g, est, k, bw, use_pq ? pq_lut_layout(g, k, bw, nq) : kLutWhole) > 160 * 1024)
     throw std::invalid_argument("beam_width, k and dim need more than 160 KB of LDS");
 }
 
-template <int METRIC, int K, int P>
+template <int METRIC, int K, int P, int LUT = kLutWhole>
 void launch_directional(const DirArgs& a, uint32_t nq, size_t lds, hipStream_t stream) {
-  auto kern = directional_kernel<METRIC, K, P>;
+  auto kern = directional_kernel<METRIC, K, P, LUT>;
   if (lds > 64 * 1024)
     hip_check(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
               "LDS size");
@@ -1840,7 +1976,8 @@ void directional_search_run(Graph& g, int est, const void* queries, int64_t nq, 
   a.out_dists = out_dists;
   a.stats = stats;
   a.unique = unique ? 1u : 0u;
-  const size_t lds = directional_lds_bytes(g, est, k, bw);
+  const int lut_layout = use_pq ? pq_lut_layout(g, k, bw, nq) : kLutWhole;
+  const size_t lds = directional_lds_bytes(g, est, k, bw, lut_layout);
   const bool l2 = g.metric == kL2;
   if (est == kEstRabitq) {
     const RabitqArtifacts& rq = *g.rabitq;
@@ -1865,26 +2002,33 @@ void directional_search_run(Graph& g, int est, const void* queries, int64_t nq, 
     a.pq_w = pq_group_width(a.M);
     a.pq_groups = pq_groups(a.M);
     a.norms = g.vector_norms;
-    float* luts = (float*)scratch.take((size_t)nq * a.M * 256 * 4);
+    float* luts = (float*)scratch.take((size_t)nq * pq_lut_rows(a.M) * 256 * 4);
     const auto small_lut = [&](auto kern) {
-      const dim3 lgrid((uint32_t)((nq + kLutQueries - 1) / kLutQueries), a.M);
+      const dim3 lgrid((uint32_t)((nq + kLutQueries - 1) / kLutQueries), pq_lut_rows(a.M));
       hipLaunchKernelGGL(kern, lgrid, dim3(256), 0, stream, qsrc, nq, a.dp, a.M, a.dsub, a.centroids, luts);
     };
     if (a.dsub <= 8) small_lut(pq_lut_small_kernel<8>);
     else if (a.dsub <= 16) small_lut(pq_lut_small_kernel<16>);
     else if (a.dsub <= 32) small_lut(pq_lut_small_kernel<32>);
     else {
-      const dim3 lgrid((uint32_t)nq, (a.M * 256 + kLutWaveEntries - 1) / kLutWaveEntries);
+      const dim3 lgrid((uint32_t)nq, (pq_lut_rows(a.M) * 256 + kLutWaveEntries - 1) / kLutWaveEntries);
       hipLaunchKernelGGL(pq_lut_kernel, lgrid, dim3(64), 0, stream, qsrc, a.dp, a.M, a.dsub, a.centroids, luts);
     }
     hip_check(hipGetLastError(), "launch PQ table kernel");
     a.luts = luts;
+    const uint32_t n32 = (uint32_t)nq;
     if (a.M <= 16) {
-      if (l2) launch_directional<kL2, 0, 1>(a, (uint32_t)nq, lds, stream);
-      else launch_directional<kIP, 0, 1>(a, (uint32_t)nq, lds, stream);
+      if (l2) launch_directional<kL2, 0, 1>(a, n32, lds, stream);
+      else launch_directional<kIP, 0, 1>(a, n32, lds, stream);
+    } else if (lut_layout == kLutSplitLast) {
+      if (l2) launch_directional<kL2, 0, 8, kLutSplitLast>(a, n32, lds, stream);
+      else launch_directional<kIP, 0, 8, kLutSplitLast>(a, n32, lds, stream);
+    } else if (lut_layout == kLutSplit) {
+      if (l2) launch_directional<kL2, 0, 8, kLutSplit>(a, n32, lds, stream);
+      else launch_directional<kIP, 0, 8, kLutSplit>(a, n32, lds, stream);
     } else {
-      if (l2) launch_directional<kL2, 0, 8>(a, (uint32_t)nq, lds, stream);
-      else launch_directional<kIP, 0, 8>(a, (uint32_t)nq, lds, stream);
+      if (l2) launch_directional<kL2, 0, 8>(a, n32, lds, stream);
+      else launch_directional<kIP, 0, 8>(a, n32, lds, stream);
     }
   } else {
     a.K = g.lsh->k_ranks;
@@ -1967,7 +2111,7 @@ size_t directional_scratch_bytes(const Graph& g, int est, int64_t nq) {
   if (nq <= 0) return 0;
   const size_t rows = round256((size_t)nq * g.dp * 2);
   size_t b = rows + (g.prerotate ? rows : 0);
-  if (est == kEstPq && g.pq) b += round256((size_t)nq * g.pq->m * 256 * 4);
+  if (est == kEstPq && g.pq) b += round256((size_t)nq * pq_lut_rows(g.pq->m) * 256 * 4);
   return b;
 }
 

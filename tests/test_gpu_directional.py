@@ -182,6 +182,44 @@ def test_config4_shape(jasper, oracle_lib, tmp_path, pq_m):
           bws=(32, 64), pq_train=2000, pq_iters=3, pq_m=pq_m)
 
 
+@pytest.mark.parametrize("pq_m", [80, 96, 120])
+def test_pq_table_split(jasper, oracle_lib, pq_m):
+    """More queries than the device has CUs with a table of more than 64
+    subspaces: each query's wave keeps the first 4 groups of 16 subspaces'
+    table rows in LDS and reads the rest from global memory, so that two
+    queries share a CU. 600 queries at d = 960, R = 64, M = 80 (one group
+    gathered), 96 (two) and 120 (config 4: the last group's 8 rows in LDS
+    beside the first 4 groups at beam width 64, gathered with groups 4-6
+    at 256), plain and distinct-results traversals: bit-identical to the
+    oracle, and to the first 24 queries searched alone (a launch that keeps
+    the whole table in LDS)."""
+    from jasper_amd import datasets
+    dim, R = 960, 64
+    x = datasets.sparse_abs(1500, dim, 42)
+    q = datasets.sparse_abs(600, dim, 43)
+    xt = torch.from_numpy(x.astype(np.float16)).cuda()
+    print(f"[pq split] M={pq_m} n=1500 nq=600", flush=True)
+    gg = jasper.Graph.build(xt, n_neighbors=R, distance="l2", build_pq=True, prerotate=True, pq_train=1500,
+                            pq_kmeans_iter=2, pq_seed=11, pq_m=pq_m)
+    rows = gg.export_vectors()
+    g = oracle.build(rows.view(np.float16)[:, :dim].astype(np.float32), R=R, distance="l2", alpha=1.2)
+    cent, codes, norms = gg.export_pq()
+    assert np.array_equal(codes, oracle.pq_encode(g, pq_m, cent)), "PQ codes differ"
+    art = oracle.PqArtifacts(pq_m, g.dp // pq_m, cent, codes, norms)
+    q_rows = gg.directional_query_rows(torch.from_numpy(q.astype(np.float16)).cuda())
+    for bw in (64, 256):
+        for unique in (False, True):
+            print(f"[pq split] M={pq_m} bw={bw} unique={unique}", flush=True)
+            ids, d = _search(gg, "pq_search", q, 10, bw, unique=unique)
+            rid, rd = oracle.directional_search(g, q_rows, pq=art, k=10, beam_width=bw, unique=unique)
+            msg = compare_search(ids, d, rid, rd)
+            assert msg is None, f"M={pq_m} bw={bw} unique={unique}: {msg}"
+            ids24, d24 = _search(gg, "pq_search", q[:24], 10, bw, unique=unique)
+            msg = compare_search(ids24, d24, ids[:24], d[:24])
+            assert msg is None, f"M={pq_m} bw={bw} unique={unique}, 24 queries alone: {msg}"
+    gg.free()
+
+
 @pytest.mark.parametrize("pq_m", [8, 12, 24, 32])
 def test_pq_subspace_counts(jasper, oracle_lib, tmp_path, pq_m):
     """PQ at subspace counts between the reference's 4 and 16 and beyond:
