@@ -213,6 +213,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a 512 MiB device-to-device copy (3 times) first: the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--calibrate-gather", action="store_true",
+                    help="gather 1M random rows of 64, 128, 192 and 256 bytes (index_select from 256 MiB "
+                         "tables) first: reference kernels of known traffic for the counters of random reads")
     ap.add_argument("--path", default="search",
                     choices=["search", "directional", "pq", "bruteforce", "rotate", "rabitq", "c4", "c5", "c5plain",
                              "updates", "scale", "diskann"],
@@ -267,6 +270,19 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
         log("calibration copy: 3 x 512 MiB device-to-device")
+    if args.calibrate_gather:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(5)
+        for row_bytes in (64, 128, 192, 256):
+            rows = 256 * 2 ** 20 // row_bytes
+            table = torch.empty((rows, row_bytes // 2), dtype=torch.float16, device=dev)
+            idx = torch.randperm(rows, device=dev, generator=gen)[:2 ** 20]
+            torch.cuda.synchronize()
+            out = table.index_select(0, idx)
+            torch.cuda.synchronize()
+            del table, idx, out
+            log(f"calibration gather: 1,048,576 random rows of {row_bytes} B from a {rows}-row table "
+                f"({2 ** 20 * row_bytes} B gathered, 8 MiB of int64 indices)")
     if args.path != "search":
         return OTHER_PATHS[args.path](args, torch, jasper_amd, datasets, dev, log)
 
