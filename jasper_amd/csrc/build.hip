@@ -250,6 +250,9 @@ static float gram_margin_scale() {
 #define JASPER_GRAM8_WAVES 4
 #endif
 // The forward prune on byte rows takes the Gram form for up to 96 candidates.
+#ifndef JASPER_RQ_BUILD_L
+#define JASPER_RQ_BUILD_L kBuildL
+#endif
 #ifndef JASPER_FWD_GRAM
 #define JASPER_FWD_GRAM 1
 #endif
@@ -814,7 +817,7 @@ void build_range(Graph& g, float alpha, int64_t first, int64_t last, int64_t max
       }
       timer.start();
       if (rabitq_search)
-        rabitq_build_search(g, (uint32_t)count, (uint32_t)bs, kBuildL, kBuildLimit, kBuildMaxResult, ws.visited,
+        rabitq_build_search(g, (uint32_t)count, (uint32_t)bs, JASPER_RQ_BUILD_L, kBuildLimit, kBuildMaxResult, ws.visited,
                             ws.vcounts, stream);
       else
         launch_beam_search(g, r, stream);

@@ -374,7 +374,7 @@ __device__ __forceinline__ float quad_partial(const float (&qf)[CPL * 8], const 
 #pragma unroll
     for (int t = 0; t < CPL; ++t) {
       const uint32_t c = ql + 4u * (uint32_t)t;
-      if (c < nlimit) {
+      if (t < CPL - 1 || c < nlimit) {  // only the last slot can pass the row (CPL = ceil(chunks / 4))
         const uint32_t w[4] = {x[t].x, x[t].y, x[t].z, x[t].w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -387,11 +387,20 @@ __device__ __forceinline__ float quad_partial(const float (&qf)[CPL * 8], const 
     }
   } else {
     // element order within reference lane ql: chunk 0 (ql, ql+4), chunk 1, ...
+    // Rows and queries are zero-padded to whole chunks, so an element past
+    // nlimit inside the last chunk adds fma(0, 0, acc) == acc: acc starts at
+    // +0.0f and (+0) + (+-0) is +0 under round to nearest, so it is never
+    // -0.0f. Only chunks past the row are left out; with CPL = ceil(chunks
+    // / 4) those are among the last 4 slots, one uniform test each (a test
+    // per element was one mask per element, which the compiler held in
+    // scalar registers across the search loop and spilled).
+    const uint32_t nck = (nlimit + 7u) >> 3;
 #pragma unroll
     for (int t = 0; t < CPL; ++t) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int c = 4 * t + s;  // chunk index, held by quad lane s in slot t
+        if (c >= 4 * (CPL - 1) && (uint32_t)c >= nck) continue;
         uint32_t w[4];
         const uint32_t src[4] = {x[t].x, x[t].y, x[t].z, x[t].w};
 #pragma unroll
@@ -406,9 +415,8 @@ __device__ __forceinline__ float quad_partial(const float (&qf)[CPL * 8], const 
         const uint32_t w1 = (e1 >> 1) == 2 ? w[2] : w[3];
         const float v0 = (e0 & 1u) ? h2f_hi(w0) : h2f_lo(w0);
         const float v1 = (e1 & 1u) ? h2f_hi(w1) : h2f_lo(w1);
-        const uint32_t base = 8u * (uint32_t)c;
-        if (base + e0 < nlimit) acc = __builtin_fmaf(qf[2 * c], v0, acc);
-        if (base + e1 < nlimit) acc = __builtin_fmaf(qf[2 * c + 1], v1, acc);
+        acc = __builtin_fmaf(qf[2 * c], v0, acc);
+        acc = __builtin_fmaf(qf[2 * c + 1], v1, acc);
       }
     }
   }
@@ -442,7 +450,7 @@ __device__ __forceinline__ float quad_partial_l2h(const RowFrag<CPL>& qf, const 
 #pragma unroll
   for (int t = 0; t < CPL; ++t) {
     const uint32_t c = ql + 4u * (uint32_t)t;
-    if (c < nlimit) {
+    if (t < CPL - 1 || c < nlimit) {  // only the last slot can pass the row (CPL = ceil(chunks / 4))
       const uint32_t qw[4] = {qh[t].x, qh[t].y, qh[t].z, qh[t].w};
       const uint32_t w[4] = {x[t].x, x[t].y, x[t].z, x[t].w};
 #pragma unroll
@@ -573,7 +581,7 @@ __device__ __forceinline__ float quad_partial_l2_int(const RowFrag<CPL>& qf, con
 #pragma unroll
   for (int t = 0; t < CPL; ++t) {
     const uint32_t c = ql + 4u * (uint32_t)t;
-    if (c < nlimit) {
+    if (t < CPL - 1 || c < nlimit) {  // only the last slot can pass the row (CPL = ceil(chunks / 4))
       acc = dot2_sqdiff(qf.x[t].x, xf.x[t].x, acc);
       acc = dot2_sqdiff(qf.x[t].y, xf.x[t].y, acc);
       acc = dot2_sqdiff(qf.x[t].z, xf.x[t].z, acc);
