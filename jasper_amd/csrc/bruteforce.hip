@@ -325,11 +325,22 @@ __device__ __noinline__ void bf_append(uint32_t* qcount, uint64_t* qcand, uint32
 // (row srow[i], chunk scol[i]) of the ROWS-row tile starting at v0.
 // (native vector registers: a uint4 struct copied under a condition stays in
 // private memory)
+// offb[i]: the element's byte offset in a whole tile (srow[i] * nck +
+// scol[i] chunks), so a whole tile's loads add a per-thread constant to a
+// uniform base and need no address arithmetic; the chunk's last, partial
+// tile clamps its rows to the chunk.
 template <int PER, int ROWS, int METRIC>
 __device__ __forceinline__ void bf_gload(const uint4* base4, const float* vsq, int64_t v0, int64_t v_begin,
                                          int64_t v_end, uint32_t nck, uint32_t nel, uint32_t tid,
                                          const uint32_t (&srow)[PER], const uint32_t (&scol)[PER],
-                                         u32x4 (&stage)[PER], float& svs) {
+                                         const uint32_t (&offb)[PER], u32x4 (&stage)[PER], float& svs) {
+  if (v0 + ROWS <= v_end) {
+    const char* tb = reinterpret_cast<const char*>(base4 + (size_t)v0 * nck);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) stage[i] = *reinterpret_cast<const u32x4*>(tb + offb[i]);
+    if constexpr (METRIC == kL2) svs = vsq[v0 + (tid & (uint32_t)(ROWS - 1))];
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     // elements past the tile re-read chunk 0 of the first row and are not stored
@@ -362,8 +373,12 @@ __device__ __forceinline__ void bf_sstore(uint4* tile, float* tvs, uint32_t buf,
 
 // TILES: 32-query tiles per wave; SUB: 32-row base tiles per step (one
 // barrier per SUB tiles, SUB independent matrix-core chains per query tile).
+// Two waves per SIMD up to 128 values per row (the pipelined loop's two
+// accumulator sets then fit 256 registers: config 2, 1M x 128, 5.38 ms ->
+// 4.98 ms against one wave); wider rows keep one (two spill: 1M x 256,
+// 12.9 ms at one wave, 18.2 ms at two).
 template <int KS, int TILES, int SUB, int METRIC>
-__global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restrict__ base, int64_t n, uint32_t dp,
+__global__ __launch_bounds__(256, (KS <= 8 ? 2 : 1)) void bf_filter_kernel(const uint16_t* __restrict__ base, int64_t n, uint32_t dp,
                                                         const uint16_t* __restrict__ queries, int64_t nq,
                                                         const float* __restrict__ vsq, const float* __restrict__ qsq,
                                                         const float* __restrict__ qthr, uint32_t thr_stride,
@@ -440,12 +455,13 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
   // cooperative tile loads: thread element i is (row srow[i], chunk scol[i])
   constexpr int kPer = (ROWS * 2 * KS + 255) / 256;
   const uint32_t nel = ROWS * nck;
-  uint32_t srow[kPer], scol[kPer];
+  uint32_t srow[kPer], scol[kPer], offb[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const uint32_t e = tid + 256u * (uint32_t)i;
     srow[i] = e / nck;
     scol[i] = e % nck;
+    offb[i] = e < nel ? e * 16u : 0u;  // srow * nck + scol chunks; past the tile: chunk 0 of the first row
   }
   // base tiles: tile i is in LDS buffer i % 2 while tile i + 1 waits in
   // registers and tile i + 2 is loading, so a load has two steps of work to
@@ -453,20 +469,30 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
   u32x4 sta[kPer], stb[kPer];
   float sva = 0.0f, svb = 0.0f;
   if (v_begin < v_end) {
-    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v_begin, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v_begin, v_begin, v_end, nck, nel, tid, srow, scol, offb, sta, sva);
     bf_sstore<kPer, ROWS>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
-    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v_begin + ROWS, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v_begin + ROWS, v_begin, v_end, nck, nel, tid, srow, scol, offb, stb, svb);
   }
   __syncthreads();
   // every load issued so far (query fragments, first tiles) completes here:
   // otherwise the loop's first MFMA waits for all outstanding loads on every
   // iteration, the prefetched tile included
   __builtin_amdgcn_s_waitcnt(0);
-  auto step = [&](int64_t v0, uint32_t buf) {
-    // the chains of every (query tile, base sub-tile) interleaved; each
-    // accumulates over s in order, as bf_scan_kernel does: the distances
-    // must match it bit for bit
-    float16v accs[TILES][SUB];
+  // the cheap test's c_q of this lane's 16 rows per query tile (rows 8g +
+  // 4ah + j), held in registers for the whole loop
+  float cq[TILES][16];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cq[t][4 * g + j] = scr[(w * TILES + t) * 32 + 8 * g + 4 * ah + j];
+  // One tile's products: the chains of every (query tile, base sub-tile)
+  // interleaved; each accumulates over s in order, as bf_scan_kernel does
+  // (the distances must match it bit for bit). The tile's norms are taken
+  // into registers with it, so its LDS buffer is free once the MFMAs are
+  // issued.
+  auto mma = [&](uint32_t buf, float16v (&accs)[TILES][SUB], float (&vs)[SUB], float (&vsm)[SUB]) {
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
@@ -484,8 +510,14 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
     }
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
-      const float vs = tvs[buf * ROWS + 32u * u + am];
-      const float vsm = tvs[2 * ROWS + buf * ROWS + 32u * u + am];
+      vs[u] = tvs[buf * ROWS + 32u * u + am];
+      vsm[u] = tvs[2 * ROWS + buf * ROWS + 32u * u + am];
+    }
+  };
+  // One tile's tests and appends.
+  auto epi = [&](int64_t v0, const float16v (&accs)[TILES][SUB], const float (&vs)[SUB], const float (&vsm)[SUB]) {
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
       const int64_t v = v0 + 32 * u + am;
       const bool vok = v < v_end;
 #pragma unroll
@@ -494,13 +526,7 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
         if constexpr (METRIC == kL2) {
           uint64_t any = 0;  // lanes with a passing score, one compare mask per score
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint32_t row0 = 8u * (uint32_t)g + 4u * ah;
-            const float4 c4 = *reinterpret_cast<const float4*>(scr + (w * TILES + t) * 32 + row0);
-            const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) any |= ballot(__builtin_fmaf(2.0f, acc[4 * g + j], -vsm) >= cv[j]);
-          }
+          for (int i = 0; i < 16; ++i) any |= ballot(__builtin_fmaf(2.0f, acc[i], -vsm[u]) >= cq[t][i]);
           if (any == 0) continue;
         }
 #pragma unroll
@@ -513,7 +539,7 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             float d;
-            if constexpr (METRIC == kL2) d = __builtin_fmaf(-2.0f, acc[4 * g + j], qsv[j] + vs);
+            if constexpr (METRIC == kL2) d = __builtin_fmaf(-2.0f, acc[4 * g + j], qsv[j] + vs[u]);
             else d = -__half2float(__float2half_rn(acc[4 * g + j]));
             if (vok && d <= thv[j]) {
               if constexpr (METRIC == kL2) d = d < 0.0f ? 0.0f : d;
@@ -529,21 +555,41 @@ __global__ __launch_bounds__(256) void bf_filter_kernel(const uint16_t* __restri
       }
     }
   };
-  for (int64_t v0 = v_begin; v0 < v_end; v0 += 2 * ROWS) {
-    // tile v0 in buffer 0, tile v0 + ROWS in stb, tile v0 + 2 ROWS loads into sta.
-    // Loads and stores are unconditional (rows past the chunk are clamped
-    // reads, stored but never scored): with a conditional store the
-    // compiler cannot prove the staging registers free at the loop head and
-    // waits there for every load in flight, the prefetch included.
-    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v0 + 2 * ROWS, v_begin, v_end, nck, nel, tid, srow, scol, sta, sva);
-    step(v0, 0u);
+  // Software pipeline over tiles of ROWS rows: tile i + 1's MFMAs are
+  // issued before tile i's tests, so the matrix cores work while the VALU
+  // runs the tests. Invariant at the loop head: tile v0's products are in
+  // accA, tile v0 + ROWS is in LDS buffer 1 and tile v0 + 2 ROWS is loading
+  // into sta. A tile's LDS buffer is overwritten only after the barrier
+  // that follows its MFMAs' reads. Loads and stores are unconditional
+  // inside the loop (rows past the chunk are clamped reads, stored but
+  // never scored): with a conditional store the compiler cannot prove the
+  // staging registers free at the loop head and waits there for every load
+  // in flight, the prefetch included.
+  float16v accA[TILES][SUB], accB[TILES][SUB];
+  float vsA[SUB], vsmA[SUB], vsB[SUB], vsmB[SUB];
+  if (v_begin < v_end) {
+    mma(0u, accA, vsA, vsmA);
     bf_sstore<kPer, ROWS>(bf_tile, tvs, 1u, rs, nel, tid, srow, scol, stb, svb);
-    __syncthreads();
-    if (v0 + ROWS >= v_end) break;
-    // tile v0 + ROWS in buffer 1, tile v0 + 2 ROWS in sta, tile v0 + 3 ROWS loads into stb
-    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v0 + 3 * ROWS, v_begin, v_end, nck, nel, tid, srow, scol, stb, svb);
-    step(v0 + ROWS, 1u);
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v_begin + 2 * ROWS, v_begin, v_end, nck, nel, tid, srow, scol, offb, sta,
+                                 sva);
+  }
+  __syncthreads();
+  for (int64_t v0 = v_begin; v0 < v_end; v0 += 2 * ROWS) {
+    const bool more1 = v0 + ROWS < v_end;
+    if (more1) mma(1u, accB, vsB, vsmB);
+    epi(v0, accA, vsA, vsmA);
+    if (!more1) break;
+    // tile v0 + 2 ROWS into buffer 0, tile v0 + 3 ROWS loads into stb
     bf_sstore<kPer, ROWS>(bf_tile, tvs, 0u, rs, nel, tid, srow, scol, sta, sva);
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v0 + 3 * ROWS, v_begin, v_end, nck, nel, tid, srow, scol, offb, stb, svb);
+    __syncthreads();
+    const bool more2 = v0 + 2 * ROWS < v_end;
+    if (more2) mma(0u, accA, vsA, vsmA);
+    epi(v0 + ROWS, accB, vsB, vsmB);
+    if (!more2) break;
+    // tile v0 + 3 ROWS into buffer 1, tile v0 + 4 ROWS loads into sta
+    bf_sstore<kPer, ROWS>(bf_tile, tvs, 1u, rs, nel, tid, srow, scol, stb, svb);
+    bf_gload<kPer, ROWS, METRIC>(base4, vsq, v0 + 4 * ROWS, v_begin, v_end, nck, nel, tid, srow, scol, offb, sta, sva);
     __syncthreads();
   }
   // flush the staged candidates: one HBM slot reservation per query row
