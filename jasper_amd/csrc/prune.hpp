@@ -356,9 +356,11 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   constexpr int KS = I8 ? kGramMaxChunks / 4 : kGramMaxChunks / 2;
   const uint32_t lane = lane_id();
   const uint32_t r = lane & 31u, h = lane >> 5;
-  // per candidate i: U_i = T_i - |a_i|^2 (prune_int_threshold), so that
-  // "j prunes i" is |a_j|^2 - 2 a_i.a_j < U_i in exact integers
+  // per candidate i: U_i = T_i - |a_i|^2 (prune_int_threshold) in the
+  // registers of the lanes that hold i's column, |a_i|^2 in gu[i], so that
+  // "i prunes j" is |a_i|^2 - 2 a_i.a_j < U_j in exact integers
   int* gu = reinterpret_cast<int*>(gn);
+  int ucol[T];
 
   // MFMA operand of tile t, step s for candidate 32t + r, shifted; chunks
   // past the summed length are zero
@@ -391,7 +393,8 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
       }
       nrm[t] = acc + __shfl_xor(acc, 32, 64);  // below 2^24
-      if (h == 0) gu[i] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
+      ucol[t] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
+      if (h == 0) gu[i] = nrm[t];
     }
   } else if constexpr (I8 == 1) {
 #pragma unroll
@@ -429,7 +432,8 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
       }
       nrm[t] = acc + __shfl_xor(acc, 32, 64);  // below 2^24
-      if (h == 0) gu[i] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
+      ucol[t] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
+      if (h == 0) gu[i] = nrm[t];
     }
   } else {
 #pragma unroll
@@ -443,7 +447,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         const uint32_t c = 2u * (uint32_t)s + h;
         fr[t][s] = row[min(c, p.nchunks - 1u)];
       }
-      if (h == 0) gu[i] = prune_int_threshold(key_dist(key), p.alpha);
+      ucol[t] = prune_int_threshold(key_dist(key), p.alpha);
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -467,18 +471,22 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
     }
     wave_sync();
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-      if (h == 0) gu[32u * (uint32_t)t + r] -= nrm[t];
+    for (int t = 0; t < T; ++t) {
+      ucol[t] -= nrm[t];
+      if (h == 0) gu[32u * (uint32_t)t + r] = nrm[t];
+    }
   }
   wave_sync();
-  // rows 8g + 4h + q of a diagonal block that follow this lane's column r
+  // rows 8g + 4h + q of a diagonal block that precede this lane's column r
   uint32_t diagm = 0u;
 #pragma unroll
   for (int e = 0; e < 16; ++e)
-    if (r < (uint32_t)(8 * (e >> 2) + 4 * (int)h + (e & 3))) diagm |= 1u << e;
+    if ((uint32_t)(8 * (e >> 2) + 4 * (int)h + (e & 3)) < r) diagm |= 1u << e;
 
-  // W[t][t2], lane (r, h): bit b set when candidate 32 t + b is pruned by
-  // candidate 32 t2 + r (which precedes it): the column of the pair block
+  // W[t][t2] (t <= t2), lane (r, h): bit b set when candidate 32 t + b
+  // prunes candidate 32 t2 + r (which follows it): the block of rows t and
+  // columns t2 (the Gram matrix is symmetric), so the lanes of a candidate's
+  // column hold the candidates that prune it
   uint32_t W[T][T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -488,7 +496,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
 #pragma unroll
   for (int t = 0; t < T; ++t) {
 #pragma unroll
-    for (int t2 = 0; t2 <= t; ++t2) {
+    for (int t2 = t; t2 < T; ++t2) {
       gram_i16 ai;
       if constexpr (I8 != 0) {
         ai = gram_i16{};
@@ -503,18 +511,18 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
 #pragma unroll
         for (int e = 0; e < 16; ++e) ai[e] = (int)acc[e];  // exact: |a_i . a_j| < 2^24
       }
-      // lane holds column j = 32 t2 + r (whose norm it holds) and rows
-      // 32 t + 8g + 4h + q; bit 4g + q: j prunes that row, built from the
-      // top bit down
-      const int nj = nrm[t2];
+      // lane holds column j = 32 t2 + r (whose U_j it holds) and rows i =
+      // 32 t + 8g + 4h + q; bit 4g + q: i prunes j, built from the top bit
+      // down
+      const int uj = ucol[t2];
       uint32_t w16 = 0u;
 #pragma unroll
       for (int g = 3; g >= 0; --g) {
-        const int4 u = *reinterpret_cast<const int4*>(gu + 32 * t + 8 * g + 4 * h);
+        const int4 nn = *reinterpret_cast<const int4*>(gu + 32 * t + 8 * g + 4 * h);
 #pragma unroll
         for (int q = 3; q >= 0; --q) {
-          const int uq = q == 0 ? u.x : q == 1 ? u.y : q == 2 ? u.z : u.w;
-          w16 = (w16 << 1) | (nj - 2 * ai[4 * g + q] < uq ? 1u : 0u);
+          const int ni = q == 0 ? nn.x : q == 1 ? nn.y : q == 2 ? nn.z : nn.w;
+          w16 = (w16 << 1) | (ni - 2 * ai[4 * g + q] < uj ? 1u : 0u);
         }
       }
       if (t == t2) w16 &= diagm;
@@ -523,43 +531,47 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // column words by candidate: lane i % 64 of set A (candidates 0..63) or
-  // set B (64..95) holds, per row tile t, the rows that candidate prunes
-  uint32_t colA[T], colB[T];
+  // row words by candidate: lane i % 64 of set A (candidates 0..63) or set
+  // B (64..95) holds, per row tile t, the candidates of tile t that prune it
+  uint32_t rowA[T], rowB[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    colA[t] = T >= 2 && h ? W[t][T >= 2 ? 1 : 0] : W[t][0];
-    colB[t] = T == 3 ? W[t][T - 1] : 0u;
+    const uint32_t w0 = t == 0 ? W[0][0] : 0u;
+    const uint32_t w1 = T >= 2 && t <= 1 ? W[t][T >= 2 ? 1 : 0] : 0u;
+    rowA[t] = T >= 2 && h ? w1 : w0;
+    rowB[t] = T == 3 ? W[t][T - 1] : 0u;
   }
 
-  // selection: the first live candidate is taken and the candidates it
-  // prunes leave the live set (every one before it is already settled)
+  // selection (RobustPrune's greedy: a candidate is taken when no taken
+  // candidate before it prunes it) as the fixed point of S = {valid j : no
+  // i in S prunes j}: the relation only runs from earlier to later
+  // candidates, so the fixed point is unique and it is the greedy's set;
+  // iterating from S = every valid candidate reaches it in at most (the
+  // longest chain of the relation) + 1 rounds, each a few ANDs and two
+  // ballots. The cap of R keeps the first R of the set.
   const bool validA = lane < nc && key_id(C[lane]) != self;
   const bool validB = T == 3 && lane < 32u && 64u + lane < nc && key_id(C[64u + lane]) != self;
-  uint64_t liveA = ballot(validA), liveB = ballot(validB);
-  uint64_t selA = 0, selB = 0;
-  uint32_t ns = 0;
-  while (ns < p.R && (liveA | liveB)) {
-    uint32_t p0, p1, p2;
-    if (liveA) {
-      const uint32_t i = (uint32_t)__builtin_ctzll(liveA);
-      liveA &= liveA - 1u;
-      selA |= 1ull << i;
-      p0 = (uint32_t)__builtin_amdgcn_readlane((int)colA[0], (int)i);
-      p1 = T >= 2 ? (uint32_t)__builtin_amdgcn_readlane((int)colA[T >= 2 ? 1 : 0], (int)i) : 0u;
-      p2 = T == 3 ? (uint32_t)__builtin_amdgcn_readlane((int)colA[T - 1], (int)i) : 0u;
-    } else {
-      const uint32_t i = (uint32_t)__builtin_ctzll(liveB);
-      liveB &= liveB - 1u;
-      selB |= 1ull << i;
-      p0 = 0u;  // rows before the candidate are settled
-      p1 = 0u;
-      p2 = (uint32_t)__builtin_amdgcn_readlane((int)colB[T - 1], (int)i);
+  uint64_t selA = ballot(validA), selB = ballot(validB);
+  for (uint32_t round = 0; round <= kGramMaxCands; ++round) {
+    const uint32_t s0 = (uint32_t)selA, s1 = (uint32_t)(selA >> 32), s2 = (uint32_t)selB;
+    uint32_t hitA = rowA[0] & s0, hitB = rowB[0] & s0;
+    if constexpr (T >= 2) {
+      hitA |= rowA[1] & s1;
+      hitB |= rowB[1] & s1;
     }
-    liveA &= ~((uint64_t)p0 | ((uint64_t)p1 << 32));
-    liveB &= ~(uint64_t)p2;
-    ns += 1;
+    if constexpr (T == 3) {
+      hitA |= rowA[2] & s2;
+      hitB |= rowB[2] & s2;
+    }
+    const uint64_t nA = ballot(validA && hitA == 0u), nB = ballot(validB && hitB == 0u);
+    if (nA == selA && nB == selB) break;
+    selA = nA;
+    selB = nB;
   }
+  const uint32_t allA = (uint32_t)__builtin_popcountll(selA);
+  const uint32_t ns = min(p.R, allA + (uint32_t)__builtin_popcountll(selB));
+  selA = ballot(((selA >> lane) & 1ull) && mbcnt(selA) < p.R);
+  selB = ballot(lane < 32u && ((selB >> lane) & 1ull) && allA + mbcnt(selB) < p.R);
   // the selection in candidate order
   const uint32_t nA = (uint32_t)__builtin_popcountll(selA);
   if ((selA >> lane) & 1ull) {
