@@ -613,7 +613,6 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
   constexpr int KS = kGramMaxChunks / 2;
   const uint32_t lane = lane_id();
   const uint32_t r = lane & 31u, h = lane >> 5;
-  float* gcd = gn + kGramMaxCands;
   // chunks summed: L2 counts chunks, IP elements (padding past dim is zero)
   const uint32_t climit = METRIC == kL2 ? p.nlimit : (p.nlimit + 7u) / 8u;
   const float nsum = 8.0f * (float)climit;
@@ -621,7 +620,7 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
   const float sub = 1.2207031e-4f * sqrtf(nsum);  // 2^-13 * sqrt(n)
 
   uint4 fr[T][KS];
-  float nrm[T];
+  float nrm[T], cdc[T];  // the norm and distance of this lane's candidate 32 t + r
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const uint32_t i = 32u * (uint32_t)t + r;
@@ -633,7 +632,7 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
       const uint32_t c = 2u * (uint32_t)s + h;
       fr[t][s] = row[min(c, p.nchunks - 1u)];
     }
-    if (h == 0) gcd[i] = key_dist(key);
+    cdc[t] = key_dist(key);
   }
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -658,8 +657,11 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
   }
   wave_sync();
 
-  // P: proved pruned, A: not proved either way (column words as in
-  // robust_prune_gram)
+  // P: proved "i prunes j", A: not proved either way, for rows i of tile
+  // t <= column tile t2 (rows precede columns; the Gram matrix is
+  // symmetric): the lanes of column j = 32 t2 + r hold the bits of rows i =
+  // 32 t + 8g + 4h + q, so a candidate's lanes hold the candidates that may
+  // prune it
   uint32_t WP[T][T], WA[T][T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -672,23 +674,22 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
 #pragma unroll
   for (int t = 0; t < T; ++t) {
 #pragma unroll
-    for (int t2 = 0; t2 <= t; ++t2) {
+    for (int t2 = t; t2 < T; ++t2) {
       gram_f16 acc = {};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_gram_h8(fr[t][s]), as_gram_h8(fr[t2][s]), acc, 0, 0, 0);
       const float nj = nrm[t2];
       const float sj = sqrtf(nj);
+      const float cdj = cdc[t2];
       uint32_t wp = 0u, wa = 0u;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float4 ni = *reinterpret_cast<const float4*>(gn + 32 * t + 8 * g + 4 * h);
-        const float4 cd = *reinterpret_cast<const float4*>(gcd + 32 * t + 8 * g + 4 * h);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float gij = acc[4 * g + q];
           const float niq = q == 0 ? ni.x : q == 1 ? ni.y : q == 2 ? ni.z : ni.w;
-          const float cdq = q == 0 ? cd.x : q == 1 ? cd.y : q == 2 ? cd.z : cd.w;
           float d, e;
           if constexpr (METRIC == kL2) {
             d = (niq - gij) + (nj - gij);
@@ -698,12 +699,12 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
             e = U * (1.25f * nsum + 16.0f) * (niq + nj);
           }
           e += sub * (sqrtf(niq) + sj);
-          const float x = d * p.alpha - cdq;
-          const float m = p.margin_scale * 4.0f * (p.alpha * e + 2.0f * U * (fabsf(d * p.alpha) + fabsf(cdq)));
+          const float x = d * p.alpha - cdj;
+          const float m = p.margin_scale * 4.0f * (p.alpha * e + 2.0f * U * (fabsf(d * p.alpha) + fabsf(cdj)));
           bool pr = x < -m;
           bool am = !pr && !(x > m);  // NaN or infinite values: not proved
           if (t == t2) {
-            const bool before = r < (uint32_t)(8 * g + 4 * (int)h + q);
+            const bool before = (uint32_t)(8 * g + 4 * (int)h + q) < r;
             pr = pr && before;
             am = am && before;
           }
@@ -718,104 +719,130 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // row words by candidate (lane i % 64 of set A, candidates 0..63, or set
+  // B, 64..95): per row tile t, the candidates of tile t that prune it
+  // (pA, pB) or may (aA, aB)
   uint32_t pA[T], pB[T], aA[T], aB[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    pA[t] = T >= 2 && h ? WP[t][T >= 2 ? 1 : 0] : WP[t][0];
-    aA[t] = T >= 2 && h ? WA[t][T >= 2 ? 1 : 0] : WA[t][0];
+    const uint32_t tA = T >= 2 && h ? 1u : 0u;
+    pA[t] = (uint32_t)t <= tA ? (tA ? WP[t][T >= 2 ? 1 : 0] : WP[t][0]) : 0u;
+    aA[t] = (uint32_t)t <= tA ? (tA ? WA[t][T >= 2 ? 1 : 0] : WA[t][0]) : 0u;
     pB[t] = T == 3 ? WP[t][T - 1] : 0u;
     aB[t] = T == 3 ? WA[t][T - 1] : 0u;
   }
 
   const bool validA = lane < nc && key_id(C[lane]) != self;
   const bool validB = T == 3 && lane < 32u && 64u + lane < nc && key_id(C[64u + lane]) != self;
-  uint64_t liveA = ballot(validA), liveB = ballot(validB);
-  uint64_t selA = 0, selB = 0, pendA = 0, pendB = 0;
-  uint32_t ns = 0;
+  // Every pair the margin leaves open is settled by the chain (the
+  // reference's order, one quad per pair, 16 pairs per pass): its bit moves
+  // to the proved words when i prunes j.
   const uint32_t ql = lane & 3u, qg = lane >> 2;
-  while (ns < p.R && (liveA | liveB)) {
-    const bool inA = liveA != 0;
-    const uint32_t i = inA ? (uint32_t)__builtin_ctzll(liveA) : 64u + (uint32_t)__builtin_ctzll(liveB);
-    const bool pend = inA ? ((pendA >> i) & 1u) : ((pendB >> (i - 64u)) & 1u);
-    if (pend) {
-      // members j < i selected so far whose pair with i was not proved
-      const uint32_t ti = i >> 5, bi = i & 31u;
-      uint32_t wa = aA[0], wb = aB[0];
+  for (;;) {
+    uint32_t anyA = 0u, anyB = 0u;
 #pragma unroll
-      for (int t = 1; t < T; ++t) {
-        if (ti == (uint32_t)t) { wa = aA[t]; wb = aB[t]; }
-      }
-      uint64_t jm_a = ballot(((selA >> lane) & 1u) && ((wa >> bi) & 1u));
-      uint64_t jm_b = ballot(lane < 32u && ((selB >> lane) & 1u) && ((wb >> bi) & 1u));
-      const uint64_t ki = C[i];
-      const float cdi = key_dist(ki);
-      RowFrag<CPL> xi;
-      load_row_frag<CPL>(p.vecs + (size_t)key_id(ki) * p.nchunks, ql, p.nchunks, true, xi);
-      LeftFrag<CPL, METRIC> li;
-      left_from_row<CPL, METRIC>(xi, ql, li);
-      bool pruned = false;
-      while ((jm_a | jm_b) && !pruned) {
-        // up to 16 members per pass, one per quad
-        uint32_t jq = 0xFFFFFFFFu;
-        for (uint32_t g = 0; g < 16u && (jm_a | jm_b); ++g) {
-          uint32_t j;
-          if (jm_a) {
-            j = (uint32_t)__builtin_ctzll(jm_a);
-            jm_a &= jm_a - 1u;
-          } else {
-            j = 64u + (uint32_t)__builtin_ctzll(jm_b);
-            jm_b &= jm_b - 1u;
-          }
-          if (qg == g) jq = j;
+    for (int t = 0; t < T; ++t) {
+      anyA |= aA[t];
+      anyB |= aB[t];
+    }
+    uint64_t openA = ballot(validA && anyA != 0u), openB = ballot(validB && anyB != 0u);
+    if (!(openA | openB)) break;
+    // up to 16 pairs (i, j) in lane order of j, then row order of i
+    uint32_t iq = 0xFFFFFFFFu, jq = 0xFFFFFFFFu;
+    uint32_t cur_j = 0xFFFFFFFFu, w0 = 0u, w1 = 0u, w2 = 0u;
+    for (uint32_t g = 0; g < 16u; ++g) {
+      if (cur_j == 0xFFFFFFFFu || !(w0 | w1 | w2)) {
+        if (!(openA | openB)) break;
+        uint32_t src;
+        const bool inA = openA != 0;
+        if (inA) {
+          src = (uint32_t)__builtin_ctzll(openA);
+          openA &= openA - 1u;
+          cur_j = src;
+        } else {
+          src = (uint32_t)__builtin_ctzll(openB);
+          openB &= openB - 1u;
+          cur_j = 64u + src;
         }
-        const bool act = jq != 0xFFFFFFFFu;
-        const uint32_t jid = act ? key_id(C[jq]) : key_id(ki);
-        RowFrag<CPL> xj;
-        load_row_frag<CPL>(p.vecs + (size_t)jid * p.nchunks, ql, p.nchunks, true, xj);
-        const float d = left_distance<CPL, METRIC, false>(li, xj, ql, p.nchunks, p.nlimit);
-        pruned = ballot(act && d * p.alpha < cdi) != 0;
+        w0 = (uint32_t)__builtin_amdgcn_readlane((int)(inA ? aA[0] : aB[0]), (int)src);
+        w1 = T >= 2 ? (uint32_t)__builtin_amdgcn_readlane((int)(inA ? aA[T >= 2 ? 1 : 0] : aB[T >= 2 ? 1 : 0]), (int)src)
+                    : 0u;
+        w2 = T == 3 ? (uint32_t)__builtin_amdgcn_readlane((int)(inA ? aA[T - 1] : aB[T - 1]), (int)src) : 0u;
       }
-      if (inA) {
-        pendA &= ~(1ull << i);
+      uint32_t i;
+      if (w0) {
+        i = (uint32_t)__builtin_ctz(w0);
+        w0 &= w0 - 1u;
+      } else if (w1) {
+        i = 32u + (uint32_t)__builtin_ctz(w1);
+        w1 &= w1 - 1u;
       } else {
-        pendB &= ~(1ull << (i - 64u));
+        i = 64u + (uint32_t)__builtin_ctz(w2);
+        w2 &= w2 - 1u;
       }
-      if (pruned) {
-        if (inA) liveA &= ~(1ull << i);
-        else liveB &= ~(1ull << (i - 64u));
-        continue;
+      if (qg == g) {
+        iq = i;
+        jq = cur_j;
       }
     }
-    if (inA) {
-      liveA &= ~(1ull << i);
-      selA |= 1ull << i;
-    } else {
-      liveB &= ~(1ull << (i - 64u));
-      selB |= 1ull << (i - 64u);
-    }
-    ns += 1;
-    const uint32_t src = inA ? i : i - 64u;
-    uint32_t p0 = 0, p1 = 0, p2 = 0, a0 = 0, a1 = 0, a2 = 0;
-    if (inA) {
-      p0 = (uint32_t)__builtin_amdgcn_readlane((int)pA[0], (int)src);
-      a0 = (uint32_t)__builtin_amdgcn_readlane((int)aA[0], (int)src);
-      if constexpr (T >= 2) {
-        p1 = (uint32_t)__builtin_amdgcn_readlane((int)pA[T >= 2 ? 1 : 0], (int)src);
-        a1 = (uint32_t)__builtin_amdgcn_readlane((int)aA[T >= 2 ? 1 : 0], (int)src);
+    const bool act = jq != 0xFFFFFFFFu;
+    const uint64_t ki = act ? C[iq] : C[0];
+    const uint64_t kj = act ? C[jq] : C[0];
+    RowFrag<CPL> xj, xi;
+    load_row_frag<CPL>(p.vecs + (size_t)key_id(kj) * p.nchunks, ql, p.nchunks, true, xj);
+    load_row_frag<CPL>(p.vecs + (size_t)key_id(ki) * p.nchunks, ql, p.nchunks, true, xi);
+    LeftFrag<CPL, METRIC> lj;
+    left_from_row<CPL, METRIC>(xj, ql, lj);
+    // d(j, i) in the order the sequential prune computes it: the candidate
+    // j as the left operand, the member i as the row
+    const float d = left_distance<CPL, METRIC, false>(lj, xi, ql, p.nchunks, p.nlimit);
+    const uint64_t prq = ballot(act && ql == 0u && d * p.alpha < key_dist(kj));
+    const uint64_t doneq = ballot(act && ql == 0u);
+    // each settled pair: the owner lanes of j clear the open bit of i and
+    // set the proved bit when i prunes j
+    for (uint64_t m = doneq; m; m &= m - 1u) {
+      const uint32_t l = (uint32_t)__builtin_ctzll(m);
+      const uint32_t pi = (uint32_t)__builtin_amdgcn_readlane((int)iq, (int)l);
+      const uint32_t pj = (uint32_t)__builtin_amdgcn_readlane((int)jq, (int)l);
+      const bool pruned = (prq >> l) & 1ull;
+      const uint32_t ti = pi >> 5, bit = 1u << (pi & 31u);
+      const bool own = pj < 64u ? lane == pj : lane == pj - 64u;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if ((uint32_t)t != ti || !own) continue;
+        if (pj < 64u) {
+          aA[t] &= ~bit;
+          if (pruned) pA[t] |= bit;
+        } else {
+          aB[t] &= ~bit;
+          if (pruned) pB[t] |= bit;
+        }
       }
-      if constexpr (T == 3) {
-        p2 = (uint32_t)__builtin_amdgcn_readlane((int)pA[T - 1], (int)src);
-        a2 = (uint32_t)__builtin_amdgcn_readlane((int)aA[T - 1], (int)src);
-      }
-    } else {
-      p2 = (uint32_t)__builtin_amdgcn_readlane((int)pB[T - 1], (int)src);
-      a2 = (uint32_t)__builtin_amdgcn_readlane((int)aB[T - 1], (int)src);
     }
-    liveA &= ~((uint64_t)p0 | ((uint64_t)p1 << 32));
-    liveB &= ~(uint64_t)p2;
-    pendA |= ((uint64_t)a0 | ((uint64_t)a1 << 32)) & liveA;
-    pendB |= (uint64_t)a2 & liveB;
   }
+  // selection as the fixed point of S = {valid j : no i in S prunes j}
+  // (robust_prune_gram): the greedy's set, capped at the first R
+  uint64_t selA = ballot(validA), selB = ballot(validB);
+  for (uint32_t round = 0; round <= kGramMaxCands; ++round) {
+    const uint32_t s0 = (uint32_t)selA, s1 = (uint32_t)(selA >> 32), s2 = (uint32_t)selB;
+    uint32_t hitA = pA[0] & s0, hitB = pB[0] & s0;
+    if constexpr (T >= 2) {
+      hitA |= pA[1] & s1;
+      hitB |= pB[1] & s1;
+    }
+    if constexpr (T == 3) {
+      hitA |= pA[2] & s2;
+      hitB |= pB[2] & s2;
+    }
+    const uint64_t nA = ballot(validA && hitA == 0u), nB = ballot(validB && hitB == 0u);
+    if (nA == selA && nB == selB) break;
+    selA = nA;
+    selB = nB;
+  }
+  const uint32_t allA = (uint32_t)__builtin_popcountll(selA);
+  const uint32_t ns = min(p.R, allA + (uint32_t)__builtin_popcountll(selB));
+  selA = ballot(((selA >> lane) & 1ull) && mbcnt(selA) < p.R);
+  selB = ballot(lane < 32u && ((selB >> lane) & 1ull) && allA + mbcnt(selB) < p.R);
   const uint32_t nA = (uint32_t)__builtin_popcountll(selA);
   if ((selA >> lane) & 1ull) {
     const uint32_t k = mbcnt(selA);
