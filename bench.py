@@ -849,7 +849,6 @@ def run_c5(args, torch, jasper_amd, datasets, dev, log):
                              f"32768 samples, {nq} queries, k=10",
                  "build_vectors_per_s": n / build_s, "build_s": build_s, "lsh_s": lsh_s,
                  "build_max_batch": int(bst["max_batch"]),
-            "build_roofline": build_roof,
                  "exact_build_vectors_per_s": n / exact_build_s, "exact_build_s": exact_build_s,
                  "beam_width": bw, "unique": unique, "recall_at_10": rec, "target_recall": 0.9,
                  "curve": curve, "curve_rabitq_search": rq_curve, "curve_exact_search_rabitq_built": exact_rq,
