@@ -329,13 +329,27 @@ __device__ __forceinline__ uint32_t spread_nibbles(uint32_t w) {
 // The prune test d * alpha < cd (fp32) on an exact integer distance d is
 // d < T for one integer T per candidate: fl(d * alpha) is non-decreasing in
 // d for alpha >= 0, so the passing d form a prefix. T is the smallest d >= 0
-// that fails (found from cd / alpha and stepped to the boundary), or 2^30
-// when every d below it passes. Callers route alpha < 0 and NaN elsewhere.
-__device__ __forceinline__ int prune_int_threshold(float cd, float alpha) {
+// that fails, or 2^30 when every d below it passes. Callers route alpha < 0
+// and NaN elsewhere; inv_alpha is any estimate of 1 / alpha (it only places
+// the search).
+//
+// With d0 = floor(cd * inv_alpha) and b = max(d0 - 2, 0) the test is made
+// at b .. b + 5: when it passes at b and fails at b + 5 (or fails at b = 0)
+// the prefix ends among them, and T = b + (the passes among b .. b + 4).
+// For cd / alpha below 2^23 and inv_alpha within an ulp, T lies in
+// [d0 - 1, d0 + 3], so that window always holds it; otherwise the search
+// steps from d0 one value at a time to the boundary.
+__device__ __forceinline__ int prune_int_threshold(float cd, float alpha, float inv_alpha) {
   if (!(cd > 0.0f)) return 0;            // 0 * alpha < cd fails, and so does every d
   if (!(alpha > 0.0f)) return 1 << 30;   // alpha == 0: every d passes
-  const float q = cd / alpha;
+  const float q = cd * inv_alpha;
   int d = q >= 1073741824.0f ? (1 << 30) : (int)q;
+  const int b = max(d - 2, 0);
+  int n = 0;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) n += (float)(b + k) * alpha < cd ? 1 : 0;
+  const bool past = (float)(b + 5) * alpha < cd;
+  if (!past && (n > 0 || b == 0)) return min(b + n, 1 << 30);
   while (d < (1 << 30) && (float)d * alpha < cd) ++d;
   while (d > 0 && !((float)(d - 1) * alpha < cd)) --d;
   return d;
@@ -361,6 +375,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
   // "i prunes j" is |a_i|^2 - 2 a_i.a_j < U_j in exact integers
   int* gu = reinterpret_cast<int*>(gn);
   int ucol[T];
+  const float inv_alpha = 1.0f / p.alpha;  // places the threshold search
 
   // MFMA operand of tile t, step s for candidate 32t + r, shifted; chunks
   // past the summed length are zero
@@ -393,7 +408,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
       }
       nrm[t] = acc + __shfl_xor(acc, 32, 64);  // below 2^24
-      ucol[t] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
+      ucol[t] = prune_int_threshold(key_dist(key), p.alpha, inv_alpha) - nrm[t];
       if (h == 0) gu[i] = nrm[t];
     }
   } else if constexpr (I8 == 1) {
@@ -432,7 +447,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_sdot4((int)wd[u], (int)wd[u], acc, false);
       }
       nrm[t] = acc + __shfl_xor(acc, 32, 64);  // below 2^24
-      ucol[t] = prune_int_threshold(key_dist(key), p.alpha) - nrm[t];
+      ucol[t] = prune_int_threshold(key_dist(key), p.alpha, inv_alpha) - nrm[t];
       if (h == 0) gu[i] = nrm[t];
     }
   } else {
@@ -447,7 +462,7 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         const uint32_t c = 2u * (uint32_t)s + h;
         fr[t][s] = row[min(c, p.nchunks - 1u)];
       }
-      ucol[t] = prune_int_threshold(key_dist(key), p.alpha);
+      ucol[t] = prune_int_threshold(key_dist(key), p.alpha, inv_alpha);
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -477,11 +492,10 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
     }
   }
   wave_sync();
-  // rows 8g + 4h + q of a diagonal block that precede this lane's column r
-  uint32_t diagm = 0u;
-#pragma unroll
-  for (int e = 0; e < 16; ++e)
-    if ((uint32_t)(8 * (e >> 2) + 4 * (int)h + (e & 3)) < r) diagm |= 1u << e;
+  // rows 8g + 4h + q of a diagonal block that precede this lane's column r,
+  // at bit 8g + q: the bits below r - 4h that lie in the low nibbles
+  const int dm = (int)r - 4 * (int)h;
+  const uint32_t diagm8 = dm > 0 ? ((1u << dm) - 1u) & 0x0F0F0F0Fu : 0u;
 
   // W[t][t2] (t <= t2), lane (r, h): bit b set when candidate 32 t + b
   // prunes candidate 32 t2 + r (which follows it): the block of rows t and
@@ -512,21 +526,28 @@ __device__ uint32_t robust_prune_gram(const PruneCtx& p, const uint64_t* C, uint
         for (int e = 0; e < 16; ++e) ai[e] = (int)acc[e];  // exact: |a_i . a_j| < 2^24
       }
       // lane holds column j = 32 t2 + r (whose U_j it holds) and rows i =
-      // 32 t + 8g + 4h + q; bit 4g + q: i prunes j, built from the top bit
-      // down
-      const int uj = ucol[t2];
-      uint32_t w16 = 0u;
+      // 32 t + 8g + 4h + q; bit 8g + q: i prunes j, i.e. the sign of
+      // |a_i|^2 - (2 a_i.a_j + U_j) (no overflow: |a_i|^2 and |a_i.a_j| are
+      // below 2^24, U_j below 2^30), shifted in from the top bit down by one
+      // v_alignbit each, with a zero nibble between groups
+      const uint32_t uj = (uint32_t)ucol[t2];
+      uint32_t w = 0u;
 #pragma unroll
       for (int g = 3; g >= 0; --g) {
         const int4 nn = *reinterpret_cast<const int4*>(gu + 32 * t + 8 * g + 4 * h);
+        if (g < 3) w <<= 4;
 #pragma unroll
         for (int q = 3; q >= 0; --q) {
-          const int ni = q == 0 ? nn.x : q == 1 ? nn.y : q == 2 ? nn.z : nn.w;
-          w16 = (w16 << 1) | (ni - 2 * ai[4 * g + q] < uj ? 1u : 0u);
+          const uint32_t ni = (uint32_t)(q == 0 ? nn.x : q == 1 ? nn.y : q == 2 ? nn.z : nn.w);
+          // (the barrier keeps 2 a_i.a_j + U_j one v_lshl_add_u32, not
+          // reassociated into a shift, a subtraction and an addition)
+          uint32_t t2u = ((uint32_t)ai[4 * g + q] << 1) + uj;
+          asm volatile("" : "+v"(t2u));
+          w = __builtin_amdgcn_alignbit(w, ni - t2u, 31u);  // (w << 1) | sign bit
         }
       }
-      if (t == t2) w16 &= diagm;
-      const uint32_t w = spread_nibbles(w16) << (4u * h);  // rows 8g + 4h + q
+      if (t == t2) w &= diagm8;
+      w <<= 4u * h;  // rows 8g + 4h + q
       W[t][t2] = w | xor_lane<32>(w);
       __builtin_amdgcn_sched_barrier(0);
     }
