@@ -168,12 +168,19 @@ __device__ __forceinline__ void sort_candidates(uint64_t* C, uint32_t nc) {
 // Sorts a reverse target's candidates: C[0, nE) its existing edges in slot
 // order (stored bf16 distances), C[nE, nE + taken) its new sources. A stored
 // row is the output of an earlier prune, so its keys are usually ascending
-// already (ties of the rounded distances can break the id order): they are
-// sorted only when a lane finds its predecessor larger, the few sources are
-// sorted apart, and the two lists meet in one bitonic merge (64 wide when
-// they fit, else 128 wide over two registers) in place of a full sort of
-// both. The keys are distinct or identical 64-bit values, so the result is
-// the full sort's.
+// already; ties of the rounded distances can break the id order (on config
+// 2 one row in six, almost all of them one or two odd-even transposition
+// passes from sorted). The existing keys take such passes while a lane
+// finds its predecessor larger (the full bitonic sort after four). Up to
+// kInsertSources sources are then placed by counting: existing key e_i goes
+// to i + #{t_k <= e_i}, source t_j to #{t_k before t_j} + #{e_i < t_j}, with
+// one broadcast per source. More sources are sorted apart and the two lists
+// meet in one bitonic merge (64 wide when they fit, else 128 wide over two
+// registers). The keys are distinct or identical 64-bit values, so the
+// result is the full sort's.
+constexpr uint32_t kInsertSources = 8;
+constexpr int kOddEvenPasses = 4;
+
 __device__ __forceinline__ void sort_reverse_candidates(uint64_t* C, uint32_t nE, uint32_t taken) {
   const uint32_t nc = nE + taken;
   if (nE > 64u || taken > 64u) {
@@ -183,8 +190,39 @@ __device__ __forceinline__ void sort_reverse_candidates(uint64_t* C, uint32_t nE
   const uint32_t lane = lane_id();
   uint64_t e = lane < nE ? C[lane] : kEmptyKey;
   uint64_t t = lane < taken ? C[nE + lane] : kEmptyKey;
-  const uint64_t prev = __shfl_up(e, 1, 64);
-  if (ballot(lane > 0u && lane < nE && e < prev)) e = wave_bitonic_sort<64>(e);
+  // lanes past nE hold the largest key, so they never start a descent (the
+  // shuffles run in every lane: a lane reading an inactive one gets 0)
+  uint64_t prev = __shfl_up(e, 1, 64);
+  uint64_t desc = ballot(lane > 0u && e < prev);
+  if (desc) {
+    // odd phase partners (2i + 1, 2i + 2); lanes 0 and 63 pair with themselves
+    const int podd = (lane & 1u) ? (int)min(lane + 1u, 63u) : (int)(lane == 0u ? 0u : lane - 1u);
+    for (int pass = 0; desc != 0 && pass < kOddEvenPasses; ++pass) {
+      e = bitonic_stage<64, 1>(e, lane);  // even phase: pairs (2i, 2i + 1)
+      const uint64_t o = __shfl(e, podd, 64);
+      const bool lower = (lane & 1u) != 0u;  // the odd lane keeps the smaller key
+      e = lower ? (o < e ? o : e) : (o < e ? e : o);
+      prev = __shfl_up(e, 1, 64);
+      desc = ballot(lane > 0u && e < prev);
+    }
+    if (desc) e = wave_bitonic_sort<64>(e);
+  }
+  if (taken <= kInsertSources) {
+    uint32_t pe = lane, pt = 0;
+    for (uint32_t k = 0; k < taken; ++k) {
+      const uint64_t tk = readlane64(t, (int)k);
+      const bool e_lt = e < tk;
+      const uint32_t below = (uint32_t)__builtin_popcountll(ballot(lane < nE && e_lt));
+      pe += e_lt ? 0u : 1u;                                    // t_k <= e_i: t_k goes first
+      pt += (tk < t || (tk == t && k < lane)) ? 1u : 0u;       // t_k before t_j
+      pt += lane == k ? below : 0u;                            // e_i < t_j
+    }
+    wave_sync();  // every read of C precedes the writes below
+    if (lane < nE) C[pe] = e;
+    if (lane < taken) C[pt] = t;
+    wave_sync();
+    return;
+  }
   t = wave_sort_upto(t, taken);
   wave_sync();  // every read of C precedes the writes below
   // e ascending then the sources descending: a bitonic sequence of 128
