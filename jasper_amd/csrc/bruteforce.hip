@@ -109,7 +109,7 @@ __global__ __launch_bounds__(64) void bf_scan_kernel(const uint16_t* __restrict_
                                                      uint32_t k, uint32_t cap, int64_t chunk, uint32_t n_chunks,
                                                      uint64_t* __restrict__ out /* [nq][n_chunks][k] */,
                                                      const uint8_t* __restrict__ tile_flags) {
-  // cap = k + kBfStep rounded up to 8: candidate slots per query.
+  // cap >= k + kBfStep (a multiple of 8): candidate slots per query.
   // KS = 0: rows longer than 32 K steps; the query and base fragments are
   // read per slice of kBfSlice steps instead of held in registers.
   extern __shared__ uint64_t bf_lds[];
@@ -658,7 +658,13 @@ static void bf_one_pass(const void* base, int64_t n, uint32_t dp, const void* qu
   uint64_t* lists = nullptr;
   hip_check(hipMallocAsync((void**)&lists, (size_t)nq * n_chunks * k * 8, s), "alloc chunk lists");
   const dim3 grid((uint32_t)qtiles, n_chunks);
-  const uint32_t cap = (k + kBfStep + 7u) & ~7u;
+  // at least 64 slots: a buffer is compacted (a 64-key register sort, then
+  // every row's threshold reloaded) once it holds more than cap - kBfStep
+  // keys, so at k = 10 the 48 slots of k + kBfStep compacted each query
+  // after every 6 or so new candidates; 64 allow 22 between compactions
+  // and keep all of config 2's 1,878 work-groups resident (18.4 KB of LDS
+  // each): its 65,536-row sample scan 0.90 -> 0.77 ms
+  const uint32_t cap = std::max<uint32_t>((k + kBfStep + 7u) & ~7u, 64u);
   const size_t lds = ((size_t)32 * cap + kBfScratch) * 8;
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(64), lds, s, (const uint16_t*)base, n, dp, (const uint16_t*)queries, nq,
