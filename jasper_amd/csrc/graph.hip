@@ -201,8 +201,26 @@ __global__ void int_range_kernel(const uint4* __restrict__ v, size_t count8, int
     hi = fmaxf(hi, __shfl_xor(hi, d, 64));
   }
   const bool any_bad = __ballot(bad) != 0;
+  // one set of atomics per block (each on one of three words: the launch's
+  // thousands of waves contending for them had cost more than the scan)
+  __shared__ float s_lo[4], s_hi[4];
+  __shared__ int s_bad[4];
+  const uint32_t wv = threadIdx.x >> 6;
   if ((threadIdx.x & 63u) == 0) {
-    if (any_bad) atomicMax(&out[0], 1);
+    s_lo[wv] = lo;
+    s_hi[wv] = hi;
+    s_bad[wv] = any_bad ? 1 : 0;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t nw = blockDim.x >> 6;
+    for (uint32_t i = 1; i < nw; ++i) {
+      lo = fminf(lo, s_lo[i]);
+      hi = fmaxf(hi, s_hi[i]);
+    }
+    int b = 0;
+    for (uint32_t i = 0; i < nw; ++i) b |= s_bad[i];
+    if (b) atomicMax(&out[0], 1);
     atomicMin(&out[1], (int32_t)lo);
     atomicMax(&out[2], (int32_t)hi);
   }
@@ -327,7 +345,7 @@ static void scan_int_range_only(Graph& g, int64_t row0, int64_t n, hipStream_t s
   hip_check(hipMemcpyAsync(d, init, 12, hipMemcpyHostToDevice, stream), "init range");
   const size_t count8 = (size_t)n * g.dp / 8;  // dp is a multiple of 8
   const uint4* first = (const uint4*)g.vecs + (size_t)row0 * g.dp / 8;
-  const uint32_t grid = (uint32_t)std::min<size_t>((count8 + 255) / 256, 8192);
+  const uint32_t grid = (uint32_t)std::min<size_t>((count8 + 255) / 256, 1024);  // 4 blocks per CU
   hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, stream, first, count8, d);
   hip_check(hipGetLastError(), "launch int_range_kernel");
   int32_t h[3];
