@@ -678,11 +678,39 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
   }
   wave_sync();
 
+  // The margin, linear in a row term, a column term and |d|: with c1, c2
+  // the coefficients of e (L2: U (1.5 n + 16) and U (0.25 n + 8); IP:
+  // U (1.25 n + 16) and no |d| term), K1 = 4 ms |alpha| and
+  //   e = c1 (n_i + n_j) + c2 |d| + sub (sqrt n_i + sqrt n_j),
+  //   M = 4 ms (|alpha| e + 2 U (|alpha| |d| + |c_j|))
+  //     = a_i + C_j + K2 |d|,  a_i = K1 (c1 n_i + sub sqrt n_i),
+  //   C_j = K1 (c1 n_j + sub sqrt n_j) + 8 ms U |c_j|, K2 = K1 c2 + 8 ms U |alpha|
+  // (|alpha|: a sound bound for either sign). a_i sits in gn[96 + i].
+  const float aalpha = fabsf(p.alpha);
+  const float K1 = p.margin_scale * 4.0f * aalpha;
+  const float c1 = METRIC == kL2 ? U * (1.5f * nsum + 16.0f) : U * (1.25f * nsum + 16.0f);
+  const float c2 = METRIC == kL2 ? U * (0.25f * nsum + 8.0f) : 0.0f;
+  const float K2 = K1 * c2 + p.margin_scale * 8.0f * U * aalpha;
+  float ccol[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const float sn = sqrtf(nrm[t]);
+    ccol[t] = K1 * (c1 * nrm[t] + sub * sn) + p.margin_scale * 8.0f * U * fabsf(cdc[t]);
+    if (h == 0) gn[kGramMaxCands + 32u * (uint32_t)t + r] = K1 * (c1 * nrm[t] + sub * sn);
+  }
+  wave_sync();
+  // rows 8g + 4h + q of a diagonal block that precede this lane's column r,
+  // at bit 8g + q
+  const int dm = (int)r - 4 * (int)h;
+  const uint32_t diagm8 = dm > 0 ? ((1u << dm) - 1u) & 0x0F0F0F0Fu : 0u;
+
   // P: proved "i prunes j", A: not proved either way, for rows i of tile
   // t <= column tile t2 (rows precede columns; the Gram matrix is
   // symmetric): the lanes of column j = 32 t2 + r hold the bits of rows i =
   // 32 t + 8g + 4h + q, so a candidate's lanes hold the candidates that may
-  // prune it
+  // prune it. With x = d alpha - c_j: proved when x + M < 0, not proved
+  // when additionally M - x >= 0 fails neither (NaN sums count as not
+  // proved); each bit is a sign shifted in by one v_alignbit.
   uint32_t WP[T][T], WA[T][T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -701,40 +729,38 @@ __device__ uint32_t robust_prune_gram_f(const PruneCtx& p, const uint64_t* C, ui
       for (int s = 0; s < KS; ++s)
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_gram_h8(fr[t][s]), as_gram_h8(fr[t2][s]), acc, 0, 0, 0);
       const float nj = nrm[t2];
-      const float sj = sqrtf(nj);
       const float cdj = cdc[t2];
-      uint32_t wp = 0u, wa = 0u;
+      const float cj = ccol[t2];
+      uint32_t wy = 0u, wz = 0u;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int g = 3; g >= 0; --g) {
         const float4 ni = *reinterpret_cast<const float4*>(gn + 32 * t + 8 * g + 4 * h);
+        const float4 ai = *reinterpret_cast<const float4*>(gn + kGramMaxCands + 32 * t + 8 * g + 4 * h);
+        if (g < 3) {
+          wy <<= 4;
+          wz <<= 4;
+        }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 3; q >= 0; --q) {
           const float gij = acc[4 * g + q];
           const float niq = q == 0 ? ni.x : q == 1 ? ni.y : q == 2 ? ni.z : ni.w;
-          float d, e;
-          if constexpr (METRIC == kL2) {
-            d = (niq - gij) + (nj - gij);
-            e = U * (1.5f * nsum + 16.0f) * (niq + nj) + U * (0.25f * nsum + 8.0f) * fabsf(d);
-          } else {
-            d = -gij;
-            e = U * (1.25f * nsum + 16.0f) * (niq + nj);
-          }
-          e += sub * (sqrtf(niq) + sj);
-          const float x = d * p.alpha - cdj;
-          const float m = p.margin_scale * 4.0f * (p.alpha * e + 2.0f * U * (fabsf(d * p.alpha) + fabsf(cdj)));
-          bool pr = x < -m;
-          bool am = !pr && !(x > m);  // NaN or infinite values: not proved
-          if (t == t2) {
-            const bool before = (uint32_t)(8 * g + 4 * (int)h + q) < r;
-            pr = pr && before;
-            am = am && before;
-          }
-          wp |= pr ? (1u << (4 * g + q)) : 0u;
-          wa |= am ? (1u << (4 * g + q)) : 0u;
+          const float aiq = q == 0 ? ai.x : q == 1 ? ai.y : q == 2 ? ai.z : ai.w;
+          const float d = METRIC == kL2 ? (niq - gij) + (nj - gij) : -gij;
+          const float x = __builtin_fmaf(d, p.alpha, -cdj);
+          const float m = __builtin_fmaf(K2, fabsf(d), aiq + cj);
+          const float y = fminf(x + m, __builtin_inff());  // NaN -> +inf: not proved
+          const float z = fminf(m - x, __builtin_inff());
+          wy = __builtin_amdgcn_alignbit(wy, __float_as_uint(y), 31u);
+          wz = __builtin_amdgcn_alignbit(wz, __float_as_uint(z), 31u);
         }
       }
-      const uint32_t sp = spread_nibbles(wp) << (4u * h);
-      const uint32_t sa = spread_nibbles(wa) << (4u * h);
+      uint32_t wp = wy, wa = ~(wy | wz) & 0x0F0F0F0Fu;
+      if (t == t2) {
+        wp &= diagm8;
+        wa &= diagm8;
+      }
+      const uint32_t sp = wp << (4u * h);
+      const uint32_t sa = wa << (4u * h);
       WP[t][t2] = sp | xor_lane<32>(sp);
       WA[t][t2] = sa | xor_lane<32>(sa);
       __builtin_amdgcn_sched_barrier(0);
