@@ -304,8 +304,17 @@ static_assert(kGramLdsWords <= kCandBuf, "the Gram prune's scratch reuses the so
 // index/construct_scale_kernels.cuh:193-194).
 // BYTES: the graph keeps byte rows (CPL 4, L2, integer rows): the prune
 // works on them (robust_prune_wave_u8)
+// The forward prune takes the Gram prune wherever the reverse prune does
+// (rows of up to 128 values, at most 96 candidates): on byte rows the
+// integer form at four waves per SIMD, on other rows the fp16 integer form
+// or the form with proof at two.
+template <int CPL, int METRIC, bool INTX, bool SCALE, bool BYTES>
+constexpr int forward_waves_per_simd() {
+  return !SCALE && JASPER_FWD_GRAM ? (BYTES ? JASPER_GRAM8_WAVES : CPL >= 1 && CPL <= 4 ? JASPER_GRAM_WAVES : 1) : 1;
+}
+
 template <int CPL, int METRIC, bool INTX, bool SCALE, bool BYTES = false>
-__global__ __launch_bounds__(64, (BYTES && !SCALE && JASPER_FWD_GRAM ? JASPER_GRAM8_WAVES : 1)) void
+__global__ __launch_bounds__(64, (forward_waves_per_simd<CPL, METRIC, INTX, SCALE, BYTES>())) void
 forward_prune_kernel(PruneKernelArgs a) {
   static_assert(!BYTES || (CPL == 4 && METRIC == kL2 && INTX), "byte rows: integer L2 rows of 112/128");
   extern __shared__ uint64_t smem[];
@@ -345,6 +354,24 @@ forward_prune_kernel(PruneKernelArgs a) {
     else ns = robust_prune_wave_u8<SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   } else if constexpr (BYTES) {
     ns = robust_prune_wave_u8<SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+  } else if constexpr (!SCALE && JASPER_FWD_GRAM && CPL >= 1 && CPL <= 4) {
+    // the reverse prune's choice: pair distances on the matrix cores, exact
+    // for integer rows (alpha >= 0), proved otherwise
+    const uint32_t climit = METRIC == kL2 ? a.pc.nlimit : (a.pc.nlimit + 7u) / 8u;
+    float* gn = reinterpret_cast<float*>(l.srcs);
+    if (nc <= kGramMaxCands && climit <= kGramMaxChunks && (!INTX || a.pc.alpha >= 0.0f)) {
+      if constexpr (INTX) {
+        if (nc <= 32) ns = robust_prune_gram<1, 0>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+        else if (nc <= 64) ns = robust_prune_gram<2, 0>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+        else ns = robust_prune_gram<3, 0>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+      } else {
+        if (nc <= 32) ns = robust_prune_gram_f<1, CPL, METRIC>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+        else if (nc <= 64) ns = robust_prune_gram_f<2, CPL, METRIC>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+        else ns = robust_prune_gram_f<3, CPL, METRIC>(a.pc, l.C, nc, v, l.S_ids, l.S_dist, gn);
+      }
+    } else {
+      ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
+    }
   } else {
     ns = robust_prune_wave<CPL, METRIC, INTX, SCALE>(a.pc, l.C, nc, v, l.S_ids, l.S_dist);
   }
