@@ -302,6 +302,14 @@ def main() -> int:
     bst = jasper_amd.last_build_stats()
     log(f"build {args.n} vectors in {build_s:.2f}s ({args.n / build_s:.0f} vec/s), "
         f"batches={int(bst['batches'])} max_batch={int(bst['max_batch'])}")
+    # the same build again in this process: the first one also pays the
+    # one-time loading of the build's code objects at their first launches
+    t0 = time.perf_counter()
+    g_rep = jasper_amd.Graph.build(base_t, n_neighbors=64, distance="l2", alpha=1.2)
+    torch.cuda.synchronize()
+    build_repeat_s = time.perf_counter() - t0
+    g_rep.free()
+    log(f"build again in the same process: {build_repeat_s:.3f}s ({args.n / build_repeat_s:.0f} vec/s)")
 
     build_total_ms = bst["total_ms"]
     build_roof = None if args.no_build_roofline else build_roofline(jasper_amd, base_t, 64, build_s, build_total_ms,
@@ -396,6 +404,8 @@ def main() -> int:
             "target_recall": args.target_recall,
             "build_vectors_per_s": args.n / build_s,
             "build_s": build_s,
+            "build_repeat_vectors_per_s": args.n / build_repeat_s,
+            "build_repeat_s": build_repeat_s,
             "build_max_batch": int(bst["max_batch"]),
             "build_roofline": build_roof,
             "storage": ("fp16 vectors; the search reads byte rows (value - lo) for integer rows spanning "
