@@ -338,7 +338,8 @@ __device__ __forceinline__ uint32_t spread_nibbles(uint32_t w) {
 // the prefix ends among them, and T = b + (the passes among b .. b + 4).
 // For cd / alpha below 2^23 and inv_alpha within an ulp, T lies in
 // [d0 - 1, d0 + 3], so that window always holds it; otherwise the search
-// steps from d0 one value at a time to the boundary.
+// steps one value at a time to the boundary from floor(cd / alpha), as it
+// did before the window.
 __device__ __forceinline__ int prune_int_threshold(float cd, float alpha, float inv_alpha) {
   if (!(cd > 0.0f)) return 0;            // 0 * alpha < cd fails, and so does every d
   if (!(alpha > 0.0f)) return 1 << 30;   // alpha == 0: every d passes
@@ -350,6 +351,10 @@ __device__ __forceinline__ int prune_int_threshold(float cd, float alpha, float 
   for (int k = 0; k < 5; ++k) n += (float)(b + k) * alpha < cd ? 1 : 0;
   const bool past = (float)(b + 5) * alpha < cd;
   if (!past && (n > 0 || b == 0)) return min(b + n, 1 << 30);
+  // the stepped search from the quotient itself (cd * inv_alpha can be far
+  // off, e.g. infinite for a subnormal alpha, where cd / alpha is not)
+  const float q2 = cd / alpha;
+  d = q2 >= 1073741824.0f ? (1 << 30) : (int)q2;
   while (d < (1 << 30) && (float)d * alpha < cd) ++d;
   while (d > 0 && !((float)(d - 1) * alpha < cd)) --d;
   return d;
