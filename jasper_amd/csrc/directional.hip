@@ -366,6 +366,121 @@ __global__ __launch_bounds__(64) void lsh_populate_kernel(const uint16_t* __rest
   }
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ void cx_desc(uint32_t& a, uint32_t& b) {
+  const uint32_t hi = max(a, b), lo = min(a, b);
+  a = hi;
+  b = lo;
+}
+
+// populate_lsh for rows of at most 128 coordinates and at most 64 edges
+// (the same words and magnitudes as lsh_populate_kernel). Each row of 16
+// lanes takes one edge, four edges per wave at a time; lane j holds
+// coordinates 8j..8j+7 of the edge's difference vector.
+//  - Keys: the key of coordinate i is (|d| bits, sign, i), unique for
+//    nonzero keys. The K largest, in descending order, are the words the
+//    repeated wave-max extracts. Each lane sorts its eight keys (a
+//    19-comparator network), then each of the K rounds takes the row's
+//    largest head by four DPP max steps (xor 1, xor 2 in the quad, half-row
+//    and row mirrors), and the lane holding it shifts its list up. Lane r
+//    keeps round r's word. A round whose largest head is 0 outputs word 0,
+//    as the wave-max does when only zero keys remain.
+//  - Magnitude: the 128-thread reduction of the squares, virtual thread t
+//    holding coordinate t. Warp w's butterfly tree (strides 16, 8, 4, 2, 1
+//    over its 32 coordinates) has lanes 4w..4w+3 of the row: stride 16 is
+//    lane xor 2, stride 8 lane xor 1, and strides 4, 2, 1 stay inside the
+//    lane. Lane 0 then forms (W0 + W2) + (W1 + W3) by row shifts of 8 and
+//    4.
+//  - Edges past the vertex's count (and slots of a partial group) take
+//    zero keys and squares, which give the zero words and magnitude that
+//    the row holds there.
+__global__ __launch_bounds__(256) void lsh_populate_rows_kernel(const uint16_t* __restrict__ vecs, int64_t n,
+                                                                uint32_t dp, const uint32_t* __restrict__ edges,
+                                                                const uint8_t* __restrict__ counts, uint32_t R,
+                                                                uint32_t K, uint32_t pbytes,
+                                                                uint8_t* __restrict__ rows, uint32_t row_bytes) {
+  const uint32_t lane = threadIdx.x & 63u, j = lane & 15u, g = lane >> 4;
+  const uint32_t coord_bits = pbytes * 8 - 1;
+  const uint32_t word_mask = (1u << (coord_bits + 1)) - 1u;
+  const bool has = 8u * j < dp;
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  for (int64_t u = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); u < n; u += waves) {
+    const uint32_t cnt = min((uint32_t)counts[u], R);
+    const uint32_t my_edge = lane < cnt ? edges[(size_t)u * R + lane] : 0u;
+    uint4 uw = make_uint4(0, 0, 0, 0);
+    if (has) uw = *reinterpret_cast<const uint4*>(vecs + (size_t)u * dp + 8u * j);
+    uint8_t* row = rows + (size_t)u * row_bytes;
+    for (uint32_t e0 = 0; e0 < R; e0 += 4) {
+      const uint32_t e = e0 + g;
+      const uint32_t nb = (uint32_t)__shfl((int)my_edge, (int)min(e, 63u), 64);
+      uint32_t word = 0;
+      float mag = 0.0f;
+      if (e0 < cnt) {
+        uint4 nw = make_uint4(0, 0, 0, 0);
+        if (has && e < cnt) nw = *reinterpret_cast<const uint4*>(vecs + (size_t)nb * dp + 8u * j);
+        const uint32_t dw[4] = {hsub2_bits(nw.x, uw.x), hsub2_bits(nw.y, uw.y), hsub2_bits(nw.z, uw.z),
+                                hsub2_bits(nw.w, uw.w)};
+        uint32_t k[8];
+        float x[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const uint32_t d = (m & 1) ? dw[m >> 1] >> 16 : dw[m >> 1] & 0xFFFFu;
+          const uint32_t i = 8u * j + (uint32_t)m;
+          k[m] = has && e < cnt ? ((d & 0x7FFFu) << (coord_bits + 1)) | ((d >> 15) << coord_bits) | i : 0u;
+          const float f = h2f16((uint16_t)d);
+          x[m] = has && e < cnt ? __builtin_fmaf(f, f, 0.0f) : 0.0f;
+        }
+        // the squares' tree: strides 16 and 8 across the quad, 4, 2, 1 in the lane
+#pragma unroll
+        for (int m = 0; m < 8; ++m) x[m] = x[m] + dpp_f<0x4E>(x[m]);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) x[m] = x[m] + dpp_f<0xB1>(x[m]);
+        const float w = ((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7]));
+        const float s = w + row_shl_f<8>(w);
+        mag = s + row_shl_f<4>(s);
+        cx_desc(k[0], k[2]); cx_desc(k[1], k[3]); cx_desc(k[4], k[6]); cx_desc(k[5], k[7]);
+        cx_desc(k[0], k[4]); cx_desc(k[1], k[5]); cx_desc(k[2], k[6]); cx_desc(k[3], k[7]);
+        cx_desc(k[0], k[1]); cx_desc(k[2], k[3]); cx_desc(k[4], k[5]); cx_desc(k[6], k[7]);
+        cx_desc(k[2], k[4]); cx_desc(k[3], k[5]);
+        cx_desc(k[1], k[4]); cx_desc(k[3], k[6]);
+        cx_desc(k[1], k[2]); cx_desc(k[3], k[4]); cx_desc(k[5], k[6]);
+        for (uint32_t r = 0; r < K; ++r) {
+          uint32_t m = k[0];
+          m = max(m, dpp_u32<0xB1>(m));
+          m = max(m, dpp_u32<0x4E>(m));
+          m = max(m, dpp_u32<0x141>(m));
+          m = max(m, dpp_u32<0x140>(m));
+          if (j == r) word = m & word_mask;
+          if (k[0] == m) {
+#pragma unroll
+            for (int q = 0; q < 7; ++q) k[q] = k[q + 1];
+            k[7] = 0;
+          }
+        }
+      }
+      if (e < R) {
+        if (j < K) {
+          const size_t at = ((size_t)e * K + j) * pbytes;
+          if (pbytes == 2)
+            *reinterpret_cast<uint16_t*>(row + at) = (uint16_t)word;
+          else
+            row[at] = (uint8_t)word;
+        }
+        if (j == 0) *reinterpret_cast<uint16_t*>(row + (size_t)R * K * pbytes + 2 * (size_t)e) = f2bf(mag);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------- PQ build --
 
 // pq_sample_residuals (pq_kernels.cuh:64-106): residual nb - u (fp16) of a
@@ -1582,10 +1697,17 @@ void build_lsh(Graph& g, int64_t n_samples, uint64_t seed) {
     art->c_per_rank.assign(h.begin(), h.begin() + K);
     art->norm_denom = h[K];
     hip_check(hipMalloc(&art->rows, (size_t)g.n * art->row_bytes), "alloc edge lsh rows");
-    const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
-    hipLaunchKernelGGL(lsh_populate_kernel, dim3(grid), dim3(64), plds, s, (const uint16_t*)g.vecs, g.n, g.dp,
-                       g.edges, g.counts, g.R, K, P, (uint8_t*)art->rows, (uint32_t)art->row_bytes);
-    hip_check(hipGetLastError(), "launch lsh_populate_kernel");
+    if (g.dp <= 128 && g.R <= 64) {
+      const uint32_t grid = (uint32_t)std::min<int64_t>((g.n + 3) / 4, 65536);
+      hipLaunchKernelGGL(lsh_populate_rows_kernel, dim3(grid), dim3(256), 0, s, (const uint16_t*)g.vecs, g.n, g.dp,
+                         g.edges, g.counts, g.R, K, P, (uint8_t*)art->rows, (uint32_t)art->row_bytes);
+      hip_check(hipGetLastError(), "launch lsh_populate_rows_kernel");
+    } else {
+      const uint32_t grid = (uint32_t)std::min<int64_t>(g.n, 65536);
+      hipLaunchKernelGGL(lsh_populate_kernel, dim3(grid), dim3(64), plds, s, (const uint16_t*)g.vecs, g.n, g.dp,
+                         g.edges, g.counts, g.R, K, P, (uint8_t*)art->rows, (uint32_t)art->row_bytes);
+      hip_check(hipGetLastError(), "launch lsh_populate_kernel");
+    }
     hip_check(hipDeviceSynchronize(), "lsh build");
   } catch (...) {
     (void)hipFree(contrib);

@@ -251,6 +251,30 @@ def test_large_dim_u16_words(jasper, oracle_lib, tmp_path):
           bws=(32,))
 
 
+@pytest.mark.parametrize("dim,R,k_ranks", [(40, 32, 16), (40, 32, 4), (100, 64, 16), (128, 32, 4)])
+def test_lsh_rows_short_dims(jasper, oracle_lib, tmp_path, dim, R, k_ranks):
+    """LSH rows of the at-most-128-coordinate kernel against the oracle: row
+    widths that leave lanes without coordinates (dim 40, and dim 100 whose
+    rows pad to 104), K below and equal to the lane count, vertices with
+    fewer than R edges, and repeated rows (zero differences, whose keys
+    carry only the coordinate index)."""
+    x = gaussian(900, dim, 33)
+    x[300:330] = x[200:230]
+    x[600] = x[601]
+    gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=R, build_lsh=True,
+                            k_ranks=k_ranks, lsh_samples=500, prerotate=False)
+    path = tmp_path / "dir.bin"
+    gg.save(str(path))
+    g = oracle.load_graph(path, dim, R, "l2")
+    assert (g.counts < R).any()
+    _, _, lrows = gg.export_lsh()
+    want = oracle.populate_lsh(g, k_ranks, 1)
+    assert lrows.shape == want.shape
+    bad = np.nonzero((lrows != want).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} LSH rows differ, first vertex {bad[0] if bad.size else None}"
+    gg.free()
+
+
 def test_lsh_only_then_pq_search_rejected(jasper, oracle_lib):
     x = gaussian(600, 64, 28)
     gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=32, build_lsh=True,
