@@ -973,12 +973,11 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   const uint32_t lut_words = PQ ? ((LUT == kLutWhole ? pq_lut_rows(a.M) : 64u) + lut_tail_rows) * 128u : 0u;
   uint64_t* sm = smem + lut_words;
   uint64_t* buf0 = sm;
-  uint64_t* buf1 = buf0 + cap;
-  uint64_t* T = buf1 + cap;
+  uint64_t* T = buf0 + cap;
   float* Fd = reinterpret_cast<float*>(T + 64);  // frontier distances (exact bits)
   uint32_t* Fi = reinterpret_cast<uint32_t*>(Fd + a.k);
   // marks of the new keys' positions in the general merge (nonzero = new)
-  uint8_t* MK = reinterpret_cast<uint8_t*>(sm + ((2 * cap + 64 + a.k + 1) & ~1u));
+  uint8_t* MK = reinterpret_cast<uint8_t*>(sm + ((cap + 64 + a.k + 1) & ~1u));
   // LSH with 1-byte words (dp <= 128): q and q - u take 16 chunks each,
   // zero past dp, so any 7-bit coordinate reads inside them
   constexpr bool LSH8 = !PQ && !RQ && P == 1;
@@ -986,7 +985,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   constexpr int kGlobGroups = (PQ && P == 8 && LUT != kLutWhole) ? 4 : 0;
   static_assert(LUT == kLutWhole || (PQ && P == 8), "split tables need 8 groups");
   const uint32_t qchunks = LSH8 ? 16u : nchunks;
-  uint4* qv = reinterpret_cast<uint4*>(sm + ((2 * cap + 64 + a.k + 1) & ~1u) + dir_mark_words(cap));  // 16-byte aligned
+  uint4* qv = reinterpret_cast<uint4*>(sm + ((cap + 64 + a.k + 1) & ~1u) + dir_mark_words(cap));  // 16-byte aligned
   for (uint32_t i = lane; i < dir_mark_words(cap) * 2u; i += 64) reinterpret_cast<uint32_t*>(MK)[i] = 0u;
   uint4* xv = qv + qchunks;  // L2 LSH: fp16 q - u
   // PQ: the query's LUT; LSH: the bf16 sqrt table
@@ -1096,7 +1095,6 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
 
   // B = [(medoid, est 0.0, unvisited)], F empty (graph_beam_search.cuh:141-149)
   uint64_t* B = buf0;
-  uint64_t* NB = buf1;
   if (lane == 0) B[0] = make_key(0.0f, a.medoid);
   uint32_t cnt = 1, fc = 0, vc = 0, loop = 0, n_hops = 0, n_adj = 0;
   float fdr = FLT_MAX;     // F's distances and ids in registers when k <= 64
@@ -1473,8 +1471,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     // smallest key's insertion point lo0 keep their entries; the merge and
     // the dedup start there.
     uint32_t lo0;
-    uint32_t lo_v = 0;       // counting path: lane i < nt holds lo_i
-    bool in_place = false;   // the counting path merged into B itself
+    uint32_t lo_v = 0;       // lane i < nt holds lo_i
     if (nt <= kCountMerge && cnt <= 128) {
       // few new keys and a head of at most two rows: the head is held in
       // registers, so the merge writes B in place. Key i is counted against
@@ -1506,8 +1503,14 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       if (lane < nt) B[lane + lo_v] = t;
       if (lane >= lo0 && lane < cnt) B[lane + s0] = h0;
       if (lane + 64u >= lo0 && lane + 64u < cnt) B[lane + 64u + s1] = h1;
-      in_place = true;
     } else {
+      // wider heads or more keys: each key finds lo_i by a binary search
+      // and marks its position lo_i + i; every other position o >= lo0
+      // takes head entry o - (new keys below o), a count that a ballot over
+      // the marks gives per 64-entry row. The rows run from the top down,
+      // so each reads only entries not yet overwritten (a source lies at
+      // most nt <= 64 slots below its position), and the keys are written
+      // last, into B itself.
       const uint32_t top = pow2_ceil(cnt);
       uint32_t lo = 0;
       if (lane < nt) {
@@ -1516,34 +1519,39 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
           const uint32_t probe = lo + step;
           if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
         }
-        NB[lane + lo] = t;
         MK[lane + lo] = 1u;
       }
       lo0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
+      lo_v = lo;
       lds_wave_sync();
-      // every other position o >= lo0 takes head entry o - (new keys below
-      // o): a ballot over the marks counts them per 64-entry row
       const uint32_t tot = cnt + nt;
-      uint32_t below = 0;
-      for (uint32_t o0 = lo0; o0 < tot; o0 += 64) {
-        const uint32_t o = o0 + lane;
+      uint32_t above = 0;  // new keys at positions past the current row
+      for (uint32_t r = (tot - lo0 + 63u) / 64u; r-- > 0;) {
+        const uint32_t o = lo0 + 64u * r + lane;
         const bool valid = o < tot;
         const bool isnew = valid && MK[o] != 0u;
         const uint64_t m = ballot(isnew);
-        if (valid && !isnew) NB[o] = B[o - below - mbcnt(m)];
-        below = uniform(below + (uint32_t)__builtin_popcountll(m));
+        if (valid && !isnew) {
+          const uint32_t below = nt - above - (uint32_t)__builtin_popcountll(m >> lane);
+          const uint64_t v = B[o - below];
+          B[o] = v;
+        }
+        above = uniform(above + (uint32_t)__builtin_popcountll(m));
       }
-      if (lane < nt) MK[lane + lo] = 0u;
+      if (lane < nt) {
+        B[lane + lo] = t;
+        MK[lane + lo] = 0u;
+      }
     }
     lds_wave_sync();
     const uint32_t total = cnt + nt;
     // Dedup: drop each entry whose id equals the previous entry's. Merging
     // never makes two head entries adjacent that were not, and B holds no
     // adjacent equal ids, so an entry can only be dropped at a new key or
-    // right after one. The in-place merge checks those two places and is
-    // done when neither drops anything (the usual case).
-    bool dedup = true;
-    if (in_place) {
+    // right after one. The merge checks those two places and is done when
+    // neither drops anything (the usual case).
+    bool dedup;
+    {
       bool d = false;
       if (lane < nt) {
         const uint32_t pos = lane + lo_v, id = key_id(t);
@@ -1554,10 +1562,10 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     }
     uint32_t kept = total;
     if (dedup) {
-      // in order from lo0, reading the merged entries (B itself after the
-      // in-place merge: each row is read before any of its slots is written,
-      // and writes only go to slots at or below the ones read)
-      const uint64_t* src = in_place ? B : NB;
+      // in order from lo0, reading the merged entries in B itself: each row
+      // is read before any of its slots is written, and writes only go to
+      // slots at or below the ones read
+      const uint64_t* src = B;
       // the previous entry's id: the lane below (DPP wave shift), or for
       // lane 0 the last id of the previous row (the head's entry below lo0
       // at first)
@@ -1975,7 +1983,7 @@ const uint16_t* directional_query_rows(const Graph& g, const void* queries, int6
 
 // LDS of one query's wave, less the PQ table.
 size_t directional_base_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
-  size_t lds = ((size_t)((2 * (bw + g.R) + 64 + k + 1) & ~(int64_t)1) + dir_mark_words((uint32_t)(bw + g.R))) * 8;
+  size_t lds = ((size_t)(((bw + g.R) + 64 + k + 1) & ~(int64_t)1) + dir_mark_words((uint32_t)(bw + g.R))) * 8;
   if (est == kEstLsh) {
     // q and q - u (16 chunks each with 1-byte words), the sqrt table
     const size_t chunks = g.lsh->packed_bytes == 1 ? 16 : g.dp / 8;
