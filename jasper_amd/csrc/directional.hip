@@ -280,27 +280,43 @@ __global__ __launch_bounds__(64) void lsh_calib_kernel(const uint16_t* __restric
   if (lane == 0) valid[s] = 1;
 }
 
-// finalize_lsh_globals (lsh_globals.cuh:160-178), sums in sample order.
-__global__ void lsh_finalize_kernel(const float* __restrict__ contrib, const uint8_t* __restrict__ valid,
-                                    int64_t n_samples, uint32_t K, float* __restrict__ out /* K + 2 */) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  float sum[16];
-  for (uint32_t r = 0; r < K; ++r) sum[r] = 0.0f;
+// finalize_lsh_globals (lsh_globals.cuh:160-178), sums in sample order:
+// lane r < K of one wave keeps rank r's running sum, over tiles of 256
+// samples staged in LDS (a sample's K values are contiguous, so the tile
+// loads are coalesced).
+__global__ __launch_bounds__(64) void lsh_finalize_kernel(const float* __restrict__ contrib,
+                                                          const uint8_t* __restrict__ valid, int64_t n_samples,
+                                                          uint32_t K, float* __restrict__ out /* K + 2 */) {
+  constexpr uint32_t kTile = 256;
+  __shared__ float tile[kTile * 16];
+  __shared__ uint8_t ok[kTile];
+  const uint32_t lane = threadIdx.x;
+  float sum = 0.0f;
   int64_t nv = 0;
-  for (int64_t s = 0; s < n_samples; ++s) {
-    if (!valid[s]) continue;
-    ++nv;
-    for (uint32_t r = 0; r < K; ++r) sum[r] = sum[r] + contrib[s * K + r];
+  for (int64_t s0 = 0; s0 < n_samples; s0 += kTile) {
+    const uint32_t ns = (uint32_t)min<int64_t>(kTile, n_samples - s0);
+    wave_sync();
+    for (uint32_t i = lane; i < ns * K; i += 64) tile[i] = contrib[s0 * K + i];
+    for (uint32_t i = lane; i < ns; i += 64) ok[i] = valid[s0 + i];
+    wave_sync();
+    for (uint32_t s = 0; s < ns; ++s) {
+      if (!ok[s]) continue;
+      ++nv;
+      if (lane < K) sum = sum + tile[s * K + lane];
+    }
   }
   const float inv_n = div_rn(1.0f, (float)nv);
+  const float c = sum * inv_n;
+  if (lane < K) out[lane] = c;
   float denom = 0.0f;
   for (uint32_t r = 0; r < K; ++r) {
-    const float c = sum[r] * inv_n;
-    out[r] = c;
-    denom = __builtin_fmaf(c, c, denom);
+    const float cr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), (int)r));
+    denom = __builtin_fmaf(cr, cr, denom);
   }
-  out[K] = denom;
-  out[K + 1] = (float)nv;
+  if (lane == 0) {
+    out[K] = denom;
+    out[K + 1] = (float)nv;
+  }
 }
 
 // populate_lsh (lsh/lsh_kernels.cuh:9-132): one wave per vertex, edges
@@ -1698,7 +1714,7 @@ void build_lsh(Graph& g, int64_t n_samples, uint64_t seed) {
       hipLaunchKernelGGL(lsh_calib_kernel, dim3((uint32_t)n_samples), dim3(64), g.dp * 4, s, (const uint16_t*)g.vecs,
                          g.n, g.dp, g.edges, g.counts, g.R, K, seed, contrib, valid);
     hip_check(hipGetLastError(), "launch lsh_calib_kernel");
-    hipLaunchKernelGGL(lsh_finalize_kernel, dim3(1), dim3(1), 0, s, contrib, valid, n_samples, K, out);
+    hipLaunchKernelGGL(lsh_finalize_kernel, dim3(1), dim3(64), 0, s, contrib, valid, n_samples, K, out);
     hip_check(hipGetLastError(), "launch lsh_finalize_kernel");
     std::vector<float> h(K + 2);
     hip_check(hipMemcpy(h.data(), out, (K + 2) * 4, hipMemcpyDeviceToHost), "download lsh globals");
