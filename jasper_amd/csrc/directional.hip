@@ -944,6 +944,27 @@ __device__ __forceinline__ float visit_exact(const uint4* qrow, const uint4 (&qr
   return block128_sum_rows(p[0], p[1], nchunks);
 }
 
+// The build mode's L2 visit for rows of at most C chunks (RaBitQ graphs:
+// ceil(dim / 8) chunks, at most 4 per code dword): the lane's chunks ql,
+// ql + 4, ... of u's row are loaded together, then summed in that order,
+// the chain stream_partial_l2 forms.
+template <uint32_t C>
+__device__ __forceinline__ float visit_partial_l2(const uint4* q, const uint4* row, uint32_t ql, uint32_t nchunks) {
+  uint4 xb[C / 4];
+#pragma unroll
+  for (uint32_t u = 0; u < C / 4; ++u) {
+    const uint32_t c = ql + 4u * u;
+    xb[u] = c < nchunks ? row[c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (uint32_t u = 0; u < C / 4; ++u) {
+    const uint32_t c = ql + 4u * u;
+    if (c < nchunks) l2_chunk(q[c], xb[u], acc);
+  }
+  return acc;
+}
+
 // One LSH word (sign in the MSB, coordinate below) of rank r from the
 // edge's K * P bytes held in registers.
 template <int P>
@@ -970,8 +991,19 @@ __host__ __device__ __forceinline__ uint32_t dir_mark_words(uint32_t cap) { retu
 // (P = 8, more than 64 subspaces) let two queries' waves share a CU.
 constexpr int kLutWhole = 0, kLutSplitLast = 1, kLutSplit = 2;
 
+#ifndef JASPER_DIR_RQ_WAVES
+#define JASPER_DIR_RQ_WAVES 1
+#endif
+
+// Waves per SIMD the compiler must leave room for: the RaBitQ instances
+// (the build's search stage) are compiled for more resident waves.
+template <int K>
+constexpr int dir_waves_per_simd() {
+  return K == 1 ? JASPER_DIR_RQ_WAVES : 1;
+}
+
 template <int METRIC, int K, int P, int LUT = kLutWhole>
-__global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
+__global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
   constexpr bool L2 = METRIC == kL2;
   constexpr bool PQ = K == 0;
@@ -1304,7 +1336,7 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
     } else if (RQ && a.visited) {
       // build mode: the plain search's distance (distance.cuh's 4-lane
       // order), so visits carry the values the plain build search records
-      const float part = L2 ? stream_partial_l2(qv, urow, lane & 3u, nchunks)
+      const float part = L2 ? visit_partial_l2<4u * P>(qv, urow, lane & 3u, nchunks)
                             : stream_partial_ip(qv, urow, lane & 3u, nchunks, a.dp);
       stored = __shfl(quad_finish<METRIC>(part), 0, 64);
       if (lane == 0) a.visited[(size_t)qid * a.max_result + vc] = make_key(stored, u);
