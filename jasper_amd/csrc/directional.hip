@@ -977,12 +977,10 @@ __device__ __forceinline__ uint32_t lsh_word(const uint32_t* w, int r) {
 // the binary searches).
 constexpr uint32_t kCountMerge = 16;
 
-// K = 0: the PQ estimator, with up to 16 * P subspaces (the edge's codes are
-// P groups of 16 bytes in registers); K = 1: the RaBitQ estimator with codes
-// of up to 32 * P dims; K in {4, 16} with P-byte words: the LSH estimator.
-// 8-byte words of the merge's position marks (one byte per slot of the
-// candidate buffer, rounded to 16 bytes).
-__host__ __device__ __forceinline__ uint32_t dir_mark_words(uint32_t cap) { return ((cap + 15u) & ~15u) / 8u; }
+// 8-byte words of the merge's position marks (one bit per slot of the
+// candidate buffer, rounded to 128 slots so that what follows stays 16-byte
+// aligned).
+__host__ __device__ __forceinline__ uint32_t dir_mark_words(uint32_t cap) { return ((cap + 127u) & ~127u) / 64u; }
 
 // PQ table layouts in LDS (the last argument of directional_kernel): the
 // whole table; the first 4 groups of 16 subspaces and the last, partly
@@ -1002,6 +1000,9 @@ constexpr int dir_waves_per_simd() {
   return K == 1 ? JASPER_DIR_RQ_WAVES : 1;
 }
 
+// K = 0: the PQ estimator, with up to 16 * P subspaces (the edge's codes are
+// P groups of 16 bytes in registers); K = 1: the RaBitQ estimator with codes
+// of up to 32 * P dims; K in {4, 16} with P-byte words: the LSH estimator.
 template <int METRIC, int K, int P, int LUT = kLutWhole>
 __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
@@ -1024,8 +1025,9 @@ __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_ker
   uint64_t* T = buf0 + cap;
   float* Fd = reinterpret_cast<float*>(T + 64);  // frontier distances (exact bits)
   uint32_t* Fi = reinterpret_cast<uint32_t*>(Fd + a.k);
-  // marks of the new keys' positions in the general merge (nonzero = new)
-  uint8_t* MK = reinterpret_cast<uint8_t*>(sm + ((cap + 64 + a.k + 1) & ~1u));
+  // marks of the new keys' positions in the general merge (bit o of the
+  // array set = position o holds a new key)
+  uint32_t* MK = reinterpret_cast<uint32_t*>(sm + ((cap + 64 + a.k + 1) & ~1u));
   // LSH with 1-byte words (dp <= 128): q and q - u take 16 chunks each,
   // zero past dp, so any 7-bit coordinate reads inside them
   constexpr bool LSH8 = !PQ && !RQ && P == 1;
@@ -1034,7 +1036,7 @@ __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_ker
   static_assert(LUT == kLutWhole || (PQ && P == 8), "split tables need 8 groups");
   const uint32_t qchunks = LSH8 ? 16u : nchunks;
   uint4* qv = reinterpret_cast<uint4*>(sm + ((cap + 64 + a.k + 1) & ~1u) + dir_mark_words(cap));  // 16-byte aligned
-  for (uint32_t i = lane; i < dir_mark_words(cap) * 2u; i += 64) reinterpret_cast<uint32_t*>(MK)[i] = 0u;
+  for (uint32_t i = lane; i < dir_mark_words(cap) * 2u; i += 64) MK[i] = 0u;
   uint4* xv = qv + qchunks;  // L2 LSH: fp16 q - u
   // PQ: the query's LUT; LSH: the bf16 sqrt table
   float* lut = PQ ? reinterpret_cast<float*>(smem) : reinterpret_cast<float*>(xv + qchunks);
@@ -1567,7 +1569,7 @@ __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_ker
           const uint32_t probe = lo + step;
           if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
         }
-        MK[lane + lo] = 1u;
+        atomicOr(&MK[(lane + lo) >> 5], 1u << ((lane + lo) & 31u));
       }
       lo0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
       lo_v = lo;
@@ -1577,7 +1579,7 @@ __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_ker
       for (uint32_t r = (tot - lo0 + 63u) / 64u; r-- > 0;) {
         const uint32_t o = lo0 + 64u * r + lane;
         const bool valid = o < tot;
-        const bool isnew = valid && MK[o] != 0u;
+        const bool isnew = valid && ((MK[o >> 5] >> (o & 31u)) & 1u) != 0u;
         const uint64_t m = ballot(isnew);
         if (valid && !isnew) {
           const uint32_t below = nt - above - (uint32_t)__builtin_popcountll(m >> lane);
@@ -1588,7 +1590,7 @@ __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_ker
       }
       if (lane < nt) {
         B[lane + lo] = t;
-        MK[lane + lo] = 0u;
+        MK[(lane + lo) >> 5] = 0u;  // every set bit is a new key's
       }
     }
     lds_wave_sync();
