@@ -868,6 +868,8 @@ struct DirArgs {
   uint32_t row_bytes;
   float c[16];
   float inv_norm_denom;
+  // 1: the bf16 square-root table sits in LDS; 0: each root is computed
+  uint32_t sqrt_lds;
   // PQ
   uint32_t M, dsub;
   const float* centroids;
@@ -1050,7 +1052,9 @@ __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_ker
       xv[i] = make_uint4(0u, 0u, 0u, 0u);
     }
   }
-  if constexpr (!PQ && !RQ) fill_sqrt_table(lut, lane);
+  if constexpr (!PQ && !RQ) {
+    if (a.sqrt_lds) fill_sqrt_table(lut, lane);
+  }
   uint4 qreg[2];
   qreg[0] = lane < nchunks ? qsrc[lane] : make_uint4(0u, 0u, 0u, 0u);
   qreg[1] = lane + 64u < nchunks ? qsrc[lane + 64u] : make_uint4(0u, 0u, 0u, 0u);
@@ -1484,7 +1488,7 @@ __global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_ker
           }
           const float mag_sq = bf2f((uint16_t)mag_bits);
           const float dot_est = dot_acc * a.inv_norm_denom;
-          const float mag = bf16_sqrt(lut, mag_bits);
+          const float mag = a.sqrt_lds ? bf16_sqrt(lut, mag_bits) : sqrt_rn(bf2f((uint16_t)mag_bits));
           est = L2 ? __builtin_fmaf(-(2.0f * mag), dot_est, exact_u + mag_sq)
                    : -__builtin_fmaf(mag, dot_est, exact_u);
         }
@@ -2031,13 +2035,27 @@ const uint16_t* directional_query_rows(const Graph& g, const void* queries, int6
   return rot;
 }
 
-// LDS of one query's wave, less the PQ table.
-size_t directional_base_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw) {
+// The LSH estimate's bf16 square-root table (1 KB) stays in LDS unless LDS
+// bounds how many queries share a CU and dropping it lets one more in (wide
+// beams); the kernel then computes each root with sqrt_rn, whose values the
+// table holds. lds: the query's LDS without the table.
+bool lsh_sqrt_in_lds(size_t lds) {
+  const size_t cu = 160 * 1024, with = lds + 256 * 4;
+  return cu / with >= 32 || cu / lds == cu / with;
+}
+
+// LDS of one query's wave, less the PQ table; *sqrt_lds (LSH) tells whether
+// the square-root table is part of it.
+size_t directional_base_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw, bool* sqrt_lds = nullptr) {
   size_t lds = ((size_t)(((bw + g.R) + 64 + k + 1) & ~(int64_t)1) + dir_mark_words((uint32_t)(bw + g.R))) * 8;
+  if (sqrt_lds) *sqrt_lds = false;
   if (est == kEstLsh) {
     // q and q - u (16 chunks each with 1-byte words), the sqrt table
     const size_t chunks = g.lsh->packed_bytes == 1 ? 16 : g.dp / 8;
-    lds += 2 * chunks * 16 + 256 * 4;
+    lds += 2 * chunks * 16;
+    const bool tab = lsh_sqrt_in_lds(lds);
+    if (tab) lds += 256 * 4;
+    if (sqrt_lds) *sqrt_lds = tab;
   } else {
     lds += (size_t)2 * g.dp * 2;
   }
@@ -2069,8 +2087,9 @@ int pq_lut_layout(const Graph& g, int64_t k, int64_t bw, int64_t nq) {
 }
 
 // LDS of one query's wave, with the PQ table in the given layout.
-size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw, int lut_layout = kLutWhole) {
-  size_t lds = directional_base_lds_bytes(g, est, k, bw);
+size_t directional_lds_bytes(const Graph& g, int est, int64_t k, int64_t bw, int lut_layout = kLutWhole,
+                             bool* sqrt_lds = nullptr) {
+  size_t lds = directional_base_lds_bytes(g, est, k, bw, sqrt_lds);
   if (est == kEstPq) {
     const uint32_t m = g.pq->m;
     const uint32_t rows = lut_layout == kLutWhole ? pq_lut_rows(m)
@@ -2157,7 +2176,9 @@ void directional_search_run(Graph& g, int est, const void* queries, int64_t nq, 
   a.stats = stats;
   a.unique = unique ? 1u : 0u;
   const int lut_layout = use_pq ? pq_lut_layout(g, k, bw, nq) : kLutWhole;
-  const size_t lds = directional_lds_bytes(g, est, k, bw, lut_layout);
+  bool sqrt_lds = false;
+  const size_t lds = directional_lds_bytes(g, est, k, bw, lut_layout, &sqrt_lds);
+  a.sqrt_lds = sqrt_lds ? 1u : 0u;
   const bool l2 = g.metric == kL2;
   if (est == kEstRabitq) {
     const RabitqArtifacts& rq = *g.rabitq;

@@ -275,6 +275,29 @@ def test_lsh_rows_short_dims(jasper, oracle_lib, tmp_path, dim, R, k_ranks):
     gg.free()
 
 
+def test_lsh_wide_beam(jasper, oracle_lib, tmp_path):
+    """A beam of 1024 at R = 64, K = 16: the general merge on a head of
+    more than 128 entries on most hops, and LDS bounds residency, so the
+    square roots are computed instead of read from the LDS table. Both
+    traversals against the oracle."""
+    x = integer_clustered(3000, 128, 34)
+    q = integer_clustered(24, 128, 35)
+    gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=64, build_lsh=True,
+                            k_ranks=16, lsh_samples=2000, prerotate=False)
+    path = tmp_path / "dir.bin"
+    gg.save(str(path))
+    g = oracle.load_graph(path, 128, 64, "l2")
+    c, nd, lrows = gg.export_lsh()
+    art = oracle.LshArtifacts(16, 1, c, nd, lrows)
+    q_rows = oracle.as_padded_f16(q)
+    for unique in (False, True):
+        ids, d = _search(gg, "directional_search", q, 10, 1024, unique=unique)
+        rid, rd = oracle.directional_search(g, q_rows, lsh=art, k=10, beam_width=1024, unique=unique)
+        msg = compare_search(ids, d, rid, rd)
+        assert msg is None, f"unique={unique}: {msg}"
+    gg.free()
+
+
 def test_lsh_only_then_pq_search_rejected(jasper, oracle_lib):
     x = gaussian(600, 64, 28)
     gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=32, build_lsh=True,
