@@ -293,16 +293,31 @@ __global__ __launch_bounds__(64) void lsh_finalize_kernel(const float* __restric
   const uint32_t lane = threadIdx.x;
   float sum = 0.0f;
   int64_t nv = 0;
+  const uint32_t rk = min(lane, K - 1u);  // lanes past K repeat rank K - 1's reads
   for (int64_t s0 = 0; s0 < n_samples; s0 += kTile) {
     const uint32_t ns = (uint32_t)min<int64_t>(kTile, n_samples - s0);
     wave_sync();
     for (uint32_t i = lane; i < ns * K; i += 64) tile[i] = contrib[s0 * K + i];
     for (uint32_t i = lane; i < ns; i += 64) ok[i] = valid[s0 + i];
     wave_sync();
-    for (uint32_t s = 0; s < ns; ++s) {
-      if (!ok[s]) continue;
-      ++nv;
-      if (lane < K) sum = sum + tile[s * K + lane];
+    // 64 samples at a time: their validity as one mask, each add kept or
+    // dropped by a select, so the reads do not wait on a branch
+    for (uint32_t b = 0; b < ns; b += 64) {
+      const uint64_t vm = ballot(b + lane < ns && ok[b + lane] != 0u);
+      nv += __builtin_popcountll(vm);
+      const uint32_t nb = min(ns - b, 64u);
+      for (uint32_t j = 0; j < nb; j += 8) {
+        // eight reads in flight (slots past the tile's samples are inside
+        // the array and dropped by the mask), then the adds in order
+        float x[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) x[u] = tile[(b + j + u) * K + rk];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+          const float y = sum + x[u];
+          sum = ((vm >> (j + u)) & 1ull) ? y : sum;
+        }
+      }
     }
   }
   const float inv_n = div_rn(1.0f, (float)nv);
