@@ -1006,22 +1006,11 @@ __host__ __device__ __forceinline__ uint32_t dir_mark_words(uint32_t cap) { retu
 // (P = 8, more than 64 subspaces) let two queries' waves share a CU.
 constexpr int kLutWhole = 0, kLutSplitLast = 1, kLutSplit = 2;
 
-#ifndef JASPER_DIR_RQ_WAVES
-#define JASPER_DIR_RQ_WAVES 1
-#endif
-
-// Waves per SIMD the compiler must leave room for: the RaBitQ instances
-// (the build's search stage) are compiled for more resident waves.
-template <int K>
-constexpr int dir_waves_per_simd() {
-  return K == 1 ? JASPER_DIR_RQ_WAVES : 1;
-}
-
 // K = 0: the PQ estimator, with up to 16 * P subspaces (the edge's codes are
 // P groups of 16 bytes in registers); K = 1: the RaBitQ estimator with codes
 // of up to 32 * P dims; K in {4, 16} with P-byte words: the LSH estimator.
 template <int METRIC, int K, int P, int LUT = kLutWhole>
-__global__ __launch_bounds__(64, (dir_waves_per_simd<K>())) void directional_kernel(DirArgs a) {
+__global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
   extern __shared__ uint64_t smem[];
   constexpr bool L2 = METRIC == kL2;
   constexpr bool PQ = K == 0;
