@@ -993,6 +993,9 @@ __device__ __forceinline__ uint32_t lsh_word(const uint32_t* w, int r) {
 // Largest number of new keys a hop merges by counting (larger ones take
 // the binary searches).
 constexpr uint32_t kCountMerge = 16;
+// Largest number of 64-entry rows the general merge moves with marks in LDS
+// (more rows take masks built in scalar registers).
+constexpr uint32_t kMarkRows = 8;
 
 // 8-byte words of the merge's position marks (one bit per slot of the
 // candidate buffer, rounded to 128 slots so that what follows stays 16-byte
@@ -1562,13 +1565,13 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       if (lane >= lo0 && lane < cnt) B[lane + s0] = h0;
       if (lane + 64u >= lo0 && lane + 64u < cnt) B[lane + 64u + s1] = h1;
     } else {
-      // wider heads or more keys: each key finds lo_i by a binary search
-      // and marks its position lo_i + i; every other position o >= lo0
-      // takes head entry o - (new keys below o), a count that a ballot over
-      // the marks gives per 64-entry row. The rows run from the top down,
-      // so each reads only entries not yet overwritten (a source lies at
-      // most nt <= 64 slots below its position), and the keys are written
-      // last, into B itself.
+      // wider heads or more keys: each key finds lo_i by a binary search,
+      // and its position is lo_i + i; every other position o >= lo0 takes
+      // head entry o - (new keys below o), counted per 64-entry row from a
+      // mask of the row's new positions. The rows run from the top down, so
+      // each reads only entries not yet overwritten (a source lies at most
+      // nt <= 64 slots below its position), and the keys are written last,
+      // into B itself.
       const uint32_t top = pow2_ceil(cnt);
       uint32_t lo = 0;
       if (lane < nt) {
@@ -1577,29 +1580,53 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
           const uint32_t probe = lo + step;
           if (probe <= cnt && key_rank(B[probe - 1]) <= key_rank(t)) lo = probe;
         }
-        atomicOr(&MK[(lane + lo) >> 5], 1u << ((lane + lo) & 31u));
       }
       lo0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
       lo_v = lo;
-      lds_wave_sync();
       const uint32_t tot = cnt + nt;
+      const uint32_t rows = (tot - lo0 + 63u) / 64u;
       uint32_t above = 0;  // new keys at positions past the current row
-      for (uint32_t r = (tot - lo0 + 63u) / 64u; r-- > 0;) {
-        const uint32_t o = lo0 + 64u * r + lane;
-        const bool valid = o < tot;
-        const bool isnew = valid && ((MK[o >> 5] >> (o & 31u)) & 1u) != 0u;
-        const uint64_t m = ballot(isnew);
-        if (valid && !isnew) {
-          const uint32_t below = nt - above - (uint32_t)__builtin_popcountll(m >> lane);
-          const uint64_t v = B[o - below];
-          B[o] = v;
+      if (rows <= kMarkRows) {
+        // a few rows: the masks come from marks in LDS, one bit per slot
+        if (lane < nt) atomicOr(&MK[(lane + lo) >> 5], 1u << ((lane + lo) & 31u));
+        lds_wave_sync();
+        for (uint32_t r = rows; r-- > 0;) {
+          const uint32_t o = lo0 + 64u * r + lane;
+          const bool valid = o < tot;
+          const bool isnew = valid && ((MK[o >> 5] >> (o & 31u)) & 1u) != 0u;
+          const uint64_t m = ballot(isnew);
+          if (valid && !isnew) {
+            const uint32_t below = nt - above - (uint32_t)__builtin_popcountll(m >> lane);
+            const uint64_t v = B[o - below];
+            B[o] = v;
+          }
+          above = uniform(above + (uint32_t)__builtin_popcountll(m));
         }
-        above = uniform(above + (uint32_t)__builtin_popcountll(m));
+        if (lane < nt) MK[(lane + lo) >> 5] = 0u;  // every set bit is a new key's
+      } else {
+        // many rows (a wide head): each row's mask is folded in scalar
+        // registers from the keys whose positions fall in it (a run of
+        // lanes, the keys being sorted), which takes an LDS round trip off
+        // every row
+        const uint32_t pos_v = lane < nt ? lo + lane : 0xFFFFFFFFu;  // key `lane`'s position
+        for (uint32_t r = rows; r-- > 0;) {
+          const uint32_t o0 = lo0 + 64u * r, o = o0 + lane;
+          uint64_t in_row = ballot(pos_v >= o0 && pos_v < o0 + 64u);
+          uint64_t m = 0;  // bit l: position o0 + l holds a new key
+          while (in_row) {
+            const int i = __builtin_ctzll(in_row);
+            in_row &= in_row - 1u;
+            m |= 1ull << ((uint32_t)__builtin_amdgcn_readlane((int)pos_v, i) - o0);
+          }
+          if (o < tot && ((m >> lane) & 1ull) == 0u) {
+            const uint32_t below = nt - above - (uint32_t)__builtin_popcountll(m >> lane);
+            const uint64_t v = B[o - below];
+            B[o] = v;
+          }
+          above = uniform(above + (uint32_t)__builtin_popcountll(m));
+        }
       }
-      if (lane < nt) {
-        B[lane + lo] = t;
-        MK[(lane + lo) >> 5] = 0u;  // every set bit is a new key's
-      }
+      if (lane < nt) B[lane + lo] = t;
     }
     lds_wave_sync();
     const uint32_t total = cnt + nt;
