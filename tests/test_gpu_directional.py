@@ -277,24 +277,30 @@ def test_lsh_rows_short_dims(jasper, oracle_lib, tmp_path, dim, R, k_ranks):
 
 def test_lsh_wide_beam(jasper, oracle_lib, tmp_path):
     """A beam of 1024 at R = 64, K = 16: the general merge on a head of
-    more than 128 entries on most hops, and LDS bounds residency, so the
-    square roots are computed instead of read from the LDS table. Both
-    traversals against the oracle."""
+    more than 128 entries on most hops, with more than 8 rows to move on
+    many (the row masks then come from the keys' positions in scalar
+    registers), and LDS bounds residency, so the square roots are computed
+    instead of read from the LDS table. Both traversals against the oracle,
+    for LSH and for PQ (M = 16) on the same graph."""
     x = integer_clustered(3000, 128, 34)
     q = integer_clustered(24, 128, 35)
     gg = jasper.Graph.build(torch.from_numpy(x.astype(np.float16)).cuda(), n_neighbors=64, build_lsh=True,
-                            k_ranks=16, lsh_samples=2000, prerotate=False)
+                            build_pq=True, k_ranks=16, lsh_samples=2000, pq_train=2000, pq_kmeans_iter=3,
+                            pq_seed=11, prerotate=False)
     path = tmp_path / "dir.bin"
     gg.save(str(path))
     g = oracle.load_graph(path, 128, 64, "l2")
     c, nd, lrows = gg.export_lsh()
-    art = oracle.LshArtifacts(16, 1, c, nd, lrows)
+    lsh = oracle.LshArtifacts(16, 1, c, nd, lrows)
+    cent, codes, norms = gg.export_pq()
+    pq = oracle.PqArtifacts(16, g.dp // 16, cent, codes, norms)
     q_rows = oracle.as_padded_f16(q)
-    for unique in (False, True):
-        ids, d = _search(gg, "directional_search", q, 10, 1024, unique=unique)
-        rid, rd = oracle.directional_search(g, q_rows, lsh=art, k=10, beam_width=1024, unique=unique)
-        msg = compare_search(ids, d, rid, rd)
-        assert msg is None, f"unique={unique}: {msg}"
+    for fn, art in (("directional_search", {"lsh": lsh}), ("pq_search", {"pq": pq})):
+        for unique in (False, True):
+            ids, d = _search(gg, fn, q, 10, 1024, unique=unique)
+            rid, rd = oracle.directional_search(g, q_rows, k=10, beam_width=1024, unique=unique, **art)
+            msg = compare_search(ids, d, rid, rd)
+            assert msg is None, f"{fn} unique={unique}: {msg}"
     gg.free()
 
 
