@@ -1430,14 +1430,16 @@ __global__ __launch_bounds__(64) void directional_kernel(DirArgs a) {
       if (valid_v) {
         float est;
         if constexpr (RQ) {
-          int32_t dot = 0, pc = 0;
+          // one count per bit plane (v_bcnt accumulates), weighted once
+          int32_t dj[4] = {0, 0, 0, 0}, pc = 0;
 #pragma unroll
           for (int w = 0; w < P; ++w) {
             const uint32_t c = rq_code[w];
             pc += __builtin_popcount(c);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dot += __builtin_popcount(c & rq_planes[j * P + w]) << j;
+            for (int j = 0; j < 4; ++j) dj[j] += __builtin_popcount(c & rq_planes[j * P + w]);
           }
+          const int32_t dot = dj[0] + 2 * dj[1] + 4 * dj[2] + 8 * dj[3];
           const float t1 = (float)(2 * dot - rq_sumq), t2 = (float)(2 * pc - (int32_t)a.rq_dim);
           const float ipq = __builtin_fmaf(rq_hd, t1, rq_hl * t2);
           est = __builtin_fmaf(rq_fres, ipq, rq_fadd + rq_gadd);
